@@ -1,0 +1,270 @@
+#!/usr/bin/env python3
+"""Velurex ternary GEMV decode weight stream on one MI355X.
+
+One "step" is the projection stream of one decoded Falcon3-10B token at bs=1: for each of the 40 layers the stacked
+q|k|v projection (5120 x 3072), o (3072 x 3072), the row-interleaved gate|up projection (46080 x 3072) and down
+(3072 x 23040) -- 9,500,098,560 ternary weights, 1.90 GB at 1.60 bpw -- each on its own int8 input vector (per-token
+absmax int8 of N(0,1) fp32), with the fp32 epilogue. The reference measures the same projection set as CUDA graphs
+(docs/benchmarks.md, "Projections against Microsoft's W2A8 GPU kernel"); here the 160 launches are one HIP graph.
+Weights are i.i.d. trits, P(-1) = P(+1) = 0.35, generated on the GPU, far larger than the 256 MB last-level cache,
+so every replay streams them from HBM. Inputs are resident in HBM when the timed region starts.
+
+Prints one JSON line (the driver's contract). `--gpus N` with N > 1 is refused: this build runs on one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Gweights/s + HBM GB/s (% of peak), Falcon3-10B decode GEMV; tok/s at bs=1"
+HBM_PEAK_GBPS = 8000.0
+LAYERS, HIDDEN, FFN, KV = 40, 3072, 23040, 1024
+# (name, rows, cols): the launches of one layer; q|k|v stacked, gate|up interleaved row by row.
+LAYER_SHAPES = [("qkv", HIDDEN + 2 * KV, HIDDEN), ("o", HIDDEN, HIDDEN), ("gate_up", 2 * FFN, HIDDEN),
+                ("down", HIDDEN, FFN)]
+REF_CPU_GWEIGHTS = 221.6  # quintrit_512, 4 threads, EPYC 9V45 (docs/benchmarks.md:77)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--layers", type=int, default=LAYERS, help=argparse.SUPPRESS)  # smoke runs only
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-breakdown", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def random_planar(torch, rows: int, cols: int, gen) -> "torch.Tensor":
+    """Planar velurex bytes (quintrit-core/src/pack.rs:66-131) of i.i.d. trits with P(-1)=P(+1)=0.35, on the GPU."""
+    nb = (cols + 159) // 160
+    out = torch.empty(rows * nb * 32, dtype=torch.uint8, device="cuda")
+    radix = torch.tensor([1, 3, 9, 28, 84], dtype=torch.int16, device="cuda").view(1, 1, 5, 1)
+    step = max(1, (1 << 26) // (nb * 160))
+    for r0 in range(0, rows, step):
+        r1 = min(rows, r0 + step)
+        u = torch.randint(0, 100, (r1 - r0, nb * 160), dtype=torch.int16, device="cuda", generator=gen)
+        d = (u >= 35).to(torch.int16) + (u >= 65).to(torch.int16)  # digit = trit + 1
+        if nb * 160 > cols:
+            d[:, cols:] = 1  # padding trits are zero
+        b = (d.view(r1 - r0, nb, 5, 32) * radix).sum(dim=2).to(torch.uint8)
+        out[r0 * nb * 32:r1 * nb * 32] = b.view(-1)
+    return out
+
+
+def quantize_i8(torch, x):
+    """Per-token absmax int8 (quintrit-runtime/src/ops.rs:241-267): s = 127/amax, q = round-half-away(x s)."""
+    amax = x.abs().max()
+    s = 127.0 / amax
+    v = x * s
+    q = torch.sign(v) * torch.floor(v.abs() + 0.5)
+    return q.clamp(-128, 127).to(torch.int8), float(s)
+
+
+class Stream:
+    """The 40-layer projection stream resident on the GPU."""
+
+    def __init__(self, torch, L, lib, layers: int):
+        self.torch, self.L, self.lib = torch, L, lib
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(0x5EED)
+        self.mats = []      # per layer: list of (name, handle, rows, cols)
+        self.inputs = []    # per layer: staged input per launch
+        self.outs = []
+        self.weights = 0
+        self.alg_bytes = 0
+        self.device_bytes = 0
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for li in range(layers):
+            row = []
+            ins = []
+            outs = []
+            for name, rows, cols in LAYER_SHAPES:
+                planar = random_planar(torch, rows, cols, gen)
+                h = ctypes.c_void_p()
+                lib.check(L.vx_matrix_create_dev(ctypes.c_void_p(planar.data_ptr()), planar.numel(), rows, cols,
+                                                 ctypes.c_float(0.02), ctypes.byref(h)))
+                del planar
+                x = torch.randn(cols, device="cuda", generator=gen, dtype=torch.float32)
+                q, s = quantize_i8(torch, x)
+                nbytes = lib.staged_bytes(cols)
+                staged = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+                lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(q.data_ptr()), cols, cols,
+                                              ctypes.c_void_p(staged.data_ptr()), nbytes, stream))
+                row.append((name, h, rows, cols))
+                ins.append((staged, nbytes, s))
+                outs.append(torch.empty(rows, dtype=torch.float32, device="cuda"))
+                self.weights += rows * cols
+                self.alg_bytes += rows * cols / 5.0
+                self.device_bytes += lib.layout(rows, cols)["device_bytes"]
+            self.mats.append(row)
+            self.inputs.append(ins)
+            self.outs.append(outs)
+        torch.cuda.synchronize()
+
+    def launch(self, li: int, k: int) -> None:
+        _, h, rows, _ = self.mats[li][k]
+        staged, nbytes, s = self.inputs[li][k]
+        out = self.outs[li][k]
+        st = self.L.vx_gemv_staged_f32_dev(h, ctypes.c_void_p(staged.data_ptr()), nbytes, ctypes.c_float(s),
+                                           ctypes.c_void_p(out.data_ptr()), rows,
+                                           ctypes.c_void_p(self.torch.cuda.current_stream().cuda_stream))
+        self.lib.check(st)
+
+    def step(self) -> None:
+        for li in range(len(self.mats)):
+            for k in range(len(LAYER_SHAPES)):
+                self.launch(li, k)
+
+    def free(self):
+        for row in self.mats:
+            for _, h, _, _ in row:
+                self.lib.check(self.L.vx_matrix_free(h))
+
+
+def capture(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # eager warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, steps: int, warmup: int):
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    t0.record()
+    for _ in range(steps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    return t0.elapsed_time(t1) / steps, wall
+
+
+def cpu_baseline(budget_s: float):
+    """The CPU oracle's restatement of the reference's table GEMV (oracle/velurex_oracle.c, avx512.rs:1526-1626
+    algorithm, scalar C, one thread) timed on this host over a bounded sample: the seven projections of one Falcon3-10B
+    layer in model order, repeated until the budget is used."""
+    import numpy as np
+    from oracle import oracle
+    L = oracle.lib()
+    shapes = [(HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN),
+              (HIDDEN, FFN)]
+    mats = []
+    for i, (r, c) in enumerate(shapes):
+        t = oracle.gen_trits(100 + i, (r, c))
+        planar = oracle.pack_matrix(t)
+        tiles = oracle.tile_rows(planar, r, c)
+        a = oracle.gen_i8(200 + i, c, -127, 127)
+        mats.append((np.ascontiguousarray(tiles), r, c, a, np.empty(r, np.int32)))
+    weights = 0
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for tiles, r, c, a, out in mats:
+            L.vxo_gemv_lut_tilerows(tiles.ctypes.data_as(ctypes.c_void_p), r, c, a.ctypes.data_as(ctypes.c_void_p),
+                                    out.ctypes.data_as(ctypes.c_void_p))
+            weights += r * c
+        reps += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(weights / dt / 1e9, 3), "unit": "Gweights/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} pass(es) over the 7 projections of one Falcon3-10B layer ({sum(r * c for _, r, c, _, _ in mats)} "
+                      f"weights/pass), scalar C restatement of the table kernel, 1 thread, {dt:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is described in "
+                                   "DESIGN.md, not built)"}))
+        return 2
+    import torch
+    from quintrit_amd import _lib
+    L = _lib.lib()
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU"}))
+        return 1
+    torch.cuda.set_device(0)
+    log(f"building the {args.layers}-layer weight stream on the GPU")
+    st = Stream(torch, L, _lib, args.layers)
+    log(f"{st.weights} weights, {st.alg_bytes / 1e9:.4f} GB algorithmic, {st.device_bytes / 1e9:.4f} GB device layout")
+    g = capture(torch, st.step)
+    log("graph captured; timing")
+    ms, wall = time_graph(torch, g, args.steps, args.warmup)
+    gw = st.weights / (ms / 1e3) / 1e9
+    gbps = st.alg_bytes / (ms / 1e3) / 1e9
+    log(f"{ms:.4f} ms/step, {gw:.1f} Gweights/s, {gbps:.1f} GB/s algorithmic, wall {wall / args.steps * 1e3:.4f} ms/step")
+
+    breakdown = {}
+    if not args.no_breakdown:
+        # Each launch type alone, rotated through all layers (distinct weights, so no cache reuse): average duration.
+        for k, (name, rows, cols) in enumerate(LAYER_SHAPES):
+            gk = capture(torch, lambda k=k: [st.launch(li, k) for li in range(len(st.mats))])
+            mk, _ = time_graph(torch, gk, max(3, args.steps // 5), 2)
+            per = mk / len(st.mats)
+            alg = rows * cols / 5.0
+            breakdown[name] = {"rows": rows, "cols": cols, "us_per_launch": round(per * 1e3, 3),
+                               "alg_GBps": round(alg / (per / 1e3) / 1e9, 1)}
+            log(f"  {name:8s} {rows}x{cols}: {per * 1e3:.2f} us/launch, {alg / (per / 1e3) / 1e9:.1f} GB/s")
+            del gk
+    dom = breakdown.get("gate_up")
+    if dom:
+        achieved = dom["alg_GBps"]
+        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                    "kernel": "gemv_lut_kernel (gate|up 46080x3072)",
+                    "alg_bytes_per_launch": int(2 * FFN * HIDDEN / 5)}
+    else:
+        roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                    "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "whole step"}
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline")
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']} Gweights/s")
+    st.free()
+    line = {
+        "metric": METRIC, "value": round(gw, 1), "unit": "Gweights/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": round(gw / REF_CPU_GWEIGHTS, 2), "dtype": "int32", "data": "synthetic",
+        "config": {"workload": "falcon3-10b-decode-projection-stream (BASELINE.json configs[1])", "layers": args.layers,
+                   "hidden": HIDDEN, "ffn": FFN, "kv_rows": KV, "batch": 1, "weights_per_step": st.weights,
+                   "launches_per_step": len(LAYER_SHAPES) * args.layers, "parallelism": "single-gpu"},
+        "hbm_alg_GBps": round(gbps, 1), "hbm_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
+        "device_layout_GBps": round(st.device_bytes / (ms / 1e3) / 1e9, 1),
+        "tok_s_projection_bound": round(1e3 / ms, 1),
+        "vs_baseline_ref": f"{REF_CPU_GWEIGHTS} Gweights/s, reference AVX-512 kernel, 4 threads (docs/benchmarks.md:77)",
+        "breakdown": breakdown, "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

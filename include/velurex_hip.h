@@ -1,0 +1,194 @@
+/*
+ * velurex_hip.h - C ABI of the MI355X (gfx950) velurex ternary GEMV library (libvelurex_hip.so).
+ *
+ * Ternary weights {-1, 0, +1} are stored five to a byte (velurex encoding, 1.60 bits per weight) and multiplied with
+ * int8 activations by hand-written CDNA4 HIP kernels. The integer products are exact (int32); the fp32 epilogue is the
+ * one of the reference's projection layers.
+ *
+ * This header replaces, for one GPU, the kernel-level entry points of the reference's C ABI
+ * (rust/crates/quintrit-c/include/quintrit.h:73-218) and the Rust trait the runtime calls
+ * (rust/crates/quintrit-runtime/src/layer.rs:72-87, TernaryGemvLayer). Each declaration below names the reference
+ * interface it stands in for.
+ *
+ * Conventions (the reference's, quintrit.h:11-22):
+ *   - Every function that can fail returns an int status: VX_OK (0) or a VX_ERR_* code. The codes have the values of
+ *     QUINTRIT_OK / QUINTRIT_ERR_* (quintrit.h:73-88), so a binding can forward them unchanged. On failure
+ *     vx_last_error_message() describes the failure (per thread).
+ *   - Every pointer argument is validated, every buffer comes with an explicit length, sizes are size_t. A NULL pointer,
+ *     an undersized buffer or a bad shape yields an error code, never a crash.
+ *   - Versioned structs start with a uint32_t struct_size the caller sets to sizeof(the struct).
+ *   - No C++ exception crosses the boundary.
+ *
+ * Device pointers and streams: functions with the suffix _dev take device pointers and a HIP stream (hipStream_t,
+ * passed as void*; NULL is the null stream); they enqueue work and return without waiting. Every other function takes
+ * host pointers and returns when the result is in host memory.
+ *
+ * Thread safety: functions are thread-safe on distinct matrix handles. A matrix handle owns a small device workspace
+ * (split-K accumulators and activation staging); calls on one handle must be ordered: either one stream per handle,
+ * or events between streams. The host-pointer functions serialise calls on one handle internally.
+ */
+#ifndef VELUREX_HIP_H
+#define VELUREX_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VX_VERSION_STRING "0.1.0"
+#define VX_ABI_VERSION 1
+
+/* ---- status codes: same values as quintrit.h:73-88 ----------------------------------------------------------------- */
+#define VX_OK                      0
+#define VX_ERR_NULL_POINTER        1
+#define VX_ERR_INVALID_ARGUMENT    2
+#define VX_ERR_INVALID_SHAPE       3
+#define VX_ERR_BUFFER_TOO_SMALL    4
+#define VX_ERR_INVALID_VALUE       5  /* a packed byte that is not one of the 243 velurex values */
+#define VX_ERR_UNSUPPORTED         6  /* no gfx950 device, or the library was built without it */
+#define VX_ERR_IO                  7
+#define VX_ERR_FORMAT              8
+#define VX_ERR_NOT_FOUND           9
+#define VX_ERR_MODEL              10
+#define VX_ERR_CONTEXT_OVERFLOW   11
+#define VX_ERR_BUSY               12
+#define VX_ERR_INTERNAL           13
+#define VX_ERR_INVALID_HANDLE     14
+#define VX_ERR_DEVICE             15  /* a HIP call failed (driver error, out of device memory) */
+
+/* Largest column count: keeps |sum| < 2^24 so float(acc) is exact (quintrit-core/src/limits.rs:7-19). */
+#define VX_MAX_GEMV_COLS 131072
+/* Largest row count accepted. */
+#define VX_MAX_ROWS ((size_t)1 << 31)
+
+/* Replaces quintrit_status_string (quintrit.h:91). Static string, never NULL. */
+const char* vx_status_string(int status);
+/* Replaces quintrit_last_error_code (quintrit.h:94). */
+int vx_last_error_code(void);
+/* Replaces quintrit_last_error_message (quintrit.h:100). Valid until the next vx_* call on the same thread. */
+const char* vx_last_error_message(void);
+/* Replaces quintrit_version / quintrit_abi_version (quintrit.h:107-110). */
+const char* vx_version(void);
+uint32_t vx_abi_version(void);
+
+/* Number of usable gfx950 devices (0 when there is none; the call itself succeeds). Counterpart of the reference's GPU
+ * queries (quintrit-c/src/cuda.rs). */
+int vx_device_count(int32_t* out_count);
+
+/* ---- layout ------------------------------------------------------------------------------------------------------------ */
+
+/*
+ * Device layout of a rows x cols matrix. The interchange format is the planar layout of the reference
+ * (quintrit-core/src/pack.rs:10-16: a row is ceil(cols/160) blocks of 32 bytes; byte j of block b packs columns
+ * b*160 + p*32 + j, p = 0..4). On upload each row is re-encoded with the packed tail of pack.rs:212-276 (the partial
+ * last block stored five trits per byte, tile_row_bytes(cols) bytes), padded to a multiple of 16 bytes, and rows are
+ * grouped in tiles of 64: byte c of row r lives at tile(r)*64*device_row_bytes + (c/16)*1024 + (r%64)*16 + c%16.
+ * Counterpart of quintrit_tiled_layout_t (quintrit.h:181-196).
+ */
+typedef struct vx_layout {
+    uint32_t struct_size;       /* set to sizeof(vx_layout_t) */
+    uint32_t tile_rows;         /* 64 */
+    uint64_t rows;
+    uint64_t cols;
+    uint64_t padded_rows;       /* rows rounded up to a multiple of 64 */
+    uint64_t planar_row_bytes;  /* ceil(cols/160) * 32: bytes of one row of the interchange (planar) format */
+    uint64_t tile_row_bytes;    /* bytes of one row with the packed tail (pack.rs:222-225) */
+    uint64_t device_row_bytes;  /* tile_row_bytes rounded up to 16 */
+    uint64_t device_bytes;      /* padded_rows * device_row_bytes */
+} vx_layout_t;
+
+/* Replaces quintrit_tiled_layout (quintrit.h:199). rows and cols must be in [1, 2^31] and cols <= VX_MAX_GEMV_COLS. */
+int vx_layout(size_t rows, size_t cols, vx_layout_t* out_layout);
+
+/*
+ * Host-side conversion of a planar matrix into the device layout (out_capacity >= device_bytes of vx_layout). Checks
+ * every byte like vx_matrix_create. Counterpart of quintrit_pack_matrix's tiling step (quintrit.h:222-224) for the
+ * device layout; vx_matrix_create performs the same conversion.
+ */
+int vx_device_layout_pack(const uint8_t* planar, size_t planar_len, size_t rows, size_t cols, uint8_t* out,
+                          size_t out_capacity);
+
+/* ---- matrix handles (weights resident in HBM) ------------------------------------------------------------------------ */
+
+typedef struct vx_matrix vx_matrix_t;
+
+/*
+ * Uploads a planar velurex matrix (planar_len >= rows * planar_row_bytes) to the current HIP device and returns an owned
+ * handle. Every byte is checked: a byte outside the 243 velurex values gives VX_ERR_INVALID_VALUE. weight_scale is the
+ * per-tensor scale alpha of TernaryGemvLayer::weight_scale (layer.rs:86). Stands in for the construction of a
+ * QuintritLutAVX512Layer (layer.rs:192-203) plus the upload the GPU path does (quintrit-runtime/src/gpu.rs:183-260).
+ */
+int vx_matrix_create(const uint8_t* planar, size_t planar_len, size_t rows, size_t cols, float weight_scale,
+                     vx_matrix_t** out_matrix);
+/*
+ * As vx_matrix_create, with the planar bytes already in device memory (planar_dev on the current device). The layout
+ * transform and the byte check run on the GPU; the call returns when the handle is ready. The planar buffer is not
+ * kept. Counterpart of the upload of planar weights in the reference's GPU path (quintrit-runtime/src/gpu.rs:120-138).
+ */
+int vx_matrix_create_dev(const uint8_t* planar_dev, size_t planar_len, size_t rows, size_t cols, float weight_scale,
+                         vx_matrix_t** out_matrix);
+/* Frees a handle (NULL is a no-op). */
+int vx_matrix_free(vx_matrix_t* matrix);
+/* TernaryGemvLayer::shape (layer.rs:83). */
+int vx_matrix_shape(const vx_matrix_t* matrix, size_t* out_rows, size_t* out_cols);
+/* TernaryGemvLayer::memory_bytes (layer.rs:80): bytes of the weights in device memory. */
+int vx_matrix_memory_bytes(const vx_matrix_t* matrix, size_t* out_bytes);
+/* TernaryGemvLayer::weight_scale (layer.rs:86). */
+int vx_matrix_weight_scale(const vx_matrix_t* matrix, float* out_scale);
+/* Device address of the weights in the layout of vx_layout (for callers that fuse their own kernels). */
+int vx_matrix_device_weights(const vx_matrix_t* matrix, const void** out_ptr);
+
+/* ---- GEMV ------------------------------------------------------------------------------------------------------------ */
+
+/*
+ * Integer GEMV on device memory: out[i] = sum_j W[i][j] * acts[j] for i < rows, exact for the whole int8 range.
+ * acts_len >= cols, out_capacity >= rows. Enqueued on `stream`. Device counterpart of quintrit_gemv_i32
+ * (quintrit.h:208-210).
+ */
+int vx_gemv_i32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, int32_t* out, size_t out_capacity,
+                    void* stream);
+
+/*
+ * Dequantised GEMV on device memory with the layers' epilogue (layer.rs:246-253): post = weight_scale / act_scale
+ * (one fp32 division), out[i] = float(acc[i]) * post; act_scale <= 0 (or NaN) gives zeros.
+ */
+int vx_gemv_f32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, float act_scale, float* out,
+                    size_t out_capacity, void* stream);
+
+/*
+ * Staged activations: the GEMV kernels read the activations of each device byte-column as two dwords (the activations
+ * of its five trits, a0..a3 packed and a4), staged once per input vector and shareable by every matrix with the same
+ * cols (Q, K and V share one input, gate and up another). vx_staged_bytes gives the size of the staging buffer.
+ * The reference stages its GPU inputs the same way, one permuted entry per byte-column (quintrit-cuda/src/pack.rs:75-85).
+ */
+int vx_staged_bytes(size_t cols, size_t* out_bytes);
+int vx_stage_acts_dev(const int8_t* acts, size_t acts_len, size_t cols, void* staged, size_t staged_capacity,
+                      void* stream);
+/* GEMVs on staged activations (staged by vx_stage_acts_dev for the matrix's cols); same results as the _dev calls. */
+int vx_gemv_staged_i32_dev(const vx_matrix_t* matrix, const void* staged, size_t staged_len, int32_t* out,
+                           size_t out_capacity, void* stream);
+int vx_gemv_staged_f32_dev(const vx_matrix_t* matrix, const void* staged, size_t staged_len, float act_scale, float* out,
+                           size_t out_capacity, void* stream);
+
+/*
+ * TernaryGemvLayer::forward (layer.rs:74) on host memory: acts (acts_len >= cols) and out (out_capacity >= rows) are
+ * host buffers; the call returns when out holds y = alpha * beta * (W x) with the epilogue of vx_gemv_f32_dev.
+ */
+int vx_layer_forward(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, float act_scale, float* out,
+                     size_t out_capacity);
+
+/*
+ * One-shot host GEMVs with the argument order of quintrit_gemv_i32 / quintrit_gemv_f32 (quintrit.h:208-218), for the
+ * planar layout: the weights are uploaded, multiplied and freed in the call. quintrit_gemv_f32's out = scale * acc.
+ */
+int vx_gemv_planar_i32(const uint8_t* weights, size_t weights_len, size_t rows, size_t cols, const int8_t* acts,
+                       size_t acts_len, int32_t* out, size_t out_capacity);
+int vx_gemv_planar_f32(const uint8_t* weights, size_t weights_len, size_t rows, size_t cols, const int8_t* acts,
+                       size_t acts_len, float scale, float* out, size_t out_capacity);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

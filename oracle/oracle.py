@@ -1,0 +1,271 @@
+"""numpy front end of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg import this module, as the checker or
+the timed CPU baseline. The product never imports it. The C sources (velurex_oracle.c) cite the reference file:line
+each function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "libvelurex_oracle.so")
+
+_lib = None
+
+
+def build() -> None:
+    """Compiles the oracle with gcc (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    vp, sz, u8, f32, u64, uint = (ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint8, ctypes.c_float,
+                                  ctypes.c_uint64, ctypes.c_uint)
+    sig = {
+        "vxo_pack_5trits": (u8, [vp]),
+        "vxo_byte_to_trits": (None, [u8, vp]),
+        "vxo_byte_is_valid": (ctypes.c_int, [u8]),
+        "vxo_planar_row_bytes": (sz, [sz]),
+        "vxo_pack_matrix": (None, [vp, sz, sz, vp]),
+        "vxo_unpack_matrix": (None, [vp, sz, sz, vp]),
+        "vxo_tile_full_columns": (sz, [sz]),
+        "vxo_tile_row_bytes": (sz, [sz]),
+        "vxo_column_activation_index": (sz, [sz, sz, sz]),
+        "vxo_tile_byte": (u8, [vp, sz, sz]),
+        "vxo_untile_row": (None, [vp, sz, vp]),
+        "vxo_split_hi_lo": (None, [vp, sz, vp, vp]),
+        "vxo_wide_lut_len": (sz, [sz]),
+        "vxo_build_compact_wide_lut": (None, [vp, sz, vp]),
+        "vxo_decode_u_l": (None, [u8, vp, vp]),
+        "vxo_gemv_lut_tilerows": (None, [vp, sz, sz, vp, vp]),
+        "vxo_gemv_lut_planar": (None, [vp, sz, sz, vp, vp]),
+        "vxo_tile_rows": (None, [vp, sz, sz, vp]),
+        "vxo_gemv_bruteforce": (None, [vp, sz, sz, vp, vp]),
+        "vxo_epilogue_f32": (None, [vp, sz, f32, f32, vp]),
+        "vxo_scale_f32": (None, [vp, sz, f32, vp]),
+        "vxo_quantize_i8": (f32, [vp, sz, f32, vp]),
+        "vxo_quantize_q8_0": (None, [vp, sz, vp, vp]),
+        "vxo_f32_to_f16": (ctypes.c_uint16, [f32]),
+        "vxo_f16_to_f32": (f32, [ctypes.c_uint16]),
+        "vxo_rms_norm": (None, [vp, vp, sz, f32, vp]),
+        "vxo_q2_0_dot_row": (f32, [vp, vp, vp, vp, sz]),
+        "vxo_q2_0_gemv": (None, [vp, vp, vp, vp, sz, sz, vp]),
+        "vxo_q2_0_lane_sums": (None, [vp, vp, sz, sz, vp]),
+        "vxo_gen_trits": (None, [u64, sz, uint, uint, vp]),
+        "vxo_gen_i8": (None, [u64, sz, ctypes.c_int, ctypes.c_int, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+# ---- encoding ----------------------------------------------------------------------------------------------------
+
+def pack_5trits(t) -> int:
+    a = np.ascontiguousarray(t, dtype=np.int8)
+    return int(lib().vxo_pack_5trits(_p(a)))
+
+
+def byte_to_trits(b: int) -> np.ndarray:
+    out = np.zeros(5, np.int8)
+    lib().vxo_byte_to_trits(b, _p(out))
+    return out
+
+
+def byte_is_valid(b: int) -> bool:
+    return bool(lib().vxo_byte_is_valid(b))
+
+
+def planar_row_bytes(cols: int) -> int:
+    return int(lib().vxo_planar_row_bytes(cols))
+
+
+def pack_matrix(trits: np.ndarray) -> np.ndarray:
+    """Planar velurex bytes of a rows x cols trit matrix (rows x planar_row_bytes)."""
+    t = np.ascontiguousarray(trits, dtype=np.int8)
+    rows, cols = t.shape
+    out = np.empty((rows, planar_row_bytes(cols)), np.uint8)
+    lib().vxo_pack_matrix(_p(t), rows, cols, _p(out))
+    return out
+
+
+def unpack_matrix(packed: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    out = np.zeros((rows, cols), np.int8)
+    lib().vxo_unpack_matrix(_p(p), rows, cols, _p(out))
+    return out
+
+
+def tile_full_columns(cols: int) -> int:
+    return int(lib().vxo_tile_full_columns(cols))
+
+
+def tile_row_bytes(cols: int) -> int:
+    return int(lib().vxo_tile_row_bytes(cols))
+
+
+def column_activation_index(cols: int, c: int, p: int) -> int:
+    return int(lib().vxo_column_activation_index(cols, c, p))
+
+
+def tile_row(planar_row: np.ndarray, cols: int) -> np.ndarray:
+    r = np.ascontiguousarray(planar_row, dtype=np.uint8)
+    return np.array([lib().vxo_tile_byte(_p(r), cols, c) for c in range(tile_row_bytes(cols))], np.uint8)
+
+
+def tile_rows(planar: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    p = np.ascontiguousarray(planar, dtype=np.uint8)
+    out = np.empty((rows, tile_row_bytes(cols)), np.uint8)
+    lib().vxo_tile_rows(_p(p), rows, cols, _p(out))
+    return out
+
+
+def untile_row(tile_row_bytes_: np.ndarray, cols: int) -> np.ndarray:
+    t = np.ascontiguousarray(tile_row_bytes_, dtype=np.uint8)
+    out = np.zeros(planar_row_bytes(cols), np.uint8)
+    lib().vxo_untile_row(_p(t), cols, _p(out))
+    return out
+
+
+# ---- tables and GEMV ----------------------------------------------------------------------------------------------
+
+def split_hi_lo(acts: np.ndarray):
+    a = np.ascontiguousarray(acts, dtype=np.int8)
+    hi = np.empty_like(a)
+    lo = np.empty_like(a)
+    lib().vxo_split_hi_lo(_p(a), a.size, _p(hi), _p(lo))
+    return hi, lo
+
+
+def build_compact_wide_lut(acts: np.ndarray, cols: int) -> np.ndarray:
+    a = np.ascontiguousarray(acts, dtype=np.int8)
+    out = np.empty(int(lib().vxo_wide_lut_len(cols)), np.int8)
+    lib().vxo_build_compact_wide_lut(_p(a), cols, _p(out))
+    return out
+
+
+def decode_u_l(b: int):
+    u = ctypes.c_uint8()
+    l = ctypes.c_uint8()
+    lib().vxo_decode_u_l(b, ctypes.byref(u), ctypes.byref(l))
+    return u.value, l.value
+
+
+def gemv_lut_planar(planar: np.ndarray, rows: int, cols: int, acts: np.ndarray) -> np.ndarray:
+    p = np.ascontiguousarray(planar, dtype=np.uint8)
+    a = np.ascontiguousarray(acts, dtype=np.int8)
+    out = np.empty(rows, np.int32)
+    lib().vxo_gemv_lut_planar(_p(p), rows, cols, _p(a), _p(out))
+    return out
+
+
+def gemv_bruteforce(trits: np.ndarray, acts: np.ndarray) -> np.ndarray:
+    t = np.ascontiguousarray(trits, dtype=np.int8)
+    a = np.ascontiguousarray(acts, dtype=np.int8)
+    rows, cols = t.shape
+    out = np.empty(rows, np.int64)
+    lib().vxo_gemv_bruteforce(_p(t), rows, cols, _p(a), _p(out))
+    return out
+
+
+def epilogue_f32(acc: np.ndarray, weight_scale: float, act_scale: float) -> np.ndarray:
+    a = np.ascontiguousarray(acc, dtype=np.int32)
+    out = np.empty(a.size, np.float32)
+    lib().vxo_epilogue_f32(_p(a), a.size, weight_scale, act_scale, _p(out))
+    return out
+
+
+def scale_f32(acc: np.ndarray, scale: float) -> np.ndarray:
+    a = np.ascontiguousarray(acc, dtype=np.int32)
+    out = np.empty(a.size, np.float32)
+    lib().vxo_scale_f32(_p(a), a.size, scale, _p(out))
+    return out
+
+
+# ---- quantizers, norms ---------------------------------------------------------------------------------------------
+
+def quantize_i8(x: np.ndarray, levels: float = 127.0):
+    v = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(v.size, np.int8)
+    s = lib().vxo_quantize_i8(_p(v), v.size, levels, _p(q))
+    return q, float(np.float32(s))
+
+
+def quantize_q8_0(x: np.ndarray):
+    v = np.ascontiguousarray(x, dtype=np.float32)
+    qs = np.empty(v.size, np.int8)
+    d = np.empty(v.size // 32, np.float32)
+    lib().vxo_quantize_q8_0(_p(v), v.size, _p(qs), _p(d))
+    return qs, d
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return int(lib().vxo_f32_to_f16(x))
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return float(lib().vxo_f16_to_f32(h))
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    xv = np.ascontiguousarray(x, dtype=np.float32)
+    wv = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(xv)
+    lib().vxo_rms_norm(_p(xv), _p(wv), xv.size, eps, _p(out))
+    return out
+
+
+# ---- Q2_0 -------------------------------------------------------------------------------------------------------
+
+def q2_0_gemv(packed: np.ndarray, w_scales: np.ndarray, acts: np.ndarray, a_scales: np.ndarray, rows: int,
+              cols: int) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    ws = np.ascontiguousarray(w_scales, dtype=np.float32)
+    a = np.ascontiguousarray(acts, dtype=np.int8)
+    as_ = np.ascontiguousarray(a_scales, dtype=np.float32)
+    out = np.empty(rows, np.float32)
+    lib().vxo_q2_0_gemv(_p(p), _p(ws), _p(a), _p(as_), rows, cols, _p(out))
+    return out
+
+
+def q2_0_lane_sums(packed: np.ndarray, acts: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    p = np.ascontiguousarray(packed, dtype=np.uint8)
+    a = np.ascontiguousarray(acts, dtype=np.int8)
+    out = np.empty((rows, cols // 32, 8), np.int32)
+    lib().vxo_q2_0_lane_sums(_p(p), _p(a), rows, cols, _p(out))
+    return out
+
+
+# ---- generators ----------------------------------------------------------------------------------------------------
+
+def gen_trits(seed: int, shape, p_minus: int = 35, p_zero: int = 30) -> np.ndarray:
+    n = int(np.prod(shape))
+    out = np.empty(n, np.int8)
+    lib().vxo_gen_trits(seed, n, p_minus, p_zero, _p(out))
+    return out.reshape(shape)
+
+
+def gen_i8(seed: int, n: int, lo: int = -127, hi: int = 127) -> np.ndarray:
+    out = np.empty(n, np.int8)
+    lib().vxo_gen_i8(seed, n, lo, hi, _p(out))
+    return out

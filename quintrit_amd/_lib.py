@@ -1,0 +1,123 @@
+"""ctypes binding of libvelurex_hip.so (include/velurex_hip.h).
+
+The library is the product: there is no CPU fallback. Importing a compute entry point without the built library, or
+calling one without a gfx950 GPU, raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvelurex_hip.so")
+
+VX_OK = 0
+STATUS_NAMES = {
+    0: "VX_OK", 1: "VX_ERR_NULL_POINTER", 2: "VX_ERR_INVALID_ARGUMENT", 3: "VX_ERR_INVALID_SHAPE",
+    4: "VX_ERR_BUFFER_TOO_SMALL", 5: "VX_ERR_INVALID_VALUE", 6: "VX_ERR_UNSUPPORTED", 7: "VX_ERR_IO",
+    8: "VX_ERR_FORMAT", 9: "VX_ERR_NOT_FOUND", 10: "VX_ERR_MODEL", 11: "VX_ERR_CONTEXT_OVERFLOW",
+    12: "VX_ERR_BUSY", 13: "VX_ERR_INTERNAL", 14: "VX_ERR_INVALID_HANDLE", 15: "VX_ERR_DEVICE",
+}
+
+
+class VxError(RuntimeError):
+    """A vx_* call returned a status other than VX_OK."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+class _Layout(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("tile_rows", ctypes.c_uint32), ("rows", ctypes.c_uint64),
+                ("cols", ctypes.c_uint64), ("padded_rows", ctypes.c_uint64), ("planar_row_bytes", ctypes.c_uint64),
+                ("tile_row_bytes", ctypes.c_uint64), ("device_row_bytes", ctypes.c_uint64),
+                ("device_bytes", ctypes.c_uint64)]
+
+
+_lib = None
+
+# name -> (restype, argtypes); every symbol include/velurex_hip.h declares.
+_vp, _sz, _f32, _i32 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float, ctypes.c_int
+SIGNATURES = {
+    "vx_status_string": (ctypes.c_char_p, [_i32]),
+    "vx_last_error_code": (_i32, []),
+    "vx_last_error_message": (ctypes.c_char_p, []),
+    "vx_version": (ctypes.c_char_p, []),
+    "vx_abi_version": (ctypes.c_uint32, []),
+    "vx_device_count": (_i32, [_vp]),
+    "vx_layout": (_i32, [_sz, _sz, _vp]),
+    "vx_device_layout_pack": (_i32, [_vp, _sz, _sz, _sz, _vp, _sz]),
+    "vx_matrix_create": (_i32, [_vp, _sz, _sz, _sz, _f32, _vp]),
+    "vx_matrix_create_dev": (_i32, [_vp, _sz, _sz, _sz, _f32, _vp]),
+    "vx_matrix_free": (_i32, [_vp]),
+    "vx_matrix_shape": (_i32, [_vp, _vp, _vp]),
+    "vx_matrix_memory_bytes": (_i32, [_vp, _vp]),
+    "vx_matrix_weight_scale": (_i32, [_vp, _vp]),
+    "vx_matrix_device_weights": (_i32, [_vp, _vp]),
+    "vx_gemv_i32_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "vx_gemv_f32_dev": (_i32, [_vp, _vp, _sz, _f32, _vp, _sz, _vp]),
+    "vx_staged_bytes": (_i32, [_sz, _vp]),
+    "vx_stage_acts_dev": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
+    "vx_gemv_staged_i32_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "vx_gemv_staged_f32_dev": (_i32, [_vp, _vp, _sz, _f32, _vp, _sz, _vp]),
+    "vx_layer_forward": (_i32, [_vp, _vp, _sz, _f32, _vp, _sz]),
+    "vx_gemv_planar_i32": (_i32, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz]),
+    "vx_gemv_planar_f32": (_i32, [_vp, _sz, _sz, _sz, _vp, _sz, _f32, _vp, _sz]),
+}
+
+
+def lib() -> ctypes.CDLL:
+    """Loads the HIP library; raises if it was not built (there is no fallback)."""
+    global _lib
+    if _lib is None:
+        try:  # one HIP runtime per process: torch's, when torch is present (it is matched by soname)
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() (or make -C "
+                               f"quintrit_amd/csrc); there is no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != VX_OK:
+        msg = lib().vx_last_error_message()
+        raise VxError(status, msg.decode() if msg else "")
+
+
+def layout(rows: int, cols: int) -> dict:
+    lay = _Layout()
+    lay.struct_size = ctypes.sizeof(_Layout)
+    check(lib().vx_layout(rows, cols, ctypes.byref(lay)))
+    return {name: getattr(lay, name) for name, _ in _Layout._fields_ if name != "struct_size"}
+
+
+def device_layout_pack(planar, rows: int, cols: int):
+    """Host conversion of planar bytes into the device layout (vx_device_layout_pack)."""
+    import numpy as np
+    p = np.ascontiguousarray(planar, dtype=np.uint8).reshape(-1)
+    n = layout(rows, cols)["device_bytes"]
+    out = np.empty(n, np.uint8)
+    check(lib().vx_device_layout_pack(p.ctypes.data_as(ctypes.c_void_p), p.size, rows, cols,
+                                      out.ctypes.data_as(ctypes.c_void_p), out.size))
+    return out
+
+
+def staged_bytes(cols: int) -> int:
+    n = ctypes.c_size_t()
+    check(lib().vx_staged_bytes(cols, ctypes.byref(n)))
+    return n.value
+
+
+def device_count() -> int:
+    n = ctypes.c_int32()
+    check(lib().vx_device_count(ctypes.byref(n)))
+    return n.value

@@ -1,0 +1,464 @@
+// C ABI of libvelurex_hip (include/velurex_hip.h): argument checks, the per-thread error slot and the matrix handles.
+// Error conventions follow the reference's C ABI (quintrit-c/src/error.rs:8-80, quintrit-c/src/tiles.rs:192-228).
+#include "vx_internal.h"
+
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+namespace vx {
+
+int launch_gemv(vx_matrix* m, const int8_t* acts, void* out, bool out_f32, float post, hipStream_t stream);
+int launch_stage(const int8_t* acts, size_t cols, uint2* staged, hipStream_t stream);
+int launch_gemv_staged(vx_matrix* m, const uint2* staged, void* out, bool out_f32, float post, hipStream_t stream);
+int launch_device_layout(const uint8_t* planar_dev, const Geometry& g, uint8_t* dst, hipStream_t stream);
+int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
+int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
+size_t find_invalid_byte(const uint8_t* planar, size_t n);
+void planar_to_device_layout(const uint8_t* planar, const Geometry& g, uint8_t* dst);
+
+static thread_local Error t_error{VX_OK, std::string()};
+
+void set_error(int code, const std::string& msg) {
+    t_error.code = code;
+    t_error.msg = msg;
+}
+
+void clear_error() {
+    t_error.code = VX_OK;
+    t_error.msg.clear();
+}
+
+int check_shape(size_t rows, size_t cols) {
+    if (rows == 0 || rows > VX_MAX_ROWS) VX_FAIL(VX_ERR_INVALID_SHAPE, "rows must be in 1..=%zu (got %zu)", (size_t)VX_MAX_ROWS, rows);
+    if (cols == 0) VX_FAIL(VX_ERR_INVALID_SHAPE, "cols must be at least 1");
+    if (cols > VX_MAX_GEMV_COLS)
+        VX_FAIL(VX_ERR_INVALID_SHAPE, "cols = %zu exceeds %d, the largest count for which the accumulators are exact", cols,
+                VX_MAX_GEMV_COLS);
+    return VX_OK;
+}
+
+int device_info(DeviceInfo* out) {
+    int dev = 0;
+    VX_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    VX_HIP(hipGetDeviceProperties(&prop, dev));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "device %d is %s; this library is built for gfx950 (MI355X) only", dev, prop.gcnArchName);
+    out->device = dev;
+    out->num_cus = prop.multiProcessorCount;
+    return VX_OK;
+}
+
+static int check_matrix(const vx_matrix_t* m) {
+    if (m == nullptr) VX_FAIL(VX_ERR_INVALID_HANDLE, "matrix handle is NULL");
+    if (m->magic != kMatrixMagic) VX_FAIL(VX_ERR_INVALID_HANDLE, "matrix handle is not valid (freed or foreign)");
+    return VX_OK;
+}
+
+static int set_device_of(const vx_matrix_t* m) {
+    int cur = -1;
+    VX_HIP(hipGetDevice(&cur));
+    if (cur != m->device) VX_HIP(hipSetDevice(m->device));
+    return VX_OK;
+}
+
+static void destroy(vx_matrix* m) {
+    if (m->d_w) (void)hipFree(m->d_w);
+    if (m->d_acc) (void)hipFree(m->d_acc);
+    if (m->d_cnt) (void)hipFree(m->d_cnt);
+    if (m->d_actp) (void)hipFree(m->d_actp);
+    if (m->d_io) (void)hipFree(m->d_io);
+    m->magic = 0;
+    delete m;
+}
+
+static int check_planar(const uint8_t* planar, size_t planar_len, size_t rows, size_t cols) {
+    VX_TRY(check_shape(rows, cols));
+    if (planar == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "planar is NULL");
+    const size_t need = rows * planar_row_bytes(cols);
+    if (planar_len < need)
+        VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "planar holds %zu bytes but a %zu x %zu matrix needs %zu", planar_len, rows, cols, need);
+    return VX_OK;
+}
+
+// Allocates a handle and its device buffers (weights left uninitialised).
+static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix** out) {
+    DeviceInfo di;
+    VX_TRY(device_info(&di));
+    vx_matrix* m = new vx_matrix();
+    m->magic = kMatrixMagic;
+    m->g = geometry(rows, cols);
+    m->weight_scale = weight_scale;
+    m->device = di.device;
+    m->num_cus = di.num_cus;
+    m->d_w = nullptr;
+    m->d_acc = nullptr;
+    m->d_cnt = nullptr;
+    m->d_actp = nullptr;
+    m->d_io = nullptr;
+
+    const size_t io_bytes = round_up(cols, 256) + m->g.padded_rows * 4;
+    hipError_t e = hipMalloc(&m->d_w, m->g.device_bytes);
+    if (e == hipSuccess) e = hipMalloc(&m->d_acc, m->g.padded_rows * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(&m->d_cnt, m->g.n_tiles * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&m->d_actp, m->g.dbr * sizeof(uint2));
+    if (e == hipSuccess) e = hipMalloc(&m->d_io, io_bytes);
+    if (e == hipSuccess) e = hipMemset(m->d_acc, 0, m->g.padded_rows * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMemset(m->d_cnt, 0, m->g.n_tiles * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        const size_t bytes = m->g.device_bytes;
+        destroy(m);
+        VX_FAIL(VX_ERR_DEVICE, "device allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+    }
+    *out = m;
+    return VX_OK;
+}
+
+static int create_matrix(const uint8_t* planar, size_t planar_len, size_t rows, size_t cols, float weight_scale,
+                         vx_matrix_t** out) {
+    if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_matrix is NULL");
+    *out = nullptr;
+    VX_TRY(check_planar(planar, planar_len, rows, cols));
+    const size_t need = rows * planar_row_bytes(cols);
+    const size_t bad = find_invalid_byte(planar, need);
+    if (bad != SIZE_MAX)
+        VX_FAIL(VX_ERR_INVALID_VALUE, "byte %zu (value %u) is not a velurex byte", bad, static_cast<unsigned>(planar[bad]));
+    vx_matrix* m = nullptr;
+    VX_TRY(alloc_matrix(rows, cols, weight_scale, &m));
+    std::vector<uint8_t> host(m->g.device_bytes);
+    planar_to_device_layout(planar, m->g, host.data());
+    hipError_t e = hipMemcpy(m->d_w, host.data(), m->g.device_bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        destroy(m);
+        VX_FAIL(VX_ERR_DEVICE, "upload failed: %s", hipGetErrorString(e));
+    }
+    *out = m;
+    return VX_OK;
+}
+
+static int create_matrix_dev(const uint8_t* planar_dev, size_t planar_len, size_t rows, size_t cols, float weight_scale,
+                             vx_matrix_t** out) {
+    if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_matrix is NULL");
+    *out = nullptr;
+    VX_TRY(check_planar(planar_dev, planar_len, rows, cols));
+    const size_t need = rows * planar_row_bytes(cols);
+    vx_matrix* m = nullptr;
+    VX_TRY(alloc_matrix(rows, cols, weight_scale, &m));
+    unsigned long long* d_first = nullptr;
+    unsigned long long first = ~0ull;
+    hipError_t e = hipMalloc(&d_first, sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMemcpy(d_first, &first, sizeof first, hipMemcpyHostToDevice);
+    int st = VX_OK;
+    if (e == hipSuccess) st = launch_find_invalid(planar_dev, need, d_first, nullptr);
+    if (e == hipSuccess && st == VX_OK) st = launch_device_layout(planar_dev, m->g, m->d_w, nullptr);
+    if (e == hipSuccess && st == VX_OK) e = hipMemcpy(&first, d_first, sizeof first, hipMemcpyDeviceToHost);
+    if (d_first) (void)hipFree(d_first);
+    if (st != VX_OK || e != hipSuccess) {
+        destroy(m);
+        if (st != VX_OK) return st;
+        VX_FAIL(VX_ERR_DEVICE, "device layout transform failed: %s", hipGetErrorString(e));
+    }
+    if (first != ~0ull) {
+        destroy(m);
+        VX_FAIL(VX_ERR_INVALID_VALUE, "byte %llu is not a velurex byte", first);
+    }
+    *out = m;
+    return VX_OK;
+}
+
+static int check_io(const vx_matrix_t* m, const void* acts, size_t acts_len, const void* out, size_t out_capacity) {
+    if (acts == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "activations is NULL");
+    if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out is NULL");
+    if (acts_len < m->g.cols)
+        VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "activations hold %zu values but cols = %zu", acts_len, m->g.cols);
+    if (out_capacity < m->g.rows)
+        VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "output holds %zu values but rows = %zu", out_capacity, m->g.rows);
+    return VX_OK;
+}
+
+// out = float(acc) * (ws / as); zeros when as <= 0 or NaN (layer.rs:246-253).
+static int gemv_f32_dev(vx_matrix* m, const int8_t* acts, float act_scale, float* out, hipStream_t s) {
+    if (act_scale > 0.0f) return launch_gemv(m, acts, out, true, m->weight_scale / act_scale, s);
+    return launch_fill_f32(out, m->g.rows, 0.0f, s);
+}
+
+}  // namespace vx
+
+using namespace vx;
+
+extern "C" {
+
+const char* vx_status_string(int status) {
+    switch (status) {
+        case VX_OK: return "ok";
+        case VX_ERR_NULL_POINTER: return "null pointer";
+        case VX_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case VX_ERR_INVALID_SHAPE: return "invalid shape";
+        case VX_ERR_BUFFER_TOO_SMALL: return "buffer too small";
+        case VX_ERR_INVALID_VALUE: return "invalid value";
+        case VX_ERR_UNSUPPORTED: return "unsupported";
+        case VX_ERR_IO: return "i/o error";
+        case VX_ERR_FORMAT: return "format error";
+        case VX_ERR_NOT_FOUND: return "not found";
+        case VX_ERR_MODEL: return "model error";
+        case VX_ERR_CONTEXT_OVERFLOW: return "context overflow";
+        case VX_ERR_BUSY: return "busy";
+        case VX_ERR_INTERNAL: return "internal error";
+        case VX_ERR_INVALID_HANDLE: return "invalid handle";
+        case VX_ERR_DEVICE: return "device error";
+        default: return "unknown status";
+    }
+}
+
+int vx_last_error_code(void) { return t_error.code; }
+const char* vx_last_error_message(void) { return t_error.msg.c_str(); }
+const char* vx_version(void) { return VX_VERSION_STRING; }
+uint32_t vx_abi_version(void) { return VX_ABI_VERSION; }
+
+int vx_device_count(int32_t* out_count) {
+    return guard([&]() -> int {
+        if (out_count == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_count is NULL");
+        *out_count = 0;
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess) {
+            (void)hipGetLastError();
+            return VX_OK;
+        }
+        int32_t c = 0;
+        for (int d = 0; d < n; ++d) {
+            hipDeviceProp_t prop;
+            if (hipGetDeviceProperties(&prop, d) == hipSuccess && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ++c;
+        }
+        *out_count = c;
+        return VX_OK;
+    });
+}
+
+int vx_layout(size_t rows, size_t cols, vx_layout_t* out_layout) {
+    return guard([&]() -> int {
+        if (out_layout == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_layout is NULL");
+        if (out_layout->struct_size != sizeof(vx_layout_t))
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "struct_size is %u, expected %zu", out_layout->struct_size, sizeof(vx_layout_t));
+        VX_TRY(check_shape(rows, cols));
+        const Geometry g = geometry(rows, cols);
+        out_layout->tile_rows = kTileRows;
+        out_layout->rows = rows;
+        out_layout->cols = cols;
+        out_layout->padded_rows = g.padded_rows;
+        out_layout->planar_row_bytes = planar_row_bytes(cols);
+        out_layout->tile_row_bytes = g.tbr;
+        out_layout->device_row_bytes = g.dbr;
+        out_layout->device_bytes = g.device_bytes;
+        return VX_OK;
+    });
+}
+
+int vx_matrix_create(const uint8_t* planar, size_t planar_len, size_t rows, size_t cols, float weight_scale,
+                     vx_matrix_t** out_matrix) {
+    return guard([&]() -> int { return create_matrix(planar, planar_len, rows, cols, weight_scale, out_matrix); });
+}
+
+int vx_matrix_create_dev(const uint8_t* planar_dev, size_t planar_len, size_t rows, size_t cols, float weight_scale,
+                         vx_matrix_t** out_matrix) {
+    return guard([&]() -> int { return create_matrix_dev(planar_dev, planar_len, rows, cols, weight_scale, out_matrix); });
+}
+
+int vx_device_layout_pack(const uint8_t* planar, size_t planar_len, size_t rows, size_t cols, uint8_t* out,
+                          size_t out_capacity) {
+    return guard([&]() -> int {
+        VX_TRY(check_planar(planar, planar_len, rows, cols));
+        if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out is NULL");
+        const Geometry g = geometry(rows, cols);
+        if (out_capacity < g.device_bytes)
+            VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "out holds %zu bytes but the device layout needs %zu", out_capacity, g.device_bytes);
+        const size_t bad = find_invalid_byte(planar, rows * planar_row_bytes(cols));
+        if (bad != SIZE_MAX)
+            VX_FAIL(VX_ERR_INVALID_VALUE, "byte %zu (value %u) is not a velurex byte", bad, static_cast<unsigned>(planar[bad]));
+        planar_to_device_layout(planar, g, out);
+        return VX_OK;
+    });
+}
+
+int vx_staged_bytes(size_t cols, size_t* out_bytes) {
+    return guard([&]() -> int {
+        if (out_bytes == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_bytes is NULL");
+        VX_TRY(check_shape(1, cols));
+        *out_bytes = device_row_bytes(cols) * sizeof(uint2);
+        return VX_OK;
+    });
+}
+
+int vx_stage_acts_dev(const int8_t* acts, size_t acts_len, size_t cols, void* staged, size_t staged_capacity,
+                      void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_shape(1, cols));
+        if (acts == nullptr || staged == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "activations or staged is NULL");
+        if (acts_len < cols) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "activations hold %zu values but cols = %zu", acts_len, cols);
+        const size_t need = device_row_bytes(cols) * sizeof(uint2);
+        if (staged_capacity < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "staged holds %zu bytes, %zu needed", staged_capacity, need);
+        return launch_stage(acts, cols, static_cast<uint2*>(staged), static_cast<hipStream_t>(stream));
+    });
+}
+
+static int check_staged(const vx_matrix_t* m, const void* staged, size_t staged_len, const void* out, size_t out_capacity) {
+    if (staged == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "staged is NULL");
+    if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out is NULL");
+    const size_t need = m->g.dbr * sizeof(uint2);
+    if (staged_len < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "staged holds %zu bytes, %zu needed", staged_len, need);
+    if (out_capacity < m->g.rows)
+        VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "output holds %zu values but rows = %zu", out_capacity, m->g.rows);
+    return VX_OK;
+}
+
+int vx_gemv_staged_i32_dev(const vx_matrix_t* matrix, const void* staged, size_t staged_len, int32_t* out,
+                           size_t out_capacity, void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_staged(matrix, staged, staged_len, out, out_capacity));
+        VX_TRY(set_device_of(matrix));
+        return launch_gemv_staged(const_cast<vx_matrix*>(matrix), static_cast<const uint2*>(staged), out, false, 1.0f,
+                                  static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_gemv_staged_f32_dev(const vx_matrix_t* matrix, const void* staged, size_t staged_len, float act_scale, float* out,
+                           size_t out_capacity, void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_staged(matrix, staged, staged_len, out, out_capacity));
+        VX_TRY(set_device_of(matrix));
+        vx_matrix* m = const_cast<vx_matrix*>(matrix);
+        if (act_scale > 0.0f)
+            return launch_gemv_staged(m, static_cast<const uint2*>(staged), out, true, m->weight_scale / act_scale,
+                                      static_cast<hipStream_t>(stream));
+        return launch_fill_f32(out, m->g.rows, 0.0f, static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_matrix_free(vx_matrix_t* matrix) {
+    return guard([&]() -> int {
+        if (matrix == nullptr) return VX_OK;
+        VX_TRY(check_matrix(matrix));
+        VX_TRY(set_device_of(matrix));
+        VX_HIP(hipDeviceSynchronize());
+        destroy(matrix);
+        return VX_OK;
+    });
+}
+
+int vx_matrix_shape(const vx_matrix_t* matrix, size_t* out_rows, size_t* out_cols) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        if (out_rows == nullptr || out_cols == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "output pointer is NULL");
+        *out_rows = matrix->g.rows;
+        *out_cols = matrix->g.cols;
+        return VX_OK;
+    });
+}
+
+int vx_matrix_memory_bytes(const vx_matrix_t* matrix, size_t* out_bytes) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        if (out_bytes == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_bytes is NULL");
+        *out_bytes = matrix->g.device_bytes;
+        return VX_OK;
+    });
+}
+
+int vx_matrix_weight_scale(const vx_matrix_t* matrix, float* out_scale) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        if (out_scale == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_scale is NULL");
+        *out_scale = matrix->weight_scale;
+        return VX_OK;
+    });
+}
+
+int vx_matrix_device_weights(const vx_matrix_t* matrix, const void** out_ptr) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        if (out_ptr == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_ptr is NULL");
+        *out_ptr = matrix->d_w;
+        return VX_OK;
+    });
+}
+
+int vx_gemv_i32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, int32_t* out, size_t out_capacity,
+                    void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_io(matrix, acts, acts_len, out, out_capacity));
+        VX_TRY(set_device_of(matrix));
+        return launch_gemv(const_cast<vx_matrix*>(matrix), acts, out, false, 1.0f, static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_gemv_f32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, float act_scale, float* out,
+                    size_t out_capacity, void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_io(matrix, acts, acts_len, out, out_capacity));
+        VX_TRY(set_device_of(matrix));
+        return gemv_f32_dev(const_cast<vx_matrix*>(matrix), acts, act_scale, out, static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_layer_forward(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, float act_scale, float* out,
+                     size_t out_capacity) {
+    return guard([&]() -> int {
+        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_io(matrix, acts, acts_len, out, out_capacity));
+        vx_matrix* m = const_cast<vx_matrix*>(matrix);
+        std::lock_guard<std::mutex> lock(m->mu);
+        VX_TRY(set_device_of(m));
+        int8_t* d_acts = m->d_io;
+        float* d_out = reinterpret_cast<float*>(m->d_io + round_up(m->g.cols, 256));
+        VX_HIP(hipMemcpy(d_acts, acts, m->g.cols, hipMemcpyHostToDevice));
+        VX_TRY(gemv_f32_dev(m, d_acts, act_scale, d_out, nullptr));
+        VX_HIP(hipMemcpy(out, d_out, m->g.rows * sizeof(float), hipMemcpyDeviceToHost));
+        return VX_OK;
+    });
+}
+
+static int planar_oneshot(const uint8_t* weights, size_t weights_len, size_t rows, size_t cols, const int8_t* acts,
+                          size_t acts_len, void* out, size_t out_capacity, bool f32, float scale) {
+    if (acts == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "activations is NULL");
+    if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out is NULL");
+    VX_TRY(check_shape(rows, cols));
+    if (out_capacity < rows) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "output holds %zu values but rows = %zu", out_capacity, rows);
+    if (acts_len < cols) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "activations hold %zu values but cols = %zu", acts_len, cols);
+    vx_matrix_t* m = nullptr;
+    VX_TRY(create_matrix(weights, weights_len, rows, cols, 1.0f, &m));
+    int8_t* d_acts = m->d_io;
+    void* d_out = m->d_io + round_up(cols, 256);
+    int st = VX_OK;
+    hipError_t e = hipMemcpy(d_acts, acts, cols, hipMemcpyHostToDevice);
+    if (e == hipSuccess) {
+        st = launch_gemv(m, d_acts, d_out, f32, scale, nullptr);
+        if (st == VX_OK) e = hipMemcpy(out, d_out, rows * 4, hipMemcpyDeviceToHost);
+    }
+    (void)hipDeviceSynchronize();
+    destroy(m);
+    if (st != VX_OK) return st;
+    if (e != hipSuccess) VX_FAIL(VX_ERR_DEVICE, "copy failed: %s", hipGetErrorString(e));
+    return VX_OK;
+}
+
+int vx_gemv_planar_i32(const uint8_t* weights, size_t weights_len, size_t rows, size_t cols, const int8_t* acts,
+                       size_t acts_len, int32_t* out, size_t out_capacity) {
+    return guard([&]() -> int {
+        return planar_oneshot(weights, weights_len, rows, cols, acts, acts_len, out, out_capacity, false, 1.0f);
+    });
+}
+
+int vx_gemv_planar_f32(const uint8_t* weights, size_t weights_len, size_t rows, size_t cols, const int8_t* acts,
+                       size_t acts_len, float scale, float* out, size_t out_capacity) {
+    return guard([&]() -> int {
+        return planar_oneshot(weights, weights_len, rows, cols, acts, acts_len, out, out_capacity, true, scale);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,105 @@
+"""The C ABI (include/velurex_hip.h) on the CPU: the library loads, exports every declared symbol, keeps the reference's
+status codes, computes the device layout on the host and rejects bad arguments before any GPU work."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from quintrit_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "velurex_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = declared_functions()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(L, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_status_codes_match_the_reference():
+    # quintrit-c/include/quintrit.h:73-88
+    want = {"VX_OK": 0, "VX_ERR_NULL_POINTER": 1, "VX_ERR_INVALID_ARGUMENT": 2, "VX_ERR_INVALID_SHAPE": 3,
+            "VX_ERR_BUFFER_TOO_SMALL": 4, "VX_ERR_INVALID_VALUE": 5, "VX_ERR_UNSUPPORTED": 6, "VX_ERR_IO": 7,
+            "VX_ERR_FORMAT": 8, "VX_ERR_NOT_FOUND": 9, "VX_ERR_MODEL": 10, "VX_ERR_CONTEXT_OVERFLOW": 11,
+            "VX_ERR_BUSY": 12, "VX_ERR_INTERNAL": 13, "VX_ERR_INVALID_HANDLE": 14, "VX_ERR_DEVICE": 15}
+    text = open(HEADER).read()
+    for name, value in want.items():
+        m = re.search(rf"#define {name}\s+(\d+)", text)
+        assert m and int(m.group(1)) == value, name
+        assert _lib.STATUS_NAMES[value] == name
+    L = _lib.lib()
+    assert L.vx_status_string(0) == b"ok"
+    assert L.vx_status_string(999) == b"unknown status"
+    assert L.vx_abi_version() == 1 and L.vx_version() == b"0.1.0"
+
+
+def test_layout_matches_the_oracle(oracle):
+    for rows, cols in [(1, 1), (64, 160), (65, 161), (3072, 3072), (23040, 3072), (3072, 23040), (7, 4096)]:
+        lay = _lib.layout(rows, cols)
+        assert lay["tile_rows"] == 64
+        assert lay["padded_rows"] == -(-rows // 64) * 64
+        assert lay["planar_row_bytes"] == oracle.planar_row_bytes(cols)
+        assert lay["tile_row_bytes"] == oracle.tile_row_bytes(cols)
+        assert lay["device_row_bytes"] == -(-oracle.tile_row_bytes(cols) // 16) * 16
+        assert lay["device_bytes"] == lay["padded_rows"] * lay["device_row_bytes"]
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 161), (64, 160), (70, 3072), (130, 4096), (5, 23040)])
+def test_device_layout_pack_places_every_byte(oracle, rows, cols):
+    # The device layout (velurex_hip.h, vx_layout): tile row bytes (the oracle's tile_byte, pack.rs:240-256) placed at
+    # tile*64*dbr + (c/16)*1024 + (r%64)*16 + c%16; padding is byte 125 (five zero trits).
+    rng = np.random.default_rng(rows * 7 + cols)
+    trits = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+    planar = oracle.pack_matrix(trits)
+    dev = _lib.device_layout_pack(planar, rows, cols)
+    lay = _lib.layout(rows, cols)
+    dbr, tbr = lay["device_row_bytes"], lay["tile_row_bytes"]
+    want = np.full((lay["padded_rows"], dbr), 125, np.uint8)
+    for r in range(rows):
+        want[r, :tbr] = oracle.tile_row(planar[r], cols)
+    t = want.reshape(-1, 64, dbr // 16, 16).transpose(0, 2, 1, 3).reshape(-1)
+    assert np.array_equal(dev, t)
+
+
+def test_invalid_bytes_are_rejected(oracle):
+    planar = oracle.pack_matrix(np.zeros((2, 160), np.int8))
+    for bad in (27, 251, 255):
+        p = planar.copy()
+        p[1, 5] = bad
+        with pytest.raises(_lib.VxError) as e:
+            _lib.device_layout_pack(p, 2, 160)
+        assert e.value.status == 5  # VX_ERR_INVALID_VALUE
+        assert "byte 37" in str(e.value)
+
+
+def test_argument_errors_without_gpu():
+    L = _lib.lib()
+    vp = ctypes.c_void_p
+    buf = (ctypes.c_uint8 * 64)()
+    h = vp()
+    assert L.vx_matrix_create(None, 0, 1, 1, 1.0, ctypes.byref(h)) == 1          # NULL planar
+    assert L.vx_matrix_create(buf, 64, 0, 1, 1.0, ctypes.byref(h)) == 3          # rows = 0
+    assert L.vx_matrix_create(buf, 64, 1, 131073, 1.0, ctypes.byref(h)) == 3     # cols too large
+    assert L.vx_matrix_create(buf, 16, 1, 160, 1.0, ctypes.byref(h)) == 4        # planar too short
+    assert b"needs 32" in L.vx_last_error_message()
+    assert L.vx_last_error_code() == 4
+    assert L.vx_matrix_free(None) == 0
+    assert L.vx_gemv_i32_dev(None, buf, 1, buf, 1, None) == 14                   # NULL handle
+    lay = _lib._Layout()
+    lay.struct_size = 3
+    assert L.vx_layout(1, 1, ctypes.byref(lay)) == 2                              # wrong struct_size
+    with pytest.raises(_lib.VxError):
+        _lib.staged_bytes(0)
+    assert _lib.staged_bytes(3072) == 624 * 8

@@ -1,0 +1,202 @@
+"""GPU parity of the velurex GEMV (libvelurex_hip through its C ABI) against the oracle and brute force.
+
+The integer results must be bit-exact; the fp32 epilogue must equal the oracle's bit for bit (it is one fp32 division
+and one fp32 multiplication per row, layer.rs:246-253). Shapes and patterns follow the reference's GPU tests
+(quintrit-cuda/tests/gemv.rs:46-64,77-125) and BASELINE.json configs 0-2.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def exact_gemv(trits, acts):
+    """Brute-force product; float32 BLAS is exact here (|partial sums| < 2^24, integer operands)."""
+    return (trits.astype(np.float32) @ acts.astype(np.float32)).astype(np.int64)
+
+
+def weights(kind, rows, cols, rng):
+    return {"random": lambda: rng.integers(-1, 2, size=(rows, cols), dtype=np.int8),
+            "plus": lambda: np.ones((rows, cols), np.int8),
+            "minus": lambda: -np.ones((rows, cols), np.int8),
+            "zero": lambda: np.zeros((rows, cols), np.int8)}[kind]()
+
+
+def activations(kind, cols, rng):
+    return {"random": lambda: rng.integers(-128, 128, size=cols, dtype=np.int8),
+            "max": lambda: np.full(cols, 127, np.int8),
+            "min": lambda: np.full(cols, -128, np.int8),
+            "alternating": lambda: np.where(np.arange(cols) % 2 == 0, 127, -128).astype(np.int8)}[kind]()
+
+
+def gpu_gemv_i32(torch, layer, acts):
+    a = torch.from_numpy(acts).cuda()
+    out = torch.empty(layer.shape()[0], dtype=torch.int32, device="cuda")
+    layer.gemv_i32(a, out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("cols", [1, 160, 161, 320, 2560, 3072, 4096, 13312, 23040])
+def test_pattern_grid_is_exact(torch_dev, oracle, cols):
+    from quintrit_amd import VelurexHipLayer
+    print(f"[gemv grid] cols={cols}", flush=True)
+    rng = np.random.default_rng(cols)
+    rows = 64
+    for wk in ("random", "plus", "minus", "zero"):
+        t = weights(wk, rows, cols, rng)
+        layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, 1.0)
+        for ak in ("random", "max", "min", "alternating"):
+            a = activations(ak, cols, rng)
+            got = gpu_gemv_i32(torch_dev, layer, a)
+            assert np.array_equal(got.astype(np.int64), exact_gemv(t, a)), (cols, wk, ak)
+        layer.close()
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 160), (2, 160), (6, 3072), (12, 2560), (40, 3072), (65, 161),
+                                       (2560, 2560), (3456, 2560), (1024, 3072), (3072, 23040), (23040, 3072),
+                                       (5120, 3072), (7, 131072)])
+def test_awkward_and_model_shapes(torch_dev, oracle, rows, cols):
+    from quintrit_amd import VelurexHipLayer
+    print(f"[gemv shapes] {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows * 131 + cols)
+    t = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+    a = rng.integers(-128, 128, size=cols, dtype=np.int8)
+    layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, 1.0)
+    want = exact_gemv(t, a)
+    for _ in range(3):  # the split-K accumulators must be clean again after every call
+        got = gpu_gemv_i32(torch_dev, layer, a)
+        assert np.array_equal(got.astype(np.int64), want)
+    layer.close()
+
+
+def test_config0_exact_and_epilogue(torch_dev, oracle):
+    """W 2560x2560, P(-1)=P(+1)=0.35, x uniform in [-127, 127], y = float(acc) * 0.02."""
+    from quintrit_amd import VelurexHipLayer
+    t = oracle.gen_trits(0xC0FFEE, (2560, 2560))
+    a = oracle.gen_i8(0xBEEF, 2560, -127, 127)
+    planar = oracle.pack_matrix(t)
+    layer = VelurexHipLayer(planar, 2560, 2560, 0.02)
+    acc = gpu_gemv_i32(torch_dev, layer, a)
+    want = oracle.gemv_lut_planar(planar, 2560, 2560, a)
+    assert np.array_equal(acc, want)
+    assert np.array_equal(acc.astype(np.int64), oracle.gemv_bruteforce(t, a))
+    y = np.empty(2560, np.float32)
+    layer.forward(a, 1.0, y)                       # TernaryGemvLayer::forward with act_scale = 1
+    assert np.array_equal(y.view(np.uint32), oracle.epilogue_f32(want, 0.02, 1.0).view(np.uint32))
+    layer.forward(a, 0.37, y)
+    assert np.array_equal(y.view(np.uint32), oracle.epilogue_f32(want, 0.02, 0.37).view(np.uint32))
+    for bad in (0.0, -1.0, float("nan")):
+        layer.forward(a, bad, y)
+        assert np.array_equal(y.view(np.uint32), np.zeros(2560, np.uint32))   # +0.0, as out.fill(0.0)
+    layer.close()
+
+
+def test_staged_activations_shared_by_matrices(torch_dev, oracle):
+    from quintrit_amd import VelurexHipLayer, _lib
+    torch = torch_dev
+    rng = np.random.default_rng(99)
+    cols = 3072
+    a = rng.integers(-128, 128, size=cols, dtype=np.int8)
+    da = torch.from_numpy(a).cuda()
+    nbytes = _lib.staged_bytes(cols)
+    staged = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    L = _lib.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(da.data_ptr()), cols, cols, ctypes.c_void_p(staged.data_ptr()),
+                                   nbytes, stream))
+    for rows in (3072, 1024, 23040):
+        t = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+        layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, 0.05)
+        out = torch.empty(rows, dtype=torch.int32, device="cuda")
+        _lib.check(L.vx_gemv_staged_i32_dev(layer.handle, ctypes.c_void_p(staged.data_ptr()), nbytes,
+                                            ctypes.c_void_p(out.data_ptr()), rows, stream))
+        outf = torch.empty(rows, dtype=torch.float32, device="cuda")
+        _lib.check(L.vx_gemv_staged_f32_dev(layer.handle, ctypes.c_void_p(staged.data_ptr()), nbytes,
+                                            ctypes.c_float(0.25), ctypes.c_void_p(outf.data_ptr()), rows, stream))
+        torch.cuda.synchronize()
+        want = exact_gemv(t, a)
+        assert np.array_equal(out.cpu().numpy().astype(np.int64), want)
+        assert np.array_equal(outf.cpu().numpy().view(np.uint32),
+                              oracle.epilogue_f32(want.astype(np.int32), 0.05, 0.25).view(np.uint32))
+        layer.close()
+
+
+def test_create_from_device_memory(torch_dev, oracle):
+    from quintrit_amd import _lib
+    torch = torch_dev
+    L = _lib.lib()
+    for rows, cols in ((100, 3072), (64, 161), (3, 23040)):
+        rng = np.random.default_rng(rows + cols)
+        t = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+        planar = oracle.pack_matrix(t)
+        dp = torch.from_numpy(planar.reshape(-1)).cuda()
+        h = ctypes.c_void_p()
+        _lib.check(L.vx_matrix_create_dev(ctypes.c_void_p(dp.data_ptr()), planar.size, rows, cols, ctypes.c_float(1.0),
+                                          ctypes.byref(h)))
+        # the device transform writes exactly the host layout
+        wp = ctypes.c_void_p()
+        _lib.check(L.vx_matrix_device_weights(h, ctypes.byref(wp)))
+        n = _lib.layout(rows, cols)["device_bytes"]
+        host = np.empty(n, np.uint8)
+        torch.cuda.synchronize()
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+        assert hip.hipMemcpy(host.ctypes.data_as(ctypes.c_void_p), wp, n, 2) == 0
+        assert np.array_equal(host, _lib.device_layout_pack(planar, rows, cols))
+        a = rng.integers(-128, 128, size=cols, dtype=np.int8)
+        da = torch.from_numpy(a).cuda()
+        out = torch.empty(rows, dtype=torch.int32, device="cuda")
+        _lib.check(L.vx_gemv_i32_dev(h, ctypes.c_void_p(da.data_ptr()), cols, ctypes.c_void_p(out.data_ptr()), rows,
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().astype(np.int64), exact_gemv(t, a))
+        _lib.check(L.vx_matrix_free(h))
+    # an invalid byte in device memory is reported with its index
+    planar = oracle.pack_matrix(np.zeros((2, 160), np.int8))
+    planar[1, 3] = 252
+    dp = torch.from_numpy(planar.reshape(-1)).cuda()
+    h = ctypes.c_void_p()
+    st = L.vx_matrix_create_dev(ctypes.c_void_p(dp.data_ptr()), planar.size, 2, 160, ctypes.c_float(1.0), ctypes.byref(h))
+    assert st == 5 and b"byte 35" in L.vx_last_error_message()
+
+
+def test_planar_oneshot_api(torch_dev, oracle):
+    from quintrit_amd import gemv_planar_f32, gemv_planar_i32
+    rng = np.random.default_rng(5)
+    t = rng.integers(-1, 2, size=(96, 3072), dtype=np.int8)
+    a = rng.integers(-128, 128, size=3072, dtype=np.int8)
+    planar = oracle.pack_matrix(t)
+    got = gemv_planar_i32(planar, 96, 3072, a)
+    assert np.array_equal(got.astype(np.int64), exact_gemv(t, a))
+    f = gemv_planar_f32(planar, 96, 3072, a, 0.125)
+    assert np.array_equal(f.view(np.uint32), oracle.scale_f32(got, 0.125).view(np.uint32))
+
+
+def test_golden_fixtures(torch_dev):
+    """The committed fixtures (tests/golden) reproduce on the GPU."""
+    import os
+    from quintrit_amd import VelurexHipLayer
+    gdir = os.path.join(os.path.dirname(__file__), "golden")
+    for name in sorted(os.listdir(gdir)):
+        if not (name.startswith("gemv_") and name.endswith(".npz")):
+            continue
+        z = np.load(os.path.join(gdir, name))
+        rows, cols = (int(v) for v in z["shape"])
+        layer = VelurexHipLayer(z["planar"], rows, cols, float(z["weight_scale"]))
+        acc = gpu_gemv_i32(torch_dev, layer, z["acts"])
+        assert np.array_equal(acc, z["acc"]), name
+        y = np.empty(rows, np.float32)
+        layer.forward(z["acts"], float(z["act_scale"]), y)
+        assert np.array_equal(y.view(np.uint32), z["y"].view(np.uint32)), name
+        layer.close()
