@@ -5,7 +5,8 @@ One "step" is the projection stream of one decoded Falcon3-10B token at bs=1: fo
 q|k|v projection (5120 x 3072), o (3072 x 3072), the row-interleaved gate|up projection (46080 x 3072) and down
 (3072 x 23040) -- 9,500,098,560 ternary weights, 1.90 GB at 1.60 bpw -- each on its own int8 input vector (per-token
 absmax int8 of N(0,1) fp32), with the fp32 epilogue. The reference measures the same projection set as CUDA graphs
-(docs/benchmarks.md, "Projections against Microsoft's W2A8 GPU kernel"); here the 160 launches are one HIP graph.
+(docs/benchmarks.md, "Projections against Microsoft's W2A8 GPU kernel"); here they are one batched plan (vx_plan_run:
+one persistent GEMV launch plus the K-slice finish), and, for comparison, 160 lone-GEMV launches in one HIP graph.
 Weights are i.i.d. trits, P(-1) = P(+1) = 0.35, generated on the GPU, far larger than the 256 MB last-level cache,
 so every replay streams them from HBM. Inputs are resident in HBM when the timed region starts.
 
@@ -75,23 +76,24 @@ def quantize_i8(torch, x):
 
 
 class Stream:
-    """The 40-layer projection stream resident on the GPU."""
+    """The 40-layer projection stream resident on the GPU, with one staged input vector per projection."""
 
     def __init__(self, torch, L, lib, layers: int):
         self.torch, self.L, self.lib = torch, L, lib
         gen = torch.Generator(device="cuda")
         gen.manual_seed(0x5EED)
         self.mats = []      # per layer: list of (name, handle, rows, cols)
-        self.inputs = []    # per layer: staged input per launch
+        self.staged = []    # per launch: (tensor, nbytes)
         self.outs = []
         self.weights = 0
         self.alg_bytes = 0
         self.device_bytes = 0
+        n = layers * len(LAYER_SHAPES)
+        self.scales = torch.empty(n, dtype=torch.float32, device="cuda")
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        k = 0
         for li in range(layers):
             row = []
-            ins = []
-            outs = []
             for name, rows, cols in LAYER_SHAPES:
                 planar = random_planar(torch, rows, cols, gen)
                 h = ctypes.c_void_p()
@@ -104,30 +106,42 @@ class Stream:
                 staged = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
                 lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(q.data_ptr()), cols, cols,
                                               ctypes.c_void_p(staged.data_ptr()), nbytes, stream))
+                self.scales[k] = s
                 row.append((name, h, rows, cols))
-                ins.append((staged, nbytes, s))
-                outs.append(torch.empty(rows, dtype=torch.float32, device="cuda"))
+                self.staged.append((staged, nbytes))
+                self.outs.append(torch.empty(rows, dtype=torch.float32, device="cuda"))
                 self.weights += rows * cols
                 self.alg_bytes += rows * cols / 5.0
                 self.device_bytes += lib.layout(rows, cols)["device_bytes"]
+                k += 1
             self.mats.append(row)
-            self.inputs.append(ins)
-            self.outs.append(outs)
         torch.cuda.synchronize()
 
-    def launch(self, li: int, k: int) -> None:
-        _, h, rows, _ = self.mats[li][k]
-        staged, nbytes, s = self.inputs[li][k]
-        out = self.outs[li][k]
-        st = self.L.vx_gemv_staged_f32_dev(h, ctypes.c_void_p(staged.data_ptr()), nbytes, ctypes.c_float(s),
-                                           ctypes.c_void_p(out.data_ptr()), rows,
-                                           ctypes.c_void_p(self.torch.cuda.current_stream().cuda_stream))
-        self.lib.check(st)
+    def jobs(self, which=None):
+        """vx_gemv_job_t list in model order (all launch types, or only LAYER_SHAPES[which])."""
+        out = []
+        k = 0
+        for row in self.mats:
+            for t, (_, h, rows, _) in enumerate(row):
+                if which is None or which == t:
+                    staged, nbytes = self.staged[k]
+                    out.append(self.lib.GemvJob(out_f32=1, matrix=h.value, staged=staged.data_ptr(), staged_len=nbytes,
+                                                act_scale_dev=self.scales.data_ptr() + 4 * k,
+                                                out=self.outs[k].data_ptr(), out_capacity=rows))
+                k += 1
+        return out
 
-    def step(self) -> None:
-        for li in range(len(self.mats)):
-            for k in range(len(LAYER_SHAPES)):
-                self.launch(li, k)
+    def chain_step(self) -> None:
+        """The same projections as 160 dependent launches (one GEMV call each, as a decode step issues them)."""
+        st = ctypes.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+        k = 0
+        for row in self.mats:
+            for _, h, rows, _ in row:
+                staged, nbytes = self.staged[k]
+                self.lib.check(self.L.vx_gemv_staged_f32_dev(h, ctypes.c_void_p(staged.data_ptr()), nbytes,
+                                                             ctypes.c_float(1.0), ctypes.c_void_p(self.outs[k].data_ptr()),
+                                                             rows, st))
+                k += 1
 
     def free(self):
         for row in self.mats:
@@ -149,16 +163,17 @@ def capture(torch, fn):
     return g
 
 
-def time_graph(torch, g, steps: int, warmup: int):
+def time_fn(torch, fn, steps: int, warmup: int):
+    """Average device time per call of fn (torch events on the current stream, which fn launches on) and wall time."""
     for _ in range(warmup):
-        g.replay()
+        fn()
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     w0 = time.perf_counter()
     t0.record()
     for _ in range(steps):
-        g.replay()
+        fn()
     t1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
@@ -201,8 +216,8 @@ def cpu_baseline(budget_s: float):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is described in "
-                                   "DESIGN.md, not built)"}))
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (how the path would shard over "
+                                   "several GPUs is described in DESIGN.md, not built)"}))
         return 2
     import torch
     from quintrit_amd import _lib
@@ -214,40 +229,47 @@ def main():
     log(f"building the {args.layers}-layer weight stream on the GPU")
     st = Stream(torch, L, _lib, args.layers)
     log(f"{st.weights} weights, {st.alg_bytes / 1e9:.4f} GB algorithmic, {st.device_bytes / 1e9:.4f} GB device layout")
-    g = capture(torch, st.step)
-    log("graph captured; timing")
-    ms, wall = time_graph(torch, g, args.steps, args.warmup)
+    plan = _lib.Plan(st.jobs())
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    step = lambda: plan.run(stream())  # noqa: E731
+    log(f"plan: {len(st.jobs())} GEMVs, {plan.work_items()} work items; timing")
+    ms, wall = time_fn(torch, step, args.steps, args.warmup)
     gw = st.weights / (ms / 1e3) / 1e9
     gbps = st.alg_bytes / (ms / 1e3) / 1e9
-    log(f"{ms:.4f} ms/step, {gw:.1f} Gweights/s, {gbps:.1f} GB/s algorithmic, wall {wall / args.steps * 1e3:.4f} ms/step")
+    log(f"{ms:.4f} ms/step, {gw:.1f} Gweights/s, {gbps:.1f} GB/s algorithmic ({gbps / HBM_PEAK_GBPS:.1%} of peak), "
+        f"wall {wall / args.steps * 1e3:.4f} ms/step")
 
     breakdown = {}
+    chain = None
     if not args.no_breakdown:
-        # Each launch type alone, rotated through all layers (distinct weights, so no cache reuse): average duration.
-        for k, (name, rows, cols) in enumerate(LAYER_SHAPES):
-            gk = capture(torch, lambda k=k: [st.launch(li, k) for li in range(len(st.mats))])
-            mk, _ = time_graph(torch, gk, max(3, args.steps // 5), 2)
-            per = mk / len(st.mats)
-            alg = rows * cols / 5.0
-            breakdown[name] = {"rows": rows, "cols": cols, "us_per_launch": round(per * 1e3, 3),
-                               "alg_GBps": round(alg / (per / 1e3) / 1e9, 1)}
-            log(f"  {name:8s} {rows}x{cols}: {per * 1e3:.2f} us/launch, {alg / (per / 1e3) / 1e9:.1f} GB/s")
-            del gk
-    dom = breakdown.get("gate_up")
-    if dom:
-        achieved = dom["alg_GBps"]
-        roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                    "kernel": "gemv_lut_kernel (gate|up 46080x3072)",
-                    "alg_bytes_per_launch": int(2 * FFN * HIDDEN / 5)}
-    else:
-        roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": "whole step"}
+        # each launch type alone, over all layers (distinct weights, so no cache reuse)
+        for t, (name, rows, cols) in enumerate(LAYER_SHAPES):
+            p = _lib.Plan(st.jobs(t))
+            mk, _ = time_fn(torch, lambda p=p: p.run(stream()), max(3, args.steps // 2), 2)
+            alg = rows * cols / 5.0 * len(st.mats)
+            breakdown[name] = {"rows": rows, "cols": cols, "us_per_matrix": round(mk * 1e3 / len(st.mats), 3),
+                               "alg_GBps": round(alg / (mk / 1e3) / 1e9, 1)}
+            log(f"  {name:8s} {rows}x{cols}: {mk * 1e3 / len(st.mats):.2f} us/matrix, {alg / (mk / 1e3) / 1e9:.1f} GB/s")
+            p.close()
+        # the dependent form: one GEMV launch per projection, captured as one HIP graph
+        g = capture(torch, st.chain_step)
+        mc, _ = time_fn(torch, g.replay, max(3, args.steps // 2), 2)
+        chain = {"ms_per_step": round(mc, 4), "Gweights_s": round(st.weights / (mc / 1e3) / 1e9, 1),
+                 "alg_GBps": round(st.alg_bytes / (mc / 1e3) / 1e9, 1), "launches": len(st.jobs()),
+                 "note": "one lone-GEMV call per projection (each waits for the previous), as a HIP graph"}
+        log(f"  chain of {len(st.jobs())} lone GEMVs in a graph: {mc:.4f} ms/step, {chain['alg_GBps']} GB/s")
+        del g
+    roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": "vx::gemv_kernel (one plan run: all 160 projections of a token; event-timed region also "
+                          "holds the K-slice finish kernel)",
+                "alg_bytes_per_launch": int(st.alg_bytes)}
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU baseline")
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"cpu baseline {cpu['value']} Gweights/s")
+    plan.close()
     st.free()
     line = {
         "metric": METRIC, "value": round(gw, 1), "unit": "Gweights/s", "n_gpus": 1, "steps": args.steps,
@@ -255,12 +277,13 @@ def main():
         "vs_baseline": round(gw / REF_CPU_GWEIGHTS, 2), "dtype": "int32", "data": "synthetic",
         "config": {"workload": "falcon3-10b-decode-projection-stream (BASELINE.json configs[1])", "layers": args.layers,
                    "hidden": HIDDEN, "ffn": FFN, "kv_rows": KV, "batch": 1, "weights_per_step": st.weights,
-                   "launches_per_step": len(LAYER_SHAPES) * args.layers, "parallelism": "single-gpu"},
+                   "gemvs_per_step": len(LAYER_SHAPES) * args.layers, "parallelism": "single-gpu"},
         "hbm_alg_GBps": round(gbps, 1), "hbm_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
         "device_layout_GBps": round(st.device_bytes / (ms / 1e3) / 1e9, 1),
         "tok_s_projection_bound": round(1e3 / ms, 1),
-        "vs_baseline_ref": f"{REF_CPU_GWEIGHTS} Gweights/s, reference AVX-512 kernel, 4 threads (docs/benchmarks.md:77)",
-        "breakdown": breakdown, "roofline": roofline, "cpu_baseline": cpu,
+        "vs_baseline_ref": f"{REF_CPU_GWEIGHTS} Gweights/s, the published Falcon3-10B weight-stream rate of the reference AVX-512 kernel, 4 threads, EPYC 9V45 "
+                                   f"(docs/benchmarks.md:77)",
+        "chain": chain, "breakdown": breakdown, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -24,7 +24,7 @@
  * host pointers and returns when the result is in host memory.
  *
  * Thread safety: functions are thread-safe on distinct matrix handles. A matrix handle owns a small device workspace
- * (split-K accumulators and activation staging); calls on one handle must be ordered: either one stream per handle,
+ * (K-slice partial sums and activation staging); calls on one handle must be ordered: either one stream per handle,
  * or events between streams. The host-pointer functions serialise calls on one handle internally.
  */
 #ifndef VELUREX_HIP_H
@@ -37,8 +37,8 @@
 extern "C" {
 #endif
 
-#define VX_VERSION_STRING "0.1.0"
-#define VX_ABI_VERSION 1
+#define VX_VERSION_STRING "0.2.0"
+#define VX_ABI_VERSION 2
 
 /* ---- status codes: same values as quintrit.h:73-88 ----------------------------------------------------------------- */
 #define VX_OK                      0
@@ -83,13 +83,19 @@ int vx_device_count(int32_t* out_count);
  * Device layout of a rows x cols matrix. The interchange format is the planar layout of the reference
  * (quintrit-core/src/pack.rs:10-16: a row is ceil(cols/160) blocks of 32 bytes; byte j of block b packs columns
  * b*160 + p*32 + j, p = 0..4). On upload each row is re-encoded with the packed tail of pack.rs:212-276 (the partial
- * last block stored five trits per byte, tile_row_bytes(cols) bytes), padded to a multiple of 16 bytes, and rows are
- * grouped in tiles of 64: byte c of row r lives at tile(r)*64*device_row_bytes + (c/16)*1024 + (r%64)*16 + c%16.
- * Counterpart of quintrit_tiled_layout_t (quintrit.h:181-196).
+ * last block stored five trits per byte, tile_row_bytes(cols) bytes) and padded with byte 125 (five zero trits) to
+ * device_row_bytes, a multiple of 16. Rows form tiles of 64 (tile_rows) and tiles form groups of 16 (tile_group); the
+ * 16-byte chunk q of tile t lives at KiB (g * 16 * n_chunks + q * T + t') of the buffer, with g = t / 16, t' = t % 16,
+ * T = the number of tiles in group g (16, or fewer in the last group) and n_chunks = device_row_bytes / 16; inside the
+ * chunk, row r % 64 holds bytes 16 (r % 64) .. +15. A GPU wave (64 lanes = 64 rows) thus reads 1 KiB per load, and the 16
+ * waves of a workgroup that work on one tile group read 16 consecutive KiB. Counterpart of quintrit_tiled_layout_t
+ * (quintrit.h:181-196).
  */
 typedef struct vx_layout {
     uint32_t struct_size;       /* set to sizeof(vx_layout_t) */
     uint32_t tile_rows;         /* 64 */
+    uint32_t tile_group;        /* 16 */
+    uint32_t reserved;
     uint64_t rows;
     uint64_t cols;
     uint64_t padded_rows;       /* rows rounded up to a multiple of 64 */
@@ -158,10 +164,12 @@ int vx_gemv_f32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_l
                     size_t out_capacity, void* stream);
 
 /*
- * Staged activations: the GEMV kernels read the activations of each device byte-column as two dwords (the activations
- * of its five trits, a0..a3 packed and a4), staged once per input vector and shareable by every matrix with the same
- * cols (Q, K and V share one input, gate and up another). vx_staged_bytes gives the size of the staging buffer.
- * The reference stages its GPU inputs the same way, one permuted entry per byte-column (quintrit-cuda/src/pack.rs:75-85).
+ * Staged activations: the GEMV kernels read the activations of each device byte-column c (the five activations
+ * column_activation_index(cols, c, p), p = 0..4, of quintrit-core/src/pack.rs:230-237) as two dwords: the low nibbles
+ * (x & 15) and the high nibbles (x >> 4) of the five values, 4 bits each, so that x = 16 hi + lo (lut.rs:380-388 splits
+ * the same way). A 64-byte header holds the sum of all activations. vx_staged_bytes(cols) = 64 + 8 * device_row_bytes.
+ * One staged vector serves every matrix with the same cols (Q, K and V share one input, gate and up another). The
+ * reference stages its GPU inputs the same way, one permuted entry per byte-column (quintrit-cuda/src/pack.rs:75-85).
  */
 int vx_staged_bytes(size_t cols, size_t* out_bytes);
 int vx_stage_acts_dev(const int8_t* acts, size_t acts_len, size_t cols, void* staged, size_t staged_capacity,
@@ -187,6 +195,43 @@ int vx_gemv_planar_i32(const uint8_t* weights, size_t weights_len, size_t rows, 
                        size_t acts_len, int32_t* out, size_t out_capacity);
 int vx_gemv_planar_f32(const uint8_t* weights, size_t weights_len, size_t rows, size_t cols, const int8_t* acts,
                        size_t acts_len, float scale, float* out, size_t out_capacity);
+
+/* ---- batched GEMV plans --------------------------------------------------------------------------------------------- */
+
+/*
+ * One GEMV of a plan. out_f32 = 0: out receives the int32 accumulators. out_f32 = 1: out receives
+ * float(acc) * (weight_scale / *act_scale_dev), the division done once per job in fp32, and zeros when the scale is not
+ * > 0 (the epilogue of layer.rs:246-253); the scale is read from device memory when the plan runs, so a producer kernel
+ * on the same stream can write it.
+ */
+typedef struct vx_gemv_job {
+    uint32_t struct_size;        /* sizeof(vx_gemv_job_t) */
+    int32_t out_f32;
+    const vx_matrix_t* matrix;
+    const void* staged;          /* device; staged by vx_stage_acts_dev for the matrix's cols */
+    size_t staged_len;
+    const float* act_scale_dev;  /* device; read when out_f32 = 1 */
+    void* out;                   /* device; rows values */
+    size_t out_capacity;
+} vx_gemv_job_t;
+
+typedef struct vx_plan vx_plan_t;
+
+/*
+ * Builds a plan of n_jobs GEMVs (1..65535) that run as one persistent launch (plus one launch that adds the K-slice
+ * partial sums of long rows). The pointers of the jobs are fixed in the plan; their contents may change between runs.
+ * The plan owns its job table and partial-sum workspace, so a run allocates nothing and can be captured in a HIP graph.
+ * The reference runs the projections of a layer concurrently on its thread pool (quintrit-runtime/src/layer.rs:657-716,
+ * forward_linear_pair/triple) and the projections of a token as one CUDA graph (quintrit-runtime/src/gpu.rs:389-493);
+ * a plan is the single-launch form of both.
+ */
+int vx_plan_create(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan);
+/* Enqueues the plan on `stream`. Runs of one plan must not overlap (they share the partial-sum workspace). */
+int vx_plan_run(const vx_plan_t* plan, void* stream);
+/* Number of work items (tile group x K slice) of the plan. */
+int vx_plan_work_items(const vx_plan_t* plan, uint32_t* out_items);
+/* Frees a plan (NULL is a no-op); waits for the device first. */
+int vx_plan_free(vx_plan_t* plan);
 
 #ifdef __cplusplus
 }

@@ -29,7 +29,8 @@ class VxError(RuntimeError):
 
 
 class _Layout(ctypes.Structure):
-    _fields_ = [("struct_size", ctypes.c_uint32), ("tile_rows", ctypes.c_uint32), ("rows", ctypes.c_uint64),
+    _fields_ = [("struct_size", ctypes.c_uint32), ("tile_rows", ctypes.c_uint32), ("tile_group", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32), ("rows", ctypes.c_uint64),
                 ("cols", ctypes.c_uint64), ("padded_rows", ctypes.c_uint64), ("planar_row_bytes", ctypes.c_uint64),
                 ("tile_row_bytes", ctypes.c_uint64), ("device_row_bytes", ctypes.c_uint64),
                 ("device_bytes", ctypes.c_uint64)]
@@ -64,6 +65,10 @@ SIGNATURES = {
     "vx_layer_forward": (_i32, [_vp, _vp, _sz, _f32, _vp, _sz]),
     "vx_gemv_planar_i32": (_i32, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz]),
     "vx_gemv_planar_f32": (_i32, [_vp, _sz, _sz, _sz, _vp, _sz, _f32, _vp, _sz]),
+    "vx_plan_create": (_i32, [_vp, _sz, _vp]),
+    "vx_plan_run": (_i32, [_vp, _vp]),
+    "vx_plan_work_items": (_i32, [_vp, _vp]),
+    "vx_plan_free": (_i32, [_vp]),
 }
 
 
@@ -97,7 +102,7 @@ def layout(rows: int, cols: int) -> dict:
     lay = _Layout()
     lay.struct_size = ctypes.sizeof(_Layout)
     check(lib().vx_layout(rows, cols, ctypes.byref(lay)))
-    return {name: getattr(lay, name) for name, _ in _Layout._fields_ if name != "struct_size"}
+    return {name: getattr(lay, name) for name, _ in _Layout._fields_ if name not in ("struct_size", "reserved")}
 
 
 def device_layout_pack(planar, rows: int, cols: int):
@@ -121,3 +126,42 @@ def device_count() -> int:
     n = ctypes.c_int32()
     check(lib().vx_device_count(ctypes.byref(n)))
     return n.value
+
+
+class GemvJob(ctypes.Structure):
+    """vx_gemv_job_t (include/velurex_hip.h)."""
+    _fields_ = [("struct_size", ctypes.c_uint32), ("out_f32", ctypes.c_int32), ("matrix", ctypes.c_void_p),
+                ("staged", ctypes.c_void_p), ("staged_len", ctypes.c_size_t), ("act_scale_dev", ctypes.c_void_p),
+                ("out", ctypes.c_void_p), ("out_capacity", ctypes.c_size_t)]
+
+
+class Plan:
+    """A batched GEMV plan (vx_plan_t): many GEMVs in one persistent launch."""
+
+    def __init__(self, jobs):
+        arr = (GemvJob * len(jobs))()
+        for i, j in enumerate(jobs):
+            arr[i] = j
+            arr[i].struct_size = ctypes.sizeof(GemvJob)
+        h = ctypes.c_void_p()
+        check(lib().vx_plan_create(arr, len(jobs), ctypes.byref(h)))
+        self._h = h
+
+    def run(self, stream_ptr) -> None:
+        check(lib().vx_plan_run(self._h, stream_ptr))
+
+    def work_items(self) -> int:
+        n = ctypes.c_uint32()
+        check(lib().vx_plan_work_items(self._h, ctypes.byref(n)))
+        return n.value
+
+    def close(self) -> None:
+        if self._h:
+            check(lib().vx_plan_free(self._h))
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -2,21 +2,13 @@
 // Error conventions follow the reference's C ABI (quintrit-c/src/error.rs:8-80, quintrit-c/src/tiles.rs:192-228).
 #include "vx_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
 #include <vector>
 
 namespace vx {
-
-int launch_gemv(vx_matrix* m, const int8_t* acts, void* out, bool out_f32, float post, hipStream_t stream);
-int launch_stage(const int8_t* acts, size_t cols, uint2* staged, hipStream_t stream);
-int launch_gemv_staged(vx_matrix* m, const uint2* staged, void* out, bool out_f32, float post, hipStream_t stream);
-int launch_device_layout(const uint8_t* planar_dev, const Geometry& g, uint8_t* dst, hipStream_t stream);
-int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
-int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
-size_t find_invalid_byte(const uint8_t* planar, size_t n);
-void planar_to_device_layout(const uint8_t* planar, const Geometry& g, uint8_t* dst);
 
 static thread_local Error t_error{VX_OK, std::string()};
 
@@ -66,9 +58,8 @@ static int set_device_of(const vx_matrix_t* m) {
 
 static void destroy(vx_matrix* m) {
     if (m->d_w) (void)hipFree(m->d_w);
-    if (m->d_acc) (void)hipFree(m->d_acc);
-    if (m->d_cnt) (void)hipFree(m->d_cnt);
-    if (m->d_actp) (void)hipFree(m->d_actp);
+    if (m->d_part) (void)hipFree(m->d_part);
+    if (m->d_staged) (void)hipFree(m->d_staged);
     if (m->d_io) (void)hipFree(m->d_io);
     m->magic = 0;
     delete m;
@@ -94,19 +85,19 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     m->device = di.device;
     m->num_cus = di.num_cus;
     m->d_w = nullptr;
-    m->d_acc = nullptr;
-    m->d_cnt = nullptr;
-    m->d_actp = nullptr;
+    m->d_part = nullptr;
+    m->d_staged = nullptr;
     m->d_io = nullptr;
+    Job probe{};
+    plan_job(probe, m->g, 2u * static_cast<uint32_t>(di.num_cus));
+    m->kslices = probe.kslices;
+    m->slice_chunks = probe.slice_chunks;
 
     const size_t io_bytes = round_up(cols, 256) + m->g.padded_rows * 4;
     hipError_t e = hipMalloc(&m->d_w, m->g.device_bytes);
-    if (e == hipSuccess) e = hipMalloc(&m->d_acc, m->g.padded_rows * sizeof(int32_t));
-    if (e == hipSuccess) e = hipMalloc(&m->d_cnt, m->g.n_tiles * sizeof(uint32_t));
-    if (e == hipSuccess) e = hipMalloc(&m->d_actp, m->g.dbr * sizeof(uint2));
+    if (e == hipSuccess && m->kslices > 1) e = hipMalloc(&m->d_part, static_cast<size_t>(m->kslices) * m->g.padded_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&m->d_staged, staged_bytes(cols));
     if (e == hipSuccess) e = hipMalloc(&m->d_io, io_bytes);
-    if (e == hipSuccess) e = hipMemset(m->d_acc, 0, m->g.padded_rows * sizeof(int32_t));
-    if (e == hipSuccess) e = hipMemset(m->d_cnt, 0, m->g.n_tiles * sizeof(uint32_t));
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         const size_t bytes = m->g.device_bytes;
@@ -179,10 +170,43 @@ static int check_io(const vx_matrix_t* m, const void* acts, size_t acts_len, con
     return VX_OK;
 }
 
-// out = float(acc) * (ws / as); zeros when as <= 0 or NaN (layer.rs:246-253).
-static int gemv_f32_dev(vx_matrix* m, const int8_t* acts, float act_scale, float* out, hipStream_t s) {
-    if (act_scale > 0.0f) return launch_gemv(m, acts, out, true, m->weight_scale / act_scale, s);
+// A lone GEMV of matrix m on staged activations: one launch (plus the K-slice finish when the matrix is split).
+static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint32_t out_kind, float post,
+                      hipStream_t s) {
+    LaunchArgs a{};
+    a.jobs = nullptr;
+    a.n_jobs = 1;
+    Job& j = a.one;
+    plan_job(j, m->g, 2u * static_cast<uint32_t>(m->num_cus));
+    j.w = m->d_w;
+    j.staged = staged;
+    j.part = m->d_part;
+    j.out = out;
+    j.act_scale = nullptr;
+    j.post = post;
+    j.weight_scale = m->weight_scale;
+    j.out_kind = out_kind;
+    j.item_begin = 0;
+    a.total_items = job_items(j);
+    return launch_gemv(a, j.rows, j.kslices > 1, m->num_cus, s);
+}
+
+// out = float(acc) * (ws / as) with the division done once here, as the layers do; zeros when as <= 0 or NaN
+// (layer.rs:246-253).
+static int gemv_f32_staged(const vx_matrix* m, const uint8_t* staged, float act_scale, float* out, hipStream_t s) {
+    if (act_scale > 0.0f) return run_single(m, staged, out, kOutF32Post, m->weight_scale / act_scale, s);
     return launch_fill_f32(out, m->g.rows, 0.0f, s);
+}
+
+static int gemv_f32_dev(vx_matrix* m, const int8_t* acts, float act_scale, float* out, hipStream_t s) {
+    if (!(act_scale > 0.0f)) return launch_fill_f32(out, m->g.rows, 0.0f, s);
+    VX_TRY(launch_stage(acts, m->g.cols, m->d_staged, s));
+    return gemv_f32_staged(m, m->d_staged, act_scale, out, s);
+}
+
+static int gemv_i32_dev(vx_matrix* m, const int8_t* acts, int32_t* out, hipStream_t s) {
+    VX_TRY(launch_stage(acts, m->g.cols, m->d_staged, s));
+    return run_single(m, m->d_staged, out, kOutI32, 1.0f, s);
 }
 
 }  // namespace vx
@@ -245,6 +269,7 @@ int vx_layout(size_t rows, size_t cols, vx_layout_t* out_layout) {
         VX_TRY(check_shape(rows, cols));
         const Geometry g = geometry(rows, cols);
         out_layout->tile_rows = kTileRows;
+        out_layout->tile_group = kTileGroup;
         out_layout->rows = rows;
         out_layout->cols = cols;
         out_layout->padded_rows = g.padded_rows;
@@ -286,7 +311,7 @@ int vx_staged_bytes(size_t cols, size_t* out_bytes) {
     return guard([&]() -> int {
         if (out_bytes == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_bytes is NULL");
         VX_TRY(check_shape(1, cols));
-        *out_bytes = device_row_bytes(cols) * sizeof(uint2);
+        *out_bytes = staged_bytes(cols);
         return VX_OK;
     });
 }
@@ -297,16 +322,16 @@ int vx_stage_acts_dev(const int8_t* acts, size_t acts_len, size_t cols, void* st
         VX_TRY(check_shape(1, cols));
         if (acts == nullptr || staged == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "activations or staged is NULL");
         if (acts_len < cols) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "activations hold %zu values but cols = %zu", acts_len, cols);
-        const size_t need = device_row_bytes(cols) * sizeof(uint2);
+        const size_t need = staged_bytes(cols);
         if (staged_capacity < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "staged holds %zu bytes, %zu needed", staged_capacity, need);
-        return launch_stage(acts, cols, static_cast<uint2*>(staged), static_cast<hipStream_t>(stream));
+        return launch_stage(acts, cols, static_cast<uint8_t*>(staged), static_cast<hipStream_t>(stream));
     });
 }
 
 static int check_staged(const vx_matrix_t* m, const void* staged, size_t staged_len, const void* out, size_t out_capacity) {
     if (staged == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "staged is NULL");
     if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out is NULL");
-    const size_t need = m->g.dbr * sizeof(uint2);
+    const size_t need = staged_bytes(m->g.cols);
     if (staged_len < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "staged holds %zu bytes, %zu needed", staged_len, need);
     if (out_capacity < m->g.rows)
         VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "output holds %zu values but rows = %zu", out_capacity, m->g.rows);
@@ -319,8 +344,7 @@ int vx_gemv_staged_i32_dev(const vx_matrix_t* matrix, const void* staged, size_t
         VX_TRY(check_matrix(matrix));
         VX_TRY(check_staged(matrix, staged, staged_len, out, out_capacity));
         VX_TRY(set_device_of(matrix));
-        return launch_gemv_staged(const_cast<vx_matrix*>(matrix), static_cast<const uint2*>(staged), out, false, 1.0f,
-                                  static_cast<hipStream_t>(stream));
+        return run_single(matrix, static_cast<const uint8_t*>(staged), out, kOutI32, 1.0f, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -330,11 +354,7 @@ int vx_gemv_staged_f32_dev(const vx_matrix_t* matrix, const void* staged, size_t
         VX_TRY(check_matrix(matrix));
         VX_TRY(check_staged(matrix, staged, staged_len, out, out_capacity));
         VX_TRY(set_device_of(matrix));
-        vx_matrix* m = const_cast<vx_matrix*>(matrix);
-        if (act_scale > 0.0f)
-            return launch_gemv_staged(m, static_cast<const uint2*>(staged), out, true, m->weight_scale / act_scale,
-                                      static_cast<hipStream_t>(stream));
-        return launch_fill_f32(out, m->g.rows, 0.0f, static_cast<hipStream_t>(stream));
+        return gemv_f32_staged(matrix, static_cast<const uint8_t*>(staged), act_scale, out, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -392,7 +412,7 @@ int vx_gemv_i32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_l
         VX_TRY(check_matrix(matrix));
         VX_TRY(check_io(matrix, acts, acts_len, out, out_capacity));
         VX_TRY(set_device_of(matrix));
-        return launch_gemv(const_cast<vx_matrix*>(matrix), acts, out, false, 1.0f, static_cast<hipStream_t>(stream));
+        return gemv_i32_dev(const_cast<vx_matrix*>(matrix), acts, out, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -437,7 +457,8 @@ static int planar_oneshot(const uint8_t* weights, size_t weights_len, size_t row
     int st = VX_OK;
     hipError_t e = hipMemcpy(d_acts, acts, cols, hipMemcpyHostToDevice);
     if (e == hipSuccess) {
-        st = launch_gemv(m, d_acts, d_out, f32, scale, nullptr);
+        st = launch_stage(d_acts, cols, m->d_staged, nullptr);
+        if (st == VX_OK) st = run_single(m, m->d_staged, d_out, f32 ? kOutF32Post : kOutI32, scale, nullptr);
         if (st == VX_OK) e = hipMemcpy(out, d_out, rows * 4, hipMemcpyDeviceToHost);
     }
     (void)hipDeviceSynchronize();
@@ -458,6 +479,138 @@ int vx_gemv_planar_f32(const uint8_t* weights, size_t weights_len, size_t rows, 
                        size_t acts_len, float scale, float* out, size_t out_capacity) {
     return guard([&]() -> int {
         return planar_oneshot(weights, weights_len, rows, cols, acts, acts_len, out, out_capacity, true, scale);
+    });
+}
+
+}  // extern "C"
+
+// ---- batched GEMV plans -------------------------------------------------------------------------------------------------
+
+namespace vx {
+
+static int check_plan(const vx_plan_t* p) {
+    if (p == nullptr) VX_FAIL(VX_ERR_INVALID_HANDLE, "plan handle is NULL");
+    if (p->magic != kPlanMagic) VX_FAIL(VX_ERR_INVALID_HANDLE, "plan handle is not valid (freed or foreign)");
+    return VX_OK;
+}
+
+static void destroy_plan(vx_plan* p) {
+    if (p->d_jobs) (void)hipFree(p->d_jobs);
+    if (p->d_part) (void)hipFree(p->d_part);
+    p->magic = 0;
+    delete p;
+}
+
+static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out) {
+    if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_plan is NULL");
+    *out = nullptr;
+    if (jobs == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "jobs is NULL");
+    if (n_jobs == 0 || n_jobs > 65535) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "n_jobs must be in 1..=65535 (got %zu)", n_jobs);
+    DeviceInfo di;
+    VX_TRY(device_info(&di));
+    std::vector<Job> hj(n_jobs);
+    size_t part_ints = 0;
+    uint32_t items = 0, max_rows = 0;
+    bool any_split = false;
+    for (size_t i = 0; i < n_jobs; ++i) {
+        const vx_gemv_job_t& u = jobs[i];
+        if (u.struct_size != sizeof(vx_gemv_job_t))
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].struct_size is %u, expected %zu", i, u.struct_size, sizeof(vx_gemv_job_t));
+        VX_TRY(check_matrix(u.matrix));
+        const vx_matrix* m = u.matrix;
+        if (m->device != di.device)
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].matrix lives on device %d, the current device is %d", i, m->device, di.device);
+        if (u.staged == nullptr || u.out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "jobs[%zu]: staged or out is NULL", i);
+        if (u.staged_len < staged_bytes(m->g.cols))
+            VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "jobs[%zu]: staged holds %zu bytes, %zu needed", i, u.staged_len, staged_bytes(m->g.cols));
+        if (u.out_capacity < m->g.rows)
+            VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "jobs[%zu]: out holds %zu values but rows = %zu", i, u.out_capacity, m->g.rows);
+        if (u.out_f32 != 0 && u.out_f32 != 1) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].out_f32 must be 0 or 1", i);
+        if (u.out_f32 == 1 && u.act_scale_dev == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "jobs[%zu].act_scale_dev is NULL", i);
+        Job& j = hj[i];
+        j = Job{};
+        plan_job(j, m->g, 0);
+        j.w = m->d_w;
+        j.staged = static_cast<const uint8_t*>(u.staged);
+        j.out = u.out;
+        j.act_scale = u.act_scale_dev;
+        j.weight_scale = m->weight_scale;
+        j.out_kind = u.out_f32 ? kOutF32Dev : kOutI32;
+        j.item_begin = items;
+        const uint64_t next = static_cast<uint64_t>(items) + job_items(j);
+        if (next > 0x7fffffffu) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the plan has too many work items");
+        items = static_cast<uint32_t>(next);
+        if (j.kslices > 1) {
+            j.part = reinterpret_cast<int32_t*>(part_ints);  // offset, rebased below
+            part_ints += static_cast<size_t>(j.kslices) * j.padded_rows;
+            any_split = true;
+        }
+        max_rows = std::max(max_rows, j.rows);
+    }
+    vx_plan* p = new vx_plan();
+    p->magic = kPlanMagic;
+    p->device = di.device;
+    p->num_cus = di.num_cus;
+    p->d_jobs = nullptr;
+    p->d_part = nullptr;
+    p->n_jobs = static_cast<uint32_t>(n_jobs);
+    p->total_items = items;
+    p->max_rows = max_rows;
+    p->any_split = any_split;
+    hipError_t e = hipMalloc(&p->d_jobs, n_jobs * sizeof(Job));
+    if (e == hipSuccess && part_ints) e = hipMalloc(&p->d_part, part_ints * sizeof(int32_t));
+    if (e == hipSuccess) {
+        for (auto& j : hj)
+            if (j.kslices > 1) j.part = p->d_part + reinterpret_cast<size_t>(j.part);
+        e = hipMemcpy(p->d_jobs, hj.data(), n_jobs * sizeof(Job), hipMemcpyHostToDevice);
+    }
+    if (e != hipSuccess) {
+        destroy_plan(p);
+        VX_FAIL(VX_ERR_DEVICE, "plan allocation failed: %s", hipGetErrorString(e));
+    }
+    *out = p;
+    return VX_OK;
+}
+
+}  // namespace vx
+
+extern "C" {
+
+int vx_plan_create(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan) {
+    return guard([&]() -> int { return create_plan(jobs, n_jobs, out_plan); });
+}
+
+int vx_plan_run(const vx_plan_t* plan, void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_plan(plan));
+        int cur = -1;
+        VX_HIP(hipGetDevice(&cur));
+        if (cur != plan->device) VX_HIP(hipSetDevice(plan->device));
+        LaunchArgs a{};
+        a.jobs = plan->d_jobs;
+        a.n_jobs = plan->n_jobs;
+        a.total_items = plan->total_items;
+        return launch_gemv(a, plan->max_rows, plan->any_split, plan->num_cus, static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_plan_work_items(const vx_plan_t* plan, uint32_t* out_items) {
+    return guard([&]() -> int {
+        VX_TRY(check_plan(plan));
+        if (out_items == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_items is NULL");
+        *out_items = plan->total_items;
+        return VX_OK;
+    });
+}
+
+int vx_plan_free(vx_plan_t* plan) {
+    return guard([&]() -> int {
+        if (plan == nullptr) return VX_OK;
+        VX_TRY(check_plan(plan));
+        VX_HIP(hipSetDevice(plan->device));
+        VX_HIP(hipDeviceSynchronize());
+        destroy_plan(plan);
+        return VX_OK;
     });
 }
 

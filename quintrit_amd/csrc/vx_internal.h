@@ -1,4 +1,5 @@
-// Internal helpers of libvelurex_hip: the per-thread error slot, argument checks and the device layout arithmetic.
+// Internal helpers of libvelurex_hip: the per-thread error slot, argument checks, the device layout arithmetic and the
+// GEMV job descriptors shared by the host planner and the kernels.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -61,10 +62,13 @@ int guard(F&& body) {
 
 // ---- layout ---------------------------------------------------------------------------------------------------------
 
-constexpr int kTileRows = 64;   // rows per tile = lanes of a wavefront
-constexpr int kChunk = 16;      // bytes one lane loads per step (global_load_dwordx4)
-constexpr size_t kQK5 = 160;    // trits per planar block (pack.rs:19)
+constexpr int kTileRows = 64;    // rows per tile = lanes of a wavefront
+constexpr int kChunk = 16;       // bytes one lane loads per step (global_load_dwordx4)
+constexpr int kTileGroup = 16;   // tiles whose chunks are interleaved (= waves of a GEMV workgroup)
+constexpr size_t kQK5 = 160;     // trits per planar block (pack.rs:19)
 constexpr size_t kBlockBytes = 32;
+constexpr size_t kStageHeader = 64;  // staged activations: int32 sum of the activations, then the chunk entries
+constexpr uint8_t kZeroByte = 125;   // five zero trits (every digit d = t + 1 is 1)
 
 inline size_t planar_row_bytes(size_t cols) { return (cols + kQK5 - 1) / kQK5 * kBlockBytes; }
 inline size_t tile_full_columns(size_t cols) { return cols / kQK5 * kBlockBytes; }
@@ -74,9 +78,10 @@ inline size_t tile_row_bytes(size_t cols) {  // pack.rs:222-225
 }
 inline size_t device_row_bytes(size_t cols) { return (tile_row_bytes(cols) + kChunk - 1) / kChunk * kChunk; }
 inline size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+inline size_t staged_bytes(size_t cols) { return kStageHeader + device_row_bytes(cols) * 8; }
 
 struct Geometry {
-    size_t rows, cols, padded_rows, n_tiles, tbr, dbr, n_chunks, device_bytes;
+    size_t rows, cols, padded_rows, n_tiles, n_groups, tbr, dbr, n_chunks, device_bytes;
 };
 
 inline Geometry geometry(size_t rows, size_t cols) {
@@ -85,6 +90,7 @@ inline Geometry geometry(size_t rows, size_t cols) {
     g.cols = cols;
     g.padded_rows = round_up(rows, kTileRows);
     g.n_tiles = g.padded_rows / kTileRows;
+    g.n_groups = (g.n_tiles + kTileGroup - 1) / kTileGroup;
     g.tbr = tile_row_bytes(cols);
     g.dbr = device_row_bytes(cols);
     g.n_chunks = g.dbr / kChunk;
@@ -92,7 +98,66 @@ inline Geometry geometry(size_t rows, size_t cols) {
     return g;
 }
 
+// Byte offset of (row r, device byte-column c) in the device layout (vx_layout in include/velurex_hip.h).
+__host__ __device__ inline uint64_t layout_offset(uint64_t r, uint32_t c, uint32_t n_tiles, uint32_t n_chunks) {
+    const uint32_t tile = static_cast<uint32_t>(r / kTileRows);
+    const uint32_t grp = tile / kTileGroup, t = tile - grp * kTileGroup;
+    const uint32_t T = (n_tiles - grp * kTileGroup) < static_cast<uint32_t>(kTileGroup) ? n_tiles - grp * kTileGroup
+                                                                                         : static_cast<uint32_t>(kTileGroup);
+    const uint32_t q = c / kChunk;
+    const uint64_t kib = static_cast<uint64_t>(grp) * kTileGroup * n_chunks + static_cast<uint64_t>(q) * T + t;
+    return kib * 1024u + (r % kTileRows) * kChunk + c % kChunk;
+}
+
 int check_shape(size_t rows, size_t cols);
+
+// ---- GEMV jobs --------------------------------------------------------------------------------------------------------
+
+enum OutKind : uint32_t {
+    kOutI32 = 0,       // int32 accumulators
+    kOutF32Post = 1,   // float(acc) * post, post = weight_scale / act_scale computed on the host
+    kOutF32Dev = 2,    // float(acc) * (weight_scale / *act_scale_dev), zeros when the scale is not > 0
+};
+
+// One GEMV of a launch: rows x cols weights in the device layout times one staged activation vector.
+struct Job {
+    const uint8_t* w;           // device layout
+    const uint8_t* staged;      // staged activations (kStageHeader + n_chunks * 128 bytes)
+    int32_t* part;              // K-slice partial sums [kslices][padded_rows] (kslices > 1)
+    void* out;                  // rows values
+    const float* act_scale;     // kOutF32Dev
+    float post;                 // kOutF32Post
+    float weight_scale;         // kOutF32Dev
+    uint32_t out_kind;
+    uint32_t rows, padded_rows, n_tiles, n_chunks;
+    uint32_t kslices, slice_chunks;  // K split: slices of slice_chunks chunks (the last may be shorter)
+    uint32_t item_begin;             // first work item of this job in the launch
+    uint32_t pad;
+};
+
+struct LaunchArgs {
+    const Job* jobs;       // device array of n_jobs jobs, or nullptr: use `one`
+    uint32_t n_jobs;
+    uint32_t total_items;  // work items: (tile group, K slice) pairs summed over the jobs
+    Job one;
+};
+
+constexpr uint32_t kMaxSliceChunks = 40;  // chunks per K slice staged in LDS (5 KiB of activations)
+
+// Host planner: fills kslices/slice_chunks of a job. `target_items` spreads a lone GEMV over the GPU; 0 keeps slices as
+// long as kMaxSliceChunks allows (the batched launches, which have work enough).
+void plan_job(Job& j, const Geometry& g, uint32_t target_items);
+inline uint32_t job_items(const Job& j) {
+    return (j.n_tiles + kTileGroup - 1) / kTileGroup * j.kslices;
+}
+
+int launch_stage(const int8_t* acts, size_t cols, uint8_t* staged, hipStream_t stream);
+int launch_gemv(const LaunchArgs& a, uint32_t max_rows, bool any_split, int num_cus, hipStream_t stream);
+int launch_device_layout(const uint8_t* planar_dev, const Geometry& g, uint8_t* dst, hipStream_t stream);
+int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
+int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
+size_t find_invalid_byte(const uint8_t* planar, size_t n);
+void planar_to_device_layout(const uint8_t* planar, const Geometry& g, uint8_t* dst);
 
 // ---- device state -------------------------------------------------------------------------------------------------------
 
@@ -104,7 +169,7 @@ int device_info(DeviceInfo* out);  // current device; VX_ERR_UNSUPPORTED if it i
 
 }  // namespace vx
 
-// ---- the matrix handle --------------------------------------------------------------------------------------------------
+// ---- handles ------------------------------------------------------------------------------------------------------------
 
 struct vx_matrix {
     uint32_t magic;
@@ -112,12 +177,24 @@ struct vx_matrix {
     float weight_scale;
     int device;
     int num_cus;
+    uint32_t kslices, slice_chunks;  // K split of a lone GEMV on this matrix
     uint8_t* d_w;       // weights, device layout (vx_layout)
-    int32_t* d_acc;     // split-K accumulators, padded_rows, kept at zero between calls
-    uint32_t* d_cnt;    // split-K arrival counters, n_tiles, kept at zero between calls
-    uint2* d_actp;      // activation staging: one entry per device byte-column
+    int32_t* d_part;    // K-slice partial sums of a lone GEMV
+    uint8_t* d_staged;  // activation staging of the calls that take raw int8 activations
     int8_t* d_io;       // host-API staging: cols bytes of activations + padded_rows * 4 bytes of output
     std::mutex mu;      // serialises the host-pointer API on this handle
 };
 
-constexpr uint32_t kMatrixMagic = 0x56584d31u;  // "VXM1"
+constexpr uint32_t kMatrixMagic = 0x56584d32u;  // "VXM2"
+
+struct vx_plan {
+    uint32_t magic;
+    int device;
+    int num_cus;
+    vx::Job* d_jobs;
+    int32_t* d_part;
+    uint32_t n_jobs, total_items, max_rows;
+    bool any_split;
+};
+
+constexpr uint32_t kPlanMagic = 0x56585031u;  // "VXP1"

@@ -42,11 +42,11 @@ def test_status_codes_match_the_reference():
     L = _lib.lib()
     assert L.vx_status_string(0) == b"ok"
     assert L.vx_status_string(999) == b"unknown status"
-    assert L.vx_abi_version() == 1 and L.vx_version() == b"0.1.0"
+    assert L.vx_abi_version() == 2 and L.vx_version() == b"0.2.0"
 
 
 def test_layout_matches_the_oracle(oracle):
-    for rows, cols in [(1, 1), (64, 160), (65, 161), (3072, 3072), (23040, 3072), (3072, 23040), (7, 4096)]:
+    for rows, cols in [(1, 1), (64, 160), (65, 161), (3072, 3072), (23040, 3072), (3072, 23040), (7, 4096), (1100, 160)]:
         lay = _lib.layout(rows, cols)
         assert lay["tile_rows"] == 64
         assert lay["padded_rows"] == -(-rows // 64) * 64
@@ -56,10 +56,12 @@ def test_layout_matches_the_oracle(oracle):
         assert lay["device_bytes"] == lay["padded_rows"] * lay["device_row_bytes"]
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 161), (64, 160), (70, 3072), (130, 4096), (5, 23040)])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 161), (64, 160), (70, 3072), (130, 4096), (5, 23040), (1100, 160),
+                                       (2049, 321)])
 def test_device_layout_pack_places_every_byte(oracle, rows, cols):
-    # The device layout (velurex_hip.h, vx_layout): tile row bytes (the oracle's tile_byte, pack.rs:240-256) placed at
-    # tile*64*dbr + (c/16)*1024 + (r%64)*16 + c%16; padding is byte 125 (five zero trits).
+    # The device layout (velurex_hip.h, vx_layout): tile row bytes (the oracle's tile_byte, pack.rs:240-256) in 16-byte
+    # chunks; chunk q of tile t sits at KiB g*16*n_chunks + q*T + t%16 (g = t//16, T = tiles of group g); padding is
+    # byte 125 (five zero trits).
     rng = np.random.default_rng(rows * 7 + cols)
     trits = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
     planar = oracle.pack_matrix(trits)
@@ -69,8 +71,14 @@ def test_device_layout_pack_places_every_byte(oracle, rows, cols):
     want = np.full((lay["padded_rows"], dbr), 125, np.uint8)
     for r in range(rows):
         want[r, :tbr] = oracle.tile_row(planar[r], cols)
-    t = want.reshape(-1, 64, dbr // 16, 16).transpose(0, 2, 1, 3).reshape(-1)
-    assert np.array_equal(dev, t)
+    n_tiles, n_chunks = lay["padded_rows"] // 64, dbr // 16
+    tiles = want.reshape(n_tiles, 64, n_chunks, 16).transpose(0, 2, 1, 3)  # [tile][chunk][row][16]
+    parts = []
+    for g0 in range(0, n_tiles, 16):
+        grp = tiles[g0:g0 + 16]                                               # [T][chunk][row][16]
+        parts.append(grp.transpose(1, 0, 2, 3).reshape(-1))                  # chunk-major, then tile
+    assert lay["tile_group"] == 16
+    assert np.array_equal(dev, np.concatenate(parts))
 
 
 def test_invalid_bytes_are_rejected(oracle):
@@ -102,4 +110,11 @@ def test_argument_errors_without_gpu():
     assert L.vx_layout(1, 1, ctypes.byref(lay)) == 2                              # wrong struct_size
     with pytest.raises(_lib.VxError):
         _lib.staged_bytes(0)
-    assert _lib.staged_bytes(3072) == 624 * 8
+    assert _lib.staged_bytes(3072) == 64 + 624 * 8
+    # plans: argument checks happen before any device work
+    jobs = (_lib.GemvJob * 1)()
+    jobs[0].struct_size = ctypes.sizeof(_lib.GemvJob)
+    assert L.vx_plan_create(jobs, 0, ctypes.byref(h)) == 2                       # no jobs
+    assert L.vx_plan_create(None, 1, ctypes.byref(h)) == 1                       # NULL jobs
+    assert L.vx_plan_run(None, None) == 14                                        # NULL plan
+    assert L.vx_plan_free(None) == 0

@@ -200,3 +200,94 @@ def test_golden_fixtures(torch_dev):
         layer.forward(z["acts"], float(z["act_scale"]), y)
         assert np.array_equal(y.view(np.uint32), z["y"].view(np.uint32)), name
         layer.close()
+
+
+def test_batched_plan_mixed_jobs(torch_dev, oracle):
+    """vx_plan_*: many GEMVs in one persistent launch, int32 and fp32 (scale read from device memory), long rows split
+    into K slices; the plan runs again after its inputs change (its pointers are fixed, the contents are not)."""
+    from quintrit_amd import VelurexHipLayer, _lib
+    torch = torch_dev
+    L = _lib.lib()
+    rng = np.random.default_rng(2024)
+    shapes = [(5120, 3072), (3072, 3072), (3072, 23040), (65, 161), (1, 1), (1100, 160), (7, 131072), (2560, 6912)]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    layers, mats, staged, outs, scales, jobs = [], [], [], [], [], []
+    for i, (rows, cols) in enumerate(shapes):
+        print(f"[plan] job {i}: {rows}x{cols}", flush=True)
+        t = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+        layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, float(0.01 * (i + 1)))
+        nb = _lib.staged_bytes(cols)
+        st = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        f32 = i % 2 == 1
+        out = torch.empty(rows, dtype=torch.float32 if f32 else torch.int32, device="cuda")
+        sc = torch.tensor([0.5 + i], dtype=torch.float32, device="cuda")
+        layers.append(layer), mats.append(t), staged.append(st), outs.append(out), scales.append(sc)
+        jobs.append(_lib.GemvJob(out_f32=int(f32), matrix=layer.handle.value, staged=st.data_ptr(), staged_len=nb,
+                                 act_scale_dev=sc.data_ptr(), out=out.data_ptr(), out_capacity=rows))
+    plan = _lib.Plan(jobs)
+    assert plan.work_items() > 0
+    for rep in range(2):
+        acts = []
+        for (rows, cols), st in zip(shapes, staged):
+            a = rng.integers(-128, 128, size=cols, dtype=np.int8)
+            da = torch.from_numpy(a).cuda()
+            _lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(da.data_ptr()), cols, cols, ctypes.c_void_p(st.data_ptr()),
+                                           st.numel(), stream))
+            acts.append(a)
+        plan.run(stream)
+        torch.cuda.synchronize()
+        for i, ((rows, cols), t, a, out) in enumerate(zip(shapes, mats, acts, outs)):
+            want = exact_gemv(t, a)
+            got = out.cpu().numpy()
+            if i % 2 == 1:
+                y = oracle.epilogue_f32(want.astype(np.int32), float(np.float32(0.01 * (i + 1))), 0.5 + i)
+                assert np.array_equal(got.view(np.uint32), y.view(np.uint32)), (rep, i)
+            else:
+                assert np.array_equal(got.astype(np.int64), want), (rep, i)
+    # a non-positive device scale gives zeros (layer.rs:246-253)
+    scales[1].fill_(0.0)
+    plan.run(stream)
+    torch.cuda.synchronize()
+    assert np.array_equal(outs[1].cpu().numpy().view(np.uint32), np.zeros(shapes[1][0], np.uint32))
+    plan.close()
+    for layer in layers:
+        layer.close()
+
+
+def test_plan_in_hip_graph_replays(torch_dev, oracle):
+    """A plan captured in a HIP graph gives the eager result on every replay, with eager work in between."""
+    from quintrit_amd import VelurexHipLayer, _lib
+    torch = torch_dev
+    L = _lib.lib()
+    rng = np.random.default_rng(77)
+    rows, cols = 3072, 23040
+    t = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+    layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, 1.0)
+    a = rng.integers(-128, 128, size=cols, dtype=np.int8)
+    da = torch.from_numpy(a).cuda()
+    nb = _lib.staged_bytes(cols)
+    st = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    out = torch.empty(rows, dtype=torch.int32, device="cuda")
+    plan = _lib.Plan([_lib.GemvJob(out_f32=0, matrix=layer.handle.value, staged=st.data_ptr(), staged_len=nb,
+                                   act_scale_dev=None, out=out.data_ptr(), out_capacity=rows)])
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        sp = ctypes.c_void_p(s.cuda_stream)
+        _lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(da.data_ptr()), cols, cols, ctypes.c_void_p(st.data_ptr()), nb, sp))
+        plan.run(sp)
+    torch.cuda.synchronize()
+    eager = out.cpu().numpy().copy()
+    assert np.array_equal(eager.astype(np.int64), exact_gemv(t, a))
+    with torch.cuda.graph(g, stream=s):
+        sp = ctypes.c_void_p(s.cuda_stream)
+        _lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(da.data_ptr()), cols, cols, ctypes.c_void_p(st.data_ptr()), nb, sp))
+        plan.run(sp)
+    for _ in range(4):
+        out.fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), eager)
+    plan.close()
+    layer.close()
