@@ -31,6 +31,9 @@ LAYERS, HIDDEN, FFN, KV = 40, 3072, 23040, 1024
 LAYER_SHAPES = [("qkv", HIDDEN + 2 * KV, HIDDEN), ("o", HIDDEN, HIDDEN), ("gate_up", 2 * FFN, HIDDEN),
                 ("down", HIDDEN, FFN)]
 REF_CPU_GWEIGHTS = 221.6  # quintrit_512, 4 threads, EPYC 9V45 (docs/benchmarks.md:77)
+# HBM bytes of one full-step gemv_kernel launch, from rocprofv3 FETCH_SIZE and WRITE_SIZE scaled by a plain-copy
+# calibration (profiles/gemv_kernel_falcon3_projection_stream.md). Only valid for the default 40-layer workload.
+TRAFFIC_BYTES_PER_STEP = 1_893_508 * 1024
 
 
 def parse():
@@ -42,6 +45,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only copy 256 MiB device to device 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -226,6 +231,14 @@ def main():
         print(json.dumps({"error": "no GPU"}))
         return 1
     torch.cuda.set_device(0)
+    if args.copy_probe:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel(), "copies": 5}), flush=True)
+        return 0
     log(f"building the {args.layers}-layer weight stream on the GPU")
     st = Stream(torch, L, _lib, args.layers)
     log(f"{st.weights} weights, {st.alg_bytes / 1e9:.4f} GB algorithmic, {st.device_bytes / 1e9:.4f} GB device layout")
@@ -260,7 +273,8 @@ def main():
         log(f"  chain of {len(st.jobs())} lone GEMVs in a graph: {mc:.4f} ms/step, {chain['alg_GBps']} GB/s")
         del g
     roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                "traffic": TRAFFIC_BYTES_PER_STEP if args.layers == LAYERS else None,
                 "kernel": "vx::gemv_kernel (one plan run: all 160 projections of a token; event-timed region also "
                           "holds the K-slice finish kernel)",
                 "alg_bytes_per_launch": int(st.alg_bytes)}

@@ -89,7 +89,7 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     m->d_staged = nullptr;
     m->d_io = nullptr;
     Job probe{};
-    plan_job(probe, m->g, 2u * static_cast<uint32_t>(di.num_cus));
+    plan_job(probe, m->g, static_cast<uint32_t>(di.num_cus));
     m->kslices = probe.kslices;
     m->slice_chunks = probe.slice_chunks;
 
@@ -177,7 +177,7 @@ static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint
     a.jobs = nullptr;
     a.n_jobs = 1;
     Job& j = a.one;
-    plan_job(j, m->g, 2u * static_cast<uint32_t>(m->num_cus));
+    plan_job(j, m->g, static_cast<uint32_t>(m->num_cus));
     j.w = m->d_w;
     j.staged = staged;
     j.part = m->d_part;
@@ -188,7 +188,7 @@ static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint
     j.out_kind = out_kind;
     j.item_begin = 0;
     a.total_items = job_items(j);
-    return launch_gemv(a, j.rows, j.kslices > 1, m->num_cus, s);
+    return launch_gemv(a, j.rows, nullptr, j.kslices > 1 ? 1u : 0u, m->num_cus, s);
 }
 
 // out = float(acc) * (ws / as) with the division done once here, as the layers do; zeros when as <= 0 or NaN
@@ -497,6 +497,7 @@ static int check_plan(const vx_plan_t* p) {
 static void destroy_plan(vx_plan* p) {
     if (p->d_jobs) (void)hipFree(p->d_jobs);
     if (p->d_part) (void)hipFree(p->d_part);
+    if (p->d_split) (void)hipFree(p->d_split);
     p->magic = 0;
     delete p;
 }
@@ -510,8 +511,8 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
     VX_TRY(device_info(&di));
     std::vector<Job> hj(n_jobs);
     size_t part_ints = 0;
-    uint32_t items = 0, max_rows = 0;
-    bool any_split = false;
+    uint32_t items = 0;
+    std::vector<uint32_t> split;
     for (size_t i = 0; i < n_jobs; ++i) {
         const vx_gemv_job_t& u = jobs[i];
         if (u.struct_size != sizeof(vx_gemv_job_t))
@@ -543,9 +544,8 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
         if (j.kslices > 1) {
             j.part = reinterpret_cast<int32_t*>(part_ints);  // offset, rebased below
             part_ints += static_cast<size_t>(j.kslices) * j.padded_rows;
-            any_split = true;
+            split.push_back(static_cast<uint32_t>(i));
         }
-        max_rows = std::max(max_rows, j.rows);
     }
     vx_plan* p = new vx_plan();
     p->magic = kPlanMagic;
@@ -553,12 +553,17 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
     p->num_cus = di.num_cus;
     p->d_jobs = nullptr;
     p->d_part = nullptr;
+    p->d_split = nullptr;
     p->n_jobs = static_cast<uint32_t>(n_jobs);
     p->total_items = items;
-    p->max_rows = max_rows;
-    p->any_split = any_split;
+    p->max_rows = 0;
+    p->n_split = static_cast<uint32_t>(split.size());
+    for (uint32_t i : split) p->max_rows = std::max(p->max_rows, hj[i].rows);
     hipError_t e = hipMalloc(&p->d_jobs, n_jobs * sizeof(Job));
     if (e == hipSuccess && part_ints) e = hipMalloc(&p->d_part, part_ints * sizeof(int32_t));
+    if (e == hipSuccess && !split.empty()) e = hipMalloc(&p->d_split, split.size() * sizeof(uint32_t));
+    if (e == hipSuccess && !split.empty())
+        e = hipMemcpy(p->d_split, split.data(), split.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
     if (e == hipSuccess) {
         for (auto& j : hj)
             if (j.kslices > 1) j.part = p->d_part + reinterpret_cast<size_t>(j.part);
@@ -590,7 +595,7 @@ int vx_plan_run(const vx_plan_t* plan, void* stream) {
         a.jobs = plan->d_jobs;
         a.n_jobs = plan->n_jobs;
         a.total_items = plan->total_items;
-        return launch_gemv(a, plan->max_rows, plan->any_split, plan->num_cus, static_cast<hipStream_t>(stream));
+        return launch_gemv(a, plan->max_rows, plan->d_split, plan->n_split, plan->num_cus, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -178,16 +178,13 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    for (uint32_t i = tid; i < 256u * 16u; i += kWaves * 64u) {  // 16 uint4 stores per entry
-        const uint32_t e = digit_nibbles(i >> 4);
-        reinterpret_cast<uint4*>(tab)[i] = make_uint4(e, e, e, e);
-    }
     const char* tabb = reinterpret_cast<const char*>(tab);
     const uint32_t lane_off = lane * 4u;
+    const c_job* cj = (const c_job*)(args.jobs);
 
     uint32_t j = 0, buf = 0;
+    bool first = true;
     for (uint32_t item = blockIdx.x; item < args.total_items; item += gridDim.x, buf ^= 1u) {
-        const c_job* cj = (const c_job*)(args.jobs);
         if (MANY)
             while (j + 1 < args.n_jobs && item >= cj[j + 1].item_begin) ++j;
         Job jb;
@@ -199,22 +196,38 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
         const uint32_t q0 = ks * jb.slice_chunks;
         const uint32_t nq = min(jb.slice_chunks, jb.n_chunks - q0);
         const uint32_t nqp = (nq + kGroup - 1) / kGroup * kGroup;
-
-        // Stage this slice's activations (zero past nq, so the clamped tail loads below add nothing).
+        const bool active = wave < T;
+        const g_u4* wp = reinterpret_cast<const g_u4*>(0);
+        size_t cs = 0;
+        // The first weight group is requested before the table build, the activation staging and the barrier, so
+        // its HBM latency overlaps them.
+        u32x4 b[kGroup];
+        if (active) {
+            wp = (const g_u4*)(jb.w) + (static_cast<size_t>(grp) * kTileGroup * jb.n_chunks + static_cast<size_t>(q0) * T + wave) * 64u + lane;
+            cs = static_cast<size_t>(T) * 64u;  // chunk stride of a tile, in uint4
+#pragma unroll
+            for (int i = 0; i < kGroup; ++i) b[i] = __builtin_nontemporal_load(wp + min(static_cast<uint32_t>(i), nq - 1u) * cs);
+        }
+        if (first) {
+            for (uint32_t i = tid; i < 256u * 16u; i += kWaves * 64u) {  // 16 uint4 stores per entry
+                const uint32_t e = digit_nibbles(i >> 4);
+                reinterpret_cast<uint4*>(tab)[i] = make_uint4(e, e, e, e);
+            }
+            first = false;
+        }
+        // Stage this slice's activations (zero past nq, so the clamped tail loads add nothing).
         const uint4* src = reinterpret_cast<const uint4*>(jb.staged + kStageHeader) + static_cast<size_t>(q0) * 8u;
         uint4* ab = acts[buf];
         for (uint32_t i = tid; i < nqp * 8u; i += kWaves * 64u) ab[i] = i < nq * 8u ? src[i] : make_uint4(0, 0, 0, 0);
         __syncthreads();
 
-        if (wave < T) {
-            const g_u4* wp = (const g_u4*)(jb.w) +
-                             (static_cast<size_t>(grp) * kTileGroup * jb.n_chunks + static_cast<size_t>(q0) * T + wave) * 64u + lane;
-            const size_t cs = static_cast<size_t>(T) * 64u;  // chunk stride of a tile, in uint4
+        if (active) {
             int acc_lo = 0, acc_hi = 0;
             for (uint32_t g = 0; g < nq; g += kGroup) {
-                u32x4 b[kGroup];
+                if (g) {
 #pragma unroll
-                for (int i = 0; i < kGroup; ++i) b[i] = __builtin_nontemporal_load(wp + min(g + i, nq - 1u) * cs);
+                    for (int i = 0; i < kGroup; ++i) b[i] = __builtin_nontemporal_load(wp + min(g + i, nq - 1u) * cs);
+                }
 #pragma unroll
                 for (int i = 0; i < kGroup; ++i) {
                     const uint32_t dw[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
@@ -248,20 +261,34 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
     }
 }
 
-// Adds the K-slice partial sums of every split job and applies its epilogue.
+// Adds the K-slice partial sums of the split jobs and applies their epilogue. Block = 64 rows x 4 waves; wave w adds
+// the slices w, w + 4, ... of its 64 rows, then the 4 waves combine through LDS. blockIdx.y indexes `split` (the
+// plan's split jobs) or, without a job array, the one job.
 template <bool MANY>
-__global__ __launch_bounds__(256) void finish_kernel(LaunchArgs args) {
+__global__ __launch_bounds__(256) void finish_kernel(LaunchArgs args, const uint32_t* __restrict__ split) {
+    __shared__ int red[4][64];
     Job jb;
-    if (MANY) __builtin_memcpy(&jb, (const Job*)((const c_job*)(args.jobs) + blockIdx.y), sizeof(Job));
+    if (MANY) __builtin_memcpy(&jb, (const Job*)((const c_job*)(args.jobs) + split[blockIdx.y]), sizeof(Job));
     else jb = args.one;
-    if (jb.kslices == 1) return;
-    const uint32_t row = blockIdx.x * 256u + threadIdx.x;
-    if (row >= jb.rows) return;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.x * 64u;
+    if (row0 >= jb.rows) return;
+    const uint32_t row = row0 + lane;
+    const int32_t* p = jb.part + row;
     int s = 0;
-    for (uint32_t k = 0; k < jb.kslices; ++k) s += jb.part[static_cast<size_t>(k) * jb.padded_rows + row];
-    bool zero;
-    const float post = job_post(jb, &zero);
-    store_out(jb, row, s - staged_sum(jb), post, zero);
+    uint32_t k = wave;
+    for (; k + 12 < jb.kslices; k += 16)
+        s += p[static_cast<size_t>(k) * jb.padded_rows] + p[static_cast<size_t>(k + 4) * jb.padded_rows] +
+             p[static_cast<size_t>(k + 8) * jb.padded_rows] + p[static_cast<size_t>(k + 12) * jb.padded_rows];
+    for (; k < jb.kslices; k += 4) s += p[static_cast<size_t>(k) * jb.padded_rows];
+    red[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0) {
+        s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+        bool zero;
+        const float post = job_post(jb, &zero);
+        store_out(jb, row, s - staged_sum(jb), post, zero);
+    }
 }
 
 // ---- host side ---------------------------------------------------------------------------------------------------------------
@@ -287,15 +314,17 @@ int launch_stage(const int8_t* acts, size_t cols, uint8_t* staged, hipStream_t s
     return VX_OK;
 }
 
-int launch_gemv(const LaunchArgs& a, uint32_t max_rows, bool any_split, int num_cus, hipStream_t stream) {
+int launch_gemv(const LaunchArgs& a, uint32_t max_rows, const uint32_t* split, uint32_t n_split, int num_cus,
+                hipStream_t stream) {
     if (a.total_items == 0) return VX_OK;
     const uint32_t grid = std::min<uint32_t>(a.total_items, 2u * static_cast<uint32_t>(num_cus));
     if (a.jobs) hipLaunchKernelGGL(gemv_kernel<true>, dim3(grid), dim3(kWaves * 64), 0, stream, a);
     else hipLaunchKernelGGL(gemv_kernel<false>, dim3(grid), dim3(kWaves * 64), 0, stream, a);
     VX_HIP(hipGetLastError());
-    if (any_split) {
-        if (a.jobs) hipLaunchKernelGGL(finish_kernel<true>, dim3((max_rows + 255u) / 256u, a.n_jobs), dim3(256), 0, stream, a);
-        else hipLaunchKernelGGL(finish_kernel<false>, dim3((max_rows + 255u) / 256u, 1), dim3(256), 0, stream, a);
+    if (n_split) {
+        const dim3 fgrid((max_rows + 63u) / 64u, n_split);
+        if (a.jobs) hipLaunchKernelGGL(finish_kernel<true>, fgrid, dim3(256), 0, stream, a, split);
+        else hipLaunchKernelGGL(finish_kernel<false>, fgrid, dim3(256), 0, stream, a, split);
         VX_HIP(hipGetLastError());
     }
     return VX_OK;

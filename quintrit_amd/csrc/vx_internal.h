@@ -152,7 +152,10 @@ inline uint32_t job_items(const Job& j) {
 }
 
 int launch_stage(const int8_t* acts, size_t cols, uint8_t* staged, hipStream_t stream);
-int launch_gemv(const LaunchArgs& a, uint32_t max_rows, bool any_split, int num_cus, hipStream_t stream);
+// Launches the GEMV kernel and, when n_split > 0, the finish kernel over the split jobs (`split`: device array of their
+// indices in a.jobs; unused without a job array).
+int launch_gemv(const LaunchArgs& a, uint32_t max_rows, const uint32_t* split, uint32_t n_split, int num_cus,
+                hipStream_t stream);
 int launch_device_layout(const uint8_t* planar_dev, const Geometry& g, uint8_t* dst, hipStream_t stream);
 int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
 int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
@@ -193,8 +196,8 @@ struct vx_plan {
     int num_cus;
     vx::Job* d_jobs;
     int32_t* d_part;
-    uint32_t n_jobs, total_items, max_rows;
-    bool any_split;
+    uint32_t* d_split;  // indices of the jobs split into K slices
+    uint32_t n_jobs, total_items, max_rows, n_split;
 };
 
 constexpr uint32_t kPlanMagic = 0x56585031u;  // "VXP1"
