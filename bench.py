@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
+    ap.add_argument("--workload", choices=["stream", "gemm"], default="stream",
+                    help="stream: the driver's line (configs[1]); gemm: the batched GEMM of configs[2]")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device to device 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -218,6 +220,46 @@ def cpu_baseline(budget_s: float):
                       f"weights/pass), scalar C restatement of the table kernel, 1 thread, {dt:.1f} s"}
 
 
+def gemm_bench(torch, L, lib, args) -> int:
+    """Y = X W^T for W 23040 x 3072 and 3072 x 23040 (velurex), X M x K int8 quantized per
+    token from N(0,1), M in {8, 32, 128, 512}; exact int32 on the matrix cores. One JSON line per call of this mode;
+    ops = 2 M N K; bytes = weights (N K / 5) + X + Y."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xC2)
+    results = []
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for rows, cols in ((23040, 3072), (3072, 23040)):
+        planar = random_planar(torch, rows, cols, gen)
+        h = ctypes.c_void_p()
+        lib.check(L.vx_matrix_create_dev(ctypes.c_void_p(planar.data_ptr()), planar.numel(), rows, cols,
+                                         ctypes.c_float(0.02), ctypes.byref(h)))
+        del planar
+        for m in (8, 32, 128, 512):
+            x = torch.randn((m, cols), device="cuda", generator=gen)
+            q = torch.empty((m, cols), dtype=torch.int8, device="cuda")
+            for i in range(m):
+                q[i] = quantize_i8(torch, x[i])[0]
+            y = torch.empty((m, rows), dtype=torch.int32, device="cuda")
+            n = ctypes.c_size_t()
+            lib.check(L.vx_gemm_workspace_bytes(h, m, ctypes.byref(n)))
+            ws = torch.empty(n.value, dtype=torch.uint8, device="cuda")
+            call = lambda: lib.check(L.vx_gemm_i32_dev(h, ctypes.c_void_p(q.data_ptr()), m, cols,  # noqa: E731
+                                                       ctypes.c_void_p(y.data_ptr()), rows,
+                                                       ctypes.c_void_p(ws.data_ptr()), n.value, stream))
+            ms, _ = time_fn(torch, call, max(5, args.steps), max(2, args.warmup))
+            ops = 2.0 * m * rows * cols
+            byts = rows * cols / 5.0 + m * cols + 4.0 * m * rows
+            r = {"rows": rows, "cols": cols, "m": m, "us": round(ms * 1e3, 2), "TOPS": round(ops / (ms / 1e3) / 1e12, 2),
+                 "GBps": round(byts / (ms / 1e3) / 1e9, 1)}
+            log(f"gemm {rows}x{cols} m={m}: {r['us']} us, {r['TOPS']} TOPS, {r['GBps']} GB/s")
+            results.append(r)
+        lib.check(L.vx_matrix_free(h))
+    print(json.dumps({"workload": "batched ternary GEMM, BASELINE.json configs[2]", "dtype": "int8 x ternary -> int32",
+                      "data": "synthetic", "note": "time per vx_gemm_i32_dev call (activation staging + GEMM + "
+                      "K-slice finish), HIP events", "results": results}), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -239,6 +281,8 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": src.numel(), "copies": 5}), flush=True)
         return 0
+    if args.workload == "gemm":
+        return gemm_bench(torch, L, _lib, args)
     log(f"building the {args.layers}-layer weight stream on the GPU")
     st = Stream(torch, L, _lib, args.layers)
     log(f"{st.weights} weights, {st.alg_bytes / 1e9:.4f} GB algorithmic, {st.device_bytes / 1e9:.4f} GB device layout")

@@ -233,6 +233,23 @@ int vx_plan_work_items(const vx_plan_t* plan, uint32_t* out_items);
 /* Frees a plan (NULL is a no-op); waits for the device first. */
 int vx_plan_free(vx_plan_t* plan);
 
+/* ---- batched (multi-token) GEMM ---------------------------------------------------------------------------------- */
+
+/* Largest token count of one GEMM call. */
+#define VX_MAX_GEMM_TOKENS 65536
+
+/*
+ * Y[t][i] = sum_j W[i][j] * X[t][j] for t < m tokens, exact int32: the same numbers as m calls of vx_gemv_i32_dev, on
+ * the matrix cores (v_mfma_i32_16x16x64_i8). x: m rows of ldx >= cols int8 (device); y: m rows of ldy >= rows int32
+ * (device); workspace: device memory of vx_gemm_workspace_bytes(matrix, m) bytes, 256-byte aligned, owned by the
+ * caller (the call allocates nothing, so it can be captured in a HIP graph; concurrent calls need distinct
+ * workspaces). The reference has no multi-token kernel: its prefill calls the GEMV once per token
+ * (quintrit-runtime/src/engine.rs:625-631), which defines the result.
+ */
+int vx_gemm_workspace_bytes(const vx_matrix_t* matrix, size_t m, size_t* out_bytes);
+int vx_gemm_i32_dev(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t ldx, int32_t* y, size_t ldy,
+                    void* workspace, size_t workspace_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

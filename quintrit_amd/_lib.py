@@ -69,6 +69,8 @@ SIGNATURES = {
     "vx_plan_run": (_i32, [_vp, _vp]),
     "vx_plan_work_items": (_i32, [_vp, _vp]),
     "vx_plan_free": (_i32, [_vp]),
+    "vx_gemm_workspace_bytes": (_i32, [_vp, _sz, _vp]),
+    "vx_gemm_i32_dev": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, _sz, _vp]),
 }
 
 

@@ -159,6 +159,9 @@ int launch_gemv(const LaunchArgs& a, uint32_t max_rows, const uint32_t* split, u
 int launch_device_layout(const uint8_t* planar_dev, const Geometry& g, uint8_t* dst, hipStream_t stream);
 int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
 int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
+size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
+int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
+                size_t ldy, uint8_t* ws, hipStream_t stream);
 size_t find_invalid_byte(const uint8_t* planar, size_t n);
 void planar_to_device_layout(const uint8_t* planar, const Geometry& g, uint8_t* dst);
 

@@ -118,3 +118,6 @@ def test_argument_errors_without_gpu():
     assert L.vx_plan_create(None, 1, ctypes.byref(h)) == 1                       # NULL jobs
     assert L.vx_plan_run(None, None) == 14                                        # NULL plan
     assert L.vx_plan_free(None) == 0
+    n = ctypes.c_size_t()
+    assert L.vx_gemm_workspace_bytes(None, 8, ctypes.byref(n)) == 14               # NULL handle
+    assert L.vx_gemm_i32_dev(None, buf, 8, 64, buf, 64, buf, 64, None) == 14
