@@ -45,8 +45,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
-    ap.add_argument("--workload", choices=["stream", "gemm"], default="stream",
-                    help="stream: the driver's line (configs[1]); gemm: the batched GEMM of configs[2]")
+    ap.add_argument("--workload", choices=["stream", "gemm", "q2"], default="stream",
+                    help="stream: the driver's line (configs[1]); gemm: the batched GEMM of configs[2]; q2: the "
+                         "block-scaled GEMV stream of configs[4]")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device to device 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -260,6 +261,56 @@ def gemm_bench(torch, L, lib, args) -> int:
     return 0
 
 
+def q2_bench(torch, L, lib, args) -> int:
+    """the projections of one Qwen3-8B-like token (36 layers; q, o 4096 x 4096; k, v
+    1024 x 4096; gate, up 12288 x 4096; down 4096 x 12288) as Q2_0 GEMVs: velurex trits plus one fp16 scale per 64
+    weights (log-uniform in [0.005, 0.05]) stored beside them, Q8_0 activations (int8 uniform in [-127, 127], one f32
+    scale per 32, log-uniform in [0.005, 0.05]). One step = one plan run over all 252 projections."""
+    import numpy as np
+    layers = 36 if args.layers == LAYERS else args.layers
+    shapes = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096), (12288, 4096), (4096, 12288)]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xC4)
+    rng = np.random.default_rng(0xC4)
+    mats, jobs, keep = [], [], []
+    weights = 0
+    dev_bytes = 0
+    log(f"building {layers} layers of Q2_0 matrices")
+    for _ in range(layers):
+        for rows, cols in shapes:
+            planar = random_planar(torch, rows, cols, gen).cpu().numpy()
+            ws16 = np.exp(rng.uniform(np.log(0.005), np.log(0.05), size=rows * cols // 64)).astype(np.float16)
+            m = lib.Q2Matrix(planar, ws16, rows, cols)
+            del planar
+            acts = torch.randint(-127, 128, (cols,), dtype=torch.int8, device="cuda", generator=gen)
+            a_s = torch.from_numpy(np.exp(rng.uniform(np.log(0.005), np.log(0.05), size=cols // 32))
+                                   .astype(np.float32)).cuda()
+            out = torch.empty(rows, dtype=torch.float32, device="cuda")
+            jobs.append(lib.Q2Job(matrix=m.handle.value, acts=acts.data_ptr(), acts_len=cols, act_scales=a_s.data_ptr(),
+                                  n_act_scales=cols // 32, out=out.data_ptr(), out_capacity=rows))
+            mats.append(m)
+            keep.append((acts, a_s, out))
+            weights += rows * cols
+            n = ctypes.c_size_t()
+            lib.check(L.vx_matrix_memory_bytes(m.handle, ctypes.byref(n)))
+            dev_bytes += n.value
+    plan = lib.Q2Plan(jobs)
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    ms, _ = time_fn(torch, lambda: plan.run(stream()), args.steps, args.warmup)
+    alg = weights / 5.0 + 2.0 * weights / 64.0
+    r = {"workload": "Q2_0 projection stream, BASELINE.json configs[4]", "layers": layers, "weights": weights,
+         "ms_per_step": round(ms, 4), "Gweights_s": round(weights / (ms / 1e3) / 1e9, 1),
+         "alg_bytes": int(alg), "alg_GBps": round(alg / (ms / 1e3) / 1e9, 1),
+         "device_bytes": dev_bytes, "device_GBps": round(dev_bytes / (ms / 1e3) / 1e9, 1),
+         "tok_s_projection_bound": round(1e3 / ms, 1), "data": "synthetic", "dtype": "int8 x ternary, fp32 chains"}
+    log(f"q2 stream: {ms:.4f} ms/step, {r['Gweights_s']} Gweights/s, {r['alg_GBps']} GB/s algorithmic")
+    print(json.dumps(r), flush=True)
+    plan.close()
+    for m in mats:
+        m.close()
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -283,6 +334,8 @@ def main():
         return 0
     if args.workload == "gemm":
         return gemm_bench(torch, L, _lib, args)
+    if args.workload == "q2":
+        return q2_bench(torch, L, _lib, args)
     log(f"building the {args.layers}-layer weight stream on the GPU")
     st = Stream(torch, L, _lib, args.layers)
     log(f"{st.weights} weights, {st.alg_bytes / 1e9:.4f} GB algorithmic, {st.device_bytes / 1e9:.4f} GB device layout")

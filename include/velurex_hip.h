@@ -250,6 +250,40 @@ int vx_gemm_workspace_bytes(const vx_matrix_t* matrix, size_t m, size_t* out_byt
 int vx_gemm_i32_dev(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t ldx, int32_t* y, size_t ldy,
                     void* workspace, size_t workspace_len, void* stream);
 
+/* ---- block-scaled (Q2_0) GEMV -------------------------------------------------------------------------------------- */
+
+/*
+ * Q2_0 weights against Q8_0 activations (quintrit-core/src/block_scaled.rs; llama.cpp's ggml_vec_dot_q2_0_q8_0):
+ * ternary weights in the planar velurex layout plus one scale per 64 weights of a row (here fp16, stored beside the
+ * trits on the device; the reference keeps them as f32: each fp16 is widened exactly), int8 activations with one fp32
+ * scale per 32 values. out[r] is bit-identical to the reference's dot_row_scalar (block_scaled.rs:175-202): the eight
+ * lane sums of every 32-value block s are accumulated as fma(w_scale[s/2] * a_scale[s], lane, acc[(s/2) & 1][lane])
+ * in increasing s, then reduced ((l0+l4) + (l2+l6)) + ((l1+l5) + (l3+l7)).
+ * cols must be a multiple of 64 and at most 12288.
+ */
+int vx_q2_matrix_create(const uint8_t* planar, size_t planar_len, const uint16_t* scales_f16, size_t n_scales,
+                        size_t rows, size_t cols, vx_matrix_t** out_matrix);
+/* acts: cols int8 (device, 4-byte aligned); act_scales: cols/32 fp32 (device); out: rows fp32 (device). */
+int vx_q2_gemv_f32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, const float* act_scales,
+                       size_t n_act_scales, float* out, size_t out_capacity, void* stream);
+/* The exact integer part: out[(r * (cols/32) + s) * 8 + j] = sum_{k<4} t[r][32s + 4j + k] * acts[32s + 4j + k]. */
+int vx_q2_lane_sums_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, int32_t* out,
+                        size_t out_capacity, void* stream);
+
+typedef struct vx_q2_job {
+    uint32_t struct_size;        /* sizeof(vx_q2_job_t) */
+    uint32_t reserved;
+    const vx_matrix_t* matrix;   /* created by vx_q2_matrix_create */
+    const int8_t* acts;          /* device */
+    size_t acts_len;
+    const float* act_scales;     /* device */
+    size_t n_act_scales;
+    float* out;                  /* device */
+    size_t out_capacity;
+} vx_q2_job_t;
+/* A plan of Q2_0 GEMVs, run with vx_plan_run and freed with vx_plan_free like the velurex plans. */
+int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan);
+
 #ifdef __cplusplus
 }
 #endif

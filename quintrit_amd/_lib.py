@@ -71,6 +71,10 @@ SIGNATURES = {
     "vx_plan_free": (_i32, [_vp]),
     "vx_gemm_workspace_bytes": (_i32, [_vp, _sz, _vp]),
     "vx_gemm_i32_dev": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, _sz, _vp]),
+    "vx_q2_matrix_create": (_i32, [_vp, _sz, _vp, _sz, _sz, _sz, _vp]),
+    "vx_q2_gemv_f32_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _vp]),
+    "vx_q2_lane_sums_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "vx_q2_plan_create": (_i32, [_vp, _sz, _vp]),
 }
 
 
@@ -161,6 +165,59 @@ class Plan:
         if self._h:
             check(lib().vx_plan_free(self._h))
             self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Q2Job(ctypes.Structure):
+    """vx_q2_job_t (include/velurex_hip.h)."""
+    _fields_ = [("struct_size", ctypes.c_uint32), ("reserved", ctypes.c_uint32), ("matrix", ctypes.c_void_p),
+                ("acts", ctypes.c_void_p), ("acts_len", ctypes.c_size_t), ("act_scales", ctypes.c_void_p),
+                ("n_act_scales", ctypes.c_size_t), ("out", ctypes.c_void_p), ("out_capacity", ctypes.c_size_t)]
+
+
+class Q2Plan(Plan):
+    """A plan of Q2_0 GEMVs (vx_q2_plan_create), run and freed like Plan."""
+
+    def __init__(self, jobs):  # noqa: super().__init__ builds velurex plans
+        arr = (Q2Job * len(jobs))()
+        for i, j in enumerate(jobs):
+            arr[i] = j
+            arr[i].struct_size = ctypes.sizeof(Q2Job)
+        h = ctypes.c_void_p()
+        check(lib().vx_q2_plan_create(arr, len(jobs), ctypes.byref(h)))
+        self._h = h
+
+
+class Q2Matrix:
+    """A Q2_0 matrix in GPU memory (vx_q2_matrix_create): planar trits + fp16 scales, one per 64 weights."""
+
+    def __init__(self, planar, scales_f16, rows: int, cols: int):
+        import numpy as np
+        p = np.ascontiguousarray(planar, dtype=np.uint8).reshape(-1)
+        s = np.ascontiguousarray(scales_f16, dtype=np.float16).view(np.uint16).reshape(-1)
+        h = ctypes.c_void_p()
+        check(lib().vx_q2_matrix_create(p.ctypes.data_as(ctypes.c_void_p), p.size, s.ctypes.data_as(ctypes.c_void_p),
+                                        s.size, rows, cols, ctypes.byref(h)))
+        self.handle, self.rows, self.cols = h, rows, cols
+
+    def gemv_f32(self, acts_dev, act_scales_dev, out_dev, stream_ptr) -> None:
+        check(lib().vx_q2_gemv_f32_dev(self.handle, ctypes.c_void_p(acts_dev.data_ptr()), acts_dev.numel(),
+                                       ctypes.c_void_p(act_scales_dev.data_ptr()), act_scales_dev.numel(),
+                                       ctypes.c_void_p(out_dev.data_ptr()), out_dev.numel(), stream_ptr))
+
+    def lane_sums(self, acts_dev, out_dev, stream_ptr) -> None:
+        check(lib().vx_q2_lane_sums_dev(self.handle, ctypes.c_void_p(acts_dev.data_ptr()), acts_dev.numel(),
+                                        ctypes.c_void_p(out_dev.data_ptr()), out_dev.numel(), stream_ptr))
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().vx_matrix_free(self.handle))
+            self.handle = ctypes.c_void_p()
 
     def __del__(self):
         try:

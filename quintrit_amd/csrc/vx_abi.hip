@@ -49,6 +49,14 @@ static int check_matrix(const vx_matrix_t* m) {
     return VX_OK;
 }
 
+// Entry points of the GEMV/GEMM layout reject Q2_0 matrices and the other way round.
+static int check_kind(const vx_matrix_t* m, uint32_t kind) {
+    VX_TRY(check_matrix(m));
+    if (m->kind != kind)
+        VX_FAIL(VX_ERR_INVALID_HANDLE, "the matrix was created for %s", m->kind == kKindQ2 ? "the Q2_0 (block-scaled) GEMV" : "the velurex GEMV");
+    return VX_OK;
+}
+
 static int set_device_of(const vx_matrix_t* m) {
     int cur = -1;
     VX_HIP(hipGetDevice(&cur));
@@ -80,6 +88,7 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     VX_TRY(device_info(&di));
     vx_matrix* m = new vx_matrix();
     m->magic = kMatrixMagic;
+    m->kind = kKindVelurex;
     m->g = geometry(rows, cols);
     m->weight_scale = weight_scale;
     m->device = di.device;
@@ -341,7 +350,7 @@ static int check_staged(const vx_matrix_t* m, const void* staged, size_t staged_
 int vx_gemv_staged_i32_dev(const vx_matrix_t* matrix, const void* staged, size_t staged_len, int32_t* out,
                            size_t out_capacity, void* stream) {
     return guard([&]() -> int {
-        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_kind(matrix, kKindVelurex));
         VX_TRY(check_staged(matrix, staged, staged_len, out, out_capacity));
         VX_TRY(set_device_of(matrix));
         return run_single(matrix, static_cast<const uint8_t*>(staged), out, kOutI32, 1.0f, static_cast<hipStream_t>(stream));
@@ -351,7 +360,7 @@ int vx_gemv_staged_i32_dev(const vx_matrix_t* matrix, const void* staged, size_t
 int vx_gemv_staged_f32_dev(const vx_matrix_t* matrix, const void* staged, size_t staged_len, float act_scale, float* out,
                            size_t out_capacity, void* stream) {
     return guard([&]() -> int {
-        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_kind(matrix, kKindVelurex));
         VX_TRY(check_staged(matrix, staged, staged_len, out, out_capacity));
         VX_TRY(set_device_of(matrix));
         return gemv_f32_staged(matrix, static_cast<const uint8_t*>(staged), act_scale, out, static_cast<hipStream_t>(stream));
@@ -409,7 +418,7 @@ int vx_matrix_device_weights(const vx_matrix_t* matrix, const void** out_ptr) {
 int vx_gemv_i32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, int32_t* out, size_t out_capacity,
                     void* stream) {
     return guard([&]() -> int {
-        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_kind(matrix, kKindVelurex));
         VX_TRY(check_io(matrix, acts, acts_len, out, out_capacity));
         VX_TRY(set_device_of(matrix));
         return gemv_i32_dev(const_cast<vx_matrix*>(matrix), acts, out, static_cast<hipStream_t>(stream));
@@ -419,7 +428,7 @@ int vx_gemv_i32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_l
 int vx_gemv_f32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, float act_scale, float* out,
                     size_t out_capacity, void* stream) {
     return guard([&]() -> int {
-        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_kind(matrix, kKindVelurex));
         VX_TRY(check_io(matrix, acts, acts_len, out, out_capacity));
         VX_TRY(set_device_of(matrix));
         return gemv_f32_dev(const_cast<vx_matrix*>(matrix), acts, act_scale, out, static_cast<hipStream_t>(stream));
@@ -429,7 +438,7 @@ int vx_gemv_f32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_l
 int vx_layer_forward(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, float act_scale, float* out,
                      size_t out_capacity) {
     return guard([&]() -> int {
-        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_kind(matrix, kKindVelurex));
         VX_TRY(check_io(matrix, acts, acts_len, out, out_capacity));
         vx_matrix* m = const_cast<vx_matrix*>(matrix);
         std::lock_guard<std::mutex> lock(m->mu);
@@ -498,6 +507,7 @@ static void destroy_plan(vx_plan* p) {
     if (p->d_jobs) (void)hipFree(p->d_jobs);
     if (p->d_part) (void)hipFree(p->d_part);
     if (p->d_split) (void)hipFree(p->d_split);
+    if (p->d_q2jobs) (void)hipFree(p->d_q2jobs);
     p->magic = 0;
     delete p;
 }
@@ -517,7 +527,7 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
         const vx_gemv_job_t& u = jobs[i];
         if (u.struct_size != sizeof(vx_gemv_job_t))
             VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].struct_size is %u, expected %zu", i, u.struct_size, sizeof(vx_gemv_job_t));
-        VX_TRY(check_matrix(u.matrix));
+        VX_TRY(check_kind(u.matrix, kKindVelurex));
         const vx_matrix* m = u.matrix;
         if (m->device != di.device)
             VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].matrix lives on device %d, the current device is %d", i, m->device, di.device);
@@ -554,6 +564,7 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
     p->d_jobs = nullptr;
     p->d_part = nullptr;
     p->d_split = nullptr;
+    p->d_q2jobs = nullptr;
     p->n_jobs = static_cast<uint32_t>(n_jobs);
     p->total_items = items;
     p->max_rows = 0;
@@ -591,6 +602,13 @@ int vx_plan_run(const vx_plan_t* plan, void* stream) {
         int cur = -1;
         VX_HIP(hipGetDevice(&cur));
         if (cur != plan->device) VX_HIP(hipSetDevice(plan->device));
+        if (plan->d_q2jobs) {
+            Q2Args q{};
+            q.jobs = plan->d_q2jobs;
+            q.n_jobs = plan->n_jobs;
+            q.total_items = plan->total_items;
+            return launch_q2(q, plan->num_cus, static_cast<hipStream_t>(stream));
+        }
         LaunchArgs a{};
         a.jobs = plan->d_jobs;
         a.n_jobs = plan->n_jobs;
@@ -627,7 +645,7 @@ extern "C" {
 
 int vx_gemm_workspace_bytes(const vx_matrix_t* matrix, size_t m, size_t* out_bytes) {
     return guard([&]() -> int {
-        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_kind(matrix, kKindVelurex));
         if (out_bytes == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_bytes is NULL");
         if (m == 0 || m > VX_MAX_GEMM_TOKENS) VX_FAIL(VX_ERR_INVALID_SHAPE, "m must be in 1..=%d (got %zu)", VX_MAX_GEMM_TOKENS, m);
         *out_bytes = gemm_workspace_bytes(matrix->g, m, matrix->num_cus);
@@ -638,7 +656,7 @@ int vx_gemm_workspace_bytes(const vx_matrix_t* matrix, size_t m, size_t* out_byt
 int vx_gemm_i32_dev(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t ldx, int32_t* y, size_t ldy,
                     void* workspace, size_t workspace_len, void* stream) {
     return guard([&]() -> int {
-        VX_TRY(check_matrix(matrix));
+        VX_TRY(check_kind(matrix, kKindVelurex));
         if (x == nullptr || y == nullptr || workspace == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "x, y or workspace is NULL");
         if (m == 0 || m > VX_MAX_GEMM_TOKENS) VX_FAIL(VX_ERR_INVALID_SHAPE, "m must be in 1..=%d (got %zu)", VX_MAX_GEMM_TOKENS, m);
         if (ldx < matrix->g.cols) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "ldx = %zu is less than cols = %zu", ldx, matrix->g.cols);
@@ -649,6 +667,162 @@ int vx_gemm_i32_dev(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t
         VX_TRY(set_device_of(matrix));
         return launch_gemm(matrix->d_w, matrix->g, matrix->num_cus, x, m, ldx, y, ldy, static_cast<uint8_t*>(workspace),
                            static_cast<hipStream_t>(stream));
+    });
+}
+
+}  // extern "C"
+
+// ---- Q2_0 (block-scaled) ------------------------------------------------------------------------------------------------
+
+namespace vx {
+
+static int check_q2_shape(size_t rows, size_t cols) {
+    VX_TRY(check_shape(rows, cols));
+    if (cols % 64 != 0) VX_FAIL(VX_ERR_INVALID_SHAPE, "cols = %zu is not a multiple of 64 (one scale per 64 weights)", cols);
+    if (cols > kQ2MaxCols) VX_FAIL(VX_ERR_INVALID_SHAPE, "cols = %zu exceeds %zu for the Q2_0 GEMV", cols, kQ2MaxCols);
+    return VX_OK;
+}
+
+static Q2Job q2_job(const vx_matrix* m, const int8_t* acts, const float* act_scales, float* out) {
+    Q2Job j{};
+    j.w = m->d_w;
+    j.scales = reinterpret_cast<const uint16_t*>(m->d_w + q2_weight_bytes(m->g.rows, m->g.cols));
+    j.acts = acts;
+    j.act_scales = act_scales;
+    j.out = out;
+    j.rows = static_cast<uint32_t>(m->g.rows);
+    j.cols = static_cast<uint32_t>(m->g.cols);
+    j.scale_stride = static_cast<uint32_t>(q2_scale_stride(m->g.cols));
+    j.item_begin = 0;
+    return j;
+}
+
+static int check_q2_io(const vx_matrix* m, const int8_t* acts, size_t acts_len, const float* act_scales, size_t n_scales,
+                       const void* out, size_t out_capacity) {
+    if (acts == nullptr || act_scales == nullptr || out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "acts, act_scales or out is NULL");
+    if (acts_len < m->g.cols) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "acts hold %zu values but cols = %zu", acts_len, m->g.cols);
+    if (reinterpret_cast<uintptr_t>(acts) % 4u) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "acts must be 4-byte aligned");
+    if (n_scales < m->g.cols / 32) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "act_scales hold %zu values, %zu needed", n_scales, m->g.cols / 32);
+    if (out_capacity < m->g.rows) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "out holds %zu values but rows = %zu", out_capacity, m->g.rows);
+    return VX_OK;
+}
+
+}  // namespace vx
+
+extern "C" {
+
+int vx_q2_matrix_create(const uint8_t* planar, size_t planar_len, const uint16_t* scales_f16, size_t n_scales,
+                        size_t rows, size_t cols, vx_matrix_t** out_matrix) {
+    return guard([&]() -> int {
+        if (out_matrix == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_matrix is NULL");
+        *out_matrix = nullptr;
+        VX_TRY(check_q2_shape(rows, cols));
+        if (planar == nullptr || scales_f16 == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "planar or scales_f16 is NULL");
+        const size_t need = rows * planar_row_bytes(cols);
+        if (planar_len < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "planar holds %zu bytes, %zu needed", planar_len, need);
+        if (n_scales < rows * (cols / 64)) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "scales hold %zu values, %zu needed", n_scales, rows * (cols / 64));
+        const size_t bad = find_invalid_byte(planar, need);
+        if (bad != SIZE_MAX)
+            VX_FAIL(VX_ERR_INVALID_VALUE, "byte %zu (value %u) is not a velurex byte", bad, static_cast<unsigned>(planar[bad]));
+        DeviceInfo di;
+        VX_TRY(device_info(&di));
+        vx_matrix* m = new vx_matrix();
+        m->magic = kMatrixMagic;
+        m->kind = kKindQ2;
+        m->g = geometry(rows, cols);
+        m->weight_scale = 1.0f;
+        m->device = di.device;
+        m->num_cus = di.num_cus;
+        m->kslices = 1;
+        m->slice_chunks = 0;
+        m->d_w = nullptr;
+        m->d_part = nullptr;
+        m->d_staged = nullptr;
+        m->d_io = nullptr;
+        const size_t bytes = q2_device_bytes(rows, cols);
+        std::vector<uint8_t> host(bytes);
+        q2_to_device_layout(planar, scales_f16, rows, cols, host.data());
+        hipError_t e = hipMalloc(&m->d_w, bytes);
+        if (e == hipSuccess) e = hipMemcpy(m->d_w, host.data(), bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            destroy(m);
+            VX_FAIL(VX_ERR_DEVICE, "device allocation or upload of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+        }
+        m->g.device_bytes = bytes;
+        *out_matrix = m;
+        return VX_OK;
+    });
+}
+
+int vx_q2_gemv_f32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, const float* act_scales,
+                       size_t n_act_scales, float* out, size_t out_capacity, void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_kind(matrix, kKindQ2));
+        VX_TRY(check_q2_io(matrix, acts, acts_len, act_scales, n_act_scales, out, out_capacity));
+        VX_TRY(set_device_of(matrix));
+        Q2Args a{};
+        a.jobs = nullptr;
+        a.n_jobs = 1;
+        a.one = q2_job(matrix, acts, act_scales, out);
+        a.total_items = q2_items(a.one.rows);
+        return launch_q2(a, matrix->num_cus, static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_q2_lane_sums_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, int32_t* out,
+                        size_t out_capacity, void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_kind(matrix, kKindQ2));
+        if (acts == nullptr || out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "acts or out is NULL");
+        if (acts_len < matrix->g.cols) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "acts hold %zu values but cols = %zu", acts_len, matrix->g.cols);
+        const size_t need = matrix->g.rows * (matrix->g.cols / 32) * 8;
+        if (out_capacity < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "out holds %zu values, %zu needed", out_capacity, need);
+        VX_TRY(set_device_of(matrix));
+        return launch_q2_lane_sums(q2_job(matrix, acts, nullptr, nullptr), out, static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan) {
+    return guard([&]() -> int {
+        if (out_plan == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_plan is NULL");
+        *out_plan = nullptr;
+        if (jobs == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "jobs is NULL");
+        if (n_jobs == 0 || n_jobs > 65535) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "n_jobs must be in 1..=65535 (got %zu)", n_jobs);
+        DeviceInfo di;
+        VX_TRY(device_info(&di));
+        std::vector<Q2Job> hj(n_jobs);
+        uint32_t items = 0;
+        for (size_t i = 0; i < n_jobs; ++i) {
+            const vx_q2_job_t& u = jobs[i];
+            if (u.struct_size != sizeof(vx_q2_job_t))
+                VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].struct_size is %u, expected %zu", i, u.struct_size, sizeof(vx_q2_job_t));
+            VX_TRY(check_kind(u.matrix, kKindQ2));
+            if (u.matrix->device != di.device) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].matrix lives on another device", i);
+            VX_TRY(check_q2_io(u.matrix, u.acts, u.acts_len, u.act_scales, u.n_act_scales, u.out, u.out_capacity));
+            hj[i] = q2_job(u.matrix, u.acts, u.act_scales, u.out);
+            hj[i].item_begin = items;
+            items += q2_items(hj[i].rows);
+        }
+        vx_plan* p = new vx_plan();
+        p->magic = kPlanMagic;
+        p->device = di.device;
+        p->num_cus = di.num_cus;
+        p->d_jobs = nullptr;
+        p->d_part = nullptr;
+        p->d_split = nullptr;
+        p->d_q2jobs = nullptr;
+        p->n_jobs = static_cast<uint32_t>(n_jobs);
+        p->total_items = items;
+        p->max_rows = 0;
+        p->n_split = 0;
+        hipError_t e = hipMalloc(&p->d_q2jobs, n_jobs * sizeof(Q2Job));
+        if (e == hipSuccess) e = hipMemcpy(p->d_q2jobs, hj.data(), n_jobs * sizeof(Q2Job), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            destroy_plan(p);
+            VX_FAIL(VX_ERR_DEVICE, "plan allocation failed: %s", hipGetErrorString(e));
+        }
+        *out_plan = p;
+        return VX_OK;
     });
 }
 

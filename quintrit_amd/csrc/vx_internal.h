@@ -165,6 +165,33 @@ int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* 
 size_t find_invalid_byte(const uint8_t* planar, size_t n);
 void planar_to_device_layout(const uint8_t* planar, const Geometry& g, uint8_t* dst);
 
+// ---- Q2_0 (block-scaled) jobs ---------------------------------------------------------------------------------------
+
+struct Q2Job {
+    const uint8_t* w;            // Q2 device layout (vx_q2.hip)
+    const uint16_t* scales;      // fp16 weight scales, [tile of 8][row % 8][scale_stride]
+    const int8_t* acts;          // cols int8 codes (4-byte aligned)
+    const float* act_scales;     // cols / 32 fp32 scales
+    float* out;                  // rows values
+    uint32_t rows, cols, scale_stride, item_begin;
+};
+
+struct Q2Args {
+    const Q2Job* jobs;  // device array, or nullptr: use `one`
+    uint32_t n_jobs;
+    uint32_t total_items;  // tile groups (16 tiles of 8 rows) summed over the jobs
+    Q2Job one;
+};
+
+size_t q2_blocks(size_t cols);
+size_t q2_scale_stride(size_t cols);
+size_t q2_weight_bytes(size_t rows, size_t cols);
+size_t q2_device_bytes(size_t rows, size_t cols);
+void q2_to_device_layout(const uint8_t* planar, const uint16_t* scales, size_t rows, size_t cols, uint8_t* dst);
+inline uint32_t q2_items(uint32_t rows) { return ((rows + 7) / 8 + kTileGroup - 1) / kTileGroup; }
+int launch_q2(const Q2Args& a, int num_cus, hipStream_t stream);
+int launch_q2_lane_sums(const Q2Job& j, int32_t* out, hipStream_t stream);
+
 // ---- device state -------------------------------------------------------------------------------------------------------
 
 struct DeviceInfo {
@@ -179,6 +206,7 @@ int device_info(DeviceInfo* out);  // current device; VX_ERR_UNSUPPORTED if it i
 
 struct vx_matrix {
     uint32_t magic;
+    uint32_t kind;      // kKindVelurex (GEMV/GEMM layout) or kKindQ2 (block-scaled layout)
     vx::Geometry g;
     float weight_scale;
     int device;
@@ -192,6 +220,9 @@ struct vx_matrix {
 };
 
 constexpr uint32_t kMatrixMagic = 0x56584d32u;  // "VXM2"
+constexpr uint32_t kKindVelurex = 0;
+constexpr uint32_t kKindQ2 = 1;
+constexpr size_t kQ2MaxCols = 12288;  // activations of one Q2_0 row staged in LDS (two workgroups per CU)
 
 struct vx_plan {
     uint32_t magic;
@@ -200,6 +231,7 @@ struct vx_plan {
     vx::Job* d_jobs;
     int32_t* d_part;
     uint32_t* d_split;  // indices of the jobs split into K slices
+    vx::Q2Job* d_q2jobs;  // Q2_0 plans: their job table (d_jobs unused)
     uint32_t n_jobs, total_items, max_rows, n_split;
 };
 

@@ -121,3 +121,8 @@ def test_argument_errors_without_gpu():
     n = ctypes.c_size_t()
     assert L.vx_gemm_workspace_bytes(None, 8, ctypes.byref(n)) == 14               # NULL handle
     assert L.vx_gemm_i32_dev(None, buf, 8, 64, buf, 64, buf, 64, None) == 14
+    # Q2_0: shape rules before any device work (cols a multiple of 64, at most 12288)
+    assert L.vx_q2_matrix_create(buf, 64, buf, 64, 1, 100, ctypes.byref(h)) == 3
+    assert L.vx_q2_matrix_create(buf, 64, buf, 64, 1, 12352, ctypes.byref(h)) == 3
+    assert L.vx_q2_matrix_create(buf, 16, buf, 64, 1, 64, ctypes.byref(h)) == 4   # planar too short
+    assert L.vx_q2_gemv_f32_dev(None, buf, 64, buf, 2, buf, 1, None) == 14
