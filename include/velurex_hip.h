@@ -284,6 +284,55 @@ typedef struct vx_q2_job {
 /* A plan of Q2_0 GEMVs, run with vx_plan_run and freed with vx_plan_free like the velurex plans. */
 int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan);
 
+/* ---- decode token loop ------------------------------------------------------------------------------------------------
+ * A ternary decoder of the BitNet-b1.58 family on one GPU, step for step the reference's CPU token loop
+ * (QuintritModel::forward_token_with_scratchpad, quintrit-runtime/src/model.rs:282-377, with
+ * AttentionBlock::forward_with_scratchpad, attention.rs:115-260, and the BitnetCpp numerics: RMSNorm with an f64 sum,
+ * per-token absmax int8, velurex projections with the fp32 epilogue, NEOX RoPE, an F16 KV cache, FP16-accumulator
+ * attention with the 4-chunk split, sub-norms, ReLU^2, a tied bf16 head, greedy argmax), so that logits and tokens are
+ * bit-identical to it. One step is one HIP graph: embed, 30 x (norm, q/k/v, RoPE + KV append, attention, sub-norm, o,
+ * norm, gate/up, ReLU^2 * up + sub-norm, down), final norm, head, argmax, with the position and the token kept on the
+ * device (the reference's CUDA decode graph does the same, quintrit-runtime/src/gpu.rs:459-493).
+ * Supported: head_dim 128, max_ctx <= 4096, hidden, n_heads * head_dim and ffn <= 8192, hidden a multiple of 32. */
+typedef struct vx_decoder vx_decoder_t;
+
+typedef struct vx_decoder_config {
+    uint32_t struct_size; /* sizeof(vx_decoder_config_t) */
+    uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx;
+    float rms_eps, rope_theta;
+} vx_decoder_config_t;
+
+/* Projection kinds (vx_decoder_set_projection) and norm kinds (vx_decoder_set_norm). */
+enum {
+    VX_PROJ_Q = 0, VX_PROJ_K = 1, VX_PROJ_V = 2, VX_PROJ_O = 3, VX_PROJ_GATE = 4, VX_PROJ_UP = 5, VX_PROJ_DOWN = 6
+};
+enum { VX_NORM_ATTN = 0, VX_NORM_ATTN_SUB = 1, VX_NORM_FFN = 2, VX_NORM_FFN_SUB = 3 };
+
+/* ModelConfig (quintrit-runtime/src/config.rs:155-177) of the model; allocates the KV cache and work buffers. */
+int vx_decoder_create(const vx_decoder_config_t* config, vx_decoder_t** out_decoder);
+/* A planar velurex matrix (host memory) with its per-tensor scale: Q/K/V rows n_heads*head_dim or n_kv_heads*head_dim,
+ * cols hidden; O hidden x n_heads*head_dim; gate/up ffn x hidden; down hidden x ffn (the reference's BitLinear). */
+int vx_decoder_set_projection(vx_decoder_t* decoder, uint32_t layer, uint32_t kind, const uint8_t* planar,
+                              size_t planar_len, float weight_scale);
+/* RMSNorm weights (host f32). layer == n_layers with kind VX_NORM_ATTN sets the output norm. */
+int vx_decoder_set_norm(vx_decoder_t* decoder, uint32_t layer, uint32_t kind, const float* weights, size_t n);
+/* The tied embedding / head, vocab x hidden bf16 (host). */
+int vx_decoder_set_embedding_bf16(vx_decoder_t* decoder, const uint16_t* embedding, size_t n);
+/* One token at position pos (forward_token): KV entries 0..pos-1 must come from earlier steps. logits (host, may be
+ * NULL) receives vocab values; out_next (may be NULL) the greedy token. */
+int vx_decoder_step(vx_decoder_t* decoder, uint32_t token, uint32_t pos, float* logits, size_t logits_capacity,
+                    uint32_t* out_next);
+/* Greedy generation from position 0 (engine.rs:590-686 with the greedy sampler, the prompt fed one token at a time):
+ * n_new tokens into out_tokens (host). n_prompt >= 1 and n_prompt + n_new - 1 <= max_ctx. */
+int vx_decoder_generate(vx_decoder_t* decoder, const uint32_t* prompt, size_t n_prompt, size_t n_new,
+                        uint32_t* out_tokens, size_t out_capacity);
+/* Device bytes held by the decoder (weights, KV cache, work buffers). */
+int vx_decoder_memory_bytes(const vx_decoder_t* decoder, size_t* out_bytes);
+int vx_decoder_free(vx_decoder_t* decoder);
+
+/* glibc's expf (the reference's f32::exp) evaluated on the device, as used by the attention softmax: n values. */
+int vx_expf_dev(const float* x, size_t n, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

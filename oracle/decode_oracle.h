@@ -1,0 +1,49 @@
+/* decode_oracle.h - CPU restatement of the reference's decode step (test infrastructure only; see decode_oracle.c). */
+#ifndef DECODE_ORACLE_H
+#define DECODE_ORACLE_H
+
+#include "velurex_oracle.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VXO_MAX_LAYERS 64
+
+typedef struct vxo_model_config {
+    uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx;
+    float rms_eps, rope_theta;
+} vxo_model_config;
+
+typedef struct vxo_model vxo_model;
+
+float vxo_bf16_to_f32(uint16_t h);                                        /* ops.rs:652-655 */
+uint16_t vxo_f32_to_bf16(float f);                                        /* ops.rs:658-665 */
+float vxo_ggml_dot_bf16(const uint16_t* x, const uint16_t* y, size_t n);  /* ops.rs:669-713 */
+float vxo_ggml_dot_f16(const uint16_t* x, const uint16_t* y, size_t n);   /* ops.rs:960-1015, 1078-1093 */
+void vxo_vec_mad_f16(uint16_t* y, const uint16_t* x, float v, size_t n);  /* ops.rs:1254-1300 */
+void vxo_vec_scale_f16(uint16_t* y, float v, size_t n);                   /* ops.rs:1304-1345 */
+void vxo_expf_batch(const float* x, size_t n, float* out);                /* the host libm expf */
+void vxo_rope_cache(size_t pos, size_t n_dims, float freq_base, float* cache);            /* ops.rs:121-140 */
+void vxo_rope_neox(float* x, size_t heads, size_t head_dim, const float* cache, size_t n_dims); /* ops.rs:199-221 */
+void vxo_attend_head(const uint16_t* q_f16, const uint16_t* kbase, const uint16_t* vbase, size_t stride,
+                     size_t head_dim, size_t seq_len, size_t max_ctx, float scale, float* out); /* attention.rs:436-542 */
+void vxo_projection(const uint8_t* planar, size_t rows, size_t cols, float ws, const int8_t* q, float as, float* out);
+
+/* The model of BASELINE.json configs[3] with weights generated from `seed` (projections: kind 0..6 = q, k, v, o, gate,
+ * up, down; norms: kind 0..3 = attn, attn_sub, ffn, ffn_sub, layer n_layers kind 0 = output norm). */
+void vxo_projection_shape(const vxo_model_config* c, int kind, size_t* rows, size_t* cols);
+vxo_model* vxo_model_create(const vxo_model_config* cfg, uint64_t seed);
+void vxo_model_free(vxo_model* m);
+const uint8_t* vxo_model_projection(const vxo_model* m, size_t layer, int kind, float* weight_scale);
+const float* vxo_model_norm(const vxo_model* m, size_t layer, int kind);
+const uint16_t* vxo_model_embedding(const vxo_model* m);
+const float* vxo_model_rope_table(const vxo_model* m);
+void vxo_model_reset(vxo_model* m);
+uint32_t vxo_model_forward(vxo_model* m, uint32_t token, size_t pos, float* logits);
+void vxo_model_generate(vxo_model* m, const uint32_t* prompt, size_t n_prompt, size_t n_new, uint32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -72,6 +72,28 @@ def _declare(L: ctypes.CDLL) -> None:
         "vxo_q2_0_lane_sums": (None, [vp, vp, sz, sz, vp]),
         "vxo_gen_trits": (None, [u64, sz, uint, uint, vp]),
         "vxo_gen_i8": (None, [u64, sz, ctypes.c_int, ctypes.c_int, vp]),
+        # decode step (decode_oracle.c)
+        "vxo_bf16_to_f32": (f32, [ctypes.c_uint16]),
+        "vxo_f32_to_bf16": (ctypes.c_uint16, [f32]),
+        "vxo_ggml_dot_bf16": (f32, [vp, vp, sz]),
+        "vxo_ggml_dot_f16": (f32, [vp, vp, sz]),
+        "vxo_vec_mad_f16": (None, [vp, vp, f32, sz]),
+        "vxo_vec_scale_f16": (None, [vp, f32, sz]),
+        "vxo_expf_batch": (None, [vp, sz, vp]),
+        "vxo_rope_cache": (None, [sz, sz, f32, vp]),
+        "vxo_rope_neox": (None, [vp, sz, sz, vp, sz]),
+        "vxo_attend_head": (None, [vp, vp, vp, sz, sz, sz, sz, f32, vp]),
+        "vxo_projection": (None, [vp, sz, sz, f32, vp, f32, vp]),
+        "vxo_projection_shape": (None, [vp, ctypes.c_int, vp, vp]),
+        "vxo_model_create": (vp, [vp, u64]),
+        "vxo_model_free": (None, [vp]),
+        "vxo_model_projection": (vp, [vp, sz, ctypes.c_int, vp]),
+        "vxo_model_norm": (vp, [vp, sz, ctypes.c_int]),
+        "vxo_model_embedding": (vp, [vp]),
+        "vxo_model_rope_table": (vp, [vp]),
+        "vxo_model_reset": (None, [vp]),
+        "vxo_model_forward": (ctypes.c_uint32, [vp, ctypes.c_uint32, sz, vp]),
+        "vxo_model_generate": (None, [vp, vp, sz, sz, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -268,4 +290,146 @@ def gen_trits(seed: int, shape, p_minus: int = 35, p_zero: int = 30) -> np.ndarr
 def gen_i8(seed: int, n: int, lo: int = -127, hi: int = 127) -> np.ndarray:
     out = np.empty(n, np.int8)
     lib().vxo_gen_i8(seed, n, lo, hi, _p(out))
+    return out
+
+
+# ---- decode step (decode_oracle.c) ----------------------------------------------------------------------------------
+
+class ModelConfig(ctypes.Structure):
+    """vxo_model_config: the decoder shape (BASELINE.json configs[3] uses bitnet_2b())."""
+    _fields_ = [("n_layers", ctypes.c_uint32), ("hidden", ctypes.c_uint32), ("n_heads", ctypes.c_uint32),
+                ("n_kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32), ("ffn", ctypes.c_uint32),
+                ("vocab", ctypes.c_uint32), ("max_ctx", ctypes.c_uint32), ("rms_eps", ctypes.c_float),
+                ("rope_theta", ctypes.c_float)]
+
+
+def bitnet_2b(max_ctx: int = 4096) -> ModelConfig:
+    """ModelConfig::bitnet_2b_default (quintrit-runtime/src/config.rs:155-177)."""
+    return ModelConfig(30, 2560, 20, 5, 128, 6912, 128256, max_ctx, 1e-5, 500000.0)
+
+
+PROJ_NAMES = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+class Model:
+    """The oracle's decoder with weights generated from a seed (vxo_model_*)."""
+
+    def __init__(self, cfg: ModelConfig, seed: int):
+        self.cfg = cfg
+        self._h = lib().vxo_model_create(ctypes.byref(cfg), seed)
+        if not self._h:
+            raise ValueError("unsupported model shape")
+
+    def close(self):
+        if self._h:
+            lib().vxo_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def projection_shape(self, kind: int):
+        r, c = ctypes.c_size_t(), ctypes.c_size_t()
+        lib().vxo_projection_shape(ctypes.byref(self.cfg), kind, ctypes.byref(r), ctypes.byref(c))
+        return r.value, c.value
+
+    def projection(self, layer: int, kind: int):
+        """(planar bytes, weight scale) of projection `kind` of `layer` (a copy)."""
+        ws = ctypes.c_float()
+        p = lib().vxo_model_projection(self._h, layer, kind, ctypes.byref(ws))
+        rows, cols = self.projection_shape(kind)
+        n = rows * planar_row_bytes(cols)
+        return np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(p)).copy(), float(ws.value)
+
+    def norm(self, layer: int, kind: int) -> np.ndarray:
+        c = self.cfg
+        n = c.ffn if kind == 3 else (c.n_heads * c.head_dim if kind == 1 else c.hidden)
+        if layer == c.n_layers:
+            n = c.hidden
+        p = lib().vxo_model_norm(self._h, layer, kind)
+        return np.ctypeslib.as_array((ctypes.c_float * n).from_address(p)).copy()
+
+    def embedding(self) -> np.ndarray:
+        n = self.cfg.vocab * self.cfg.hidden
+        p = lib().vxo_model_embedding(self._h)
+        return np.ctypeslib.as_array((ctypes.c_uint16 * n).from_address(p)).reshape(self.cfg.vocab, self.cfg.hidden)
+
+    def rope_table(self) -> np.ndarray:
+        n = self.cfg.max_ctx * self.cfg.head_dim
+        p = lib().vxo_model_rope_table(self._h)
+        return np.ctypeslib.as_array((ctypes.c_float * n).from_address(p)).reshape(self.cfg.max_ctx, self.cfg.head_dim)
+
+    def reset(self):
+        lib().vxo_model_reset(self._h)
+
+    def forward(self, token: int, pos: int):
+        logits = np.empty(self.cfg.vocab, np.float32)
+        nxt = lib().vxo_model_forward(self._h, token, pos, _p(logits))
+        return int(nxt), logits
+
+    def generate(self, prompt, n_new: int) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.empty(n_new, np.uint32)
+        lib().vxo_model_generate(self._h, _p(p), p.size, n_new, _p(out))
+        return out
+
+
+def f32_to_bf16(x: float) -> int:
+    return int(lib().vxo_f32_to_bf16(x))
+
+
+def bf16_to_f32(h: int) -> float:
+    return float(lib().vxo_bf16_to_f32(h))
+
+
+def ggml_dot_bf16(x: np.ndarray, y: np.ndarray) -> float:
+    a, b = np.ascontiguousarray(x, np.uint16), np.ascontiguousarray(y, np.uint16)
+    return float(np.float32(lib().vxo_ggml_dot_bf16(_p(a), _p(b), a.size)))
+
+
+def ggml_dot_f16(x: np.ndarray, y: np.ndarray) -> float:
+    a, b = np.ascontiguousarray(x, np.uint16), np.ascontiguousarray(y, np.uint16)
+    return float(np.float32(lib().vxo_ggml_dot_f16(_p(a), _p(b), a.size)))
+
+
+def vec_mad_f16(y: np.ndarray, x: np.ndarray, v: float) -> np.ndarray:
+    out = np.ascontiguousarray(y, np.uint16).copy()
+    xx = np.ascontiguousarray(x, np.uint16)
+    lib().vxo_vec_mad_f16(_p(out), _p(xx), v, out.size)
+    return out
+
+
+def vec_scale_f16(y: np.ndarray, v: float) -> np.ndarray:
+    out = np.ascontiguousarray(y, np.uint16).copy()
+    lib().vxo_vec_scale_f16(_p(out), v, out.size)
+    return out
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    lib().vxo_expf_batch(_p(a), a.size, _p(out))
+    return out
+
+
+def rope_cache(pos: int, n_dims: int, base: float) -> np.ndarray:
+    out = np.empty(n_dims, np.float32)
+    lib().vxo_rope_cache(pos, n_dims, base, _p(out))
+    return out
+
+
+def rope_neox(x: np.ndarray, heads: int, head_dim: int, cache: np.ndarray) -> np.ndarray:
+    out = np.ascontiguousarray(x, np.float32).copy()
+    c = np.ascontiguousarray(cache, np.float32)
+    lib().vxo_rope_neox(_p(out), heads, head_dim, _p(c), c.size)
+    return out
+
+
+def attend_head(q_f16, k_f16, v_f16, seq_len: int, max_ctx: int, scale: float) -> np.ndarray:
+    """One head over k/v rows [0, seq_len) (arrays [positions][head_dim] of f16 bits)."""
+    q = np.ascontiguousarray(q_f16, np.uint16)
+    k = np.ascontiguousarray(k_f16, np.uint16)
+    v = np.ascontiguousarray(v_f16, np.uint16)
+    out = np.empty(q.size, np.float32)
+    lib().vxo_attend_head(_p(q), _p(k), _p(v), q.size, q.size, seq_len, max_ctx, scale, _p(out))
     return out

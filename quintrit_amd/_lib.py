@@ -75,6 +75,15 @@ SIGNATURES = {
     "vx_q2_gemv_f32_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _vp]),
     "vx_q2_lane_sums_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp]),
     "vx_q2_plan_create": (_i32, [_vp, _sz, _vp]),
+    "vx_decoder_create": (_i32, [_vp, _vp]),
+    "vx_decoder_set_projection": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _sz, _f32]),
+    "vx_decoder_set_norm": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _sz]),
+    "vx_decoder_set_embedding_bf16": (_i32, [_vp, _vp, _sz]),
+    "vx_decoder_step": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _sz, _vp]),
+    "vx_decoder_generate": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz]),
+    "vx_decoder_memory_bytes": (_i32, [_vp, _vp]),
+    "vx_decoder_free": (_i32, [_vp]),
+    "vx_expf_dev": (_i32, [_vp, _sz, _vp, _vp]),
 }
 
 

@@ -1,0 +1,118 @@
+"""Greedy decoding of a ternary (BitNet-b1.58 family) model on the GPU: the token loop of vx_decoder_* in
+include/velurex_hip.h.
+
+Mirrors the reference's runtime surface for this path: ModelConfig (quintrit-runtime/src/config.rs:155-177),
+QuintritModel::forward_token (model.rs:282-377: one token at one position, logits out) and the greedy generation loop
+(engine.rs:590-686 with Sampler::sample greedy, sampler.rs:73-83). Weights are handed over as the reference holds them:
+planar velurex bytes with a per-tensor scale per projection, f32 RMSNorm weights, a bf16 embedding that is also the
+head. Everything runs in libvelurex_hip.so; without it (or without a gfx950 GPU) construction raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import check, lib
+
+PROJ_Q, PROJ_K, PROJ_V, PROJ_O, PROJ_GATE, PROJ_UP, PROJ_DOWN = range(7)
+NORM_ATTN, NORM_ATTN_SUB, NORM_FFN, NORM_FFN_SUB = range(4)
+
+
+class _Config(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("n_layers", ctypes.c_uint32), ("hidden", ctypes.c_uint32),
+                ("n_heads", ctypes.c_uint32), ("n_kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
+                ("ffn", ctypes.c_uint32), ("vocab", ctypes.c_uint32), ("max_ctx", ctypes.c_uint32),
+                ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    """The model shape (ModelConfig): layers, widths, heads, vocabulary, context and the RMSNorm/RoPE constants."""
+
+    n_layers: int
+    hidden: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    ffn: int
+    vocab: int
+    max_ctx: int
+    rms_eps: float = 1e-5
+    rope_theta: float = 500000.0
+
+    @classmethod
+    def bitnet_2b(cls, max_ctx: int = 4096) -> "DecoderConfig":
+        """ModelConfig::bitnet_2b_default (config.rs:155-177)."""
+        return cls(30, 2560, 20, 5, 128, 6912, 128256, max_ctx, 1e-5, 500000.0)
+
+    def projection_shape(self, kind: int) -> tuple:
+        qd, kvd = self.n_heads * self.head_dim, self.n_kv_heads * self.head_dim
+        return {PROJ_Q: (qd, self.hidden), PROJ_K: (kvd, self.hidden), PROJ_V: (kvd, self.hidden),
+                PROJ_O: (self.hidden, qd), PROJ_GATE: (self.ffn, self.hidden), PROJ_UP: (self.ffn, self.hidden),
+                PROJ_DOWN: (self.hidden, self.ffn)}[kind]
+
+    def _c(self) -> _Config:
+        c = _Config()
+        c.struct_size = ctypes.sizeof(_Config)
+        for f in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab", "max_ctx", "rms_eps",
+                  "rope_theta"):
+            setattr(c, f, getattr(self, f))
+        return c
+
+
+def _ptr(a: np.ndarray) -> ctypes.c_void_p:
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Decoder:
+    """A model resident on the GPU with its KV cache; step() is forward_token, generate() the greedy loop."""
+
+    def __init__(self, config: DecoderConfig):
+        self.config = config
+        h = ctypes.c_void_p()
+        check(lib().vx_decoder_create(ctypes.byref(config._c()), ctypes.byref(h)))
+        self.handle = h
+
+    def set_projection(self, layer: int, kind: int, planar, weight_scale: float) -> None:
+        p = np.ascontiguousarray(planar, dtype=np.uint8).reshape(-1)
+        check(lib().vx_decoder_set_projection(self.handle, layer, kind, _ptr(p), p.size, weight_scale))
+
+    def set_norm(self, layer: int, kind: int, weights) -> None:
+        w = np.ascontiguousarray(weights, dtype=np.float32).reshape(-1)
+        check(lib().vx_decoder_set_norm(self.handle, layer, kind, _ptr(w), w.size))
+
+    def set_embedding_bf16(self, emb_bits) -> None:
+        e = np.ascontiguousarray(emb_bits, dtype=np.uint16).reshape(-1)
+        check(lib().vx_decoder_set_embedding_bf16(self.handle, _ptr(e), e.size))
+
+    def step(self, token: int, pos: int, want_logits: bool = True):
+        """forward_token: (logits as float32 array or None, greedy next token)."""
+        logits = np.empty(self.config.vocab, dtype=np.float32) if want_logits else None
+        nxt = ctypes.c_uint32()
+        check(lib().vx_decoder_step(self.handle, token, pos, _ptr(logits) if want_logits else None,
+                                    logits.size if want_logits else 0, ctypes.byref(nxt)))
+        return logits, int(nxt.value)
+
+    def generate(self, prompt, n_new: int) -> list:
+        p = np.ascontiguousarray(prompt, dtype=np.uint32).reshape(-1)
+        out = np.zeros(max(n_new, 1), dtype=np.uint32)
+        check(lib().vx_decoder_generate(self.handle, _ptr(p), p.size, n_new, _ptr(out), out.size))
+        return [int(t) for t in out[:n_new]]
+
+    def memory_bytes(self) -> int:
+        b = ctypes.c_size_t()
+        check(lib().vx_decoder_memory_bytes(self.handle, ctypes.byref(b)))
+        return b.value
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().vx_decoder_free(self.handle))
+            self.handle = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,168 @@
+"""GPU parity of the decode token loop through the C ABI (vx_decoder_*).
+
+The reference's loop (QuintritModel::forward_token_with_scratchpad, quintrit-runtime/src/model.rs:282-377, with
+attention.rs:115-260 and 483-542, ops.rs and sampler.rs:73-83) is restated by the oracle (oracle/decode_oracle.c). The
+GPU keeps every floating-point operation of it in the same order, so logits are compared bit for bit at every
+position, and greedy tokens must be identical. The tiny model covers the three attention regimes: one online softmax
+(padded KV length 256), the 4-chunk split at 512, and a padded length clamped to max_ctx (640). The full
+BitNet-b1.58-2B-shaped model is checked against the committed 256-token continuation
+(tests/golden/bitnet2b_greedy.json, written by tests/golden/make_bitnet_golden.py from the oracle).
+"""
+import ctypes
+import json
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def tiny_cfg(oracle, max_ctx=640):
+    return oracle.ModelConfig(2, 256, 4, 2, 128, 384, 1000, max_ctx, 1e-5, 10000.0)
+
+
+def load_decoder(oracle, model):
+    """A GPU decoder holding the oracle model's weights."""
+    from quintrit_amd.decoder import Decoder, DecoderConfig
+    c = model.cfg
+    dc = DecoderConfig(c.n_layers, c.hidden, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn, c.vocab, c.max_ctx,
+                       float(np.float32(c.rms_eps)), float(np.float32(c.rope_theta)))
+    dec = Decoder(dc)
+    for layer in range(c.n_layers):
+        for kind in range(7):
+            planar, ws = model.projection(layer, kind)
+            dec.set_projection(layer, kind, planar, ws)
+        for kind in range(4):
+            dec.set_norm(layer, kind, model.norm(layer, kind))
+    dec.set_norm(c.n_layers, 0, model.norm(c.n_layers, 0))
+    dec.set_embedding_bf16(model.embedding())
+    return dec
+
+
+def assert_same_bits(got, want, what):
+    g, w = np.asarray(got, np.float32).view(np.uint32), np.asarray(want, np.float32).view(np.uint32)
+    bad = np.flatnonzero(g != w)
+    assert bad.size == 0, (f"{what}: {bad.size} of {g.size} values differ, first at {bad[0]}: "
+                           f"{got[bad[0]]!r} vs {want[bad[0]]!r}")
+
+
+def test_expf_matches_host_libm(torch_dev, oracle):
+    """The attention's exponentials: the device expf equals the host's glibc expf (the reference's f32::exp)."""
+    torch = torch_dev
+    from quintrit_amd._lib import check, lib
+    rng = np.random.default_rng(7)
+    x = np.concatenate([
+        rng.uniform(-110.0, 90.0, 1 << 20).astype(np.float32),
+        -np.abs(rng.standard_normal(1 << 18).astype(np.float32)) * np.float32(4.0),  # softmax range: x <= 0
+        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 88.72283, 88.72284, -103.97207, -103.97208, -87.33654, 1e-30,
+                  -1e-30, 1e-45], np.float32),
+        rng.integers(0, 1 << 32, 1 << 16, dtype=np.uint64).astype(np.uint32).view(np.float32),
+    ])
+    want = oracle.expf(x)
+    xd = torch.from_numpy(x).cuda()
+    out = torch.empty_like(xd)
+    check(lib().vx_expf_dev(ctypes.c_void_p(xd.data_ptr()), x.size, ctypes.c_void_p(out.data_ptr()),
+                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert_same_bits(got[~nan], want[~nan], "expf")
+
+
+def test_tiny_step_logits_bit_exact(torch_dev, oracle):
+    """forward_token at positions 0..599 (teacher forced): every logit bit-identical, every greedy token equal."""
+    model = oracle.Model(tiny_cfg(oracle), 11)
+    dec = load_decoder(oracle, model)
+    try:
+        rng = np.random.default_rng(5)
+        tokens = rng.integers(0, model.cfg.vocab, 600)
+        for pos, tok in enumerate(tokens):
+            want_next, want = model.forward(int(tok), pos)
+            got, got_next = dec.step(int(tok), pos)
+            assert_same_bits(got, want, f"logits at pos {pos}")
+            assert got_next == want_next, f"pos {pos}"
+    finally:
+        dec.close()
+        model.close()
+
+
+@pytest.mark.parametrize("max_ctx,n_prompt,n_new", [(640, 8, 300), (4096, 1, 40), (512, 200, 313)])
+def test_tiny_generate_tokens_identical(torch_dev, oracle, max_ctx, n_prompt, n_new):
+    """The greedy loop in one graph per step (device-side position and token) against the oracle's loop."""
+    model = oracle.Model(tiny_cfg(oracle, max_ctx), 23)
+    dec = load_decoder(oracle, model)
+    try:
+        prompt = np.random.default_rng(max_ctx + n_prompt).integers(0, model.cfg.vocab, n_prompt)
+        want = [int(t) for t in model.generate(prompt, n_new)]
+        got = dec.generate(prompt, n_new)
+        assert got == want
+        # the same decoder again: state from the previous generation must not leak into the next
+        assert dec.generate(prompt, n_new) == want
+    finally:
+        dec.close()
+        model.close()
+
+
+def test_decoder_argument_errors(torch_dev, oracle):
+    from quintrit_amd._lib import VxError
+    from quintrit_amd.decoder import Decoder, DecoderConfig
+    dec = Decoder(DecoderConfig(1, 256, 2, 1, 128, 256, 100, 64))
+    try:
+        with pytest.raises(VxError, match="not set"):
+            dec.step(0, 0)
+        with pytest.raises(VxError, match="INVALID_SHAPE"):
+            dec.set_norm(0, 0, np.ones(255, np.float32))
+        with pytest.raises(VxError, match="out of range"):
+            dec.set_norm(2, 0, np.ones(256, np.float32))
+        with pytest.raises(VxError, match="BUFFER_TOO_SMALL"):
+            dec.set_projection(0, 0, np.zeros(10, np.uint8), 1.0)
+        with pytest.raises(VxError, match="kind"):
+            dec.set_projection(0, 7, np.zeros(10, np.uint8), 1.0)
+    finally:
+        dec.close()
+    model = oracle.Model(oracle.ModelConfig(1, 256, 2, 1, 128, 256, 100, 64, 1e-5, 10000.0), 3)
+    dec = load_decoder(oracle, model)
+    try:
+        with pytest.raises(VxError, match="token"):
+            dec.step(100, 0)
+        with pytest.raises(VxError, match="pos"):
+            dec.step(0, 64)
+        with pytest.raises(VxError, match="exceed"):
+            dec.generate([1, 2, 3], 63)
+        with pytest.raises(VxError, match="empty"):
+            dec.generate([], 3)
+        assert len(dec.generate([1, 2, 3], 62)) == 62
+        assert dec.memory_bytes() > 0
+    finally:
+        dec.close()
+        model.close()
+
+
+def test_bitnet2b_greedy_golden(torch_dev, oracle):
+    """64 prompt tokens, 256 greedy tokens identical to the CPU reference's."""
+    with open(os.path.join(HERE, "golden", "bitnet2b_greedy.json")) as f:
+        gold = json.load(f)
+    model = oracle.Model(oracle.bitnet_2b(gold["max_ctx"]), gold["seed"])
+    dec = load_decoder(oracle, model)
+    model.close()
+    try:
+        logits, _ = dec.step(gold["prompt"][0], 0)
+        assert int(logits.view(np.uint32).astype(np.uint64).sum()) == gold["logits_pos0_f32_bits_sum"]
+        np.testing.assert_array_equal(logits[:8], np.array(gold["logits_pos0_head"], np.float32))
+        got = dec.generate(gold["prompt"], len(gold["tokens"]))
+        first_bad = next((i for i, (a, b) in enumerate(zip(got, gold["tokens"])) if a != b), None)
+        assert first_bad is None, f"token {first_bad} differs: {got[first_bad]} vs {gold['tokens'][first_bad]}"
+    finally:
+        dec.close()
