@@ -45,9 +45,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
-    ap.add_argument("--workload", choices=["stream", "gemm", "q2"], default="stream",
+    ap.add_argument("--workload", choices=["stream", "gemm", "q2", "decode"], default="stream",
                     help="stream: the driver's line (configs[1]); gemm: the batched GEMM of configs[2]; q2: the "
-                         "block-scaled GEMV stream of configs[4]")
+                         "block-scaled GEMV stream of configs[4]; decode: bs=1 greedy decode of configs[3]")
+    ap.add_argument("--decode-new", type=int, default=256, help="decode mode: generated tokens per run")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device to device 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -188,15 +189,113 @@ def time_fn(torch, fn, steps: int, warmup: int):
     return t0.elapsed_time(t1) / steps, wall
 
 
-def cpu_baseline(budget_s: float):
-    """The CPU oracle's restatement of the reference's table GEMV (oracle/velurex_oracle.c, avx512.rs:1526-1626
-    algorithm, scalar C, one thread) timed on this host over a bounded sample: the seven projections of one Falcon3-10B
-    layer in model order, repeated until the budget is used."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _physical_cores() -> int:
+    """Distinct (physical id, core id) pairs in /proc/cpuinfo among the CPUs this process may use."""
+    allowed = os.sched_getaffinity(0)
+    cores, cpu, phys = set(), None, None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "processor":
+                    cpu = int(v)
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id" and cpu in allowed:
+                    cores.add((phys, v))
+    except OSError:
+        return len(allowed)
+    return len(cores) or len(allowed)
+
+
+def cpu_baseline(budget_s: float, layers: int = 8):
+    """The reference's production CPU GEMV (gemv_compact_multi::<3, 4096, T0, 0, true>, avx512.rs:1526-1626 with the
+    compact tables of avx512.rs:1216-1247), transcribed with AVX-512 intrinsics (oracle/cpu_avx512.c), timed on this
+    host over the Falcon3-10B stream in model order (q, k, v, o, gate, up, down) for `layers` distinct layers (larger
+    than any last-level cache), tables built per call as the reference's GEMV does. Threads 1 .. all usable CPUs,
+    swept up then down, best pass per count; the transcription is first checked against the brute-force product on
+    one 64-row block of every shape. Falls back to the scalar restatement (1 thread) on hosts without AVX-512 VBMI."""
     import numpy as np
+    ncpu, phys = len(os.sched_getaffinity(0)), _physical_cores()  # before libgomp binds this thread
+    os.environ.setdefault("OMP_PROC_BIND", "close")
+    os.environ.setdefault("OMP_PLACES", "cores")
     from oracle import oracle
     L = oracle.lib()
     shapes = [(HIDDEN, HIDDEN), (KV, HIDDEN), (KV, HIDDEN), (HIDDEN, HIDDEN), (FFN, HIDDEN), (FFN, HIDDEN),
               (HIDDEN, FFN)]
+    if not oracle.cpu_avx512_supported():
+        return cpu_baseline_scalar(budget_s, shapes)
+    rng = np.random.default_rng(0xCB)
+    for i, (r, c) in enumerate(shapes):  # exactness of the transcription, every shape
+        t = oracle.gen_trits(300 + i, (64, c))
+        a = oracle.gen_i8(400 + i, c, -127, 127)
+        got = oracle.gemv_avx512(oracle.tile64(oracle.pack_matrix(t), 64, c), a, 64, c, 2)
+        if not np.array_equal(got.astype(np.int64), oracle.gemv_bruteforce(t, a)):
+            raise RuntimeError(f"AVX-512 transcription differs from the brute-force product at {r}x{c}")
+    valid = np.array([b for b in range(256) if oracle.byte_is_valid(b)], np.uint8)
+    mats = []
+    for _ in range(layers):
+        for r, c in shapes:
+            tiles = valid[rng.integers(0, valid.size, r * oracle.tile_row_bytes(c), dtype=np.uint16)]
+            acts = rng.integers(-127, 128, c, dtype=np.int16).astype(np.int8)
+            mats.append((tiles, acts, r, c, np.empty(r, np.float32), np.empty(int(L.vxc_table_bytes(c)), np.int8)))
+    weights = sum(r * c for _, _, r, c, _, _ in mats)
+    counts = sorted({t for t in (1, 2, 4, 8, 16, 32, 64, ncpu) if t <= ncpu})
+
+    def one_pass(th):
+        t0 = time.perf_counter()
+        for tiles, acts, r, c, out, scratch in mats:
+            L.vxc_gemv(tiles.ctypes.data_as(ctypes.c_void_p), acts.ctypes.data_as(ctypes.c_void_p), r, c,
+                       out.ctypes.data_as(ctypes.c_void_p), th, scratch.ctypes.data_as(ctypes.c_void_p))
+        return time.perf_counter() - t0
+
+    best = {t: float("inf") for t in counts}
+    per_point = budget_s / (2 * len(counts))
+    t_all = time.perf_counter()
+    for order in (counts, counts[::-1]):
+        for th in order:
+            t0 = time.perf_counter()
+            n = 0
+            while n < 1 or (n < 5 and time.perf_counter() - t0 < per_point):
+                best[th] = min(best[th], one_pass(th))
+                n += 1
+    sweep = {str(t): round(weights / best[t] / 1e9, 1) for t in counts}
+    top = max(counts, key=lambda t: weights / best[t])
+    buf = np.ones((1 << 30) // 8, np.uint64)
+    t0 = time.perf_counter()
+    L.vxc_read_stream(buf.ctypes.data_as(ctypes.c_void_p), buf.size, top)
+    t0 = time.perf_counter()
+    L.vxc_read_stream(buf.ctypes.data_as(ctypes.c_void_p), buf.size, top)
+    read_gbps = buf.nbytes / (time.perf_counter() - t0) / 1e9
+    wbytes = sum(t.size for t, *_ in mats)
+    return {"value": round(weights / best[top] / 1e9, 1), "unit": "Gweights/s", "cores": top, "kind": "port",
+            "sample": f"Falcon3-10B stream in model order over {layers} distinct layers ({weights} weights, "
+                      f"{wbytes / 1e6:.0f} MB of 64-row tiles per pass), AVX-512 transcription of the reference's "
+                      f"compact_multi_block (NB 3, 4 KiB prefetch), tables built per call; threads swept "
+                      f"{counts} up and down, best pass each; {time.perf_counter() - t_all:.1f} s",
+            "sweep_gweights_s": sweep, "weight_GBps_at_best": round(wbytes / best[top] / 1e9, 1),
+            "cpu_model": _cpu_model(), "logical_cpus": ncpu, "physical_cores": phys,
+            "host_read_GBps_1GiB": round(read_gbps, 1)}
+
+
+def cpu_baseline_scalar(budget_s: float, shapes):
+    """The CPU oracle's scalar restatement of the reference's table GEMV (oracle/velurex_oracle.c), one thread, over
+    the seven projections of one Falcon3-10B layer repeated until the budget is used (hosts without AVX-512 VBMI)."""
+    import numpy as np
+    from oracle import oracle
+    L = oracle.lib()
     mats = []
     for i, (r, c) in enumerate(shapes):
         t = oracle.gen_trits(100 + i, (r, c))
@@ -217,8 +316,8 @@ def cpu_baseline(budget_s: float):
             break
     dt = time.perf_counter() - t0
     return {"value": round(weights / dt / 1e9, 3), "unit": "Gweights/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} pass(es) over the 7 projections of one Falcon3-10B layer ({sum(r * c for _, r, c, _, _ in mats)} "
-                      f"weights/pass), scalar C restatement of the table kernel, 1 thread, {dt:.1f} s"}
+            "sample": f"{reps} pass(es) over the 7 projections of one Falcon3-10B layer, scalar C restatement of the "
+                      f"table kernel (no AVX-512 VBMI on this host), 1 thread, {dt:.1f} s"}
 
 
 def gemm_bench(torch, L, lib, args) -> int:
@@ -311,6 +410,121 @@ def q2_bench(torch, L, lib, args) -> int:
     return 0
 
 
+def synth_bitnet_planar(np, rng, rows: int, cols: int):
+    """Planar velurex bytes (pack.rs:66-131) of i.i.d. trits, P(-1) = P(+1) = 0.35, on the host: each byte of a full
+    160-trit block is drawn from the distribution of its five digits (a 65536-entry inverse-CDF table); bytes of the
+    last, partial block carry zero trits past `cols`."""
+    p = np.array([0.35, 0.30, 0.35])
+    digits = np.stack(np.meshgrid(*[np.arange(3)] * 5, indexing="ij"), -1).reshape(-1, 5)  # d0..d4
+    prob = np.prod(p[digits], axis=1)
+    byte = digits @ np.array([1, 3, 9, 28, 84])
+    cdf = np.cumsum(prob)
+    table = byte[np.minimum(np.searchsorted(cdf, (np.arange(65536) + 0.5) / 65536.0), len(byte) - 1)].astype(np.uint8)
+    nb = (cols + 159) // 160
+    out = table[rng.integers(0, 65536, rows * nb * 32, dtype=np.uint16)].reshape(rows, nb, 32)
+    rem = cols - (nb - 1) * 160
+    if rem < 160:  # trits p*32 + j >= rem of the last block are zero (digit 1)
+        v = out[:, nb - 1, :].astype(np.int64)
+        dig = np.empty((rows, 5, 32), np.int64)
+        u = v // 28
+        lo = v - 28 * u
+        dig[:, 0], dig[:, 1], dig[:, 2] = lo % 3, (lo // 3) % 3, lo // 9
+        dig[:, 3], dig[:, 4] = u % 3, u // 3
+        col = np.arange(5)[:, None] * 32 + np.arange(32)[None, :]
+        dig[:, col >= rem] = 1
+        out[:, nb - 1, :] = (dig * np.array([1, 3, 9, 28, 84])[None, :, None]).sum(1).astype(np.uint8)
+    return out.reshape(-1)
+
+
+def synth_bf16(np, rng, n: int, sigma: float):
+    """bf16 bits of N(0, sigma) values (round to nearest even)."""
+    out = np.empty(n, np.uint16)
+    step = 1 << 24
+    for i in range(0, n, step):
+        x = (rng.standard_normal(min(step, n - i), dtype=np.float32) * np.float32(sigma)).view(np.uint32)
+        out[i:i + x.size] = ((x + 0x7FFF + ((x >> 16) & 1)) >> 16).astype(np.uint16)
+    return out
+
+
+def decode_cpu_baseline(budget_s: float, prompt, cfg):
+    """The oracle's decode step (oracle/decode_oracle.c: the reference's CPU token loop restated in C, projections
+    exact, OpenMP over output rows) on this host's cores, a bounded number of tokens of the same model shape."""
+    from oracle import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    m = oracle.Model(oracle.bitnet_2b(cfg.max_ctx), 0xB17)
+    t0 = time.perf_counter()
+    n = 0
+    for pos, tok in enumerate(prompt):
+        m.forward(int(tok), pos)
+        n += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    m.close()
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} decode steps (positions 0..{n - 1}) of the BitNet-b1.58-2B-shaped model by the C "
+                      f"restatement of the reference's token loop, {threads} OpenMP threads, {dt:.1f} s"}
+
+
+def decode_bench(torch, args) -> int:
+    """greedy bs=1 decode of a random-init BitNet-b1.58-2B-shaped model (30 layers, hidden
+    2560, 20/5 heads x 128, FFN 6912 ReLU^2, vocab 128256, tied bf16 head), 64 prompt tokens then --decode-new
+    generated tokens, every step one replay of the decode graph. tok/s counts every decoded position (prompt tokens
+    are fed one at a time, as the reference's loop does)."""
+    import numpy as np
+    from quintrit_amd.decoder import Decoder, DecoderConfig
+    cfg = DecoderConfig.bitnet_2b()
+    rng = np.random.default_rng(0xB17)
+    log("building a random-init BitNet-2B-shaped model on the host")
+    dec = Decoder(cfg)
+    trits = 0
+    for layer in range(cfg.n_layers):
+        for kind in range(7):
+            rows, cols = cfg.projection_shape(kind)
+            dec.set_projection(layer, kind, synth_bitnet_planar(np, rng, rows, cols), 1.0 / float(np.sqrt(np.float32(cols))))
+            trits += rows * cols
+        for kind, n in enumerate((cfg.hidden, cfg.n_heads * cfg.head_dim, cfg.hidden, cfg.ffn)):
+            dec.set_norm(layer, kind, rng.uniform(0.75, 1.25, n).astype(np.float32))
+    dec.set_norm(cfg.n_layers, 0, rng.uniform(0.75, 1.25, cfg.hidden).astype(np.float32))
+    dec.set_embedding_bf16(synth_bf16(np, rng, cfg.vocab * cfg.hidden, 0.02))
+    prompt = rng.integers(0, cfg.vocab, 64)
+    n_new = args.decode_new
+    steps_per_run = len(prompt) + n_new - 1
+    log(f"{trits} trits ({trits / 5 / 1e9:.3f} GB at 1.60 bpw), {dec.memory_bytes() / 1e9:.2f} GB on the device; warmup")
+    for _ in range(max(1, args.warmup // 10)):
+        dec.generate(prompt, n_new)
+    runs = max(1, args.steps // 10)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(runs):
+        toks = dec.generate(prompt, n_new)
+    dt = (time.perf_counter() - t0) / runs
+    ms_tok = dt / steps_per_run * 1e3
+    head_bytes = cfg.vocab * cfg.hidden * 2
+    alg = trits / 5.0 + head_bytes
+    log(f"{runs} run(s) of {steps_per_run} steps: {ms_tok:.4f} ms/token, {1e3 / ms_tok:.1f} tok/s; tokens {toks[:8]}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (oracle decode steps)")
+        cpu = decode_cpu_baseline(args.cpu_seconds, prompt, cfg)
+        log(f"cpu baseline {cpu['value']} tok/s")
+    line = {
+        "metric": METRIC, "value": round(1e3 / ms_tok, 1), "unit": "tok/s", "n_gpus": 1, "steps": runs * steps_per_run,
+        "warmup": max(1, args.warmup // 10) * steps_per_run, "ms_per_step": round(ms_tok, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8 x ternary, fp32/f16 attention",
+        "data": "synthetic (random-init weights, random prompt)",
+        "config": {"workload": "bitnet-b1.58-2b greedy decode bs=1 (BASELINE.json configs[3])", "layers": cfg.n_layers,
+                   "hidden": cfg.hidden, "ffn": cfg.ffn, "vocab": cfg.vocab, "prompt": len(prompt), "new_tokens": n_new,
+                   "parallelism": "single-gpu"},
+        "generate_tok_s": round(n_new / dt, 1), "wall_s_per_run": round(dt, 4),
+        "alg_bytes_per_token": int(alg), "alg_GBps": round(alg / (ms_tok / 1e3) / 1e9, 1),
+        "hbm_bound_tok_s": round(HBM_PEAK_GBPS * 1e9 / alg, 1), "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    dec.close()
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -336,6 +550,8 @@ def main():
         return gemm_bench(torch, L, _lib, args)
     if args.workload == "q2":
         return q2_bench(torch, L, _lib, args)
+    if args.workload == "decode":
+        return decode_bench(torch, args)
     log(f"building the {args.layers}-layer weight stream on the GPU")
     st = Stream(torch, L, _lib, args.layers)
     log(f"{st.weights} weights, {st.alg_bytes / 1e9:.4f} GB algorithmic, {st.device_bytes / 1e9:.4f} GB device layout")

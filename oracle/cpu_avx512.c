@@ -1,0 +1,203 @@
+/*
+ * cpu_avx512.c - the reference's production CPU GEMV, transcribed with AVX-512 intrinsics (CPU BASELINE ONLY).
+ *
+ * bench.py times this beside the GPU as the reported CPU baseline; tests/ check it against the brute-force product.
+ * The product (quintrit_amd/) never calls it. The Rust original cannot be built here (no Rust toolchain), so the
+ * algorithm is restated in C with the same instruction sequence:
+ *   - activation tables: build_compact_wide_impl (quintrit-core/src/simd/avx512.rs:1216-1247): per tile column byte c
+ *     one 64-byte table per part (x = 16 hi + lo, lo = ((x + 8) & 15) - 8): entries 0..8 hold the sums over (a3, a4)
+ *     for the 9 digit pairs, entries 9..35 the sums over (a0, a1, a2) for the 27 digit triples, formed by masked
+ *     adds and subtracts of the broadcast parts (avx512.rs:1180-1197 for the masks);
+ *   - kernel: gemv_compact_multi::<3, 4096, T0, 0, true> -> compact_multi_block (avx512.rs:1526-1626): three 64-row
+ *     blocks per pass, per column two vpermb lookups per part after the shuffle decode of the weight byte
+ *     (h34 = w / 28 and r3 + 9 = w - (28 h34 - 9) from two 64-entry tables on w >> 2, avx512.rs:1255-1300), int8 sums
+ *     over 3 columns, vpmaddubsw with (1, 16) into int16 over chunks of 45 columns, int32 accumulators, a 4 KiB T0
+ *     prefetch of the weights;
+ *   - threads: whole 64-row blocks, ceil(blocks / threads) * 64 rows per thread (avx512.rs:1150-1168).
+ * Weights are in the reference's 64-row tiled layout (transform_weights_lut_64, avx512.rs:53-78): block b holds, for
+ * each tile column byte c, the bytes of its 64 rows contiguously at b * 64 * tbr + c * 64.
+ */
+#include "cpu_avx512.h"
+
+#include <immintrin.h>
+#include <omp.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "velurex_oracle.h"
+
+#define VXC_TARGET __attribute__((target("avx512f,avx512bw,avx512vbmi")))
+
+int vxc_supported(void) {
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+           __builtin_cpu_supports("avx512vbmi");
+}
+
+size_t vxc_table_bytes(size_t cols) { return 2 * vxo_tile_row_bytes(cols) * 64; }
+
+void vxc_tile64(const uint8_t* planar, size_t rows, size_t cols, uint8_t* out) {
+    const size_t prb = vxo_planar_row_bytes(cols), bpr = vxo_tile_row_bytes(cols);
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < bpr; ++c)
+            out[(r / 64) * 64 * bpr + c * 64 + r % 64] = vxo_tile_byte(planar + r * prb, cols, c);
+}
+
+/* Lane masks (positive, negative coefficient) of activation position p in a compact table. */
+static void coefficient_masks(uint64_t pos[5], uint64_t neg[5]) {
+    memset(pos, 0, 5 * sizeof(uint64_t));
+    memset(neg, 0, 5 * sizeof(uint64_t));
+    for (int s = 0; s < 9; ++s) {
+        const int c3 = s % 3 - 1, c4 = s / 3 - 1;
+        if (c3 > 0) pos[3] |= 1ull << s;
+        if (c3 < 0) neg[3] |= 1ull << s;
+        if (c4 > 0) pos[4] |= 1ull << s;
+        if (c4 < 0) neg[4] |= 1ull << s;
+    }
+    for (int s = 0; s < 27; ++s) {
+        const int lane = 9 + s;
+        const int c[3] = {s % 3 - 1, (s / 3) % 3 - 1, s / 9 - 1};
+        for (int p = 0; p < 3; ++p) {
+            if (c[p] > 0) pos[p] |= 1ull << lane;
+            if (c[p] < 0) neg[p] |= 1ull << lane;
+        }
+    }
+}
+
+VXC_TARGET void vxc_build_tables(const int8_t* acts, size_t cols, int8_t* tables) {
+    const size_t bpr = vxo_tile_row_bytes(cols);
+    uint64_t pos[5], neg[5];
+    coefficient_masks(pos, neg);
+    int8_t* lo_dst = tables;
+    int8_t* hi_dst = tables + bpr * 64;
+    for (size_t c = 0; c < bpr; ++c) {
+        __m512i acc_lo = _mm512_setzero_si512(), acc_hi = _mm512_setzero_si512();
+        for (size_t p = 0; p < 5; ++p) {
+            const size_t idx = vxo_column_activation_index(cols, c, p);
+            const int x = idx < cols ? acts[idx] : 0;
+            const int l = ((x + 8) & 15) - 8;
+            const __m512i bl = _mm512_set1_epi8((char)l), bh = _mm512_set1_epi8((char)((x - l) >> 4));
+            acc_lo = _mm512_mask_add_epi8(acc_lo, pos[p], acc_lo, bl);
+            acc_lo = _mm512_mask_sub_epi8(acc_lo, neg[p], acc_lo, bl);
+            acc_hi = _mm512_mask_add_epi8(acc_hi, pos[p], acc_hi, bh);
+            acc_hi = _mm512_mask_sub_epi8(acc_hi, neg[p], acc_hi, bh);
+        }
+        _mm512_storeu_si512((void*)(lo_dst + c * 64), acc_lo);
+        _mm512_storeu_si512((void*)(hi_dst + c * 64), acc_hi);
+    }
+}
+
+/* The rows of one block from its four int32 accumulators: vpunpck{l,h}bw splits each 128-bit lane into rows 0..7 and
+ * 8..15 of its 16 rows; the low and high 256 bits of the int16 sums hold lanes 0-1 and 2-3. */
+VXC_TARGET static void put_rows(__m512i a0, __m512i a1, __m512i b0, __m512i b1, float* out) {
+    int32_t t[16];
+    const __m512i acc[4] = {a0, b0, a1, b1};
+    const int first[4] = {0, 8, 32, 40};
+    for (int k = 0; k < 4; ++k) {
+        _mm512_storeu_si512((void*)t, acc[k]);
+        for (int i = 0; i < 8; ++i) {
+            out[first[k] + i] = (float)t[i];
+            out[first[k] + 16 + i] = (float)t[8 + i];
+        }
+    }
+}
+
+#define VXC_NB_MAX 3
+#define VXC_CHUNK 45
+#define VXC_PF 4096
+
+VXC_TARGET static inline __attribute__((always_inline)) void multi_block(const int nb, const uint8_t* w, size_t stride,
+                                                                          const int8_t* lo, const int8_t* hi,
+                                                                          size_t bpr, float* out) {
+    uint8_t th_b[64], tm_b[64];
+    for (int i = 0; i < 64; ++i) {
+        th_b[i] = (uint8_t)(i / 7);
+        tm_b[i] = (uint8_t)(28 * (i / 7) - 9);
+    }
+    const __m512i th = _mm512_loadu_si512((const void*)th_b), tm = _mm512_loadu_si512((const void*)tm_b);
+    const __m512i combine = _mm512_set1_epi16(0x1001);
+    const __m512i zero = _mm512_setzero_si512();
+    __m512i a0[VXC_NB_MAX], a1[VXC_NB_MAX], b0[VXC_NB_MAX], b1[VXC_NB_MAX];
+    for (int b = 0; b < nb; ++b) a0[b] = a1[b] = b0[b] = b1[b] = zero;
+    for (size_t c = 0; c < bpr;) {
+        const size_t len = bpr - c < VXC_CHUNK ? bpr - c : VXC_CHUNK;
+        __m512i sa[VXC_NB_MAX], sb[VXC_NB_MAX];
+        for (int b = 0; b < nb; ++b) sa[b] = sb[b] = zero;
+        for (size_t ci = 0; ci < len;) {
+            const size_t n = len - ci < 3 ? len - ci : 3;
+            for (int b = 0; b < nb; ++b) {
+                const char* base = (const char*)(w + b * stride + (c + ci) * 64);
+                _mm_prefetch(base + VXC_PF, _MM_HINT_T0);
+                _mm_prefetch(base + VXC_PF + 64, _MM_HINT_T0);
+                _mm_prefetch(base + VXC_PF + 128, _MM_HINT_T0);
+            }
+            __m512i slo[VXC_NB_MAX], shi[VXC_NB_MAX];
+            for (size_t j = 0; j < n; ++j) {
+                const size_t col = c + ci + j;
+                const __m512i tl = _mm512_loadu_si512((const void*)(lo + col * 64));
+                const __m512i tt = _mm512_loadu_si512((const void*)(hi + col * 64));
+                for (int b = 0; b < nb; ++b) {
+                    const __m512i wv = _mm512_loadu_si512((const void*)(w + b * stride + col * 64));
+                    const __m512i idx = _mm512_srli_epi16(wv, 2);
+                    const __m512i h34 = _mm512_permutexvar_epi8(idx, th);
+                    const __m512i r3 = _mm512_sub_epi8(wv, _mm512_permutexvar_epi8(idx, tm));
+                    const __m512i l = _mm512_add_epi8(_mm512_permutexvar_epi8(h34, tl), _mm512_permutexvar_epi8(r3, tl));
+                    const __m512i h = _mm512_add_epi8(_mm512_permutexvar_epi8(h34, tt), _mm512_permutexvar_epi8(r3, tt));
+                    slo[b] = j == 0 ? l : _mm512_add_epi8(slo[b], l);
+                    shi[b] = j == 0 ? h : _mm512_add_epi8(shi[b], h);
+                }
+            }
+            for (int b = 0; b < nb; ++b) {
+                sa[b] = _mm512_add_epi16(sa[b], _mm512_maddubs_epi16(combine, _mm512_unpacklo_epi8(slo[b], shi[b])));
+                sb[b] = _mm512_add_epi16(sb[b], _mm512_maddubs_epi16(combine, _mm512_unpackhi_epi8(slo[b], shi[b])));
+            }
+            ci += n;
+        }
+        for (int b = 0; b < nb; ++b) {
+            a0[b] = _mm512_add_epi32(a0[b], _mm512_cvtepi16_epi32(_mm512_castsi512_si256(sa[b])));
+            a1[b] = _mm512_add_epi32(a1[b], _mm512_cvtepi16_epi32(_mm512_extracti64x4_epi64(sa[b], 1)));
+            b0[b] = _mm512_add_epi32(b0[b], _mm512_cvtepi16_epi32(_mm512_castsi512_si256(sb[b])));
+            b1[b] = _mm512_add_epi32(b1[b], _mm512_cvtepi16_epi32(_mm512_extracti64x4_epi64(sb[b], 1)));
+        }
+        c += len;
+    }
+    for (int b = 0; b < nb; ++b) put_rows(a0[b], a1[b], b0[b], b1[b], out + b * 64);
+}
+
+VXC_TARGET static void gemv_blocks(const uint8_t* w, const int8_t* tables, size_t nblocks, size_t bpr, float* out) {
+    const size_t stride = 64 * bpr;
+    const int8_t* lo = tables;
+    const int8_t* hi = tables + bpr * 64;
+    size_t b = 0;
+    for (; b + 3 <= nblocks; b += 3) multi_block(3, w + b * stride, stride, lo, hi, bpr, out + b * 64);
+    for (; b < nblocks; ++b) multi_block(1, w + b * stride, stride, lo, hi, bpr, out + b * 64);
+}
+
+void vxc_gemv_tables(const uint8_t* tiles64, const int8_t* tables, size_t rows, size_t cols, float* out, int threads) {
+    const size_t bpr = vxo_tile_row_bytes(cols), nblocks = rows / 64;
+    if (threads <= 1 || nblocks < (size_t)threads) {
+        gemv_blocks(tiles64, tables, nblocks, bpr, out);
+        return;
+    }
+    const size_t per = (nblocks + (size_t)threads - 1) / (size_t)threads; /* blocks per thread */
+    const size_t chunks = (nblocks + per - 1) / per;
+#pragma omp parallel for num_threads(threads) schedule(static, 1)
+    for (size_t t = 0; t < chunks; ++t) {
+        const size_t b0 = t * per, nb = nblocks - b0 < per ? nblocks - b0 : per;
+        gemv_blocks(tiles64 + b0 * 64 * bpr, tables, nb, bpr, out + b0 * 64);
+    }
+}
+
+void vxc_gemv(const uint8_t* tiles64, const int8_t* acts, size_t rows, size_t cols, float* out, int threads,
+              int8_t* table_scratch) {
+    vxc_build_tables(acts, cols, table_scratch);
+    vxc_gemv_tables(tiles64, table_scratch, rows, cols, out, threads);
+}
+
+/* Host read bandwidth: `threads` threads each sum their share of `bytes` (64-bit words); returns the sum. */
+uint64_t vxc_read_stream(const uint64_t* buf, size_t words, int threads) {
+    uint64_t total = 0;
+#pragma omp parallel for num_threads(threads) schedule(static) reduction(+ : total)
+    for (size_t i = 0; i < words; ++i) total += buf[i];
+    return total;
+}

@@ -1,0 +1,29 @@
+/* cpu_avx512.h - the reference's production CPU GEMV in AVX-512 (CPU BASELINE ONLY; see cpu_avx512.c). */
+#ifndef VXC_CPU_AVX512_H
+#define VXC_CPU_AVX512_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* 1 when the host has AVX-512 F, BW and VBMI (the kernel's instructions). */
+int vxc_supported(void);
+/* Bytes of the compact wide tables of one activation vector: 2 * tile_row_bytes(cols) * 64. */
+size_t vxc_table_bytes(size_t cols);
+/* Planar rows -> the 64-row tiled layout (rows a multiple of 64). */
+void vxc_tile64(const uint8_t* planar, size_t rows, size_t cols, uint8_t* out);
+void vxc_build_tables(const int8_t* acts, size_t cols, int8_t* tables);
+/* out[r] = float(sum_k t[r][k] * acts[k]) for rows a multiple of 64, from prebuilt tables. */
+void vxc_gemv_tables(const uint8_t* tiles64, const int8_t* tables, size_t rows, size_t cols, float* out, int threads);
+/* Tables then kernel (one call of the reference's GEMV); table_scratch holds vxc_table_bytes(cols). */
+void vxc_gemv(const uint8_t* tiles64, const int8_t* acts, size_t rows, size_t cols, float* out, int threads,
+              int8_t* table_scratch);
+uint64_t vxc_read_stream(const uint64_t* buf, size_t words, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

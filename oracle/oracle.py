@@ -94,6 +94,13 @@ def _declare(L: ctypes.CDLL) -> None:
         "vxo_model_reset": (None, [vp]),
         "vxo_model_forward": (ctypes.c_uint32, [vp, ctypes.c_uint32, sz, vp]),
         "vxo_model_generate": (None, [vp, vp, sz, sz, vp]),
+        "vxc_supported": (ctypes.c_int, []),
+        "vxc_table_bytes": (sz, [sz]),
+        "vxc_tile64": (None, [vp, sz, sz, vp]),
+        "vxc_build_tables": (None, [vp, sz, vp]),
+        "vxc_gemv_tables": (None, [vp, vp, sz, sz, vp, ctypes.c_int]),
+        "vxc_gemv": (None, [vp, vp, sz, sz, vp, ctypes.c_int, vp]),
+        "vxc_read_stream": (u64, [vp, sz, ctypes.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -432,4 +439,30 @@ def attend_head(q_f16, k_f16, v_f16, seq_len: int, max_ctx: int, scale: float) -
     v = np.ascontiguousarray(v_f16, np.uint16)
     out = np.empty(q.size, np.float32)
     lib().vxo_attend_head(_p(q), _p(k), _p(v), q.size, q.size, seq_len, max_ctx, scale, _p(out))
+    return out
+
+
+# ---- the AVX-512 transcription of the reference's production CPU GEMV (cpu_avx512.c; the CPU baseline) ----------
+
+def cpu_avx512_supported() -> bool:
+    return bool(lib().vxc_supported())
+
+
+def tile64(planar: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Planar rows -> the reference's 64-row tiled layout (transform_weights_lut_64); rows a multiple of 64."""
+    p = np.ascontiguousarray(planar, dtype=np.uint8)
+    out = np.empty(rows * tile_row_bytes(cols), np.uint8)
+    lib().vxc_tile64(_p(p), rows, cols, _p(out))
+    return out
+
+
+def gemv_avx512(tiles64_: np.ndarray, acts: np.ndarray, rows: int, cols: int, threads: int = 1) -> np.ndarray:
+    """float(sum_k t[r][k] acts[k]) by the AVX-512 kernel (raises when the host lacks AVX-512 VBMI)."""
+    if not cpu_avx512_supported():
+        raise RuntimeError("this host has no AVX-512 F/BW/VBMI")
+    t = np.ascontiguousarray(tiles64_, dtype=np.uint8)
+    a = np.ascontiguousarray(acts, dtype=np.int8)
+    out = np.empty(rows, np.float32)
+    scratch = np.empty(int(lib().vxc_table_bytes(cols)), np.int8)
+    lib().vxc_gemv(_p(t), _p(a), rows, cols, _p(out), threads, _p(scratch))
     return out

@@ -126,3 +126,24 @@ def test_argument_errors_without_gpu():
     assert L.vx_q2_matrix_create(buf, 64, buf, 64, 1, 12352, ctypes.byref(h)) == 3
     assert L.vx_q2_matrix_create(buf, 16, buf, 64, 1, 64, ctypes.byref(h)) == 4   # planar too short
     assert L.vx_q2_gemv_f32_dev(None, buf, 64, buf, 2, buf, 1, None) == 14
+
+
+def test_decoder_config_errors_before_device():
+    """vx_decoder_create checks its configuration before touching a device (so these run without a GPU)."""
+    import ctypes
+    from quintrit_amd import _lib
+    from quintrit_amd.decoder import DecoderConfig
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    assert L.vx_decoder_create(None, ctypes.byref(h)) == 1  # NULL config
+    c = DecoderConfig.bitnet_2b()._c()
+    c.struct_size = 4
+    assert L.vx_decoder_create(ctypes.byref(c), ctypes.byref(h)) == 2
+    for field, value, status in (("head_dim", 64, 6), ("max_ctx", 8192, 6), ("n_kv_heads", 3, 2), ("hidden", 100, 6),
+                                 ("ffn", 9000, 6), ("vocab", 0, 2), ("n_layers", 0, 2)):
+        c = DecoderConfig.bitnet_2b()._c()
+        setattr(c, field, value)
+        assert L.vx_decoder_create(ctypes.byref(c), ctypes.byref(h)) == status, field
+        assert field.split("_")[0] in L.vx_last_error_message().decode() or status == 2
+    assert L.vx_decoder_free(None) == 0
+    assert L.vx_decoder_step(None, 0, 0, None, 0, None) == 14
