@@ -67,6 +67,7 @@ static int set_device_of(const vx_matrix_t* m) {
 static void destroy(vx_matrix* m) {
     if (m->d_w) (void)hipFree(m->d_w);
     if (m->d_part) (void)hipFree(m->d_part);
+    if (m->d_dsum) (void)hipFree(m->d_dsum);
     if (m->d_staged) (void)hipFree(m->d_staged);
     if (m->d_io) (void)hipFree(m->d_io);
     m->magic = 0;
@@ -95,6 +96,7 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     m->num_cus = di.num_cus;
     m->d_w = nullptr;
     m->d_part = nullptr;
+    m->d_dsum = nullptr;
     m->d_staged = nullptr;
     m->d_io = nullptr;
     Job probe{};
@@ -105,6 +107,7 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     const size_t io_bytes = round_up(cols, 256) + m->g.padded_rows * 4;
     hipError_t e = hipMalloc(&m->d_w, m->g.device_bytes);
     if (e == hipSuccess && m->kslices > 1) e = hipMalloc(&m->d_part, static_cast<size_t>(m->kslices) * m->g.padded_rows * 4);
+    if (e == hipSuccess) e = hipMalloc(&m->d_dsum, m->g.padded_rows * 4);
     if (e == hipSuccess) e = hipMalloc(&m->d_staged, staged_bytes(cols));
     if (e == hipSuccess) e = hipMalloc(&m->d_io, io_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -131,8 +134,11 @@ static int create_matrix(const uint8_t* planar, size_t planar_len, size_t rows, 
     std::vector<uint8_t> host(m->g.device_bytes);
     planar_to_device_layout(planar, m->g, host.data());
     hipError_t e = hipMemcpy(m->d_w, host.data(), m->g.device_bytes, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
+    int st = e == hipSuccess ? launch_digit_sums(m->d_w, m->g, m->d_dsum, nullptr) : VX_OK;
+    if (e == hipSuccess && st == VX_OK) e = hipDeviceSynchronize();
+    if (e != hipSuccess || st != VX_OK) {
         destroy(m);
+        if (st != VX_OK) return st;
         VX_FAIL(VX_ERR_DEVICE, "upload failed: %s", hipGetErrorString(e));
     }
     *out = m;
@@ -154,6 +160,7 @@ static int create_matrix_dev(const uint8_t* planar_dev, size_t planar_len, size_
     int st = VX_OK;
     if (e == hipSuccess) st = launch_find_invalid(planar_dev, need, d_first, nullptr);
     if (e == hipSuccess && st == VX_OK) st = launch_device_layout(planar_dev, m->g, m->d_w, nullptr);
+    if (e == hipSuccess && st == VX_OK) st = launch_digit_sums(m->d_w, m->g, m->d_dsum, nullptr);
     if (e == hipSuccess && st == VX_OK) e = hipMemcpy(&first, d_first, sizeof first, hipMemcpyDeviceToHost);
     if (d_first) (void)hipFree(d_first);
     if (st != VX_OK || e != hipSuccess) {
@@ -190,6 +197,7 @@ static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint
     j.w = m->d_w;
     j.staged = staged;
     j.part = m->d_part;
+    j.dsum = m->d_dsum;
     j.out = out;
     j.act_scale = nullptr;
     j.post = post;
@@ -542,6 +550,7 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
         j = Job{};
         plan_job(j, m->g, 0);
         j.w = m->d_w;
+        j.dsum = m->d_dsum;
         j.staged = static_cast<const uint8_t*>(u.staged);
         j.out = u.out;
         j.act_scale = u.act_scale_dev;
@@ -737,6 +746,7 @@ int vx_q2_matrix_create(const uint8_t* planar, size_t planar_len, const uint16_t
         m->slice_chunks = 0;
         m->d_w = nullptr;
         m->d_part = nullptr;
+        m->d_dsum = nullptr;
         m->d_staged = nullptr;
         m->d_io = nullptr;
         const size_t bytes = q2_device_bytes(rows, cols);

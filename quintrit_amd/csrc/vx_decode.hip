@@ -161,16 +161,14 @@ __global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(NormArgs p) {
     const uint32_t full = n / 160u * 32u;
     uint2* ent = reinterpret_cast<uint2*>(p.staged + kStageHeader);
     int sum = 0;
-    for (uint32_t c = tid; c < p.dbr; c += kNormThreads) {
+    for (uint32_t c = tid; c < p.dbr; c += kNormThreads) {  // the entries of vx_stage_acts_dev
         uint32_t lo = 0, hi = 0;
-        if (c < p.tbr) {
-            for (uint32_t k = 0; k < 5; ++k) {
-                const uint32_t idx = c < full ? (c / 32u) * 160u + k * 32u + (c % 32u) : (n / 160u) * 160u + 5u * (c - full) + k;
-                const int x = idx < n ? qs[idx] : 0;
-                lo |= (static_cast<uint32_t>(x) & 15u) << (4 * k);
-                hi |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * k);
-                sum += x;
-            }
+        for (uint32_t k = 0; k < 5; ++k) {
+            const uint32_t idx = c < full ? (c / 32u) * 160u + k * 32u + (c % 32u) : (n / 160u) * 160u + 5u * (c - full) + k;
+            const int x = c < p.tbr && idx < n ? qs[idx] : 0;
+            lo |= ((static_cast<uint32_t>(x) & 15u) ^ 8u) << (4 * k);
+            hi |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * k);
+            sum += x;
         }
         ent[c] = make_uint2(lo, hi);
     }
@@ -814,6 +812,7 @@ static int build_plans(vx_decoder* d) {
                 Job j{};
                 plan_job(j, m->g, target);
                 j.w = m->d_w;
+                j.dsum = m->d_dsum;
                 j.staged = d->d_stage[s];
                 j.out = outs[k];
                 j.act_scale = d->d_as + s;

@@ -59,9 +59,10 @@ __host__ __device__ inline int trit_of(uint32_t b, uint32_t p) {
 
 // ---- activation staging -----------------------------------------------------------------------------------------------
 
-// One workgroup. Entry c (device byte-column c): dword 2c = the lo nibbles of the five activations of the column,
-// dword 2c+1 = their hi nibbles; activation p of column c is column_activation_index(cols, c, p) (pack.rs:230-237), zero
-// past the end of the row. The header holds the sum of all activations.
+// One workgroup. Entry c (device byte-column c): dword 2c = the low nibbles of the five activations of the column,
+// stored as (x & 15) ^ 8 (the signed nibble (x & 15) - 8), dword 2c+1 = their high nibbles x >> 4 (signed);
+// activation p of column c is column_activation_index(cols, c, p) (pack.rs:230-237), zero past the end of the row and
+// in the padding columns. The header holds the sum of all activations.
 __global__ __launch_bounds__(1024) void stage_kernel(const int8_t* __restrict__ acts, uint32_t cols, uint32_t tbr,
                                                      uint32_t dbr, uint8_t* __restrict__ staged) {
     __shared__ int wsum[16];
@@ -71,14 +72,12 @@ __global__ __launch_bounds__(1024) void stage_kernel(const int8_t* __restrict__ 
     int sum = 0;
     for (uint32_t c = tid; c < dbr; c += 1024u) {
         uint32_t lo = 0, hi = 0;
-        if (c < tbr) {
-            for (uint32_t p = 0; p < 5; ++p) {
-                const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
-                const int x = idx < cols ? acts[idx] : 0;
-                lo |= (static_cast<uint32_t>(x) & 15u) << (4 * p);
-                hi |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * p);
-                sum += x;
-            }
+        for (uint32_t p = 0; p < 5; ++p) {
+            const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
+            const int x = c < tbr && idx < cols ? acts[idx] : 0;
+            lo |= ((static_cast<uint32_t>(x) & 15u) ^ 8u) << (4 * p);
+            hi |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * p);
+            sum += x;
         }
         ent[c] = make_uint2(lo, hi);
     }
@@ -138,6 +137,20 @@ __global__ void find_invalid_kernel(const uint8_t* __restrict__ planar, uint64_t
     if (!byte_valid(planar[i])) atomicMin(first, static_cast<unsigned long long>(i));
 }
 
+// One row per thread: the sum of the digits (t + 1) of the five trits of every device byte of the row, padding bytes
+// included (their activations are zero, staged as low nibble -8, so the correction 8 * dsum cancels them).
+__global__ void digit_sum_kernel(const uint8_t* __restrict__ w, uint32_t padded_rows, uint32_t n_tiles, uint32_t n_chunks,
+                                 int32_t* __restrict__ dsum) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= padded_rows) return;
+    int s = 0;
+    for (uint32_t c = 0; c < n_chunks * kChunk; ++c) {
+        const uint32_t e = digit_nibbles(w[layout_offset(r, c, n_tiles, n_chunks)]);
+        s += static_cast<int>((e & 15u) + ((e >> 4) & 15u) + ((e >> 8) & 15u) + ((e >> 12) & 15u) + ((e >> 16) & 15u));
+    }
+    dsum[r] = s;
+}
+
 __global__ void fill_f32_kernel(float* __restrict__ out, uint32_t n, float v) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = v;
@@ -164,6 +177,33 @@ __device__ __forceinline__ void store_out(const Job& jb, uint32_t row, int acc, 
 
 __device__ __forceinline__ int staged_sum(const Job& jb) { return *(const c_int*)(jb.staged); }
 
+// The integer result of row `row` from the two dot-product accumulators summed over all K slices: lo holds
+// sum d (l - 8) with l = x & 15, hi holds sum d (x >> 4), so sum t x = 16 hi + lo + 8 sum d - sum x.
+__device__ __forceinline__ int row_result(const Job& jb, uint32_t row, int lo_plus_16hi) {
+    return lo_plus_16hi + 8 * jb.dsum[row] - staged_sum(jb);
+}
+
+
+// Four bytes of a lane's weights against their activations: lo += dot8(L of byte K + j, t_j), hi += dot8(H, t_j) for
+// j = 0..3, where t_j is the digit-nibble table entry of byte j and the activation dwords of the 16 byte-columns of a
+// chunk sit in lanes 0..15 of every 16-lane row of L and H, broadcast by DPP row_newbcast. v_dot8c_i32_i4 multiplies
+// signed nibbles: the digits (0..2), the high nibbles x >> 4 and the low nibbles (x & 15) - 8. L and H come from LDS
+// loads; the s_nop keeps the two wait states a DPP read needs after any VALU write of its source.
+template <int K>
+__device__ __forceinline__ void dot4_bcast(int& lo, int& hi, uint32_t L, uint32_t H, uint32_t t0, uint32_t t1, uint32_t t2,
+                                           uint32_t t3) {
+    asm("s_nop 1\n\t"
+        "v_dot8c_i32_i4_dpp %0, %2, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot8c_i32_i4_dpp %1, %3, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot8c_i32_i4_dpp %0, %2, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot8c_i32_i4_dpp %1, %3, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot8c_i32_i4_dpp %0, %2, %6 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot8c_i32_i4_dpp %1, %3, %6 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot8c_i32_i4_dpp %0, %2, %7 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot8c_i32_i4_dpp %1, %3, %7 row_newbcast:%11 row_mask:0xf bank_mask:0xf"
+        : "+v"(lo), "+v"(hi)
+        : "v"(L), "v"(H), "v"(t0), "v"(t1), "v"(t2), "v"(t3), "n"(K), "n"(K + 1), "n"(K + 2), "n"(K + 3));
+}
 
 constexpr int kWaves = 16;   // waves per workgroup = tiles per group
 constexpr int kGroup = 4;    // chunks loaded together by a wave
@@ -231,21 +271,20 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
 #pragma unroll
                 for (int i = 0; i < kGroup; ++i) {
                     const uint32_t dw[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
-                    const uint4* a = ab + (g + i) * 8u;
+                    // this lane's activation entry: byte-column lane % 16 of the chunk (the same in all four rows)
+                    const uint2 e = reinterpret_cast<const uint2*>(ab)[(g + i) * 16u + (lane & 15u)];
                     __builtin_amdgcn_sched_barrier(0);
+                    uint32_t t[16];
 #pragma unroll
-                    for (int k2 = 0; k2 < 8; ++k2) {  // one uint4 of activations = two byte-columns
-                        const uint4 av = a[k2];
-#pragma unroll
-                        for (int h = 0; h < 2; ++h) {
-                            const int k = 2 * k2 + h;
-                            const uint32_t addr =
-                                __builtin_amdgcn_perm(dw[k >> 2], lane_off, 0x0c0c0000u | ((4u + (k & 3)) << 8));
-                            const uint32_t t = *reinterpret_cast<const uint32_t*>(tabb + addr);
-                            acc_lo = static_cast<int>(__builtin_amdgcn_udot8(t, h ? av.z : av.x, static_cast<uint32_t>(acc_lo), false));
-                            acc_hi = __builtin_amdgcn_sdot8(static_cast<int>(t), static_cast<int>(h ? av.w : av.y), acc_hi, false);
-                        }
+                    for (int k = 0; k < 16; ++k) {
+                        const uint32_t addr =
+                            __builtin_amdgcn_perm(dw[k >> 2], lane_off, 0x0c0c0000u | ((4u + (k & 3)) << 8));
+                        t[k] = *reinterpret_cast<const uint32_t*>(tabb + addr);
                     }
+                    dot4_bcast<0>(acc_lo, acc_hi, e.x, e.y, t[0], t[1], t[2], t[3]);
+                    dot4_bcast<4>(acc_lo, acc_hi, e.x, e.y, t[4], t[5], t[6], t[7]);
+                    dot4_bcast<8>(acc_lo, acc_hi, e.x, e.y, t[8], t[9], t[10], t[11]);
+                    dot4_bcast<12>(acc_lo, acc_hi, e.x, e.y, t[12], t[13], t[14], t[15]);
                 }
             }
             const int v = acc_lo + 16 * acc_hi;
@@ -253,7 +292,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
             if (jb.kslices == 1) {
                 bool zero;
                 const float post = job_post(jb, &zero);
-                store_out(jb, row, v - staged_sum(jb), post, zero);
+                store_out(jb, row, row_result(jb, row, v), post, zero);
             } else {
                 jb.part[static_cast<size_t>(ks) * jb.padded_rows + row] = v;
             }
@@ -287,7 +326,7 @@ __global__ __launch_bounds__(256) void finish_kernel(LaunchArgs args, const uint
         s = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
         bool zero;
         const float post = job_post(jb, &zero);
-        store_out(jb, row, s - staged_sum(jb), post, zero);
+        store_out(jb, row, row_result(jb, row, s), post, zero);
     }
 }
 
@@ -337,6 +376,14 @@ int launch_device_layout(const uint8_t* planar_dev, const Geometry& g, uint8_t* 
                        static_cast<uint64_t>(g.rows), static_cast<uint32_t>(g.cols),
                        static_cast<uint32_t>(planar_row_bytes(g.cols)), static_cast<uint32_t>(g.tbr),
                        static_cast<uint32_t>(g.n_tiles), static_cast<uint32_t>(g.n_chunks), total, dst);
+    VX_HIP(hipGetLastError());
+    return VX_OK;
+}
+
+int launch_digit_sums(const uint8_t* w, const Geometry& g, int32_t* dsum, hipStream_t stream) {
+    const uint32_t rows = static_cast<uint32_t>(g.padded_rows);
+    hipLaunchKernelGGL(digit_sum_kernel, dim3((rows + 255u) / 256u), dim3(256), 0, stream, w, rows,
+                       static_cast<uint32_t>(g.n_tiles), static_cast<uint32_t>(g.n_chunks), dsum);
     VX_HIP(hipGetLastError());
     return VX_OK;
 }

@@ -124,6 +124,7 @@ struct Job {
     const uint8_t* w;           // device layout
     const uint8_t* staged;      // staged activations (kStageHeader + n_chunks * 128 bytes)
     int32_t* part;              // K-slice partial sums [kslices][padded_rows] (kslices > 1)
+    const int32_t* dsum;        // per row: sum of the five digits (t + 1) of every device byte of the row
     void* out;                  // rows values
     const float* act_scale;     // kOutF32Dev
     float post;                 // kOutF32Post
@@ -157,6 +158,8 @@ int launch_stage(const int8_t* acts, size_t cols, uint8_t* staged, hipStream_t s
 int launch_gemv(const LaunchArgs& a, uint32_t max_rows, const uint32_t* split, uint32_t n_split, int num_cus,
                 hipStream_t stream);
 int launch_device_layout(const uint8_t* planar_dev, const Geometry& g, uint8_t* dst, hipStream_t stream);
+// dsum[r] = digit sum of the device row r (every byte of the device layout, padding included).
+int launch_digit_sums(const uint8_t* w, const Geometry& g, int32_t* dsum, hipStream_t stream);
 int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
 int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
@@ -214,6 +217,7 @@ struct vx_matrix {
     uint32_t kslices, slice_chunks;  // K split of a lone GEMV on this matrix
     uint8_t* d_w;       // weights, device layout (vx_layout)
     int32_t* d_part;    // K-slice partial sums of a lone GEMV
+    int32_t* d_dsum;    // per padded row: digit sum of the device row (the signed low-nibble correction)
     uint8_t* d_staged;  // activation staging of the calls that take raw int8 activations
     int8_t* d_io;       // host-API staging: cols bytes of activations + padded_rows * 4 bytes of output
     std::mutex mu;      // serialises the host-pointer API on this handle
