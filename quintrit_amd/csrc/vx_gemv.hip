@@ -3,23 +3,28 @@
 // Arithmetic. A velurex byte B = d0 + 3 d1 + 9 d2 + 28 d3 + 84 d4 holds five digits d = t + 1 in {0, 1, 2}
 // (docs/velurex-encoding.md section 1; quintrit-core/src/pack.rs:28-58). The activations are split as x = 16 hi + lo with
 // lo = x & 15 in [0, 15] and hi = x >> 4 in [-8, 7] (the 16 hi + lo split of quintrit-core/src/lut.rs:380-388, with
-// lo taken unsigned so that both halves are 4-bit operands). Then
-//     sum_p t_p x_p = sum_p d_p lo_p + 16 sum_p d_p hi_p - sum_p x_p,
-// and both digit sums are one dot product each of five 4-bit lanes: v_dot8_u32_u4 (digits x lo) and v_dot8_i32_i4
-// (digits x hi). The last term is the sum of the activations, subtracted once per row. Everything is exact in int32 for
+// lo taken unsigned so that both halves are 4-bit operands), and lo is staged as the signed nibble lo - 8. Then
+//     sum_p t_p x_p = sum_p d_p (lo_p - 8) + 16 sum_p d_p hi_p + 8 sum_p d_p - sum_p x_p,
+// and both digit sums are one signed dot product each of five 4-bit lanes (v_dot8c_i32_i4). The row's digit sum
+// sum_p d_p is computed once per matrix and the activation sum once per staged vector. Everything is exact in int32 for
 // cols <= 131072 (|sum| < 2^24, quintrit-core/src/limits.rs:7-19).
 //
 // Decode. The digit nibbles of every byte come from a 256-entry table in LDS (one dword per byte: d0..d4 in nibbles
-// 0..4; bytes that are not velurex values map to five zero trits, like BYTE_TO_TRITS). The table is replicated 64
-// times, entry B of copy k at dword B * 64 + k, and lane l reads copy l, so the lookup hits 64 distinct banks whatever
-// the bytes are; its address (B << 8) | (l << 2) is one v_perm_b32. Per weight byte the inner loop is one v_perm, one
+// 0..4; bytes that are not velurex values map to five zero trits, like BYTE_TO_TRITS). The table is replicated 32
+// times in the first half of a 256-byte LDS row per entry (copy k of entry B at byte B * 256 + 4k) and lane l reads
+// copy l % 32: LDS serves a wave in two halves of 32 lanes, so the gather hits 32 distinct banks whatever the bytes
+// are, and its address (B << 8) | ((l % 32) << 2) is one v_perm_b32. Per weight byte the inner loop is one v_perm, one
 // ds_read_b32 and two dot products.
 //
 // Work split. The device layout (vx_layout) stores rows in tiles of 64 (lane = row) and interleaves 16-byte chunks of
 // 16 consecutive tiles, so one workgroup of 16 waves that processes a tile group reads 16 consecutive KiB per chunk step:
 // the whole GPU sweeps memory nearly in address order. A work item is (tile group, K slice); the activations of the
 // slice are staged in LDS once per item and read back as wave-uniform values. Long rows are split into K slices whose
-// partial sums are written with plain stores and added by a second kernel, so no workgroup ever waits for another.
+// partial sums are written to a workspace and added by a second kernel, so no workgroup ever waits for another.
+//
+// Output. Writes that reach HBM while the weight stream is running cost far more than their bytes (a few MB of scattered
+// stores slow a 2 GB read stream by several percent), so a workgroup keeps the results of up to kSlots items in the
+// free second halves of the table rows and writes them out, non-temporally, when the slots are full and at its end.
 //
 // Reference path: quintrit-core/src/simd/avx512.rs:1526-1626 (production CPU kernel: table decode, exact int8/int16/
 // int32 sums) and quintrit-runtime/src/layer.rs:210-254 (the fp32 epilogue out = float(acc) * (ws / as)).
@@ -169,10 +174,14 @@ __device__ __forceinline__ float job_post(const Job& jb, bool* zero) {
     return *zero ? 0.0f : jb.weight_scale / as;
 }
 
+__device__ __forceinline__ float out_value(const Job& jb, int acc, float post, bool zero) {
+    return zero ? 0.0f : static_cast<float>(acc) * post;
+}
+
 __device__ __forceinline__ void store_out(const Job& jb, uint32_t row, int acc, float post, bool zero) {
     if (row >= jb.rows) return;
-    if (jb.out_kind == kOutI32) static_cast<int32_t*>(jb.out)[row] = acc;
-    else static_cast<float*>(jb.out)[row] = zero ? 0.0f : static_cast<float>(acc) * post;
+    if (jb.out_kind == kOutI32) __builtin_nontemporal_store(acc, static_cast<int32_t*>(jb.out) + row);
+    else __builtin_nontemporal_store(out_value(jb, acc, post, zero), static_cast<float*>(jb.out) + row);
 }
 
 __device__ __forceinline__ int staged_sum(const Job& jb) { return *(const c_int*)(jb.staged); }
@@ -207,23 +216,60 @@ __device__ __forceinline__ void dot4_bcast(int& lo, int& hi, uint32_t L, uint32_
 
 constexpr int kWaves = 16;   // waves per workgroup = tiles per group
 constexpr int kGroup = 4;    // chunks loaded together by a wave
+constexpr int kSlots = 8;    // items whose results a workgroup holds in LDS (1024 rows each: 32 of the 128-byte holes)
 
-// Two workgroups per CU (64 KiB table + 11 KiB activations each), 8 waves per SIMD: at most 64 VGPRs.
+// Where the results of a held item go: kOutI32/kOutF32* rows of `out` or one K slice of `part`, 4 bytes per row.
+struct Held {
+    void* dst;       // first row of the item's tile group
+    uint32_t count;  // rows to write (the tile group, clipped to the matrix)
+    uint32_t pad;
+};
+
+// LDS byte offset of row r (0..1023) of held slot s: the second half of table row s * 32 + r / 32.
+__device__ __forceinline__ uint32_t held_offset(uint32_t s, uint32_t r) {
+    return ((s * 32u + (r >> 5)) << 8) + 128u + ((r & 31u) << 2);
+}
+
+typedef __attribute__((address_space(3))) const u32x4 l_u4;
+
+// Writes the n held items that precede ring position `end` (slots (end - n) % kSlots ... (end - 1) % kSlots). A unit of
+// work is 256 rows of one item (one 16-byte load from LDS and one 16-byte store per lane); wave w takes units w, w + 16.
+__device__ __forceinline__ void flush_held(const char* lds, const Held* held, uint32_t end, uint32_t n, uint32_t wave,
+                                           uint32_t lane) {
+    for (uint32_t u = wave; u < n * 4u; u += kWaves) {
+        const uint32_t s = (end - n + u / 4u) % kSlots;
+        const uint32_t r = (u % 4u) * 256u + lane * 4u;
+        const Held h = held[s];
+        const u32x4 v = *reinterpret_cast<l_u4*>(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)) + held_offset(s, r));
+        uint32_t* d = static_cast<uint32_t*>(h.dst) + r;
+        if (r + 3u < h.count && (reinterpret_cast<uintptr_t>(h.dst) & 15u) == 0) {
+            __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(d));
+        } else {
+            if (r < h.count) __builtin_nontemporal_store(v.x, d);
+            if (r + 1u < h.count) __builtin_nontemporal_store(v.y, d + 1);
+            if (r + 2u < h.count) __builtin_nontemporal_store(v.z, d + 2);
+            if (r + 3u < h.count) __builtin_nontemporal_store(v.w, d + 3);
+        }
+    }
+}
+
+// Two workgroups per CU (64 KiB table and held results + 11 KiB activations each), 8 waves per SIMD: at most 64 VGPRs.
 // MANY: the jobs are a device array (a plan); otherwise the one job travels in the kernel arguments.
 template <bool MANY>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 8))) void gemv_kernel(LaunchArgs args) {
-    __shared__ uint32_t tab[256 * 64];
+    __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of entry B, then 128 bytes of held results
     __shared__ uint4 acts[2][(kMaxSliceChunks + kGroup) * 8];
+    __shared__ Held held[kSlots];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const char* tabb = reinterpret_cast<const char*>(tab);
-    const uint32_t lane_off = lane * 4u;
+    const uint32_t lane_off = (lane & 31u) * 4u;
     const c_job* cj = (const c_job*)(args.jobs);
 
     uint32_t j = 0, buf = 0;
-    bool first = true;
+    uint32_t done = 0, pending = 0;  // items this workgroup has finished / of those, held in LDS
     for (uint32_t item = blockIdx.x; item < args.total_items; item += gridDim.x, buf ^= 1u) {
         if (MANY)
             while (j + 1 < args.n_jobs && item >= cj[j + 1].item_begin) ++j;
@@ -248,18 +294,36 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
 #pragma unroll
             for (int i = 0; i < kGroup; ++i) b[i] = __builtin_nontemporal_load(wp + min(static_cast<uint32_t>(i), nq - 1u) * cs);
         }
-        if (first) {
-            for (uint32_t i = tid; i < 256u * 16u; i += kWaves * 64u) {  // 16 uint4 stores per entry
-                const uint32_t e = digit_nibbles(i >> 4);
-                reinterpret_cast<uint4*>(tab)[i] = make_uint4(e, e, e, e);
+        if (done == 0) {
+            for (uint32_t i = tid; i < 256u * 8u; i += kWaves * 64u) {  // 8 uint4 stores per entry
+                const uint32_t e = digit_nibbles(i >> 3);
+                *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
             }
-            first = false;
         }
         // Stage this slice's activations (zero past nq, so the clamped tail loads add nothing).
         const uint4* src = reinterpret_cast<const uint4*>(jb.staged + kStageHeader) + static_cast<size_t>(q0) * 8u;
         uint4* ab = acts[buf];
         for (uint32_t i = tid; i < nqp * 8u; i += kWaves * 64u) ab[i] = i < nq * 8u ? src[i] : make_uint4(0, 0, 0, 0);
+        const uint32_t slot = done % kSlots;
+        if (tid == 0) {
+            const size_t first = static_cast<size_t>(grp) * kTileGroup * kTileRows;
+            Held h;
+            if (jb.kslices == 1) {
+                h.dst = static_cast<uint32_t*>(jb.out) + first;
+                h.count = static_cast<uint32_t>(min(static_cast<size_t>(kTileGroup * kTileRows), jb.rows - first));
+            } else {
+                h.dst = jb.part + static_cast<size_t>(ks) * jb.padded_rows + first;
+                h.count = static_cast<uint32_t>(min(static_cast<size_t>(kTileGroup * kTileRows), jb.padded_rows - first));
+            }
+            h.pad = 0;
+            held[slot] = h;
+        }
         __syncthreads();
+        // Every slot but this item's is full: write them out (their results and descriptors precede the barrier).
+        if (pending == kSlots - 1) {
+            flush_held(tabb, held, done, pending, wave, lane);
+            pending = 0;
+        }
 
         if (active) {
             int acc_lo = 0, acc_hi = 0;
@@ -288,16 +352,26 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
                 }
             }
             const int v = acc_lo + 16 * acc_hi;
-            const uint32_t row = (grp * kTileGroup + wave) * kTileRows + lane;
-            if (jb.kslices == 1) {
-                bool zero;
-                const float post = job_post(jb, &zero);
-                store_out(jb, row, row_result(jb, row, v), post, zero);
-            } else {
-                jb.part[static_cast<size_t>(ks) * jb.padded_rows + row] = v;
+            const uint32_t r = wave * kTileRows + lane;  // row within the tile group
+            const uint32_t row = grp * kTileGroup * kTileRows + r;
+            uint32_t word = static_cast<uint32_t>(v);
+            if (jb.kslices == 1 && row < jb.rows) {
+                const int acc = row_result(jb, row, v);
+                if (jb.out_kind == kOutI32) {
+                    word = static_cast<uint32_t>(acc);
+                } else {
+                    bool zero;
+                    const float post = job_post(jb, &zero);
+                    word = __float_as_uint(out_value(jb, acc, post, zero));
+                }
             }
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(tab) + held_offset(slot, r)) = word;
         }
+        ++done;
+        ++pending;
     }
+    __syncthreads();
+    flush_held(tabb, held, done, pending, wave, lane);
 }
 
 // Adds the K-slice partial sums of the split jobs and applies their epilogue. Block = 64 rows x 4 waves; wave w adds
