@@ -33,7 +33,7 @@ LAYER_SHAPES = [("qkv", HIDDEN + 2 * KV, HIDDEN), ("o", HIDDEN, HIDDEN), ("gate_
 REF_CPU_GWEIGHTS = 221.6  # quintrit_512, 4 threads, EPYC 9V45 (docs/benchmarks.md:77)
 # HBM bytes of one full-step gemv_kernel launch, from rocprofv3 FETCH_SIZE and WRITE_SIZE scaled by a plain-copy
 # calibration (profiles/gemv_kernel_falcon3_projection_stream.md). Only valid for the default 40-layer workload.
-TRAFFIC_BYTES_PER_STEP = 1_893_508 * 1024
+TRAFFIC_BYTES_PER_STEP = 1_902_252 * 1024
 
 
 def parse():
