@@ -1,4 +1,18 @@
-/* decode_oracle.h - CPU restatement of the reference's decode step (test infrastructure only; see decode_oracle.c). */
+/* decode_oracle.h - CPU restatement of the reference's decode step (test infrastructure only; see decode_oracle.c).
+ *
+ * How each function is pinned (tests/test_oracle_decode.py; nothing here is checked only against itself):
+ *   vxo_ggml_dot_f16   bit for bit against the reference test's dot_f16_model (quintrit-runtime/src/ops.rs:2008-2060)
+ *   vxo_ggml_dot_bf16  bit for bit against the reference's portable ggml_vec_dot_bf16_scalar (ops.rs:686-713)
+ *   vxo_vec_mad_f16, vxo_vec_scale_f16  element by element against the rounding the reference's AVX2 code performs
+ *   vxo_f32_to_bf16, vxo_bf16_to_f32, f16 conversions  against torch / numpy round-to-nearest-even
+ *   vxo_rope_cache     position 0 is exact; the theta recurrence in f32; cos/sin within 2 ulps of float64
+ *   vxo_rope_neox      exact one-hot rotations (pairing, signs) and float64 closeness
+ *   vxo_attend_head    float64 softmax attention, single and 4-chunk paths (FP16 accumulator tolerance)
+ *   vxo_model_forward  a float64 model written from model.rs / attention.rs (logits within 6 % of the largest; the
+ *                      structural mistakes tried land at 57-190 %), plus a negative control
+ *   quantizer, RMSNorm (velurex_oracle.c)  the reference's known answers (ops.rs:1968-1991); the reference text
+ * Only the bits of libm-dependent values (expf, cosf, sinf, powf) rest on the host glibc being the reference's libm:
+ * the reference computes them with Rust's f32 methods, which call the same C library on Linux. */
 #ifndef DECODE_ORACLE_H
 #define DECODE_ORACLE_H
 

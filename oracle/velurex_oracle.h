@@ -7,7 +7,8 @@
  *
  * Every function names the reference file:line it restates (paths relative to the reference repository root,
  * rust/crates/...). Where a function is pinned by a check that does not retype its formula (brute force, closed
- * form, round trip, reference test vector), the test that pins it is named in tests/test_oracle.py.
+ * form, round trip, reference test vector), the test that pins it is named in tests/test_oracle.py (encoding, GEMV,
+ * Q2_0) or tests/test_oracle_decode.py (quantizer known answers, RMSNorm).
  *
  * Conventions: trits are int8 values in {-1, 0, +1}; activations are int8 over the full range; sizes are size_t;
  * integer GEMV results are exact (int32 or int64).
