@@ -1,5 +1,5 @@
 // Batched ternary GEMM for gfx950 (MI355X): Y[m][i] = sum_j W[i][j] X[m][j] for M tokens, exact int32, on the matrix
-// cores (v_mfma_i32_16x16x64_i8).
+// cores (v_mfma_i32_32x32x32_i8).
 //
 // The reference has no multi-token kernel: its prefill runs one GEMV per token (quintrit-runtime/src/engine.rs:625-631),
 // so the definition is M independent GEMVs (quintrit-core/src/simd/avx512.rs:1526-1626), and the result must equal
@@ -7,14 +7,22 @@
 // decoded to int8 trits in registers right before the matrix-core instruction; activations are staged once per call
 // in the order of the MFMA B operand.
 //
-// K order. A 16-byte chunk of a weight row holds 16 byte-columns x 5 planes = 80 trits. Four chunks (64 byte-columns,
-// 320 trits) make one K step of five 64-deep MFMA blocks: block kb < 4 holds planes 0..3 of chunk kb, block 4 holds
-// plane 4 of the four chunks. In block kb < 4, lane (i, s) (i = lane % 16 the row, s = lane / 16) supplies the 4 x 4
-// trits of bytes 4s .. 4s+3 of its row's chunk: one 32-bit word of weights, decoded by four lookups of a 256-entry
-// table (t0..t3 as int8). In block 4 the lane supplies plane 4 of the same word in each of the four chunks; d4 (the
-// digit, t4 + 1) comes from two byte-wise compares done four bytes at a time (B >= 84, B >= 168), and the missing
+// MFMA operands (v_mfma_i32_32x32x32_i8): lane l supplies 16 int8 of row l % 32 of A (a weight row) and of column
+// l % 32 of B (a token); lanes l and l + 32 hold the two halves of the 32-deep K block, and C register r of lane l is
+// row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32. Any order of K works as long as A and B use the same one.
+//
+// K order. A K step is two 16-byte chunks of a weight row: 32 byte-columns x 5 planes = 160 trits = five 32-deep MFMA
+// blocks. Lane (i, s) (i = row in the 32-row block, s = lane / 32) holds chunk 2 ks + s of its row in one 16-byte load.
+// Block m < 4 takes dword m of that chunk: bytes 4m .. 4m+3, planes 0..3 (t0..t3 as int8, one LDS table lookup per
+// byte). Block 4 takes plane 4 of all 16 bytes: d4 = t4 + 1 from byte-wise compares (B >= 84, B >= 168), and the missing
 // "- 1" is subtracted once per token as the sum of that token's plane-4 activations. The activation staging writes X
 // in exactly this order, so A and B pair every weight with its activation.
+//
+// Work split. A wave computes 64 weight rows (two 32-row blocks, one tile of the device layout) x T groups of 32
+// tokens over a range of K steps; the A fragments of a K step are decoded once and used for all T token groups. A
+// workgroup of 8 waves takes 8 consecutive tiles with the same tokens and K range, so the B fragments of a K step are
+// staged once per workgroup in LDS (double-buffered, the next step's loaded while this one is multiplied). Long K is
+// split into slices whose int32 partial sums a second kernel adds; the host picks T and the number of slices.
 #include "vx_internal.h"
 
 #include <algorithm>
@@ -22,7 +30,9 @@
 namespace vx {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(4))) const uint32_t c_u32;
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4g __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4g g_u4g;
 
 // t0..t3 of byte B as int8 in a dword; non-values give zero trits (pack.rs:41-58).
 __device__ inline uint32_t trits03(uint32_t b) {
@@ -38,6 +48,10 @@ __device__ __forceinline__ uint32_t d4_bytes(uint32_t w) {
     return (((x + 0x56565656u) >> 7) & 0x01010101u) + (((x + 0x2c2c2c2cu) >> 7) & 0x01010101u);
 }
 
+constexpr uint32_t kStepChunks = 2;  // 16-byte chunks per K step
+constexpr int kGemmWaves = 8;        // waves (= 64-row tiles) per workgroup
+constexpr uint32_t kZeroWord = 0x7d7d7d7du;  // four bytes of five zero trits
+
 // ---- activation staging --------------------------------------------------------------------------------------------
 
 // Activation p of device byte-column c of token m (column_activation_index, pack.rs:230-237), 0 outside.
@@ -49,49 +63,64 @@ __device__ inline int act_at(const int8_t* __restrict__ x, uint32_t ldx, uint32_
     return idx < cols ? x[static_cast<size_t>(m) * ldx + idx] : 0;
 }
 
-// One thread per 16-byte B fragment: xs[kstep][kb][tg][lane] (see the K order above).
-__global__ void gemm_stage_kernel(const int8_t* __restrict__ x, uint32_t ldx, uint32_t M, uint32_t n_tg, uint32_t cols,
-                                  uint32_t tbr, uint32_t n_ksteps, uint4* __restrict__ xs) {
-    const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const uint64_t total = static_cast<uint64_t>(n_ksteps) * 5u * n_tg * 64u;
-    if (idx >= total) return;
-    const uint32_t lane = static_cast<uint32_t>(idx & 63u);
-    uint64_t r = idx >> 6;
-    const uint32_t tg = static_cast<uint32_t>(r % n_tg);
-    r /= n_tg;
-    const uint32_t kb = static_cast<uint32_t>(r % 5u);
-    const uint32_t ks = static_cast<uint32_t>(r / 5u);
-    const uint32_t m = tg * 16u + (lane & 15u), s = lane >> 4;
-    uint32_t w[4];
-    for (uint32_t d = 0; d < 4; ++d) {
-        uint32_t v = 0;
-        for (uint32_t e = 0; e < 4; ++e) {
-            uint32_t c, p;
-            if (kb < 4) {  // dword d = byte-column 4s + d of chunk kb, bytes = planes 0..3
-                c = (4u * ks + kb) * 16u + 4u * s + d;
-                p = e;
-            } else {       // dword d = chunk d, byte e = byte-column 4s + e, plane 4
-                c = (4u * ks + d) * 16u + 4u * s + e;
-                p = 4;
-            }
-            v |= (static_cast<uint32_t>(act_at(x, ldx, m, M, cols, tbr, c, p)) & 0xffu) << (8 * e);
-        }
-        w[d] = v;
-    }
-    xs[idx] = make_uint4(w[0], w[1], w[2], w[3]);
-}
+// One workgroup per (token m, slice kx of 64 K steps): the token's activations for those steps are read once, with 16-byte loads,
+// into LDS; each thread then writes 16-byte B fragments xs[ks][kb][tg][lane] (tg = m / 32, lane = (m % 32) + 32 s for
+// chunk 2 ks + s), gathering the five planes of each device byte-column (column_activation_index, pack.rs:230-237).
+// The workgroup also writes s4p[kx][m], its part of the sum of the token's plane-4 activations (the
+// correction for d4 = t4 + 1); the GEMM adds the parts.
+constexpr uint32_t kStageSteps = 64;                               // K steps per staging workgroup
+constexpr uint32_t kStageCols = kStageSteps * kStepChunks * 16;    // device byte-columns per staging workgroup
 
-// s4[m] = sum over byte-columns of activation plane 4 (the correction for using d4 = t4 + 1). One block per token.
-__global__ __launch_bounds__(256) void gemm_s4_kernel(const int8_t* __restrict__ x, uint32_t ldx, uint32_t M,
-                                                       uint32_t cols, uint32_t tbr, int* __restrict__ s4) {
+__global__ __launch_bounds__(256) void gemm_stage_kernel(const int8_t* __restrict__ x, uint32_t ldx, uint32_t n_tg,
+                                                         uint32_t cols, uint32_t tbr, uint32_t n_ksteps,
+                                                         uint4* __restrict__ xs, int* __restrict__ s4p, uint32_t M) {
+    __shared__ uint32_t raw[kStageCols * 5 / 4 + 64];  // the token's activations of this slice (5 per byte-column)
     __shared__ int red[4];
-    const uint32_t m = blockIdx.x;
-    int s = 0;
-    for (uint32_t c = threadIdx.x; c < tbr; c += 256u) s += act_at(x, ldx, m, M, cols, tbr, c, 4);
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = s;
+    const uint32_t m = blockIdx.x, kx = blockIdx.y, tid = threadIdx.x;
+    const uint32_t ks0 = kx * kStageSteps, ks1 = min(ks0 + kStageSteps, n_ksteps);
+    const uint32_t c0 = ks0 * kStepChunks * 16u;             // first byte-column; a multiple of 2048, so of 32
+    const uint32_t full = cols / 160u * 32u;                 // byte-columns of whole 160-trit blocks
+    // Activation index of byte-column c0 is 5 c0 (c0 is a multiple of 32 and c0 <= full, or past it in the tail,
+    // where the tail columns hold 5 consecutive activations each): the slice is the contiguous range
+    // [5 c0, 5 (c0 + ncols)) of the token's row, padded with zeros past cols.
+    const uint32_t a0 = 5u * c0;
+    const uint32_t nb = 5u * kStageCols;                      // bytes of the slice
+    const int8_t* xr = x + static_cast<size_t>(m) * ldx;
+    const bool vec = (reinterpret_cast<uintptr_t>(xr) & 15u) == 0;
+    uint8_t* rb = reinterpret_cast<uint8_t*>(raw);
+    for (uint32_t i = tid * 16u; i < nb; i += 256u * 16u) {
+        const uint32_t g = a0 + i;
+        if (vec && g + 16u <= cols) {
+            *reinterpret_cast<uint4*>(rb + i) = *reinterpret_cast<const uint4*>(xr + g);
+        } else {
+            for (uint32_t k = 0; k < 16; ++k) rb[i + k] = g + k < cols ? static_cast<uint8_t>(xr[g + k]) : 0u;
+        }
+    }
     __syncthreads();
-    if (threadIdx.x == 0) s4[m] = red[0] + red[1] + red[2] + red[3];
+    // byte-column c (absolute) -> position of activation p in raw
+    auto at = [&](uint32_t c, uint32_t p) -> uint32_t {
+        if (c >= tbr) return 0u;
+        const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
+        return idx < cols ? rb[idx - a0] : 0u;
+    };
+    int s = 0;
+    for (uint32_t c = c0 + tid; c < c0 + (ks1 - ks0) * kStepChunks * 16u; c += 256u) s += static_cast<int8_t>(at(c, 4));
+    const uint32_t tg = m / 32u, lane0 = m % 32u;
+    for (uint32_t i = tid; i < (ks1 - ks0) * 10u; i += 256u) {
+        const uint32_t ks = ks0 + i / 10u, kb = (i % 10u) / 2u, hs = i % 2u;
+        const uint32_t cb = (ks * kStepChunks + hs) * 16u;  // first byte-column of the chunk
+        uint32_t w[4];
+        for (uint32_t d = 0; d < 4; ++d) {
+            uint32_t v = 0;
+            for (uint32_t e = 0; e < 4; ++e) v |= (kb < 4 ? at(cb + 4u * kb + d, e) : at(cb + 4u * d + e, 4)) << (8 * e);
+            w[d] = v;
+        }
+        xs[(static_cast<size_t>(ks * 5u + kb) * n_tg + tg) * 64u + lane0 + 32u * hs] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if ((tid & 63u) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    if (tid == 0) s4p[static_cast<size_t>(kx) * M + m] = red[0] + red[1] + red[2] + red[3];
 }
 
 // ---- GEMM -------------------------------------------------------------------------------------------------------------
@@ -99,127 +128,167 @@ __global__ __launch_bounds__(256) void gemm_s4_kernel(const int8_t* __restrict__
 struct GemmArgs {
     const uint8_t* w;      // device layout
     const uint4* xs;       // staged activations
-    const int* s4;         // per-token plane-4 sums
+    const int* s4p;        // per staging workgroup and token: parts of the plane-4 sums, s4p[kx * M + m]
     int32_t* y;            // M x ldy (kslices == 1)
-    int32_t* part;         // kslices x Mp x rows_p partial sums (kslices > 1)
+    int32_t* part;         // kslices x (n_tg * 32) x rows_p partial sums (kslices > 1)
     uint32_t rows, n_tiles, n_chunks, n_ksteps;
-    uint32_t M, n_tg, ldy;
-    uint32_t kslices, ksteps_per_slice, rows_p;
+    uint32_t M, n_tg, ldy, y_vec4;   // y_vec4: y and ldy allow 16-byte stores
+    uint32_t kslices, ksteps_per_slice, rows_p, s4_parts;
 };
 
-constexpr int kGemmWaves = 4;   // one 64-row tile per wave
-constexpr int kGemmTg = 4;      // 16-token groups per workgroup
+__device__ __forceinline__ int plane4_sum(const GemmArgs& a, uint32_t m) {
+    int s = 0;
+    for (uint32_t k = 0; k < a.s4_parts; ++k) s += a.s4p[static_cast<size_t>(k) * a.M + m];
+    return s;
+}
 
+// Workgroup (rg, tt, kz): tiles 8 rg .. 8 rg + 7, token groups T tt .. T tt + T - 1, K steps of slice kz. LDS: the
+// trit table (32 copies of each entry in the first half of a 256-byte row; lane l reads copy l % 32, conflict-free
+// because LDS serves a wave in two 32-lane halves) and two buffers of one K step's B fragments.
+template <int T>
 __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
     __shared__ uint32_t tab[256 * 64];
-    __shared__ uint4 bsm[2][5 * kGemmTg * 64];
+    __shared__ uint4 bs[2][5 * T * 64];
+    constexpr uint32_t kB = 5u * T * 64u;                             // B fragments of a K step
+    constexpr uint32_t kBPer = (kB + kGemmWaves * 64u - 1) / (kGemmWaves * 64u);  // per thread
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t tile = blockIdx.x * kGemmWaves + wave;
-    const uint32_t tg0 = blockIdx.y * kGemmTg;
-    const uint32_t ntg = min(static_cast<uint32_t>(kGemmTg), a.n_tg - tg0);
-    const uint32_t kz = blockIdx.z;
+    const uint32_t tt = blockIdx.y, kz = blockIdx.z;
     const uint32_t ks0 = kz * a.ksteps_per_slice;
     const uint32_t ks1 = min(ks0 + a.ksteps_per_slice, a.n_ksteps);
+    const bool active = tile < a.n_tiles;
 
-    for (uint32_t i = tid; i < 256u * 16u; i += kGemmWaves * 64u) {
-        const uint32_t e = trits03(i >> 4);
-        reinterpret_cast<uint4*>(tab)[i] = make_uint4(e, e, e, e);
+    for (uint32_t i = tid; i < 256u * 8u; i += kGemmWaves * 64u) {
+        const uint32_t e = trits03(i >> 3);
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
     }
     const char* tabb = reinterpret_cast<const char*>(tab);
-    const uint32_t lane_off = lane * 4u;
-    const bool active = tile < a.n_tiles;
-    // Base of this wave's tile in the device layout, and the byte of lane (i, s) inside a chunk.
-    const uint32_t grp = tile / kTileGroup, tt = tile - grp * kTileGroup;
-    const uint32_t T = active ? min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup) : 1u;
-    const uint8_t* wbase = a.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + tt) * 1024u + (lane & 15u) * 16u + (lane >> 4) * 4u;
+    const uint32_t lane_off = (lane & 31u) * 4u;
 
-    v4i acc[4][kGemmTg];
-#pragma unroll
-    for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-        for (int g = 0; g < kGemmTg; ++g) acc[rb][g] = v4i{0, 0, 0, 0};
+    // This lane's row (i = lane % 32 of each 32-row block) in the device layout: tile t of group grp, row 16 bytes. A
+    // wave past the last tile reads the last tile (and stores nothing), so every load has a valid address and none
+    // sits behind a branch (the compiler would then wait for all loads before the next use).
+    const uint32_t ltile = min(tile, a.n_tiles - 1u);
+    const uint32_t grp = ltile / kTileGroup, tt16 = ltile - grp * kTileGroup;
+    const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup);
+    const uint8_t* wbase = a.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + tt16) * 1024u + (lane & 31u) * 16u;
+    const uint32_t half = lane >> 5;
 
-    // weights of one K step: 4 row blocks x 4 chunks, one 32-bit word each (byte 125 = zero trits past the row)
-    auto load_w = [&](uint32_t (&wv)[4][4], uint32_t ks) {
+    // Chunk 2 ks + s of the lane's rows; a chunk past the row (odd n_chunks) reads the last one and is replaced by
+    // zero trits when it is decoded.
+    auto load_w = [&](uint32_t ks, u32x4g (&wv)[2]) {
+        const uint32_t q = min(ks * kStepChunks + half, a.n_chunks - 1u);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t chunk = 4u * ks + q;
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-                wv[rb][q] = chunk < a.n_chunks
-                                ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(
-                                      wbase + (static_cast<size_t>(chunk) * T) * 1024u + rb * 256u))
-                                : 0x7d7d7d7du;
-        }
+        for (int rb = 0; rb < 2; ++rb)
+            wv[rb] = __builtin_nontemporal_load((g_u4g*)(wbase + static_cast<size_t>(q) * Tg * 1024u + rb * 512u));
     };
-    uint32_t wv[4][4], wn[4][4];
-    if (active && ks0 < ks1) load_w(wv, ks0);
-    uint32_t buf = 0;
-    for (uint32_t ks = ks0; ks < ks1; ++ks, buf ^= 1u) {
-        if (active && ks + 1 < ks1) load_w(wn, ks + 1);  // next step's weights stream in during this step's MFMAs
-        // stage the B fragments of this K step
-        const uint4* src = a.xs + static_cast<size_t>(ks) * 5u * a.n_tg * 64u;
-        uint4* dst = bsm[buf];
-        for (uint32_t i = tid; i < 5u * ntg * 64u; i += kGemmWaves * 64u) {
-            const uint32_t kb = i / (ntg * 64u), rem = i - kb * ntg * 64u;
-            dst[kb * kGemmTg * 64u + rem] = src[(static_cast<size_t>(kb) * a.n_tg + tg0) * 64u + rem];
-        }
-        __syncthreads();
+    // B fragments of step ks (kBPer <= 3 per thread, kept in named registers: an array here would be moved to
+    // scratch LDS and waited for at once); slots past the token groups read a valid fragment that no stored output
+    // depends on (only C columns of tokens >= M).
+    auto b_index = [&](uint32_t ks, uint32_t k) -> size_t {
+        const uint32_t idx = min(tid + k * kGemmWaves * 64u, kB - 1u);
+        const uint32_t kb = idx / (T * 64u), rem = idx - kb * T * 64u;
+        const uint32_t tg = min(tt * T + rem / 64u, a.n_tg - 1u);
+        return (static_cast<size_t>(ks * 5u + kb) * a.n_tg + tg) * 64u + (rem & 63u);
+    };
+    uint4 bv0, bv1, bv2;
+    auto load_b = [&](uint32_t ks) {
+        bv0 = a.xs[b_index(ks, 0)];
+        if (kBPer > 1) bv1 = a.xs[b_index(ks, 1)];
+        if (kBPer > 2) bv2 = a.xs[b_index(ks, 2)];
+    };
+    auto store_b = [&](uint32_t buf) {
+        if (tid < kB) bs[buf][tid] = bv0;
+        if (kBPer > 1 && tid + kGemmWaves * 64u < kB) bs[buf][tid + kGemmWaves * 64u] = bv1;
+        if (kBPer > 2 && tid + 2u * kGemmWaves * 64u < kB) bs[buf][tid + 2u * kGemmWaves * 64u] = bv2;
+    };
+
+    v16i acc[2][T];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int g = 0; g < T; ++g) acc[rb][g] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+    // One K step ahead: the loads of step ks + 1 (B first, then weights) go out before step ks is multiplied. Every
+    // load is unconditional (the index is clamped at the last step), so the compiler's waits stay exact: the multiply
+    // waits only for step ks's weights, the LDS store at the end of the step only for the B fragments.
+    u32x4g wc[2], wn[2];
+    if (ks0 < ks1) {
+        load_b(ks0);
+        load_w(ks0, wc);
+        store_b(0);
+    }
+    for (uint32_t ks = ks0; ks < ks1; ++ks) {
+        const uint32_t cur = (ks - ks0) & 1u;
+        const uint32_t kn = min(ks + 1, ks1 - 1);
+        load_b(kn);
+        load_w(kn, wn);
+        __syncthreads();  // bs[cur] is complete; every wave is done with bs[cur ^ 1]
         if (active) {
+            const bool inside = ks * kStepChunks + half < a.n_chunks;
+            v4i A[2][5];
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) {
-                v4i A[5];
+            for (int rb = 0; rb < 2; ++rb) {
+                const uint32_t dw[4] = {inside ? wc[rb].x : kZeroWord, inside ? wc[rb].y : kZeroWord,
+                                        inside ? wc[rb].z : kZeroWord, inside ? wc[rb].w : kZeroWord};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t w = wv[rb][q];
+                for (int m = 0; m < 4; ++m) {
                     int t[4];
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
-                        const uint32_t addr = __builtin_amdgcn_perm(w, lane_off, 0x0c0c0000u | ((4u + b) << 8));
+                        const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + b) << 8));
                         t[b] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
                     }
-                    A[q] = v4i{t[0], t[1], t[2], t[3]};
+                    A[rb][m] = v4i{t[0], t[1], t[2], t[3]};
                 }
-                A[4] = v4i{static_cast<int>(d4_bytes(wv[rb][0])), static_cast<int>(d4_bytes(wv[rb][1])),
-                           static_cast<int>(d4_bytes(wv[rb][2])), static_cast<int>(d4_bytes(wv[rb][3]))};
+                A[rb][4] = v4i{static_cast<int>(d4_bytes(dw[0])), static_cast<int>(d4_bytes(dw[1])),
+                               static_cast<int>(d4_bytes(dw[2])), static_cast<int>(d4_bytes(dw[3]))};
+            }
+            // K block outer, token group inner: 2 T independent accumulators between two MFMAs on the same one.
 #pragma unroll
-                for (int g = 0; g < kGemmTg; ++g) {
-                    if (static_cast<uint32_t>(g) < ntg) {
+            for (int kb = 0; kb < 5; ++kb) {
 #pragma unroll
-                        for (int kb = 0; kb < 5; ++kb) {
-                            const uint4 bv = bsm[buf][(kb * kGemmTg + g) * 64u + lane];
-                            const v4i B = v4i{static_cast<int>(bv.x), static_cast<int>(bv.y), static_cast<int>(bv.z),
-                                              static_cast<int>(bv.w)};
-                            acc[rb][g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[kb], B, acc[rb][g], 0, 0, 0);
-                        }
-                    }
+                for (int g = 0; g < T; ++g) {
+                    const uint4 b = bs[cur][(kb * T + g) * 64u + lane];
+                    const v4i B = v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
+                    acc[0][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0][kb], B, acc[0][g], 0, 0, 0);
+                    acc[1][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1][kb], B, acc[1][g], 0, 0, 0);
                 }
             }
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) wv[rb][q] = wn[rb][q];
         }
+        store_b(cur ^ 1u);  // after the last step this writes a buffer nobody reads
+        wc[0] = wn[0];
+        wc[1] = wn[1];
     }
     if (!active) return;
-    // C fragment: lane (j, s) holds rows 4s + r of the 16-row block, token j.
-    const uint32_t j = lane & 15u, s = lane >> 4;
+    // C of block (rb, g): lane l, register r -> weight row 8 (r / 4) + 4 (l / 32) + r % 4 of the block, token l % 32.
+    const uint32_t j = lane & 31u;
 #pragma unroll
-    for (int g = 0; g < kGemmTg; ++g) {
-        if (static_cast<uint32_t>(g) >= ntg) continue;
-        const uint32_t m = (tg0 + g) * 16u + j;
+    for (int g = 0; g < T; ++g) {
+        const uint32_t m = (tt * T + g) * 32u + j;
         if (m >= a.M) continue;
-        const int corr = a.kslices == 1 ? a.s4[m] : 0;
+        const int corr = a.kslices == 1 ? plane4_sum(a, m) : 0;
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t n = tile * 64u + rb * 16u + 4u * s + r;
-                if (n >= a.rows) continue;
-                if (a.kslices == 1) a.y[static_cast<size_t>(m) * a.ldy + n] = acc[rb][g][r] - corr;
-                else a.part[(static_cast<size_t>(kz) * a.n_tg * 16u + m) * a.rows_p + n] = acc[rb][g][r];
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const uint32_t n = tile * 64u + rb * 32u + 8u * r4 + 4u * half;
+                const int v0 = acc[rb][g][4 * r4] - corr, v1 = acc[rb][g][4 * r4 + 1] - corr;
+                const int v2 = acc[rb][g][4 * r4 + 2] - corr, v3 = acc[rb][g][4 * r4 + 3] - corr;
+                if (a.kslices > 1) {
+                    *reinterpret_cast<int4*>(a.part + (static_cast<size_t>(kz) * a.n_tg * 32u + m) * a.rows_p + n) =
+                        make_int4(v0, v1, v2, v3);
+                } else if (a.y_vec4 && n + 3 < a.rows) {
+                    *reinterpret_cast<int4*>(a.y + static_cast<size_t>(m) * a.ldy + n) = make_int4(v0, v1, v2, v3);
+                } else {
+                    int32_t* yr = a.y + static_cast<size_t>(m) * a.ldy;
+                    if (n < a.rows) yr[n] = v0;
+                    if (n + 1 < a.rows) yr[n + 1] = v1;
+                    if (n + 2 < a.rows) yr[n + 2] = v2;
+                    if (n + 3 < a.rows) yr[n + 3] = v3;
+                }
             }
         }
     }
@@ -228,32 +297,61 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
 __global__ __launch_bounds__(256) void gemm_finish_kernel(GemmArgs a) {
     const uint32_t n = blockIdx.x * 256u + threadIdx.x, m = blockIdx.y;
     if (n >= a.rows) return;
-    int s = -a.s4[m];
-    for (uint32_t k = 0; k < a.kslices; ++k) s += a.part[(static_cast<size_t>(k) * a.n_tg * 16u + m) * a.rows_p + n];
-    a.y[static_cast<size_t>(m) * a.ldy + n] = s;
+    const size_t stride = static_cast<size_t>(a.n_tg) * 32u * a.rows_p;
+    const int32_t* p = a.part + static_cast<size_t>(m) * a.rows_p + n;
+    int s0 = -plane4_sum(a, m), s1 = 0, s2 = 0, s3 = 0;
+    uint32_t k = 0;
+    for (; k + 4 <= a.kslices; k += 4) {
+        s0 += p[k * stride];
+        s1 += p[(k + 1) * stride];
+        s2 += p[(k + 2) * stride];
+        s3 += p[(k + 3) * stride];
+    }
+    for (; k < a.kslices; ++k) s0 += p[k * stride];
+    a.y[static_cast<size_t>(m) * a.ldy + n] = (s0 + s1) + (s2 + s3);
 }
 
 // ---- host side ---------------------------------------------------------------------------------------------------------
 
 struct GemmPlan {
-    uint32_t n_ksteps, n_tg, kslices, ksteps_per_slice, grid_x, grid_y;
+    uint32_t n_ksteps, n_tg, T, n_tt, grid_x, kslices, ksteps_per_slice, stage_x;
     size_t xs_bytes, s4_bytes, part_bytes;
 };
 
+// T (token groups per wave) from M; then the K split that minimises an estimate of the time: rounds of workgroups
+// times K steps per workgroup times the time of a K step, plus the HBM traffic of the partial sums and their finish.
+// A K step of a wave is 10 T MFMAs (32 cycles each, two waves per SIMD), but not less than the HBM latency (the
+// weights are loaded one step ahead).
 static GemmPlan gemm_plan(const Geometry& g, size_t M, int num_cus) {
     GemmPlan p{};
-    p.n_ksteps = static_cast<uint32_t>((g.n_chunks + 3) / 4);
-    p.n_tg = static_cast<uint32_t>((M + 15) / 16);
+    p.n_ksteps = static_cast<uint32_t>((g.n_chunks + kStepChunks - 1) / kStepChunks);
+    p.n_tg = static_cast<uint32_t>((M + 31) / 32);
+    p.T = p.n_tg >= 4 ? 4u : (p.n_tg >= 2 ? 2u : 1u);
+    p.n_tt = (p.n_tg + p.T - 1) / p.T;
     p.grid_x = static_cast<uint32_t>((g.n_tiles + kGemmWaves - 1) / kGemmWaves);
-    p.grid_y = (p.n_tg + kGemmTg - 1) / kGemmTg;
-    const uint32_t blocks = p.grid_x * p.grid_y;
-    const uint32_t want = static_cast<uint32_t>(num_cus);  // one workgroup (104 KiB LDS) per CU
-    uint32_t ks = std::max<uint32_t>(1u, std::min<uint32_t>(p.n_ksteps, (want + blocks - 1) / blocks));
-    p.ksteps_per_slice = (p.n_ksteps + ks - 1) / ks;
+    const uint64_t base = static_cast<uint64_t>(p.grid_x) * p.n_tt;
+    const uint64_t slots = static_cast<uint64_t>(std::max(num_cus, 1)) * (p.T == 1 ? 2u : 1u);  // workgroups per CU (LDS)
+    const double t_step = std::max(0.29e-6 * p.T, 1.0e-6);
+    double best = 1e30;
+    uint32_t best_ks = 1;
+    for (uint32_t ks = 1; ks <= std::min<uint32_t>(p.n_ksteps, 64u); ++ks) {
+        const uint32_t per = (p.n_ksteps + ks - 1) / ks;
+        const uint32_t slices = (p.n_ksteps + per - 1) / per;
+        if (slices != ks) continue;
+        const double rounds = static_cast<double>((base * slices + slots - 1) / slots);
+        const double part = slices > 1 ? 8.0 * slices * static_cast<double>(M) * g.padded_rows / 2.5e12 + 4.0e-6 : 0.0;
+        const double t = rounds * per * t_step + part;
+        if (t < best) {
+            best = t;
+            best_ks = slices;
+        }
+    }
+    p.ksteps_per_slice = (p.n_ksteps + best_ks - 1) / best_ks;
     p.kslices = (p.n_ksteps + p.ksteps_per_slice - 1) / p.ksteps_per_slice;
     p.xs_bytes = round_up(static_cast<size_t>(p.n_ksteps) * 5u * p.n_tg * 1024u, 256);
-    p.s4_bytes = round_up(static_cast<size_t>(p.n_tg) * 16u * 4u, 256);
-    p.part_bytes = p.kslices > 1 ? static_cast<size_t>(p.kslices) * p.n_tg * 16u * g.padded_rows * 4u : 0;
+    p.stage_x = (p.n_ksteps + kStageSteps - 1) / kStageSteps;
+    p.s4_bytes = round_up(static_cast<size_t>(p.stage_x) * M * 4u, 256);
+    p.part_bytes = p.kslices > 1 ? static_cast<size_t>(p.kslices) * p.n_tg * 32u * g.padded_rows * 4u : 0;
     return p;
 }
 
@@ -266,20 +364,19 @@ int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* 
                 size_t ldy, uint8_t* ws, hipStream_t stream) {
     const GemmPlan p = gemm_plan(g, M, num_cus);
     uint4* xs = reinterpret_cast<uint4*>(ws);
-    int* s4 = reinterpret_cast<int*>(ws + p.xs_bytes);
+    int* s4p = reinterpret_cast<int*>(ws + p.xs_bytes);
     int32_t* part = p.kslices > 1 ? reinterpret_cast<int32_t*>(ws + p.xs_bytes + p.s4_bytes) : nullptr;
-    const uint64_t frags = static_cast<uint64_t>(p.n_ksteps) * 5u * p.n_tg * 64u;
-    hipLaunchKernelGGL(gemm_stage_kernel, dim3(static_cast<uint32_t>((frags + 255) / 256)), dim3(256), 0, stream, x,
-                       static_cast<uint32_t>(ldx), static_cast<uint32_t>(M), p.n_tg, static_cast<uint32_t>(g.cols),
-                       static_cast<uint32_t>(g.tbr), p.n_ksteps, xs);
-    VX_HIP(hipGetLastError());
-    hipLaunchKernelGGL(gemm_s4_kernel, dim3(static_cast<uint32_t>(M)), dim3(256), 0, stream, x, static_cast<uint32_t>(ldx),
-                       static_cast<uint32_t>(M), static_cast<uint32_t>(g.cols), static_cast<uint32_t>(g.tbr), s4);
+    // B fragments of tokens past M (the rest of the last 32-token group) are left as they are: they only reach C
+    // columns that are never stored.
+    hipLaunchKernelGGL(gemm_stage_kernel, dim3(static_cast<uint32_t>(M), p.stage_x), dim3(256), 0, stream, x,
+                       static_cast<uint32_t>(ldx), p.n_tg, static_cast<uint32_t>(g.cols), static_cast<uint32_t>(g.tbr),
+                       p.n_ksteps, xs, s4p, static_cast<uint32_t>(M));
     VX_HIP(hipGetLastError());
     GemmArgs a{};
     a.w = w;
     a.xs = xs;
-    a.s4 = s4;
+    a.s4p = s4p;
+    a.s4_parts = p.stage_x;
     a.y = y;
     a.part = part;
     a.rows = static_cast<uint32_t>(g.rows);
@@ -289,10 +386,14 @@ int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* 
     a.M = static_cast<uint32_t>(M);
     a.n_tg = p.n_tg;
     a.ldy = static_cast<uint32_t>(ldy);
+    a.y_vec4 = (ldy % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0) ? 1u : 0u;
     a.kslices = p.kslices;
     a.ksteps_per_slice = p.ksteps_per_slice;
     a.rows_p = static_cast<uint32_t>(g.padded_rows);
-    hipLaunchKernelGGL(gemm_kernel, dim3(p.grid_x, p.grid_y, p.kslices), dim3(kGemmWaves * 64), 0, stream, a);
+    const dim3 grid(p.grid_x, p.n_tt, p.kslices);
+    if (p.T == 4) hipLaunchKernelGGL(gemm_kernel<4>, grid, dim3(kGemmWaves * 64), 0, stream, a);
+    else if (p.T == 2) hipLaunchKernelGGL(gemm_kernel<2>, grid, dim3(kGemmWaves * 64), 0, stream, a);
+    else hipLaunchKernelGGL(gemm_kernel<1>, grid, dim3(kGemmWaves * 64), 0, stream, a);
     VX_HIP(hipGetLastError());
     if (p.kslices > 1) {
         hipLaunchKernelGGL(gemm_finish_kernel, dim3((a.rows + 255u) / 256u, static_cast<uint32_t>(M)), dim3(256), 0, stream, a);
