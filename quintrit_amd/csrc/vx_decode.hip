@@ -3,20 +3,32 @@
 // One step follows the reference's CPU runtime operation by operation (quintrit-runtime/src/model.rs:64-377,
 // attention.rs:115-542, ops.rs), so that logits and greedy tokens are bit-identical to it:
 //   embed (bf16 row -> f32)
-//   per layer: [residual add +] RMSNorm + int8 quantization -> staged activations (one kernel)
-//              q, k, v projections (one plan, the fp32 layer epilogue)           -> NEOX RoPE, f16 KV append
-//              FP16-accumulator flash attention with bitnet.cpp's 4-chunk split  -> sub-norm + quantization
-//              o projection -> residual add + RMSNorm + quantization -> gate, up (one plan)
+//   per layer: [residual add +] RMSNorm + int8 quantization -> q, k, v projections (the fp32 layer epilogue)
+//              NEOX RoPE, f16 KV append, FP16-accumulator attention with bitnet.cpp's 4-chunk split
+//              sub-norm + quantization -> o projection
+//              residual add + RMSNorm + quantization -> gate, up projections
 //              ReLU^2(gate) * up + sub-norm + quantization -> down projection
 //   residual add + final RMSNorm -> bf16 -> tied bf16 head (ggml_vec_dot_bf16 order) -> greedy argmax (first maximum)
-// The position, the token and the generated ids live in device memory, so the whole step is one HIP graph replayed per
-// token (the reference's CUDA graph is position-independent the same way, quintrit-runtime/src/gpu.rs:459-493).
+//
+// Kernels. A step is 1 + 5 per layer launches, replayed as one HIP graph per token with the position, the token and the
+// generated ids in device memory (the reference's CUDA graph is position-independent the same way,
+// quintrit-runtime/src/gpu.rs:459-493):
+//   dgemv_kernel x4   per layer and projection stage, one workgroup per 64-row tile: every workgroup first computes
+//                     the stage input itself (the embedding row or a residual add or ReLU^2 gating of the previous
+//                     projections' outputs, RMSNorm, int8 quantization, GEMV staging, all in LDS) while its weights
+//                     are in flight, then its 16 waves split the row's chunks and add their exact int32 sums in LDS;
+//                     one wave applies the layer epilogue and stores the tile's fp32 outputs
+//   attention_kernel  per query head: RoPE of q and k, the KV append, attention
+//   head_kernel       final residual + RMSNorm, the bf16 head, and the greedy argmax across workgroups
+// Computing a stage input in every workgroup repeats a few microseconds of work that one workgroup would do alone, but
+// it runs in parallel with the weight loads and saves a launch and a wait on a single-CU kernel.
 //
 // RMSNorm (ops.rs:43-57) sums the f32 squares sequentially in f64 and rounds sum / n to f32. Here the squares are
 // summed as a tree; both sums differ from the exact one by at most (n - 1) 2^-53 sum, so when the f32 mean is the same
 // at both ends of that interval the tree's mean is the reference's; otherwise (rare) one lane redoes the sum in the
 // reference's order. The exponentials are glibc's expf (vx_expf.h).
 #include "vx_expf.h"
+#include "vx_gemv_core.h"
 #include "vx_internal.h"
 
 #include <algorithm>
@@ -29,6 +41,7 @@ namespace vx {
 // ---- small helpers --------------------------------------------------------------------------------------------------------
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 g_u4;
 
 __device__ __forceinline__ float bf16_f32(uint16_t h) { return bits_f32(static_cast<uint32_t>(h) << 16); }
 
@@ -50,141 +63,70 @@ __device__ __forceinline__ uint16_t f32_f16(float f) {
 }
 __device__ __forceinline__ float f16_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
 
-// ---- RMSNorm + quantization ------------------------------------------------------------------------------------------------
+// ---- wave reductions (DPP within rows of 16 lanes, then the four row results) ------------------------------------------------
 
-enum NormInput : uint32_t {
-    kInPlain = 0,     // v = a[i]
-    kInResidual = 1,  // v = a[i] + b[i], written back to a (add_residual, ops.rs:476-481)
-    kInRelu2Mul = 2,  // v = relu2(a[i]) * b[i] (ops.rs:301-308, 467-473)
-};
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // row_half_mirror: lane i of 8 reads lane 7 - i
+constexpr int kDppMirror = 0x140;     // row_mirror: lane i of 16 reads lane 15 - i
 
-struct NormArgs {
-    float* a;
-    const float* b;
-    const float* gamma;
-    uint32_t n;
-    float eps;
-    uint32_t input;
-    uint32_t quantize;      // 1: int8 codes into `staged` + scale into act_scale; 0: bf16 of y into out_bf16
-    uint8_t* staged;        // GEMV staging (kStageHeader + dbr * 8 bytes)
-    float* act_scale;
-    uint16_t* out_bf16;
-    uint32_t tbr, dbr;      // tile and device row bytes of n columns
-};
-
-constexpr int kNormThreads = 1024;
-constexpr uint32_t kNormMax = 8192;  // largest vector
-
-__global__ __launch_bounds__(kNormThreads) void norm_quant_kernel(NormArgs p) {
-    __shared__ float ys[kNormMax];
-    __shared__ int8_t qs[kNormMax];
-    __shared__ double red_d[16];
-    __shared__ float red_f[16];
-    __shared__ int red_i[16];
-    __shared__ float s_mean;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t n = p.n;
-
-    double ss = 0.0;
-    for (uint32_t i = tid; i < n; i += kNormThreads) {
-        float v;
-        if (p.input == kInPlain) {
-            v = p.a[i];
-        } else if (p.input == kInResidual) {
-            v = p.a[i] + p.b[i];
-            p.a[i] = v;
-        } else {
-            const float g = p.a[i];
-            const float pos = g > 0.0f ? g : 0.0f;
-            const float sq = pos * pos;
-            v = sq * p.b[i];
-        }
-        ys[i] = v;
-        const float sqv = v * v;
-        ss += static_cast<double>(sqv);
-    }
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    if (lane == 0) red_d[wave] = ss;
-    __syncthreads();
-    if (tid == 0) {
-        double t = 0.0;
-        for (int w = 0; w < kNormThreads / 64; ++w) t += red_d[w];
-        // the sequential f64 sum of the reference lies within d of t (both within (n-1) 2^-53 t of the exact sum)
-        const double d = 2.0 * static_cast<double>(n) * 0x1.0p-53 * t;
-        float mean = static_cast<float>(t / static_cast<double>(n));
-        const float lo = static_cast<float>((t - d) / static_cast<double>(n));
-        const float hi = static_cast<float>((t + d) / static_cast<double>(n));
-        if (lo != hi) {  // too close to an f32 rounding boundary: redo the sum in the reference's order
-            double seq = 0.0;
-            for (uint32_t i = 0; i < n; ++i) {
-                const float sqv = ys[i] * ys[i];
-                seq += static_cast<double>(sqv);
-            }
-            mean = static_cast<float>(seq / static_cast<double>(n));
-        }
-        s_mean = mean;
-    }
-    __syncthreads();
-    const float scale = 1.0f / __builtin_sqrtf(s_mean + p.eps);
-    float mx = 0.0f;
-    for (uint32_t i = tid; i < n; i += kNormThreads) {
-        const float t = ys[i] * scale;
-        const float y = t * p.gamma[i];
-        ys[i] = y;
-        const float ay = __builtin_fabsf(y);
-        if (ay > mx) mx = ay;
-        if (!p.quantize) p.out_bf16[i] = f32_bf16(y);
-    }
-    if (!p.quantize) return;
-    for (int off = 32; off > 0; off >>= 1) {
-        const float o = __shfl_xor(mx, off);
-        if (o > mx) mx = o;
-    }
-    if (lane == 0) red_f[wave] = mx;
-    __syncthreads();
-    float m = 0.0f;
-    for (int w = 0; w < kNormThreads / 64; ++w)
-        if (red_f[w] > m) m = red_f[w];
-    // quantize_activations_int8_with_range (ops.rs:241-267), levels 127
-    const float s = m > 0.0f ? 127.0f / m : 0.0f;
-    for (uint32_t i = tid; i < n; i += kNormThreads) {
-        int q = 0;
-        if (m > 0.0f) {
-            float r = __builtin_roundf(ys[i] * s);
-            r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
-            q = static_cast<int>(r);
-        }
-        qs[i] = static_cast<int8_t>(q);
-    }
-    __syncthreads();
-    // GEMV staging (vx_stage_acts_dev's format): nibbles of the five activations of each device byte-column
-    const uint32_t full = n / 160u * 32u;
-    uint2* ent = reinterpret_cast<uint2*>(p.staged + kStageHeader);
-    int sum = 0;
-    for (uint32_t c = tid; c < p.dbr; c += kNormThreads) {  // the entries of vx_stage_acts_dev
-        uint32_t lo = 0, hi = 0;
-        for (uint32_t k = 0; k < 5; ++k) {
-            const uint32_t idx = c < full ? (c / 32u) * 160u + k * 32u + (c % 32u) : (n / 160u) * 160u + 5u * (c - full) + k;
-            const int x = c < p.tbr && idx < n ? qs[idx] : 0;
-            lo |= ((static_cast<uint32_t>(x) & 15u) ^ 8u) << (4 * k);
-            hi |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * k);
-            sum += x;
-        }
-        ent[c] = make_uint2(lo, hi);
-    }
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    if (lane == 0) red_i[wave] = sum;
-    __syncthreads();
-    if (tid < 16) {
-        int t = 0;
-        if (tid == 0)
-            for (int w = 0; w < kNormThreads / 64; ++w) t += red_i[w];
-        reinterpret_cast<int*>(p.staged)[tid] = t;
-        if (tid == 0) *p.act_scale = s;
-    }
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double x) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint64_t lo = dpp32<CTRL>(static_cast<uint32_t>(u)), hi = dpp32<CTRL>(static_cast<uint32_t>(u >> 32));
+    return __builtin_bit_cast(double, (hi << 32) | lo);
+}
+__device__ __forceinline__ double readlane_f64(double x, int l) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u), l));
+    const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), l));
+    return __builtin_bit_cast(double, (hi << 32) | lo);
 }
 
-// ---- embedding, RoPE + KV append ---------------------------------------------------------------------------------------------
+// After the four DPP steps every lane holds the result of its row of 16; the wave's is combined from lanes 0, 16, 32, 48.
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    x += dpp_f64<kDppXor1>(x);
+    x += dpp_f64<kDppXor2>(x);
+    x += dpp_f64<kDppHalfMirror>(x);
+    x += dpp_f64<kDppMirror>(x);
+    return (readlane_f64(x, 0) + readlane_f64(x, 16)) + (readlane_f64(x, 32) + readlane_f64(x, 48));
+}
+
+__device__ __forceinline__ int wave_sum_i32(int x) {
+    x += static_cast<int>(dpp32<kDppXor1>(static_cast<uint32_t>(x)));
+    x += static_cast<int>(dpp32<kDppXor2>(static_cast<uint32_t>(x)));
+    x += static_cast<int>(dpp32<kDppHalfMirror>(static_cast<uint32_t>(x)));
+    x += static_cast<int>(dpp32<kDppMirror>(static_cast<uint32_t>(x)));
+    return (__builtin_amdgcn_readlane(x, 0) + __builtin_amdgcn_readlane(x, 16)) +
+           (__builtin_amdgcn_readlane(x, 32) + __builtin_amdgcn_readlane(x, 48));
+}
+
+// Largest of non-negative, non-NaN values.
+__device__ __forceinline__ float fmax_nn(float a, float b) { return b > a ? b : a; }
+__device__ __forceinline__ float wave_max_f32(float x) {
+    x = fmax_nn(x, bits_f32(dpp32<kDppXor1>(f32_bits(x))));
+    x = fmax_nn(x, bits_f32(dpp32<kDppXor2>(f32_bits(x))));
+    x = fmax_nn(x, bits_f32(dpp32<kDppHalfMirror>(f32_bits(x))));
+    x = fmax_nn(x, bits_f32(dpp32<kDppMirror>(f32_bits(x))));
+    const float a = bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(f32_bits(x)), 0)));
+    const float b = bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(f32_bits(x)), 16)));
+    const float c = bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(f32_bits(x)), 32)));
+    const float d = bits_f32(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(f32_bits(x)), 48)));
+    return fmax_nn(fmax_nn(a, b), fmax_nn(c, d));
+}
+
+// ---- the stage input: embedding / residual add / ReLU^2 gating, RMSNorm, int8 quantization --------------------------------
+
+constexpr int kNT = 1024;            // threads of the kernels that compute a stage input
+constexpr uint32_t kNormMax = 8192;  // longest input vector
+constexpr uint32_t kStChunks = 112;  // 16-byte chunks of a staged input in LDS (device_row_bytes(8192) / 16 + 4 fit)
+constexpr int kPer4 = kNormMax / (4 * kNT);  // float4 groups of the input per thread at most
+constexpr int kMaxSlicesA = 6;       // K slices of a projection read as a residual-add input or a stage-0 head input
+constexpr int kMaxSlicesB = 2;       // K slices of the gate and up projections (the ReLU^2 inputs)
 
 struct Ctl {          // device-resident loop state
     uint32_t pos;     // position of the step
@@ -193,67 +135,426 @@ struct Ctl {          // device-resident loop state
     uint32_t n_out;   // capacity of the generated-token array
 };
 
-__global__ void embed_kernel(const Ctl* __restrict__ ctl, const uint32_t* __restrict__ prompt,
-                             const uint16_t* __restrict__ emb, uint32_t hidden, float* __restrict__ x) {
-    const uint32_t pos = ctl->pos;
-    const uint32_t tok = pos < ctl->n_prompt ? prompt[pos] : ctl->token;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
-        x[i] = bf16_f32(emb[static_cast<size_t>(tok) * hidden + i]);
+// *p if c, else zero (a branch, not a select between a load and a zero held in memory).
+template <class T>
+__device__ __forceinline__ T load_if(const T* p, bool c) {
+    T v{};
+    if (c) v = *p;
+    return v;
 }
 
-struct RopeArgs {
-    const Ctl* ctl;
-    const float* q;
-    const float* k;
-    const float* v;
-    const float* rope;  // [max_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i + 1
-    uint16_t* qh;       // f16 queries
-    uint16_t* kc;       // f16 [kv_head][max_ctx][head_dim] of this layer
-    uint16_t* vc;
-    uint32_t n_heads, n_kv_heads, head_dim, max_ctx;
+// A projection output as its consumers read it: row i is float(sum_k part[k * stride + i]) * (ws / as), zero when as is
+// not > 0 (the layer epilogue, layer.rs:246-253; the K-slice sums are exact int32, so their order does not matter).
+struct ProjOut {
+    const int32_t* part;  // [kslices][stride]; slice 0 holds the row corrections
+    const float* as;      // activation scale of the producing stage
+    float ws;             // weight scale
+    uint32_t kslices, stride;
 };
 
-// NEOX pairing over all head_dim coordinates (ops.rs:199-221): x0' = fma(x0, c, -(x1 s)), x1' = fma(x0, s, x1 c).
-__global__ void rope_kv_kernel(RopeArgs a) {
-    const uint32_t half = a.head_dim / 2u;
-    const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-    const uint32_t pos = a.ctl->pos;
-    const float* cache = a.rope + static_cast<size_t>(pos) * a.head_dim;
-    const uint32_t nq = a.n_heads * half, nk = a.n_kv_heads * half;
-    if (t < nq + nk) {
-        const bool isq = t < nq;
-        const uint32_t u = isq ? t : t - nq;
-        const uint32_t h = u / half, i = u - h * half;
-        const float* src = (isq ? a.q : a.k) + static_cast<size_t>(h) * a.head_dim;
-        const float c = cache[2 * i], s = cache[2 * i + 1];
-        const float x0 = src[i], x1 = src[i + half];
-        const float x1s = x1 * s, x1c = x1 * c;
-        const float y0 = __builtin_fmaf(x0, c, -x1s);
-        const float y1 = __builtin_fmaf(x0, s, x1c);
-        if (isq) {
-            a.qh[h * a.head_dim + i] = f32_f16(y0);
-            a.qh[h * a.head_dim + i + half] = f32_f16(y1);
-        } else {
-            uint16_t* dst = a.kc + (static_cast<size_t>(h) * a.max_ctx + pos) * a.head_dim;
-            dst[i] = f32_f16(y0);
-            dst[i + half] = f32_f16(y1);
+__device__ __forceinline__ float proj_post(const ProjOut& o, bool* zero) {
+    const float as = *o.as;
+    *zero = !(as > 0.0f);
+    return *zero ? 0.0f : o.ws / as;
+}
+__device__ __forceinline__ float proj_value(int32_t acc, float post, bool zero) {
+    return zero ? 0.0f : static_cast<float>(acc) * post;
+}
+// Row i of o (attention inputs: a few values per thread); every slice is loaded before the sum uses one.
+__device__ __forceinline__ float proj_at(const ProjOut& o, uint32_t i, float post, bool zero) {
+    int32_t v[kMaxSlicesA];
+#pragma unroll
+    for (int k = 0; k < kMaxSlicesA; ++k) v[k] = load_if(o.part + static_cast<size_t>(k) * o.stride + i, static_cast<uint32_t>(k) < o.kslices);
+    int32_t acc = 0;
+#pragma unroll
+    for (int k = 0; k < kMaxSlicesA; ++k) acc += v[k];
+    return proj_value(acc, post, zero);
+}
+
+enum InputKind : uint32_t {
+    kInEmbed = 0,     // v = the token's embedding row (bf16 -> f32, model.rs:309-316); the token from the loop state
+    kInResidual = 1,  // v = x_in[i] + a[i] (add_residual, ops.rs:476-481)
+    kInPlain = 2,     // v = x_in[i]
+    kInRelu2Mul = 3,  // v = relu2(a[i]) * b[i] (ops.rs:301-308, 467-473)
+};
+
+struct StageInput {
+    uint32_t kind, n;     // n: a multiple of 4, at most kNormMax
+    const float* x_in;
+    ProjOut a, b;         // the previous projections (residual: o or down; ReLU^2: gate and up)
+    float* x_out;         // kInEmbed, kInResidual: v, the residual stream (workgroup 0 writes it), or null
+    const float* gamma;   // RMSNorm weights
+    float eps;
+    const Ctl* ctl;       // kInEmbed
+    const uint32_t* prompt;
+    const uint16_t* emb;
+};
+
+// The loaded inputs of a thread: element e of float4 group k is 4 (tid + k kNT) + e.
+struct InputRegs {
+    uint4 x[kPer4];                // embedding bits (x, y) or x_in
+    int4 pa[kMaxSlicesA][kPer4];   // K-slice partials of a
+    int4 pb[kMaxSlicesB][kPer4];   // K-slice partials of b
+    float4 g[kPer4];               // gamma
+};
+
+struct __align__(16) InputLds {  // ys is accessed 16 bytes at a time
+    float ys[kNormMax];
+    double red_d[kNT / 64];
+    float red_f[kNT / 64];
+    int red_i[kNT / 64];
+    float mean;
+};
+
+__device__ __forceinline__ uint32_t elem4(uint32_t tid, int k) { return 4u * (tid + static_cast<uint32_t>(k) * kNT); }
+
+
+// Issues every load of the thread's inputs (16 bytes each) without using any, so that the loads a kernel issues after
+// it (weights) do not delay them: vector-memory loads complete in issue order.
+__device__ __forceinline__ void stage_load(const StageInput& p, InputRegs& r) {
+    const uint32_t tid = threadIdx.x, n = p.n;
+    if (p.kind == kInEmbed) {
+        const uint32_t pos = p.ctl->pos;
+        const uint32_t tok = pos < p.ctl->n_prompt ? p.prompt[pos] : p.ctl->token;
+        const uint2* row = reinterpret_cast<const uint2*>(p.emb + static_cast<size_t>(tok) * n);
+#pragma unroll
+        for (int k = 0; k < kPer4; ++k) {
+            const uint32_t i = elem4(tid, k);
+            const uint2 e = load_if(row + i / 4u, i < n);
+            r.x[k] = make_uint4(e.x, e.y, 0u, 0u);
+        }
+    } else if (p.kind != kInRelu2Mul) {
+#pragma unroll
+        for (int k = 0; k < kPer4; ++k) {
+            const uint32_t i = elem4(tid, k);
+            r.x[k] = load_if(reinterpret_cast<const uint4*>(p.x_in + i), i < n);
         }
     }
-    const uint32_t kvd = a.n_kv_heads * a.head_dim;
-    if (t < kvd) {
-        const uint32_t h = t / a.head_dim, d = t - h * a.head_dim;
-        a.vc[(static_cast<size_t>(h) * a.max_ctx + pos) * a.head_dim + d] = f32_f16(a.v[t]);
+    if (p.kind == kInResidual || p.kind == kInRelu2Mul) {
+#pragma unroll
+        for (int s = 0; s < kMaxSlicesA; ++s)
+#pragma unroll
+            for (int k = 0; k < kPer4; ++k) {
+                const uint32_t i = elem4(tid, k);
+                r.pa[s][k] = load_if(reinterpret_cast<const int4*>(p.a.part + static_cast<size_t>(s) * p.a.stride + i),
+                                     i < n && static_cast<uint32_t>(s) < p.a.kslices);
+            }
     }
+    if (p.kind == kInRelu2Mul) {
+#pragma unroll
+        for (int s = 0; s < kMaxSlicesB; ++s)
+#pragma unroll
+            for (int k = 0; k < kPer4; ++k) {
+                const uint32_t i = elem4(tid, k);
+                r.pb[s][k] = load_if(reinterpret_cast<const int4*>(p.b.part + static_cast<size_t>(s) * p.b.stride + i),
+                                     i < n && static_cast<uint32_t>(s) < p.b.kslices);
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < kPer4; ++k) {
+        const uint32_t i = elem4(tid, k);
+        r.g[k] = load_if(reinterpret_cast<const float4*>(p.gamma + i), i < n);
+    }
+}
+
+// v (by kind) from the loaded inputs into s.ys, then its RMSNorm y = (v * inv) * gamma (rms_norm, ops.rs:19-96) in
+// place. Every thread derives the mean from the per-wave sums itself, so the common path has one barrier. Returns this
+// thread's largest |y| (NaN never counts); the elements of s.ys a thread did not write are readable after the next
+// barrier. With write_x, an input that has an x_out also stores v there.
+__device__ __forceinline__ float stage_norm(const StageInput& p, const InputRegs& r, InputLds& s, bool write_x) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t n = p.n;
+    float v[kPer4][4];
+    if (p.kind == kInEmbed) {
+#pragma unroll
+        for (int k = 0; k < kPer4; ++k) {
+            v[k][0] = bits_f32(r.x[k].x << 16);
+            v[k][1] = bits_f32(r.x[k].x & 0xffff0000u);
+            v[k][2] = bits_f32(r.x[k].y << 16);
+            v[k][3] = bits_f32(r.x[k].y & 0xffff0000u);
+        }
+    } else if (p.kind == kInRelu2Mul) {
+        bool za, zb;
+        const float pa = proj_post(p.a, &za), pb = proj_post(p.b, &zb);
+#pragma unroll
+        for (int k = 0; k < kPer4; ++k) {
+            const int32_t ga[4] = {r.pa[0][k].x, r.pa[0][k].y, r.pa[0][k].z, r.pa[0][k].w};
+            const int32_t ub[4] = {r.pb[0][k].x, r.pb[0][k].y, r.pb[0][k].z, r.pb[0][k].w};
+            int32_t sa[4] = {ga[0], ga[1], ga[2], ga[3]}, sb[4] = {ub[0], ub[1], ub[2], ub[3]};
+#pragma unroll
+            for (int s2 = 1; s2 < kMaxSlicesA; ++s2) {
+                sa[0] += r.pa[s2][k].x;
+                sa[1] += r.pa[s2][k].y;
+                sa[2] += r.pa[s2][k].z;
+                sa[3] += r.pa[s2][k].w;
+            }
+#pragma unroll
+            for (int s2 = 1; s2 < kMaxSlicesB; ++s2) {
+                sb[0] += r.pb[s2][k].x;
+                sb[1] += r.pb[s2][k].y;
+                sb[2] += r.pb[s2][k].z;
+                sb[3] += r.pb[s2][k].w;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float g = proj_value(sa[e], pa, za), u = proj_value(sb[e], pb, zb);
+                const float pos = g > 0.0f ? g : 0.0f;
+                const float sq = pos * pos;
+                v[k][e] = sq * u;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kPer4; ++k) {
+            v[k][0] = bits_f32(r.x[k].x);
+            v[k][1] = bits_f32(r.x[k].y);
+            v[k][2] = bits_f32(r.x[k].z);
+            v[k][3] = bits_f32(r.x[k].w);
+        }
+        if (p.kind == kInResidual) {
+            bool za;
+            const float pa = proj_post(p.a, &za);
+#pragma unroll
+            for (int k = 0; k < kPer4; ++k) {
+                int32_t sa[4] = {r.pa[0][k].x, r.pa[0][k].y, r.pa[0][k].z, r.pa[0][k].w};
+#pragma unroll
+                for (int s2 = 1; s2 < kMaxSlicesA; ++s2) {
+                    sa[0] += r.pa[s2][k].x;
+                    sa[1] += r.pa[s2][k].y;
+                    sa[2] += r.pa[s2][k].z;
+                    sa[3] += r.pa[s2][k].w;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[k][e] = v[k][e] + proj_value(sa[e], pa, za);
+            }
+        }
+    }
+    if (write_x && p.kind != kInPlain && p.kind != kInRelu2Mul && p.x_out != nullptr) {
+#pragma unroll
+        for (int k = 0; k < kPer4; ++k)
+            if (elem4(tid, k) < n)
+                *reinterpret_cast<float4*>(p.x_out + elem4(tid, k)) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < kPer4; ++k) {
+        const uint32_t i = elem4(tid, k);
+        if (i < n) {
+            *reinterpret_cast<float4*>(s.ys + i) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float sqv = v[k][e] * v[k][e];
+                ss += static_cast<double>(sqv);
+            }
+        }
+    }
+    ss = wave_sum_f64(ss);
+    if (lane == 0) s.red_d[wave] = ss;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < kNT / 64; ++w) t += s.red_d[w];
+    // the sequential f64 sum of the reference lies within d of t (both within (n-1) 2^-53 t of the exact sum)
+    const double d = 2.0 * static_cast<double>(n) * 0x1.0p-53 * t;
+    float mean = static_cast<float>(t / static_cast<double>(n));
+    const float lo = static_cast<float>((t - d) / static_cast<double>(n));
+    const float hi = static_cast<float>((t + d) / static_cast<double>(n));
+    if (lo != hi) {  // (the same in every thread) too close to an f32 rounding boundary: the reference's order
+        if (tid == 0) {
+            double seq = 0.0;
+            for (uint32_t i = 0; i < n; ++i) {
+                const float sqv = s.ys[i] * s.ys[i];
+                seq += static_cast<double>(sqv);
+            }
+            s.mean = static_cast<float>(seq / static_cast<double>(n));
+        }
+        __syncthreads();
+        mean = s.mean;
+    }
+    const float scale = 1.0f / __builtin_sqrtf(mean + p.eps);
+    float mx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kPer4; ++k) {
+        const uint32_t i = elem4(tid, k);
+        if (i < n) {
+            const float gm[4] = {r.g[k].x, r.g[k].y, r.g[k].z, r.g[k].w};
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float tt = v[k][e] * scale;
+                y[e] = tt * gm[e];
+                const float ay = __builtin_fabsf(y[e]);
+                if (ay > mx) mx = ay;
+            }
+            *reinterpret_cast<float4*>(s.ys + i) = make_float4(y[0], y[1], y[2], y[3]);
+        }
+    }
+    return mx;
+}
+
+// Per-token absmax int8 quantization of s.ys (quantize_activations_int8_with_range, ops.rs:241-267, levels 127) and the
+// GEMV staging of the codes into st: entry c (device byte-column c) holds the low nibbles ((x & 15) ^ 8) and the high
+// nibbles (x >> 4) of its five activations (column_activation_index, pack.rs:230-237; zero past the row), entries from
+// dbr to (dbr / 16 + 4) * 16 are zero. Each entry quantizes its own five values. Two barriers; afterwards st is
+// complete, *scale is the activation scale and *act_sum the sum of the codes, in every thread.
+__device__ __forceinline__ void stage_quant(InputLds& s, float mx, uint32_t n, uint32_t tbr, uint32_t dbr, uint2* st, float* scale,
+                            int* act_sum) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    mx = wave_max_f32(mx);
+    if (lane == 0) s.red_f[wave] = mx;
+    __syncthreads();
+    float m = 0.0f;
+    for (int w = 0; w < kNT / 64; ++w) m = fmax_nn(m, s.red_f[w]);
+    const float sc = m > 0.0f ? 127.0f / m : 0.0f;
+    const uint32_t full = n / 160u * 32u;
+    const uint32_t st_len = (dbr / 16u + 4u) * 16u;
+    int sum = 0;
+    for (uint32_t c = tid; c < st_len; c += kNT) {
+        uint32_t lo = 0, hi = 0;
+        if (c < dbr) {
+            const uint32_t base = c < full ? (c / 32u) * 160u + (c % 32u) : (n / 160u) * 160u + 5u * (c - full);
+            const uint32_t step = c < full ? 32u : 1u;
+#pragma unroll
+            for (uint32_t k = 0; k < 5; ++k) {
+                const uint32_t idx = base + k * step;
+                int x = 0;
+                if (c < tbr && idx < n && m > 0.0f) {
+                    float rr = __builtin_roundf(s.ys[idx] * sc);
+                    rr = rr < -128.0f ? -128.0f : (rr > 127.0f ? 127.0f : rr);
+                    x = static_cast<int>(rr);
+                }
+                lo |= ((static_cast<uint32_t>(x) & 15u) ^ 8u) << (4 * k);
+                hi |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * k);
+                sum += x;
+            }
+        }
+        st[c] = make_uint2(lo, hi);
+    }
+    sum = wave_sum_i32(sum);
+    if (lane == 0) s.red_i[wave] = sum;
+    __syncthreads();
+    int t = 0;
+    for (int w = 0; w < kNT / 64; ++w) t += s.red_i[w];
+    *act_sum = t;
+    *scale = sc;
+}
+
+// ---- decode-step GEMV ------------------------------------------------------------------------------------------------------
+
+// One projection of a stage. A work item is (64-row tile, K slice): the 16 waves of a workgroup split the slice's
+// chunks and add their int32 sums in LDS, and the tile's slice sums (with the row corrections on slice 0) are stored
+// as part[ks][row]; the consumers add the slices and apply the epilogue (ProjOut).
+struct DJob {
+    const uint8_t* w;      // device layout (vx_layout)
+    const int32_t* dsum;   // per padded row: digit sum of the device row
+    int32_t* part;         // [kslices][padded_rows]
+    uint32_t rows, padded_rows, n_tiles, n_chunks, kslices, slice_chunks, item_begin;
+};
+
+constexpr int kMaxStageJobs = 3;
+constexpr int kDPer = 7;  // chunks of a slice per wave at most: ceil(device_row_bytes(8192) / 16 / 16)
+
+struct DStageArgs {
+    DJob job[kMaxStageJobs];
+    uint32_t n_jobs, total_items;
+    StageInput in;
+    uint32_t tbr, dbr;  // tile and device row bytes of in.n columns
+    float* as_out;      // the stage's activation scale (workgroup 0)
+};
+
+__constant__ DigitTable g_digits = make_digit_table();
+
+// One workgroup per work item. Order of the loads: the stage input, the digit table, then wave w's chunks
+// q0 + w, q0 + w + 16, ... of the tile (1 KiB each in the device layout), so the input is computed while the weights
+// are in flight; the digit-nibble table and the arithmetic are those of the lone GEMV (vx_gemv.hip).
+__global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
+    __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of the digit nibbles of byte B (first half)
+    __shared__ uint2 st[kStChunks * 16];
+    __shared__ InputLds s;
+    __shared__ int red[kNT / 64][64];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const char* tabb = reinterpret_cast<const char*>(tab);
+    const uint32_t lane_off = (lane & 31u) * 4u;
+
+    InputRegs r;
+    stage_load(a.in, r);
+    uint32_t dig[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) dig[k] = g_digits.v[(tid + k * kNT) >> 3];
+
+    const uint32_t item = blockIdx.x;
+    uint32_t j = 0;
+    if (a.n_jobs > 1 && item >= a.job[1].item_begin) j = 1;
+    if (a.n_jobs > 2 && item >= a.job[2].item_begin) j = 2;
+    const DJob jb = j == 0 ? a.job[0] : (j == 1 ? a.job[1] : a.job[2]);
+    const uint32_t local = item - jb.item_begin;
+    const uint32_t tile = local / jb.kslices, ks = local - tile * jb.kslices;
+    const uint32_t grp = tile / kTileGroup, tt = tile - grp * kTileGroup;
+    const uint32_t T = min(static_cast<uint32_t>(kTileGroup), jb.n_tiles - grp * kTileGroup);
+    const uint32_t q0 = ks * jb.slice_chunks, nq = min(jb.slice_chunks, jb.n_chunks - q0);
+    const uint32_t cnt = wave < nq ? (nq - wave + kTileGroup - 1) / kTileGroup : 0u;  // this wave's chunks
+    const g_u4* wp = (const g_u4*)(jb.w) + (static_cast<size_t>(grp) * kTileGroup * jb.n_chunks + tt) * 64u + lane;
+    const size_t cs = static_cast<size_t>(T) * 64u;  // uint4 between chunks q and q + 1 of the tile
+    u32x4 b[kDPer];
+#pragma unroll
+    for (int i = 0; i < kDPer; ++i) {
+        if (static_cast<uint32_t>(i) < cnt)
+            b[i] = __builtin_nontemporal_load(wp + (q0 + wave + kTileGroup * static_cast<size_t>(i)) * cs);
+    }
+
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {  // 8 uint4 stores per entry
+        const uint32_t i = tid + k * kNT;
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) =
+            make_uint4(dig[k], dig[k], dig[k], dig[k]);
+    }
+    const float mx = stage_norm(a.in, r, s, blockIdx.x == 0);
+    float act_scale;
+    int act_sum;
+    stage_quant(s, mx, a.in.n, a.tbr, a.dbr, st, &act_scale, &act_sum);
+    if (blockIdx.x == 0 && tid == 0) *a.as_out = act_scale;
+
+    int acc_lo = 0, acc_hi = 0;
+#pragma unroll
+    for (int i = 0; i < kDPer; ++i) {
+        if (static_cast<uint32_t>(i) >= cnt) break;
+        const uint32_t q = q0 + wave + kTileGroup * i;
+        const uint32_t dw[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
+        const uint2 e = st[q * 16u + (lane & 15u)];
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t t[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const uint32_t addr = __builtin_amdgcn_perm(dw[k >> 2], lane_off, 0x0c0c0000u | ((4u + (k & 3)) << 8));
+            t[k] = *reinterpret_cast<const uint32_t*>(tabb + addr);
+        }
+        dot4_bcast<0>(acc_lo, acc_hi, e.x, e.y, t[0], t[1], t[2], t[3]);
+        dot4_bcast<4>(acc_lo, acc_hi, e.x, e.y, t[4], t[5], t[6], t[7]);
+        dot4_bcast<8>(acc_lo, acc_hi, e.x, e.y, t[8], t[9], t[10], t[11]);
+        dot4_bcast<12>(acc_lo, acc_hi, e.x, e.y, t[12], t[13], t[14], t[15]);
+    }
+    red[wave][lane] = acc_lo + 16 * acc_hi;
+    __syncthreads();
+    if (wave != 0) return;
+    // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in slice 0
+    int v = 0;
+#pragma unroll
+    for (int w = 0; w < kNT / 64; ++w) v += red[w][lane];
+    const uint32_t row = tile * kTileRows + lane;
+    if (ks == 0) v += 8 * jb.dsum[row] - act_sum;
+    jb.part[static_cast<size_t>(ks) * jb.padded_rows + row] = v;
 }
 
 // ---- attention ------------------------------------------------------------------------------------------------------------
 
 struct AttnArgs {
     const Ctl* ctl;
-    const uint16_t* qh;  // f16 queries, n_heads x kAttnHd
-    const uint16_t* kc;  // this layer: [kv_head][max_ctx][kAttnHd]
-    const uint16_t* vc;
-    float* out;          // n_heads x kAttnHd
+    ProjOut q, k, v;       // the q, k, v projections of this layer
+    const float* rope;     // [max_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i + 1
+    uint16_t* kc;          // this layer: [kv_head][max_ctx][kAttnHd] f16
+    uint16_t* vc;
+    float* out;            // n_heads x kAttnHd
     uint32_t n_heads, gqa, max_ctx;
     float scale;
 };
@@ -262,20 +563,27 @@ constexpr uint32_t kAttnHd = 128;       // head_dim of the attention kernel
 constexpr uint32_t kAttnMaxCtx = 4096;  // KV positions held in LDS (scores, running maxima)
 constexpr uint32_t kAttnWaves = 8;      // 4 chunks x 2 halves of the head
 constexpr uint32_t kAttnWin = 64;       // positions of V staged per wave at a time
+constexpr uint32_t kAttnBatch = 8;      // positions whose LDS operands are read ahead of the accumulator chain
+
+// The 16 uint4 of a 128-value f16 row.
+__device__ __forceinline__ void load_row128(const uint16_t* k, uint4 (&kr)[16]) {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) kr[c] = *reinterpret_cast<const uint4*>(k + 8 * c);
+}
 
 // ggml_vec_dot_f16 of 128 values (ops.rs:960-1015): four accumulators of eight lanes take fma per 32 values,
-// red = (s0 + s2) + (s1 + s3), t[k] = red[k] + red[k + 4], (t0 + t1) + (t2 + t3).
-__device__ float dot_f16_128(const uint16_t* q, const uint16_t* __restrict__ k) {
+// red = (s0 + s2) + (s1 + s3), t[k] = red[k] + red[k + 4], (t0 + t1) + (t2 + t3). q is in LDS, k in registers.
+__device__ __forceinline__ float dot_f16_128(const uint16_t* q, const uint4 (&kr)[16]) {
     float acc[4][8];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int l = 0; l < 8; ++l) acc[j][l] = 0.0f;
-#pragma unroll 1
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint4 kv = *reinterpret_cast<const uint4*>(k + 32 * i + 8 * j);
+            const uint4 kv = kr[4 * i + j];
             const uint4 qv = *reinterpret_cast<const uint4*>(q + 32 * i + 8 * j);
             const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
@@ -296,10 +604,14 @@ __device__ float dot_f16_128(const uint16_t* q, const uint16_t* __restrict__ k) 
 // f16 value of an f32 (round to nearest even, after the f32 rounding of x), kept in an f32
 __device__ __forceinline__ float r16(float x) { return static_cast<float>(static_cast<_Float16>(keep_f32(x))); }
 
-// One workgroup per query head; the reference's attend_head (attention.rs:483-542) over the positions 0..pos.
-// Below a padded KV length of 512 one online softmax covers all positions; from 512 on, 4 chunks of ceil(n_kv / 4)
-// positions run one each and are combined in order. The online softmax of a chunk (attend_range,
-// attention.rs:436-468) is rebuilt without its serial dependences except the FP16 accumulator itself:
+// One workgroup per query head. First the inputs of the position: q of this head and k, v of its KV head, NEOX RoPE over all head_dim coordinates (ops.rs:199-221:
+// x0' = fma(x0, c, -(x1 s)), x1' = fma(x0, s, x1 c)) and the f16 rounding of the cache (kv_cache.rs:24-182); the first
+// query head of each KV head appends k and v to the cache, and every workgroup uses its own copy of them for the
+// position itself (the other positions come from earlier steps).
+// Then the reference's attend_head (attention.rs:483-542) over the positions 0..pos. Below a padded KV length of 512 one
+// online softmax covers all positions; from 512 on, 4 chunks of ceil(n_kv / 4) positions run one each and are combined
+// in order. The online softmax of a chunk (attend_range, attention.rs:436-468) is rebuilt without its serial
+// dependences except the FP16 accumulator itself:
 //   scores        every position in parallel: ggml_vec_dot_f16(q, k) * scale
 //   running max   a scan per chunk; the reference's max moves only on score > max, the scan combines the same way
 //   factors       every position in parallel: a new maximum gives ms = expf(m_old - score), vs = 1; otherwise ms = 1,
@@ -312,96 +624,159 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     __shared__ float pm[kAttnMaxCtx];
     __shared__ __align__(16) uint16_t vbuf[kAttnWaves][kAttnWin * 64];
     __shared__ __align__(16) uint16_t qs[kAttnHd];
+    __shared__ __align__(16) uint16_t kp[kAttnHd];  // k and v of the position itself
+    __shared__ __align__(16) uint16_t vp[kAttnHd];
     __shared__ float cm[4], cs[4];
     __shared__ uint16_t cv[4][kAttnHd];
-    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t kvh = h / a.gqa;
-    const uint32_t seq = a.ctl->pos + 1;
+    const uint32_t pos = a.ctl->pos;
+    const uint32_t seq = pos + 1;
+    const uint16_t* kb = a.kc + static_cast<size_t>(kvh) * a.max_ctx * kAttnHd;
+    const uint16_t* vb = a.vc + static_cast<size_t>(kvh) * a.max_ctx * kAttnHd;
+
     uint32_t n_kv = (seq + 255u) / 256u * 256u;
     if (n_kv > a.max_ctx) n_kv = a.max_ctx;
     const bool split = n_kv >= 512u;
     const uint32_t chunk = split ? (n_kv + 3u) / 4u : seq;
     const uint32_t n_chunks = split ? 4u : 1u;
-    const uint16_t* kb = a.kc + static_cast<size_t>(kvh) * a.max_ctx * kAttnHd;
-    const uint16_t* vb = a.vc + static_cast<size_t>(kvh) * a.max_ctx * kAttnHd;
-    if (tid < kAttnHd) qs[tid] = a.qh[h * kAttnHd + tid];
-    __syncthreads();
-
-    for (uint32_t p = tid; p < seq; p += kAttnWaves * 64u) sc[p] = dot_f16_128(qs, kb + static_cast<size_t>(p) * kAttnHd) * a.scale;
-    __syncthreads();
-
-    if (wave < n_chunks) {
-        const uint32_t st = wave * chunk, en = min(min(st + chunk, n_kv), seq);
-        float carry = -__builtin_inff();
-        for (uint32_t base = st; base < en; base += 64u) {
-            const uint32_t p = base + lane;
-            float v = p < en ? sc[p] : -__builtin_inff();
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float o = __shfl_up(v, off);
-                if (lane >= static_cast<uint32_t>(off)) v = v > o ? v : o;
-            }
-            v = v > carry ? v : carry;
-            if (p < en) pm[p] = v;
-            carry = __shfl(v, 63);
-        }
-    }
-    __syncthreads();
-
-    for (uint32_t p = tid; p < seq; p += kAttnWaves * 64u) {
-        const uint32_t st = split ? p / chunk * chunk : 0u;
-        const float prev = p == st ? -__builtin_inff() : pm[p - 1];
-        const float s = sc[p];
-        sc[p] = s > prev ? -glibc_expf(prev - s) : glibc_expf(s - prev);
-    }
-    __syncthreads();
-
+    // This wave's chunk and half of the head.
     const uint32_t c = wave >> 1, half = wave & 1u, d = half * 64u + lane;
     uint32_t st = 0, en = 0;
     if (c < n_chunks) {
         st = c * chunk;
         en = min(min(st + chunk, n_kv), seq);
     }
+
+    {
+        constexpr uint32_t hh = kAttnHd / 2u;
+        const float* cache = a.rope + static_cast<size_t>(pos) * kAttnHd;
+        if (tid < 2u * hh) {  // q (tid < 64) or k: the rotation of pair i
+            const bool isq = tid < hh;
+            const uint32_t i = tid & (hh - 1u);
+            const ProjOut& o = isq ? a.q : a.k;
+            const uint32_t base = (isq ? h : kvh) * kAttnHd;
+            bool zero;
+            const float post = proj_post(o, &zero);
+            const float x0 = proj_at(o, base + i, post, zero), x1 = proj_at(o, base + i + hh, post, zero);
+            const float cc = cache[2 * i], ss = cache[2 * i + 1];
+            const float x1s = x1 * ss, x1c = x1 * cc;
+            const float y0 = __builtin_fmaf(x0, cc, -x1s);
+            const float y1 = __builtin_fmaf(x0, ss, x1c);
+            uint16_t* dst = isq ? qs : kp;
+            dst[i] = f32_f16(y0);
+            dst[i + hh] = f32_f16(y1);
+        } else if (tid < 4u * hh) {
+            const uint32_t dd = tid - 2u * hh;
+            bool zero;
+            const float post = proj_post(a.v, &zero);
+            vp[dd] = f32_f16(proj_at(a.v, kvh * kAttnHd + dd, post, zero));
+        }
+    }
+    __syncthreads();
+    if (h % a.gqa == 0 && tid < kAttnHd) {
+        a.kc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * kAttnHd + tid] = kp[tid];
+        a.vc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * kAttnHd + tid] = vp[tid];
+    }
+    // This wave's first window of V, requested before the scores so that its latency overlaps them, the scan and
+    // the exponentials; the position itself comes from LDS.
+    const uint32_t off = half * 64u + (lane & 7u) * 8u;
+    const uint16_t* vsrc = vb + off;
+    auto load_v = [&](uint32_t p) -> u32x4 {
+        return p == pos ? *reinterpret_cast<const u32x4*>(vp + off)
+                        : *reinterpret_cast<const u32x4*>(vsrc + static_cast<size_t>(p) * kAttnHd);
+    };
+    u32x4 r[8];
+    if (st < en) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = load_v(min(st + 8u * j + (lane >> 3), en - 1u));
+    }
+
+    for (uint32_t p = tid; p < seq; p += kAttnWaves * 64u) {
+        uint4 kr[16];
+        load_row128(p == pos ? kp : kb + static_cast<size_t>(p) * kAttnHd, kr);
+        sc[p] = dot_f16_128(qs, kr) * a.scale;
+    }
+    __syncthreads();
+
+    if (wave < n_chunks) {  // the running maximum of chunk `wave`
+        const uint32_t s0 = wave * chunk, s1 = min(min(s0 + chunk, n_kv), seq);
+        float carry = -__builtin_inff();
+        for (uint32_t base = s0; base < s1; base += 64u) {
+            const uint32_t p = base + lane;
+            float v = p < s1 ? sc[p] : -__builtin_inff();
+#pragma unroll
+            for (int sh = 1; sh < 64; sh <<= 1) {
+                const float o = __shfl_up(v, sh);
+                if (lane >= static_cast<uint32_t>(sh)) v = v > o ? v : o;
+            }
+            v = v > carry ? v : carry;
+            if (p < s1) pm[p] = v;
+            carry = __shfl(v, 63);
+        }
+    }
+    __syncthreads();
+
+    for (uint32_t p = tid; p < seq; p += kAttnWaves * 64u) {
+        const uint32_t s0 = split ? p / chunk * chunk : 0u;
+        const float prev = p == s0 ? -__builtin_inff() : pm[p - 1];
+        const float s = sc[p];
+        sc[p] = s > prev ? -glibc_expf(prev - s) : glibc_expf(s - prev);
+    }
+    __syncthreads();
+
     float y = 0.0f, ssum = 0.0f;
     if (st < en) {
         uint16_t* buf = vbuf[wave];
-        const uint16_t* vsrc = vb + half * 64u + (lane & 7u) * 8u;
-        u32x4 r[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t p = min(st + 8u * j + (lane >> 3), en - 1u);
-            r[j] = *reinterpret_cast<const u32x4*>(vsrc + static_cast<size_t>(p) * kAttnHd);
-        }
         for (uint32_t base = st; base < en; base += kAttnWin) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(buf + (8u * j + (lane >> 3)) * 64u + (lane & 7u) * 8u) = r[j];
             if (base + kAttnWin < en) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t p = min(base + kAttnWin + 8u * j + (lane >> 3), en - 1u);
-                    r[j] = *reinterpret_cast<const u32x4*>(vsrc + static_cast<size_t>(p) * kAttnHd);
-                }
+                for (int j = 0; j < 8; ++j) r[j] = load_v(min(base + kAttnWin + 8u * j + (lane >> 3), en - 1u));
             }
-            const uint32_t n = min(kAttnWin, en - base);
+            const uint32_t n = min(kAttnWin, en - base);  // wave-uniform
             const float f = lane < n ? sc[base + lane] : 0.0f;
-            if (__ballot(__builtin_signbit(f)) == 0) {  // no new maximum in the window: ms = 1
-                for (uint32_t i = 0; i < n; ++i) {
-                    const float e = sc[base + i];
-                    const float v = f16_f32(buf[i * 64u + lane]);
+            const uint32_t nb = n & ~(kAttnBatch - 1u);
+            // Whole batches of kAttnBatch positions, their LDS operands read before the serial chain uses them; a
+            // window without a new maximum (ms = 1 throughout) takes the shorter chain.
+            if (__ballot(__builtin_signbit(f)) == 0) {
+                auto step = [&](float e, float v) {
                     y = r16(__builtin_fmaf(v, e, y));
                     ssum = ssum + e;
+                };
+                for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
+                    float fe[kAttnBatch], fv[kAttnBatch];
+#pragma unroll
+                    for (uint32_t u = 0; u < kAttnBatch; ++u) {
+                        fe[u] = sc[base + i0 + u];
+                        fv[u] = f16_f32(buf[(i0 + u) * 64u + lane]);
+                    }
+#pragma unroll
+                    for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
                 }
+                for (uint32_t i = nb; i < n; ++i) step(sc[base + i], f16_f32(buf[i * 64u + lane]));
             } else {
-                for (uint32_t i = 0; i < n; ++i) {
-                    const float fi = sc[base + i];
+                auto step = [&](float fi, float v) {
                     const bool nm = __builtin_signbit(fi);
                     const float e = __builtin_fabsf(fi);
                     const float ms = nm ? e : 1.0f, vs = nm ? 1.0f : e;
-                    const float v = f16_f32(buf[i * 64u + lane]);
                     y = r16(y * ms);
                     y = r16(__builtin_fmaf(v, vs, y));
                     ssum = __builtin_fmaf(ssum, ms, vs);
+                };
+                for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
+                    float fe[kAttnBatch], fv[kAttnBatch];
+#pragma unroll
+                    for (uint32_t u = 0; u < kAttnBatch; ++u) {
+                        fe[u] = sc[base + i0 + u];
+                        fv[u] = f16_f32(buf[(i0 + u) * 64u + lane]);
+                    }
+#pragma unroll
+                    for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
                 }
+                for (uint32_t i = nb; i < n; ++i) step(sc[base + i], f16_f32(buf[i * 64u + lane]));
             }
         }
     }
@@ -443,106 +818,105 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
 
 // ---- head and greedy argmax ----------------------------------------------------------------------------------------------
 
-// logits[r] = ggml_vec_dot_bf16(x, emb[r]) (ops.rs:669-713): lane (r, j) of four per row holds the eight lanes of
-// accumulator j, acc + x*y rounded separately, then (a0 + a2) + (a1 + a3) across the four lanes and
-// ((l0+l4) + (l2+l6)) + ((l1+l5) + (l3+l7)) inside one. hidden must be a multiple of 32.
-__global__ __launch_bounds__(256) void head_kernel(const uint16_t* __restrict__ xb, const uint16_t* __restrict__ emb,
-                                                   uint32_t hidden, uint32_t vocab, float* __restrict__ logits) {
-    __shared__ uint4 xs[kNormMax / 8];
-    for (uint32_t i = threadIdx.x; i < hidden / 8u; i += 256u) xs[i] = reinterpret_cast<const uint4*>(xb)[i];
-    __syncthreads();
-    const uint32_t r = blockIdx.x * 64u + (threadIdx.x >> 2), j = threadIdx.x & 3u;
-    if (r >= vocab) return;
-    const u32x4* row = reinterpret_cast<const u32x4*>(emb + static_cast<size_t>(r) * hidden);
-    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (uint32_t i = 0; i < hidden / 32u; ++i) {
-        const u32x4 w = __builtin_nontemporal_load(row + 4u * i + j);
-        const uint4 x = xs[4u * i + j];
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xx[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (int l = 0; l < 8; ++l) {
-            const float wf = bits_f32((ww[l >> 1] >> ((l & 1) * 16)) << 16);
-            const float xf = bits_f32((xx[l >> 1] >> ((l & 1) * 16)) << 16);
-            const float p = xf * wf;
-            acc[l] = acc[l] + p;
-        }
-    }
-    // (a0 + a2) + (a1 + a3): lanes j and j ^ 2, then j and j ^ 1
-#pragma unroll
-    for (int l = 0; l < 8; ++l) {
-        acc[l] = acc[l] + __shfl_xor(acc[l], 2);
-        acc[l] = acc[l] + __shfl_xor(acc[l], 1);
-    }
-    if (j == 0) {
-        const float g0 = acc[4] + acc[0], g1 = acc[5] + acc[1], g2 = acc[6] + acc[2], g3 = acc[7] + acc[3];
-        logits[r] = (g0 + g2) + (g1 + g3);
-    }
+// Ordered key of a logit for the greedy argmax (sampler.rs:73-83: max_val = logits[0], then the first i with
+// logits[i] > max_val): larger values first, then lower indices; -0 counts as +0, NaN never wins except at index 0,
+// where it wins outright (the reference then returns 0). The maximum key over all rows names the token (0 if none).
+__device__ __forceinline__ unsigned long long logit_key(float v, uint32_t r) {
+    if (v != v) return r == 0 ? ~0ull : 0ull;
+    uint32_t u = f32_bits(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<unsigned long long>(u) << 32) | (0xffffffffu - r);
 }
 
-// Greedy sampling (sampler.rs:73-83): the first index of the maximum; NaN never replaces (a NaN first logit wins).
-// Then the loop state advances: the token is recorded once the prompt is consumed and the position moves on.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, uint32_t vocab, Ctl* ctl,
-                                                      uint32_t* __restrict__ out_tokens) {
-    __shared__ float bv[16];
-    __shared__ uint32_t bi[16];
-    const uint32_t tid = threadIdx.x;
-    float v = -__builtin_inff();
-    uint32_t idx = 0xffffffffu;
-    for (uint32_t i = tid; i < vocab; i += 1024u) {
-        const float x = logits[i];
-        if (x > v || (idx == 0xffffffffu && x == v)) {
-            v = x;
-            idx = i;
+struct HeadArgs {
+    StageInput in;         // the final residual add (x + down of the last layer) and the output norm
+    const uint16_t* emb;   // tied bf16 embedding: vocab x hidden
+    uint32_t hidden, vocab;
+    float* logits;
+    Ctl* ctl;
+    uint32_t* out_tokens;
+    unsigned long long* key;  // argmax across workgroups: the largest logit_key (0 between steps)
+    uint32_t* ticket;         // workgroups done (0 between steps)
+};
+
+// Every workgroup computes the normed bf16 vector itself, then rows r0 + tid / 4: logits[r] = ggml_vec_dot_bf16(x,
+// emb[r]) (ops.rs:669-713): lane (r, j) of four per row holds the eight lanes of accumulator j, acc + x*y rounded
+// separately, then (a0 + a2) + (a1 + a3) across the four lanes and ((l0+l4) + (l2+l6)) + ((l1+l5) + (l3+l7)) inside
+// one. hidden must be a multiple of 32. The workgroup's best key goes into *key with an atomic maximum; the last
+// workgroup to finish reads the winner, resets key and ticket, and advances the loop state: the token is recorded once
+// the prompt is consumed and the position moves on.
+__global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
+    __shared__ InputLds s;
+    __shared__ uint4 xs[kNormMax / 8];
+    __shared__ unsigned long long wbest[kNT / 64];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    InputRegs r;
+    stage_load(a.in, r);
+    (void)stage_norm(a.in, r, s, false);
+    __syncthreads();
+    uint16_t* xh = reinterpret_cast<uint16_t*>(xs);
+    for (uint32_t i = tid; i < a.hidden; i += kNT) xh[i] = f32_bf16(s.ys[i]);
+    __syncthreads();
+    const uint32_t j = tid & 3u;
+    unsigned long long best = 0;
+    for (uint32_t r0 = blockIdx.x * (kNT / 4u); r0 < a.vocab; r0 += gridDim.x * (kNT / 4u)) {
+        const uint32_t r = r0 + (tid >> 2);
+        const u32x4* row = reinterpret_cast<const u32x4*>(a.emb + static_cast<size_t>(min(r, a.vocab - 1u)) * a.hidden);
+        float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (uint32_t i = 0; i < a.hidden / 32u; ++i) {
+            const u32x4 w = __builtin_nontemporal_load(row + 4u * i + j);
+            const uint4 x = xs[4u * i + j];
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xx[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                const float wf = bits_f32((ww[l >> 1] >> ((l & 1) * 16)) << 16);
+                const float xf = bits_f32((xx[l >> 1] >> ((l & 1) * 16)) << 16);
+                const float p = xf * wf;
+                acc[l] = acc[l] + p;
+            }
+        }
+        // (a0 + a2) + (a1 + a3): lanes j and j ^ 2, then j and j ^ 1
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            acc[l] = acc[l] + __shfl_xor(acc[l], 2);
+            acc[l] = acc[l] + __shfl_xor(acc[l], 1);
+        }
+        if (j == 0 && r < a.vocab) {
+            const float g0 = acc[4] + acc[0], g1 = acc[5] + acc[1], g2 = acc[6] + acc[2], g3 = acc[7] + acc[3];
+            const float v = (g0 + g2) + (g1 + g3);
+            a.logits[r] = v;
+            const unsigned long long k = logit_key(v, r);
+            if (k > best) best = k;
         }
     }
     for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(v, off);
-        const uint32_t oi = __shfl_xor(idx, off);
-        if (ov > v || (ov == v && oi < idx)) {
-            v = ov;
-            idx = oi;
-        }
+        const unsigned long long o = __shfl_xor(best, off);
+        if (o > best) best = o;
     }
-    if ((tid & 63u) == 0) {
-        bv[tid >> 6] = v;
-        bi[tid >> 6] = idx;
-    }
+    if (lane == 0) wbest[wave] = best;
     __syncthreads();
-    if (tid == 0) {
-        for (int w = 1; w < 16; ++w)
-            if (bv[w] > v || (bv[w] == v && bi[w] < idx)) {
-                v = bv[w];
-                idx = bi[w];
-            }
-        if (logits[0] != logits[0] || idx == 0xffffffffu) idx = 0;
-        const uint32_t pos = ctl->pos;
-        ctl->token = idx;
-        if (pos + 1 >= ctl->n_prompt) {
-            const uint32_t k = pos + 1 - ctl->n_prompt;
-            if (k < ctl->n_out) out_tokens[k] = idx;
-        }
-        ctl->pos = pos + 1;
+    if (tid != 0) return;
+    for (int w = 1; w < kNT / 64; ++w)
+        if (wbest[w] > best) best = wbest[w];
+    atomicMax(a.key, best);
+    __threadfence();
+    if (atomicAdd(a.ticket, 1u) != gridDim.x - 1u) return;
+    const unsigned long long k = atomicExch(a.key, 0ull);
+    atomicExch(a.ticket, 0u);
+    const uint32_t idx = k == 0 ? 0u : 0xffffffffu - static_cast<uint32_t>(k);
+    const uint32_t pos = a.ctl->pos;
+    a.ctl->token = idx;
+    if (pos + 1 >= a.ctl->n_prompt) {
+        const uint32_t t = pos + 1 - a.ctl->n_prompt;
+        if (t < a.ctl->n_out) a.out_tokens[t] = idx;
     }
+    a.ctl->pos = pos + 1;
 }
 
 // ---- launches ----------------------------------------------------------------------------------------------------------------
 
-int launch_norm(const NormArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(norm_quant_kernel, dim3(1), dim3(kNormThreads), 0, s, a);
-    VX_HIP(hipGetLastError());
-    return VX_OK;
-}
-
-int launch_embed(const void* ctl, const uint32_t* prompt, const uint16_t* emb, uint32_t hidden, float* x, hipStream_t s) {
-    hipLaunchKernelGGL(embed_kernel, dim3((hidden + 255u) / 256u), dim3(256), 0, s, static_cast<const Ctl*>(ctl), prompt,
-                       emb, hidden, x);
-    VX_HIP(hipGetLastError());
-    return VX_OK;
-}
-
-int launch_rope_kv(const RopeArgs& a, hipStream_t s) {
-    const uint32_t n = std::max(a.n_heads * a.head_dim / 2u + a.n_kv_heads * a.head_dim / 2u, a.n_kv_heads * a.head_dim);
-    hipLaunchKernelGGL(rope_kv_kernel, dim3((n + 255u) / 256u), dim3(256), 0, s, a);
+int launch_dgemv(const DStageArgs& a, hipStream_t s) {
+    hipLaunchKernelGGL(dgemv_kernel, dim3(a.total_items), dim3(kNT), 0, s, a);
     VX_HIP(hipGetLastError());
     return VX_OK;
 }
@@ -553,14 +927,8 @@ int launch_attention(const AttnArgs& a, hipStream_t s) {
     return VX_OK;
 }
 
-int launch_head(const uint16_t* xb, const uint16_t* emb, uint32_t hidden, uint32_t vocab, float* logits, hipStream_t s) {
-    hipLaunchKernelGGL(head_kernel, dim3((vocab + 63u) / 64u), dim3(256), 0, s, xb, emb, hidden, vocab, logits);
-    VX_HIP(hipGetLastError());
-    return VX_OK;
-}
-
-int launch_argmax(const float* logits, uint32_t vocab, void* ctl, uint32_t* out_tokens, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, vocab, static_cast<Ctl*>(ctl), out_tokens);
+int launch_head(const HeadArgs& a, uint32_t grid, hipStream_t s) {
+    hipLaunchKernelGGL(head_kernel, dim3(grid), dim3(kNT), 0, s, a);
     VX_HIP(hipGetLastError());
     return VX_OK;
 }
@@ -582,14 +950,7 @@ int launch_expf(const float* x, size_t n, float* out, hipStream_t s) {
 constexpr uint32_t kDecoderMagic = 0x56584431u;  // "VXD1"
 constexpr int kProjKinds = 7;
 constexpr int kNormKinds = 4;
-
-// The GEMV launches of one layer stage (q/k/v, o, gate/up, down) with their K-split finish.
-struct StageLaunch {
-    LaunchArgs a;
-    uint32_t max_rows;
-    const uint32_t* split;
-    uint32_t n_split;
-};
+constexpr int kStages = 4;  // projection stages of a layer: q/k/v, o, gate/up, down
 
 }  // namespace vx
 
@@ -604,17 +965,17 @@ struct vx_decoder {
     uint16_t* d_emb;
     float* d_rope;
     uint16_t *d_kc, *d_vc;            // [layer][kv_head][max_ctx][head_dim]
-    float *d_x, *d_q, *d_k, *d_v, *d_att, *d_o, *d_gate, *d_up, *d_down, *d_logits;
-    uint16_t *d_qh, *d_xb;
-    uint8_t* d_stage[4];              // staged activations of the q/k/v, o, gate/up and down inputs
-    float* d_as;                      // their activation scales
+    float *d_xa, *d_xb;               // the residual stream (written alternately by the stages that add to it)
+    int32_t* d_part[vx::kProjKinds];  // K-slice sums of the q, k, v, o, gate, up, down outputs, reused by every layer
+    uint32_t kslices[vx::kProjKinds];
+    float* d_as;                      // activation scale of each projection stage, reused by every layer
+    float *d_att, *d_logits;
+    unsigned long long* d_key;        // argmax key and ticket of the head kernel
+    uint32_t* d_ticket;
     vx::Ctl* d_ctl;
     uint32_t* d_prompt;
     uint32_t* d_tokens;
-    vx::Job* d_jobs;
-    int32_t* d_part;
-    uint32_t* d_split;
-    std::vector<vx::StageLaunch> stages;  // [layer * 4 + stage]
+    std::vector<vx::DStageArgs> stages;  // [layer * 4 + stage]
     vx::Ctl* h_ctl;                   // pinned
     hipStream_t stream;
     hipGraph_t graph;
@@ -653,12 +1014,13 @@ static void destroy_decoder(vx_decoder* d) {
         if (m) (void)vx_matrix_free(m);
     for (auto* p : d->norms)
         if (p) (void)hipFree(p);
-    void* bufs[] = {d->d_emb,  d->d_rope, d->d_kc,    d->d_vc,     d->d_x,      d->d_q,      d->d_k,      d->d_v,
-                    d->d_att,  d->d_o,    d->d_gate,  d->d_up,     d->d_down,   d->d_logits, d->d_qh,     d->d_xb,
-                    d->d_as,   d->d_ctl,  d->d_prompt, d->d_tokens, d->d_jobs,  d->d_part,   d->d_split,  d->d_stage[0],
-                    d->d_stage[1], d->d_stage[2], d->d_stage[3]};
+    void* bufs[] = {d->d_emb, d->d_rope, d->d_kc,  d->d_vc,     d->d_xa,     d->d_xb,     d->d_att,   d->d_logits,
+                    d->d_key, d->d_ctl,  d->d_prompt, d->d_tokens};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
+    for (int32_t* b : d->d_part)
+        if (b) (void)hipFree(b);
+    if (d->d_as) (void)hipFree(d->d_as);
     if (d->h_ctl) (void)hipHostFree(d->h_ctl);
     if (d->stream) (void)hipStreamDestroy(d->stream);
     d->magic = 0;
@@ -726,10 +1088,11 @@ static int create_decoder(const vx_decoder_config_t* c, vx_decoder_t** out) {
     if (c->max_ctx == 0 || c->max_ctx > kAttnMaxCtx) VX_FAIL(VX_ERR_UNSUPPORTED, "max_ctx must be in 1..=%u", kAttnMaxCtx);
     if (c->hidden == 0 || c->hidden % 32 || c->hidden > kNormMax)
         VX_FAIL(VX_ERR_UNSUPPORTED, "hidden must be a positive multiple of 32 up to %u", kNormMax);
-    if (static_cast<size_t>(c->n_heads) * c->head_dim > kNormMax || c->ffn == 0 || c->ffn > kNormMax)
-        VX_FAIL(VX_ERR_UNSUPPORTED, "n_heads * head_dim and ffn must be in 1..=%u", kNormMax);
+    if (static_cast<size_t>(c->n_heads) * c->head_dim > kNormMax || c->ffn == 0 || c->ffn > kNormMax || c->ffn % 4)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "n_heads * head_dim and ffn must be multiples of 4 in 1..=%u", kNormMax);
     if (c->vocab == 0 || c->vocab > (1u << 24)) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "vocab must be in 1..=2^24");
     if (!(c->rms_eps >= 0.0f) || !(c->rope_theta > 0.0f)) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "rms_eps must be >= 0 and rope_theta > 0");
+    static_assert(kNormMax / 160 * 32 + 16 <= (kStChunks - 4) * 16, "the staged input of kNormMax columns fits in LDS");
     DeviceInfo di;
     VX_TRY(device_info(&di));
     vx_decoder* d = new vx_decoder();
@@ -743,27 +1106,20 @@ static int create_decoder(const vx_decoder_config_t* c, vx_decoder_t** out) {
     d->norms.assign(static_cast<size_t>(c->n_layers + 1) * kNormKinds, nullptr);
     d->norm_set.assign(d->norms.size(), 0);
     d->emb_set.assign(1, 0);
-    const size_t L = c->n_layers, H = c->hidden, F = c->ffn;
+    const size_t L = c->n_layers, H = c->hidden;
     const size_t kv_elems = L * d->kvd * c->max_ctx;
     hipError_t e = dalloc(d, &d->d_emb, static_cast<size_t>(c->vocab) * H * 2);
     if (e == hipSuccess) e = dalloc(d, &d->d_rope, static_cast<size_t>(c->max_ctx) * c->head_dim * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_kc, kv_elems * 2);
     if (e == hipSuccess) e = dalloc(d, &d->d_vc, kv_elems * 2);
-    if (e == hipSuccess) e = dalloc(d, &d->d_x, H * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_q, d->qd * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_k, d->kvd * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_v, d->kvd * 4);
+    if (e == hipSuccess) e = dalloc(d, &d->d_xa, H * 4);
+    if (e == hipSuccess) e = dalloc(d, &d->d_xb, H * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_att, d->qd * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_o, H * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_gate, F * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_up, F * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_down, H * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_logits, static_cast<size_t>(c->vocab) * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_qh, d->qd * 2);
-    if (e == hipSuccess) e = dalloc(d, &d->d_xb, H * 2);
-    const size_t stage_cols[4] = {H, d->qd, H, F};
-    for (int s = 0; s < 4 && e == hipSuccess; ++s) e = dalloc(d, &d->d_stage[s], staged_bytes(stage_cols[s]));
-    if (e == hipSuccess) e = dalloc(d, &d->d_as, 4 * sizeof(float));
+    if (e == hipSuccess) e = dalloc(d, &d->d_as, kStages * sizeof(float));
+    if (e == hipSuccess) e = dalloc(d, &d->d_key, 16);
+    if (e == hipSuccess) e = hipMemset(d->d_key, 0, 16);
+    if (e == hipSuccess) d->d_ticket = reinterpret_cast<uint32_t*>(d->d_key + 1);
     if (e == hipSuccess) e = dalloc(d, &d->d_ctl, sizeof(Ctl));
     if (e == hipSuccess) e = dalloc(d, &d->d_prompt, static_cast<size_t>(c->max_ctx) * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_tokens, static_cast<size_t>(c->max_ctx) * 4);
@@ -782,155 +1138,157 @@ static int create_decoder(const vx_decoder_config_t* c, vx_decoder_t** out) {
     return VX_OK;
 }
 
-// The GEMV plans of every stage: each job's K slices are chosen so that a stage offers about one work item per CU in
-// proportion to its weight bytes (bs = 1 matrices are small: one tile group per K slice would leave most CUs idle).
-static int build_plans(vx_decoder* d) {
-    const size_t L = d->cfg.n_layers;
-    static const int kStageKinds[4][3] = {{VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}, {VX_PROJ_O, -1, -1},
-                                          {VX_PROJ_GATE, VX_PROJ_UP, -1}, {VX_PROJ_DOWN, -1, -1}};
-    float* outs[kProjKinds] = {d->d_q, d->d_k, d->d_v, d->d_o, d->d_gate, d->d_up, d->d_down};
-    std::vector<Job> jobs;
-    std::vector<uint32_t> split;
-    std::vector<size_t> job_first(L * 4), split_first(L * 4);
-    std::vector<uint32_t> stage_jobs(L * 4), stage_items(L * 4), stage_rows(L * 4), stage_split(L * 4);
-    size_t part_ints = 0;
-    for (size_t l = 0; l < L; ++l)
-        for (int s = 0; s < 4; ++s) {
-            const size_t si = l * 4 + s;
-            size_t stage_bytes = 0;
-            for (int k : kStageKinds[s])
-                if (k >= 0) stage_bytes += d->proj[l * kProjKinds + k]->g.device_bytes;
-            job_first[si] = jobs.size();
-            split_first[si] = split.size();
-            uint32_t items = 0, max_rows = 0;
-            size_t part = 0;
+static StageInput stage_input(const vx_decoder* d, uint32_t kind, size_t n, const float* x_in, float* x_out,
+                              const float* gamma) {
+    StageInput p{};
+    p.kind = kind;
+    p.n = static_cast<uint32_t>(n);
+    p.x_in = x_in;
+    p.x_out = x_out;
+    p.gamma = gamma;
+    p.eps = d->cfg.rms_eps;
+    return p;
+}
+
+static const int kStageKinds[kStages][kMaxStageJobs] = {{VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}, {VX_PROJ_O, -1, -1},
+                                                       {VX_PROJ_GATE, VX_PROJ_UP, -1}, {VX_PROJ_DOWN, -1, -1}};
+static int stage_of(int kind) {
+    for (int s = 0; s < kStages; ++s)
+        for (int k : kStageKinds[s])
+            if (k == kind) return s;
+    return 0;
+}
+
+// Projection `kind` of `layer` as its consumers read it.
+static ProjOut proj_out(const vx_decoder* d, size_t layer, int kind) {
+    const vx_matrix* m = d->proj[layer * kProjKinds + kind];
+    ProjOut o{};
+    o.part = d->d_part[kind];
+    o.as = d->d_as + stage_of(kind);
+    o.ws = m->weight_scale;
+    o.kslices = d->kslices[kind];
+    o.stride = static_cast<uint32_t>(m->g.padded_rows);
+    return o;
+}
+
+// The stage launches of every layer. A stage's work items are (64-row tile, K slice) pairs of its projections; the K
+// split gives each stage about one item per CU (a 2560-row projection has only 40 tiles), within the slice counts its
+// consumers read (kMaxSlicesB for the ReLU^2 inputs, kMaxSlicesA otherwise).
+static int build_stages(vx_decoder* d) {
+    const size_t L = d->cfg.n_layers, H = d->cfg.hidden, F = d->cfg.ffn;
+    for (int s = 0; s < kStages; ++s) {
+        uint32_t tiles = 0, min_chunks = 0xffffffffu;
+        for (int k : kStageKinds[s]) {
+            if (k < 0) continue;
+            tiles += static_cast<uint32_t>(d->proj[k]->g.n_tiles);
+            min_chunks = std::min(min_chunks, static_cast<uint32_t>(d->proj[k]->g.n_chunks));
+            if (d->proj[k]->g.n_chunks > static_cast<size_t>(kDPer) * kTileGroup)
+                VX_FAIL(VX_ERR_INTERNAL, "projection %d has %zu chunks per row", k, d->proj[k]->g.n_chunks);
+        }
+        const uint32_t limit = s == 2 ? kMaxSlicesB : kMaxSlicesA;
+        uint32_t ks = (static_cast<uint32_t>(d->num_cus) + tiles / 2) / tiles;
+        ks = std::max(1u, std::min({ks, limit, min_chunks}));
+        for (int k : kStageKinds[s]) {
+            if (k < 0) continue;
+            const Geometry& g = d->proj[k]->g;
+            const uint32_t nc = static_cast<uint32_t>(g.n_chunks);
+            const uint32_t sc = (nc + ks - 1) / ks;
+            d->kslices[k] = (nc + sc - 1) / sc;
+            if (d->d_part[k]) (void)hipFree(d->d_part[k]);
+            d->d_part[k] = nullptr;
+            VX_HIP(hipMalloc(&d->d_part[k], static_cast<size_t>(d->kslices[k]) * g.padded_rows * 4));
+        }
+    }
+    d->stages.assign(L * kStages, DStageArgs{});
+    for (size_t l = 0; l < L; ++l) {
+        const float* const* nw = d->norms.data() + l * kNormKinds;
+        for (int s = 0; s < kStages; ++s) {
+            DStageArgs& a = d->stages[l * kStages + s];
+            uint32_t items = 0;
             for (int k : kStageKinds[s]) {
                 if (k < 0) continue;
                 const vx_matrix* m = d->proj[l * kProjKinds + k];
-                const uint32_t target = static_cast<uint32_t>(
-                    (static_cast<uint64_t>(d->num_cus) * m->g.device_bytes + stage_bytes - 1) / stage_bytes);
-                Job j{};
-                plan_job(j, m->g, target);
+                DJob& j = a.job[a.n_jobs++];
                 j.w = m->d_w;
                 j.dsum = m->d_dsum;
-                j.staged = d->d_stage[s];
-                j.out = outs[k];
-                j.act_scale = d->d_as + s;
-                j.weight_scale = m->weight_scale;
-                j.out_kind = kOutF32Dev;
+                j.part = d->d_part[k];
+                j.rows = static_cast<uint32_t>(m->g.rows);
+                j.padded_rows = static_cast<uint32_t>(m->g.padded_rows);
+                j.n_tiles = static_cast<uint32_t>(m->g.n_tiles);
+                j.n_chunks = static_cast<uint32_t>(m->g.n_chunks);
+                j.kslices = d->kslices[k];
+                j.slice_chunks = (j.n_chunks + j.kslices - 1) / j.kslices;
                 j.item_begin = items;
-                items += job_items(j);
-                if (j.kslices > 1) {
-                    j.part = reinterpret_cast<int32_t*>(part);  // offset into the shared partial buffer, rebased below
-                    part += static_cast<size_t>(j.kslices) * j.padded_rows;
-                    split.push_back(static_cast<uint32_t>(jobs.size() - job_first[si]));
-                    max_rows = std::max(max_rows, j.rows);
-                }
-                jobs.push_back(j);
+                items += j.n_tiles * j.kslices;
             }
-            stage_jobs[si] = static_cast<uint32_t>(jobs.size() - job_first[si]);
-            stage_items[si] = items;
-            stage_rows[si] = max_rows;
-            stage_split[si] = static_cast<uint32_t>(split.size() - split_first[si]);
-            part_ints = std::max(part_ints, part);
+            a.total_items = items;
+            StageInput& in = a.in;
+            if (s == 0 && l == 0) {  // embedding -> attention norm
+                in = stage_input(d, kInEmbed, H, nullptr, d->d_xa, nw[VX_NORM_ATTN]);
+                in.ctl = d->d_ctl;
+                in.prompt = d->d_prompt;
+                in.emb = d->d_emb;
+            } else if (s == 0) {  // x + down of the previous layer -> attention norm
+                in = stage_input(d, kInResidual, H, d->d_xb, d->d_xa, nw[VX_NORM_ATTN]);
+                in.a = proj_out(d, l - 1, VX_PROJ_DOWN);
+            } else if (s == 1) {  // attention output -> attention sub-norm
+                in = stage_input(d, kInPlain, d->qd, d->d_att, nullptr, nw[VX_NORM_ATTN_SUB]);
+            } else if (s == 2) {  // x + o -> FFN norm
+                in = stage_input(d, kInResidual, H, d->d_xa, d->d_xb, nw[VX_NORM_FFN]);
+                in.a = proj_out(d, l, VX_PROJ_O);
+            } else {  // relu2(gate) * up -> FFN sub-norm
+                in = stage_input(d, kInRelu2Mul, F, nullptr, nullptr, nw[VX_NORM_FFN_SUB]);
+                in.a = proj_out(d, l, VX_PROJ_GATE);
+                in.b = proj_out(d, l, VX_PROJ_UP);
+            }
+            a.tbr = static_cast<uint32_t>(tile_row_bytes(in.n));
+            a.dbr = static_cast<uint32_t>(device_row_bytes(in.n));
+            a.as_out = d->d_as + s;
         }
-    if (d->d_jobs) (void)hipFree(d->d_jobs);
-    if (d->d_part) (void)hipFree(d->d_part);
-    if (d->d_split) (void)hipFree(d->d_split);
-    d->d_jobs = nullptr;
-    d->d_part = nullptr;
-    d->d_split = nullptr;
-    VX_HIP(hipMalloc(&d->d_jobs, jobs.size() * sizeof(Job)));
-    VX_HIP(hipMalloc(&d->d_part, std::max<size_t>(part_ints, 1) * 4));
-    VX_HIP(hipMalloc(&d->d_split, std::max<size_t>(split.size(), 1) * 4));
-    for (auto& j : jobs)
-        if (j.kslices > 1) j.part = d->d_part + reinterpret_cast<size_t>(j.part);
-    VX_HIP(hipMemcpy(d->d_jobs, jobs.data(), jobs.size() * sizeof(Job), hipMemcpyHostToDevice));
-    if (!split.empty()) VX_HIP(hipMemcpy(d->d_split, split.data(), split.size() * 4, hipMemcpyHostToDevice));
-    d->stages.assign(L * 4, StageLaunch{});
-    for (size_t si = 0; si < L * 4; ++si) {
-        StageLaunch& st = d->stages[si];
-        st.a.jobs = d->d_jobs + job_first[si];
-        st.a.n_jobs = stage_jobs[si];
-        st.a.total_items = stage_items[si];
-        st.max_rows = stage_rows[si];
-        st.split = d->d_split + split_first[si];
-        st.n_split = stage_split[si];
     }
     return VX_OK;
-}
-
-static int run_stage(const vx_decoder* d, size_t layer, int s, hipStream_t st) {
-    const StageLaunch& sl = d->stages[layer * 4 + s];
-    return launch_gemv(sl.a, sl.max_rows, sl.split, sl.n_split, d->num_cus, st);
-}
-
-static NormArgs norm_args(const vx_decoder* d, float* a, const float* b, uint32_t input, const float* gamma, size_t n,
-                          int stage) {
-    NormArgs p{};
-    p.a = a;
-    p.b = b;
-    p.gamma = gamma;
-    p.n = static_cast<uint32_t>(n);
-    p.eps = d->cfg.rms_eps;
-    p.input = input;
-    p.quantize = stage >= 0 ? 1u : 0u;
-    p.staged = stage >= 0 ? d->d_stage[stage] : nullptr;
-    p.act_scale = stage >= 0 ? d->d_as + stage : nullptr;
-    p.out_bf16 = stage >= 0 ? nullptr : d->d_xb;
-    p.tbr = static_cast<uint32_t>(tile_row_bytes(n));
-    p.dbr = static_cast<uint32_t>(device_row_bytes(n));
-    return p;
 }
 
 // Enqueues one decode step on `st` (also the sequence captured into the step graph).
 static int record_step(const vx_decoder* d, hipStream_t st) {
     const vx_decoder_config_t& c = d->cfg;
-    const size_t L = c.n_layers, H = c.hidden;
-    VX_TRY(launch_embed(d->d_ctl, d->d_prompt, d->d_emb, c.hidden, d->d_x, st));
+    const size_t L = c.n_layers;
     const size_t layer_kv = d->kvd * c.max_ctx;
     for (size_t l = 0; l < L; ++l) {
-        float* const* nw = d->norms.data() + l * kNormKinds;
-        VX_TRY(launch_norm(norm_args(d, d->d_x, d->d_down, l == 0 ? kInPlain : kInResidual, nw[VX_NORM_ATTN], H, 0), st));
-        VX_TRY(run_stage(d, l, 0, st));
-        RopeArgs r{};
-        r.ctl = d->d_ctl;
-        r.q = d->d_q;
-        r.k = d->d_k;
-        r.v = d->d_v;
-        r.rope = d->d_rope;
-        r.qh = d->d_qh;
-        r.kc = d->d_kc + l * layer_kv;
-        r.vc = d->d_vc + l * layer_kv;
-        r.n_heads = c.n_heads;
-        r.n_kv_heads = c.n_kv_heads;
-        r.head_dim = c.head_dim;
-        r.max_ctx = c.max_ctx;
-        VX_TRY(launch_rope_kv(r, st));
+        VX_TRY(launch_dgemv(d->stages[l * kStages + 0], st));
         AttnArgs at{};
         at.ctl = d->d_ctl;
-        at.qh = d->d_qh;
-        at.kc = r.kc;
-        at.vc = r.vc;
+        at.q = proj_out(d, l, VX_PROJ_Q);
+        at.k = proj_out(d, l, VX_PROJ_K);
+        at.v = proj_out(d, l, VX_PROJ_V);
+        at.rope = d->d_rope;
+        at.kc = d->d_kc + l * layer_kv;
+        at.vc = d->d_vc + l * layer_kv;
         at.out = d->d_att;
         at.n_heads = c.n_heads;
         at.gqa = c.n_heads / c.n_kv_heads;
         at.max_ctx = c.max_ctx;
         at.scale = 1.0f / sqrtf(static_cast<float>(c.head_dim));
         VX_TRY(launch_attention(at, st));
-        VX_TRY(launch_norm(norm_args(d, d->d_att, nullptr, kInPlain, nw[VX_NORM_ATTN_SUB], d->qd, 1), st));
-        VX_TRY(run_stage(d, l, 1, st));
-        VX_TRY(launch_norm(norm_args(d, d->d_x, d->d_o, kInResidual, nw[VX_NORM_FFN], H, 2), st));
-        VX_TRY(run_stage(d, l, 2, st));
-        VX_TRY(launch_norm(norm_args(d, d->d_gate, d->d_up, kInRelu2Mul, nw[VX_NORM_FFN_SUB], c.ffn, 3), st));
-        VX_TRY(run_stage(d, l, 3, st));
+        for (int s = 1; s < kStages; ++s) VX_TRY(launch_dgemv(d->stages[l * kStages + s], st));
     }
-    VX_TRY(launch_norm(norm_args(d, d->d_x, d->d_down, kInResidual, d->norms[L * kNormKinds], H, -1), st));
-    VX_TRY(launch_head(d->d_xb, d->d_emb, c.hidden, c.vocab, d->d_logits, st));
-    return launch_argmax(d->d_logits, c.vocab, d->d_ctl, d->d_tokens, st);
+    HeadArgs h{};
+    h.in = stage_input(d, kInResidual, c.hidden, d->d_xb, nullptr, d->norms[L * kNormKinds]);
+    h.in.a = proj_out(d, L - 1, VX_PROJ_DOWN);
+    h.emb = d->d_emb;
+    h.hidden = c.hidden;
+    h.vocab = c.vocab;
+    h.logits = d->d_logits;
+    h.ctl = d->d_ctl;
+    h.out_tokens = d->d_tokens;
+    h.key = d->d_key;
+    h.ticket = d->d_ticket;
+    const uint32_t rows_per_wg = kNT / 4;
+    const uint32_t grid = std::min<uint32_t>((c.vocab + rows_per_wg - 1) / rows_per_wg, 2u * static_cast<uint32_t>(d->num_cus));
+    return launch_head(h, grid, st);
 }
 
-// Builds the plans and captures the step graph once every weight is set.
+// Builds the stage launches and captures the step graph once every weight is set.
 static int prepare(vx_decoder* d) {
     if (d->ready) return VX_OK;
     const size_t L = d->cfg.n_layers;
@@ -941,7 +1299,7 @@ static int prepare(vx_decoder* d) {
             if (!d->norm_set[l * kNormKinds + k]) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "norm %d of layer %zu is not set", k, l);
     if (!d->emb_set[0]) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the embedding is not set");
     drop_graph(d);
-    VX_TRY(build_plans(d));
+    VX_TRY(build_stages(d));
     VX_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
     const int st = record_step(d, d->stream);
     hipGraph_t g = nullptr;

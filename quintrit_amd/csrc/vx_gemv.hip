@@ -28,6 +28,7 @@
 //
 // Reference path: quintrit-core/src/simd/avx512.rs:1526-1626 (production CPU kernel: table decode, exact int8/int16/
 // int32 sums) and quintrit-runtime/src/layer.rs:210-254 (the fp32 epilogue out = float(acc) * (ws / as)).
+#include "vx_gemv_core.h"
 #include "vx_internal.h"
 
 #include <algorithm>
@@ -42,25 +43,6 @@ typedef __attribute__((address_space(1))) const u32x4 g_u4;
 typedef __attribute__((address_space(4))) const Job c_job;
 typedef __attribute__((address_space(4))) const int c_int;
 typedef __attribute__((address_space(4))) const float c_float;
-
-// ---- digits of a velurex byte ---------------------------------------------------------------------------------------
-
-// U = floor(B / 28) is the 2-trit group (d3, d4), L = B - 28 U the 3-trit group (d0, d1, d2); B is a velurex value iff
-// B <= 250 and L <= 26 (docs/velurex-encoding.md sections 2-3).
-__host__ __device__ inline bool byte_valid(uint32_t b) {
-    const uint32_t u = b / 28u, l = b - 28u * u;
-    return b <= 250u && l <= 26u;
-}
-
-__host__ __device__ inline uint32_t digit_nibbles(uint32_t b) {
-    if (!byte_valid(b)) return 0x11111u;  // five zero trits
-    const uint32_t u = b / 28u, l = b - 28u * u;
-    return (l % 3u) | ((l / 3u % 3u) << 4) | ((l / 9u) << 8) | ((u % 3u) << 12) | ((u / 3u) << 16);
-}
-
-__host__ __device__ inline int trit_of(uint32_t b, uint32_t p) {
-    return static_cast<int>((digit_nibbles(b) >> (4 * p)) & 15u) - 1;
-}
 
 // ---- activation staging -----------------------------------------------------------------------------------------------
 
@@ -192,27 +174,6 @@ __device__ __forceinline__ int row_result(const Job& jb, uint32_t row, int lo_pl
     return lo_plus_16hi + 8 * jb.dsum[row] - staged_sum(jb);
 }
 
-
-// Four bytes of a lane's weights against their activations: lo += dot8(L of byte K + j, t_j), hi += dot8(H, t_j) for
-// j = 0..3, where t_j is the digit-nibble table entry of byte j and the activation dwords of the 16 byte-columns of a
-// chunk sit in lanes 0..15 of every 16-lane row of L and H, broadcast by DPP row_newbcast. v_dot8c_i32_i4 multiplies
-// signed nibbles: the digits (0..2), the high nibbles x >> 4 and the low nibbles (x & 15) - 8. L and H come from LDS
-// loads; the s_nop keeps the two wait states a DPP read needs after any VALU write of its source.
-template <int K>
-__device__ __forceinline__ void dot4_bcast(int& lo, int& hi, uint32_t L, uint32_t H, uint32_t t0, uint32_t t1, uint32_t t2,
-                                           uint32_t t3) {
-    asm("s_nop 1\n\t"
-        "v_dot8c_i32_i4_dpp %0, %2, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot8c_i32_i4_dpp %1, %3, %4 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot8c_i32_i4_dpp %0, %2, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot8c_i32_i4_dpp %1, %3, %5 row_newbcast:%9 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot8c_i32_i4_dpp %0, %2, %6 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot8c_i32_i4_dpp %1, %3, %6 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot8c_i32_i4_dpp %0, %2, %7 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
-        "v_dot8c_i32_i4_dpp %1, %3, %7 row_newbcast:%11 row_mask:0xf bank_mask:0xf"
-        : "+v"(lo), "+v"(hi)
-        : "v"(L), "v"(H), "v"(t0), "v"(t1), "v"(t2), "v"(t3), "n"(K), "n"(K + 1), "n"(K + 2), "n"(K + 3));
-}
 
 constexpr int kWaves = 16;   // waves per workgroup = tiles per group
 constexpr int kGroup = 4;    // chunks loaded together by a wave
