@@ -353,11 +353,14 @@ __device__ __forceinline__ float stage_norm(const StageInput& p, const InputRegs
     __syncthreads();
     double t = 0.0;
     for (int w = 0; w < kNT / 64; ++w) t += s.red_d[w];
-    // the sequential f64 sum of the reference lies within d of t (both within (n-1) 2^-53 t of the exact sum)
-    const double d = 2.0 * static_cast<double>(n) * 0x1.0p-53 * t;
-    float mean = static_cast<float>(t / static_cast<double>(n));
-    const float lo = static_cast<float>((t - d) / static_cast<double>(n));
-    const float hi = static_cast<float>((t + d) / static_cast<double>(n));
+    // The reference's sequential f64 sum and t both lie within (n - 1) 2^-53 S of the exact sum S of the nonnegative
+    // squares, so the reference's quotient by n (rounded) lies within (2 (n - 1) + 3) 2^-53 q of q = t / n and of the
+    // rounded ends of [q - e, q + e] for e = (2 n + 8) 2^-53 q; when both ends round to the same f32, so does it.
+    const double q = t / static_cast<double>(n);
+    const double e = (2.0 * static_cast<double>(n) + 8.0) * 0x1.0p-53 * q;
+    float mean = static_cast<float>(q);
+    const float lo = static_cast<float>(q - e);
+    const float hi = static_cast<float>(q + e);
     if (lo != hi) {  // (the same in every thread) too close to an f32 rounding boundary: the reference's order
         if (tid == 0) {
             double seq = 0.0;
@@ -503,13 +506,15 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
             b[i] = __builtin_nontemporal_load(wp + (q0 + wave + kTileGroup * static_cast<size_t>(i)) * cs);
     }
 
+    const float mx = stage_norm(a.in, r, s, blockIdx.x == 0);
+    // The table is filled after the input is normed (its loads were issued after the input's, so waiting for them
+    // earlier would also wait for the input) and before the quantization's first barrier.
 #pragma unroll
     for (int k = 0; k < 2; ++k) {  // 8 uint4 stores per entry
         const uint32_t i = tid + k * kNT;
         *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) =
             make_uint4(dig[k], dig[k], dig[k], dig[k]);
     }
-    const float mx = stage_norm(a.in, r, s, blockIdx.x == 0);
     float act_scale;
     int act_sum;
     stage_quant(s, mx, a.in.n, a.tbr, a.dbr, st, &act_scale, &act_sum);
@@ -863,8 +868,7 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
         const uint32_t r = r0 + (tid >> 2);
         const u32x4* row = reinterpret_cast<const u32x4*>(a.emb + static_cast<size_t>(min(r, a.vocab - 1u)) * a.hidden);
         float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (uint32_t i = 0; i < a.hidden / 32u; ++i) {
-            const u32x4 w = __builtin_nontemporal_load(row + 4u * i + j);
+        auto block = [&](const u32x4& w, uint32_t i) {  // the 32-value block i: lane j's accumulator j
             const uint4 x = xs[4u * i + j];
             const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xx[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
@@ -874,7 +878,16 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
                 const float p = xf * wf;
                 acc[l] = acc[l] + p;
             }
+        };
+        const uint32_t nblk = a.hidden / 32u, nblk8 = nblk & ~7u;
+        for (uint32_t i0 = 0; i0 < nblk8; i0 += 8u) {  // eight loads in flight per lane
+            u32x4 w[8];
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u) w[u] = __builtin_nontemporal_load(row + 4u * (i0 + u) + j);
+#pragma unroll
+            for (uint32_t u = 0; u < 8; ++u) block(w[u], i0 + u);
         }
+        for (uint32_t i = nblk8; i < nblk; ++i) block(__builtin_nontemporal_load(row + 4u * i + j), i);
         // (a0 + a2) + (a1 + a3): lanes j and j ^ 2, then j and j ^ 1
 #pragma unroll
         for (int l = 0; l < 8; ++l) {
@@ -1283,8 +1296,10 @@ static int record_step(const vx_decoder* d, hipStream_t st) {
     h.out_tokens = d->d_tokens;
     h.key = d->d_key;
     h.ticket = d->d_ticket;
+    // One workgroup per CU (its registers allow one), each computing the normed vector once and looping over blocks
+    // of kNT / 4 rows.
     const uint32_t rows_per_wg = kNT / 4;
-    const uint32_t grid = std::min<uint32_t>((c.vocab + rows_per_wg - 1) / rows_per_wg, 2u * static_cast<uint32_t>(d->num_cus));
+    const uint32_t grid = std::min<uint32_t>((c.vocab + rows_per_wg - 1) / rows_per_wg, static_cast<uint32_t>(d->num_cus));
     return launch_head(h, grid, st);
 }
 
