@@ -701,7 +701,8 @@ static Q2Job q2_job(const vx_matrix* m, const int8_t* acts, const float* act_sca
     j.out = out;
     j.rows = static_cast<uint32_t>(m->g.rows);
     j.cols = static_cast<uint32_t>(m->g.cols);
-    j.scale_stride = static_cast<uint32_t>(q2_scale_stride(m->g.cols));
+    j.n_tiles = static_cast<uint32_t>(m->g.n_tiles);
+    j.nb = static_cast<uint32_t>(q2_blocks(m->g.cols));
     j.item_begin = 0;
     return j;
 }

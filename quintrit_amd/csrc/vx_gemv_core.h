@@ -34,6 +34,32 @@ constexpr DigitTable make_digit_table() {
     return t;
 }
 
+// t0..t3 of byte b as int8 in a dword (byte p = trit p); bytes that are not velurex values give zero trits.
+__host__ __device__ constexpr uint32_t trits03_word(uint32_t b) {
+    if (!byte_valid(b)) return 0u;
+    const uint32_t e = digit_nibbles(b);
+    uint32_t w = 0;
+    for (uint32_t p = 0; p < 4; ++p) w |= ((((e >> (4 * p)) & 15u) - 1u) & 0xffu) << (8 * p);
+    return w;
+}
+struct TritTable {
+    uint32_t v[256];
+};
+constexpr TritTable make_trit_table() {
+    TritTable t{};
+    for (uint32_t b = 0; b < 256; ++b) t.v[b] = trits03_word(b);
+    return t;
+}
+
+// t4 of each byte of w as int8: d4 = floor(B / 84) from B >= 84 and B >= 168, tested with 7-bit adds that cannot carry
+// (the halved byte B >> 1 is below 128), then t4 = d4 - 1 per byte as (d4 + 0x7f) ^ 0x80, again without carries.
+// Every byte must be a velurex value.
+__host__ __device__ constexpr uint32_t t4_bytes(uint32_t w) {
+    const uint32_t x = (w >> 1) & 0x7f7f7f7fu;
+    const uint32_t d4 = (((x + 0x56565656u) >> 7) & 0x01010101u) + (((x + 0x2c2c2c2cu) >> 7) & 0x01010101u);
+    return (d4 + 0x7f7f7f7fu) ^ 0x80808080u;
+}
+
 __host__ __device__ inline int trit_of(uint32_t b, uint32_t p) {
     return static_cast<int>((digit_nibbles(b) >> (4 * p)) & 15u) - 1;
 }

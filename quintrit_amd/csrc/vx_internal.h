@@ -171,27 +171,27 @@ void planar_to_device_layout(const uint8_t* planar, const Geometry& g, uint8_t* 
 // ---- Q2_0 (block-scaled) jobs ---------------------------------------------------------------------------------------
 
 struct Q2Job {
-    const uint8_t* w;            // Q2 device layout (vx_q2.hip)
-    const uint16_t* scales;      // fp16 weight scales, [tile of 8][row % 8][scale_stride]
+    const uint8_t* w;            // Q2 device layout (vx_q2.hip): planar blocks in the GEMV tile layout
+    const uint16_t* scales;      // fp16 weight scales, [tile][group of 4 blocks][row of the tile][10]
     const int8_t* acts;          // cols int8 codes (4-byte aligned)
     const float* act_scales;     // cols / 32 fp32 scales
     float* out;                  // rows values
-    uint32_t rows, cols, scale_stride, item_begin;
+    uint32_t rows, cols, n_tiles, nb, item_begin;  // nb: 160-trit blocks per row
 };
 
 struct Q2Args {
     const Q2Job* jobs;  // device array, or nullptr: use `one`
     uint32_t n_jobs;
-    uint32_t total_items;  // tile groups (16 tiles of 8 rows) summed over the jobs
+    uint32_t total_items;  // runs of 8 tiles (64 rows each) summed over the jobs
     Q2Job one;
 };
 
 size_t q2_blocks(size_t cols);
-size_t q2_scale_stride(size_t cols);
+size_t q2_kgroups(size_t cols);
 size_t q2_weight_bytes(size_t rows, size_t cols);
 size_t q2_device_bytes(size_t rows, size_t cols);
 void q2_to_device_layout(const uint8_t* planar, const uint16_t* scales, size_t rows, size_t cols, uint8_t* dst);
-inline uint32_t q2_items(uint32_t rows) { return ((rows + 7) / 8 + kTileGroup - 1) / kTileGroup; }
+inline uint32_t q2_items(uint32_t rows) { return ((rows + kTileRows - 1) / kTileRows + 7) / 8; }
 int launch_q2(const Q2Args& a, int num_cus, hipStream_t stream);
 int launch_q2_lane_sums(const Q2Job& j, int32_t* out, hipStream_t stream);
 

@@ -2,22 +2,30 @@
 // activations with one fp32 scale per 32 values (Q8_0), with fp32 results bit-identical to the reference's definition.
 //
 // The reference (quintrit-core/src/block_scaled.rs:1-19, dot_row_scalar 175-202) reproduces ggml_vec_dot_q2_0_q8_0:
-// every 32-value activation block s gives eight exact integer lane sums (lane j covers values 4j..4j+3); each is
-// accumulated as acc[(s/2) & 1][j] = fma(w_scale[s/2] * a_scale[s], float(lane), acc[...][j]), s in increasing order;
-// then l[j] = acc[0][j] + acc[1][j] and the result is ((l0+l4) + (l2+l6)) + ((l1+l5) + (l3+l7)). The weights are the
-// velurex planar layout, so plane p of 160-trit block b is activation block s = 5b + p.
+// every 32-value activation block s gives eight exact integer lane sums L[s][j] (lane j covers values 4j..4j+3); each
+// is accumulated as acc[(s/2) & 1][j] = fma(w_scale[s/2] * a_scale[s], float(L[s][j]), acc[...][j]), s in increasing
+// order; then l[j] = acc[0][j] + acc[1][j] and the result is ((l0+l4) + (l2+l6)) + ((l1+l5) + (l3+l7)). The weights are
+// the velurex planar layout, so plane p of 160-trit block b is activation block s = 5b + p, and byte k of the block
+// belongs to lane j = k / 4 of every plane.
 //
-// Here one lane owns one (row, j) pair: its two accumulators are exactly the reference's acc[0][j], acc[1][j] of that
-// row, fed in the same order, and the final tree is three xor-shuffles over the eight lanes of the row. The lane reads
-// one 32-bit word of weights per 160-trit block (bytes 4j..4j+3); planes 0..3 of its four bytes come from four LDS table
-// lookups (t0..t3 as int8) transposed with v_perm, plane 4 from byte-wise compares (d4 = t4 + 1, corrected by the lane's
-// activation sum); each lane sum is one v_dot4_i32_i8.
+// Lane sums on the matrix cores. For one 160-trit block b and 32 weight rows, the 40 lane sums (p, j) of every row are
+// a product C = A' W^T on v_mfma_i32_32x32x32_i8, transposed so that the rows of C are lane sums and its columns
+// weight rows: lane l of the output then holds column n = l % 32 (one weight row) and C rows 8 (r / 4) + 4 (l / 32) +
+// r % 4, r = 0..15. With C row 8 p + j for planes 0..3, lane l holds the sums (p, j) of its row for every p < 4 and
+// j = 4 (l / 32) + r % 4; a second product holds plane 4 in C rows j. So each lane runs the reference's fp32 chains of
+// its row's four lanes j in registers, in the reference's order, with no exchange between lanes until the final sum.
+//   W operand: the weights decoded exactly as the batched GEMM decodes its A operand (vx_gemm.hip): lane (n, h) holds
+//     the 16 bytes 16 h .. 16 h + 15 of block b of row n; K block m < 4 takes bytes 4 m .. 4 m + 3 with their
+//     trits t0..t3 (one LDS table lookup per byte), K block 4 takes t4 of all 16 bytes (byte arithmetic).
+//   A' operand (one 32 x 32 int8 block per K block, built per lane with v_perm from the raw activations in LDS): for K
+//     block m, row 8 p + j holds a(5b + p, 4 j + q) at the K position of (byte 4 j + q, plane p) when j = 4 h + m,
+//     zero elsewhere; for K block 4, row j holds a(5b + 4, 4 j + q) at the position of byte 4 j + q.
 //
-// Device layout (vx_q2_matrix_create): rows form tiles of 8 and tiles form groups of 16. The 32-byte planar block b of
-// row r lives at 256-byte unit (g * 16 * nb + b * T + t') with g = tile / 16, t' = tile % 16, T the tiles of the group and
-// nb the blocks per row, at byte (r % 8) * 32; a wave (one tile) reads 256 consecutive bytes per block and the 16 waves
-// of a workgroup 4 KiB. The fp16 scales of row r follow the weights: tile-major, then row % 8, then k (padded to a
-// multiple of 10 per row, so a lane reads the ten scales of four blocks as five aligned words).
+// Device layout (vx_q2_matrix_create): the planar bytes of each row (ceil(cols / 160) blocks of 32 bytes, a partial
+// last block padded with zero trits as the planar layout pads it) in the GEMV's tile layout (64-row tiles, 16-byte
+// chunks interleaved over groups of 16 tiles, vx_layout), followed by the fp16 scales as [tile][group of 4 blocks]
+// [row of the tile][10 scales]: the ten scales of 20 activation blocks, one 20-byte load per lane.
+#include "vx_gemv_core.h"
 #include "vx_internal.h"
 
 #include <algorithm>
@@ -26,174 +34,219 @@
 
 namespace vx {
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 g_u4;
+
 // ---- layout -----------------------------------------------------------------------------------------------------------
 
 size_t q2_blocks(size_t cols) { return (cols + kQK5 - 1) / kQK5; }
-size_t q2_scale_stride(size_t cols) { return round_up(cols / 64, 10); }
-size_t q2_weight_bytes(size_t rows, size_t cols) { return round_up(rows, 8) * q2_blocks(cols) * 32; }
+size_t q2_kgroups(size_t cols) { return (q2_blocks(cols) + 3) / 4; }
+size_t q2_weight_bytes(size_t rows, size_t cols) { return round_up(rows, kTileRows) * q2_blocks(cols) * kBlockBytes; }
 size_t q2_device_bytes(size_t rows, size_t cols) {
-    return q2_weight_bytes(rows, cols) + round_up(rows, 8) * q2_scale_stride(cols) * 2;
+    return q2_weight_bytes(rows, cols) + round_up(rows, kTileRows) * q2_kgroups(cols) * 10 * 2;
 }
 
 void q2_to_device_layout(const uint8_t* planar, const uint16_t* scales, size_t rows, size_t cols, uint8_t* dst) {
-    const size_t nb = q2_blocks(cols), nk = cols / 64, ks = q2_scale_stride(cols);
-    const size_t tiles = (rows + 7) / 8;
+    const size_t nb = q2_blocks(cols), nk = cols / 64, ng = q2_kgroups(cols);
+    const size_t padded = round_up(rows, kTileRows), n_tiles = padded / kTileRows, n_chunks = nb * 2;
     std::memset(dst, 0, q2_device_bytes(rows, cols));
-    for (size_t r = 0; r < round_up(rows, 8); ++r) {
-        const size_t tile = r / 8, grp = tile / kTileGroup, t = tile % kTileGroup;
-        const size_t T = std::min<size_t>(kTileGroup, tiles - grp * kTileGroup);
-        for (size_t b = 0; b < nb; ++b) {
-            uint8_t* d = dst + ((grp * kTileGroup * nb + b * T + t) * 256) + (r % 8) * 32;
-            if (r < rows) std::memcpy(d, planar + r * nb * 32 + b * 32, 32);
-            else std::memset(d, kZeroByte, 32);
+    for (size_t r = 0; r < padded; ++r)
+        for (size_t q = 0; q < n_chunks; ++q) {
+            uint8_t* d = dst + layout_offset(r, static_cast<uint32_t>(q * kChunk), static_cast<uint32_t>(n_tiles),
+                                             static_cast<uint32_t>(n_chunks));
+            if (r < rows) std::memcpy(d, planar + r * nb * kBlockBytes + q * kChunk, kChunk);
+            else std::memset(d, kZeroByte, kChunk);
         }
-        uint16_t* sd = reinterpret_cast<uint16_t*>(dst + q2_weight_bytes(rows, cols)) + (tile * 8 + r % 8) * ks;
-        for (size_t k = 0; k < nk; ++k) sd[k] = r < rows ? scales[r * nk + k] : 0;
+    uint16_t* sd = reinterpret_cast<uint16_t*>(dst + q2_weight_bytes(rows, cols));
+    for (size_t r = 0; r < rows; ++r) {
+        const size_t tile = r / kTileRows;
+        for (size_t k = 0; k < nk; ++k) sd[((tile * ng + k / 10) * kTileRows + r % kTileRows) * 10 + k % 10] = scales[r * nk + k];
     }
 }
 
 // ---- kernel -----------------------------------------------------------------------------------------------------------
 
-__device__ inline uint32_t q2_trits03(uint32_t b) {
-    const uint32_t u = b / 28u, l = b - 28u * u;
-    if (b > 250u || l > 26u) return 0u;
-    const uint32_t d0 = l % 3u, d1 = l / 3u % 3u, d2 = l / 9u, d3 = u % 3u;
-    return ((d0 - 1u) & 0xffu) | (((d1 - 1u) & 0xffu) << 8) | (((d2 - 1u) & 0xffu) << 16) | (((d3 - 1u) & 0xffu) << 24);
-}
+constexpr int kQ2Waves = 16;   // 8 tiles x 2 halves of 32 rows
+constexpr int kQ2Pre = 8;      // blocks of weights in flight per wave
 
-__device__ __forceinline__ uint32_t q2_d4(uint32_t w) {
-    const uint32_t x = (w >> 1) & 0x7f7f7f7fu;
-    return (((x + 0x56565656u) >> 7) & 0x01010101u) + (((x + 0x2c2c2c2cu) >> 7) & 0x01010101u);
-}
+__constant__ TritTable g_trits = make_trit_table();
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));  // exact widening
 }
 
-constexpr int kQ2Waves = 16;
-constexpr int kQ2Group = 4;  // 160-trit blocks per prefetch group (ten scales)
-
 typedef __attribute__((address_space(4))) const Q2Job c_q2job;
 
-// MANY: the jobs are a device array (a plan); otherwise the one job travels in the kernel arguments.
+// Work item: 8 consecutive tiles of a tile group (wave w: tile 8 half + w / 2, rows 32 (w % 2) .. + 31 of it). The
+// activations and their scales are staged in LDS once per item; every wave then streams its rows' blocks in order.
 template <bool MANY>
-__global__ __launch_bounds__(kQ2Waves * 64) __attribute__((amdgpu_waves_per_eu(8, 8))) void q2_kernel(Q2Args args) {
-    __shared__ uint32_t tab[256 * 64];
-    __shared__ uint32_t acts[kQ2MaxCols / 4];
+__global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
+    __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of t0..t3 of byte B (first half)
+    __shared__ uint32_t actw[kQ2MaxCols / 4 + 64];
     __shared__ float ascl[kQ2MaxCols / 32];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t j = lane & 7u, rl = lane >> 3;
-    for (uint32_t i = tid; i < 256u * 16u; i += kQ2Waves * 64u) {
-        const uint32_t e = q2_trits03(i >> 4);
-        reinterpret_cast<uint4*>(tab)[i] = make_uint4(e, e, e, e);
+    for (uint32_t i = tid; i < 256u * 8u; i += kQ2Waves * 64u) {
+        const uint32_t e = g_trits.v[i >> 3];
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
     }
     const char* tabb = reinterpret_cast<const char*>(tab);
-    const uint32_t lane_off = lane * 4u;
+    const uint32_t lane_off = (lane & 31u) * 4u;
 
-    uint32_t jj = 0;
+    // This lane's A' rows: C row mr = lane % 32 (plane p = mr / 8, lane sum j = mr % 8) and K half hh = lane / 32.
+    // sel[q] places byte q of the activation dword at byte p of K dword q (v_perm selector 0x0c gives 0x00); the
+    // result is used in the one K block m = j % 4 of the lanes with j / 4 == hh (on[m]) and is zero elsewhere. The
+    // plane-4 dword goes to dword u = j % 4 of the lanes with mr < 8 and mr / 4 == hh (on4[u]).
+    const uint32_t mr = lane & 31u, hh = lane >> 5, pl = mr >> 3, jl = mr & 7u;
+    uint32_t sel[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sel[q] = (0x0c0c0c0cu & ~(0xffu << (8u * pl))) | (static_cast<uint32_t>(q) << (8u * pl));
+    bool on[4], on4[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) on[m] = (jl >> 2) == hh && (jl & 3u) == static_cast<uint32_t>(m);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) on4[u] = mr < 8u && (mr >> 2) == hh && (mr & 3u) == static_cast<uint32_t>(u);
+
+    uint32_t jj_job = 0;
     for (uint32_t item = blockIdx.x; item < args.total_items; item += gridDim.x) {
         const c_q2job* cj = (const c_q2job*)(args.jobs);
         if (MANY)
-            while (jj + 1 < args.n_jobs && item >= cj[jj + 1].item_begin) ++jj;
+            while (jj_job + 1 < args.n_jobs && item >= cj[jj_job + 1].item_begin) ++jj_job;
         Q2Job jb;
-        if (MANY) __builtin_memcpy(&jb, (const Q2Job*)(cj + jj), sizeof(Q2Job));
+        if (MANY) __builtin_memcpy(&jb, (const Q2Job*)(cj + jj_job), sizeof(Q2Job));
         else jb = args.one;
-        const uint32_t grp = item - jb.item_begin;
-        const uint32_t tiles = (jb.rows + 7u) / 8u;
-        const uint32_t T = min(static_cast<uint32_t>(kTileGroup), tiles - grp * kTileGroup);
-        const uint32_t ns = jb.cols / 32u, nb = (jb.cols + 159u) / 160u;
-        __syncthreads();  // the previous item is done with acts / ascl
+        const uint32_t local = item - jb.item_begin;
+        const uint32_t grp = local >> 1, tt = (local & 1u) * 8u + (wave >> 1), rb = wave & 1u;
+        const uint32_t T = min(static_cast<uint32_t>(kTileGroup), jb.n_tiles - grp * kTileGroup);
+        const uint32_t ns = jb.cols / 32u, nb = jb.nb, n_chunks = 2u * nb, ng = (nb + 3u) / 4u;
+        __syncthreads();  // the previous item is done with actw / ascl
         const uint32_t* a32 = reinterpret_cast<const uint32_t*>(jb.acts);
-        for (uint32_t i = tid; i < jb.cols / 4u; i += kQ2Waves * 64u) acts[i] = a32[i];
+        for (uint32_t i = tid; i < nb * 40u; i += kQ2Waves * 64u) actw[i] = i < jb.cols / 4u ? a32[i] : 0u;
         for (uint32_t i = tid; i < ns; i += kQ2Waves * 64u) ascl[i] = jb.act_scales[i];
         __syncthreads();
-        if (wave >= T) continue;
-        const uint32_t tile = grp * kTileGroup + wave;
-        const uint32_t row = tile * 8u + rl;
-        const uint32_t* wp = reinterpret_cast<const uint32_t*>(jb.w + (static_cast<size_t>(grp) * kTileGroup * nb + wave) * 256u) + lane;
-        const size_t bstride = static_cast<size_t>(T) * 64u;  // dwords between blocks of this tile
-        const uint32_t* sp = reinterpret_cast<const uint32_t*>(jb.scales + (static_cast<size_t>(tile) * 8u + rl) * jb.scale_stride);
-        float acc0 = 0.0f, acc1 = 0.0f;
-        for (uint32_t b0 = 0; b0 < nb; b0 += kQ2Group) {
-            uint32_t w[kQ2Group], sc[5];
+        if (tt >= T) continue;
+        const uint32_t tile = grp * kTileGroup + tt;
+        const uint32_t row = tile * kTileRows + rb * 32u + (lane & 31u);
+
+        // weights: chunk 2 b + hh of this row (16 bytes), chunks of a tile T KiB apart
+        const g_u4* wp = (const g_u4*)(jb.w + (static_cast<size_t>(grp) * kTileGroup * n_chunks + tt) * 1024u + rb * 512u +
+                                       (lane & 31u) * 16u + static_cast<size_t>(hh) * T * 1024u);
+        const size_t bstride = static_cast<size_t>(T) * 128u;  // uint4 between blocks b and b + 1
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(jb.scales) +
+                             (static_cast<size_t>(tile) * ng * kTileRows + rb * 32u + (lane & 31u)) * 5u;
+        const size_t sstride = static_cast<size_t>(kTileRows) * 5u;  // dwords between scale groups of a tile
+
+        u32x4 wq[kQ2Pre];
 #pragma unroll
-            for (int i = 0; i < kQ2Group; ++i) w[i] = __builtin_nontemporal_load(wp + min(b0 + i, nb - 1u) * bstride);
+        for (int i = 0; i < kQ2Pre; ++i) wq[i] = __builtin_nontemporal_load(wp + min(static_cast<uint32_t>(i), nb - 1u) * bstride);
+        uint32_t sc[5], scn[5];
 #pragma unroll
-            for (int i = 0; i < 5; ++i) sc[i] = sp[5u * (b0 / 4u) + i];  // scales k0 .. k0 + 9, k0 = 5 b0 / 2
+        for (int i = 0; i < 5; ++i) sc[i] = sp[i];
 #pragma unroll
-            for (int i = 0; i < kQ2Group; ++i) {
-                const uint32_t b = b0 + i;
+        for (int i = 0; i < 5; ++i) scn[i] = sp[min(1u, ng - 1u) * sstride + i];
+
+        float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t b0 = 0; b0 < nb; b0 += kQ2Pre) {
+#pragma unroll
+            for (int ib = 0; ib < kQ2Pre; ++ib) {
+                const uint32_t b = b0 + ib;
                 if (b >= nb) break;
-                const uint32_t wv = w[i];
-                uint32_t x[4];
+                const u32x4 w = wq[ib];
+                wq[ib] = __builtin_nontemporal_load(wp + min(b + kQ2Pre, nb - 1u) * bstride);
+                if ((b & 3u) == 0 && b > 0) {  // a new group of 4 blocks: its scales, the next group's load
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint32_t addr = __builtin_amdgcn_perm(wv, lane_off, 0x0c0c0000u | ((4u + k) << 8));
-                    x[k] = *reinterpret_cast<const uint32_t*>(tabb + addr);
-                }
-                uint32_t P[5];
+                    for (int i = 0; i < 5; ++i) sc[i] = scn[i];
 #pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    const uint32_t sel = 0x0c0c0000u | ((4u + p) << 8) | static_cast<uint32_t>(p);
-                    const uint32_t lo = __builtin_amdgcn_perm(x[1], x[0], sel);
-                    const uint32_t hi = __builtin_amdgcn_perm(x[3], x[2], sel);
-                    P[p] = lo | (hi << 16);
+                    for (int i = 0; i < 5; ++i) scn[i] = sp[min(b / 4u + 1u, ng - 1u) * sstride + i];
                 }
-                P[4] = q2_d4(wv);
+                // W operand: K blocks 0..3 (t0..t3 of bytes 4 m .. 4 m + 3) and 4 (t4 of the 16 bytes)
+                const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
+                v4i Bm[5];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    int t[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + k) << 8));
+                        t[k] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
+                    }
+                    Bm[m] = v4i{t[0], t[1], t[2], t[3]};
+                }
+                Bm[4] = v4i{static_cast<int>(t4_bytes(dw[0])), static_cast<int>(t4_bytes(dw[1])),
+                            static_cast<int>(t4_bytes(dw[2])), static_cast<int>(t4_bytes(dw[3]))};
+                // A' operands from the activation dwords of this block
+                const uint32_t x = actw[(5u * b + pl) * 8u + jl];
+                const uint32_t x4 = actw[(5u * b + 4u) * 8u + (mr & 7u)];
+                v16i c = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+                v16i c4 = c;
+                const int D[4] = {static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[0])),
+                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[1])),
+                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[2])),
+                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[3]))};
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const v4i A = v4i{on[m] ? D[0] : 0, on[m] ? D[1] : 0, on[m] ? D[2] : 0, on[m] ? D[3] : 0};
+                    c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm[m], c, 0, 0, 0);
+                }
+                {
+                    const int xi = static_cast<int>(x4);
+                    const v4i A = v4i{on4[0] ? xi : 0, on4[1] ? xi : 0, on4[2] ? xi : 0, on4[3] ? xi : 0};
+                    c4 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm[4], c4, 0, 0, 0);
+                }
+                // the reference's chains: s = 5 b + p in order; register r = 4 p + jj of c holds L[s][4 hh + jj]
 #pragma unroll
                 for (int p = 0; p < 5; ++p) {
-                    const uint32_t s = 5u * b + p;
+                    const uint32_t s = 5u * b + static_cast<uint32_t>(p);
                     if (s >= ns) break;
-                    const uint32_t av = acts[s * 8u + j];
-                    int L = __builtin_amdgcn_sdot4(static_cast<int>(P[p]), static_cast<int>(av), 0, false);
-                    if (p == 4) L -= __builtin_amdgcn_sdot4(0x01010101, static_cast<int>(av), 0, false);
-                    const uint32_t kl = s / 2u - (b0 * 5u) / 2u;  // scale index inside this group's ten
+                    const uint32_t kl = (5u * (b & 3u) + static_cast<uint32_t>(p)) / 2u;  // scale index in the group
                     const uint32_t hw = sc[kl >> 1] >> ((kl & 1u) * 16u);
                     const float d = half_bits_to_float(hw & 0xffffu) * ascl[s];
-                    if ((s / 2u) & 1u) acc1 = __builtin_fmaf(d, static_cast<float>(L), acc1);
-                    else acc0 = __builtin_fmaf(d, static_cast<float>(L), acc0);
+                    const bool odd = (s / 2u) & 1u;
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const int L = p < 4 ? c[4 * p + jj] : c4[jj];
+                        if (odd) acc1[jj] = __builtin_fmaf(d, static_cast<float>(L), acc1[jj]);
+                        else acc0[jj] = __builtin_fmaf(d, static_cast<float>(L), acc0[jj]);
+                    }
                 }
             }
         }
-        float l = acc0 + acc1;
-        l = l + __shfl_xor(l, 4);
-        l = l + __shfl_xor(l, 2);
-        l = l + __shfl_xor(l, 1);
-        if (j == 0 && row < jb.rows) jb.out[row] = l;
+        // l[j] = acc[0][j] + acc[1][j]; lanes hh = 0 hold j = 0..3, hh = 1 j = 4..7
+        float l[4], o[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) l[jj] = acc0[jj] + acc1[jj];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) o[jj] = __shfl_xor(l[jj], 32);
+        if (hh == 0 && row < jb.rows) {
+            const float a0 = l[0] + o[0], a1 = l[1] + o[1], a2 = l[2] + o[2], a3 = l[3] + o[3];
+            jb.out[row] = (a0 + a2) + (a1 + a3);
+        }
     }
 }
 
 // Integer lane sums (rows x cols/32 x 8): the exact part of the product, for checking.
 __global__ __launch_bounds__(256) void q2_lane_sums_kernel(Q2Job jb, int32_t* __restrict__ out) {
     const uint64_t idx = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const uint32_t ns = jb.cols / 32u, nb = (jb.cols + 159u) / 160u;
+    const uint32_t ns = jb.cols / 32u;
     if (idx >= static_cast<uint64_t>(jb.rows) * ns * 8u) return;
     const uint32_t jl = static_cast<uint32_t>(idx % 8u);
     const uint32_t s = static_cast<uint32_t>((idx / 8u) % ns);
     const uint32_t row = static_cast<uint32_t>(idx / (8u * ns));
-    const uint32_t tiles = (jb.rows + 7u) / 8u, tile = row / 8u, grp = tile / kTileGroup, t = tile % kTileGroup;
-    const uint32_t T = min(static_cast<uint32_t>(kTileGroup), tiles - grp * kTileGroup);
     const uint32_t b = s / 5u, p = s % 5u;
-    const uint8_t* blk = jb.w + ((static_cast<size_t>(grp) * kTileGroup * nb + static_cast<size_t>(b) * T + t) * 256u) + (row % 8u) * 32u;
     int sum = 0;
     for (uint32_t k = 4u * jl; k < 4u * jl + 4u; ++k) {
-        const uint32_t B = blk[k];
-        const uint32_t u = B / 28u, l = B - 28u * u;
-        int tr = 0;
-        if (B <= 250u && l <= 26u) {
-            const uint32_t dg[5] = {l % 3u, l / 3u % 3u, l / 9u, u % 3u, u / 3u};
-            tr = static_cast<int>(dg[p]) - 1;
-        }
-        sum += tr * jb.acts[s * 32u + k];
+        const uint32_t B = jb.w[layout_offset(row, b * 32u + k, jb.n_tiles, 2u * jb.nb)];
+        sum += trit_of(B, p) * jb.acts[s * 32u + k];
     }
     out[idx] = sum;
 }
 
 int launch_q2(const Q2Args& a, int num_cus, hipStream_t stream) {
     if (a.total_items == 0) return VX_OK;
-    const uint32_t grid = std::min<uint32_t>(a.total_items, 2u * static_cast<uint32_t>(num_cus));
+    const uint32_t grid = std::min<uint32_t>(a.total_items, static_cast<uint32_t>(num_cus));
     if (a.jobs) hipLaunchKernelGGL(q2_kernel<true>, dim3(grid), dim3(kQ2Waves * 64), 0, stream, a);
     else hipLaunchKernelGGL(q2_kernel<false>, dim3(grid), dim3(kQ2Waves * 64), 0, stream, a);
     VX_HIP(hipGetLastError());
