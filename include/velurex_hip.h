@@ -291,10 +291,13 @@ int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_pl
  * AttentionBlock::forward_with_scratchpad, attention.rs:115-260, and the BitnetCpp numerics: RMSNorm with an f64 sum,
  * per-token absmax int8, velurex projections with the fp32 epilogue, NEOX RoPE, an F16 KV cache, FP16-accumulator
  * attention with the 4-chunk split, sub-norms, ReLU^2, a tied bf16 head, greedy argmax), so that logits and tokens are
- * bit-identical to it. One step is one HIP graph: embed, 30 x (norm, q/k/v, RoPE + KV append, attention, sub-norm, o,
- * norm, gate/up, ReLU^2 * up + sub-norm, down), final norm, head, argmax, with the position and the token kept on the
- * device (the reference's CUDA decode graph does the same, quintrit-runtime/src/gpu.rs:459-493).
- * Supported: head_dim 128, max_ctx <= 4096, hidden, n_heads * head_dim and ffn <= 8192, hidden a multiple of 32. */
+ * bit-identical to it. One step is one HIP graph of 1 + 5 per layer kernels: per layer the q/k/v, o, gate/up and down
+ * projection stages (each computing its own input: embedding or residual add or ReLU^2 * up, RMSNorm, int8
+ * quantization) and attention (RoPE, KV append), then the final norm, head and argmax in one kernel, with the position
+ * and the token kept on the device (the reference's CUDA decode graph does the same,
+ * quintrit-runtime/src/gpu.rs:459-493).
+ * Supported: head_dim 128, max_ctx <= 4096, hidden, n_heads * head_dim and ffn <= 8192, hidden a multiple of 32, ffn a
+ * multiple of 4. */
 typedef struct vx_decoder vx_decoder_t;
 
 typedef struct vx_decoder_config {
