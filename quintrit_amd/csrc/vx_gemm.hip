@@ -54,73 +54,79 @@ constexpr uint32_t kZeroWord = 0x7d7d7d7du;  // four bytes of five zero trits
 
 // ---- activation staging --------------------------------------------------------------------------------------------
 
-// Activation p of device byte-column c of token m (column_activation_index, pack.rs:230-237), 0 outside.
-__device__ inline int act_at(const int8_t* __restrict__ x, uint32_t ldx, uint32_t m, uint32_t M, uint32_t cols,
-                             uint32_t tbr, uint32_t c, uint32_t p) {
-    if (m >= M || c >= tbr) return 0;
+// Staging: thread (token m, pair) writes the five B fragments of K step ks = pair / 2, half hs = pair % 2 of token m:
+// xs[ks][kb][tg][lane] (tg = m / 32, lane = (m % 32) + 32 hs) for K blocks kb = 0..4, in the K order of the weight
+// decode (column_activation_index, pack.rs:230-237). In a whole 160-trit block (ks < cols / 160) the step is the 160
+// activations of block ks and half hs covers byte-columns 16 hs .. 16 hs + 15: K block kb < 4 takes, for byte-column
+// 16 hs + 4 kb + d, its activations of planes 0..3, a(160 ks + 32 e + 16 hs + 4 kb + d), e = 0..3: dword kb of the
+// four 16-byte loads at 160 ks + 32 e + 16 hs, transposed 4 x 4 bytes with v_perm; K block 4 takes plane 4 of the 16
+// byte-columns, the 16 bytes at 160 ks + 128 + 16 hs as they are. The packed tail and unaligned rows take the
+// per-byte gather. A workgroup covers kStagePairs pairs of one token and writes its part of the token's plane-4 sum
+// (the correction for d4 = t4 + 1) to s4p[blockIdx.y * M + m]; the GEMM adds the parts.
+constexpr uint32_t kStagePairs = 256;
+
+// Activation p of device byte-column c of a row (column_activation_index, pack.rs:230-237), 0 outside.
+__device__ __forceinline__ int act_of(const int8_t* __restrict__ xr, uint32_t cols, uint32_t tbr, uint32_t c, uint32_t p) {
+    if (c >= tbr) return 0;
     const uint32_t full = cols / 160u * 32u;
     const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
-    return idx < cols ? x[static_cast<size_t>(m) * ldx + idx] : 0;
+    return idx < cols ? xr[idx] : 0;
 }
-
-// One workgroup per (token m, slice kx of 64 K steps): the token's activations for those steps are read once, with 16-byte loads,
-// into LDS; each thread then writes 16-byte B fragments xs[ks][kb][tg][lane] (tg = m / 32, lane = (m % 32) + 32 s for
-// chunk 2 ks + s), gathering the five planes of each device byte-column (column_activation_index, pack.rs:230-237).
-// The workgroup also writes s4p[kx][m], its part of the sum of the token's plane-4 activations (the
-// correction for d4 = t4 + 1); the GEMM adds the parts.
-constexpr uint32_t kStageSteps = 64;                               // K steps per staging workgroup
-constexpr uint32_t kStageCols = kStageSteps * kStepChunks * 16;    // device byte-columns per staging workgroup
 
 __global__ __launch_bounds__(256) void gemm_stage_kernel(const int8_t* __restrict__ x, uint32_t ldx, uint32_t n_tg,
                                                          uint32_t cols, uint32_t tbr, uint32_t n_ksteps,
                                                          uint4* __restrict__ xs, int* __restrict__ s4p, uint32_t M) {
-    __shared__ uint32_t raw[kStageCols * 5 / 4 + 64];  // the token's activations of this slice (5 per byte-column)
     __shared__ int red[4];
-    const uint32_t m = blockIdx.x, kx = blockIdx.y, tid = threadIdx.x;
-    const uint32_t ks0 = kx * kStageSteps, ks1 = min(ks0 + kStageSteps, n_ksteps);
-    const uint32_t c0 = ks0 * kStepChunks * 16u;             // first byte-column; a multiple of 2048, so of 32
-    const uint32_t full = cols / 160u * 32u;                 // byte-columns of whole 160-trit blocks
-    // Activation index of byte-column c0 is 5 c0 (c0 is a multiple of 32 and c0 <= full, or past it in the tail,
-    // where the tail columns hold 5 consecutive activations each): the slice is the contiguous range
-    // [5 c0, 5 (c0 + ncols)) of the token's row, padded with zeros past cols.
-    const uint32_t a0 = 5u * c0;
-    const uint32_t nb = 5u * kStageCols;                      // bytes of the slice
+    const uint32_t m = blockIdx.x, tid = threadIdx.x;
+    const uint32_t pair = blockIdx.y * kStagePairs + tid, ks = pair >> 1, hs = pair & 1u;
     const int8_t* xr = x + static_cast<size_t>(m) * ldx;
-    const bool vec = (reinterpret_cast<uintptr_t>(xr) & 15u) == 0;
-    uint8_t* rb = reinterpret_cast<uint8_t*>(raw);
-    for (uint32_t i = tid * 16u; i < nb; i += 256u * 16u) {
-        const uint32_t g = a0 + i;
-        if (vec && g + 16u <= cols) {
-            *reinterpret_cast<uint4*>(rb + i) = *reinterpret_cast<const uint4*>(xr + g);
+    int s4 = 0;
+    if (ks < n_ksteps) {
+        uint4 o[5];
+        if (ks < cols / 160u && (reinterpret_cast<uintptr_t>(xr) & 15u) == 0) {
+            const int8_t* blk = xr + ks * 160u + 16u * hs;
+            uint4 X[5];
+#pragma unroll
+            for (int e = 0; e < 5; ++e) X[e] = *reinterpret_cast<const uint4*>(blk + 32 * e);
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) {
+                auto dw = [&](const uint4& v) { return kb == 0 ? v.x : (kb == 1 ? v.y : (kb == 2 ? v.z : v.w)); };
+                const uint32_t a0 = dw(X[0]), a1 = dw(X[1]), a2 = dw(X[2]), a3 = dw(X[3]);
+                const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u), hi01 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+                const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u), hi23 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+                o[kb] = make_uint4(__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                   __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u));
+            }
+            o[4] = X[4];
+            s4 = __builtin_amdgcn_sdot4(static_cast<int>(X[4].x), 0x01010101, 0, false) +
+                 __builtin_amdgcn_sdot4(static_cast<int>(X[4].y), 0x01010101, 0, false) +
+                 __builtin_amdgcn_sdot4(static_cast<int>(X[4].z), 0x01010101, 0, false) +
+                 __builtin_amdgcn_sdot4(static_cast<int>(X[4].w), 0x01010101, 0, false);
         } else {
-            for (uint32_t k = 0; k < 16; ++k) rb[i + k] = g + k < cols ? static_cast<uint8_t>(xr[g + k]) : 0u;
+            const uint32_t cb = (ks * kStepChunks + hs) * 16u;  // first byte-column of the chunk
+#pragma unroll
+            for (uint32_t kb = 0; kb < 5; ++kb) {
+                uint32_t w[4];
+                for (uint32_t d = 0; d < 4; ++d) {
+                    uint32_t v = 0;
+                    for (uint32_t e = 0; e < 4; ++e) {
+                        const int a = kb < 4 ? act_of(xr, cols, tbr, cb + 4u * kb + d, e) : act_of(xr, cols, tbr, cb + 4u * d + e, 4);
+                        if (kb == 4) s4 += a;
+                        v |= (static_cast<uint32_t>(a) & 0xffu) << (8 * e);
+                    }
+                    w[d] = v;
+                }
+                o[kb] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
         }
+        const uint32_t tg = m / 32u, lane0 = m % 32u + 32u * hs;
+#pragma unroll
+        for (uint32_t kb = 0; kb < 5; ++kb) xs[(static_cast<size_t>(ks * 5u + kb) * n_tg + tg) * 64u + lane0] = o[kb];
     }
+    for (int off = 32; off > 0; off >>= 1) s4 += __shfl_xor(s4, off);
+    if ((tid & 63u) == 0) red[tid >> 6] = s4;
     __syncthreads();
-    // byte-column c (absolute) -> position of activation p in raw
-    auto at = [&](uint32_t c, uint32_t p) -> uint32_t {
-        if (c >= tbr) return 0u;
-        const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
-        return idx < cols ? rb[idx - a0] : 0u;
-    };
-    int s = 0;
-    for (uint32_t c = c0 + tid; c < c0 + (ks1 - ks0) * kStepChunks * 16u; c += 256u) s += static_cast<int8_t>(at(c, 4));
-    const uint32_t tg = m / 32u, lane0 = m % 32u;
-    for (uint32_t i = tid; i < (ks1 - ks0) * 10u; i += 256u) {
-        const uint32_t ks = ks0 + i / 10u, kb = (i % 10u) / 2u, hs = i % 2u;
-        const uint32_t cb = (ks * kStepChunks + hs) * 16u;  // first byte-column of the chunk
-        uint32_t w[4];
-        for (uint32_t d = 0; d < 4; ++d) {
-            uint32_t v = 0;
-            for (uint32_t e = 0; e < 4; ++e) v |= (kb < 4 ? at(cb + 4u * kb + d, e) : at(cb + 4u * d + e, 4)) << (8 * e);
-            w[d] = v;
-        }
-        xs[(static_cast<size_t>(ks * 5u + kb) * n_tg + tg) * 64u + lane0 + 32u * hs] = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-    if ((tid & 63u) == 0) red[tid >> 6] = s;
-    __syncthreads();
-    if (tid == 0) s4p[static_cast<size_t>(kx) * M + m] = red[0] + red[1] + red[2] + red[3];
+    if (tid == 0) s4p[static_cast<size_t>(blockIdx.y) * M + m] = red[0] + red[1] + red[2] + red[3];
 }
 
 // ---- GEMM -------------------------------------------------------------------------------------------------------------
@@ -133,7 +139,7 @@ struct GemmArgs {
     int32_t* part;         // kslices x (n_tg * 32) x rows_p partial sums (kslices > 1)
     uint32_t rows, n_tiles, n_chunks, n_ksteps;
     uint32_t M, n_tg, ldy, y_vec4;   // y_vec4: y and ldy allow 16-byte stores
-    uint32_t kslices, ksteps_per_slice, rows_p, s4_parts;
+    uint32_t kslices, ksteps_per_slice, rows_p, s4_parts;  // s4_parts: staging workgroups per token
 };
 
 __device__ __forceinline__ int plane4_sum(const GemmArgs& a, uint32_t m) {
@@ -349,7 +355,7 @@ static GemmPlan gemm_plan(const Geometry& g, size_t M, int num_cus) {
     p.ksteps_per_slice = (p.n_ksteps + best_ks - 1) / best_ks;
     p.kslices = (p.n_ksteps + p.ksteps_per_slice - 1) / p.ksteps_per_slice;
     p.xs_bytes = round_up(static_cast<size_t>(p.n_ksteps) * 5u * p.n_tg * 1024u, 256);
-    p.stage_x = (p.n_ksteps + kStageSteps - 1) / kStageSteps;
+    p.stage_x = (2u * p.n_ksteps + kStagePairs - 1) / kStagePairs;
     p.s4_bytes = round_up(static_cast<size_t>(p.stage_x) * M * 4u, 256);
     p.part_bytes = p.kslices > 1 ? static_cast<size_t>(p.kslices) * p.n_tg * 32u * g.padded_rows * 4u : 0;
     return p;
