@@ -428,6 +428,7 @@ float vxo_q2_0_dot_row(const uint8_t* row, const float* w_scales, const int8_t* 
 void vxo_q2_0_gemv(const uint8_t* packed, const float* w_scales, const int8_t* acts, const float* a_scales,
                    size_t rows, size_t cols, float* out) {
     const size_t rb = vxo_planar_row_bytes(cols);
+#pragma omp parallel for schedule(static)
     for (size_t r = 0; r < rows; ++r)
         out[r] = vxo_q2_0_dot_row(packed + r * rb, w_scales + r * (cols / 64), acts, a_scales, cols);
 }
