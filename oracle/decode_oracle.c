@@ -3,7 +3,9 @@
  *
  * The token loop of BASELINE.json configs[3] (a BitNet-b1.58-2B-shaped model with random weights): RMSNorm, per-token
  * int8 quantization, ternary projections with the layer epilogue, NEOX RoPE, an F16 KV cache, the FP16-accumulator
- * flash attention of bitnet.cpp with its 4-chunk split, sub-norms, ReLU^2, a tied bf16 head and greedy argmax. Each
+ * flash attention of bitnet.cpp with its 4-chunk split, sub-norms, ReLU^2, a tied bf16 head and greedy argmax; and the
+ * Falcon3 variant of the same loop (Normal RoPE, no sub-norms, SwiGLU with ggml's vector expf, an f16 embedding and
+ * an untied f16 head, ModelConfig::falcon3_*_default, config.rs:179-227). Each
  * function names the reference file:line it restates; the FP operations, their order and their fused multiply-adds
  * are the reference's. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline load this code; the product
  * (quintrit_amd/) never calls it. OpenMP splits rows of independent outputs only, so results do not depend on the
@@ -117,6 +119,80 @@ void vxo_rope_neox(float* x, size_t heads, size_t head_dim, const float* cache, 
             head[i] = fmaf(x0, c, -x1s);
             head[i + half] = fmaf(x0, s, x1c);
         }
+    }
+}
+
+/* ops.rs:199-221: Normal pairing (offset 1, stride 2): pair i rotates (x[2i], x[2i + 1]) with the same fused
+ * multiply-adds. */
+void vxo_rope_normal(float* x, size_t heads, size_t head_dim, const float* cache, size_t n_dims) {
+    for (size_t h = 0; h < heads; ++h) {
+        float* head = x + h * head_dim;
+        for (size_t i = 0; i < n_dims / 2; ++i) {
+            const float c = cache[2 * i], s = cache[2 * i + 1];
+            const float x0 = head[2 * i], x1 = head[2 * i + 1];
+            const float x1s = x1 * s, x1c = x1 * c;
+            head[2 * i] = fmaf(x0, c, -x1s);
+            head[2 * i + 1] = fmaf(x0, s, x1c);
+        }
+    }
+}
+
+/* ---- SiLU / SwiGLU ------------------------------------------------------------------------------------------------ */
+
+static float f32_of(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+static uint32_t bits_of(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+/* ops.rs:314-377 (ggml_v_expf_avx2) for one lane. n = round(x log2 e) by the 1.5 * 2^23 shift; b = x - n ln 2 in two
+ * parts (fnmadd = fma with the product negated); j = the degree-5 polynomial of b without its constant term;
+ * k = 2^n built in the exponent field. |n| <= 126: k + k j. Beyond, 2^n is split into s1 s2 (s1 = 2^+-127 by the sign
+ * of n) to reach the subnormal / overflow ranges, and |n| > 192 gives s1 * s1 (0 or inf). A lane's result does not
+ * depend on the other lanes: the whole-vector shortcut returns the same fma(j, k, k). */
+float vxo_ggml_expf(float x) {
+    const float r = f32_of(0x4b400000u);
+    const float z = fmaf(x, f32_of(0x3fb8aa3bu), r);
+    const float n = z - r;
+    const float b = fmaf(-n, f32_of(0x35bfbe8eu), fmaf(-n, f32_of(0x3f317200u), x));
+    const uint32_t e = bits_of(z) << 23;
+    const float k = f32_of(e + bits_of(1.0f));
+    const float u = b * b;
+    const float j = fmaf(fmaf(fmaf(f32_of(0x3c072010u), b, f32_of(0x3d2b9f17u)), u,
+                              fmaf(f32_of(0x3e2aaf33u), b, f32_of(0x3efffedbu))),
+                         u, f32_of(0x3f7ffff6u) * b);
+    if (!(fabsf(n) > 126.0f)) return fmaf(k, j, k);
+    const uint32_t g = n <= 0.0f ? 0x82000000u : 0u;
+    const float s1 = f32_of(g + 0x7f000000u);
+    const float s2 = f32_of(e - g);
+    if (fabsf(n) > 192.0f) return s1 * s1;
+    return fmaf(s2, j, s2) * s1;
+}
+
+void vxo_ggml_expf_batch(const float* x, size_t n, float* out) {
+    for (size_t i = 0; i < n; ++i) out[i] = vxo_ggml_expf(x[i]);
+}
+
+/* ops.rs:430-464 (swiglu, AVX2 + FMA path): blocks of 8 take ggml_v_silu = x / (1 + ggml_v_expf(0 - x)) times up; the
+ * last n % 8 values take v / (1 + expf(-v)) * up with the libm exponential. */
+void vxo_swiglu(const float* gate, const float* up, size_t n, float* out) {
+    const size_t n8 = n / 8 * 8;
+    for (size_t i = 0; i < n8; ++i) {
+        const float v = gate[i];
+        const float den = 1.0f + vxo_ggml_expf(0.0f - v);
+        const float s = v / den;
+        out[i] = s * up[i];
+    }
+    for (size_t i = n8; i < n; ++i) {
+        const float v = gate[i];
+        const float den = 1.0f + expf(-v);
+        const float s = v / den;
+        out[i] = s * up[i];
     }
 }
 
@@ -234,7 +310,8 @@ struct vxo_model {
     float ws[VXO_MAX_LAYERS][NPROJ];
     float* norm[VXO_MAX_LAYERS][4]; /* attn_norm, attn_sub_norm, ffn_norm, ffn_sub_norm */
     float* out_norm;
-    uint16_t* emb; /* bf16 [vocab][hidden], also the tied head */
+    uint16_t* emb;  /* bf16 or f16 [vocab][hidden], also the head when tied */
+    uint16_t* head; /* the untied head (same type), or NULL */
     uint16_t* kc;  /* f16 [layer][pos][kv_head][head_dim] (kv_cache.rs:32-35) */
     uint16_t* vc;
     float* rope; /* [max_ctx][head_dim] cos/sin pairs */
@@ -291,6 +368,7 @@ vxo_model* vxo_model_create(const vxo_model_config* cfg, uint64_t seed) {
     for (size_t l = 0; l <= L; ++l) {
         for (int k = 0; k < 4; ++k) {
             if (l == L && k > 0) break;
+            if (cfg->no_sub_norm && (k == 1 || k == 3)) continue;
             const size_t n = (k == 3) ? cfg->ffn : (k == 1 ? (size_t)cfg->n_heads * cfg->head_dim : cfg->hidden);
             float* w = (float*)malloc(n * sizeof(float));
             uint64_t st = mix_seed(seed, 1000 + l, (uint64_t)k);
@@ -300,15 +378,20 @@ vxo_model* vxo_model_create(const vxo_model_config* cfg, uint64_t seed) {
         }
     }
     const size_t ne = (size_t)cfg->vocab * cfg->hidden;
-    m->emb = (uint16_t*)malloc(ne * 2);
     const size_t rows_per = 1024;
+    for (int t = 0; t < (cfg->untied ? 2 : 1); ++t) {
+        uint16_t* dst = (uint16_t*)malloc(ne * 2);
+        if (t == 0) m->emb = dst;
+        else m->head = dst;
 #pragma omp parallel for schedule(dynamic)
-    for (size_t r0 = 0; r0 < cfg->vocab; r0 += rows_per) {
-        const size_t r1 = r0 + rows_per < cfg->vocab ? r0 + rows_per : cfg->vocab;
-        float* tmp = (float*)malloc((r1 - r0) * cfg->hidden * sizeof(float));
-        gen_normal(mix_seed(seed, 5000 + r0, 0), (r1 - r0) * cfg->hidden, 0.02f, tmp);
-        for (size_t i = 0; i < (r1 - r0) * cfg->hidden; ++i) m->emb[r0 * cfg->hidden + i] = vxo_f32_to_bf16(tmp[i]);
-        free(tmp);
+        for (size_t r0 = 0; r0 < cfg->vocab; r0 += rows_per) {
+            const size_t r1 = r0 + rows_per < cfg->vocab ? r0 + rows_per : cfg->vocab;
+            float* tmp = (float*)malloc((r1 - r0) * cfg->hidden * sizeof(float));
+            gen_normal(mix_seed(seed, 5000 + r0, (uint64_t)t), (r1 - r0) * cfg->hidden, 0.02f, tmp);
+            for (size_t i = 0; i < (r1 - r0) * cfg->hidden; ++i)
+                dst[r0 * cfg->hidden + i] = cfg->emb_f16 ? vxo_f32_to_f16(tmp[i]) : vxo_f32_to_bf16(tmp[i]);
+            free(tmp);
+        }
     }
     const size_t kvn = L * cfg->max_ctx * cfg->n_kv_heads * cfg->head_dim;
     m->kc = (uint16_t*)calloc(kvn, 2);
@@ -326,6 +409,7 @@ void vxo_model_free(vxo_model* m) {
     }
     free(m->out_norm);
     free(m->emb);
+    free(m->head);
     free(m->kc);
     free(m->vc);
     free(m->rope);
@@ -340,6 +424,7 @@ const float* vxo_model_norm(const vxo_model* m, size_t layer, int kind) {
     return layer == m->cfg.n_layers ? m->out_norm : m->norm[layer][kind];
 }
 const uint16_t* vxo_model_embedding(const vxo_model* m) { return m->emb; }
+const uint16_t* vxo_model_head(const vxo_model* m) { return m->head ? m->head : m->emb; }
 const float* vxo_model_rope_table(const vxo_model* m) { return m->rope; }
 
 void vxo_model_reset(vxo_model* m) {
@@ -368,7 +453,10 @@ uint32_t vxo_model_forward(vxo_model* m, uint32_t token, size_t pos, float* logi
     float* inter = (float*)malloc(F * 4);
     uint16_t* qh = (uint16_t*)malloc(qd * 2);
 
-    for (size_t i = 0; i < H; ++i) x[i] = vxo_bf16_to_f32(m->emb[(size_t)token * H + i]);
+    for (size_t i = 0; i < H; ++i) {  /* model.rs:309-316 */
+        const uint16_t e = m->emb[(size_t)token * H + i];
+        x[i] = c->emb_f16 ? vxo_f16_to_f32(e) : vxo_bf16_to_f32(e);
+    }
     const float scale = 1.0f / sqrtf((float)hd);
     const size_t pos_stride = (size_t)c->n_kv_heads * hd;
     for (size_t l = 0; l < c->n_layers; ++l) {
@@ -379,8 +467,13 @@ uint32_t vxo_model_forward(vxo_model* m, uint32_t token, size_t pos, float* logi
         vxo_projection(m->w[l][K], kvd, H, m->ws[l][K], qi, as, k);
         vxo_projection(m->w[l][V], kvd, H, m->ws[l][V], qi, as, v);
         const float* cache = m->rope + pos * hd;
-        vxo_rope_neox(q, c->n_heads, hd, cache, hd);
-        vxo_rope_neox(k, c->n_kv_heads, hd, cache, hd);
+        if (c->rope_mode == VXO_ROPE_NORMAL) {
+            vxo_rope_normal(q, c->n_heads, hd, cache, hd);
+            vxo_rope_normal(k, c->n_kv_heads, hd, cache, hd);
+        } else {
+            vxo_rope_neox(q, c->n_heads, hd, cache, hd);
+            vxo_rope_neox(k, c->n_kv_heads, hd, cache, hd);
+        }
         uint16_t* kl = m->kc + l * c->max_ctx * pos_stride;
         uint16_t* vl = m->vc + l * c->max_ctx * pos_stride;
         for (size_t i = 0; i < kvd; ++i) {
@@ -395,8 +488,12 @@ uint32_t vxo_model_forward(vxo_model* m, uint32_t token, size_t pos, float* logi
             vxo_attend_head(qh + h * hd, kl + kvh * hd, vl + kvh * hd, pos_stride, hd, pos + 1, c->max_ctx, scale,
                             att + h * hd);
         }
-        vxo_rms_norm(att, m->norm[l][1], qd, c->rms_eps, xn);
-        as = vxo_quantize_i8(xn, qd, 127.0f, qi);
+        if (c->no_sub_norm) { /* attention.rs:232-254 */
+            as = vxo_quantize_i8(att, qd, 127.0f, qi);
+        } else {
+            vxo_rms_norm(att, m->norm[l][1], qd, c->rms_eps, xn);
+            as = vxo_quantize_i8(xn, qd, 127.0f, qi);
+        }
         vxo_projection(m->w[l][O], H, qd, m->ws[l][O], qi, as, proj);
         for (size_t i = 0; i < H; ++i) x[i] = x[i] + proj[i];
         /* feed-forward block (model.rs:101-199) */
@@ -404,22 +501,33 @@ uint32_t vxo_model_forward(vxo_model* m, uint32_t token, size_t pos, float* logi
         as = vxo_quantize_i8(xn, H, 127.0f, qi);
         vxo_projection(m->w[l][GATE], F, H, m->ws[l][GATE], qi, as, gate);
         vxo_projection(m->w[l][UP], F, H, m->ws[l][UP], qi, as, up);
-        for (size_t i = 0; i < F; ++i) { /* relu2 then elementwise_mul (ops.rs:301-308, 467-473) */
-            const float p = gate[i] > 0.0f ? gate[i] : 0.0f;
-            const float a = p * p;
-            inter[i] = a * up[i];
+        if (c->act == VXO_ACT_SILU) {
+            vxo_swiglu(gate, up, F, inter);
+        } else {
+            for (size_t i = 0; i < F; ++i) { /* relu2 then elementwise_mul (ops.rs:301-308, 467-473) */
+                const float p = gate[i] > 0.0f ? gate[i] : 0.0f;
+                const float a = p * p;
+                inter[i] = a * up[i];
+            }
         }
-        vxo_rms_norm(inter, m->norm[l][3], F, c->rms_eps, xn);
-        as = vxo_quantize_i8(xn, F, 127.0f, qi);
+        if (c->no_sub_norm) { /* model.rs:172-190 */
+            as = vxo_quantize_i8(inter, F, 127.0f, qi);
+        } else {
+            vxo_rms_norm(inter, m->norm[l][3], F, c->rms_eps, xn);
+            as = vxo_quantize_i8(xn, F, 127.0f, qi);
+        }
         vxo_projection(m->w[l][DOWN], H, F, m->ws[l][DOWN], qi, as, proj);
         for (size_t i = 0; i < H; ++i) x[i] = x[i] + proj[i];
     }
-    /* final norm and tied bf16 head (model.rs:326-376 with the head in bf16, ggml_vec_dot_bf16) */
+    /* final norm and the head (model.rs:326-376): x_final rounded to the head's type, then ggml_vec_dot_f16 (f16) or
+     * ggml_vec_dot_bf16 (bf16) against every row of the head (the embedding when tied) */
     vxo_rms_norm(x, m->out_norm, H, c->rms_eps, xn);
     uint16_t* xb = (uint16_t*)malloc(H * 2);
-    for (size_t i = 0; i < H; ++i) xb[i] = vxo_f32_to_bf16(xn[i]);
+    for (size_t i = 0; i < H; ++i) xb[i] = c->emb_f16 ? vxo_f32_to_f16(xn[i]) : vxo_f32_to_bf16(xn[i]);
+    const uint16_t* hw = m->head ? m->head : m->emb;
 #pragma omp parallel for schedule(static)
-    for (size_t r = 0; r < c->vocab; ++r) logits[r] = vxo_ggml_dot_bf16(xb, m->emb + r * H, H);
+    for (size_t r = 0; r < c->vocab; ++r)
+        logits[r] = c->emb_f16 ? vxo_ggml_dot_f16(xb, hw + r * H, H) : vxo_ggml_dot_bf16(xb, hw + r * H, H);
     uint32_t best = 0;
     float bv = logits[0];
     for (size_t r = 1; r < c->vocab; ++r)

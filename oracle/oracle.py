@@ -82,6 +82,11 @@ def _declare(L: ctypes.CDLL) -> None:
         "vxo_expf_batch": (None, [vp, sz, vp]),
         "vxo_rope_cache": (None, [sz, sz, f32, vp]),
         "vxo_rope_neox": (None, [vp, sz, sz, vp, sz]),
+        "vxo_rope_normal": (None, [vp, sz, sz, vp, sz]),
+        "vxo_ggml_expf": (f32, [f32]),
+        "vxo_ggml_expf_batch": (None, [vp, sz, vp]),
+        "vxo_swiglu": (None, [vp, vp, sz, vp]),
+        "vxo_model_head": (vp, [vp]),
         "vxo_attend_head": (None, [vp, vp, vp, sz, sz, sz, sz, f32, vp]),
         "vxo_projection": (None, [vp, sz, sz, f32, vp, f32, vp]),
         "vxo_projection_shape": (None, [vp, ctypes.c_int, vp, vp]),
@@ -302,17 +307,41 @@ def gen_i8(seed: int, n: int, lo: int = -127, hi: int = 127) -> np.ndarray:
 
 # ---- decode step (decode_oracle.c) ----------------------------------------------------------------------------------
 
+ACT_RELU2, ACT_SILU = 0, 1
+ROPE_NEOX, ROPE_NORMAL = 0, 1
+
+
 class ModelConfig(ctypes.Structure):
-    """vxo_model_config: the decoder shape (BASELINE.json configs[3] uses bitnet_2b())."""
+    """vxo_model_config: the decoder shape and its architecture switches (all zero: the BitNet of BASELINE.json
+    configs[3], bitnet_2b(); falcon3() sets SiLU, Normal RoPE, no sub-norms, an f16 embedding and an untied f16 head)."""
     _fields_ = [("n_layers", ctypes.c_uint32), ("hidden", ctypes.c_uint32), ("n_heads", ctypes.c_uint32),
                 ("n_kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32), ("ffn", ctypes.c_uint32),
                 ("vocab", ctypes.c_uint32), ("max_ctx", ctypes.c_uint32), ("rms_eps", ctypes.c_float),
-                ("rope_theta", ctypes.c_float)]
+                ("rope_theta", ctypes.c_float), ("act", ctypes.c_uint32), ("rope_mode", ctypes.c_uint32),
+                ("no_sub_norm", ctypes.c_uint32), ("emb_f16", ctypes.c_uint32), ("untied", ctypes.c_uint32)]
+
+    @property
+    def is_falcon3(self) -> bool:
+        return self.act == ACT_SILU
 
 
 def bitnet_2b(max_ctx: int = 4096) -> ModelConfig:
     """ModelConfig::bitnet_2b_default (quintrit-runtime/src/config.rs:155-177)."""
     return ModelConfig(30, 2560, 20, 5, 128, 6912, 128256, max_ctx, 1e-5, 500000.0)
+
+
+def falcon3(n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx, rms_eps=1e-5,
+            rope_theta=100000.0) -> ModelConfig:
+    """A Falcon3-architecture config (ModelConfig::falcon3_*_default, config.rs:179-227): SiLU / SwiGLU, Normal RoPE,
+    no sub-norms, f16 embedding and an untied f16 head."""
+    return ModelConfig(n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx, rms_eps, rope_theta,
+                       ACT_SILU, ROPE_NORMAL, 1, 1, 1)
+
+
+def falcon3_10b(max_ctx: int = 4096, n_layers: int = 40) -> ModelConfig:
+    """BASELINE.json configs[1]'s Falcon3-10B shapes (40 layers, hidden 3072, 12 / 4 heads of 256, FFN 23040) with the
+    Falcon3 vocabulary (131072) and the other constants of falcon3_7b_default (config.rs:205-227)."""
+    return falcon3(n_layers, 3072, 12, 4, 256, 23040, 131072, max_ctx)
 
 
 PROJ_NAMES = ("q", "k", "v", "o", "gate", "up", "down")
@@ -348,17 +377,27 @@ class Model:
         n = rows * planar_row_bytes(cols)
         return np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(p)).copy(), float(ws.value)
 
-    def norm(self, layer: int, kind: int) -> np.ndarray:
+    def norm(self, layer: int, kind: int):
+        """RMSNorm weights (a copy), or None for a sub-norm of a model without them."""
         c = self.cfg
         n = c.ffn if kind == 3 else (c.n_heads * c.head_dim if kind == 1 else c.hidden)
         if layer == c.n_layers:
             n = c.hidden
         p = lib().vxo_model_norm(self._h, layer, kind)
+        if not p:
+            return None
         return np.ctypeslib.as_array((ctypes.c_float * n).from_address(p)).copy()
 
     def embedding(self) -> np.ndarray:
+        """bf16 or f16 bits (cfg.emb_f16), vocab x hidden, a view into the model."""
         n = self.cfg.vocab * self.cfg.hidden
         p = lib().vxo_model_embedding(self._h)
+        return np.ctypeslib.as_array((ctypes.c_uint16 * n).from_address(p)).reshape(self.cfg.vocab, self.cfg.hidden)
+
+    def head(self) -> np.ndarray:
+        """The head (the embedding when tied), same type, a view into the model."""
+        n = self.cfg.vocab * self.cfg.hidden
+        p = lib().vxo_model_head(self._h)
         return np.ctypeslib.as_array((ctypes.c_uint16 * n).from_address(p)).reshape(self.cfg.vocab, self.cfg.hidden)
 
     def rope_table(self) -> np.ndarray:
@@ -429,6 +468,31 @@ def rope_neox(x: np.ndarray, heads: int, head_dim: int, cache: np.ndarray) -> np
     out = np.ascontiguousarray(x, np.float32).copy()
     c = np.ascontiguousarray(cache, np.float32)
     lib().vxo_rope_neox(_p(out), heads, head_dim, _p(c), c.size)
+    return out
+
+
+def rope_normal(x: np.ndarray, heads: int, head_dim: int, cache: np.ndarray) -> np.ndarray:
+    out = np.ascontiguousarray(x, np.float32).copy()
+    c = np.ascontiguousarray(cache, np.float32)
+    lib().vxo_rope_normal(_p(out), heads, head_dim, _p(c), c.size)
+    return out
+
+
+def ggml_expf(x: float) -> float:
+    return float(np.float32(lib().vxo_ggml_expf(float(x))))
+
+
+def ggml_expf_array(x: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    lib().vxo_ggml_expf_batch(_p(a), a.size, _p(out))
+    return out
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    g, u = np.ascontiguousarray(gate, np.float32), np.ascontiguousarray(up, np.float32)
+    out = np.empty_like(g)
+    lib().vxo_swiglu(_p(g), _p(u), g.size, _p(out))
     return out
 
 
