@@ -286,25 +286,35 @@ typedef struct vx_q2_job {
 int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan);
 
 /* ---- decode token loop ------------------------------------------------------------------------------------------------
- * A ternary decoder of the BitNet-b1.58 family on one GPU, step for step the reference's CPU token loop
+ * A ternary decoder of the BitNet-b1.58 / Falcon3 families on one GPU, step for step the reference's CPU token loop
  * (QuintritModel::forward_token_with_scratchpad, quintrit-runtime/src/model.rs:282-377, with
  * AttentionBlock::forward_with_scratchpad, attention.rs:115-260, and the BitnetCpp numerics: RMSNorm with an f64 sum,
- * per-token absmax int8, velurex projections with the fp32 epilogue, NEOX RoPE, an F16 KV cache, FP16-accumulator
- * attention with the 4-chunk split, sub-norms, ReLU^2, a tied bf16 head, greedy argmax), so that logits and tokens are
- * bit-identical to it. One step is one HIP graph of 1 + 5 per layer kernels: per layer the q/k/v, o, gate/up and down
- * projection stages (each computing its own input: embedding or residual add or ReLU^2 * up, RMSNorm, int8
- * quantization) and attention (RoPE, KV append), then the final norm, head and argmax in one kernel, with the position
- * and the token kept on the device (the reference's CUDA decode graph does the same,
- * quintrit-runtime/src/gpu.rs:459-493).
- * Supported: head_dim 128, max_ctx <= 4096, hidden, n_heads * head_dim and ffn <= 8192, hidden a multiple of 32, ffn a
- * multiple of 4. */
+ * per-token absmax int8, velurex projections with the fp32 epilogue, RoPE (NEOX or Normal), an F16 KV cache,
+ * FP16-accumulator attention with the 4-chunk split, optional sub-norms, ReLU^2 or SwiGLU (ggml's vector expf), a
+ * bf16 or f16 head, tied or not, greedy argmax), so that logits and tokens are bit-identical to it. One step is one HIP
+ * graph of 1 + 5 per layer kernels: per layer the q/k/v, o, gate/up and down projection stages (each computing its
+ * own input: embedding or residual add or gating, RMSNorm, int8 quantization) and attention (RoPE, KV append), then
+ * the final norm, head and argmax in one kernel, with the position and the token kept on the device (the reference's
+ * CUDA decode graph does the same, quintrit-runtime/src/gpu.rs:459-493).
+ * Supported: head_dim 128 or 256, max_ctx <= 4096, hidden a multiple of 32 up to 8192 (4480 with SiLU),
+ * n_heads * head_dim <= 8192, ffn a multiple of 4 up to 8192 (24576 with SiLU and no sub-norms). */
 typedef struct vx_decoder vx_decoder_t;
 
 typedef struct vx_decoder_config {
-    uint32_t struct_size; /* sizeof(vx_decoder_config_t) */
+    uint32_t struct_size; /* sizeof(vx_decoder_config_t); a size that ends at rope_theta leaves the switches 0 */
     uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx;
     float rms_eps, rope_theta;
+    /* Architecture switches (ModelConfig, config.rs:155-227); all 0 is ModelConfig::bitnet_2b_default with a bf16
+     * tied head, the Falcon3 defaults are VX_ACT_SILU, VX_ROPE_NORMAL, no_sub_norm 1, emb_f16 1, untied 1. */
+    uint32_t act;         /* VX_ACT_RELU2: relu2(gate) * up; VX_ACT_SILU: swiglu(gate, up) (model.rs:155-170) */
+    uint32_t rope_mode;   /* VX_ROPE_NEOX or VX_ROPE_NORMAL (ops.rs:199-221) */
+    uint32_t no_sub_norm; /* 1: no attention / FFN sub-norms (has_sub_norm = false) */
+    uint32_t emb_f16;     /* 0: bf16 embedding and head (ggml_vec_dot_bf16); 1: f16 (ggml_vec_dot_f16, model.rs:347-373) */
+    uint32_t untied;      /* 1: a head of its own (lm_head_f16, vx_decoder_set_head); 0: the embedding is the head */
 } vx_decoder_config_t;
+
+enum { VX_ACT_RELU2 = 0, VX_ACT_SILU = 1 };
+enum { VX_ROPE_NEOX = 0, VX_ROPE_NORMAL = 1 };
 
 /* Projection kinds (vx_decoder_set_projection) and norm kinds (vx_decoder_set_norm). */
 enum {
@@ -312,16 +322,20 @@ enum {
 };
 enum { VX_NORM_ATTN = 0, VX_NORM_ATTN_SUB = 1, VX_NORM_FFN = 2, VX_NORM_FFN_SUB = 3 };
 
-/* ModelConfig (quintrit-runtime/src/config.rs:155-177) of the model; allocates the KV cache and work buffers. */
+/* ModelConfig (quintrit-runtime/src/config.rs:155-227) of the model; allocates the KV cache and work buffers. */
 int vx_decoder_create(const vx_decoder_config_t* config, vx_decoder_t** out_decoder);
 /* A planar velurex matrix (host memory) with its per-tensor scale: Q/K/V rows n_heads*head_dim or n_kv_heads*head_dim,
  * cols hidden; O hidden x n_heads*head_dim; gate/up ffn x hidden; down hidden x ffn (the reference's BitLinear). */
 int vx_decoder_set_projection(vx_decoder_t* decoder, uint32_t layer, uint32_t kind, const uint8_t* planar,
                               size_t planar_len, float weight_scale);
-/* RMSNorm weights (host f32). layer == n_layers with kind VX_NORM_ATTN sets the output norm. */
+/* RMSNorm weights (host f32). layer == n_layers with kind VX_NORM_ATTN sets the output norm; the sub-norm kinds are
+ * rejected when no_sub_norm is set. */
 int vx_decoder_set_norm(vx_decoder_t* decoder, uint32_t layer, uint32_t kind, const float* weights, size_t n);
-/* The tied embedding / head, vocab x hidden bf16 (host). */
+/* The embedding (also the head when tied), vocab x hidden (host): bf16 when emb_f16 is 0, else f16. */
 int vx_decoder_set_embedding_bf16(vx_decoder_t* decoder, const uint16_t* embedding, size_t n);
+int vx_decoder_set_embedding_f16(vx_decoder_t* decoder, const uint16_t* embedding, size_t n);
+/* The untied head (untied = 1), vocab x hidden in the embedding's type (host). */
+int vx_decoder_set_head(vx_decoder_t* decoder, const uint16_t* head, size_t n);
 /* One token at position pos (forward_token): KV entries 0..pos-1 must come from earlier steps. logits (host, may be
  * NULL) receives vocab values; out_next (may be NULL) the greedy token. */
 int vx_decoder_step(vx_decoder_t* decoder, uint32_t token, uint32_t pos, float* logits, size_t logits_capacity,

@@ -79,6 +79,8 @@ SIGNATURES = {
     "vx_decoder_set_projection": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _sz, _f32]),
     "vx_decoder_set_norm": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _sz]),
     "vx_decoder_set_embedding_bf16": (_i32, [_vp, _vp, _sz]),
+    "vx_decoder_set_embedding_f16": (_i32, [_vp, _vp, _sz]),
+    "vx_decoder_set_head": (_i32, [_vp, _vp, _sz]),
     "vx_decoder_step": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _sz, _vp]),
     "vx_decoder_generate": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz]),
     "vx_decoder_memory_bytes": (_i32, [_vp, _vp]),

@@ -119,14 +119,14 @@ __device__ __forceinline__ float wave_max_f32(float x) {
     return fmax_nn(fmax_nn(a, b), fmax_nn(c, d));
 }
 
-// ---- the stage input: embedding / residual add / ReLU^2 gating, RMSNorm, int8 quantization --------------------------------
+// ---- the stage input: embedding / residual add / gating, RMSNorm, int8 quantization --------------------------------------
 
 constexpr int kNT = 1024;            // threads of the kernels that compute a stage input
-constexpr uint32_t kNormMax = 8192;  // longest input vector
-constexpr uint32_t kStChunks = 112;  // 16-byte chunks of a staged input in LDS (device_row_bytes(8192) / 16 + 4 fit)
-constexpr int kPer4 = kNormMax / (4 * kNT);  // float4 groups of the input per thread at most
-constexpr int kMaxSlicesA = 6;       // K slices of a projection read as a residual-add input or a stage-0 head input
-constexpr int kMaxSlicesB = 2;       // K slices of the gate and up projections (the ReLU^2 inputs)
+constexpr uint32_t kNormMax = 8192;  // longest normed input, and the LDS window of a staged input slice (floats)
+constexpr uint32_t kPlainMax = 24576;  // longest input without a norm (6 float4 groups per thread)
+constexpr uint32_t kStChunks = 112;  // 16-byte chunks of a staged input slice in LDS (16 waves x kDPer)
+constexpr int kMaxSlicesA = 6;       // K slices of a projection read as a residual-add input or by the attention
+constexpr int kMaxSlicesB = 2;       // K slices of the gate and up projections read by a ReLU^2 input
 
 struct Ctl {          // device-resident loop state
     uint32_t pos;     // position of the step
@@ -172,34 +172,37 @@ __device__ __forceinline__ float proj_at(const ProjOut& o, uint32_t i, float pos
 }
 
 enum InputKind : uint32_t {
-    kInEmbed = 0,     // v = the token's embedding row (bf16 -> f32, model.rs:309-316); the token from the loop state
+    kInEmbed = 0,     // v = the token's embedding row (bf16 or f16 -> f32, model.rs:309-316); the token from the loop state
     kInResidual = 1,  // v = x_in[i] + a[i] (add_residual, ops.rs:476-481)
     kInPlain = 2,     // v = x_in[i]
     kInRelu2Mul = 3,  // v = relu2(a[i]) * b[i] (ops.rs:301-308, 467-473)
 };
 
 struct StageInput {
-    uint32_t kind, n;     // n: a multiple of 4, at most kNormMax
+    uint32_t kind, n;     // n: a multiple of 4
     const float* x_in;
     ProjOut a, b;         // the previous projections (residual: o or down; ReLU^2: gate and up)
     float* x_out;         // kInEmbed, kInResidual: v, the residual stream (workgroup 0 writes it), or null
-    const float* gamma;   // RMSNorm weights
+    const float* gamma;   // RMSNorm weights (n <= kNormMax), or null: no norm, y = v (a model without sub-norms)
     float eps;
     const Ctl* ctl;       // kInEmbed
     const uint32_t* prompt;
     const uint16_t* emb;
+    uint32_t emb_f16;     // kInEmbed: the embedding holds f16 (else bf16)
 };
 
-// The loaded inputs of a thread: element e of float4 group k is 4 (tid + k kNT) + e.
+// The loaded inputs of a thread: element e of float4 group k is 4 (tid + k kNT) + e. P4 groups cover P4 * 4 kNT
+// elements; SA and SB K slices of the projections a and b (0: the kernel variant reads none).
+template <int P4, int SA, int SB>
 struct InputRegs {
-    uint4 x[kPer4];                // embedding bits (x, y) or x_in
-    int4 pa[kMaxSlicesA][kPer4];   // K-slice partials of a
-    int4 pb[kMaxSlicesB][kPer4];   // K-slice partials of b
-    float4 g[kPer4];               // gamma
+    uint4 x[P4];                         // embedding bits (x, y) or x_in
+    int4 pa[SA > 0 ? SA : 1][P4];        // K-slice partials of a
+    int4 pb[SB > 0 ? SB : 1][P4];        // K-slice partials of b
+    float4 g[P4];                        // gamma
 };
 
 struct __align__(16) InputLds {  // ys is accessed 16 bytes at a time
-    float ys[kNormMax];
+    float ys[kNormMax];          // v (a normed input, for the reference-order fallback), then this workgroup's y window
     double red_d[kNT / 64];
     float red_f[kNT / 64];
     int red_i[kNT / 64];
@@ -208,93 +211,101 @@ struct __align__(16) InputLds {  // ys is accessed 16 bytes at a time
 
 __device__ __forceinline__ uint32_t elem4(uint32_t tid, int k) { return 4u * (tid + static_cast<uint32_t>(k) * kNT); }
 
-
 // Issues every load of the thread's inputs (16 bytes each) without using any, so that the loads a kernel issues after
 // it (weights) do not delay them: vector-memory loads complete in issue order.
-__device__ __forceinline__ void stage_load(const StageInput& p, InputRegs& r) {
+template <int P4, int SA, int SB>
+__device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA, SB>& r) {
     const uint32_t tid = threadIdx.x, n = p.n;
     if (p.kind == kInEmbed) {
         const uint32_t pos = p.ctl->pos;
         const uint32_t tok = pos < p.ctl->n_prompt ? p.prompt[pos] : p.ctl->token;
         const uint2* row = reinterpret_cast<const uint2*>(p.emb + static_cast<size_t>(tok) * n);
 #pragma unroll
-        for (int k = 0; k < kPer4; ++k) {
+        for (int k = 0; k < P4; ++k) {
             const uint32_t i = elem4(tid, k);
             const uint2 e = load_if(row + i / 4u, i < n);
             r.x[k] = make_uint4(e.x, e.y, 0u, 0u);
         }
     } else if (p.kind != kInRelu2Mul) {
 #pragma unroll
-        for (int k = 0; k < kPer4; ++k) {
+        for (int k = 0; k < P4; ++k) {
             const uint32_t i = elem4(tid, k);
             r.x[k] = load_if(reinterpret_cast<const uint4*>(p.x_in + i), i < n);
         }
     }
-    if (p.kind == kInResidual || p.kind == kInRelu2Mul) {
+    if constexpr (SA > 0) {
+        if (p.kind == kInResidual || p.kind == kInRelu2Mul) {
 #pragma unroll
-        for (int s = 0; s < kMaxSlicesA; ++s)
+            for (int s = 0; s < SA; ++s)
 #pragma unroll
-            for (int k = 0; k < kPer4; ++k) {
-                const uint32_t i = elem4(tid, k);
-                r.pa[s][k] = load_if(reinterpret_cast<const int4*>(p.a.part + static_cast<size_t>(s) * p.a.stride + i),
-                                     i < n && static_cast<uint32_t>(s) < p.a.kslices);
-            }
+                for (int k = 0; k < P4; ++k) {
+                    const uint32_t i = elem4(tid, k);
+                    r.pa[s][k] = load_if(reinterpret_cast<const int4*>(p.a.part + static_cast<size_t>(s) * p.a.stride + i),
+                                         i < n && static_cast<uint32_t>(s) < p.a.kslices);
+                }
+        }
     }
-    if (p.kind == kInRelu2Mul) {
+    if constexpr (SB > 0) {
+        if (p.kind == kInRelu2Mul) {
 #pragma unroll
-        for (int s = 0; s < kMaxSlicesB; ++s)
+            for (int s = 0; s < SB; ++s)
 #pragma unroll
-            for (int k = 0; k < kPer4; ++k) {
-                const uint32_t i = elem4(tid, k);
-                r.pb[s][k] = load_if(reinterpret_cast<const int4*>(p.b.part + static_cast<size_t>(s) * p.b.stride + i),
-                                     i < n && static_cast<uint32_t>(s) < p.b.kslices);
-            }
+                for (int k = 0; k < P4; ++k) {
+                    const uint32_t i = elem4(tid, k);
+                    r.pb[s][k] = load_if(reinterpret_cast<const int4*>(p.b.part + static_cast<size_t>(s) * p.b.stride + i),
+                                         i < n && static_cast<uint32_t>(s) < p.b.kslices);
+                }
+        }
     }
+    if (p.gamma != nullptr) {
 #pragma unroll
-    for (int k = 0; k < kPer4; ++k) {
-        const uint32_t i = elem4(tid, k);
-        r.g[k] = load_if(reinterpret_cast<const float4*>(p.gamma + i), i < n);
+        for (int k = 0; k < P4; ++k) {
+            const uint32_t i = elem4(tid, k);
+            r.g[k] = load_if(reinterpret_cast<const float4*>(p.gamma + i), i < n);
+        }
     }
 }
 
-// v (by kind) from the loaded inputs into s.ys, then its RMSNorm y = (v * inv) * gamma (rms_norm, ops.rs:19-96) in
-// place. Every thread derives the mean from the per-wave sums itself, so the common path has one barrier. Returns this
-// thread's largest |y| (NaN never counts); the elements of s.ys a thread did not write are readable after the next
-// barrier. With write_x, an input that has an x_out also stores v there.
-__device__ __forceinline__ float stage_norm(const StageInput& p, const InputRegs& r, InputLds& s, bool write_x) {
+template <int P4, int SA>
+__device__ __forceinline__ void slice_sums(const int4 (&pa)[SA > 0 ? SA : 1][P4], int k, int32_t (&sa)[4]) {
+    sa[0] = pa[0][k].x;
+    sa[1] = pa[0][k].y;
+    sa[2] = pa[0][k].z;
+    sa[3] = pa[0][k].w;
+#pragma unroll
+    for (int s2 = 1; s2 < SA; ++s2) {
+        sa[0] += pa[s2][k].x;
+        sa[1] += pa[s2][k].y;
+        sa[2] += pa[s2][k].z;
+        sa[3] += pa[s2][k].w;
+    }
+}
+
+// y of the thread's elements: v by kind, then (with gamma) its RMSNorm y = (v * inv) * gamma (rms_norm, ops.rs:19-96).
+// Every thread derives the mean from the per-wave sums itself, so the common path has one barrier; without gamma none.
+// With write_x, an input that has an x_out also stores v there.
+template <int P4, int SA, int SB>
+__device__ __forceinline__ void stage_y(const StageInput& p, const InputRegs<P4, SA, SB>& r, InputLds& s, bool write_x,
+                                        float (&y)[P4][4]) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t n = p.n;
-    float v[kPer4][4];
+    float v[P4][4];
     if (p.kind == kInEmbed) {
 #pragma unroll
-        for (int k = 0; k < kPer4; ++k) {
-            v[k][0] = bits_f32(r.x[k].x << 16);
-            v[k][1] = bits_f32(r.x[k].x & 0xffff0000u);
-            v[k][2] = bits_f32(r.x[k].y << 16);
-            v[k][3] = bits_f32(r.x[k].y & 0xffff0000u);
+        for (int k = 0; k < P4; ++k) {
+            const uint32_t h[4] = {r.x[k].x & 0xffffu, r.x[k].x >> 16, r.x[k].y & 0xffffu, r.x[k].y >> 16};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[k][e] = p.emb_f16 ? f16_f32(static_cast<uint16_t>(h[e])) : bits_f32(h[e] << 16);
         }
-    } else if (p.kind == kInRelu2Mul) {
+    } else if (SA > 0 && SB > 0 && p.kind == kInRelu2Mul) {
         bool za, zb;
         const float pa = proj_post(p.a, &za), pb = proj_post(p.b, &zb);
 #pragma unroll
-        for (int k = 0; k < kPer4; ++k) {
-            const int32_t ga[4] = {r.pa[0][k].x, r.pa[0][k].y, r.pa[0][k].z, r.pa[0][k].w};
-            const int32_t ub[4] = {r.pb[0][k].x, r.pb[0][k].y, r.pb[0][k].z, r.pb[0][k].w};
-            int32_t sa[4] = {ga[0], ga[1], ga[2], ga[3]}, sb[4] = {ub[0], ub[1], ub[2], ub[3]};
-#pragma unroll
-            for (int s2 = 1; s2 < kMaxSlicesA; ++s2) {
-                sa[0] += r.pa[s2][k].x;
-                sa[1] += r.pa[s2][k].y;
-                sa[2] += r.pa[s2][k].z;
-                sa[3] += r.pa[s2][k].w;
-            }
-#pragma unroll
-            for (int s2 = 1; s2 < kMaxSlicesB; ++s2) {
-                sb[0] += r.pb[s2][k].x;
-                sb[1] += r.pb[s2][k].y;
-                sb[2] += r.pb[s2][k].z;
-                sb[3] += r.pb[s2][k].w;
-            }
+        for (int k = 0; k < P4; ++k) {
+            int32_t sa[4], sb[4];
+            slice_sums<P4, SA>(r.pa, k, sa);
+            slice_sums<P4, SB>(r.pb, k, sb);
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float g = proj_value(sa[e], pa, za), u = proj_value(sb[e], pb, zb);
@@ -305,39 +316,40 @@ __device__ __forceinline__ float stage_norm(const StageInput& p, const InputRegs
         }
     } else {
 #pragma unroll
-        for (int k = 0; k < kPer4; ++k) {
+        for (int k = 0; k < P4; ++k) {
             v[k][0] = bits_f32(r.x[k].x);
             v[k][1] = bits_f32(r.x[k].y);
             v[k][2] = bits_f32(r.x[k].z);
             v[k][3] = bits_f32(r.x[k].w);
         }
-        if (p.kind == kInResidual) {
+        if (SA > 0 && p.kind == kInResidual) {
             bool za;
             const float pa = proj_post(p.a, &za);
 #pragma unroll
-            for (int k = 0; k < kPer4; ++k) {
-                int32_t sa[4] = {r.pa[0][k].x, r.pa[0][k].y, r.pa[0][k].z, r.pa[0][k].w};
-#pragma unroll
-                for (int s2 = 1; s2 < kMaxSlicesA; ++s2) {
-                    sa[0] += r.pa[s2][k].x;
-                    sa[1] += r.pa[s2][k].y;
-                    sa[2] += r.pa[s2][k].z;
-                    sa[3] += r.pa[s2][k].w;
-                }
+            for (int k = 0; k < P4; ++k) {
+                int32_t sa[4];
+                slice_sums<P4, SA>(r.pa, k, sa);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[k][e] = v[k][e] + proj_value(sa[e], pa, za);
             }
         }
     }
-    if (write_x && p.kind != kInPlain && p.kind != kInRelu2Mul && p.x_out != nullptr) {
+    if (write_x && (p.kind == kInEmbed || p.kind == kInResidual) && p.x_out != nullptr) {
 #pragma unroll
-        for (int k = 0; k < kPer4; ++k)
+        for (int k = 0; k < P4; ++k)
             if (elem4(tid, k) < n)
                 *reinterpret_cast<float4*>(p.x_out + elem4(tid, k)) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
     }
+    if (p.gamma == nullptr) {
+#pragma unroll
+        for (int k = 0; k < P4; ++k)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[k][e] = v[k][e];
+        return;
+    }
     double ss = 0.0;
 #pragma unroll
-    for (int k = 0; k < kPer4; ++k) {
+    for (int k = 0; k < P4; ++k) {
         const uint32_t i = elem4(tid, k);
         if (i < n) {
             *reinterpret_cast<float4*>(s.ys + i) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
@@ -374,33 +386,70 @@ __device__ __forceinline__ float stage_norm(const StageInput& p, const InputRegs
         mean = s.mean;
     }
     const float scale = 1.0f / __builtin_sqrtf(mean + p.eps);
+#pragma unroll
+    for (int k = 0; k < P4; ++k) {
+        const float gm[4] = {r.g[k].x, r.g[k].y, r.g[k].z, r.g[k].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float tt = v[k][e] * scale;
+            y[k][e] = tt * gm[e];
+        }
+    }
+}
+
+// The elements [lo, hi) of a staged slice: byte-columns [c0, c1) of a row of n columns (pack.rs:230-237: column c of a
+// full 160-trit block holds elements (c / 32) 160 + c % 32 + 32 k, the packed tail 5 per column), widened to whole
+// float4 groups.
+__device__ __forceinline__ void slice_window(uint32_t n, uint32_t c0, uint32_t c1, uint32_t* lo, uint32_t* hi) {
+    const uint32_t full = n / 160u * 32u, tail0 = n / 160u * 160u;
+    if (c1 <= c0) {
+        *lo = *hi = 0;
+        return;
+    }
+    const uint32_t a = c0 < full ? c0 / 32u * 160u + c0 % 32u : tail0 + 5u * (c0 - full);
+    const uint32_t l = c1 - 1u;
+    uint32_t b = l < full ? l / 32u * 160u + l % 32u + 129u : tail0 + 5u * (l - full) + 5u;
+    b = b < n ? b : n;
+    *lo = a & ~3u;
+    *hi = (b + 3u) & ~3u;
+}
+
+// Writes the thread's y of elements [lo, hi) to s.ys[i - lo] and returns its largest |y| over all elements (NaN never
+// counts). The window must be at most kNormMax long; it is readable after the next barrier.
+template <int P4>
+__device__ __forceinline__ float stage_window(const float (&y)[P4][4], uint32_t n, uint32_t lo, uint32_t hi, InputLds& s) {
+    const uint32_t tid = threadIdx.x;
     float mx = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kPer4; ++k) {
+    for (int k = 0; k < P4; ++k) {
         const uint32_t i = elem4(tid, k);
         if (i < n) {
-            const float gm[4] = {r.g[k].x, r.g[k].y, r.g[k].z, r.g[k].w};
-            float y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float tt = v[k][e] * scale;
-                y[e] = tt * gm[e];
-                const float ay = __builtin_fabsf(y[e]);
+                const float ay = __builtin_fabsf(y[k][e]);
                 if (ay > mx) mx = ay;
             }
-            *reinterpret_cast<float4*>(s.ys + i) = make_float4(y[0], y[1], y[2], y[3]);
+            if (i >= lo && i < hi)
+                *reinterpret_cast<float4*>(s.ys + (i - lo)) = make_float4(y[k][0], y[k][1], y[k][2], y[k][3]);
         }
     }
     return mx;
 }
 
-// Per-token absmax int8 quantization of s.ys (quantize_activations_int8_with_range, ops.rs:241-267, levels 127) and the
-// GEMV staging of the codes into st: entry c (device byte-column c) holds the low nibbles ((x & 15) ^ 8) and the high
-// nibbles (x >> 4) of its five activations (column_activation_index, pack.rs:230-237; zero past the row), entries from
-// dbr to (dbr / 16 + 4) * 16 are zero. Each entry quantizes its own five values. Two barriers; afterwards st is
-// complete, *scale is the activation scale and *act_sum the sum of the codes, in every thread.
-__device__ __forceinline__ void stage_quant(InputLds& s, float mx, uint32_t n, uint32_t tbr, uint32_t dbr, uint2* st, float* scale,
-                            int* act_sum) {
+__device__ __forceinline__ int quant_code(float y, float sc) {
+    float rr = __builtin_roundf(y * sc);
+    rr = rr < -128.0f ? -128.0f : (rr > 127.0f ? 127.0f : rr);
+    return static_cast<int>(rr);
+}
+
+// Per-token absmax int8 quantization (quantize_activations_int8_with_range, ops.rs:241-267, levels 127) and the GEMV
+// staging of the codes of byte-columns [c0, c1) into st[c - c0]: entry c holds the low nibbles ((x & 15) ^ 8) and the
+// high nibbles (x >> 4) of its five activations (column_activation_index, pack.rs:230-237; zero past the row), read
+// from the window s.ys[i - lo]. The sum of all n codes comes from the thread's own y. Two barriers; afterwards the
+// entries are complete, *scale is the activation scale and *act_sum the sum of the codes, in every thread.
+template <int P4>
+__device__ __forceinline__ void stage_quant(const float (&y)[P4][4], InputLds& s, float mx, uint32_t n, uint32_t tbr,
+                                            uint32_t c0, uint32_t c1, uint32_t lo, uint2* st, float* scale, int* act_sum) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     mx = wave_max_f32(mx);
     if (lane == 0) s.red_f[wave] = mx;
@@ -408,29 +457,29 @@ __device__ __forceinline__ void stage_quant(InputLds& s, float mx, uint32_t n, u
     float m = 0.0f;
     for (int w = 0; w < kNT / 64; ++w) m = fmax_nn(m, s.red_f[w]);
     const float sc = m > 0.0f ? 127.0f / m : 0.0f;
-    const uint32_t full = n / 160u * 32u;
-    const uint32_t st_len = (dbr / 16u + 4u) * 16u;
     int sum = 0;
-    for (uint32_t c = tid; c < st_len; c += kNT) {
-        uint32_t lo = 0, hi = 0;
-        if (c < dbr) {
-            const uint32_t base = c < full ? (c / 32u) * 160u + (c % 32u) : (n / 160u) * 160u + 5u * (c - full);
-            const uint32_t step = c < full ? 32u : 1u;
+    if (m > 0.0f) {
 #pragma unroll
-            for (uint32_t k = 0; k < 5; ++k) {
-                const uint32_t idx = base + k * step;
-                int x = 0;
-                if (c < tbr && idx < n && m > 0.0f) {
-                    float rr = __builtin_roundf(s.ys[idx] * sc);
-                    rr = rr < -128.0f ? -128.0f : (rr > 127.0f ? 127.0f : rr);
-                    x = static_cast<int>(rr);
-                }
-                lo |= ((static_cast<uint32_t>(x) & 15u) ^ 8u) << (4 * k);
-                hi |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * k);
-                sum += x;
+        for (int k = 0; k < P4; ++k)
+            if (elem4(tid, k) < n) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sum += quant_code(y[k][e], sc);
             }
+    }
+    const uint32_t full = n / 160u * 32u;
+    for (uint32_t c = c0 + tid; c < c1; c += kNT) {
+        uint32_t lo_n = 0, hi_n = 0;
+        const uint32_t base = c < full ? (c / 32u) * 160u + (c % 32u) : (n / 160u) * 160u + 5u * (c - full);
+        const uint32_t step = c < full ? 32u : 1u;
+#pragma unroll
+        for (uint32_t k = 0; k < 5; ++k) {
+            const uint32_t idx = base + k * step;
+            int x = 0;
+            if (c < tbr && idx < n && m > 0.0f) x = quant_code(s.ys[idx - lo], sc);
+            lo_n |= ((static_cast<uint32_t>(x) & 15u) ^ 8u) << (4 * k);
+            hi_n |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * k);
         }
-        st[c] = make_uint2(lo, hi);
+        st[c - c0] = make_uint2(lo_n, hi_n);
     }
     sum = wave_sum_i32(sum);
     if (lane == 0) s.red_i[wave] = sum;
@@ -443,44 +492,83 @@ __device__ __forceinline__ void stage_quant(InputLds& s, float mx, uint32_t n, u
 
 // ---- decode-step GEMV ------------------------------------------------------------------------------------------------------
 
+// ggml_v_expf (quintrit-runtime/src/ops.rs:314-377) for one lane: n = round(x log2 e) by the 1.5 2^23 shift,
+// b = x - n ln 2 in two parts, j = the degree-5 polynomial of b without its constant term, k = 2^n in the exponent
+// field; |n| <= 126 gives k + k j, beyond that 2^n is split as s1 s2 to reach the subnormal and overflow ranges and
+// |n| > 192 gives s1 s1. Every multiply-add of the reference is a fused one here too (no contraction elsewhere).
+__device__ __forceinline__ float ggml_expf(float x) {
+    const float r = bits_f32(0x4b400000u);
+    const float z = __builtin_fmaf(x, bits_f32(0x3fb8aa3bu), r);
+    const float n = z - r;
+    const float b = __builtin_fmaf(-n, bits_f32(0x35bfbe8eu), __builtin_fmaf(-n, bits_f32(0x3f317200u), x));
+    const uint32_t e = f32_bits(z) << 23;
+    const float k = bits_f32(e + 0x3f800000u);
+    const float u = b * b;
+    const float j = __builtin_fmaf(__builtin_fmaf(__builtin_fmaf(bits_f32(0x3c072010u), b, bits_f32(0x3d2b9f17u)), u,
+                                                  __builtin_fmaf(bits_f32(0x3e2aaf33u), b, bits_f32(0x3efffedbu))),
+                                   u, bits_f32(0x3f7ffff6u) * b);
+    const float an = __builtin_fabsf(n);
+    if (!(an > 126.0f)) return __builtin_fmaf(k, j, k);
+    const uint32_t g = n <= 0.0f ? 0x82000000u : 0u;
+    const float s1 = bits_f32(g + 0x7f000000u);
+    const float s2 = bits_f32(e - g);
+    if (an > 192.0f) return s1 * s1;
+    return __builtin_fmaf(s2, j, s2) * s1;
+}
+
+enum GateAct : uint32_t {
+    kActRelu2 = 0,  // relu2(g) * u (ops.rs:301-308, 467-473)
+    kActSilu = 1,   // swiglu (ops.rs:430-464): whole blocks of 8 use ggml_v_silu, the last n % 8 values libm's expf
+};
+
 // One projection of a stage. A work item is (64-row tile, K slice): the 16 waves of a workgroup split the slice's
 // chunks and add their int32 sums in LDS, and the tile's slice sums (with the row corrections on slice 0) are stored
 // as part[ks][row]; the consumers add the slices and apply the epilogue (ProjOut).
+// A gated pair (w2 set: gate = w, up = w2, one K slice) instead treats the two matrices' chunks of a tile as one list,
+// applies the layer epilogue to both rows and stores act(gate, up) as f32 in act_out[row].
 struct DJob {
     const uint8_t* w;      // device layout (vx_layout)
     const int32_t* dsum;   // per padded row: digit sum of the device row
     int32_t* part;         // [kslices][padded_rows]
+    const uint8_t* w2;     // gated pair: the up projection (same geometry), else null
+    const int32_t* dsum2;
+    float* act_out;        // gated pair: [padded_rows]
+    float ws, ws2;         // gated pair: weight scales
+    uint32_t act, n8;      // gated pair: GateAct; rows below n8 take the vector exponential
     uint32_t rows, padded_rows, n_tiles, n_chunks, kslices, slice_chunks, item_begin;
 };
 
 constexpr int kMaxStageJobs = 3;
-constexpr int kDPer = 7;  // chunks of a slice per wave at most: ceil(device_row_bytes(8192) / 16 / 16)
+constexpr int kDPer = 7;  // chunks of a work item per wave at most (kStChunks / 16)
 
 struct DStageArgs {
     DJob job[kMaxStageJobs];
     uint32_t n_jobs, total_items;
     StageInput in;
-    uint32_t tbr, dbr;  // tile and device row bytes of in.n columns
+    uint32_t tbr;       // tile row bytes of in.n columns
     float* as_out;      // the stage's activation scale (workgroup 0)
+    uint32_t variant;   // the kernel instance (host side: the input's length and kinds)
 };
 
 __constant__ DigitTable g_digits = make_digit_table();
 
 // One workgroup per work item. Order of the loads: the stage input, the digit table, then wave w's chunks
 // q0 + w, q0 + w + 16, ... of the tile (1 KiB each in the device layout), so the input is computed while the weights
-// are in flight; the digit-nibble table and the arithmetic are those of the lone GEMV (vx_gemv.hip).
+// are in flight; the digit-nibble table and the arithmetic are those of the lone GEMV (vx_gemv.hip). Only the entries
+// of the item's own chunks are staged.
+template <int P4, int SA, int SB>
 __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of the digit nibbles of byte B (first half)
     __shared__ uint2 st[kStChunks * 16];
     __shared__ InputLds s;
-    __shared__ int red[kNT / 64][64];
+    __shared__ int red[2][kNT / 64][64];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const char* tabb = reinterpret_cast<const char*>(tab);
     const uint32_t lane_off = (lane & 31u) * 4u;
 
-    InputRegs r;
+    InputRegs<P4, SA, SB> r;
     stage_load(a.in, r);
     uint32_t dig[2];
 #pragma unroll
@@ -491,24 +579,36 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     if (a.n_jobs > 1 && item >= a.job[1].item_begin) j = 1;
     if (a.n_jobs > 2 && item >= a.job[2].item_begin) j = 2;
     const DJob jb = j == 0 ? a.job[0] : (j == 1 ? a.job[1] : a.job[2]);
+    const bool pair = jb.w2 != nullptr;
     const uint32_t local = item - jb.item_begin;
     const uint32_t tile = local / jb.kslices, ks = local - tile * jb.kslices;
     const uint32_t grp = tile / kTileGroup, tt = tile - grp * kTileGroup;
     const uint32_t T = min(static_cast<uint32_t>(kTileGroup), jb.n_tiles - grp * kTileGroup);
     const uint32_t q0 = ks * jb.slice_chunks, nq = min(jb.slice_chunks, jb.n_chunks - q0);
-    const uint32_t cnt = wave < nq ? (nq - wave + kTileGroup - 1) / kTileGroup : 0u;  // this wave's chunks
-    const g_u4* wp = (const g_u4*)(jb.w) + (static_cast<size_t>(grp) * kTileGroup * jb.n_chunks + tt) * 64u + lane;
+    const uint32_t nl = pair ? 2u * nq : nq;  // the item's chunk list: gate chunks, then (pair) up chunks
+    const uint32_t cnt = wave < nl ? (nl - wave + kTileGroup - 1) / kTileGroup : 0u;  // this wave's chunks
+    const size_t tile_off = (static_cast<size_t>(grp) * kTileGroup * jb.n_chunks + tt) * 64u + lane;
+    const g_u4* wp = (const g_u4*)(jb.w) + tile_off;
+    const g_u4* wp2 = pair ? (const g_u4*)(jb.w2) + tile_off : wp;
     const size_t cs = static_cast<size_t>(T) * 64u;  // uint4 between chunks q and q + 1 of the tile
     u32x4 b[kDPer];
 #pragma unroll
     for (int i = 0; i < kDPer; ++i) {
-        if (static_cast<uint32_t>(i) < cnt)
-            b[i] = __builtin_nontemporal_load(wp + (q0 + wave + kTileGroup * static_cast<size_t>(i)) * cs);
+        if (static_cast<uint32_t>(i) < cnt) {
+            const uint32_t c = wave + kTileGroup * i;
+            const bool up = c >= nq;
+            b[i] = __builtin_nontemporal_load((up ? wp2 : wp) + (q0 + (up ? c - nq : c)) * cs);
+        }
     }
 
-    const float mx = stage_norm(a.in, r, s, blockIdx.x == 0);
-    // The table is filled after the input is normed (its loads were issued after the input's, so waiting for them
-    // earlier would also wait for the input) and before the quantization's first barrier.
+    float y[P4][4];
+    stage_y(a.in, r, s, blockIdx.x == 0, y);
+    const uint32_t c0 = q0 * 16u, c1 = min((q0 + nq) * 16u, a.tbr);
+    uint32_t lo, hi;
+    slice_window(a.in.n, c0, c1, &lo, &hi);
+    const float mx = stage_window(y, a.in.n, lo, hi, s);
+    // The table is filled after the input's values are computed (its loads were issued after the input's, so waiting
+    // for them earlier would also wait for the input) and before the quantization's first barrier.
 #pragma unroll
     for (int k = 0; k < 2; ++k) {  // 8 uint4 stores per entry
         const uint32_t i = tid + k * kNT;
@@ -517,14 +617,16 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     }
     float act_scale;
     int act_sum;
-    stage_quant(s, mx, a.in.n, a.tbr, a.dbr, st, &act_scale, &act_sum);
+    stage_quant(y, s, mx, a.in.n, a.tbr, c0, (q0 + nq) * 16u, lo, st, &act_scale, &act_sum);
     if (blockIdx.x == 0 && tid == 0) *a.as_out = act_scale;
 
-    int acc_lo = 0, acc_hi = 0;
+    int acc_lo = 0, acc_hi = 0, acc2_lo = 0, acc2_hi = 0;
 #pragma unroll
     for (int i = 0; i < kDPer; ++i) {
         if (static_cast<uint32_t>(i) >= cnt) break;
-        const uint32_t q = q0 + wave + kTileGroup * i;
+        const uint32_t c = wave + kTileGroup * i;
+        const bool up = pair && c >= nq;
+        const uint32_t q = up ? c - nq : c;  // chunk of the slice
         const uint32_t dw[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
         const uint2 e = st[q * 16u + (lane & 15u)];
         __builtin_amdgcn_sched_barrier(0);
@@ -534,21 +636,60 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
             const uint32_t addr = __builtin_amdgcn_perm(dw[k >> 2], lane_off, 0x0c0c0000u | ((4u + (k & 3)) << 8));
             t[k] = *reinterpret_cast<const uint32_t*>(tabb + addr);
         }
-        dot4_bcast<0>(acc_lo, acc_hi, e.x, e.y, t[0], t[1], t[2], t[3]);
-        dot4_bcast<4>(acc_lo, acc_hi, e.x, e.y, t[4], t[5], t[6], t[7]);
-        dot4_bcast<8>(acc_lo, acc_hi, e.x, e.y, t[8], t[9], t[10], t[11]);
-        dot4_bcast<12>(acc_lo, acc_hi, e.x, e.y, t[12], t[13], t[14], t[15]);
+        if (!pair) {
+            dot4_bcast<0>(acc_lo, acc_hi, e.x, e.y, t[0], t[1], t[2], t[3]);
+            dot4_bcast<4>(acc_lo, acc_hi, e.x, e.y, t[4], t[5], t[6], t[7]);
+            dot4_bcast<8>(acc_lo, acc_hi, e.x, e.y, t[8], t[9], t[10], t[11]);
+            dot4_bcast<12>(acc_lo, acc_hi, e.x, e.y, t[12], t[13], t[14], t[15]);
+        } else {
+            int l = 0, h = 0;
+            dot4_bcast<0>(l, h, e.x, e.y, t[0], t[1], t[2], t[3]);
+            dot4_bcast<4>(l, h, e.x, e.y, t[4], t[5], t[6], t[7]);
+            dot4_bcast<8>(l, h, e.x, e.y, t[8], t[9], t[10], t[11]);
+            dot4_bcast<12>(l, h, e.x, e.y, t[12], t[13], t[14], t[15]);
+            if (up) {
+                acc2_lo += l;
+                acc2_hi += h;
+            } else {
+                acc_lo += l;
+                acc_hi += h;
+            }
+        }
     }
-    red[wave][lane] = acc_lo + 16 * acc_hi;
+    red[0][wave][lane] = acc_lo + 16 * acc_hi;
+    if (pair) red[1][wave][lane] = acc2_lo + 16 * acc2_hi;
     __syncthreads();
     if (wave != 0) return;
     // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in slice 0
     int v = 0;
 #pragma unroll
-    for (int w = 0; w < kNT / 64; ++w) v += red[w][lane];
+    for (int w = 0; w < kNT / 64; ++w) v += red[0][w][lane];
     const uint32_t row = tile * kTileRows + lane;
     if (ks == 0) v += 8 * jb.dsum[row] - act_sum;
-    jb.part[static_cast<size_t>(ks) * jb.padded_rows + row] = v;
+    if (!pair) {
+        jb.part[static_cast<size_t>(ks) * jb.padded_rows + row] = v;
+        return;
+    }
+    int v2 = 0;
+#pragma unroll
+    for (int w = 0; w < kNT / 64; ++w) v2 += red[1][w][lane];
+    v2 += 8 * jb.dsum2[row] - act_sum;
+    // the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170
+    const bool zero = !(act_scale > 0.0f);
+    const float g = zero ? 0.0f : static_cast<float>(v) * (jb.ws / act_scale);
+    const float u = zero ? 0.0f : static_cast<float>(v2) * (jb.ws2 / act_scale);
+    float o;
+    if (jb.act == kActSilu) {
+        const float ex = row < jb.n8 ? ggml_expf(0.0f - g) : glibc_expf(-g);
+        const float den = 1.0f + ex;
+        const float sl = g / den;
+        o = sl * u;
+    } else {
+        const float pos = g > 0.0f ? g : 0.0f;
+        const float sq = pos * pos;
+        o = sq * u;
+    }
+    if (row < jb.rows) jb.act_out[row] = o;
 }
 
 // ---- attention ------------------------------------------------------------------------------------------------------------
@@ -557,45 +698,48 @@ struct AttnArgs {
     const Ctl* ctl;
     ProjOut q, k, v;       // the q, k, v projections of this layer
     const float* rope;     // [max_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i + 1
-    uint16_t* kc;          // this layer: [kv_head][max_ctx][kAttnHd] f16
+    uint16_t* kc;          // this layer: [kv_head][max_ctx][head_dim] f16
     uint16_t* vc;
-    float* out;            // n_heads x kAttnHd
+    float* out;            // n_heads x head_dim
     uint32_t n_heads, gqa, max_ctx;
+    uint32_t rope_normal;  // 1: pairs (2i, 2i + 1) (RopeMode::Normal), 0: (i, i + head_dim / 2) (NEOX)
     float scale;
 };
 
-constexpr uint32_t kAttnHd = 128;       // head_dim of the attention kernel
 constexpr uint32_t kAttnMaxCtx = 4096;  // KV positions held in LDS (scores, running maxima)
 constexpr uint32_t kAttnWaves = 8;      // 4 chunks x 2 halves of the head
-constexpr uint32_t kAttnWin = 64;       // positions of V staged per wave at a time
 constexpr uint32_t kAttnBatch = 8;      // positions whose LDS operands are read ahead of the accumulator chain
 
-// The 16 uint4 of a 128-value f16 row.
-__device__ __forceinline__ void load_row128(const uint16_t* k, uint4 (&kr)[16]) {
-#pragma unroll
-    for (int c = 0; c < 16; ++c) kr[c] = *reinterpret_cast<const uint4*>(k + 8 * c);
-}
-
-// ggml_vec_dot_f16 of 128 values (ops.rs:960-1015): four accumulators of eight lanes take fma per 32 values,
-// red = (s0 + s2) + (s1 + s3), t[k] = red[k] + red[k + 4], (t0 + t1) + (t2 + t3). q is in LDS, k in registers.
-__device__ __forceinline__ float dot_f16_128(const uint16_t* q, const uint4 (&kr)[16]) {
+// ggml_vec_dot_f16 of HD values (ops.rs:960-1015): four accumulators of eight lanes take fma per 32 values,
+// red = (s0 + s2) + (s1 + s3), t[k] = red[k] + red[k + 4], (t0 + t1) + (t2 + t3). q is in LDS, k is loaded 256
+// (head_dim 128) or 128 bytes at a time.
+template <int HD>
+__device__ __forceinline__ float dot_f16(const uint16_t* q, const uint16_t* k) {
     float acc[4][8];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int l = 0; l < 8; ++l) acc[j][l] = 0.0f;
+    constexpr int kPart = HD == 128 ? 128 : 64;  // values whose k is loaded at once
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int part = 0; part < HD / kPart; ++part) {
+        uint4 kr[kPart / 8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint4 kv = kr[4 * i + j];
-            const uint4 qv = *reinterpret_cast<const uint4*>(q + 32 * i + 8 * j);
-            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
+        for (int c = 0; c < kPart / 8; ++c) kr[c] = *reinterpret_cast<const uint4*>(k + part * kPart + 8 * c);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int l = 0; l < 8; ++l) {
-                const uint16_t kb = static_cast<uint16_t>(kw[l >> 1] >> ((l & 1) * 16));
-                const uint16_t qb = static_cast<uint16_t>(qw[l >> 1] >> ((l & 1) * 16));
-                acc[j][l] = __builtin_fmaf(f16_f32(qb), f16_f32(kb), acc[j][l]);
+        for (int i = 0; i < kPart / 32; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint4 kv = kr[4 * i + j];
+                const uint4 qv = *reinterpret_cast<const uint4*>(q + part * kPart + 32 * i + 8 * j);
+                const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+                for (int l = 0; l < 8; ++l) {
+                    const uint16_t kb = static_cast<uint16_t>(kw[l >> 1] >> ((l & 1) * 16));
+                    const uint16_t qb = static_cast<uint16_t>(qw[l >> 1] >> ((l & 1) * 16));
+                    acc[j][l] = __builtin_fmaf(f16_f32(qb), f16_f32(kb), acc[j][l]);
+                }
             }
         }
     }
@@ -609,10 +753,11 @@ __device__ __forceinline__ float dot_f16_128(const uint16_t* q, const uint4 (&kr
 // f16 value of an f32 (round to nearest even, after the f32 rounding of x), kept in an f32
 __device__ __forceinline__ float r16(float x) { return static_cast<float>(static_cast<_Float16>(keep_f32(x))); }
 
-// One workgroup per query head. First the inputs of the position: q of this head and k, v of its KV head, NEOX RoPE over all head_dim coordinates (ops.rs:199-221:
-// x0' = fma(x0, c, -(x1 s)), x1' = fma(x0, s, x1 c)) and the f16 rounding of the cache (kv_cache.rs:24-182); the first
-// query head of each KV head appends k and v to the cache, and every workgroup uses its own copy of them for the
-// position itself (the other positions come from earlier steps).
+// One workgroup per query head. First the inputs of the position: q of this head and k, v of its KV head, RoPE over
+// all head_dim coordinates (ops.rs:199-221, NEOX or Normal pairing: x0' = fma(x0, c, -(x1 s)), x1' = fma(x0, s, x1 c))
+// and the f16 rounding of the cache (kv_cache.rs:24-182); the first query head of each KV head appends k and v to the
+// cache, and every workgroup uses its own copy of them for the position itself (the other positions come from
+// earlier steps).
 // Then the reference's attend_head (attention.rs:483-542) over the positions 0..pos. Below a padded KV length of 512 one
 // online softmax covers all positions; from 512 on, 4 chunks of ceil(n_kv / 4) positions run one each and are combined
 // in order. The online softmax of a chunk (attend_range, attention.rs:436-468) is rebuilt without its serial
@@ -622,24 +767,30 @@ __device__ __forceinline__ float r16(float x) { return static_cast<float>(static
 //   factors       every position in parallel: a new maximum gives ms = expf(m_old - score), vs = 1; otherwise ms = 1,
 //                 vs = expf(score - max); stored as -ms or vs (the sign marks the case)
 //   accumulator   per coordinate, in position order: y = f16(y * ms), y = f16(fma(v, vs, y)), s = fma(s, ms, vs)
-// Wave w accumulates chunk w / 2, coordinates 64 (w % 2) .. + 63, one per lane, with V streamed through LDS in
-// windows of 64 positions, the next window loaded while the current one is consumed.
+// Wave w accumulates chunk w / 2, coordinates (HD / 2) (w % 2) .. + HD / 2 - 1, HD / 128 per lane (independent
+// chains), with V streamed through LDS in windows of kWin positions, the next window loaded while the current one is
+// consumed.
+template <int HD>
 __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) {
+    constexpr uint32_t kHalf = HD / 2;         // coordinates of a wave
+    constexpr int kPerLane = HD / 128;         // coordinates of a lane
+    constexpr uint32_t kLP = kHalf / 8;        // lanes loading one position's half row (16 bytes each)
+    constexpr uint32_t kWin = 8u * (64u / kLP);  // positions of V staged per wave at a time (8 loads per lane)
     __shared__ float sc[kAttnMaxCtx];
     __shared__ float pm[kAttnMaxCtx];
-    __shared__ __align__(16) uint16_t vbuf[kAttnWaves][kAttnWin * 64];
-    __shared__ __align__(16) uint16_t qs[kAttnHd];
-    __shared__ __align__(16) uint16_t kp[kAttnHd];  // k and v of the position itself
-    __shared__ __align__(16) uint16_t vp[kAttnHd];
+    __shared__ __align__(16) uint16_t vbuf[kAttnWaves][kWin * kHalf];
+    __shared__ __align__(16) uint16_t qs[HD];
+    __shared__ __align__(16) uint16_t kp[HD];  // k and v of the position itself
+    __shared__ __align__(16) uint16_t vp[HD];
     __shared__ float cm[4], cs[4];
-    __shared__ uint16_t cv[4][kAttnHd];
+    __shared__ uint16_t cv[4][HD];
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t kvh = h / a.gqa;
     const uint32_t pos = a.ctl->pos;
     const uint32_t seq = pos + 1;
-    const uint16_t* kb = a.kc + static_cast<size_t>(kvh) * a.max_ctx * kAttnHd;
-    const uint16_t* vb = a.vc + static_cast<size_t>(kvh) * a.max_ctx * kAttnHd;
+    const uint16_t* kb = a.kc + static_cast<size_t>(kvh) * a.max_ctx * HD;
+    const uint16_t* vb = a.vc + static_cast<size_t>(kvh) * a.max_ctx * HD;
 
     uint32_t n_kv = (seq + 255u) / 256u * 256u;
     if (n_kv > a.max_ctx) n_kv = a.max_ctx;
@@ -647,7 +798,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     const uint32_t chunk = split ? (n_kv + 3u) / 4u : seq;
     const uint32_t n_chunks = split ? 4u : 1u;
     // This wave's chunk and half of the head.
-    const uint32_t c = wave >> 1, half = wave & 1u, d = half * 64u + lane;
+    const uint32_t c = wave >> 1, half = wave & 1u;
     uint32_t st = 0, en = 0;
     if (c < n_chunks) {
         st = c * chunk;
@@ -655,54 +806,53 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     }
 
     {
-        constexpr uint32_t hh = kAttnHd / 2u;
-        const float* cache = a.rope + static_cast<size_t>(pos) * kAttnHd;
-        if (tid < 2u * hh) {  // q (tid < 64) or k: the rotation of pair i
-            const bool isq = tid < hh;
-            const uint32_t i = tid & (hh - 1u);
+        const float* cache = a.rope + static_cast<size_t>(pos) * HD;
+        if (tid < HD) {  // q (tid < HD / 2) or k: the rotation of pair i
+            const bool isq = tid < kHalf;
+            const uint32_t i = tid & (kHalf - 1u);
+            const uint32_t i0 = a.rope_normal ? 2u * i : i, i1 = a.rope_normal ? 2u * i + 1u : i + kHalf;
             const ProjOut& o = isq ? a.q : a.k;
-            const uint32_t base = (isq ? h : kvh) * kAttnHd;
+            const uint32_t base = (isq ? h : kvh) * HD;
             bool zero;
             const float post = proj_post(o, &zero);
-            const float x0 = proj_at(o, base + i, post, zero), x1 = proj_at(o, base + i + hh, post, zero);
+            const float x0 = proj_at(o, base + i0, post, zero), x1 = proj_at(o, base + i1, post, zero);
             const float cc = cache[2 * i], ss = cache[2 * i + 1];
             const float x1s = x1 * ss, x1c = x1 * cc;
             const float y0 = __builtin_fmaf(x0, cc, -x1s);
             const float y1 = __builtin_fmaf(x0, ss, x1c);
             uint16_t* dst = isq ? qs : kp;
-            dst[i] = f32_f16(y0);
-            dst[i + hh] = f32_f16(y1);
-        } else if (tid < 4u * hh) {
-            const uint32_t dd = tid - 2u * hh;
+            dst[i0] = f32_f16(y0);
+            dst[i1] = f32_f16(y1);
+        } else if (tid < 2u * HD) {
+            const uint32_t dd = tid - HD;
             bool zero;
             const float post = proj_post(a.v, &zero);
-            vp[dd] = f32_f16(proj_at(a.v, kvh * kAttnHd + dd, post, zero));
+            vp[dd] = f32_f16(proj_at(a.v, kvh * HD + dd, post, zero));
         }
     }
     __syncthreads();
-    if (h % a.gqa == 0 && tid < kAttnHd) {
-        a.kc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * kAttnHd + tid] = kp[tid];
-        a.vc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * kAttnHd + tid] = vp[tid];
+    if (h % a.gqa == 0 && tid < HD) {
+        a.kc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + tid] = kp[tid];
+        a.vc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + tid] = vp[tid];
     }
     // This wave's first window of V, requested before the scores so that its latency overlaps them, the scan and
-    // the exponentials; the position itself comes from LDS.
-    const uint32_t off = half * 64u + (lane & 7u) * 8u;
+    // the exponentials; the position itself comes from LDS. Load j of a lane holds 8 coordinates of position
+    // 8 j + lane / kLP of the window.
+    const uint32_t off = half * kHalf + (lane % kLP) * 8u;
     const uint16_t* vsrc = vb + off;
     auto load_v = [&](uint32_t p) -> u32x4 {
         return p == pos ? *reinterpret_cast<const u32x4*>(vp + off)
-                        : *reinterpret_cast<const u32x4*>(vsrc + static_cast<size_t>(p) * kAttnHd);
+                        : *reinterpret_cast<const u32x4*>(vsrc + static_cast<size_t>(p) * HD);
     };
+    constexpr uint32_t kPosPerLoad = 64u / kLP;
     u32x4 r[8];
     if (st < en) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = load_v(min(st + 8u * j + (lane >> 3), en - 1u));
+        for (int j = 0; j < 8; ++j) r[j] = load_v(min(st + kPosPerLoad * j + lane / kLP, en - 1u));
     }
 
-    for (uint32_t p = tid; p < seq; p += kAttnWaves * 64u) {
-        uint4 kr[16];
-        load_row128(p == pos ? kp : kb + static_cast<size_t>(p) * kAttnHd, kr);
-        sc[p] = dot_f16_128(qs, kr) * a.scale;
-    }
+    for (uint32_t p = tid; p < seq; p += kAttnWaves * 64u)
+        sc[p] = dot_f16<HD>(qs, p == pos ? kp : kb + static_cast<size_t>(p) * HD) * a.scale;
     __syncthreads();
 
     if (wave < n_chunks) {  // the running maximum of chunk `wave`
@@ -731,70 +881,91 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     }
     __syncthreads();
 
-    float y = 0.0f, ssum = 0.0f;
+    float y[kPerLane], ssum = 0.0f;
+#pragma unroll
+    for (int m = 0; m < kPerLane; ++m) y[m] = 0.0f;
     if (st < en) {
         uint16_t* buf = vbuf[wave];
-        for (uint32_t base = st; base < en; base += kAttnWin) {
+        for (uint32_t base = st; base < en; base += kWin) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(buf + (8u * j + (lane >> 3)) * 64u + (lane & 7u) * 8u) = r[j];
-            if (base + kAttnWin < en) {
+            for (int j = 0; j < 8; ++j)
+                *reinterpret_cast<u32x4*>(buf + (kPosPerLoad * j + lane / kLP) * kHalf + (lane % kLP) * 8u) = r[j];
+            if (base + kWin < en) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) r[j] = load_v(min(base + kAttnWin + 8u * j + (lane >> 3), en - 1u));
+                for (int j = 0; j < 8; ++j) r[j] = load_v(min(base + kWin + kPosPerLoad * j + lane / kLP, en - 1u));
             }
-            const uint32_t n = min(kAttnWin, en - base);  // wave-uniform
+            const uint32_t n = min(kWin, en - base);  // wave-uniform
             const float f = lane < n ? sc[base + lane] : 0.0f;
             const uint32_t nb = n & ~(kAttnBatch - 1u);
             // Whole batches of kAttnBatch positions, their LDS operands read before the serial chain uses them; a
             // window without a new maximum (ms = 1 throughout) takes the shorter chain.
             if (__ballot(__builtin_signbit(f)) == 0) {
-                auto step = [&](float e, float v) {
-                    y = r16(__builtin_fmaf(v, e, y));
+                auto step = [&](float e, const float (&v)[kPerLane]) {
+#pragma unroll
+                    for (int m = 0; m < kPerLane; ++m) y[m] = r16(__builtin_fmaf(v[m], e, y[m]));
                     ssum = ssum + e;
                 };
                 for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
-                    float fe[kAttnBatch], fv[kAttnBatch];
+                    float fe[kAttnBatch], fv[kAttnBatch][kPerLane];
 #pragma unroll
                     for (uint32_t u = 0; u < kAttnBatch; ++u) {
                         fe[u] = sc[base + i0 + u];
-                        fv[u] = f16_f32(buf[(i0 + u) * 64u + lane]);
+#pragma unroll
+                        for (int m = 0; m < kPerLane; ++m) fv[u][m] = f16_f32(buf[(i0 + u) * kHalf + lane + 64u * m]);
                     }
 #pragma unroll
                     for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
                 }
-                for (uint32_t i = nb; i < n; ++i) step(sc[base + i], f16_f32(buf[i * 64u + lane]));
+                for (uint32_t i = nb; i < n; ++i) {
+                    float fv[kPerLane];
+#pragma unroll
+                    for (int m = 0; m < kPerLane; ++m) fv[m] = f16_f32(buf[i * kHalf + lane + 64u * m]);
+                    step(sc[base + i], fv);
+                }
             } else {
-                auto step = [&](float fi, float v) {
+                auto step = [&](float fi, const float (&v)[kPerLane]) {
                     const bool nm = __builtin_signbit(fi);
                     const float e = __builtin_fabsf(fi);
                     const float ms = nm ? e : 1.0f, vs = nm ? 1.0f : e;
-                    y = r16(y * ms);
-                    y = r16(__builtin_fmaf(v, vs, y));
+#pragma unroll
+                    for (int m = 0; m < kPerLane; ++m) {
+                        y[m] = r16(y[m] * ms);
+                        y[m] = r16(__builtin_fmaf(v[m], vs, y[m]));
+                    }
                     ssum = __builtin_fmaf(ssum, ms, vs);
                 };
                 for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
-                    float fe[kAttnBatch], fv[kAttnBatch];
+                    float fe[kAttnBatch], fv[kAttnBatch][kPerLane];
 #pragma unroll
                     for (uint32_t u = 0; u < kAttnBatch; ++u) {
                         fe[u] = sc[base + i0 + u];
-                        fv[u] = f16_f32(buf[(i0 + u) * 64u + lane]);
+#pragma unroll
+                        for (int m = 0; m < kPerLane; ++m) fv[u][m] = f16_f32(buf[(i0 + u) * kHalf + lane + 64u * m]);
                     }
 #pragma unroll
                     for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
                 }
-                for (uint32_t i = nb; i < n; ++i) step(sc[base + i], f16_f32(buf[i * 64u + lane]));
+                for (uint32_t i = nb; i < n; ++i) {
+                    float fv[kPerLane];
+#pragma unroll
+                    for (int m = 0; m < kPerLane; ++m) fv[m] = f16_f32(buf[i * kHalf + lane + 64u * m]);
+                    step(sc[base + i], fv);
+                }
             }
         }
     }
-    float* out = a.out + static_cast<size_t>(h) * kAttnHd;
+    float* out = a.out + static_cast<size_t>(h) * HD;
     if (!split) {
         if (c == 0) {
             const float s_inv = ssum == 0.0f ? 0.0f : 1.0f / ssum;
-            out[d] = y * s_inv;
+#pragma unroll
+            for (int m = 0; m < kPerLane; ++m) out[half * kHalf + lane + 64u * m] = y[m] * s_inv;
         }
         return;
     }
     if (c < 4) {
-        cv[c][d] = f32_f16(y);
+#pragma unroll
+        for (int m = 0; m < kPerLane; ++m) cv[c][half * kHalf + lane + 64u * m] = f32_f16(y[m]);
         if (half == 0 && lane == 0) {
             cm[c] = st < en ? pm[en - 1] : -__builtin_inff();
             cs[c] = ssum;
@@ -802,23 +973,27 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     }
     __syncthreads();
     if (c != 0) return;
-    float mf = -__builtin_inff(), sf = 0.0f, acc = 0.0f;
-    for (uint32_t k = 0; k < 4; ++k) {
-        const uint32_t ks = k * chunk, ke = min(min(ks + chunk, n_kv), seq);
-        if (ks >= ke) continue;
-        const float sk = cs[k];
-        if (sk == 0.0f) continue;
-        const float mk = cm[k];
-        const float mn = __builtin_fmaxf(mf, mk);
-        const float so = glibc_expf(mf - mn);
-        const float sn = glibc_expf(mk - mn);
-        const float vn = f16_f32(cv[k][d]) * sn;
-        acc = __builtin_fmaf(acc, so, vn);
-        const float ssn = sk * sn;
-        sf = __builtin_fmaf(sf, so, ssn);
-        mf = mn;
+#pragma unroll
+    for (int m = 0; m < kPerLane; ++m) {
+        const uint32_t d = half * kHalf + lane + 64u * m;
+        float mf = -__builtin_inff(), sf = 0.0f, acc = 0.0f;
+        for (uint32_t k = 0; k < 4; ++k) {
+            const uint32_t ks = k * chunk, ke = min(min(ks + chunk, n_kv), seq);
+            if (ks >= ke) continue;
+            const float sk = cs[k];
+            if (sk == 0.0f) continue;
+            const float mk = cm[k];
+            const float mn = __builtin_fmaxf(mf, mk);
+            const float so = glibc_expf(mf - mn);
+            const float sn = glibc_expf(mk - mn);
+            const float vn = f16_f32(cv[k][d]) * sn;
+            acc = __builtin_fmaf(acc, so, vn);
+            const float ssn = sk * sn;
+            sf = __builtin_fmaf(sf, so, ssn);
+            mf = mn;
+        }
+        out[d] = sf != 0.0f ? acc * (1.0f / sf) : acc;
     }
-    out[d] = sf != 0.0f ? acc * (1.0f / sf) : acc;
 }
 
 // ---- head and greedy argmax ----------------------------------------------------------------------------------------------
@@ -835,7 +1010,7 @@ __device__ __forceinline__ unsigned long long logit_key(float v, uint32_t r) {
 
 struct HeadArgs {
     StageInput in;         // the final residual add (x + down of the last layer) and the output norm
-    const uint16_t* emb;   // tied bf16 embedding: vocab x hidden
+    const uint16_t* w;     // the head: vocab x hidden, bf16 or f16 (the embedding when tied)
     uint32_t hidden, vocab;
     float* logits;
     Ctl* ctl;
@@ -844,39 +1019,56 @@ struct HeadArgs {
     uint32_t* ticket;         // workgroups done (0 between steps)
 };
 
-// Every workgroup computes the normed bf16 vector itself, then rows r0 + tid / 4: logits[r] = ggml_vec_dot_bf16(x,
-// emb[r]) (ops.rs:669-713): lane (r, j) of four per row holds the eight lanes of accumulator j, acc + x*y rounded
-// separately, then (a0 + a2) + (a1 + a3) across the four lanes and ((l0+l4) + (l2+l6)) + ((l1+l5) + (l3+l7)) inside
-// one. hidden must be a multiple of 32. The workgroup's best key goes into *key with an atomic maximum; the last
-// workgroup to finish reads the winner, resets key and ticket, and advances the loop state: the token is recorded once
-// the prompt is consumed and the position moves on.
+// Every workgroup computes the normed vector itself, rounds it to the head's type (model.rs:347-351), then rows
+// r0 + tid / 4 in blocks of kNT / 4. Lane (r, j) of four per row holds the eight lanes of accumulator j over the
+// 32-value blocks, the cross-lane sums give (a0 + a2) + (a1 + a3), and inside one lane:
+//   bf16 (ggml_vec_dot_bf16, ops.rs:669-713)   acc + x*y rounded separately; ((l0+l4) + (l2+l6)) + ((l1+l5) + (l3+l7))
+//   f16  (ggml_vec_dot_f16, ops.rs:960-1015)   fma(x, y, acc);                ((l0+l4) + (l1+l5)) + ((l2+l6) + (l3+l7))
+// hidden must be a multiple of 32. The workgroup's best key goes into *key with an atomic maximum; the last workgroup
+// to finish reads the winner, resets key and ticket, and advances the loop state: the token is recorded once the
+// prompt is consumed and the position moves on.
+template <bool F16>
 __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
     __shared__ InputLds s;
     __shared__ uint4 xs[kNormMax / 8];
     __shared__ unsigned long long wbest[kNT / 64];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    InputRegs r;
+    InputRegs<2, kMaxSlicesA, 0> r;
     stage_load(a.in, r);
-    (void)stage_norm(a.in, r, s, false);
-    __syncthreads();
+    float y[2][4];
+    stage_y(a.in, r, s, false, y);
     uint16_t* xh = reinterpret_cast<uint16_t*>(xs);
-    for (uint32_t i = tid; i < a.hidden; i += kNT) xh[i] = f32_bf16(s.ys[i]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const uint32_t i = elem4(tid, k);
+        if (i < a.hidden) {
+            uint16_t hv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) hv[e] = F16 ? f32_f16(y[k][e]) : f32_bf16(y[k][e]);
+            *reinterpret_cast<uint2*>(xh + i) = make_uint2(hv[0] | (static_cast<uint32_t>(hv[1]) << 16),
+                                                           hv[2] | (static_cast<uint32_t>(hv[3]) << 16));
+        }
+    }
     __syncthreads();
     const uint32_t j = tid & 3u;
     unsigned long long best = 0;
     for (uint32_t r0 = blockIdx.x * (kNT / 4u); r0 < a.vocab; r0 += gridDim.x * (kNT / 4u)) {
-        const uint32_t r = r0 + (tid >> 2);
-        const u32x4* row = reinterpret_cast<const u32x4*>(a.emb + static_cast<size_t>(min(r, a.vocab - 1u)) * a.hidden);
+        const uint32_t row_i = r0 + (tid >> 2);
+        const u32x4* row = reinterpret_cast<const u32x4*>(a.w + static_cast<size_t>(min(row_i, a.vocab - 1u)) * a.hidden);
         float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
         auto block = [&](const u32x4& w, uint32_t i) {  // the 32-value block i: lane j's accumulator j
             const uint4 x = xs[4u * i + j];
             const uint32_t ww[4] = {w.x, w.y, w.z, w.w}, xx[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
             for (int l = 0; l < 8; ++l) {
-                const float wf = bits_f32((ww[l >> 1] >> ((l & 1) * 16)) << 16);
-                const float xf = bits_f32((xx[l >> 1] >> ((l & 1) * 16)) << 16);
-                const float p = xf * wf;
-                acc[l] = acc[l] + p;
+                const uint16_t wb = static_cast<uint16_t>(ww[l >> 1] >> ((l & 1) * 16));
+                const uint16_t xb = static_cast<uint16_t>(xx[l >> 1] >> ((l & 1) * 16));
+                if (F16) {
+                    acc[l] = __builtin_fmaf(f16_f32(xb), f16_f32(wb), acc[l]);
+                } else {
+                    const float p = bf16_f32(xb) * bf16_f32(wb);
+                    acc[l] = acc[l] + p;
+                }
             }
         };
         const uint32_t nblk = a.hidden / 32u, nblk8 = nblk & ~7u;
@@ -894,11 +1086,11 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
             acc[l] = acc[l] + __shfl_xor(acc[l], 2);
             acc[l] = acc[l] + __shfl_xor(acc[l], 1);
         }
-        if (j == 0 && r < a.vocab) {
-            const float g0 = acc[4] + acc[0], g1 = acc[5] + acc[1], g2 = acc[6] + acc[2], g3 = acc[7] + acc[3];
-            const float v = (g0 + g2) + (g1 + g3);
-            a.logits[r] = v;
-            const unsigned long long k = logit_key(v, r);
+        if (j == 0 && row_i < a.vocab) {
+            const float g0 = acc[0] + acc[4], g1 = acc[1] + acc[5], g2 = acc[2] + acc[6], g3 = acc[3] + acc[7];
+            const float v = F16 ? (g0 + g1) + (g2 + g3) : (g0 + g2) + (g1 + g3);
+            a.logits[row_i] = v;
+            const unsigned long long k = logit_key(v, row_i);
             if (k > best) best = k;
         }
     }
@@ -928,20 +1120,34 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
 
 // ---- launches ----------------------------------------------------------------------------------------------------------------
 
+// dgemv_kernel instances (DStageArgs::variant): inputs of up to 4096 and 8192 elements of every kind, and plain or
+// embedding inputs of up to kPlainMax elements without a norm (the SwiGLU output of a model without sub-norms).
+enum DVariant : uint32_t { kDv4K = 0, kDv8K = 1, kDvPlain = 2 };
+
 int launch_dgemv(const DStageArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(dgemv_kernel, dim3(a.total_items), dim3(kNT), 0, s, a);
+    switch (a.variant) {
+        case kDv4K: hipLaunchKernelGGL((dgemv_kernel<1, kMaxSlicesA, kMaxSlicesB>), dim3(a.total_items), dim3(kNT), 0, s, a); break;
+        case kDv8K: hipLaunchKernelGGL((dgemv_kernel<2, kMaxSlicesA, kMaxSlicesB>), dim3(a.total_items), dim3(kNT), 0, s, a); break;
+        default: hipLaunchKernelGGL((dgemv_kernel<kPlainMax / (4 * kNT), 0, 0>), dim3(a.total_items), dim3(kNT), 0, s, a); break;
+    }
     VX_HIP(hipGetLastError());
     return VX_OK;
 }
 
-int launch_attention(const AttnArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(attention_kernel, dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
+int launch_attention(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
+    if (head_dim == 256)
+        hipLaunchKernelGGL(attention_kernel<256>, dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL(attention_kernel<128>, dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
     VX_HIP(hipGetLastError());
     return VX_OK;
 }
 
-int launch_head(const HeadArgs& a, uint32_t grid, hipStream_t s) {
-    hipLaunchKernelGGL(head_kernel, dim3(grid), dim3(kNT), 0, s, a);
+int launch_head(const HeadArgs& a, bool f16, uint32_t grid, hipStream_t s) {
+    if (f16)
+        hipLaunchKernelGGL(head_kernel<true>, dim3(grid), dim3(kNT), 0, s, a);
+    else
+        hipLaunchKernelGGL(head_kernel<false>, dim3(grid), dim3(kNT), 0, s, a);
     VX_HIP(hipGetLastError());
     return VX_OK;
 }
@@ -974,8 +1180,12 @@ struct vx_decoder {
     size_t qd, kvd;
     std::vector<vx_matrix_t*> proj;   // [layer * 7 + kind]
     std::vector<float*> norms;        // [layer * 4 + kind]; the output norm at [n_layers * 4]
-    std::vector<uint8_t> norm_set, emb_set;
+    std::vector<uint8_t> norm_set;
+    bool emb_set, head_set;
+    bool pair;                        // gate and up run as one gated pair (the down input is d_inter)
     uint16_t* d_emb;
+    uint16_t* d_head;                 // the untied head, or null
+    float* d_inter;                   // gated pair output: act(gate, up), [ffn rounded up to 64]
     float* d_rope;
     uint16_t *d_kc, *d_vc;            // [layer][kv_head][max_ctx][head_dim]
     float *d_xa, *d_xb;               // the residual stream (written alternately by the stages that add to it)
@@ -1027,8 +1237,8 @@ static void destroy_decoder(vx_decoder* d) {
         if (m) (void)vx_matrix_free(m);
     for (auto* p : d->norms)
         if (p) (void)hipFree(p);
-    void* bufs[] = {d->d_emb, d->d_rope, d->d_kc,  d->d_vc,     d->d_xa,     d->d_xb,     d->d_att,   d->d_logits,
-                    d->d_key, d->d_ctl,  d->d_prompt, d->d_tokens};
+    void* bufs[] = {d->d_emb, d->d_head, d->d_inter, d->d_rope,   d->d_kc,    d->d_vc,    d->d_xa,
+                    d->d_xb,  d->d_att,  d->d_logits, d->d_key, d->d_ctl, d->d_prompt, d->d_tokens};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (int32_t* b : d->d_part)
@@ -1088,24 +1298,43 @@ static hipError_t dalloc(vx_decoder* d, T** p, size_t bytes) {
     return hipMalloc(reinterpret_cast<void**>(p), bytes);
 }
 
-static int create_decoder(const vx_decoder_config_t* c, vx_decoder_t** out) {
+static bool has_sub_norms(const vx_decoder* d) { return d->cfg.no_sub_norm == 0; }
+
+static int create_decoder(const vx_decoder_config_t* cin, vx_decoder_t** out) {
     if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_decoder is NULL");
     *out = nullptr;
-    if (c == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "config is NULL");
-    if (c->struct_size != sizeof(vx_decoder_config_t))
-        VX_FAIL(VX_ERR_INVALID_ARGUMENT, "config.struct_size is %u, expected %zu", c->struct_size, sizeof(vx_decoder_config_t));
+    if (cin == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "config is NULL");
+    // The first version of the struct ended at rope_theta; its switches are 0 (BitNet).
+    constexpr size_t kV1Size = offsetof(vx_decoder_config_t, act);
+    if (cin->struct_size != sizeof(vx_decoder_config_t) && cin->struct_size != kV1Size)
+        VX_FAIL(VX_ERR_INVALID_ARGUMENT, "config.struct_size is %u, expected %zu (or %zu)", cin->struct_size,
+                sizeof(vx_decoder_config_t), kV1Size);
+    vx_decoder_config_t cfg{};
+    std::memcpy(&cfg, cin, cin->struct_size);
+    cfg.struct_size = sizeof(vx_decoder_config_t);
+    const vx_decoder_config_t* c = &cfg;
     if (c->n_layers == 0 || c->n_layers > 1024) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "n_layers must be in 1..=1024");
-    if (c->head_dim != kAttnHd) VX_FAIL(VX_ERR_UNSUPPORTED, "head_dim %u is not supported (128 only)", c->head_dim);
+    if (c->act > VX_ACT_SILU || c->rope_mode > VX_ROPE_NORMAL || c->no_sub_norm > 1 || c->emb_f16 > 1 || c->untied > 1)
+        VX_FAIL(VX_ERR_INVALID_ARGUMENT, "act, rope_mode, no_sub_norm, emb_f16 and untied take 0 or 1");
+    if (c->head_dim != 128 && c->head_dim != 256)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "head_dim %u is not supported (128 or 256)", c->head_dim);
     if (c->n_heads == 0 || c->n_kv_heads == 0 || c->n_heads % c->n_kv_heads)
         VX_FAIL(VX_ERR_INVALID_ARGUMENT, "n_heads (%u) must be a positive multiple of n_kv_heads (%u)", c->n_heads, c->n_kv_heads);
     if (c->max_ctx == 0 || c->max_ctx > kAttnMaxCtx) VX_FAIL(VX_ERR_UNSUPPORTED, "max_ctx must be in 1..=%u", kAttnMaxCtx);
     if (c->hidden == 0 || c->hidden % 32 || c->hidden > kNormMax)
         VX_FAIL(VX_ERR_UNSUPPORTED, "hidden must be a positive multiple of 32 up to %u", kNormMax);
-    if (static_cast<size_t>(c->n_heads) * c->head_dim > kNormMax || c->ffn == 0 || c->ffn > kNormMax || c->ffn % 4)
-        VX_FAIL(VX_ERR_UNSUPPORTED, "n_heads * head_dim and ffn must be multiples of 4 in 1..=%u", kNormMax);
+    if (static_cast<size_t>(c->n_heads) * c->head_dim > kNormMax)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "n_heads * head_dim must be at most %u", kNormMax);
+    // SiLU (and any ffn beyond kNormMax) runs gate and up as one gated pair: both matrices' chunks of a tile in one
+    // workgroup (at most kStChunks), the down input then a plain vector (normed only up to kNormMax).
+    const bool pair = c->act == VX_ACT_SILU || c->ffn > kNormMax;
+    const size_t ffn_max = pair && c->no_sub_norm ? kPlainMax : kNormMax;
+    if (c->ffn == 0 || c->ffn > ffn_max || c->ffn % 4)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "ffn must be a multiple of 4 in 1..=%zu for this architecture", ffn_max);
+    if (pair && 2 * device_row_bytes(c->hidden) / kChunk > kStChunks)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "hidden %u is too wide for the gated gate/up pair (SiLU)", c->hidden);
     if (c->vocab == 0 || c->vocab > (1u << 24)) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "vocab must be in 1..=2^24");
     if (!(c->rms_eps >= 0.0f) || !(c->rope_theta > 0.0f)) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "rms_eps must be >= 0 and rope_theta > 0");
-    static_assert(kNormMax / 160 * 32 + 16 <= (kStChunks - 4) * 16, "the staged input of kNormMax columns fits in LDS");
     DeviceInfo di;
     VX_TRY(device_info(&di));
     vx_decoder* d = new vx_decoder();
@@ -1113,15 +1342,17 @@ static int create_decoder(const vx_decoder_config_t* c, vx_decoder_t** out) {
     d->device = di.device;
     d->num_cus = di.num_cus;
     d->cfg = *c;
+    d->pair = pair;
     d->qd = static_cast<size_t>(c->n_heads) * c->head_dim;
     d->kvd = static_cast<size_t>(c->n_kv_heads) * c->head_dim;
     d->proj.assign(static_cast<size_t>(c->n_layers) * kProjKinds, nullptr);
     d->norms.assign(static_cast<size_t>(c->n_layers + 1) * kNormKinds, nullptr);
     d->norm_set.assign(d->norms.size(), 0);
-    d->emb_set.assign(1, 0);
     const size_t L = c->n_layers, H = c->hidden;
     const size_t kv_elems = L * d->kvd * c->max_ctx;
     hipError_t e = dalloc(d, &d->d_emb, static_cast<size_t>(c->vocab) * H * 2);
+    if (e == hipSuccess && c->untied) e = dalloc(d, &d->d_head, static_cast<size_t>(c->vocab) * H * 2);
+    if (e == hipSuccess && pair) e = dalloc(d, &d->d_inter, round_up(c->ffn, kTileRows) * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_rope, static_cast<size_t>(c->max_ctx) * c->head_dim * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_kc, kv_elems * 2);
     if (e == hipSuccess) e = dalloc(d, &d->d_vc, kv_elems * 2);
@@ -1160,6 +1391,7 @@ static StageInput stage_input(const vx_decoder* d, uint32_t kind, size_t n, cons
     p.x_out = x_out;
     p.gamma = gamma;
     p.eps = d->cfg.rms_eps;
+    p.emb_f16 = d->cfg.emb_f16;
     return p;
 }
 
@@ -1184,29 +1416,44 @@ static ProjOut proj_out(const vx_decoder* d, size_t layer, int kind) {
     return o;
 }
 
+// K slices of a projection of n_chunks chunks per row: about one work item per CU for the stage's `tiles` tiles,
+// at most `limit` (what its consumers read), and short enough for the staged slice: a slice of q chunks spans at most
+// (ceil(q / 2) + 1) 160 input elements, which must fit the kNormMax window, and 16 waves x kDPer chunks.
+static uint32_t plan_kslices(uint32_t n_chunks, uint32_t tiles, uint32_t limit, int num_cus, bool* ok) {
+    constexpr uint32_t kMaxSliceChunks = 2 * (kNormMax / 160 - 1);  // 100
+    static_assert(kMaxSliceChunks <= kStChunks, "a slice's entries fit in LDS");
+    uint32_t ks = (static_cast<uint32_t>(num_cus) + tiles / 2) / tiles;
+    ks = std::max(1u, std::min({ks, limit, n_chunks}));
+    ks = std::max(ks, (n_chunks + kMaxSliceChunks - 1) / kMaxSliceChunks);
+    const uint32_t sc = (n_chunks + ks - 1) / ks;
+    *ok = ks <= limit && sc <= kMaxSliceChunks;
+    return (n_chunks + sc - 1) / sc;
+}
+
+static uint32_t input_variant(const StageInput& in) {
+    if (in.n <= 4u * kNT) return kDv4K;
+    if (in.n <= 8u * kNT) return kDv8K;
+    return kDvPlain;  // create_decoder admits only plain, unnormed inputs beyond kNormMax
+}
+
 // The stage launches of every layer. A stage's work items are (64-row tile, K slice) pairs of its projections; the K
-// split gives each stage about one item per CU (a 2560-row projection has only 40 tiles), within the slice counts its
-// consumers read (kMaxSlicesB for the ReLU^2 inputs, kMaxSlicesA otherwise).
+// split gives each stage about one item per CU (a 2560-row projection has only 40 tiles). A gated pair (gate and up
+// with SiLU) is one job of one slice whose items cover a tile of both matrices.
 static int build_stages(vx_decoder* d) {
     const size_t L = d->cfg.n_layers, H = d->cfg.hidden, F = d->cfg.ffn;
+    const bool sub = has_sub_norms(d);
     for (int s = 0; s < kStages; ++s) {
-        uint32_t tiles = 0, min_chunks = 0xffffffffu;
-        for (int k : kStageKinds[s]) {
-            if (k < 0) continue;
-            tiles += static_cast<uint32_t>(d->proj[k]->g.n_tiles);
-            min_chunks = std::min(min_chunks, static_cast<uint32_t>(d->proj[k]->g.n_chunks));
-            if (d->proj[k]->g.n_chunks > static_cast<size_t>(kDPer) * kTileGroup)
-                VX_FAIL(VX_ERR_INTERNAL, "projection %d has %zu chunks per row", k, d->proj[k]->g.n_chunks);
-        }
+        if (s == 2 && d->pair) continue;  // one slice, no partials
+        uint32_t tiles = 0;
+        for (int k : kStageKinds[s])
+            if (k >= 0) tiles += static_cast<uint32_t>(d->proj[k]->g.n_tiles);
         const uint32_t limit = s == 2 ? kMaxSlicesB : kMaxSlicesA;
-        uint32_t ks = (static_cast<uint32_t>(d->num_cus) + tiles / 2) / tiles;
-        ks = std::max(1u, std::min({ks, limit, min_chunks}));
         for (int k : kStageKinds[s]) {
             if (k < 0) continue;
             const Geometry& g = d->proj[k]->g;
-            const uint32_t nc = static_cast<uint32_t>(g.n_chunks);
-            const uint32_t sc = (nc + ks - 1) / ks;
-            d->kslices[k] = (nc + sc - 1) / sc;
+            bool ok = false;
+            d->kslices[k] = plan_kslices(static_cast<uint32_t>(g.n_chunks), tiles, limit, d->num_cus, &ok);
+            if (!ok) VX_FAIL(VX_ERR_UNSUPPORTED, "projection %d has too many chunks per row (%zu)", k, g.n_chunks);
             if (d->d_part[k]) (void)hipFree(d->d_part[k]);
             d->d_part[k] = nullptr;
             VX_HIP(hipMalloc(&d->d_part[k], static_cast<size_t>(d->kslices[k]) * g.padded_rows * 4));
@@ -1218,21 +1465,43 @@ static int build_stages(vx_decoder* d) {
         for (int s = 0; s < kStages; ++s) {
             DStageArgs& a = d->stages[l * kStages + s];
             uint32_t items = 0;
-            for (int k : kStageKinds[s]) {
-                if (k < 0) continue;
-                const vx_matrix* m = d->proj[l * kProjKinds + k];
+            if (s == 2 && d->pair) {
+                const vx_matrix* mg = d->proj[l * kProjKinds + VX_PROJ_GATE];
+                const vx_matrix* mu = d->proj[l * kProjKinds + VX_PROJ_UP];
                 DJob& j = a.job[a.n_jobs++];
-                j.w = m->d_w;
-                j.dsum = m->d_dsum;
-                j.part = d->d_part[k];
-                j.rows = static_cast<uint32_t>(m->g.rows);
-                j.padded_rows = static_cast<uint32_t>(m->g.padded_rows);
-                j.n_tiles = static_cast<uint32_t>(m->g.n_tiles);
-                j.n_chunks = static_cast<uint32_t>(m->g.n_chunks);
-                j.kslices = d->kslices[k];
-                j.slice_chunks = (j.n_chunks + j.kslices - 1) / j.kslices;
-                j.item_begin = items;
-                items += j.n_tiles * j.kslices;
+                j.w = mg->d_w;
+                j.dsum = mg->d_dsum;
+                j.w2 = mu->d_w;
+                j.dsum2 = mu->d_dsum;
+                j.act_out = d->d_inter;
+                j.ws = mg->weight_scale;
+                j.ws2 = mu->weight_scale;
+                j.act = d->cfg.act == VX_ACT_SILU ? kActSilu : kActRelu2;
+                j.n8 = static_cast<uint32_t>(F / 8 * 8);
+                j.rows = static_cast<uint32_t>(mg->g.rows);
+                j.padded_rows = static_cast<uint32_t>(mg->g.padded_rows);
+                j.n_tiles = static_cast<uint32_t>(mg->g.n_tiles);
+                j.n_chunks = static_cast<uint32_t>(mg->g.n_chunks);
+                j.kslices = 1;
+                j.slice_chunks = j.n_chunks;
+                items = j.n_tiles;
+            } else {
+                for (int k : kStageKinds[s]) {
+                    if (k < 0) continue;
+                    const vx_matrix* m = d->proj[l * kProjKinds + k];
+                    DJob& j = a.job[a.n_jobs++];
+                    j.w = m->d_w;
+                    j.dsum = m->d_dsum;
+                    j.part = d->d_part[k];
+                    j.rows = static_cast<uint32_t>(m->g.rows);
+                    j.padded_rows = static_cast<uint32_t>(m->g.padded_rows);
+                    j.n_tiles = static_cast<uint32_t>(m->g.n_tiles);
+                    j.n_chunks = static_cast<uint32_t>(m->g.n_chunks);
+                    j.kslices = d->kslices[k];
+                    j.slice_chunks = (j.n_chunks + j.kslices - 1) / j.kslices;
+                    j.item_begin = items;
+                    items += j.n_tiles * j.kslices;
+                }
             }
             a.total_items = items;
             StageInput& in = a.in;
@@ -1244,19 +1513,23 @@ static int build_stages(vx_decoder* d) {
             } else if (s == 0) {  // x + down of the previous layer -> attention norm
                 in = stage_input(d, kInResidual, H, d->d_xb, d->d_xa, nw[VX_NORM_ATTN]);
                 in.a = proj_out(d, l - 1, VX_PROJ_DOWN);
-            } else if (s == 1) {  // attention output -> attention sub-norm
-                in = stage_input(d, kInPlain, d->qd, d->d_att, nullptr, nw[VX_NORM_ATTN_SUB]);
+            } else if (s == 1) {  // attention output -> attention sub-norm (or none)
+                in = stage_input(d, kInPlain, d->qd, d->d_att, nullptr, sub ? nw[VX_NORM_ATTN_SUB] : nullptr);
             } else if (s == 2) {  // x + o -> FFN norm
                 in = stage_input(d, kInResidual, H, d->d_xa, d->d_xb, nw[VX_NORM_FFN]);
                 in.a = proj_out(d, l, VX_PROJ_O);
-            } else {  // relu2(gate) * up -> FFN sub-norm
-                in = stage_input(d, kInRelu2Mul, F, nullptr, nullptr, nw[VX_NORM_FFN_SUB]);
+            } else if (d->pair) {  // act(gate, up) from the pair -> FFN sub-norm (or none)
+                in = stage_input(d, kInPlain, F, d->d_inter, nullptr, sub ? nw[VX_NORM_FFN_SUB] : nullptr);
+            } else {  // relu2(gate) * up -> FFN sub-norm (or none)
+                in = stage_input(d, kInRelu2Mul, F, nullptr, nullptr, sub ? nw[VX_NORM_FFN_SUB] : nullptr);
                 in.a = proj_out(d, l, VX_PROJ_GATE);
                 in.b = proj_out(d, l, VX_PROJ_UP);
             }
             a.tbr = static_cast<uint32_t>(tile_row_bytes(in.n));
-            a.dbr = static_cast<uint32_t>(device_row_bytes(in.n));
             a.as_out = d->d_as + s;
+            a.variant = input_variant(in);
+            if (a.variant == kDvPlain && (in.kind != kInPlain || in.gamma != nullptr))
+                VX_FAIL(VX_ERR_INTERNAL, "stage %d input of %u elements needs a norm", s, in.n);
         }
     }
     return VX_OK;
@@ -1281,14 +1554,15 @@ static int record_step(const vx_decoder* d, hipStream_t st) {
         at.n_heads = c.n_heads;
         at.gqa = c.n_heads / c.n_kv_heads;
         at.max_ctx = c.max_ctx;
+        at.rope_normal = c.rope_mode == VX_ROPE_NORMAL ? 1u : 0u;
         at.scale = 1.0f / sqrtf(static_cast<float>(c.head_dim));
-        VX_TRY(launch_attention(at, st));
+        VX_TRY(launch_attention(at, c.head_dim, st));
         for (int s = 1; s < kStages; ++s) VX_TRY(launch_dgemv(d->stages[l * kStages + s], st));
     }
     HeadArgs h{};
     h.in = stage_input(d, kInResidual, c.hidden, d->d_xb, nullptr, d->norms[L * kNormKinds]);
     h.in.a = proj_out(d, L - 1, VX_PROJ_DOWN);
-    h.emb = d->d_emb;
+    h.w = c.untied ? d->d_head : d->d_emb;
     h.hidden = c.hidden;
     h.vocab = c.vocab;
     h.logits = d->d_logits;
@@ -1300,7 +1574,12 @@ static int record_step(const vx_decoder* d, hipStream_t st) {
     // of kNT / 4 rows.
     const uint32_t rows_per_wg = kNT / 4;
     const uint32_t grid = std::min<uint32_t>((c.vocab + rows_per_wg - 1) / rows_per_wg, static_cast<uint32_t>(d->num_cus));
-    return launch_head(h, grid, st);
+    return launch_head(h, c.emb_f16 != 0, grid, st);
+}
+
+static bool norm_needed(const vx_decoder* d, size_t layer, int kind) {
+    if (layer == d->cfg.n_layers) return kind == VX_NORM_ATTN;
+    return has_sub_norms(d) || (kind != VX_NORM_ATTN_SUB && kind != VX_NORM_FFN_SUB);
 }
 
 // Builds the stage launches and captures the step graph once every weight is set.
@@ -1310,9 +1589,11 @@ static int prepare(vx_decoder* d) {
     for (size_t i = 0; i < L * kProjKinds; ++i)
         if (!d->proj[i]) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "projection %zu of layer %zu is not set", i % kProjKinds, i / kProjKinds);
     for (size_t l = 0; l <= L; ++l)
-        for (int k = 0; k < (l == L ? 1 : kNormKinds); ++k)
-            if (!d->norm_set[l * kNormKinds + k]) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "norm %d of layer %zu is not set", k, l);
-    if (!d->emb_set[0]) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the embedding is not set");
+        for (int k = 0; k < kNormKinds; ++k)
+            if (norm_needed(d, l, k) && !d->norm_set[l * kNormKinds + k])
+                VX_FAIL(VX_ERR_INVALID_ARGUMENT, "norm %d of layer %zu is not set", k, l);
+    if (!d->emb_set) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the embedding is not set");
+    if (d->cfg.untied && !d->head_set) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the head is not set");
     drop_graph(d);
     VX_TRY(build_stages(d));
     VX_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
@@ -1372,8 +1653,8 @@ int vx_decoder_set_norm(vx_decoder_t* d, uint32_t layer, uint32_t kind, const fl
         VX_TRY(check_decoder(d));
         std::lock_guard<std::mutex> lk(d->mu);
         if (layer > d->cfg.n_layers) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "layer %u out of range (n_layers %u)", layer, d->cfg.n_layers);
-        if (kind >= static_cast<uint32_t>(kNormKinds) || (layer == d->cfg.n_layers && kind != 0))
-            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "norm kind %u is not valid for layer %u", kind, layer);
+        if (kind >= static_cast<uint32_t>(kNormKinds) || !norm_needed(d, layer, static_cast<int>(kind)))
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "norm kind %u is not valid for layer %u of this model", kind, layer);
         if (weights == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "weights is NULL");
         const size_t need = norm_len(d, layer, kind);
         if (n != need) VX_FAIL(VX_ERR_INVALID_SHAPE, "norm %u of layer %u has %zu weights, expected %zu", kind, layer, n, need);
@@ -1386,17 +1667,35 @@ int vx_decoder_set_norm(vx_decoder_t* d, uint32_t layer, uint32_t kind, const fl
     });
 }
 
+// The embedding (head = false) or the untied head, vocab x hidden 16-bit values of the type the config names.
+static int set_table(vx_decoder_t* d, const uint16_t* src, size_t n, bool head, bool f16) {
+    VX_TRY(check_decoder(d));
+    std::lock_guard<std::mutex> lk(d->mu);
+    const char* what = head ? "head" : "embedding";
+    if (src == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "%s is NULL", what);
+    if (head && !d->cfg.untied) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the model's head is its embedding (untied = 0)");
+    if (f16 != (d->cfg.emb_f16 != 0))
+        VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the model's %s holds %s values", what, d->cfg.emb_f16 ? "f16" : "bf16");
+    const size_t need = static_cast<size_t>(d->cfg.vocab) * d->cfg.hidden;
+    if (n != need) VX_FAIL(VX_ERR_INVALID_SHAPE, "the %s has %zu values, expected vocab * hidden = %zu", what, n, need);
+    VX_TRY(set_device(d->device));
+    VX_HIP(hipMemcpy(head ? d->d_head : d->d_emb, src, need * 2, hipMemcpyHostToDevice));
+    (head ? d->head_set : d->emb_set) = true;
+    return VX_OK;
+}
+
 int vx_decoder_set_embedding_bf16(vx_decoder_t* d, const uint16_t* embedding, size_t n) {
+    return guard([&]() -> int { return set_table(d, embedding, n, false, false); });
+}
+
+int vx_decoder_set_embedding_f16(vx_decoder_t* d, const uint16_t* embedding, size_t n) {
+    return guard([&]() -> int { return set_table(d, embedding, n, false, true); });
+}
+
+int vx_decoder_set_head(vx_decoder_t* d, const uint16_t* head, size_t n) {
     return guard([&]() -> int {
         VX_TRY(check_decoder(d));
-        std::lock_guard<std::mutex> lk(d->mu);
-        if (embedding == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "embedding is NULL");
-        const size_t need = static_cast<size_t>(d->cfg.vocab) * d->cfg.hidden;
-        if (n != need) VX_FAIL(VX_ERR_INVALID_SHAPE, "the embedding has %zu values, expected vocab * hidden = %zu", n, need);
-        VX_TRY(set_device(d->device));
-        VX_HIP(hipMemcpy(d->d_emb, embedding, need * 2, hipMemcpyHostToDevice));
-        d->emb_set[0] = 1;
-        return VX_OK;
+        return set_table(d, head, n, true, d->cfg.emb_f16 != 0);
     });
 }
 

@@ -1,11 +1,12 @@
-"""Greedy decoding of a ternary (BitNet-b1.58 family) model on the GPU: the token loop of vx_decoder_* in
+"""Greedy decoding of a ternary (BitNet-b1.58 or Falcon3 family) model on the GPU: the token loop of vx_decoder_* in
 include/velurex_hip.h.
 
-Mirrors the reference's runtime surface for this path: ModelConfig (quintrit-runtime/src/config.rs:155-177),
+Mirrors the reference's runtime surface for this path: ModelConfig (quintrit-runtime/src/config.rs:155-227),
 QuintritModel::forward_token (model.rs:282-377: one token at one position, logits out) and the greedy generation loop
 (engine.rs:590-686 with Sampler::sample greedy, sampler.rs:73-83). Weights are handed over as the reference holds them:
-planar velurex bytes with a per-tensor scale per projection, f32 RMSNorm weights, a bf16 embedding that is also the
-head. Everything runs in libvelurex_hip.so; without it (or without a gfx950 GPU) construction raises.
+planar velurex bytes with a per-tensor scale per projection, f32 RMSNorm weights, a bf16 or f16 embedding that is also
+the head unless the model has its own (Falcon3's lm_head). Everything runs in libvelurex_hip.so; without it (or
+without a gfx950 GPU) construction raises.
 """
 from __future__ import annotations
 
@@ -18,18 +19,24 @@ from ._lib import check, lib
 
 PROJ_Q, PROJ_K, PROJ_V, PROJ_O, PROJ_GATE, PROJ_UP, PROJ_DOWN = range(7)
 NORM_ATTN, NORM_ATTN_SUB, NORM_FFN, NORM_FFN_SUB = range(4)
+ACT_RELU2, ACT_SILU = 0, 1
+ROPE_NEOX, ROPE_NORMAL = 0, 1
 
 
 class _Config(ctypes.Structure):
     _fields_ = [("struct_size", ctypes.c_uint32), ("n_layers", ctypes.c_uint32), ("hidden", ctypes.c_uint32),
                 ("n_heads", ctypes.c_uint32), ("n_kv_heads", ctypes.c_uint32), ("head_dim", ctypes.c_uint32),
                 ("ffn", ctypes.c_uint32), ("vocab", ctypes.c_uint32), ("max_ctx", ctypes.c_uint32),
-                ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+                ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("act", ctypes.c_uint32),
+                ("rope_mode", ctypes.c_uint32), ("no_sub_norm", ctypes.c_uint32), ("emb_f16", ctypes.c_uint32),
+                ("untied", ctypes.c_uint32)]
 
 
 @dataclass(frozen=True)
 class DecoderConfig:
-    """The model shape (ModelConfig): layers, widths, heads, vocabulary, context and the RMSNorm/RoPE constants."""
+    """The model shape (ModelConfig): layers, widths, heads, vocabulary, context, the RMSNorm/RoPE constants and the
+    architecture switches (all 0: BitNet with a tied bf16 head; falcon3(): SiLU, Normal RoPE, no sub-norms, f16
+    embedding and an untied f16 head)."""
 
     n_layers: int
     hidden: int
@@ -41,11 +48,33 @@ class DecoderConfig:
     max_ctx: int
     rms_eps: float = 1e-5
     rope_theta: float = 500000.0
+    act: int = ACT_RELU2
+    rope_mode: int = ROPE_NEOX
+    no_sub_norm: int = 0
+    emb_f16: int = 0
+    untied: int = 0
 
     @classmethod
     def bitnet_2b(cls, max_ctx: int = 4096) -> "DecoderConfig":
         """ModelConfig::bitnet_2b_default (config.rs:155-177)."""
         return cls(30, 2560, 20, 5, 128, 6912, 128256, max_ctx, 1e-5, 500000.0)
+
+    @classmethod
+    def falcon3(cls, n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx, rms_eps=1e-5,
+                rope_theta=100000.0) -> "DecoderConfig":
+        """The Falcon3 architecture (ModelConfig::falcon3_*_default, config.rs:179-227)."""
+        return cls(n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, max_ctx, rms_eps, rope_theta,
+                   ACT_SILU, ROPE_NORMAL, 1, 1, 1)
+
+    @classmethod
+    def falcon3_10b(cls, max_ctx: int = 4096, n_layers: int = 40) -> "DecoderConfig":
+        """BASELINE.json configs[1]'s Falcon3-10B shapes (40 layers, hidden 3072, 12 / 4 heads of 256, FFN 23040,
+        vocabulary 131072) with the constants of falcon3_7b_default (config.rs:205-227)."""
+        return cls.falcon3(n_layers, 3072, 12, 4, 256, 23040, 131072, max_ctx)
+
+    @property
+    def has_sub_norms(self) -> bool:
+        return not self.no_sub_norm
 
     def projection_shape(self, kind: int) -> tuple:
         qd, kvd = self.n_heads * self.head_dim, self.n_kv_heads * self.head_dim
@@ -57,7 +86,7 @@ class DecoderConfig:
         c = _Config()
         c.struct_size = ctypes.sizeof(_Config)
         for f in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab", "max_ctx", "rms_eps",
-                  "rope_theta"):
+                  "rope_theta", "act", "rope_mode", "no_sub_norm", "emb_f16", "untied"):
             setattr(c, f, getattr(self, f))
         return c
 
@@ -86,6 +115,19 @@ class Decoder:
     def set_embedding_bf16(self, emb_bits) -> None:
         e = np.ascontiguousarray(emb_bits, dtype=np.uint16).reshape(-1)
         check(lib().vx_decoder_set_embedding_bf16(self.handle, _ptr(e), e.size))
+
+    def set_embedding_f16(self, emb_bits) -> None:
+        e = np.ascontiguousarray(emb_bits, dtype=np.uint16).reshape(-1)
+        check(lib().vx_decoder_set_embedding_f16(self.handle, _ptr(e), e.size))
+
+    def set_embedding(self, emb_bits) -> None:
+        """The embedding in the config's type (f16 when emb_f16, else bf16)."""
+        (self.set_embedding_f16 if self.config.emb_f16 else self.set_embedding_bf16)(emb_bits)
+
+    def set_head(self, head_bits) -> None:
+        """The untied head (vocab x hidden, the embedding's type)."""
+        h = np.ascontiguousarray(head_bits, dtype=np.uint16).reshape(-1)
+        check(lib().vx_decoder_set_head(self.handle, _ptr(h), h.size))
 
     def step(self, token: int, pos: int, want_logits: bool = True):
         """forward_token: (logits as float32 array or None, greedy next token)."""

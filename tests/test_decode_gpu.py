@@ -1,4 +1,5 @@
-"""GPU parity of the decode token loop through the C ABI (vx_decoder_*).
+"""GPU parity of the decode token loop (and the Falcon3 architecture of configs[1]) through
+the C ABI (vx_decoder_*).
 
 The reference's loop (QuintritModel::forward_token_with_scratchpad, quintrit-runtime/src/model.rs:282-377, with
 attention.rs:115-260 and 483-542, ops.rs and sampler.rs:73-83) is restated by the oracle (oracle/decode_oracle.c). The
@@ -33,21 +34,42 @@ def tiny_cfg(oracle, max_ctx=640):
 
 
 def load_decoder(oracle, model):
-    """A GPU decoder holding the oracle model's weights."""
+    """A GPU decoder holding the oracle model's weights (and its architecture switches)."""
     from quintrit_amd.decoder import Decoder, DecoderConfig
     c = model.cfg
     dc = DecoderConfig(c.n_layers, c.hidden, c.n_heads, c.n_kv_heads, c.head_dim, c.ffn, c.vocab, c.max_ctx,
-                       float(np.float32(c.rms_eps)), float(np.float32(c.rope_theta)))
+                       float(np.float32(c.rms_eps)), float(np.float32(c.rope_theta)), c.act, c.rope_mode,
+                       c.no_sub_norm, c.emb_f16, c.untied)
     dec = Decoder(dc)
     for layer in range(c.n_layers):
         for kind in range(7):
             planar, ws = model.projection(layer, kind)
             dec.set_projection(layer, kind, planar, ws)
         for kind in range(4):
-            dec.set_norm(layer, kind, model.norm(layer, kind))
+            w = model.norm(layer, kind)
+            if w is not None:
+                dec.set_norm(layer, kind, w)
     dec.set_norm(c.n_layers, 0, model.norm(c.n_layers, 0))
-    dec.set_embedding_bf16(model.embedding())
+    dec.set_embedding(model.embedding())
+    if c.untied:
+        dec.set_head(model.head())
     return dec
+
+
+def variant_cfg(oracle, name):
+    """Architecture variants of the token loop (ModelConfig switches, config.rs:155-227), small enough for the oracle:
+    falcon3  SiLU gate/up pair, no sub-norms, a 9220-wide FFN (the unnormed wide down input, ffn % 8 = 4: the SwiGLU
+             tail on libm's expf), head_dim 256, Normal RoPE, f16 embedding and untied f16 head
+    hd256    the BitNet structure (ReLU^2, sub-norms, NEOX, tied bf16) at head_dim 256
+    silu_sub SiLU with sub-norms (the pair's output normed), NEOX, head_dim 128, bf16 embedding with an untied head
+    relu_raw ReLU^2 without sub-norms (the gating input unnormed), Normal RoPE, f16 tied head"""
+    M = oracle.ModelConfig
+    return {
+        "falcon3": oracle.falcon3(2, 256, 4, 2, 256, 9220, 1000, 640, 1e-5, 100000.0),
+        "hd256": M(2, 256, 4, 2, 256, 384, 1000, 640, 1e-5, 10000.0),
+        "silu_sub": M(2, 256, 4, 2, 128, 392, 1000, 640, 1e-5, 10000.0, oracle.ACT_SILU, oracle.ROPE_NEOX, 0, 0, 1),
+        "relu_raw": M(2, 256, 4, 1, 128, 384, 1000, 640, 1e-5, 10000.0, oracle.ACT_RELU2, oracle.ROPE_NORMAL, 1, 1, 0),
+    }[name]
 
 
 def assert_same_bits(got, want, what):
@@ -113,6 +135,78 @@ def test_tiny_generate_tokens_identical(torch_dev, oracle, max_ctx, n_prompt, n_
     finally:
         dec.close()
         model.close()
+
+
+@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw"])
+def test_variant_step_logits_bit_exact(torch_dev, oracle, name):
+    """forward_token of each architecture variant at positions 0..299 (teacher forced; the 4-chunk attention split from
+    position 256): every logit bit-identical to the oracle's, every greedy token equal."""
+    model = oracle.Model(variant_cfg(oracle, name), 41)
+    dec = load_decoder(oracle, model)
+    try:
+        tokens = np.random.default_rng(6).integers(0, model.cfg.vocab, 300)
+        for pos, tok in enumerate(tokens):
+            want_next, want = model.forward(int(tok), pos)
+            got, got_next = dec.step(int(tok), pos)
+            assert_same_bits(got, want, f"{name}: logits at pos {pos}")
+            assert got_next == want_next, f"{name}: pos {pos}"
+    finally:
+        dec.close()
+        model.close()
+
+
+def test_falcon3_generate_tokens_identical(torch_dev, oracle):
+    """The Falcon3 variant's greedy loop in one graph per step against the oracle's loop, twice on one decoder."""
+    model = oracle.Model(variant_cfg(oracle, "falcon3"), 29)
+    dec = load_decoder(oracle, model)
+    try:
+        prompt = np.random.default_rng(77).integers(0, model.cfg.vocab, 8)
+        want = [int(t) for t in model.generate(prompt, 300)]
+        assert dec.generate(prompt, 300) == want
+        assert dec.generate(prompt, 300) == want
+    finally:
+        dec.close()
+        model.close()
+
+
+def test_decoder_config_switch_errors(torch_dev, oracle):
+    """The switches' argument checks: a config of the first struct size is BitNet; sub-norms are refused without
+    them; the head setter needs an untied model; the embedding type must match emb_f16."""
+    import ctypes
+    from quintrit_amd._lib import VxError, check, lib
+    from quintrit_amd.decoder import Decoder, DecoderConfig, _Config
+    c = DecoderConfig(1, 256, 2, 1, 128, 256, 100, 64)._c()
+    c.struct_size = _Config.act.offset
+    h = ctypes.c_void_p()
+    check(lib().vx_decoder_create(ctypes.byref(c), ctypes.byref(h)))
+    check(lib().vx_decoder_free(h))
+    c.struct_size = _Config.act.offset + 4
+    with pytest.raises(VxError, match="struct_size"):
+        check(lib().vx_decoder_create(ctypes.byref(c), ctypes.byref(h)))
+    with pytest.raises(VxError, match="head_dim"):
+        Decoder(DecoderConfig(1, 256, 2, 1, 64, 256, 100, 64))
+    with pytest.raises(VxError, match="ffn"):
+        Decoder(DecoderConfig.falcon3(1, 256, 2, 1, 128, 24580, 100, 64))
+    with pytest.raises(VxError, match="ffn"):  # a normed down input is limited to 8192
+        Decoder(DecoderConfig(1, 256, 2, 1, 128, 8196, 100, 64, act=1))
+    dec = Decoder(DecoderConfig.falcon3(1, 256, 2, 1, 256, 512, 100, 64))
+    try:
+        with pytest.raises(VxError, match="not valid"):
+            dec.set_norm(0, 1, np.ones(512, np.float32))
+        with pytest.raises(VxError, match="f16"):
+            dec.set_embedding_bf16(np.zeros(100 * 256, np.uint16))
+        dec.set_embedding(np.zeros(100 * 256, np.uint16))
+        with pytest.raises(VxError, match="INVALID_SHAPE"):
+            dec.set_head(np.zeros(100 * 255, np.uint16))
+        dec.set_head(np.zeros(100 * 256, np.uint16))
+    finally:
+        dec.close()
+    dec = Decoder(DecoderConfig(1, 256, 2, 1, 128, 256, 100, 64))
+    try:
+        with pytest.raises(VxError, match="untied"):
+            dec.set_head(np.zeros(100 * 256, np.uint16))
+    finally:
+        dec.close()
 
 
 def test_decoder_argument_errors(torch_dev, oracle):
