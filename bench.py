@@ -50,6 +50,8 @@ def parse():
                     help="stream: the driver's line (configs[1]); gemm: the batched GEMM of configs[2]; q2: the "
                          "block-scaled GEMV stream of configs[4]; decode: bs=1 greedy decode of configs[3]")
     ap.add_argument("--decode-new", type=int, default=256, help="decode mode: generated tokens per run")
+    ap.add_argument("--model", choices=["bitnet-2b", "falcon3-10b"], default="bitnet-2b",
+                    help="decode mode: BASELINE.json configs[3]'s BitNet-2B, or a Falcon3-10B-shaped model (configs[1])")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only copy 256 MiB device to device 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -532,12 +534,22 @@ def synth_bf16(np, rng, n: int, sigma: float):
     return out
 
 
-def decode_cpu_baseline(budget_s: float, prompt, cfg):
+def synth_f16(np, rng, n: int, sigma: float):
+    """f16 bits of N(0, sigma) values (round to nearest even)."""
+    out = np.empty(n, np.uint16)
+    step = 1 << 24
+    for i in range(0, n, step):
+        x = rng.standard_normal(min(step, n - i), dtype=np.float32) * np.float32(sigma)
+        out[i:i + x.size] = x.astype(np.float16).view(np.uint16)
+    return out
+
+
+def decode_cpu_baseline(budget_s: float, prompt, cfg, falcon: bool):
     """The oracle's decode step (oracle/decode_oracle.c: the reference's CPU token loop restated in C, projections
     exact, OpenMP over output rows) on this host's cores, a bounded number of tokens of the same model shape."""
     from oracle import oracle
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    m = oracle.Model(oracle.bitnet_2b(cfg.max_ctx), 0xB17)
+    m = oracle.Model(oracle.falcon3_10b(cfg.max_ctx, cfg.n_layers) if falcon else oracle.bitnet_2b(cfg.max_ctx), 0xB17)
     t0 = time.perf_counter()
     n = 0
     for pos, tok in enumerate(prompt):
@@ -548,31 +560,41 @@ def decode_cpu_baseline(budget_s: float, prompt, cfg):
     dt = time.perf_counter() - t0
     m.close()
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps (positions 0..{n - 1}) of the BitNet-b1.58-2B-shaped model by the C "
-                      f"restatement of the reference's token loop, {threads} OpenMP threads, {dt:.1f} s"}
+            "sample": f"{n} decode steps (positions 0..{n - 1}) of the {'Falcon3-10B' if falcon else 'BitNet-b1.58-2B'}-"
+                      f"shaped model by the C restatement of the reference's token loop, {threads} OpenMP threads, "
+                      f"{dt:.1f} s"}
 
 
 def decode_bench(torch, args) -> int:
-    """greedy bs=1 decode of a random-init BitNet-b1.58-2B-shaped model (30 layers, hidden
-    2560, 20/5 heads x 128, FFN 6912 ReLU^2, vocab 128256, tied bf16 head), 64 prompt tokens then --decode-new
-    generated tokens, every step one replay of the decode graph. tok/s counts every decoded position (prompt tokens
-    are fed one at a time, as the reference's loop does)."""
+    """Greedy bs=1 decode of a random-init model, 64 prompt tokens then --decode-new generated tokens, every step one
+    replay of the decode graph; tok/s counts every decoded position (prompt tokens are fed one at a time, as the
+    reference's loop does).
+    bitnet-2b    BASELINE.json configs[3]: 30 layers, hidden 2560, 20/5 heads x 128, FFN 6912 ReLU^2, vocab 128256,
+                 tied bf16 head
+    falcon3-10b  configs[1]'s Falcon3-10B shapes as a whole model: 40 layers, hidden 3072, 12/4 heads x 256, FFN 23040
+                 SwiGLU, Normal RoPE, no sub-norms, vocab 131072, f16 embedding and untied f16 head"""
     import numpy as np
     from quintrit_amd.decoder import Decoder, DecoderConfig
-    cfg = DecoderConfig.bitnet_2b()
+    falcon = args.model == "falcon3-10b"
+    cfg = DecoderConfig.falcon3_10b(n_layers=args.layers) if falcon else DecoderConfig.bitnet_2b()
     rng = np.random.default_rng(0xB17)
-    log("building a random-init BitNet-2B-shaped model on the host")
+    log(f"building a random-init {args.model}-shaped model on the host")
     dec = Decoder(cfg)
     trits = 0
+    norm_kinds = (0, 1, 2, 3) if cfg.has_sub_norms else (0, 2)
     for layer in range(cfg.n_layers):
         for kind in range(7):
             rows, cols = cfg.projection_shape(kind)
             dec.set_projection(layer, kind, synth_bitnet_planar(np, rng, rows, cols), 1.0 / float(np.sqrt(np.float32(cols))))
             trits += rows * cols
-        for kind, n in enumerate((cfg.hidden, cfg.n_heads * cfg.head_dim, cfg.hidden, cfg.ffn)):
+        for kind in norm_kinds:
+            n = (cfg.hidden, cfg.n_heads * cfg.head_dim, cfg.hidden, cfg.ffn)[kind]
             dec.set_norm(layer, kind, rng.uniform(0.75, 1.25, n).astype(np.float32))
     dec.set_norm(cfg.n_layers, 0, rng.uniform(0.75, 1.25, cfg.hidden).astype(np.float32))
-    dec.set_embedding_bf16(synth_bf16(np, rng, cfg.vocab * cfg.hidden, 0.02))
+    synth = synth_f16 if cfg.emb_f16 else synth_bf16
+    dec.set_embedding(synth(np, rng, cfg.vocab * cfg.hidden, 0.02))
+    if cfg.untied:
+        dec.set_head(synth(np, rng, cfg.vocab * cfg.hidden, 0.02))
     prompt = rng.integers(0, cfg.vocab, 64)
     n_new = args.decode_new
     steps_per_run = len(prompt) + n_new - 1
@@ -592,14 +614,16 @@ def decode_bench(torch, args) -> int:
     cpu = None
     if not args.no_cpu_baseline:
         log("timing the CPU baseline (oracle decode steps)")
-        cpu = decode_cpu_baseline(args.cpu_seconds, prompt, cfg)
+        cpu = decode_cpu_baseline(args.cpu_seconds, prompt, cfg, falcon)
         log(f"cpu baseline {cpu['value']} tok/s")
     line = {
         "metric": METRIC, "value": round(1e3 / ms_tok, 1), "unit": "tok/s", "n_gpus": 1, "steps": runs * steps_per_run,
         "warmup": max(1, args.warmup // 10) * steps_per_run, "ms_per_step": round(ms_tok, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8 x ternary, fp32/f16 attention",
         "data": "synthetic (random-init weights, random prompt)",
-        "config": {"workload": "bitnet-b1.58-2b greedy decode bs=1 (BASELINE.json configs[3])", "layers": cfg.n_layers,
+        "config": {"workload": ("falcon3-10b-shaped greedy decode bs=1 (BASELINE.json configs[1] shapes)" if falcon
+                                else "bitnet-b1.58-2b greedy decode bs=1 (BASELINE.json configs[3])"),
+                   "layers": cfg.n_layers, "head_dim": cfg.head_dim,
                    "hidden": cfg.hidden, "ffn": cfg.ffn, "vocab": cfg.vocab, "prompt": len(prompt), "new_tokens": n_new,
                    "parallelism": "single-gpu"},
         "generate_tok_s": round(n_new / dt, 1), "wall_s_per_run": round(dt, 4),
@@ -607,7 +631,7 @@ def decode_bench(torch, args) -> int:
         "hbm_bound_tok_s": round(HBM_PEAK_GBPS * 1e9 / alg, 1), "cpu_baseline": cpu,
         "roofline": {"bound": "hbm", "achieved": round(alg / (ms_tok / 1e3) / 1e9, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(alg / (ms_tok / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
-                     "kernel": "one decode step (151 launches); latency-bound at bs = 1"},
+                     "kernel": f"one decode step ({5 * cfg.n_layers + 1} launches); latency-bound at bs = 1"},
     }
     print(json.dumps(line), flush=True)
     dec.close()
