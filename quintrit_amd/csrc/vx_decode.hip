@@ -548,20 +548,24 @@ struct DStageArgs {
     uint32_t tbr;       // tile row bytes of in.n columns
     float* as_out;      // the stage's activation scale (workgroup 0)
     uint32_t variant;   // the kernel instance (host side: the input's length and kinds)
+    uint32_t loop;      // every job has one K slice: a workgroup takes items blockIdx.x, + gridDim.x, ...
+    uint32_t grid;      // workgroups of the launch
 };
 
 __constant__ DigitTable g_digits = make_digit_table();
 
-// One workgroup per work item. Order of the loads: the stage input, the digit table, then wave w's chunks
-// q0 + w, q0 + w + 16, ... of the tile (1 KiB each in the device layout), so the input is computed while the weights
-// are in flight; the digit-nibble table and the arithmetic are those of the lone GEMV (vx_gemv.hip). Only the entries
-// of the item's own chunks are staged.
+// One workgroup per work item, or (loop) fewer workgroups taking every gridDim.x-th item, which computes the stage
+// input once for several items of the same K slice. Order of the loads: the stage input, the digit table, then wave
+// w's chunks q0 + w, q0 + w + 16, ... of the tile (1 KiB each in the device layout), so the input is computed while
+// the weights are in flight; a looping workgroup loads the next item's chunks as the current ones are consumed. The
+// digit-nibble table and the arithmetic are those of the lone GEMV (vx_gemv.hip). Only the entries of the item's own
+// chunks are staged.
 template <int P4, int SA, int SB>
 __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of the digit nibbles of byte B (first half)
     __shared__ uint2 st[kStChunks * 16];
     __shared__ InputLds s;
-    __shared__ int red[2][kNT / 64][64];
+    __shared__ int red[2][2][kNT / 64][64];  // [item parity][gate, up][wave][lane]
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -574,36 +578,53 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) dig[k] = g_digits.v[(tid + k * kNT) >> 3];
 
-    const uint32_t item = blockIdx.x;
-    uint32_t j = 0;
-    if (a.n_jobs > 1 && item >= a.job[1].item_begin) j = 1;
-    if (a.n_jobs > 2 && item >= a.job[2].item_begin) j = 2;
-    const DJob jb = j == 0 ? a.job[0] : (j == 1 ? a.job[1] : a.job[2]);
-    const bool pair = jb.w2 != nullptr;
-    const uint32_t local = item - jb.item_begin;
-    const uint32_t tile = local / jb.kslices, ks = local - tile * jb.kslices;
-    const uint32_t grp = tile / kTileGroup, tt = tile - grp * kTileGroup;
-    const uint32_t T = min(static_cast<uint32_t>(kTileGroup), jb.n_tiles - grp * kTileGroup);
-    const uint32_t q0 = ks * jb.slice_chunks, nq = min(jb.slice_chunks, jb.n_chunks - q0);
-    const uint32_t nl = pair ? 2u * nq : nq;  // the item's chunk list: gate chunks, then (pair) up chunks
-    const uint32_t cnt = wave < nl ? (nl - wave + kTileGroup - 1) / kTileGroup : 0u;  // this wave's chunks
-    const size_t tile_off = (static_cast<size_t>(grp) * kTileGroup * jb.n_chunks + tt) * 64u + lane;
-    const g_u4* wp = (const g_u4*)(jb.w) + tile_off;
-    const g_u4* wp2 = pair ? (const g_u4*)(jb.w2) + tile_off : wp;
-    const size_t cs = static_cast<size_t>(T) * 64u;  // uint4 between chunks q and q + 1 of the tile
+    // A work item: its job, tile and K slice, and where wave `wave`'s chunks are.
+    struct Item {
+        DJob jb;
+        uint32_t tile, ks, q0, nq, cnt;
+        const g_u4* wp;
+        const g_u4* wp2;
+        size_t cs;  // uint4 between chunks q and q + 1 of the tile
+    };
+    auto locate = [&](uint32_t item) {
+        Item it;
+        uint32_t j = 0;
+        if (a.n_jobs > 1 && item >= a.job[1].item_begin) j = 1;
+        if (a.n_jobs > 2 && item >= a.job[2].item_begin) j = 2;
+        it.jb = j == 0 ? a.job[0] : (j == 1 ? a.job[1] : a.job[2]);
+        const uint32_t local = item - it.jb.item_begin;
+        it.tile = local / it.jb.kslices;
+        it.ks = local - it.tile * it.jb.kslices;
+        const uint32_t grp = it.tile / kTileGroup, tt = it.tile - grp * kTileGroup;
+        const uint32_t T = min(static_cast<uint32_t>(kTileGroup), it.jb.n_tiles - grp * kTileGroup);
+        it.q0 = it.ks * it.jb.slice_chunks;
+        it.nq = min(it.jb.slice_chunks, it.jb.n_chunks - it.q0);
+        const uint32_t nl = it.jb.w2 != nullptr ? 2u * it.nq : it.nq;  // gate chunks, then (pair) up chunks
+        it.cnt = wave < nl ? (nl - wave + kTileGroup - 1) / kTileGroup : 0u;
+        const size_t tile_off = (static_cast<size_t>(grp) * kTileGroup * it.jb.n_chunks + tt) * 64u + lane;
+        it.wp = (const g_u4*)(it.jb.w) + tile_off;
+        it.wp2 = it.jb.w2 != nullptr ? (const g_u4*)(it.jb.w2) + tile_off : it.wp;
+        it.cs = static_cast<size_t>(T) * 64u;
+        return it;
+    };
+    auto chunk_load = [&](const Item& it, int i) {
+        const uint32_t c = wave + kTileGroup * static_cast<uint32_t>(i);
+        const bool up = c >= it.nq;
+        return __builtin_nontemporal_load((up ? it.wp2 : it.wp) + (it.q0 + (up ? c - it.nq : c)) * it.cs);
+    };
+
+    uint32_t item = blockIdx.x;
+    Item it = locate(item);
     u32x4 b[kDPer];
 #pragma unroll
-    for (int i = 0; i < kDPer; ++i) {
-        if (static_cast<uint32_t>(i) < cnt) {
-            const uint32_t c = wave + kTileGroup * i;
-            const bool up = c >= nq;
-            b[i] = __builtin_nontemporal_load((up ? wp2 : wp) + (q0 + (up ? c - nq : c)) * cs);
-        }
-    }
+    for (int i = 0; i < kDPer; ++i)
+        if (static_cast<uint32_t>(i) < it.cnt) b[i] = chunk_load(it, i);
 
     float y[P4][4];
     stage_y(a.in, r, s, blockIdx.x == 0, y);
-    const uint32_t c0 = q0 * 16u, c1 = min((q0 + nq) * 16u, a.tbr);
+    // The staged slice: every item of a workgroup has the same K slice (one workgroup per item, or a looping stage
+    // whose jobs have one slice each).
+    const uint32_t c0 = it.q0 * 16u, c1 = min((it.q0 + it.nq) * 16u, a.tbr);
     uint32_t lo, hi;
     slice_window(a.in.n, c0, c1, &lo, &hi);
     const float mx = stage_window(y, a.in.n, lo, hi, s);
@@ -617,79 +638,99 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     }
     float act_scale;
     int act_sum;
-    stage_quant(y, s, mx, a.in.n, a.tbr, c0, (q0 + nq) * 16u, lo, st, &act_scale, &act_sum);
+    stage_quant(y, s, mx, a.in.n, a.tbr, c0, (it.q0 + it.nq) * 16u, lo, st, &act_scale, &act_sum);
     if (blockIdx.x == 0 && tid == 0) *a.as_out = act_scale;
 
-    int acc_lo = 0, acc_hi = 0, acc2_lo = 0, acc2_hi = 0;
+    for (uint32_t parity = 0;; parity ^= 1u) {
+        const uint32_t next = a.loop ? item + gridDim.x : a.total_items;
+        const bool more = next < a.total_items;
+        Item nt{};
+        if (more) nt = locate(next);
+        const bool pair = it.jb.w2 != nullptr;
+        int acc_lo = 0, acc_hi = 0, acc2_lo = 0, acc2_hi = 0;
 #pragma unroll
-    for (int i = 0; i < kDPer; ++i) {
-        if (static_cast<uint32_t>(i) >= cnt) break;
-        const uint32_t c = wave + kTileGroup * i;
-        const bool up = pair && c >= nq;
-        const uint32_t q = up ? c - nq : c;  // chunk of the slice
-        const uint32_t dw[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
-        const uint2 e = st[q * 16u + (lane & 15u)];
-        __builtin_amdgcn_sched_barrier(0);
-        uint32_t t[16];
+        for (int i = 0; i < kDPer; ++i) {
+            if (static_cast<uint32_t>(i) < it.cnt) {
+                const uint32_t c = wave + kTileGroup * i;
+                const bool up = pair && c >= it.nq;
+                const uint32_t q = up ? c - it.nq : c;  // chunk of the slice
+                const uint32_t dw[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
+                const uint2 e = st[q * 16u + (lane & 15u)];
+                __builtin_amdgcn_sched_barrier(0);
+                uint32_t t[16];
 #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const uint32_t addr = __builtin_amdgcn_perm(dw[k >> 2], lane_off, 0x0c0c0000u | ((4u + (k & 3)) << 8));
-            t[k] = *reinterpret_cast<const uint32_t*>(tabb + addr);
-        }
-        if (!pair) {
-            dot4_bcast<0>(acc_lo, acc_hi, e.x, e.y, t[0], t[1], t[2], t[3]);
-            dot4_bcast<4>(acc_lo, acc_hi, e.x, e.y, t[4], t[5], t[6], t[7]);
-            dot4_bcast<8>(acc_lo, acc_hi, e.x, e.y, t[8], t[9], t[10], t[11]);
-            dot4_bcast<12>(acc_lo, acc_hi, e.x, e.y, t[12], t[13], t[14], t[15]);
-        } else {
-            int l = 0, h = 0;
-            dot4_bcast<0>(l, h, e.x, e.y, t[0], t[1], t[2], t[3]);
-            dot4_bcast<4>(l, h, e.x, e.y, t[4], t[5], t[6], t[7]);
-            dot4_bcast<8>(l, h, e.x, e.y, t[8], t[9], t[10], t[11]);
-            dot4_bcast<12>(l, h, e.x, e.y, t[12], t[13], t[14], t[15]);
-            if (up) {
-                acc2_lo += l;
-                acc2_hi += h;
-            } else {
-                acc_lo += l;
-                acc_hi += h;
+                for (int k = 0; k < 16; ++k) {
+                    const uint32_t addr = __builtin_amdgcn_perm(dw[k >> 2], lane_off, 0x0c0c0000u | ((4u + (k & 3)) << 8));
+                    t[k] = *reinterpret_cast<const uint32_t*>(tabb + addr);
+                }
+                // b[i] is free: the next item's chunk i goes into it while this one is summed
+                if (more && static_cast<uint32_t>(i) < nt.cnt) b[i] = chunk_load(nt, i);
+                if (!pair) {
+                    dot4_bcast<0>(acc_lo, acc_hi, e.x, e.y, t[0], t[1], t[2], t[3]);
+                    dot4_bcast<4>(acc_lo, acc_hi, e.x, e.y, t[4], t[5], t[6], t[7]);
+                    dot4_bcast<8>(acc_lo, acc_hi, e.x, e.y, t[8], t[9], t[10], t[11]);
+                    dot4_bcast<12>(acc_lo, acc_hi, e.x, e.y, t[12], t[13], t[14], t[15]);
+                } else {
+                    int l = 0, h = 0;
+                    dot4_bcast<0>(l, h, e.x, e.y, t[0], t[1], t[2], t[3]);
+                    dot4_bcast<4>(l, h, e.x, e.y, t[4], t[5], t[6], t[7]);
+                    dot4_bcast<8>(l, h, e.x, e.y, t[8], t[9], t[10], t[11]);
+                    dot4_bcast<12>(l, h, e.x, e.y, t[12], t[13], t[14], t[15]);
+                    if (up) {
+                        acc2_lo += l;
+                        acc2_hi += h;
+                    } else {
+                        acc_lo += l;
+                        acc_hi += h;
+                    }
+                }
+            } else if (more && static_cast<uint32_t>(i) < nt.cnt) {
+                b[i] = chunk_load(nt, i);
             }
         }
-    }
-    red[0][wave][lane] = acc_lo + 16 * acc_hi;
-    if (pair) red[1][wave][lane] = acc2_lo + 16 * acc2_hi;
-    __syncthreads();
-    if (wave != 0) return;
-    // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in slice 0
-    int v = 0;
+        red[parity][0][wave][lane] = acc_lo + 16 * acc_hi;
+        if (pair) red[parity][1][wave][lane] = acc2_lo + 16 * acc2_hi;
+        // One barrier per item: the next item writes the other parity, and the one after this parity only after the
+        // next item's barrier, which wave 0 reaches once it has read these sums.
+        __syncthreads();
+        if (wave == 0) {
+            // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in
+            // slice 0
+            const DJob& jb = it.jb;
+            int v = 0;
 #pragma unroll
-    for (int w = 0; w < kNT / 64; ++w) v += red[0][w][lane];
-    const uint32_t row = tile * kTileRows + lane;
-    if (ks == 0) v += 8 * jb.dsum[row] - act_sum;
-    if (!pair) {
-        jb.part[static_cast<size_t>(ks) * jb.padded_rows + row] = v;
-        return;
-    }
-    int v2 = 0;
+            for (int w = 0; w < kNT / 64; ++w) v += red[parity][0][w][lane];
+            const uint32_t row = it.tile * kTileRows + lane;
+            if (it.ks == 0) v += 8 * jb.dsum[row] - act_sum;
+            if (!pair) {
+                jb.part[static_cast<size_t>(it.ks) * jb.padded_rows + row] = v;
+            } else {
+                int v2 = 0;
 #pragma unroll
-    for (int w = 0; w < kNT / 64; ++w) v2 += red[1][w][lane];
-    v2 += 8 * jb.dsum2[row] - act_sum;
-    // the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170
-    const bool zero = !(act_scale > 0.0f);
-    const float g = zero ? 0.0f : static_cast<float>(v) * (jb.ws / act_scale);
-    const float u = zero ? 0.0f : static_cast<float>(v2) * (jb.ws2 / act_scale);
-    float o;
-    if (jb.act == kActSilu) {
-        const float ex = row < jb.n8 ? ggml_expf(0.0f - g) : glibc_expf(-g);
-        const float den = 1.0f + ex;
-        const float sl = g / den;
-        o = sl * u;
-    } else {
-        const float pos = g > 0.0f ? g : 0.0f;
-        const float sq = pos * pos;
-        o = sq * u;
+                for (int w = 0; w < kNT / 64; ++w) v2 += red[parity][1][w][lane];
+                v2 += 8 * jb.dsum2[row] - act_sum;
+                // the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170
+                const bool zero = !(act_scale > 0.0f);
+                const float g = zero ? 0.0f : static_cast<float>(v) * (jb.ws / act_scale);
+                const float u = zero ? 0.0f : static_cast<float>(v2) * (jb.ws2 / act_scale);
+                float o;
+                if (jb.act == kActSilu) {
+                    const float ex = row < jb.n8 ? ggml_expf(0.0f - g) : glibc_expf(-g);
+                    const float den = 1.0f + ex;
+                    const float sl = g / den;
+                    o = sl * u;
+                } else {
+                    const float pos = g > 0.0f ? g : 0.0f;
+                    const float sq = pos * pos;
+                    o = sq * u;
+                }
+                if (row < jb.rows) jb.act_out[row] = o;
+            }
+        }
+        if (!more) break;
+        item = next;
+        it = nt;
     }
-    if (row < jb.rows) jb.act_out[row] = o;
 }
 
 // ---- attention ------------------------------------------------------------------------------------------------------------
@@ -710,46 +751,6 @@ constexpr uint32_t kAttnMaxCtx = 4096;  // KV positions held in LDS (scores, run
 constexpr uint32_t kAttnWaves = 8;      // 4 chunks x 2 halves of the head
 constexpr uint32_t kAttnBatch = 8;      // positions whose LDS operands are read ahead of the accumulator chain
 
-// ggml_vec_dot_f16 of HD values (ops.rs:960-1015): four accumulators of eight lanes take fma per 32 values,
-// red = (s0 + s2) + (s1 + s3), t[k] = red[k] + red[k + 4], (t0 + t1) + (t2 + t3). q is in LDS, k is loaded 256
-// (head_dim 128) or 128 bytes at a time.
-template <int HD>
-__device__ __forceinline__ float dot_f16(const uint16_t* q, const uint16_t* k) {
-    float acc[4][8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int l = 0; l < 8; ++l) acc[j][l] = 0.0f;
-    constexpr int kPart = HD == 128 ? 128 : 64;  // values whose k is loaded at once
-#pragma unroll
-    for (int part = 0; part < HD / kPart; ++part) {
-        uint4 kr[kPart / 8];
-#pragma unroll
-        for (int c = 0; c < kPart / 8; ++c) kr[c] = *reinterpret_cast<const uint4*>(k + part * kPart + 8 * c);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < kPart / 32; ++i) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint4 kv = kr[4 * i + j];
-                const uint4 qv = *reinterpret_cast<const uint4*>(q + part * kPart + 32 * i + 8 * j);
-                const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-                for (int l = 0; l < 8; ++l) {
-                    const uint16_t kb = static_cast<uint16_t>(kw[l >> 1] >> ((l & 1) * 16));
-                    const uint16_t qb = static_cast<uint16_t>(qw[l >> 1] >> ((l & 1) * 16));
-                    acc[j][l] = __builtin_fmaf(f16_f32(qb), f16_f32(kb), acc[j][l]);
-                }
-            }
-        }
-    }
-    float red[8];
-#pragma unroll
-    for (int l = 0; l < 8; ++l) red[l] = (acc[0][l] + acc[2][l]) + (acc[1][l] + acc[3][l]);
-    const float t0 = red[0] + red[4], t1 = red[1] + red[5], t2 = red[2] + red[6], t3 = red[3] + red[7];
-    return (t0 + t1) + (t2 + t3);
-}
-
 // f16 value of an f32 (round to nearest even, after the f32 rounding of x), kept in an f32
 __device__ __forceinline__ float r16(float x) { return static_cast<float>(static_cast<_Float16>(keep_f32(x))); }
 
@@ -762,7 +763,7 @@ __device__ __forceinline__ float r16(float x) { return static_cast<float>(static
 // online softmax covers all positions; from 512 on, 4 chunks of ceil(n_kv / 4) positions run one each and are combined
 // in order. The online softmax of a chunk (attend_range, attention.rs:436-468) is rebuilt without its serial
 // dependences except the FP16 accumulator itself:
-//   scores        every position in parallel: ggml_vec_dot_f16(q, k) * scale
+//   scores        every position in parallel (four lanes each): ggml_vec_dot_f16(q, k) * scale
 //   running max   a scan per chunk; the reference's max moves only on score > max, the scan combines the same way
 //   factors       every position in parallel: a new maximum gives ms = expf(m_old - score), vs = 1; otherwise ms = 1,
 //                 vs = expf(score - max); stored as -ms or vs (the sign marks the case)
@@ -838,21 +839,80 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     // This wave's first window of V, requested before the scores so that its latency overlaps them, the scan and
     // the exponentials; the position itself comes from LDS. Load j of a lane holds 8 coordinates of position
     // 8 j + lane / kLP of the window.
+    // Rows come from the cache in global memory only (a select between an LDS and a global address would make every
+    // load a flat one); the row of the position itself, not yet visible there, is replaced from vp when a window is
+    // stored to LDS. Every row read is below max_ctx.
     const uint32_t off = half * kHalf + (lane % kLP) * 8u;
     const uint16_t* vsrc = vb + off;
-    auto load_v = [&](uint32_t p) -> u32x4 {
-        return p == pos ? *reinterpret_cast<const u32x4*>(vp + off)
-                        : *reinterpret_cast<const u32x4*>(vsrc + static_cast<size_t>(p) * HD);
-    };
+    auto load_v = [&](uint32_t p) -> u32x4 { return *reinterpret_cast<const u32x4*>(vsrc + static_cast<size_t>(p) * HD); };
+    const u32x4 vself = *reinterpret_cast<const u32x4*>(vp + off);
     constexpr uint32_t kPosPerLoad = 64u / kLP;
-    u32x4 r[8];
-    if (st < en) {
+    auto load_window = [&](uint32_t base, u32x4 (&r)[8]) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = load_v(min(st + kPosPerLoad * j + lane / kLP, en - 1u));
-    }
+        for (int j = 0; j < 8; ++j) r[j] = load_v(min(base + kPosPerLoad * j + lane / kLP, en - 1u));
+    };
+    u32x4 ra[8], rb[8];  // two windows in flight
+    if (st < en) load_window(st, ra);
+    if (st + kWin < en) load_window(st + kWin, rb);
 
-    for (uint32_t p = tid; p < seq; p += kAttnWaves * 64u)
-        sc[p] = dot_f16<HD>(qs, p == pos ? kp : kb + static_cast<size_t>(p) * HD) * a.scale;
+    // Scores, four lanes per position (ggml_vec_dot_f16, ops.rs:960-1015): lane j of a group holds accumulator j
+    // (values 32 i + 8 j .. + 7 of every 32-value block i) with q in registers; (a0 + a2) + (a1 + a3) across the
+    // group, then red[k] + red[k + 4] and (t0 + t1) + (t2 + t3) in lane 0. The next position's k is loaded while the
+    // current one is summed.
+    {
+        constexpr int kBlk = HD / 32;
+        const uint32_t j = tid & 3u, g = tid >> 2;
+        constexpr uint32_t kGroups = kAttnWaves * 64u / 4u;
+        float qf[kBlk][8];
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i) {
+            const uint4 qv = *reinterpret_cast<const uint4*>(qs + 32 * i + 8 * j);
+            const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+            for (int l = 0; l < 8; ++l) qf[i][l] = f16_f32(static_cast<uint16_t>(qw[l >> 1] >> ((l & 1) * 16)));
+        }
+        auto load_k = [&](uint32_t p, uint4 (&kr)[kBlk]) {
+            if (p == pos) {
+#pragma unroll
+                for (int i = 0; i < kBlk; ++i) kr[i] = *reinterpret_cast<const uint4*>(kp + 32 * i + 8 * j);
+            } else {
+                const uint16_t* row = kb + static_cast<size_t>(p) * HD + 8 * j;
+#pragma unroll
+                for (int i = 0; i < kBlk; ++i) kr[i] = *reinterpret_cast<const uint4*>(row + 32 * i);
+            }
+        };
+        auto score = [&](uint32_t p, const uint4 (&kr)[kBlk]) {
+            float acc[8];
+#pragma unroll
+            for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kBlk; ++i) {
+                const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+                for (int l = 0; l < 8; ++l)
+                    acc[l] = __builtin_fmaf(qf[i][l], f16_f32(static_cast<uint16_t>(kw[l >> 1] >> ((l & 1) * 16))), acc[l]);
+            }
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                acc[l] = acc[l] + __shfl_xor(acc[l], 2);
+                acc[l] = acc[l] + __shfl_xor(acc[l], 1);
+            }
+            if (j == 0) {
+                const float t0 = acc[0] + acc[4], t1 = acc[1] + acc[5], t2 = acc[2] + acc[6], t3 = acc[3] + acc[7];
+                sc[p] = ((t0 + t1) + (t2 + t3)) * a.scale;
+            }
+        };
+        uint4 ka[kBlk], kn[kBlk];
+        uint32_t p = g;
+        if (p < seq) load_k(p, ka);
+        for (; p < seq; p += 2u * kGroups) {  // unrolled by two so that the buffers keep their registers
+            if (p + kGroups < seq) load_k(p + kGroups, kn);
+            score(p, ka);
+            if (p + kGroups >= seq) break;
+            if (p + 2u * kGroups < seq) load_k(p + 2u * kGroups, ka);
+            score(p + kGroups, kn);
+        }
+    }
     __syncthreads();
 
     if (wave < n_chunks) {  // the running maximum of chunk `wave`
@@ -884,75 +944,79 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     float y[kPerLane], ssum = 0.0f;
 #pragma unroll
     for (int m = 0; m < kPerLane; ++m) y[m] = 0.0f;
-    if (st < en) {
-        uint16_t* buf = vbuf[wave];
-        for (uint32_t base = st; base < en; base += kWin) {
+    uint16_t* buf = vbuf[wave];
+    // One window: its rows (the position itself from vp) into LDS, the window two ahead into the freed registers,
+    // then the accumulator chain over its positions.
+    auto window = [&](uint32_t base, u32x4 (&r)[8]) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                *reinterpret_cast<u32x4*>(buf + (kPosPerLoad * j + lane / kLP) * kHalf + (lane % kLP) * 8u) = r[j];
-            if (base + kWin < en) {
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t pj = base + kPosPerLoad * j + lane / kLP;
+            *reinterpret_cast<u32x4*>(buf + (kPosPerLoad * j + lane / kLP) * kHalf + (lane % kLP) * 8u) =
+                pj == pos ? vself : r[j];
+        }
+        if (base + 2u * kWin < en) load_window(base + 2u * kWin, r);
+        const uint32_t n = min(kWin, en - base);  // wave-uniform
+        const float f = lane < n ? sc[base + lane] : 0.0f;
+        const uint32_t nb = n & ~(kAttnBatch - 1u);
+        // Whole batches of kAttnBatch positions, their LDS operands read before the serial chain uses them; a
+        // window without a new maximum (ms = 1 throughout) takes the shorter chain.
+        if (__ballot(__builtin_signbit(f)) == 0) {
+            auto step = [&](float e, const float (&v)[kPerLane]) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) r[j] = load_v(min(base + kWin + kPosPerLoad * j + lane / kLP, en - 1u));
+                for (int m = 0; m < kPerLane; ++m) y[m] = r16(__builtin_fmaf(v[m], e, y[m]));
+                ssum = ssum + e;
+            };
+            for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
+                float fe[kAttnBatch], fv[kAttnBatch][kPerLane];
+#pragma unroll
+                for (uint32_t u = 0; u < kAttnBatch; ++u) {
+                    fe[u] = sc[base + i0 + u];
+#pragma unroll
+                    for (int m = 0; m < kPerLane; ++m) fv[u][m] = f16_f32(buf[(i0 + u) * kHalf + lane + 64u * m]);
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
             }
-            const uint32_t n = min(kWin, en - base);  // wave-uniform
-            const float f = lane < n ? sc[base + lane] : 0.0f;
-            const uint32_t nb = n & ~(kAttnBatch - 1u);
-            // Whole batches of kAttnBatch positions, their LDS operands read before the serial chain uses them; a
-            // window without a new maximum (ms = 1 throughout) takes the shorter chain.
-            if (__ballot(__builtin_signbit(f)) == 0) {
-                auto step = [&](float e, const float (&v)[kPerLane]) {
+            for (uint32_t i = nb; i < n; ++i) {
+                float fv[kPerLane];
 #pragma unroll
-                    for (int m = 0; m < kPerLane; ++m) y[m] = r16(__builtin_fmaf(v[m], e, y[m]));
-                    ssum = ssum + e;
-                };
-                for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
-                    float fe[kAttnBatch], fv[kAttnBatch][kPerLane];
+                for (int m = 0; m < kPerLane; ++m) fv[m] = f16_f32(buf[i * kHalf + lane + 64u * m]);
+                step(sc[base + i], fv);
+            }
+        } else {
+            auto step = [&](float fi, const float (&v)[kPerLane]) {
+                const bool nm = __builtin_signbit(fi);
+                const float e = __builtin_fabsf(fi);
+                const float ms = nm ? e : 1.0f, vs = nm ? 1.0f : e;
 #pragma unroll
-                    for (uint32_t u = 0; u < kAttnBatch; ++u) {
-                        fe[u] = sc[base + i0 + u];
-#pragma unroll
-                        for (int m = 0; m < kPerLane; ++m) fv[u][m] = f16_f32(buf[(i0 + u) * kHalf + lane + 64u * m]);
-                    }
-#pragma unroll
-                    for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
+                for (int m = 0; m < kPerLane; ++m) {
+                    y[m] = r16(y[m] * ms);
+                    y[m] = r16(__builtin_fmaf(v[m], vs, y[m]));
                 }
-                for (uint32_t i = nb; i < n; ++i) {
-                    float fv[kPerLane];
+                ssum = __builtin_fmaf(ssum, ms, vs);
+            };
+            for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
+                float fe[kAttnBatch], fv[kAttnBatch][kPerLane];
 #pragma unroll
-                    for (int m = 0; m < kPerLane; ++m) fv[m] = f16_f32(buf[i * kHalf + lane + 64u * m]);
-                    step(sc[base + i], fv);
+                for (uint32_t u = 0; u < kAttnBatch; ++u) {
+                    fe[u] = sc[base + i0 + u];
+#pragma unroll
+                    for (int m = 0; m < kPerLane; ++m) fv[u][m] = f16_f32(buf[(i0 + u) * kHalf + lane + 64u * m]);
                 }
-            } else {
-                auto step = [&](float fi, const float (&v)[kPerLane]) {
-                    const bool nm = __builtin_signbit(fi);
-                    const float e = __builtin_fabsf(fi);
-                    const float ms = nm ? e : 1.0f, vs = nm ? 1.0f : e;
 #pragma unroll
-                    for (int m = 0; m < kPerLane; ++m) {
-                        y[m] = r16(y[m] * ms);
-                        y[m] = r16(__builtin_fmaf(v[m], vs, y[m]));
-                    }
-                    ssum = __builtin_fmaf(ssum, ms, vs);
-                };
-                for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
-                    float fe[kAttnBatch], fv[kAttnBatch][kPerLane];
+                for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
+            }
+            for (uint32_t i = nb; i < n; ++i) {
+                float fv[kPerLane];
 #pragma unroll
-                    for (uint32_t u = 0; u < kAttnBatch; ++u) {
-                        fe[u] = sc[base + i0 + u];
-#pragma unroll
-                        for (int m = 0; m < kPerLane; ++m) fv[u][m] = f16_f32(buf[(i0 + u) * kHalf + lane + 64u * m]);
-                    }
-#pragma unroll
-                    for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
-                }
-                for (uint32_t i = nb; i < n; ++i) {
-                    float fv[kPerLane];
-#pragma unroll
-                    for (int m = 0; m < kPerLane; ++m) fv[m] = f16_f32(buf[i * kHalf + lane + 64u * m]);
-                    step(sc[base + i], fv);
-                }
+                for (int m = 0; m < kPerLane; ++m) fv[m] = f16_f32(buf[i * kHalf + lane + 64u * m]);
+                step(sc[base + i], fv);
             }
         }
+    };
+    for (uint32_t base = st; base < en; base += 2u * kWin) {  // unrolled by two so that the windows keep their registers
+        window(base, ra);
+        if (base + kWin < en) window(base + kWin, rb);
     }
     float* out = a.out + static_cast<size_t>(h) * HD;
     if (!split) {
@@ -1126,9 +1190,9 @@ enum DVariant : uint32_t { kDv4K = 0, kDv8K = 1, kDvPlain = 2 };
 
 int launch_dgemv(const DStageArgs& a, hipStream_t s) {
     switch (a.variant) {
-        case kDv4K: hipLaunchKernelGGL((dgemv_kernel<1, kMaxSlicesA, kMaxSlicesB>), dim3(a.total_items), dim3(kNT), 0, s, a); break;
-        case kDv8K: hipLaunchKernelGGL((dgemv_kernel<2, kMaxSlicesA, kMaxSlicesB>), dim3(a.total_items), dim3(kNT), 0, s, a); break;
-        default: hipLaunchKernelGGL((dgemv_kernel<kPlainMax / (4 * kNT), 0, 0>), dim3(a.total_items), dim3(kNT), 0, s, a); break;
+        case kDv4K: hipLaunchKernelGGL((dgemv_kernel<1, kMaxSlicesA, kMaxSlicesB>), dim3(a.grid), dim3(kNT), 0, s, a); break;
+        case kDv8K: hipLaunchKernelGGL((dgemv_kernel<2, kMaxSlicesA, kMaxSlicesB>), dim3(a.grid), dim3(kNT), 0, s, a); break;
+        default: hipLaunchKernelGGL((dgemv_kernel<kPlainMax / (4 * kNT), 0, 0>), dim3(a.grid), dim3(kNT), 0, s, a); break;
     }
     VX_HIP(hipGetLastError());
     return VX_OK;
@@ -1504,6 +1568,11 @@ static int build_stages(vx_decoder* d) {
                 }
             }
             a.total_items = items;
+            // A stage whose jobs have one K slice each loops over its items with one workgroup per CU.
+            bool one_slice = true;
+            for (uint32_t jj = 0; jj < a.n_jobs; ++jj) one_slice = one_slice && a.job[jj].kslices == 1;
+            a.loop = one_slice && items > static_cast<uint32_t>(d->num_cus) ? 1u : 0u;
+            a.grid = a.loop ? static_cast<uint32_t>(d->num_cus) : items;
             StageInput& in = a.in;
             if (s == 0 && l == 0) {  // embedding -> attention norm
                 in = stage_input(d, kInEmbed, H, nullptr, d->d_xa, nw[VX_NORM_ATTN]);
