@@ -157,6 +157,11 @@ __device__ __forceinline__ float proj_post(const ProjOut& o, bool* zero) {
     *zero = !(as > 0.0f);
     return *zero ? 0.0f : o.ws / as;
 }
+// The same with the activation scale already loaded.
+__device__ __forceinline__ float proj_post(const ProjOut& o, float as, bool* zero) {
+    *zero = !(as > 0.0f);
+    return *zero ? 0.0f : o.ws / as;
+}
 __device__ __forceinline__ float proj_value(int32_t acc, float post, bool zero) {
     return zero ? 0.0f : static_cast<float>(acc) * post;
 }
@@ -199,6 +204,7 @@ struct InputRegs {
     int4 pa[SA > 0 ? SA : 1][P4];        // K-slice partials of a
     int4 pb[SB > 0 ? SB : 1][P4];        // K-slice partials of b
     float4 g[P4];                        // gamma
+    float as_a, as_b;                    // activation scales of a and b
 };
 
 struct __align__(16) InputLds {  // ys is accessed 16 bytes at a time
@@ -211,8 +217,9 @@ struct __align__(16) InputLds {  // ys is accessed 16 bytes at a time
 
 __device__ __forceinline__ uint32_t elem4(uint32_t tid, int k) { return 4u * (tid + static_cast<uint32_t>(k) * kNT); }
 
-// Issues every load of the thread's inputs (16 bytes each) without using any, so that the loads a kernel issues after
-// it (weights) do not delay them: vector-memory loads complete in issue order.
+// Issues every load of the thread's inputs (16 bytes each, and the producers' activation scales) without using any, so
+// that the loads a kernel issues after it (weights) do not delay them: vector-memory loads complete in issue order, so
+// a load issued after the weights would wait for all of them.
 template <int P4, int SA, int SB>
 __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA, SB>& r) {
     const uint32_t tid = threadIdx.x, n = p.n;
@@ -235,6 +242,7 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
     }
     if constexpr (SA > 0) {
         if (p.kind == kInResidual || p.kind == kInRelu2Mul) {
+            r.as_a = *p.a.as;
 #pragma unroll
             for (int s = 0; s < SA; ++s)
 #pragma unroll
@@ -247,6 +255,7 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
     }
     if constexpr (SB > 0) {
         if (p.kind == kInRelu2Mul) {
+            r.as_b = *p.b.as;
 #pragma unroll
             for (int s = 0; s < SB; ++s)
 #pragma unroll
@@ -264,6 +273,28 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
             r.g[k] = load_if(reinterpret_cast<const float4*>(p.gamma + i), i < n);
         }
     }
+}
+
+// Waits until the thread's input loads (and `extra`) have arrived: an empty asm reads one word folded from every loaded
+// register. (An asm that takes the registers themselves as in-out operands would pin them, and each conditional load
+// would then be copied into them under its own wait.)
+template <int P4, int SA, int SB>
+__device__ __forceinline__ void input_arrived(const InputRegs<P4, SA, SB>& r, uint32_t extra) {
+    uint32_t t = extra ^ f32_bits(r.as_a) ^ f32_bits(r.as_b);
+#pragma unroll
+    for (int k = 0; k < P4; ++k) {
+        t ^= r.x[k].x ^ r.x[k].y ^ r.x[k].z ^ r.x[k].w;
+        t ^= f32_bits(r.g[k].x) ^ f32_bits(r.g[k].y) ^ f32_bits(r.g[k].z) ^ f32_bits(r.g[k].w);
+        if constexpr (SA > 0) {
+#pragma unroll
+            for (int s = 0; s < SA; ++s) t ^= r.pa[s][k].x ^ r.pa[s][k].y ^ r.pa[s][k].z ^ r.pa[s][k].w;
+        }
+        if constexpr (SB > 0) {
+#pragma unroll
+            for (int s = 0; s < SB; ++s) t ^= r.pb[s][k].x ^ r.pb[s][k].y ^ r.pb[s][k].z ^ r.pb[s][k].w;
+        }
+    }
+    asm volatile("" : : "v"(t) : "memory");
 }
 
 template <int P4, int SA>
@@ -300,7 +331,7 @@ __device__ __forceinline__ void stage_y(const StageInput& p, const InputRegs<P4,
         }
     } else if (SA > 0 && SB > 0 && p.kind == kInRelu2Mul) {
         bool za, zb;
-        const float pa = proj_post(p.a, &za), pb = proj_post(p.b, &zb);
+        const float pa = proj_post(p.a, r.as_a, &za), pb = proj_post(p.b, r.as_b, &zb);
 #pragma unroll
         for (int k = 0; k < P4; ++k) {
             int32_t sa[4], sb[4];
@@ -324,7 +355,7 @@ __device__ __forceinline__ void stage_y(const StageInput& p, const InputRegs<P4,
         }
         if (SA > 0 && p.kind == kInResidual) {
             bool za;
-            const float pa = proj_post(p.a, &za);
+            const float pa = proj_post(p.a, r.as_a, &za);
 #pragma unroll
             for (int k = 0; k < P4; ++k) {
                 int32_t sa[4];
@@ -560,12 +591,12 @@ __constant__ DigitTable g_digits = make_digit_table();
 // the weights are in flight; a looping workgroup loads the next item's chunks as the current ones are consumed. The
 // digit-nibble table and the arithmetic are those of the lone GEMV (vx_gemv.hip). Only the entries of the item's own
 // chunks are staged.
-template <int P4, int SA, int SB>
+template <int P4, int SA, int SB, bool MULTI>
 __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of the digit nibbles of byte B (first half)
     __shared__ uint2 st[kStChunks * 16];
     __shared__ InputLds s;
-    __shared__ int red[2][2][kNT / 64][64];  // [item parity][gate, up][wave][lane]
+    __shared__ int red[MULTI ? 2 : 1][MULTI ? 2 : 1][kNT / 64][64];  // [item parity][gate, up][wave][lane]
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -599,22 +630,26 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
         const uint32_t T = min(static_cast<uint32_t>(kTileGroup), it.jb.n_tiles - grp * kTileGroup);
         it.q0 = it.ks * it.jb.slice_chunks;
         it.nq = min(it.jb.slice_chunks, it.jb.n_chunks - it.q0);
-        const uint32_t nl = it.jb.w2 != nullptr ? 2u * it.nq : it.nq;  // gate chunks, then (pair) up chunks
+        const uint32_t nl = MULTI && it.jb.w2 != nullptr ? 2u * it.nq : it.nq;  // gate chunks, then (pair) up chunks
         it.cnt = wave < nl ? (nl - wave + kTileGroup - 1) / kTileGroup : 0u;
         const size_t tile_off = (static_cast<size_t>(grp) * kTileGroup * it.jb.n_chunks + tt) * 64u + lane;
         it.wp = (const g_u4*)(it.jb.w) + tile_off;
-        it.wp2 = it.jb.w2 != nullptr ? (const g_u4*)(it.jb.w2) + tile_off : it.wp;
+        it.wp2 = MULTI && it.jb.w2 != nullptr ? (const g_u4*)(it.jb.w2) + tile_off : it.wp;
         it.cs = static_cast<size_t>(T) * 64u;
         return it;
     };
     auto chunk_load = [&](const Item& it, int i) {
         const uint32_t c = wave + kTileGroup * static_cast<uint32_t>(i);
-        const bool up = c >= it.nq;
+        const bool up = MULTI && c >= it.nq;
         return __builtin_nontemporal_load((up ? it.wp2 : it.wp) + (it.q0 + (up ? c - it.nq : c)) * it.cs);
     };
 
     uint32_t item = blockIdx.x;
     Item it = locate(item);
+    // The weight loads go out once the input and the digit table have arrived: a load issued under a runtime condition
+    // (the wave's chunk count) leaves the compiler unsure how many loads follow an earlier one, so any wait for the input
+    // after them would also wait for most of the weights.
+    input_arrived(r, dig[0] ^ dig[1]);
     u32x4 b[kDPer];
 #pragma unroll
     for (int i = 0; i < kDPer; ++i)
@@ -641,20 +676,22 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     stage_quant(y, s, mx, a.in.n, a.tbr, c0, (it.q0 + it.nq) * 16u, lo, st, &act_scale, &act_sum);
     if (blockIdx.x == 0 && tid == 0) *a.as_out = act_scale;
 
-    for (uint32_t parity = 0;; parity ^= 1u) {
-        const uint32_t next = a.loop ? item + gridDim.x : a.total_items;
-        const bool more = next < a.total_items;
+    // One item: its chunks from b (refilled with the chunks of the workgroup's next item, `refill`, as they are
+    // consumed), the slice sums reduced in LDS (parity selects the buffer) and stored by wave 0. Returns the next item.
+    auto process = [&](const Item& it, uint32_t parity, uint32_t refill) {
+        const bool more = MULTI && a.loop && refill < a.total_items;
         Item nt{};
-        if (more) nt = locate(next);
-        const bool pair = it.jb.w2 != nullptr;
+        if (more) nt = locate(refill);
+        const bool pair = MULTI && it.jb.w2 != nullptr;
         int acc_lo = 0, acc_hi = 0, acc2_lo = 0, acc2_hi = 0;
 #pragma unroll
         for (int i = 0; i < kDPer; ++i) {
+            u32x4& bi = b[i];
             if (static_cast<uint32_t>(i) < it.cnt) {
                 const uint32_t c = wave + kTileGroup * i;
                 const bool up = pair && c >= it.nq;
                 const uint32_t q = up ? c - it.nq : c;  // chunk of the slice
-                const uint32_t dw[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
+                const uint32_t dw[4] = {bi.x, bi.y, bi.z, bi.w};
                 const uint2 e = st[q * 16u + (lane & 15u)];
                 __builtin_amdgcn_sched_barrier(0);
                 uint32_t t[16];
@@ -663,8 +700,8 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
                     const uint32_t addr = __builtin_amdgcn_perm(dw[k >> 2], lane_off, 0x0c0c0000u | ((4u + (k & 3)) << 8));
                     t[k] = *reinterpret_cast<const uint32_t*>(tabb + addr);
                 }
-                // b[i] is free: the next item's chunk i goes into it while this one is summed
-                if (more && static_cast<uint32_t>(i) < nt.cnt) b[i] = chunk_load(nt, i);
+                // the register is free: the next item's chunk goes into it while this one is summed
+                if (more && static_cast<uint32_t>(i) < nt.cnt) bi = chunk_load(nt, i);
                 if (!pair) {
                     dot4_bcast<0>(acc_lo, acc_hi, e.x, e.y, t[0], t[1], t[2], t[3]);
                     dot4_bcast<4>(acc_lo, acc_hi, e.x, e.y, t[4], t[5], t[6], t[7]);
@@ -685,11 +722,11 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
                     }
                 }
             } else if (more && static_cast<uint32_t>(i) < nt.cnt) {
-                b[i] = chunk_load(nt, i);
+                bi = chunk_load(nt, i);
             }
         }
         red[parity][0][wave][lane] = acc_lo + 16 * acc_hi;
-        if (pair) red[parity][1][wave][lane] = acc2_lo + 16 * acc2_hi;
+        if (pair) red[parity][MULTI ? 1 : 0][wave][lane] = acc2_lo + 16 * acc2_hi;
         // One barrier per item: the next item writes the other parity, and the one after this parity only after the
         // next item's barrier, which wave 0 reaches once it has read these sums.
         __syncthreads();
@@ -707,7 +744,7 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
             } else {
                 int v2 = 0;
 #pragma unroll
-                for (int w = 0; w < kNT / 64; ++w) v2 += red[parity][1][w][lane];
+                for (int w = 0; w < kNT / 64; ++w) v2 += red[parity][MULTI ? 1 : 0][w][lane];
                 v2 += 8 * jb.dsum2[row] - act_sum;
                 // the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170
                 const bool zero = !(act_scale > 0.0f);
@@ -727,7 +764,13 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
                 if (row < jb.rows) jb.act_out[row] = o;
             }
         }
-        if (!more) break;
+        return nt;
+    };
+    // Items item, item + gridDim.x, ... (one unless the stage loops).
+    for (uint32_t parity = 0;; parity ^= 1u) {
+        const uint32_t next = item + gridDim.x;
+        const Item nt = process(it, parity, next);
+        if (!(MULTI && a.loop && next < a.total_items)) break;
         item = next;
         it = nt;
     }
@@ -1188,11 +1231,26 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
 // embedding inputs of up to kPlainMax elements without a norm (the SwiGLU output of a model without sub-norms).
 enum DVariant : uint32_t { kDv4K = 0, kDv8K = 1, kDvPlain = 2 };
 
+// MULTI: the instance that loops over items and runs gated pairs; the others take one plain item per workgroup.
 int launch_dgemv(const DStageArgs& a, hipStream_t s) {
+    const bool multi = a.loop || a.job[0].w2 != nullptr;
     switch (a.variant) {
-        case kDv4K: hipLaunchKernelGGL((dgemv_kernel<1, kMaxSlicesA, kMaxSlicesB>), dim3(a.grid), dim3(kNT), 0, s, a); break;
-        case kDv8K: hipLaunchKernelGGL((dgemv_kernel<2, kMaxSlicesA, kMaxSlicesB>), dim3(a.grid), dim3(kNT), 0, s, a); break;
-        default: hipLaunchKernelGGL((dgemv_kernel<kPlainMax / (4 * kNT), 0, 0>), dim3(a.grid), dim3(kNT), 0, s, a); break;
+        case kDv4K:
+            if (multi)
+                hipLaunchKernelGGL((dgemv_kernel<1, kMaxSlicesA, kMaxSlicesB, true>), dim3(a.grid), dim3(kNT), 0, s, a);
+            else
+                hipLaunchKernelGGL((dgemv_kernel<1, kMaxSlicesA, kMaxSlicesB, false>), dim3(a.grid), dim3(kNT), 0, s, a);
+            break;
+        case kDv8K:
+            if (multi)
+                hipLaunchKernelGGL((dgemv_kernel<2, kMaxSlicesA, kMaxSlicesB, true>), dim3(a.grid), dim3(kNT), 0, s, a);
+            else
+                hipLaunchKernelGGL((dgemv_kernel<2, kMaxSlicesA, kMaxSlicesB, false>), dim3(a.grid), dim3(kNT), 0, s, a);
+            break;
+        default:  // a wide plain input is a down projection's, split into several K slices: one item per workgroup
+            if (multi) VX_FAIL(VX_ERR_INTERNAL, "a looping stage with a %u-element input", a.in.n);
+            hipLaunchKernelGGL((dgemv_kernel<kPlainMax / (4 * kNT), 0, 0, false>), dim3(a.grid), dim3(kNT), 0, s, a);
+            break;
     }
     VX_HIP(hipGetLastError());
     return VX_OK;

@@ -260,3 +260,28 @@ def test_bitnet2b_greedy_golden(torch_dev, oracle):
         assert first_bad is None, f"token {first_bad} differs: {got[first_bad]} vs {gold['tokens'][first_bad]}"
     finally:
         dec.close()
+
+
+def test_falcon3_10b_golden_logits_every_position(torch_dev, oracle):
+    """A random-init Falcon3-10B-shaped model (BASELINE.json configs[1] shapes, Falcon3 architecture) against the
+    committed oracle run (tests/golden/falcon3_10b_greedy.json, written by tests/golden/make_falcon3_golden.py): at each
+    of the 319 positions the sum of the bit patterns of all 131072 logits equals the oracle's (teacher forced with the
+    oracle's tokens), and greedy generation reproduces its 256 tokens."""
+    with open(os.path.join(HERE, "golden", "falcon3_10b_greedy.json")) as f:
+        gold = json.load(f)
+    model = oracle.Model(oracle.falcon3_10b(gold["max_ctx"]), gold["seed"])
+    dec = load_decoder(oracle, model)
+    model.close()
+    try:
+        feed = list(gold["prompt"]) + list(gold["tokens"][:-1])
+        for pos, want in enumerate(gold["logits_f32_bits_sums"]):
+            logits, nxt = dec.step(feed[pos], pos)
+            got = int(logits.view(np.uint32).astype(np.uint64).sum())
+            assert got == want, f"logits at position {pos} differ (bit sum {got} vs {want})"
+            if pos == 0:
+                np.testing.assert_array_equal(logits[:8], np.array(gold["logits_pos0_head"], np.float32))
+            if pos + 1 >= len(gold["prompt"]):
+                assert nxt == gold["tokens"][pos + 1 - len(gold["prompt"])], f"token after position {pos}"
+        assert dec.generate(gold["prompt"], len(gold["tokens"])) == gold["tokens"]
+    finally:
+        dec.close()
