@@ -99,6 +99,14 @@ def _declare(L: ctypes.CDLL) -> None:
         "vxo_model_reset": (None, [vp]),
         "vxo_model_forward": (ctypes.c_uint32, [vp, ctypes.c_uint32, sz, vp]),
         "vxo_model_generate": (None, [vp, vp, sz, sz, vp]),
+        # GGUF ternary decoders (gguf_oracle.c)
+        "vxo_i2s_unpack": (ctypes.c_int, [vp, sz, sz, vp]),
+        "vxo_i2s_pack": (ctypes.c_int, [vp, sz, sz, vp]),
+        "vxo_tq2_0_unpack": (None, [vp, sz, vp]),
+        "vxo_tq1_0_unpack": (None, [vp, sz, vp]),
+        "vxo_tq2_0_pack": (None, [vp, sz, ctypes.c_uint16, vp]),
+        "vxo_tq1_0_pack": (None, [vp, sz, ctypes.c_uint16, vp]),
+        "vxo_q2_0_unpack": (sz, [vp, sz, sz, sz, vp, vp]),
         "vxc_supported": (ctypes.c_int, []),
         "vxc_table_bytes": (sz, [sz]),
         "vxc_tile64": (None, [vp, sz, sz, vp]),
@@ -530,3 +538,53 @@ def gemv_avx512(tiles64_: np.ndarray, acts: np.ndarray, rows: int, cols: int, th
     scratch = np.empty(int(lib().vxc_table_bytes(cols)), np.int8)
     lib().vxc_gemv(_p(t), _p(a), rows, cols, _p(out), threads, _p(scratch))
     return out
+
+
+# ---- GGUF ternary decoders (gguf_oracle.c) -------------------------------------------------------------------------
+
+GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_Q8_0, GGML_TYPE_BF16 = 0, 1, 8, 30
+GGML_TYPE_TQ1_0, GGML_TYPE_TQ2_0, GGML_TYPE_I2_S, GGML_TYPE_Q2_0 = 34, 35, 36, 42
+
+
+def i2s_unpack(packed: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    p = np.ascontiguousarray(packed, np.uint8)
+    out = np.empty(rows * cols, np.int8)
+    if lib().vxo_i2s_unpack(_p(p), rows, cols, _p(out)) != 0:
+        raise ValueError("I2_S cols must be a multiple of 128")
+    return out.reshape(rows, cols)
+
+
+def i2s_pack(trits: np.ndarray) -> np.ndarray:
+    t = np.ascontiguousarray(trits, np.int8)
+    rows, cols = t.shape
+    out = np.empty(rows * cols // 4, np.uint8)
+    if lib().vxo_i2s_pack(_p(t), rows, cols, _p(out)) != 0:
+        raise ValueError("I2_S cols must be a multiple of 128")
+    return out
+
+
+def tq_unpack(ty: int, data: np.ndarray, n: int) -> np.ndarray:
+    """The n trits of TQ1_0 (34) or TQ2_0 (35) blocks."""
+    d = np.ascontiguousarray(data, np.uint8)
+    out = np.empty(n, np.int8)
+    (lib().vxo_tq1_0_unpack if ty == GGML_TYPE_TQ1_0 else lib().vxo_tq2_0_unpack)(_p(d), n // 256, _p(out))
+    return out
+
+
+def tq_pack(ty: int, trits: np.ndarray, d_bits: int = 0x3800) -> np.ndarray:
+    t = np.ascontiguousarray(trits, np.int8).reshape(-1)
+    nb = t.size // 256
+    out = np.empty(nb * (54 if ty == GGML_TYPE_TQ1_0 else 66), np.uint8)
+    (lib().vxo_tq1_0_pack if ty == GGML_TYPE_TQ1_0 else lib().vxo_tq2_0_pack)(_p(t), nb, d_bits, _p(out))
+    return out
+
+
+def q2_0_unpack(data: np.ndarray, rows: int, cols: int, block_size: int = 64):
+    """(trits rows x cols, f16 scale bits per 64 weights); raises on a code 3 weight."""
+    d = np.ascontiguousarray(data, np.uint8)
+    trits = np.empty(rows * cols, np.int8)
+    scales = np.empty(rows * cols // 64, np.uint16)
+    bad = lib().vxo_q2_0_unpack(_p(d), rows, cols, block_size, _p(trits), _p(scales))
+    if bad:
+        raise ValueError(f"Q2_0 weight {bad - 1} uses code 3")
+    return trits.reshape(rows, cols), scales
