@@ -348,6 +348,80 @@ int vx_decoder_generate(vx_decoder_t* decoder, const uint32_t* prompt, size_t n_
 int vx_decoder_memory_bytes(const vx_decoder_t* decoder, size_t* out_bytes);
 int vx_decoder_free(vx_decoder_t* decoder);
 
+/* ---- GGUF files ------------------------------------------------------------------------------------------------------
+ * The format level of the reference's C API (quintrit-c/include/quintrit.h:221-308, over quintrit-format/src/gguf.rs):
+ * an open, memory-mapped GGUF v2/v3 file, checked like the reference's reader (every count and length bounded by the
+ * file, offsets aligned and inside the data section, payloads not overlapping; violations give VX_ERR_FORMAT). Names
+ * and payload pointers stay valid until vx_gguf_close. Ternary tensors (I2_S, TQ1_0, TQ2_0) convert to the planar
+ * velurex layout on the host, or upload in their GGUF size and convert in HBM into a GEMV matrix. */
+typedef struct vx_gguf vx_gguf_t;
+
+#define VX_MAX_DIMS 8
+#define VX_GGML_F32    0
+#define VX_GGML_F16    1
+#define VX_GGML_Q8_0   8
+#define VX_GGML_BF16   30
+#define VX_GGML_TQ1_0  34
+#define VX_GGML_TQ2_0  35
+#define VX_GGML_I2_S   36
+#define VX_GGML_Q2_0   42
+
+typedef struct vx_gguf_info {
+    uint32_t struct_size;     /* sizeof(vx_gguf_info_t) */
+    uint32_t version;         /* 2 or 3 */
+    uint64_t tensor_count;
+    uint64_t metadata_count;
+    uint64_t data_offset;     /* absolute file offset of the tensor data section */
+} vx_gguf_info_t;
+
+typedef struct vx_tensor_info {
+    uint32_t    struct_size;  /* sizeof(vx_tensor_info_t) */
+    int32_t     ggml_type;    /* VX_GGML_* */
+    uint32_t    n_dims;
+    int32_t     is_ternary;   /* 1 for I2_S, TQ1_0 and TQ2_0, which convert to velurex weights */
+    uint64_t    shape[VX_MAX_DIMS]; /* as stored: shape[0] is the innermost dimension (a matrix is [cols, rows]) */
+    uint64_t    num_elements;
+    uint64_t    offset;       /* offset inside the data section */
+    uint64_t    data_bytes;   /* payload bytes; 0 for types whose layout is not known here */
+    const char* name;         /* valid until vx_gguf_close */
+    const char* type_name;    /* "F32", "F16", "Q8_0", "BF16", "TQ1_0", "TQ2_0", "I2_S", "Q2_0" or "UNKNOWN" */
+    uint32_t    block_size;   /* Q2_0: weights per block (64 or 128, read from the layout, gguf.rs:460-508); else 0 */
+} vx_tensor_info_t;
+
+/* quintrit_gguf_open / _close / _info (quintrit.h:260-269). A file that cannot be opened gives VX_ERR_IO. */
+int vx_gguf_open(const char* path, vx_gguf_t** out_gguf);
+int vx_gguf_close(vx_gguf_t* gguf);
+int vx_gguf_info(const vx_gguf_t* gguf, vx_gguf_info_t* out_info);
+/* Tensor `index` in [0, tensor_count), in file order; or by name (VX_ERR_NOT_FOUND). (quintrit.h:271-275) */
+int vx_gguf_tensor_at(const vx_gguf_t* gguf, size_t index, vx_tensor_info_t* out_info);
+int vx_gguf_tensor_find(const vx_gguf_t* gguf, const char* name, vx_tensor_info_t* out_info);
+/* Metadata (quintrit.h:277-285): a string (*out_len without the NUL; BUFFER_TOO_SMALL if capacity <= *out_len), an
+ * unsigned or non-negative integer, a float (f32 widened or f64), and every entry as one JSON object
+ * {"key": {"type": t, ["array_type": a,] "value": v}} with exact floats (f32 widened to double, 17 digits). */
+int vx_gguf_metadata_string(const vx_gguf_t* gguf, const char* key, char* buffer, size_t capacity, size_t* out_len);
+int vx_gguf_metadata_u64(const vx_gguf_t* gguf, const char* key, uint64_t* out_value);
+int vx_gguf_metadata_f64(const vx_gguf_t* gguf, const char* key, double* out_value);
+int vx_gguf_metadata_json(const vx_gguf_t* gguf, char* buffer, size_t capacity, size_t* out_len);
+/* The raw payload inside the mapping (quintrit.h:287-289); VX_ERR_UNSUPPORTED for a type of unknown layout. */
+int vx_gguf_tensor_data(const vx_gguf_t* gguf, const char* name, const uint8_t** out_data, size_t* out_len);
+/* The per-tensor weight scale (gguf.rs:342-360, transcoder.rs:224-236): the f32 after an I2_S payload, the common
+ * block scale of TQ1_0 / TQ2_0 (VX_ERR_FORMAT if the blocks differ), 1 for other types. */
+int vx_gguf_tensor_scale(const vx_gguf_t* gguf, const char* name, float* out_scale);
+/* A ternary 2-D tensor in the planar velurex layout in the caller's buffer (transcoder.rs:154-205); out_rows, out_cols
+ * and out_scale may be NULL. The counterpart of quintrit_gguf_convert_tensor for the GPU's layout. */
+int vx_gguf_convert_planar(const vx_gguf_t* gguf, const char* name, uint8_t* out, size_t out_capacity, size_t* out_rows,
+                           size_t* out_cols, float* out_scale);
+/* The same for a raw payload in host memory: rows x cols weights of ggml_type (I2_S: cols a multiple of 128; TQ1_0 and
+ * TQ2_0: rows * cols a multiple of 256). */
+int vx_ggml_to_planar(int32_t ggml_type, const uint8_t* data, size_t len, size_t rows, size_t cols, uint8_t* out,
+                      size_t out_capacity);
+/* A GEMV matrix from a ternary tensor: its payload crosses to the device in its GGUF size and is converted there, with
+ * the tensor's weight scale (transcoder.rs:211-249 for the GPU). */
+int vx_gguf_upload_matrix(const vx_gguf_t* gguf, const char* name, vx_matrix_t** out_matrix);
+/* The same from a raw payload already in device memory. */
+int vx_matrix_create_ggml_dev(int32_t ggml_type, const uint8_t* data_dev, size_t len, size_t rows, size_t cols,
+                              float weight_scale, vx_matrix_t** out_matrix);
+
 /* glibc's expf (the reference's f32::exp) evaluated on the device, as used by the attention softmax: n values. */
 int vx_expf_dev(const float* x, size_t n, float* out, void* stream);
 

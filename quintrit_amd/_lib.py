@@ -86,6 +86,21 @@ SIGNATURES = {
     "vx_decoder_memory_bytes": (_i32, [_vp, _vp]),
     "vx_decoder_free": (_i32, [_vp]),
     "vx_expf_dev": (_i32, [_vp, _sz, _vp, _vp]),
+    "vx_gguf_open": (_i32, [ctypes.c_char_p, _vp]),
+    "vx_gguf_close": (_i32, [_vp]),
+    "vx_gguf_info": (_i32, [_vp, _vp]),
+    "vx_gguf_tensor_at": (_i32, [_vp, _sz, _vp]),
+    "vx_gguf_tensor_find": (_i32, [_vp, ctypes.c_char_p, _vp]),
+    "vx_gguf_metadata_string": (_i32, [_vp, ctypes.c_char_p, _vp, _sz, _vp]),
+    "vx_gguf_metadata_u64": (_i32, [_vp, ctypes.c_char_p, _vp]),
+    "vx_gguf_metadata_f64": (_i32, [_vp, ctypes.c_char_p, _vp]),
+    "vx_gguf_metadata_json": (_i32, [_vp, _vp, _sz, _vp]),
+    "vx_gguf_tensor_data": (_i32, [_vp, ctypes.c_char_p, _vp, _vp]),
+    "vx_gguf_tensor_scale": (_i32, [_vp, ctypes.c_char_p, _vp]),
+    "vx_gguf_convert_planar": (_i32, [_vp, ctypes.c_char_p, _vp, _sz, _vp, _vp, _vp]),
+    "vx_ggml_to_planar": (_i32, [ctypes.c_int32, _vp, _sz, _sz, _sz, _vp, _sz]),
+    "vx_gguf_upload_matrix": (_i32, [_vp, ctypes.c_char_p, _vp]),
+    "vx_matrix_create_ggml_dev": (_i32, [ctypes.c_int32, _vp, _sz, _sz, _sz, _f32, _vp]),
 }
 
 

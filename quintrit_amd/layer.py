@@ -32,6 +32,16 @@ class VelurexHipLayer:
         self._rows = rows
         self._cols = cols
 
+    @classmethod
+    def _from_handle(cls, handle: ctypes.c_void_p) -> "VelurexHipLayer":
+        """Takes ownership of a matrix handle created elsewhere (vx_gguf_upload_matrix, vx_matrix_create_ggml_dev)."""
+        self = cls.__new__(cls)
+        self._h = handle
+        r, c = ctypes.c_size_t(), ctypes.c_size_t()
+        _lib.check(_lib.lib().vx_matrix_shape(handle, ctypes.byref(r), ctypes.byref(c)))
+        self._rows, self._cols = r.value, c.value
+        return self
+
     def close(self) -> None:
         if self._h:
             _lib.check(_lib.lib().vx_matrix_free(self._h))
