@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU-baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
-    ap.add_argument("--workload", choices=["stream", "gemm", "q2", "decode"], default="stream",
+    ap.add_argument("--workload", choices=["stream", "gemm", "q2", "decode", "gguf"], default="stream",
                     help="stream: the driver's line (configs[1]); gemm: the batched GEMM of configs[2]; q2: the "
                          "block-scaled GEMV stream of configs[4]; decode: bs=1 greedy decode of configs[3]")
     ap.add_argument("--decode-new", type=int, default=256, help="decode mode: generated tokens per run")
@@ -638,6 +638,113 @@ def decode_bench(torch, args) -> int:
     return 0
 
 
+FALCON3_LAYER = [("q", 3072, 3072), ("k", 1024, 3072), ("v", 1024, 3072), ("o", 3072, 3072), ("gate", 23040, 3072),
+                 ("up", 23040, 3072), ("down", 3072, 23040)]
+
+
+def gguf_bench(torch, args) -> int:
+    """GGUF -> velurex transcoding (SURVEY.md's next row after the decode step): the seven ternary tensors of one
+    Falcon3-10B layer (237.5 Mweights) in I2_S, TQ1_0 and TQ2_0. Reported per type: the device-side conversion of a
+    payload resident in HBM into a GEMV matrix (vx_matrix_create_ggml_dev: payload -> planar -> device layout + row
+    digit sums), the whole upload of a GGUF file (open, mmap, PCIe copy of the payload, conversion), and the host
+    conversion to planar bytes (vx_ggml_to_planar, one thread per core). The CPU baseline is the oracle's restatement of
+    the reference's decoders and packer (decode the trits, pack_matrix), single-threaded as a scalar port."""
+    import ctypes as ct
+    import tempfile
+
+    import numpy as np
+    from oracle import oracle
+    from quintrit_amd._lib import check, lib
+    from quintrit_amd.gguf import GgufFile, ggml_to_planar
+    from quintrit_amd.layer import VelurexHipLayer
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests"))
+    from gguf_writer import build
+
+    rng = np.random.default_rng(0x6606)
+    weights = sum(r * c for _, r, c in FALCON3_LAYER)
+    results = {}
+    tmp = tempfile.mkdtemp()
+    trits = {name: rng.integers(-1, 2, (r, c)).astype(np.int8) for name, r, c in FALCON3_LAYER}
+    for ty, tname in ((36, "I2_S"), (34, "TQ1_0"), (35, "TQ2_0")):
+        pay = {name: (oracle.i2s_pack(t) if ty == 36 else oracle.tq_pack(ty, t.reshape(-1))) for name, t in trits.items()}
+        nbytes = sum(p.size for p in pay.values())
+        dev = {name: torch.from_numpy(p).cuda() for name, p in pay.items()}
+        torch.cuda.synchronize()
+
+        def device_side():
+            ms = []
+            for name, r, c in FALCON3_LAYER:
+                h = ct.c_void_p()
+                check(lib().vx_matrix_create_ggml_dev(ty, ct.c_void_p(dev[name].data_ptr()), dev[name].numel(), r, c,
+                                                      ct.c_float(1.0), ct.byref(h)))
+                ms.append(VelurexHipLayer._from_handle(h))
+            for m in ms:
+                m.close()
+        device_side()
+        reps = max(2, args.steps // 10)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            device_side()
+        torch.cuda.synchronize()
+        dt_dev = (time.perf_counter() - t0) / reps
+        path = os.path.join(tmp, f"layer_{tname}.gguf")
+        with open(path, "wb") as f:
+            f.write(build([("general.architecture", 8, "falcon3")],
+                          [(f"blk.0.{name}.weight", [c, r], ty,
+                            pay[name].tobytes() + (np.float32(0.02).tobytes() if ty == 36 else b""))
+                           for name, r, c in FALCON3_LAYER]))
+        t0 = time.perf_counter()
+        with GgufFile(path) as g:
+            ms = [g.upload_matrix(f"blk.0.{name}.weight") for name, _, _ in FALCON3_LAYER]
+            torch.cuda.synchronize()
+            dt_file = time.perf_counter() - t0
+            for m in ms:
+                m.close()
+        os.remove(path)
+        t0 = time.perf_counter()
+        for name, r, c in FALCON3_LAYER:
+            ggml_to_planar(ty, pay[name], r, c)
+        dt_host = time.perf_counter() - t0
+        results[tname] = {
+            "payload_bytes": nbytes, "device_ms": round(dt_dev * 1e3, 3),
+            "device_GBps": round(nbytes / dt_dev / 1e9, 1), "device_Gweights_s": round(weights / dt_dev / 1e9, 1),
+            "file_upload_ms": round(dt_file * 1e3, 2), "file_upload_GBps": round(nbytes / dt_file / 1e9, 2),
+            "host_ms": round(dt_host * 1e3, 1), "host_GBps": round(nbytes / dt_host / 1e9, 2)}
+        log(f"{tname}: {nbytes / 1e6:.1f} MB payload; device {dt_dev * 1e3:.2f} ms ({nbytes / dt_dev / 1e9:.1f} GB/s), "
+            f"file upload {dt_file * 1e3:.1f} ms, host {dt_host * 1e3:.1f} ms")
+        del dev
+    cpu = None
+    if not args.no_cpu_baseline:
+        # the oracle's decode + pack_matrix on one thread over a bounded sample of the layer (the I2_S q, k, v, o)
+        t0, n = time.perf_counter(), 0
+        while True:
+            for name, r, c in FALCON3_LAYER[:4]:
+                p = oracle.i2s_pack(trits[name])
+                oracle.pack_matrix(oracle.i2s_unpack(p, r, c))
+                n += r * c
+            if time.perf_counter() - t0 > min(args.cpu_seconds, 8.0):
+                break
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(n / 4 / dt / 1e9, 3), "unit": "GB/s of I2_S payload", "cores": 1, "kind": "port",
+               "sample": f"{n / 1e6:.0f} Mweights of the layer's q/k/v/o in I2_S through the oracle's decoder and "
+                         f"pack_matrix, one thread, {dt:.1f} s (timing includes the oracle's I2_S re-encode)"}
+    head = results["I2_S"]
+    line = {
+        "metric": "GGUF ternary transcoding to the velurex device layout (Falcon3-10B layer shapes)",
+        "value": head["device_GBps"], "unit": "GB/s of I2_S payload", "n_gpus": 1, "steps": max(2, args.steps // 10),
+        "warmup": 1, "ms_per_step": head["device_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8", "data": "synthetic (random trits)",
+        "config": {"workload": "gguf transcoding: one Falcon3-10B layer (7 tensors, 237.5 Mweights)", "weights": weights},
+        "results": results, "cpu_baseline": cpu,
+        "roofline": {"bound": "hbm", "achieved": round((weights / 4 + weights / 5) / (head["device_ms"] / 1e3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round((weights / 4 + weights / 5) / (head["device_ms"] / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "kernel": "device-side matrix creation (conversion, check, layout, digit sums and allocations); "
+                               "bytes = I2_S payload read + planar written"}}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -665,6 +772,8 @@ def main():
         return q2_bench(torch, L, _lib, args)
     if args.workload == "decode":
         return decode_bench(torch, args)
+    if args.workload == "gguf":
+        return gguf_bench(torch, args)
     log(f"building the {args.layers}-layer weight stream on the GPU")
     st = Stream(torch, L, _lib, args.layers)
     log(f"{st.weights} weights, {st.alg_bytes / 1e9:.4f} GB algorithmic, {st.device_bytes / 1e9:.4f} GB device layout")

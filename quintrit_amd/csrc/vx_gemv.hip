@@ -125,15 +125,26 @@ __global__ void find_invalid_kernel(const uint8_t* __restrict__ planar, uint64_t
 }
 
 // One row per thread: the sum of the digits (t + 1) of the five trits of every device byte of the row, padding bytes
-// included (their activations are zero, staged as low nibble -8, so the correction 8 * dsum cancels them).
-__global__ void digit_sum_kernel(const uint8_t* __restrict__ w, uint32_t padded_rows, uint32_t n_tiles, uint32_t n_chunks,
-                                 int32_t* __restrict__ dsum) {
+// included (their activations are zero, staged as low nibble -8, so the correction 8 * dsum cancels them). A lane reads
+// its row's 16 bytes of a chunk at once (the 64 lanes of a wave read one contiguous KiB) and looks the byte sums up in
+// an LDS table.
+__global__ __launch_bounds__(256) void digit_sum_kernel(const uint8_t* __restrict__ w, uint32_t padded_rows,
+                                                        uint32_t n_tiles, uint32_t n_chunks, int32_t* __restrict__ dsum) {
+    __shared__ uint8_t tab[256];
+    {
+        const uint32_t e = digit_nibbles(static_cast<uint8_t>(threadIdx.x));
+        tab[threadIdx.x] = static_cast<uint8_t>((e & 15u) + ((e >> 4) & 15u) + ((e >> 8) & 15u) + ((e >> 12) & 15u) +
+                                                ((e >> 16) & 15u));
+    }
+    __syncthreads();
     const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= padded_rows) return;
     int s = 0;
-    for (uint32_t c = 0; c < n_chunks * kChunk; ++c) {
-        const uint32_t e = digit_nibbles(w[layout_offset(r, c, n_tiles, n_chunks)]);
-        s += static_cast<int>((e & 15u) + ((e >> 4) & 15u) + ((e >> 8) & 15u) + ((e >> 12) & 15u) + ((e >> 16) & 15u));
+    for (uint32_t q = 0; q < n_chunks; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4*>(w + layout_offset(r, q * kChunk, n_tiles, n_chunks));
+        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) s += tab[(d[k >> 2] >> (8 * (k & 3))) & 255u];
     }
     dsum[r] = s;
 }
