@@ -346,6 +346,9 @@ int vx_decoder_generate(vx_decoder_t* decoder, const uint32_t* prompt, size_t n_
                         uint32_t* out_tokens, size_t out_capacity);
 /* Device bytes held by the decoder (weights, KV cache, work buffers). */
 int vx_decoder_memory_bytes(const vx_decoder_t* decoder, size_t* out_bytes);
+/* The decoder's configuration (the shape part of quintrit_model_info, quintrit.h:323-340); out_config->struct_size must be
+ * sizeof(vx_decoder_config_t). */
+int vx_decoder_config(const vx_decoder_t* decoder, vx_decoder_config_t* out_config);
 int vx_decoder_free(vx_decoder_t* decoder);
 
 /* ---- GGUF files ------------------------------------------------------------------------------------------------------
@@ -421,6 +424,25 @@ int vx_gguf_upload_matrix(const vx_gguf_t* gguf, const char* name, vx_matrix_t**
 /* The same from a raw payload already in device memory. */
 int vx_matrix_create_ggml_dev(int32_t ggml_type, const uint8_t* data_dev, size_t len, size_t rows, size_t cols,
                               float weight_scale, vx_matrix_t** out_matrix);
+
+/* quintrit_gpu_options_t (quintrit.h:515-520). */
+typedef struct vx_gpu_options {
+    uint32_t struct_size;    /* sizeof(vx_gpu_options_t) */
+    uint32_t device_index;   /* GPU to use, below hipGetDeviceCount */
+    uint32_t context_length; /* largest context in tokens; 0 = min(4096, the model's maximum); at most 4096 */
+    uint32_t flags;          /* 0 */
+} vx_gpu_options_t;
+
+/* Replaces quintrit_model_open_gpu (quintrit.h:527; GpuModel::load, quintrit-runtime/src/gpu.rs:149-260): a GGUF model
+ * as a decoder on the GPU. The configuration comes from the metadata as ModelConfig::from_gguf reads it (config.rs:257-440;
+ * BitNet: ReLU^2, sub-norms, NEOX RoPE; Falcon3 / LLaMA: SiLU, Normal RoPE); the ternary projections (I2_S, TQ1_0,
+ * TQ2_0) are converted to planar velurex on the host and laid out in HBM; the embedding is the F16 token_embd.weight,
+ * the head output.weight (F16) or the embedding. The context is rounded down to a multiple of 256 as gpu.rs:141-146
+ * does. Files the reference rejects give VX_ERR_MODEL (missing or misshapen tensors, no tokenizer, absurd dimensions);
+ * models it runs elsewhere than this decoder give VX_ERR_UNSUPPORTED (no I2_S tensor, Q2_0, Qwen3 / hybrid / MoE,
+ * partial or scaled RoPE, head_dim other than 128 / 256). options may be NULL (device 0, default context). On failure
+ * *out_decoder is NULL. The handle is used and freed like one from vx_decoder_create. */
+int vx_decoder_open_gguf(const char* path, const vx_gpu_options_t* options, vx_decoder_t** out_decoder);
 
 /* glibc's expf (the reference's f32::exp) evaluated on the device, as used by the attention softmax: n values. */
 int vx_expf_dev(const float* x, size_t n, float* out, void* stream);

@@ -1887,6 +1887,18 @@ int vx_decoder_memory_bytes(const vx_decoder_t* d, size_t* out_bytes) {
     });
 }
 
+int vx_decoder_config(const vx_decoder_t* d, vx_decoder_config_t* out_config) {
+    return guard([&]() -> int {
+        VX_TRY(check_decoder(d));
+        if (out_config == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_config is NULL");
+        if (out_config->struct_size != sizeof(vx_decoder_config_t))
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "out_config->struct_size is %u, expected %zu", out_config->struct_size,
+                    sizeof(vx_decoder_config_t));
+        *out_config = d->cfg;
+        return VX_OK;
+    });
+}
+
 int vx_decoder_free(vx_decoder_t* d) {
     return guard([&]() -> int {
         if (d == nullptr) return VX_OK;

@@ -615,6 +615,218 @@ static int upload_ggml(uint32_t type, const uint8_t* data, bool data_on_device, 
     return st;
 }
 
+
+// ---- model loading (quintrit_model_open_gpu) ----------------------------------------------------------------------
+
+static const Meta* meta_get(const vx_gguf* g, const std::string& key) {
+    auto it = g->meta_idx.find(key);
+    return it == g->meta_idx.end() ? nullptr : &g->meta[it->second].second;
+}
+
+// GgufMetadataValue::as_usize (gguf.rs:90-104), and config.rs:502-507 scalar_or_max: an array gives its largest entry.
+static bool meta_usize(const Meta* m, bool or_max, uint64_t* out) {
+    if (m == nullptr) return false;
+    if (or_max && m->type == 9) {
+        bool any = false;
+        uint64_t best = 0, v;
+        for (const Meta& e : m->arr)
+            if (meta_u64(e, &v)) best = any ? std::max(best, v) : v, any = true;
+        *out = best;
+        return any;
+    }
+    return meta_u64(*m, out);
+}
+
+// GgufMetadataValue::as_f32 (gguf.rs:106-112): f32, or f64 narrowed.
+static bool meta_f32(const Meta* m, float* out) {
+    if (m == nullptr || (m->type != 6 && m->type != 12)) return false;
+    *out = static_cast<float>(m->f);
+    return true;
+}
+
+// The tensor names of a layer (quintrit-runtime/src/engine.rs:455-480), in the order of the projection / norm kinds.
+static const char* const kProjNames[7] = {"attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"};
+static const char* const kNormNames[4] = {"attn_norm", "attn_sub_norm", "ffn_norm", "ffn_sub_norm"};
+
+static const TensorRec* tensor_get(const vx_gguf* g, const std::string& name) {
+    auto it = g->tensor_idx.find(name);
+    return it == g->tensor_idx.end() ? nullptr : &g->tensors[it->second];
+}
+
+// ModelConfig::from_gguf (quintrit-runtime/src/config.rs:257-440) with validate_gguf_model's table checks
+// (validate.rs:199-240) and GpuModel::check_supported / context_for (gpu.rs:141-179), narrowed to what this decoder
+// runs. A file the reference rejects is VX_ERR_MODEL; a model it runs but not on this decoder is VX_ERR_UNSUPPORTED.
+static int gguf_decoder_config(const vx_gguf* g, uint32_t context_limit, vx_decoder_config_t* c) {
+    const Meta* am = meta_get(g, "general.architecture");
+    const std::string arch = am != nullptr && am->type == 8 ? am->s : "bitnet-b1.58";
+    auto key = [&](const char* k) { return meta_get(g, arch + "." + k); };
+    if (arch == "qwen3" || arch == "qwen35" || arch == "nemotron_h_moe")
+        VX_FAIL(VX_ERR_UNSUPPORTED, "architecture '%s' (query/key norms, hybrid or mixture-of-experts layers) is not "
+                "supported by this decoder", arch.c_str());
+    const bool bitnet = arch == "bitnet" || arch == "bitnet-b1.58";
+    uint64_t vocab = 0, hidden = 2560, ffn = 6912, layers = 30, heads = 20, kv_heads = 5, ctx = 4096, v;
+    const TensorRec* emb = tensor_get(g, "token_embd.weight");
+    const Meta* tokens = meta_get(g, "tokenizer.ggml.tokens");
+    if (meta_usize(key("vocab_size"), false, &v)) vocab = v;
+    else if (emb != nullptr && emb->n_dims > 1) vocab = emb->dims[1];
+    else if (tokens != nullptr && tokens->type == 9) vocab = tokens->arr.size();
+    else vocab = 128256;
+    if (meta_usize(key("embedding_length"), false, &v)) hidden = v;
+    if (meta_usize(key("feed_forward_length"), true, &v)) ffn = v;
+    if (meta_usize(key("block_count"), false, &v)) layers = v;
+    if (meta_usize(key("attention.head_count"), true, &v)) heads = v;
+    if (meta_usize(key("attention.head_count_kv"), true, &v)) kv_heads = v;
+    if (meta_usize(key("context_length"), false, &v)) ctx = v;
+    float eps = 1e-5f, theta = 500000.0f;
+    meta_f32(key("attention.layer_norm_rms_epsilon"), &eps);
+    meta_f32(key("rope.freq_base"), &theta);
+    const uint64_t dims[] = {vocab, hidden, ffn, layers, heads, kv_heads, ctx};
+    for (uint64_t d : dims)
+        if (d == 0 || d > (uint64_t{1} << 24)) VX_FAIL(VX_ERR_MODEL, "a model dimension of '%s' is 0 or absurd (%llu)", arch.c_str(),
+                                                       static_cast<unsigned long long>(d));
+    uint64_t head_dim = hidden / heads;
+    if (meta_usize(key("attention.key_length"), false, &v)) head_dim = v;
+    if (head_dim == 0 || head_dim % 2 || head_dim > 4096)
+        VX_FAIL(VX_ERR_MODEL, "metadata '%s.attention.key_length' = %llu must be even and in 2..=4096", arch.c_str(),
+                static_cast<unsigned long long>(head_dim));
+    uint64_t n_rot = head_dim;
+    if (meta_usize(key("rope.dimension_count"), false, &v)) n_rot = v;
+    if (n_rot == 0 || n_rot % 2 || n_rot > head_dim)
+        VX_FAIL(VX_ERR_MODEL, "metadata '%s.rope.dimension_count' = %llu must be even and at most the head dimension",
+                arch.c_str(), static_cast<unsigned long long>(n_rot));
+    if (n_rot != head_dim) VX_FAIL(VX_ERR_UNSUPPORTED, "partial RoPE (%llu of %llu dimensions) is not supported",
+                                   static_cast<unsigned long long>(n_rot), static_cast<unsigned long long>(head_dim));
+    const Meta* sc = key("rope.scaling.type");
+    const std::string scaling = sc != nullptr && sc->type == 8 ? sc->s : "none";
+    float factor = 0.0f;
+    meta_f32(key("rope.scaling.factor"), &factor);
+    if (scaling != "none" && scaling != "linear" && scaling != "yarn")
+        VX_FAIL(VX_ERR_MODEL, "RoPE scaling type '%s' is not supported", scaling.c_str());
+    if (scaling != "none" && !(scaling == "linear" && (factor == 0.0f || factor == 1.0f)))
+        VX_FAIL(VX_ERR_UNSUPPORTED, "RoPE scaling '%s' (factor %g) is not supported by this decoder", scaling.c_str(), factor);
+    // validate.rs:207-240: a tokenizer, and the F16 tables and F32 output norm of the declared sizes.
+    if (tokens == nullptr || tokens->type != 9 || tokens->arr.empty() || tokens->arr.size() > vocab)
+        VX_FAIL(VX_ERR_MODEL, "metadata 'tokenizer.ggml.tokens' is missing, empty or longer than the vocabulary (%llu)",
+                static_cast<unsigned long long>(vocab));
+    bool any_i2s = false;
+    for (const TensorRec& t : g->tensors) {
+        if (t.type == VX_GGML_Q2_0)
+            VX_FAIL(VX_ERR_UNSUPPORTED, "block-scaled (Q2_0) models run on the CPU only; the GPU decoder supports I2_S models");
+        any_i2s |= t.type == VX_GGML_I2_S;
+    }
+    if (!any_i2s)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "the GPU decoder reproduces the bitnet.cpp attention numerics only (I2_S models)");
+    for (const char* name : {"token_embd.weight", "output.weight"}) {
+        const TensorRec* t = tensor_get(g, name);
+        if (t == nullptr) {
+            if (std::strcmp(name, "output.weight") == 0) continue;
+            VX_FAIL(VX_ERR_MODEL, "tensor '%s' is missing", name);
+        }
+        if (t->type == VX_GGML_Q2_0 || t->type == VX_GGML_Q8_0)
+            VX_FAIL(VX_ERR_UNSUPPORTED, "%s is not F16; the GPU decoder needs an F16 embedding and head", name);
+        if (t->type != VX_GGML_F16) VX_FAIL(VX_ERR_MODEL, "tensor '%s' has type %u, expected F16", name, t->type);
+        if (t->n_elem != vocab * hidden)
+            VX_FAIL(VX_ERR_MODEL, "tensor '%s' has %llu elements, expected %llu", name, static_cast<unsigned long long>(t->n_elem),
+                    static_cast<unsigned long long>(vocab * hidden));
+    }
+    const TensorRec* on = tensor_get(g, "output_norm.weight");
+    if (on == nullptr || on->type != VX_GGML_F32 || on->n_elem != hidden)
+        VX_FAIL(VX_ERR_MODEL, "tensor 'output_norm.weight' is missing or not %llu F32 values", static_cast<unsigned long long>(hidden));
+    if (head_dim != 128 && head_dim != 256)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "head dimension %llu is not supported (128 or 256)", static_cast<unsigned long long>(head_dim));
+    // validate.rs:241-290: every layer's projections (ternary, of the configured shapes) and F32 norms.
+    const uint64_t qd = heads * head_dim, kvd = kv_heads * head_dim;
+    const uint64_t shape[7][2] = {{qd, hidden}, {kvd, hidden}, {kvd, hidden}, {hidden, qd},
+                                 {ffn, hidden}, {ffn, hidden}, {hidden, ffn}};
+    char name[96];
+    for (uint64_t l = 0; l < layers; ++l) {
+        for (uint32_t k = 0; k < 7; ++k) {
+            std::snprintf(name, sizeof name, "blk.%llu.%s.weight", static_cast<unsigned long long>(l), kProjNames[k]);
+            const TensorRec* t = tensor_get(g, name);
+            if (t == nullptr) VX_FAIL(VX_ERR_MODEL, "tensor '%s' is missing", name);
+            if (t->n_dims != 2 || t->dims[0] != shape[k][1] || t->dims[1] != shape[k][0])
+                VX_FAIL(VX_ERR_MODEL, "tensor '%s' has the wrong shape, expected [%llu, %llu]", name,
+                        static_cast<unsigned long long>(shape[k][1]), static_cast<unsigned long long>(shape[k][0]));
+            if (t->type != VX_GGML_I2_S && t->type != VX_GGML_TQ1_0 && t->type != VX_GGML_TQ2_0)
+                VX_FAIL(VX_ERR_MODEL, "tensor '%s' (type %u) is not a ternary tensor", name, t->type);
+            VX_TRY(check_ternary(t->type, static_cast<size_t>(t->byte_len), shape[k][0], shape[k][1]));
+            float scale;
+            VX_TRY(tensor_scale(g, *t, &scale));
+        }
+        for (uint32_t k = 0; k < 4; ++k) {
+            if ((k == VX_NORM_ATTN_SUB || k == VX_NORM_FFN_SUB) && !bitnet) continue;
+            std::snprintf(name, sizeof name, "blk.%llu.%s.weight", static_cast<unsigned long long>(l), kNormNames[k]);
+            const TensorRec* t = tensor_get(g, name);
+            // The attention sub-norm acts on the n_heads * head_dim attention output, the FFN sub-norm on the ffn-wide
+            // gated vector (attention.rs:230-240, model.rs:155-190).
+            // A sub-norm may hold more values than are used (validate.rs:253-256: at least q_dim / ffn).
+            const bool sub = k == VX_NORM_ATTN_SUB || k == VX_NORM_FFN_SUB;
+            const uint64_t n = k == VX_NORM_ATTN_SUB ? qd : k == VX_NORM_FFN_SUB ? ffn : hidden;
+            if (t == nullptr || t->type != VX_GGML_F32 || t->n_elem < n || (!sub && t->n_elem != n))
+                VX_FAIL(VX_ERR_MODEL, "tensor '%s' is missing or not %s%llu F32 values", name, sub ? "at least " : "",
+                        static_cast<unsigned long long>(n));
+        }
+    }
+    // gpu.rs:141-146: the model's maximum, at most 4096 (or the caller's limit), rounded down to a multiple of 256.
+    uint64_t want = std::min<uint64_t>(ctx, context_limit ? context_limit : 4096);
+    want = std::min<uint64_t>(want, 4096);
+    if (want >= 256) want = want / 256 * 256;
+    *c = vx_decoder_config_t{};
+    c->struct_size = sizeof(vx_decoder_config_t);
+    c->n_layers = static_cast<uint32_t>(layers);
+    c->hidden = static_cast<uint32_t>(hidden);
+    c->n_heads = static_cast<uint32_t>(heads);
+    c->n_kv_heads = static_cast<uint32_t>(kv_heads);
+    c->head_dim = static_cast<uint32_t>(head_dim);
+    c->ffn = static_cast<uint32_t>(ffn);
+    c->vocab = static_cast<uint32_t>(vocab);
+    c->max_ctx = static_cast<uint32_t>(want);
+    c->rms_eps = eps;
+    c->rope_theta = theta;
+    c->act = bitnet ? VX_ACT_RELU2 : VX_ACT_SILU;  // config.rs:419-422
+    // config.rs:464-467 (rope_from_gguf): NEOX for BitNet and Qwen2, Normal for Falcon3 / LLaMA.
+    c->rope_mode = bitnet || arch == "qwen2" ? VX_ROPE_NEOX : VX_ROPE_NORMAL;
+    c->no_sub_norm = bitnet ? 0 : 1;  // has_sub_norm (config.rs:424)
+    c->emb_f16 = 1;
+    c->untied = tensor_get(g, "output.weight") != nullptr ? 1 : 0;  // tie_word_embeddings (config.rs:425)
+    return VX_OK;
+}
+
+// GpuModel::load (gpu.rs:183-260): every projection converted to planar velurex on the host (gpu.rs:120-138), the F32
+// norms and the F16 tables handed to the decoder, which lays them out in HBM.
+// The tensors were checked by gguf_decoder_config.
+static int gguf_load_decoder(const vx_gguf* g, vx_decoder_t* d, const vx_decoder_config_t& c) {
+    std::vector<uint8_t> planar;
+    char name[96];
+    for (uint32_t l = 0; l < c.n_layers; ++l) {
+        for (uint32_t k = 0; k < 7; ++k) {
+            std::snprintf(name, sizeof name, "blk.%u.%s.weight", l, kProjNames[k]);
+            const TensorRec* t = tensor_get(g, name);
+            size_t rows, cols;
+            VX_TRY(matrix_shape(*t, &rows, &cols));
+            float scale;
+            VX_TRY(tensor_scale(g, *t, &scale));
+            planar.resize(rows * planar_row_bytes(cols));
+            host_to_planar(t->type, payload(g, *t), rows, cols, planar.data());
+            VX_TRY(vx_decoder_set_projection(d, l, k, planar.data(), planar.size(), scale));
+        }
+        for (uint32_t k = 0; k < 4; ++k) {
+            if ((k == VX_NORM_ATTN_SUB || k == VX_NORM_FFN_SUB) && c.no_sub_norm) continue;
+            std::snprintf(name, sizeof name, "blk.%u.%s.weight", l, kNormNames[k]);
+            const TensorRec* t = tensor_get(g, name);
+            const size_t n = k == VX_NORM_ATTN_SUB ? size_t{c.n_heads} * c.head_dim : k == VX_NORM_FFN_SUB ? c.ffn : c.hidden;
+            VX_TRY(vx_decoder_set_norm(d, l, k, reinterpret_cast<const float*>(payload(g, *t)), n));
+        }
+    }
+    const TensorRec* on = tensor_get(g, "output_norm.weight");
+    VX_TRY(vx_decoder_set_norm(d, c.n_layers, VX_NORM_ATTN, reinterpret_cast<const float*>(payload(g, *on)), c.hidden));
+    const size_t table = size_t{c.vocab} * c.hidden;
+    const TensorRec* emb = tensor_get(g, "token_embd.weight");
+    VX_TRY(vx_decoder_set_embedding_f16(d, reinterpret_cast<const uint16_t*>(payload(g, *emb)), table));
+    if (c.untied)
+        VX_TRY(vx_decoder_set_head(d, reinterpret_cast<const uint16_t*>(payload(g, *tensor_get(g, "output.weight"))), table));
+    return VX_OK;
+}
 }  // namespace vx
 
 extern "C" {
@@ -848,6 +1060,54 @@ int vx_gguf_upload_matrix(const vx_gguf_t* g, const char* name, vx_matrix_t** ou
         float scale;
         VX_TRY(tensor_scale(g, t, &scale));
         return upload_ggml(t.type, payload(g, t), false, static_cast<size_t>(t.byte_len), rows, cols, scale, out_matrix);
+    });
+}
+
+int vx_decoder_open_gguf(const char* path, const vx_gpu_options_t* options, vx_decoder_t** out_decoder) {
+    return guard([&]() -> int {
+        if (path == nullptr || out_decoder == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "path or out_decoder is NULL");
+        *out_decoder = nullptr;
+        vx_gpu_options_t o{};
+        if (options != nullptr) {
+            if (options->struct_size != sizeof(vx_gpu_options_t))
+                VX_FAIL(VX_ERR_INVALID_ARGUMENT, "options.struct_size is %u, expected %zu", options->struct_size, sizeof(vx_gpu_options_t));
+            o = *options;
+            if (o.flags != 0) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "options.flags has unknown bits set: %#x", o.flags);
+        }
+        // The file is checked before the device, as the reference does (quintrit-c/src/runtime.rs:312-330).
+        vx_gguf_t* g = nullptr;
+        VX_TRY(vx_gguf_open(path, &g));
+        vx_decoder_config_t c;
+        int st = gguf_decoder_config(g, o.context_length, &c);
+        int count = 0;
+        if (st == VX_OK && (hipGetDeviceCount(&count) != hipSuccess || count <= 0)) {
+            set_error(VX_ERR_UNSUPPORTED, "no GPU is visible");
+            st = VX_ERR_UNSUPPORTED;
+        } else if (st == VX_OK && o.device_index >= static_cast<uint32_t>(count)) {
+            set_error(VX_ERR_INVALID_ARGUMENT, "device " + std::to_string(o.device_index) + " does not exist");
+            st = VX_ERR_INVALID_ARGUMENT;
+        }
+        int prev = -1;
+        vx_decoder_t* d = nullptr;
+        if (st == VX_OK && (hipGetDevice(&prev) != hipSuccess || hipSetDevice(static_cast<int>(o.device_index)) != hipSuccess)) {
+            set_error(VX_ERR_DEVICE, "cannot make device " + std::to_string(o.device_index) + " current");
+            st = VX_ERR_DEVICE;
+        } else if (st == VX_OK) {
+            st = vx_decoder_create(&c, &d);
+            if (st == VX_OK) st = gguf_load_decoder(g, d, c);
+            (void)hipSetDevice(prev);
+        }
+        if (st != VX_OK) {
+            // The clean-up calls clear the error slot: keep the first failure's message.
+            const std::string msg = vx_last_error_message();
+            if (d != nullptr) vx_decoder_free(d);
+            vx_gguf_close(g);
+            set_error(st, msg);
+            return st;
+        }
+        vx_gguf_close(g);
+        *out_decoder = d;
+        return VX_OK;
     });
 }
 

@@ -158,3 +158,27 @@ class Decoder:
             self.close()
         except Exception:
             pass
+
+
+class GpuOptions(ctypes.Structure):
+    """vx_gpu_options_t (quintrit_gpu_options_t): device, context limit (0 = min(4096, the model's maximum)), flags."""
+    _fields_ = [("struct_size", ctypes.c_uint32), ("device_index", ctypes.c_uint32), ("context_length", ctypes.c_uint32),
+                ("flags", ctypes.c_uint32)]
+
+
+def open_gguf(path, context_length: int = 0, device_index: int = 0) -> Decoder:
+    """quintrit_model_open_gpu (quintrit.h:527): a GGUF model (I2_S BitNet / Falcon3 / LLaMA-style) as a Decoder, parsed,
+    checked and converted by vx_decoder_open_gguf."""
+    o = GpuOptions(ctypes.sizeof(GpuOptions), device_index, context_length, 0)
+    h = ctypes.c_void_p()
+    check(lib().vx_decoder_open_gguf(str(path).encode(), ctypes.byref(o), ctypes.byref(h)))
+    c = _Config()
+    c.struct_size = ctypes.sizeof(_Config)
+    st = lib().vx_decoder_config(h, ctypes.byref(c))
+    if st != 0:
+        lib().vx_decoder_free(h)
+        check(st)
+    dec = Decoder.__new__(Decoder)
+    dec.config = DecoderConfig(*(getattr(c, f) for f, _ in _Config._fields_[1:]))
+    dec.handle = h
+    return dec
