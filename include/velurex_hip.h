@@ -425,6 +425,16 @@ int vx_gguf_upload_matrix(const vx_gguf_t* gguf, const char* name, vx_matrix_t**
 int vx_matrix_create_ggml_dev(int32_t ggml_type, const uint8_t* data_dev, size_t len, size_t rows, size_t cols,
                               float weight_scale, vx_matrix_t** out_matrix);
 
+/* A Q2_0 tensor (block size 64 or 128, as detected) as the block-scaled layer's inputs (BlockScaledLayer::from_q2_0,
+ * quintrit-runtime/src/layer.rs:453-470, over decode_q2_0_packed, quintrit-format/src/decoders/q2_0.rs:58-155): planar
+ * velurex bytes (rows * ceil(cols/160) * 32) and one f16 scale per 64 weights of a row (rows * cols / 64; a 128-weight
+ * block's scale appears twice). A code 3 gives VX_ERR_FORMAT naming the first such weight. out_rows / out_cols may be
+ * NULL; they are set before a VX_ERR_BUFFER_TOO_SMALL. */
+int vx_gguf_convert_q2_0(const vx_gguf_t* gguf, const char* name, uint8_t* planar, size_t planar_capacity,
+                         uint16_t* scales_f16, size_t scales_capacity, size_t* out_rows, size_t* out_cols);
+/* The same tensor as a Q2_0 GEMV matrix (vx_q2_matrix_create's limits apply: cols a multiple of 64, at most 12288). */
+int vx_gguf_upload_q2_matrix(const vx_gguf_t* gguf, const char* name, vx_matrix_t** out_matrix);
+
 /* quintrit_gpu_options_t (quintrit.h:515-520). */
 typedef struct vx_gpu_options {
     uint32_t struct_size;    /* sizeof(vx_gpu_options_t) */

@@ -102,6 +102,8 @@ SIGNATURES = {
     "vx_gguf_convert_planar": (_i32, [_vp, ctypes.c_char_p, _vp, _sz, _vp, _vp, _vp]),
     "vx_ggml_to_planar": (_i32, [ctypes.c_int32, _vp, _sz, _sz, _sz, _vp, _sz]),
     "vx_gguf_upload_matrix": (_i32, [_vp, ctypes.c_char_p, _vp]),
+    "vx_gguf_convert_q2_0": (_i32, [_vp, ctypes.c_char_p, _vp, _sz, _vp, _sz, _vp, _vp]),
+    "vx_gguf_upload_q2_matrix": (_i32, [_vp, ctypes.c_char_p, _vp]),
     "vx_matrix_create_ggml_dev": (_i32, [ctypes.c_int32, _vp, _sz, _sz, _sz, _f32, _vp]),
 }
 
@@ -232,6 +234,12 @@ class Q2Matrix:
         check(lib().vx_q2_matrix_create(p.ctypes.data_as(ctypes.c_void_p), p.size, s.ctypes.data_as(ctypes.c_void_p),
                                         s.size, rows, cols, ctypes.byref(h)))
         self.handle, self.rows, self.cols = h, rows, cols
+
+    @classmethod
+    def _from_handle(cls, handle, rows: int, cols: int) -> "Q2Matrix":
+        m = cls.__new__(cls)
+        m.handle, m.rows, m.cols = handle, rows, cols
+        return m
 
     def gemv_f32(self, acts_dev, act_scales_dev, out_dev, stream_ptr) -> None:
         check(lib().vx_q2_gemv_f32_dev(self.handle, ctypes.c_void_p(acts_dev.data_ptr()), acts_dev.numel(),

@@ -37,6 +37,9 @@ __host__ __device__ inline int8_t code_trit(uint32_t code) {  // 0 -> -1, 1 -> 0
     return code == 3 ? 0 : static_cast<int8_t>(static_cast<int>(code) - 1);
 }
 
+// Internal type codes of Q2_0 payloads by block size (64 or 128 weights per f16 scale) for the trit gatherer.
+constexpr uint32_t kQ2Block64 = 0x10000u | VX_GGML_Q2_0, kQ2Block128 = 0x20000u | VX_GGML_Q2_0;
+
 // TQ1_0 digit n of byte q: ((q 3^n mod 256) 3) >> 8, minus 1 (decoders/tq1_0.rs:63-67).
 __host__ __device__ inline int8_t tq1_digit(uint32_t byte, uint32_t n) {
     const uint32_t p3 = n == 0 ? 1u : n == 1 ? 3u : n == 2 ? 9u : n == 3 ? 27u : 81u;
@@ -53,6 +56,14 @@ __host__ __device__ inline int8_t ggml_trit(uint32_t type, const uint8_t* src, u
         return code_trit((b >> (6 - 2 * (j >> 5))) & 3u);
     }
     const uint64_t e = r * cols + c;
+    if (type == kQ2Block64 || type == kQ2Block128) {
+        // decoders/q2_0.rs:32-57: an f16 scale, then the block's 2-bit codes four to a byte, low bits first (the codes
+        // were checked: no 3 reaches here)
+        const uint32_t bs = type == kQ2Block64 ? 64u : 128u;
+        const uint8_t* blk = src + (e / bs) * (2 + bs / 4);
+        const uint32_t o = static_cast<uint32_t>(e % bs);
+        return code_trit((blk[2 + o / 4] >> (2 * (o & 3u))) & 3u);
+    }
     const uint32_t i = static_cast<uint32_t>(e & (kQkTq - 1));
     if (type == VX_GGML_TQ2_0) {  // decoders/tq2_0.rs:69-73: element 128 g + 32 l + m at bits 2 l of byte 32 g + m
         const uint8_t* blk = src + (e / kQkTq) * kTq2Bytes;
@@ -616,6 +627,43 @@ static int upload_ggml(uint32_t type, const uint8_t* data, bool data_on_device, 
 }
 
 
+
+// decode_q2_0_packed (decoders/q2_0.rs:17-30,58-155) on the host: the planar velurex bytes of a Q2_0 tensor and one f16
+// scale per 64 weights of a row (a 128-weight block's scale twice). A code 3 is an error naming the first such weight.
+static int q2_0_convert(const vx_gguf* g, const TensorRec& t, std::vector<uint8_t>* planar, std::vector<uint16_t>* scales,
+                        size_t* rows_out, size_t* cols_out) {
+    size_t rows, cols;
+    VX_TRY(matrix_shape(t, &rows, &cols));
+    if (t.type != VX_GGML_Q2_0) VX_FAIL(VX_ERR_UNSUPPORTED, "tensor '%s' (type %u) is not Q2_0", t.name.c_str(), t.type);
+    const uint32_t bs = t.block_size;
+    if (bs != 64 && bs != 128) VX_FAIL(VX_ERR_FORMAT, "tensor '%s': Q2_0 block size %u is not supported (64 or 128)", t.name.c_str(), bs);
+    VX_TRY(check_shape(rows, cols));
+    if (cols % bs) VX_FAIL(VX_ERR_INVALID_SHAPE, "a Q2_0 row of %zu weights is not a multiple of the block size %u", cols, bs);
+    const size_t bb = 2 + bs / 4, nblk = rows * cols / bs;
+    if (t.byte_len != nblk * bb) VX_FAIL(VX_ERR_FORMAT, "tensor '%s': the payload is not %zu blocks of %zu bytes", t.name.c_str(), nblk, bb);
+    const uint8_t* src = payload(g, t);
+    for (size_t b = 0; b < nblk; ++b) {
+        const uint8_t* q = src + b * bb + 2;
+        for (uint32_t j = 0; j < bs / 4; ++j)
+            if (q[j] & (q[j] >> 1) & 0x55u) {
+                uint32_t k = 0;
+                while (((q[j] >> (2 * k)) & 3u) != 3u) ++k;
+                VX_FAIL(VX_ERR_FORMAT, "Q2_0 weight %zu uses code 3 (+2), which is not ternary", b * bs + 4 * j + k);
+            }
+    }
+    planar->resize(rows * planar_row_bytes(cols));
+    host_to_planar(bs == 64 ? kQ2Block64 : kQ2Block128, src, rows, cols, planar->data());
+    scales->resize(rows * cols / 64);
+    for (size_t b = 0; b < nblk; ++b) {
+        uint16_t d;
+        std::memcpy(&d, src + b * bb, 2);
+        for (uint32_t s = 0; s < bs / 64; ++s) (*scales)[b * (bs / 64) + s] = d;
+    }
+    *rows_out = rows;
+    *cols_out = cols;
+    return VX_OK;
+}
+
 // ---- model loading (quintrit_model_open_gpu) ----------------------------------------------------------------------
 
 static const Meta* meta_get(const vx_gguf* g, const std::string& key) {
@@ -1060,6 +1108,40 @@ int vx_gguf_upload_matrix(const vx_gguf_t* g, const char* name, vx_matrix_t** ou
         float scale;
         VX_TRY(tensor_scale(g, t, &scale));
         return upload_ggml(t.type, payload(g, t), false, static_cast<size_t>(t.byte_len), rows, cols, scale, out_matrix);
+    });
+}
+
+int vx_gguf_convert_q2_0(const vx_gguf_t* g, const char* name, uint8_t* planar, size_t planar_capacity,
+                         uint16_t* scales_f16, size_t scales_capacity, size_t* out_rows, size_t* out_cols) {
+    return guard([&]() -> int {
+        VX_TRY(check_gguf(g));
+        size_t k, rows, cols;
+        VX_TRY(find(g, name, &k));
+        std::vector<uint8_t> p;
+        std::vector<uint16_t> sc;
+        VX_TRY(q2_0_convert(g, g->tensors[k], &p, &sc, &rows, &cols));
+        if (out_rows) *out_rows = rows;
+        if (out_cols) *out_cols = cols;
+        if (planar_capacity < p.size() || scales_capacity < sc.size())
+            VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "the planar bytes need %zu bytes and the scales %zu values", p.size(), sc.size());
+        if (planar == nullptr || scales_f16 == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "planar or scales_f16 is NULL");
+        std::memcpy(planar, p.data(), p.size());
+        std::memcpy(scales_f16, sc.data(), sc.size() * 2);
+        return VX_OK;
+    });
+}
+
+int vx_gguf_upload_q2_matrix(const vx_gguf_t* g, const char* name, vx_matrix_t** out_matrix) {
+    return guard([&]() -> int {
+        VX_TRY(check_gguf(g));
+        if (out_matrix == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_matrix is NULL");
+        *out_matrix = nullptr;
+        size_t k, rows, cols;
+        VX_TRY(find(g, name, &k));
+        std::vector<uint8_t> p;
+        std::vector<uint16_t> sc;
+        VX_TRY(q2_0_convert(g, g->tensors[k], &p, &sc, &rows, &cols));
+        return vx_q2_matrix_create(p.data(), p.size(), sc.data(), sc.size(), rows, cols, out_matrix);
     });
 }
 

@@ -212,6 +212,31 @@ class GgufFile:
         self._read.add(name)
         return out, r.value, c.value, float(s.value)
 
+    def convert_q2_0(self, name: str):
+        """(planar velurex bytes, f16 scale bits (uint16, one per 64 weights of a row), rows, cols) of a Q2_0 matrix
+        (decode_q2_0_packed); VxError for a code 3."""
+        t = self.tensors[name]
+        if len(t.shape) != 2:
+            raise VxError(3, f"tensor '{name}' is not a matrix")
+        cols, rows = t.shape
+        planar = np.empty(rows * ((cols + 159) // 160) * 32, np.uint8)
+        scales = np.empty(max(rows * cols // 64, 1), np.uint16)
+        r, c = ctypes.c_size_t(), ctypes.c_size_t()
+        check(lib().vx_gguf_convert_q2_0(self._h, name.encode(), planar.ctypes.data_as(ctypes.c_void_p), planar.size,
+                                         scales.ctypes.data_as(ctypes.c_void_p), scales.size, ctypes.byref(r),
+                                         ctypes.byref(c)))
+        self._read.add(name)
+        return planar, scales[:rows * cols // 64], r.value, c.value
+
+    def upload_q2_matrix(self, name: str):
+        """A Q2_0 GEMV matrix (Q2Matrix) from a Q2_0 tensor."""
+        from ._lib import Q2Matrix
+        h = ctypes.c_void_p()
+        check(lib().vx_gguf_upload_q2_matrix(self._h, name.encode(), ctypes.byref(h)))
+        self._read.add(name)
+        cols, rows = self.tensors[name].shape
+        return Q2Matrix._from_handle(h, rows, cols)
+
     def upload_matrix(self, name: str):
         """A GEMV matrix (VelurexHipLayer) from a ternary tensor, converted on the GPU."""
         from .layer import VelurexHipLayer

@@ -223,3 +223,48 @@ def test_truncation_at_every_length_is_an_error(write, tmp_path):
     assert seen == {8}  # VX_ERR_FORMAT at every length
     with pytest.raises(VxError, match="VX_ERR_IO"):
         GgufFile(str(tmp_path / "does_not_exist.gguf"))
+
+
+def q2_0_payload(rng, rows, cols, bs):
+    """Q2_0 blocks of bs weights with codes 0..2 and random positive f16 scales; returns (bytes, trits, scale bits)."""
+    n = rows * cols
+    codes = rng.integers(0, 3, n).astype(np.uint8)
+    d = (rng.uniform(0.01, 0.1, n // bs).astype(np.float16)).view(np.uint16)
+    out = bytearray()
+    for b in range(n // bs):
+        c = codes[b * bs:(b + 1) * bs].reshape(-1, 4)
+        out += struct.pack("<H", d[b]) + bytes((c[:, 0] | c[:, 1] << 2 | c[:, 2] << 4 | c[:, 3] << 6).astype(np.uint8))
+    return bytes(out), codes.astype(np.int8) - 1, d
+
+
+@pytest.mark.parametrize("bs", [64, 128])
+def test_q2_0_convert_matches_the_oracle(write, oracle, bs):
+    """vx_gguf_convert_q2_0 equals the oracle's Q2_0 decoder (gguf_oracle.c, decode_q2_0 of decoders/q2_0.rs:58-98)
+    followed by the planar packer; the scales are the block's f16, once per 64 weights."""
+    rng = np.random.default_rng(bs)
+    rows, cols = 5, 640
+    data, trits, d = q2_0_payload(rng, rows, cols, bs)
+    with GgufFile(write("q2", build([], [("w", [cols, rows], 42, data), ("f", [8], 0, bytes(32))]))) as g:
+        assert g.tensors["w"].block_size == bs
+        planar, scales, r, c = g.convert_q2_0("w")
+    want_t, want_s = oracle.q2_0_unpack(np.frombuffer(data, np.uint8), rows, cols, bs)
+    assert np.array_equal(want_t.reshape(-1), trits)
+    assert (r, c) == (rows, cols)
+    assert np.array_equal(planar, oracle.pack_matrix(trits.reshape(rows, cols)).reshape(-1))
+    assert np.array_equal(scales, np.asarray(want_s, np.uint16).reshape(-1))
+    assert np.array_equal(scales, np.repeat(d, bs // 64))
+
+
+def test_q2_0_code_3_and_shape_errors(write):
+    rng = np.random.default_rng(1)
+    data, _, _ = q2_0_payload(rng, 2, 128, 64)
+    bad = bytearray(data)
+    bad[18 + 2 + 5] |= 3 << 4  # block 1, byte 5, third code: weight 64 + 4 * 5 + 2
+    f2 = ("m", [8, 2], 0, bytes(64))
+    with GgufFile(write("q2bad", build([], [("w", [128, 2], 42, bytes(bad)), f2, ("f", [8], 0, bytes(32))]))) as g:
+        with pytest.raises(VxError, match="weight 86 uses code 3"):
+            g.convert_q2_0("w")
+        with pytest.raises(VxError, match="not Q2_0"):
+            g.convert_q2_0("m")
+        with pytest.raises(VxError, match="not a matrix"):
+            g.convert_q2_0("f")

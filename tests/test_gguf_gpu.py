@@ -2,6 +2,7 @@
 HBM into a GEMV matrix. Checked through the exact GEMV: int32 outputs equal brute force over the oracle's trits and the
 outputs of the matrix built from the host conversion; the tensor's weight scale reaches the fp32 epilogue."""
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -85,3 +86,39 @@ def test_upload_errors(torch_dev, oracle, tmp_path):
             g.upload_matrix("d")
         with pytest.raises(VxError, match="INVALID_SHAPE"):
             g.upload_matrix("v")
+
+
+@pytest.mark.parametrize("bs", [64, 128])
+def test_q2_0_upload_bit_exact(torch_dev, oracle, tmp_path, bs):
+    """A Q2_0 GGUF tensor uploaded as a Q2_0 GEMV matrix (vx_gguf_upload_q2_matrix) gives the oracle's
+    dot_row_scalar results (block_scaled.rs:175-202) on the decoded trits and scales, bit for bit, with its lane sums."""
+    import ctypes
+    from test_gguf import q2_0_payload
+    from gguf_writer import build
+    from quintrit_amd.gguf import GgufFile
+    rng = np.random.default_rng(11 + bs)
+    rows, cols = 300, 2560
+    data, trits, d = q2_0_payload(rng, rows, cols, bs)
+    path = os.path.join(tmp_path, "q2.gguf")
+    with open(path, "wb") as f:
+        f.write(build([], [("w", [cols, rows], 42, data), ("f", [8], 0, bytes(32))]))
+    acts = oracle.gen_i8(5, cols, -127, 127)
+    as32 = rng.uniform(0.005, 0.05, cols // 32).astype(np.float32)
+    with GgufFile(path) as g:
+        mat = g.upload_q2_matrix("w")
+    torch = torch_dev
+    try:
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        a, s = torch.from_numpy(acts).cuda(), torch.from_numpy(as32).cuda()
+        out = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+        lanes = torch.empty(rows * (cols // 32) * 8, dtype=torch.int32, device="cuda")
+        mat.gemv_f32(a, s, out, stream)
+        mat.lane_sums(a, lanes, stream)
+        torch.cuda.synchronize()
+        planar = oracle.pack_matrix(trits.reshape(rows, cols))
+        ws = np.repeat(d, bs // 64).view(np.float16).astype(np.float32)
+        want = oracle.q2_0_gemv(planar, ws, acts, as32, rows, cols)
+        assert np.array_equal(lanes.cpu().numpy(), oracle.q2_0_lane_sums(planar, acts, rows, cols).reshape(-1))
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), np.asarray(want, np.float32).view(np.uint32))
+    finally:
+        mat.close()
