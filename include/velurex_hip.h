@@ -328,6 +328,11 @@ int vx_decoder_create(const vx_decoder_config_t* config, vx_decoder_t** out_deco
  * cols hidden; O hidden x n_heads*head_dim; gate/up ffn x hidden; down hidden x ffn (the reference's BitLinear). */
 int vx_decoder_set_projection(vx_decoder_t* decoder, uint32_t layer, uint32_t kind, const uint8_t* planar,
                               size_t planar_len, float weight_scale);
+/* The same from a matrix handle (vx_matrix_create(_dev), vx_gguf_upload_matrix, vx_matrix_create_ggml_dev) of the
+ * projection's shape on the decoder's device; its weight scale is the projection's. On success the decoder owns the
+ * matrix (it is freed with the decoder or when replaced) and the caller must not use or free it; on failure the caller
+ * keeps it. The upload of the reference's GPU loader (quintrit-runtime/src/gpu.rs:201-225) without a host copy. */
+int vx_decoder_adopt_projection(vx_decoder_t* decoder, uint32_t layer, uint32_t kind, vx_matrix_t* matrix);
 /* RMSNorm weights (host f32). layer == n_layers with kind VX_NORM_ATTN sets the output norm; the sub-norm kinds are
  * rejected when no_sub_norm is set. */
 int vx_decoder_set_norm(vx_decoder_t* decoder, uint32_t layer, uint32_t kind, const float* weights, size_t n);
@@ -446,7 +451,7 @@ typedef struct vx_gpu_options {
 /* Replaces quintrit_model_open_gpu (quintrit.h:527; GpuModel::load, quintrit-runtime/src/gpu.rs:149-260): a GGUF model
  * as a decoder on the GPU. The configuration comes from the metadata as ModelConfig::from_gguf reads it (config.rs:257-440;
  * BitNet: ReLU^2, sub-norms, NEOX RoPE; Falcon3 / LLaMA: SiLU, Normal RoPE); the ternary projections (I2_S, TQ1_0,
- * TQ2_0) are converted to planar velurex on the host and laid out in HBM; the embedding is the F16 token_embd.weight,
+ * TQ2_0) are uploaded in their GGUF size and converted in HBM (as vx_gguf_upload_matrix); the embedding is the F16 token_embd.weight,
  * the head output.weight (F16) or the embedding. The context is rounded down to a multiple of 256 as gpu.rs:141-146
  * does. Files the reference rejects give VX_ERR_MODEL (missing or misshapen tensors, no tokenizer, absurd dimensions);
  * models it runs elsewhere than this decoder give VX_ERR_UNSUPPORTED (no I2_S tensor, Q2_0, Qwen3 / hybrid / MoE,

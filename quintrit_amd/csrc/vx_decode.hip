@@ -1775,6 +1775,27 @@ int vx_decoder_set_projection(vx_decoder_t* d, uint32_t layer, uint32_t kind, co
     });
 }
 
+int vx_decoder_adopt_projection(vx_decoder_t* d, uint32_t layer, uint32_t kind, vx_matrix_t* m) {
+    return guard([&]() -> int {
+        VX_TRY(check_decoder(d));
+        std::lock_guard<std::mutex> lk(d->mu);
+        if (layer >= d->cfg.n_layers) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "layer %u out of range (n_layers %u)", layer, d->cfg.n_layers);
+        if (kind >= static_cast<uint32_t>(kProjKinds)) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "projection kind %u is not 0..6", kind);
+        if (m == nullptr || m->magic != kMatrixMagic) VX_FAIL(VX_ERR_INVALID_HANDLE, "matrix handle is not valid");
+        if (m->kind != kKindVelurex) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "a Q2_0 matrix cannot be a decoder projection");
+        if (m->device != d->device) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the matrix is on device %d, the decoder on %d", m->device, d->device);
+        if (m->g.rows != proj_rows(d, kind) || m->g.cols != proj_cols(d, kind))
+            VX_FAIL(VX_ERR_INVALID_SHAPE, "projection %u is %zu x %zu, the matrix %zu x %zu", kind, proj_rows(d, kind),
+                    proj_cols(d, kind), m->g.rows, m->g.cols);
+        vx_matrix_t*& slot = d->proj[static_cast<size_t>(layer) * kProjKinds + kind];
+        if (slot == m) return VX_OK;
+        if (slot) (void)vx_matrix_free(slot);
+        slot = m;
+        drop_graph(d);
+        return VX_OK;
+    });
+}
+
 int vx_decoder_set_norm(vx_decoder_t* d, uint32_t layer, uint32_t kind, const float* weights, size_t n) {
     return guard([&]() -> int {
         VX_TRY(check_decoder(d));

@@ -840,23 +840,24 @@ static int gguf_decoder_config(const vx_gguf* g, uint32_t context_limit, vx_deco
     return VX_OK;
 }
 
-// GpuModel::load (gpu.rs:183-260): every projection converted to planar velurex on the host (gpu.rs:120-138), the F32
-// norms and the F16 tables handed to the decoder, which lays them out in HBM.
+// GpuModel::load (gpu.rs:183-260): every projection converted to velurex in HBM (the reference converts on the host,
+// gpu.rs:120-138; the bytes are the same), the F32 norms and the F16 tables handed to the decoder.
 // The tensors were checked by gguf_decoder_config.
 static int gguf_load_decoder(const vx_gguf* g, vx_decoder_t* d, const vx_decoder_config_t& c) {
-    std::vector<uint8_t> planar;
     char name[96];
     for (uint32_t l = 0; l < c.n_layers; ++l) {
         for (uint32_t k = 0; k < 7; ++k) {
+            // The payload goes to the GPU in its GGUF size and is converted there (vx_gguf_upload_matrix).
             std::snprintf(name, sizeof name, "blk.%u.%s.weight", l, kProjNames[k]);
-            const TensorRec* t = tensor_get(g, name);
-            size_t rows, cols;
-            VX_TRY(matrix_shape(*t, &rows, &cols));
-            float scale;
-            VX_TRY(tensor_scale(g, *t, &scale));
-            planar.resize(rows * planar_row_bytes(cols));
-            host_to_planar(t->type, payload(g, *t), rows, cols, planar.data());
-            VX_TRY(vx_decoder_set_projection(d, l, k, planar.data(), planar.size(), scale));
+            vx_matrix_t* m = nullptr;
+            VX_TRY(vx_gguf_upload_matrix(g, name, &m));
+            const int st = vx_decoder_adopt_projection(d, l, k, m);
+            if (st != VX_OK) {
+                const std::string msg = vx_last_error_message();
+                vx_matrix_free(m);
+                set_error(st, msg);
+                return st;
+            }
         }
         for (uint32_t k = 0; k < 4; ++k) {
             if ((k == VX_NORM_ATTN_SUB || k == VX_NORM_FFN_SUB) && c.no_sub_norm) continue;

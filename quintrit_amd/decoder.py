@@ -108,6 +108,11 @@ class Decoder:
         p = np.ascontiguousarray(planar, dtype=np.uint8).reshape(-1)
         check(lib().vx_decoder_set_projection(self.handle, layer, kind, _ptr(p), p.size, weight_scale))
 
+    def adopt_projection(self, layer: int, kind: int, matrix) -> None:
+        """vx_decoder_adopt_projection: the decoder takes over a VelurexHipLayer's matrix (the layer object is emptied)."""
+        check(lib().vx_decoder_adopt_projection(self.handle, layer, kind, matrix._h))
+        matrix._h = ctypes.c_void_p()
+
     def set_norm(self, layer: int, kind: int, weights) -> None:
         w = np.ascontiguousarray(weights, dtype=np.float32).reshape(-1)
         check(lib().vx_decoder_set_norm(self.handle, layer, kind, _ptr(w), w.size))

@@ -84,3 +84,36 @@ def test_gguf_decoder_context_option(torch_dev, oracle, tmp_path):
     finally:
         dec.close()
         model.close()
+
+
+def test_adopt_projection(torch_dev, oracle, tmp_path):
+    """vx_decoder_adopt_projection: a matrix of the wrong shape is refused and stays the caller's; one of the right
+    shape replaces the projection (here with the same weights: the logits do not change), and a replaced projection
+    with other weights changes them."""
+    from quintrit_amd import VelurexHipLayer
+    from quintrit_amd._lib import VxError
+    from quintrit_amd.decoder import PROJ_O, open_gguf
+    cfg, arch, _ = cases(oracle)["bitnet"]
+    model = oracle.Model(cfg, 71)
+    path = os.path.join(tmp_path, "adopt.gguf")
+    GM.write_model(path, oracle, model, arch)
+    dec = open_gguf(path)
+    try:
+        planar, ws = model.projection(1, PROJ_O)
+        rows, cols = model.projection_shape(PROJ_O)
+        wrong = VelurexHipLayer(planar, rows // 2, cols, ws)
+        with pytest.raises(VxError, match="projection 3"):
+            dec.adopt_projection(1, PROJ_O, wrong)
+        assert wrong.shape() == (rows // 2, cols)  # still the caller's
+        wrong.close()
+        dec.adopt_projection(1, PROJ_O, VelurexHipLayer(planar, rows, cols, ws))
+        want_next, want = model.forward(5, 0)
+        got, got_next = dec.step(5, 0)
+        assert_same_bits(got, want, "same weights adopted")
+        other = oracle.pack_matrix(np.zeros((rows, cols), np.int8))
+        dec.adopt_projection(1, PROJ_O, VelurexHipLayer(other, rows, cols, ws))
+        got2, _ = dec.step(5, 0)
+        assert not np.array_equal(got2, got)
+    finally:
+        dec.close()
+        model.close()
