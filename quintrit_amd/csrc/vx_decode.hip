@@ -194,6 +194,9 @@ struct StageInput {
     const uint32_t* prompt;
     const uint16_t* emb;
     uint32_t emb_f16;     // kInEmbed: the embedding holds f16 (else bf16)
+    // kInPlain without a norm: the largest |v| as float bits, accumulated by the producing gated pair; each workgroup
+    // then reads only the elements of its own K slice
+    const uint32_t* amax;
 };
 
 // The loaded inputs of a thread: element e of float4 group k is 4 (tid + k kNT) + e. P4 groups cover P4 * 4 kNT
@@ -205,6 +208,7 @@ struct InputRegs {
     int4 pb[SB > 0 ? SB : 1][P4];        // K-slice partials of b
     float4 g[P4];                        // gamma
     float as_a, as_b;                    // activation scales of a and b
+    uint32_t amax;                       // StageInput::amax's value
 };
 
 struct __align__(16) InputLds {  // ys is accessed 16 bytes at a time
@@ -221,7 +225,7 @@ __device__ __forceinline__ uint32_t elem4(uint32_t tid, int k) { return 4u * (ti
 // that the loads a kernel issues after it (weights) do not delay them: vector-memory loads complete in issue order, so
 // a load issued after the weights would wait for all of them.
 template <int P4, int SA, int SB>
-__device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA, SB>& r) {
+__device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA, SB>& r, uint32_t wlo, uint32_t whi) {
     const uint32_t tid = threadIdx.x, n = p.n;
     if (p.kind == kInEmbed) {
         const uint32_t pos = p.ctl->pos;
@@ -234,10 +238,13 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
             r.x[k] = make_uint4(e.x, e.y, 0u, 0u);
         }
     } else if (p.kind != kInRelu2Mul) {
+        // with a precomputed maximum only the window [wlo, whi) is read (the elements outside stay 0)
+        const bool all = p.amax == nullptr;
+        if (!all) r.amax = *p.amax;
 #pragma unroll
         for (int k = 0; k < P4; ++k) {
             const uint32_t i = elem4(tid, k);
-            r.x[k] = load_if(reinterpret_cast<const uint4*>(p.x_in + i), i < n);
+            r.x[k] = load_if(reinterpret_cast<const uint4*>(p.x_in + i), i < n && (all || (i >= wlo && i < whi)));
         }
     }
     if constexpr (SA > 0) {
@@ -488,15 +495,7 @@ __device__ __forceinline__ void stage_quant(const float (&y)[P4][4], InputLds& s
     float m = 0.0f;
     for (int w = 0; w < kNT / 64; ++w) m = fmax_nn(m, s.red_f[w]);
     const float sc = m > 0.0f ? 127.0f / m : 0.0f;
-    int sum = 0;
-    if (m > 0.0f) {
-#pragma unroll
-        for (int k = 0; k < P4; ++k)
-            if (elem4(tid, k) < n) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) sum += quant_code(y[k][e], sc);
-            }
-    }
+    int sum = 0;  // the codes of the staged columns' elements (each element belongs to one column)
     const uint32_t full = n / 160u * 32u;
     for (uint32_t c = c0 + tid; c < c1; c += kNT) {
         uint32_t lo_n = 0, hi_n = 0;
@@ -507,6 +506,7 @@ __device__ __forceinline__ void stage_quant(const float (&y)[P4][4], InputLds& s
             const uint32_t idx = base + k * step;
             int x = 0;
             if (c < tbr && idx < n && m > 0.0f) x = quant_code(s.ys[idx - lo], sc);
+            sum += x;
             lo_n |= ((static_cast<uint32_t>(x) & 15u) ^ 8u) << (4 * k);
             hi_n |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * k);
         }
@@ -566,6 +566,7 @@ struct DJob {
     float* act_out;        // gated pair: [padded_rows]
     float ws, ws2;         // gated pair: weight scales
     uint32_t act, n8;      // gated pair: GateAct; rows below n8 take the vector exponential
+    uint32_t* amax_out;    // gated pair: atomic maximum of |act_out| as float bits (a plain unnormed consumer), or null
     uint32_t rows, padded_rows, n_tiles, n_chunks, kslices, slice_chunks, item_begin;
 };
 
@@ -581,6 +582,7 @@ struct DStageArgs {
     uint32_t variant;   // the kernel instance (host side: the input's length and kinds)
     uint32_t loop;      // every job has one K slice: a workgroup takes items blockIdx.x, + gridDim.x, ...
     uint32_t grid;      // workgroups of the launch
+    uint32_t* amax_clear;  // zeroed by the stage (the StageInput::amax a later stage of the layer accumulates), or null
 };
 
 __constant__ DigitTable g_digits = make_digit_table();
@@ -602,12 +604,6 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const char* tabb = reinterpret_cast<const char*>(tab);
     const uint32_t lane_off = (lane & 31u) * 4u;
-
-    InputRegs<P4, SA, SB> r;
-    stage_load(a.in, r);
-    uint32_t dig[2];
-#pragma unroll
-    for (int k = 0; k < 2; ++k) dig[k] = g_digits.v[(tid + k * kNT) >> 3];
 
     // A work item: its job, tile and K slice, and where wave `wave`'s chunks are.
     struct Item {
@@ -646,6 +642,17 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
 
     uint32_t item = blockIdx.x;
     Item it = locate(item);
+    // The staged slice: every item of a workgroup has the same K slice (one workgroup per item, or a looping stage
+    // whose jobs have one slice each).
+    const uint32_t c0 = it.q0 * 16u, c1 = min((it.q0 + it.nq) * 16u, a.tbr);
+    uint32_t lo, hi;
+    slice_window(a.in.n, c0, c1, &lo, &hi);
+    InputRegs<P4, SA, SB> r;
+    stage_load(a.in, r, lo, hi);
+    uint32_t dig[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) dig[k] = g_digits.v[(tid + k * kNT) >> 3];
+    if (a.amax_clear != nullptr && blockIdx.x == 0 && tid == 0) *a.amax_clear = 0u;
     // The weight loads go out once the input and the digit table have arrived: a load issued under a runtime condition
     // (the wave's chunk count) leaves the compiler unsure how many loads follow an earlier one, so any wait for the input
     // after them would also wait for most of the weights.
@@ -657,12 +664,8 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
 
     float y[P4][4];
     stage_y(a.in, r, s, blockIdx.x == 0, y);
-    // The staged slice: every item of a workgroup has the same K slice (one workgroup per item, or a looping stage
-    // whose jobs have one slice each).
-    const uint32_t c0 = it.q0 * 16u, c1 = min((it.q0 + it.nq) * 16u, a.tbr);
-    uint32_t lo, hi;
-    slice_window(a.in.n, c0, c1, &lo, &hi);
-    const float mx = stage_window(y, a.in.n, lo, hi, s);
+    float mx = stage_window(y, a.in.n, lo, hi, s);
+    if (a.in.amax != nullptr) mx = __uint_as_float(r.amax);
     // The table is filled after the input's values are computed (its loads were issued after the input's, so waiting
     // for them earlier would also wait for the input) and before the quantization's first barrier.
 #pragma unroll
@@ -738,7 +741,9 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
 #pragma unroll
             for (int w = 0; w < kNT / 64; ++w) v += red[parity][0][w][lane];
             const uint32_t row = it.tile * kTileRows + lane;
-            if (it.ks == 0) v += 8 * jb.dsum[row] - act_sum;
+            // act_sum holds the codes of this slice's elements only: every slice subtracts its own
+            if (it.ks == 0) v += 8 * jb.dsum[row];
+            v -= act_sum;
             if (!pair) {
                 jb.part[static_cast<size_t>(it.ks) * jb.padded_rows + row] = v;
             } else {
@@ -762,6 +767,12 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
                     o = sq * u;
                 }
                 if (row < jb.rows) jb.act_out[row] = o;
+                if (jb.amax_out != nullptr) {  // the consumer's absmax (NaN never counts, as in stage_window)
+                    float ao = row < jb.rows ? __builtin_fabsf(o) : 0.0f;
+                    if (!(ao > 0.0f)) ao = 0.0f;
+                    ao = wave_max_f32(ao);
+                    if (lane == 0 && ao > 0.0f) atomicMax(jb.amax_out, __float_as_uint(ao));
+                }
             }
         }
         return nt;
@@ -1141,7 +1152,7 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
     __shared__ unsigned long long wbest[kNT / 64];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     InputRegs<2, kMaxSlicesA, 0> r;
-    stage_load(a.in, r);
+    stage_load(a.in, r, 0u, a.in.n);
     float y[2][4];
     stage_y(a.in, r, s, false, y);
     uint16_t* xh = reinterpret_cast<uint16_t*>(xs);
@@ -1308,6 +1319,7 @@ struct vx_decoder {
     uint16_t* d_emb;
     uint16_t* d_head;                 // the untied head, or null
     float* d_inter;                   // gated pair output: act(gate, up), [ffn rounded up to 64]
+    uint32_t* d_amax;                 // per layer: max |act(gate, up)| bits for an unnormed down input (pair, no sub-norms)
     float* d_rope;
     uint16_t *d_kc, *d_vc;            // [layer][kv_head][max_ctx][head_dim]
     float *d_xa, *d_xb;               // the residual stream (written alternately by the stages that add to it)
@@ -1360,7 +1372,7 @@ static void destroy_decoder(vx_decoder* d) {
     for (auto* p : d->norms)
         if (p) (void)hipFree(p);
     void* bufs[] = {d->d_emb, d->d_head, d->d_inter, d->d_rope,   d->d_kc,    d->d_vc,    d->d_xa,
-                    d->d_xb,  d->d_att,  d->d_logits, d->d_key, d->d_ctl, d->d_prompt, d->d_tokens};
+                    d->d_xb,  d->d_att,  d->d_logits, d->d_key, d->d_ctl, d->d_prompt, d->d_tokens, d->d_amax};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (int32_t* b : d->d_part)
@@ -1475,6 +1487,8 @@ static int create_decoder(const vx_decoder_config_t* cin, vx_decoder_t** out) {
     hipError_t e = dalloc(d, &d->d_emb, static_cast<size_t>(c->vocab) * H * 2);
     if (e == hipSuccess && c->untied) e = dalloc(d, &d->d_head, static_cast<size_t>(c->vocab) * H * 2);
     if (e == hipSuccess && pair) e = dalloc(d, &d->d_inter, round_up(c->ffn, kTileRows) * 4);
+    if (e == hipSuccess && pair) e = dalloc(d, &d->d_amax, static_cast<size_t>(c->n_layers) * 4);
+    if (e == hipSuccess && pair) e = hipMemset(d->d_amax, 0, static_cast<size_t>(c->n_layers) * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_rope, static_cast<size_t>(c->max_ctx) * c->head_dim * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_kc, kv_elems * 2);
     if (e == hipSuccess) e = dalloc(d, &d->d_vc, kv_elems * 2);
@@ -1596,6 +1610,7 @@ static int build_stages(vx_decoder* d) {
                 j.w2 = mu->d_w;
                 j.dsum2 = mu->d_dsum;
                 j.act_out = d->d_inter;
+                j.amax_out = sub ? nullptr : d->d_amax + l;
                 j.ws = mg->weight_scale;
                 j.ws2 = mu->weight_scale;
                 j.act = d->cfg.act == VX_ACT_SILU ? kActSilu : kActRelu2;
@@ -1642,11 +1657,15 @@ static int build_stages(vx_decoder* d) {
                 in.a = proj_out(d, l - 1, VX_PROJ_DOWN);
             } else if (s == 1) {  // attention output -> attention sub-norm (or none)
                 in = stage_input(d, kInPlain, d->qd, d->d_att, nullptr, sub ? nw[VX_NORM_ATTN_SUB] : nullptr);
+                // the o stage runs after the previous step's down stage and before this step's pair: it clears the
+                // layer's maximum
+                if (d->pair && !sub) a.amax_clear = d->d_amax + l;
             } else if (s == 2) {  // x + o -> FFN norm
                 in = stage_input(d, kInResidual, H, d->d_xa, d->d_xb, nw[VX_NORM_FFN]);
                 in.a = proj_out(d, l, VX_PROJ_O);
             } else if (d->pair) {  // act(gate, up) from the pair -> FFN sub-norm (or none)
                 in = stage_input(d, kInPlain, F, d->d_inter, nullptr, sub ? nw[VX_NORM_FFN_SUB] : nullptr);
+                if (!sub) in.amax = d->d_amax + l;
             } else {  // relu2(gate) * up -> FFN sub-norm (or none)
                 in = stage_input(d, kInRelu2Mul, F, nullptr, nullptr, sub ? nw[VX_NORM_FFN_SUB] : nullptr);
                 in.a = proj_out(d, l, VX_PROJ_GATE);
