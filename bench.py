@@ -643,7 +643,7 @@ FALCON3_LAYER = [("q", 3072, 3072), ("k", 1024, 3072), ("v", 1024, 3072), ("o", 
 
 
 def gguf_bench(torch, args) -> int:
-    """GGUF -> velurex transcoding (SURVEY.md's next row after the decode step): the seven ternary tensors of one
+    """GGUF -> velurex transcoding (loading real model files): the seven ternary tensors of one
     Falcon3-10B layer (237.5 Mweights) in I2_S, TQ1_0 and TQ2_0. Reported per type: the device-side conversion of a
     payload resident in HBM into a GEMV matrix (vx_matrix_create_ggml_dev: payload -> planar -> device layout + row
     digit sums), the whole upload of a GGUF file (open, mmap, PCIe copy of the payload, conversion), and the host
@@ -749,7 +749,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (how the path would shard over "
-                                   "several GPUs is described in DESIGN.md, not built)"}))
+                                   "several GPUs is a design only, not built)"}))
         return 2
     import torch
     from quintrit_amd import _lib
