@@ -241,7 +241,7 @@ int vx_plan_free(vx_plan_t* plan);
 
 /*
  * Y[t][i] = sum_j W[i][j] * X[t][j] for t < m tokens, exact int32: the same numbers as m calls of vx_gemv_i32_dev, on
- * the matrix cores (v_mfma_i32_16x16x64_i8). x: m rows of ldx >= cols int8 (device); y: m rows of ldy >= rows int32
+ * the matrix cores (v_mfma_i32_32x32x32_i8). x: m rows of ldx >= cols int8 (device); y: m rows of ldy >= rows int32
  * (device); workspace: device memory of vx_gemm_workspace_bytes(matrix, m) bytes, 256-byte aligned, owned by the
  * caller (the call allocates nothing, so it can be captured in a HIP graph; concurrent calls need distinct
  * workspaces). The reference has no multi-token kernel: its prefill calls the GEMV once per token

@@ -79,9 +79,18 @@ float vxo_ggml_dot_f16(const uint16_t* x, const uint16_t* y, size_t n) {
     return sum;
 }
 
-/* ops.rs:1254-1300: y = f16(fma(x, v, y)) element by element (the AVX2 path). */
+/* ops.rs:1254-1300 (the AVX2 path): the first n & ~31 values are y = f16(fma(x, v, y)) (_mm256_fmadd_ps), the rest
+ * y = f16(y + x * v) with a separate multiply and add (Rust does not contract; this file is built with
+ * -ffp-contract=off). */
 void vxo_vec_mad_f16(uint16_t* y, const uint16_t* x, float v, size_t n) {
-    for (size_t i = 0; i < n; ++i) y[i] = vxo_f32_to_f16(fmaf(vxo_f16_to_f32(x[i]), v, vxo_f16_to_f32(y[i])));
+    const size_t np = n & ~(size_t)31;
+    size_t i = 0;
+    for (; i < np; ++i) y[i] = vxo_f32_to_f16(fmaf(vxo_f16_to_f32(x[i]), v, vxo_f16_to_f32(y[i])));
+    for (; i < n; ++i) {
+        const float fy = vxo_f16_to_f32(y[i]), fx = vxo_f16_to_f32(x[i]);
+        const float p = fx * v;
+        y[i] = vxo_f32_to_f16(fy + p);
+    }
 }
 
 /* ops.rs:1304-1345: y = f16(y * v). */

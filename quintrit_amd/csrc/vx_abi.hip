@@ -99,6 +99,7 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     m->d_dsum = nullptr;
     m->d_staged = nullptr;
     m->d_io = nullptr;
+    m->owner = nullptr;
     Job probe{};
     plan_job(probe, m->g, static_cast<uint32_t>(di.num_cus));
     m->kslices = probe.kslices;
@@ -379,6 +380,8 @@ int vx_matrix_free(vx_matrix_t* matrix) {
     return guard([&]() -> int {
         if (matrix == nullptr) return VX_OK;
         VX_TRY(check_matrix(matrix));
+        if (matrix->owner != nullptr)
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the matrix belongs to a decoder (adopted); it is freed with the decoder");
         VX_TRY(set_device_of(matrix));
         VX_HIP(hipDeviceSynchronize());
         destroy(matrix);
@@ -750,6 +753,7 @@ int vx_q2_matrix_create(const uint8_t* planar, size_t planar_len, const uint16_t
         m->d_dsum = nullptr;
         m->d_staged = nullptr;
         m->d_io = nullptr;
+        m->owner = nullptr;
         const size_t bytes = q2_device_bytes(rows, cols);
         std::vector<uint8_t> host(bytes);
         q2_to_device_layout(planar, scales_f16, rows, cols, host.data());

@@ -1368,7 +1368,10 @@ static void drop_graph(vx_decoder* d) {
 static void destroy_decoder(vx_decoder* d) {
     drop_graph(d);
     for (auto* m : d->proj)
-        if (m) (void)vx_matrix_free(m);
+        if (m) {
+            m->owner = nullptr;
+            (void)vx_matrix_free(m);
+        }
     for (auto* p : d->norms)
         if (p) (void)hipFree(p);
     void* bufs[] = {d->d_emb, d->d_head, d->d_inter, d->d_rope,   d->d_kc,    d->d_vc,    d->d_xa,
@@ -1786,8 +1789,12 @@ int vx_decoder_set_projection(vx_decoder_t* d, uint32_t layer, uint32_t kind, co
         VX_TRY(set_device(d->device));
         vx_matrix_t* m = nullptr;
         VX_TRY(vx_matrix_create(planar, planar_len, proj_rows(d, kind), proj_cols(d, kind), weight_scale, &m));
+        m->owner = d;
         vx_matrix_t*& slot = d->proj[static_cast<size_t>(layer) * kProjKinds + kind];
-        if (slot) (void)vx_matrix_free(slot);
+        if (slot) {
+            slot->owner = nullptr;
+            (void)vx_matrix_free(slot);
+        }
         slot = m;
         drop_graph(d);
         return VX_OK;
@@ -1808,7 +1815,13 @@ int vx_decoder_adopt_projection(vx_decoder_t* d, uint32_t layer, uint32_t kind, 
                     proj_cols(d, kind), m->g.rows, m->g.cols);
         vx_matrix_t*& slot = d->proj[static_cast<size_t>(layer) * kProjKinds + kind];
         if (slot == m) return VX_OK;
-        if (slot) (void)vx_matrix_free(slot);
+        // one owner per matrix: a handle already held by a slot (of this or another decoder) would be freed twice
+        if (m->owner != nullptr) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the matrix already belongs to a decoder");
+        if (slot) {
+            slot->owner = nullptr;
+            (void)vx_matrix_free(slot);
+        }
+        m->owner = d;
         slot = m;
         drop_graph(d);
         return VX_OK;

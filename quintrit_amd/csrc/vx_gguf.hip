@@ -337,12 +337,8 @@ static void detect_q2_block(std::vector<TensorRec>& ts, uint64_t data_len, uint6
         const TensorRec& t = ts[k];
         if (t.type != VX_GGML_Q2_0) continue;
         const uint64_t n = t.n_elem;
-        uint64_t next = data_len;
-        for (uint64_t o : starts)
-            if (o > t.offset) {
-                next = o;
-                break;
-            }
+        const auto it = std::upper_bound(starts.begin(), starts.end(), t.offset);  // the next tensor's start
+        const uint64_t next = it == starts.end() ? data_len : *it;
         const uint64_t room = next > t.offset ? next - t.offset : 0;
         auto fits = [&](uint64_t bs) {
             if (n % bs) return false;

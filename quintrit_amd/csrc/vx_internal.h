@@ -220,6 +220,7 @@ struct vx_matrix {
     int32_t* d_dsum;    // per padded row: digit sum of the device row (the signed low-nibble correction)
     uint8_t* d_staged;  // activation staging of the calls that take raw int8 activations
     int8_t* d_io;       // host-API staging: cols bytes of activations + padded_rows * 4 bytes of output
+    const void* owner;  // the decoder that adopted the matrix (it frees it), or null: the caller's
     std::mutex mu;      // serialises the host-pointer API on this handle
 };
 

@@ -62,13 +62,16 @@ def variant_cfg(oracle, name):
              tail on libm's expf), head_dim 256, Normal RoPE, f16 embedding and untied f16 head
     hd256    the BitNet structure (ReLU^2, sub-norms, NEOX, tied bf16) at head_dim 256
     silu_sub SiLU with sub-norms (the pair's output normed), NEOX, head_dim 128, bf16 embedding with an untied head
-    relu_raw ReLU^2 without sub-norms (the gating input unnormed), Normal RoPE, f16 tied head"""
+    relu_raw ReLU^2 without sub-norms (the gating input unnormed), Normal RoPE, f16 tied head
+    relu_wide ReLU^2 without sub-norms and an FFN wider than a normed input (8420, not a multiple of 160): gate and up
+             run as the gated pair with the ReLU^2 epilogue, which also produces the down input's absmax"""
     M = oracle.ModelConfig
     return {
         "falcon3": oracle.falcon3(2, 256, 4, 2, 256, 9220, 1000, 640, 1e-5, 100000.0),
         "hd256": M(2, 256, 4, 2, 256, 384, 1000, 640, 1e-5, 10000.0),
         "silu_sub": M(2, 256, 4, 2, 128, 392, 1000, 640, 1e-5, 10000.0, oracle.ACT_SILU, oracle.ROPE_NEOX, 0, 0, 1),
         "relu_raw": M(2, 256, 4, 1, 128, 384, 1000, 640, 1e-5, 10000.0, oracle.ACT_RELU2, oracle.ROPE_NORMAL, 1, 1, 0),
+        "relu_wide": M(2, 256, 4, 1, 128, 8420, 1000, 640, 1e-5, 10000.0, oracle.ACT_RELU2, oracle.ROPE_NORMAL, 1, 1, 0),
     }[name]
 
 
@@ -137,7 +140,7 @@ def test_tiny_generate_tokens_identical(torch_dev, oracle, max_ctx, n_prompt, n_
         model.close()
 
 
-@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw"])
+@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw", "relu_wide"])
 def test_variant_step_logits_bit_exact(torch_dev, oracle, name):
     """forward_token of each architecture variant at positions 0..299 (teacher forced; the 4-chunk attention split from
     position 256): every logit bit-identical to the oracle's, every greedy token equal."""

@@ -154,6 +154,20 @@ def test_q2_0_block_size_from_the_layout(write):
         GgufFile(write("mixed", build([], [t64, t128, f])))
 
 
+def test_q2_0_block_detection_scales_with_many_tensors(write):
+    """A file of many small Q2_0 tensors: the block size of each is read from the next tensor's start, found by a
+    binary search over the sorted starts, so opening stays fast (a scan per tensor would be quadratic in their count)."""
+    import time
+    n_t = 40000
+    tensors = [(f"q{i}", [64], 42, bytes(18)) for i in range(n_t)]
+    path = write("many_q2", build([], tensors))
+    t0 = time.perf_counter()
+    with GgufFile(path) as g:
+        assert len(g.tensors) == n_t
+        assert g.tensors["q0"].block_size == 64 and g.tensors[f"q{n_t - 1}"].block_size == 64
+    assert time.perf_counter() - t0 < 5.0
+
+
 def valid_file():
     return build([("general.architecture", STR, "llama"), ("llama.block_count", U32, 2)],
                  [("a", [4], 0, bytes(16)), ("b", [8], 0, bytes(32))])

@@ -2,6 +2,7 @@
 quintrit.h:527) gives the oracle's logits bit for bit: the configuration read from the metadata (ModelConfig::from_gguf,
 config.rs:257-496), the I2_S projections with their trailing f32 scales converted to planar velurex (gpu.rs:120-138),
 the F32 norms and the F16 embedding and head all land where the decoder built from the oracle's arrays has them."""
+import ctypes
 import os
 
 import numpy as np
@@ -91,7 +92,7 @@ def test_adopt_projection(torch_dev, oracle, tmp_path):
     shape replaces the projection (here with the same weights: the logits do not change), and a replaced projection
     with other weights changes them."""
     from quintrit_amd import VelurexHipLayer
-    from quintrit_amd._lib import VxError
+    from quintrit_amd._lib import VxError, lib
     from quintrit_amd.decoder import PROJ_O, open_gguf
     cfg, arch, _ = cases(oracle)["bitnet"]
     model = oracle.Model(cfg, 71)
@@ -106,7 +107,12 @@ def test_adopt_projection(torch_dev, oracle, tmp_path):
             dec.adopt_projection(1, PROJ_O, wrong)
         assert wrong.shape() == (rows // 2, cols)  # still the caller's
         wrong.close()
-        dec.adopt_projection(1, PROJ_O, VelurexHipLayer(planar, rows, cols, ws))
+        adopted = VelurexHipLayer(planar, rows, cols, ws)
+        raw = ctypes.c_void_p(adopted._h.value)
+        dec.adopt_projection(1, PROJ_O, adopted)
+        # the handle now belongs to the decoder: a second adopt (another slot) and a free by the caller are refused
+        assert lib().vx_decoder_adopt_projection(dec.handle, 0, PROJ_O, raw) == 2
+        assert lib().vx_matrix_free(raw) == 2
         want_next, want = model.forward(5, 0)
         got, got_next = dec.step(5, 0)
         assert_same_bits(got, want, "same weights adopted")

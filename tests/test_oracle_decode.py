@@ -178,6 +178,54 @@ def test_vec_mad_f16_rounding_semantics(oracle):
     assert checked > 10000
 
 
+def _fused_unfused_split(rng, count):
+    """f16 (x, y) pairs and an f32 v for which f16(fma(x, v, y)) and f16(y + f32(x * v)) differ: drawn at random and
+    kept when the float64 sum x v + y is exact (so its rounding to f32 is the FMA's) and the two f16 results differ."""
+    xs, ys, vs = [], [], []
+    while len(xs) < count:
+        x = f16(rng.standard_normal(4096).astype(np.float32) * 4)
+        y = f16(rng.standard_normal(4096).astype(np.float32) * 4)
+        v = (rng.standard_normal(4096) * 3).astype(np.float32)
+        fx, fy = h2f(x).astype(np.float64), h2f(y).astype(np.float64)
+        p = fx * v.astype(np.float64)
+        s = p + fy
+        fused = f16(s.astype(np.float32))
+        unfused = f16(h2f(y) + (h2f(x) * v).astype(np.float32))
+        keep = ((s - p) == fy) & (fused != unfused)
+        xs += list(x[keep])
+        ys += list(y[keep])
+        vs += list(v[keep])
+    return np.array(xs[:count], np.uint16), np.array(ys[:count], np.uint16), np.array(vs[:count], np.float32)
+
+
+def test_vec_mad_f16_tail_is_unfused(oracle):
+    """The n % 32 tail of ggml_vec_mad_f16 (ops.rs:1282-1287) is f32_to_f16(fy + fx * v): a multiply rounded to f32,
+    then the add. Every tail element here is one where that differs from the fused f16(fma(x, v, y)) of the vector body,
+    so an oracle that fuses the tail fails on all of them; the same pairs placed in the body must come out fused."""
+    rng = np.random.default_rng(91)
+    x, y, v = _fused_unfused_split(rng, 600)
+    assert x.size == 600
+    for i in range(0, 600, 31):  # one shared v per call: the pairs with that v only
+        vi = v[i]
+        sel = v == vi
+        xt, yt = x[sel][:31], y[sel][:31]
+        n = 32 + xt.size
+        xb = f16(rng.standard_normal(32).astype(np.float32))
+        yb = f16(rng.standard_normal(32).astype(np.float32))
+        got = oracle.vec_mad_f16(np.concatenate([yb, yt]), np.concatenate([xb, xt]), float(vi))
+        tail_want = f16(h2f(yt) + (h2f(xt) * vi).astype(np.float32))
+        assert np.array_equal(got[32:n], tail_want)
+    # the same pairs in the vector body: the fused rounding
+    for k in range(0, 576, 32):
+        for j in range(32):
+            xx = np.full(32, x[k + j], np.uint16)
+            yy = np.full(32, y[k + j], np.uint16)
+            got = oracle.vec_mad_f16(yy, xx, float(v[k + j]))
+            s = h2f(xx[:1]).astype(np.float64) * np.float64(v[k + j]) + h2f(yy[:1]).astype(np.float64)
+            assert got[0] == f16(s.astype(np.float32))[0]
+            assert got[0] != f16(h2f(yy[:1]) + (h2f(xx[:1]) * v[k + j]).astype(np.float32))[0]
+
+
 def test_vec_scale_f16(oracle):
     """ggml_vec_scale_f16 (ops.rs:1304-1345): y = f16(f32(y) * v)."""
     rng = np.random.default_rng(10)
