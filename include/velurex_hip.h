@@ -251,6 +251,19 @@ int vx_gemm_workspace_bytes(const vx_matrix_t* matrix, size_t m, size_t* out_byt
 int vx_gemm_i32_dev(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t ldx, int32_t* y, size_t ldy,
                     void* workspace, size_t workspace_len, void* stream);
 
+/*
+ * vx_gemm_i32_dev without the workspace argument: the call allocates nothing (no hipMalloc, no library allocation).
+ * It has no counterpart in the reference; it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). The workspace is a library-owned array of
+ * VX_GEMM_NOALLOC_SCRATCH_BYTES per GPU, held from the first call on that GPU until the process ends; a call whose
+ * workspace (vx_gemm_workspace_bytes) would exceed it returns VX_ERR_INVALID_SHAPE. Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (two streams, two threads) race and must be ordered by the caller.
+ * Results are those of vx_gemm_i32_dev, bit for bit.
+ */
+#define VX_GEMM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int vx_gemm_i32_noalloc_dev(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t ldx, int32_t* y, size_t ldy,
+                            void* stream);
+
 /* ---- block-scaled (Q2_0) GEMV -------------------------------------------------------------------------------------- */
 
 /*

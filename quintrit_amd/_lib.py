@@ -71,6 +71,7 @@ SIGNATURES = {
     "vx_plan_free": (_i32, [_vp]),
     "vx_gemm_workspace_bytes": (_i32, [_vp, _sz, _vp]),
     "vx_gemm_i32_dev": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz, _vp, _sz, _vp]),
+    "vx_gemm_i32_noalloc_dev": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "vx_q2_matrix_create": (_i32, [_vp, _sz, _vp, _sz, _sz, _sz, _vp]),
     "vx_q2_gemv_f32_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp, _sz, _vp]),
     "vx_q2_lane_sums_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp]),

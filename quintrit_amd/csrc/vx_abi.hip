@@ -665,20 +665,36 @@ int vx_gemm_workspace_bytes(const vx_matrix_t* matrix, size_t m, size_t* out_byt
     });
 }
 
+static int check_gemm(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t ldx, const int32_t* y, size_t ldy) {
+    VX_TRY(check_kind(matrix, kKindVelurex));
+    if (x == nullptr || y == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "x or y is NULL");
+    if (m == 0 || m > VX_MAX_GEMM_TOKENS) VX_FAIL(VX_ERR_INVALID_SHAPE, "m must be in 1..=%d (got %zu)", VX_MAX_GEMM_TOKENS, m);
+    if (ldx < matrix->g.cols) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "ldx = %zu is less than cols = %zu", ldx, matrix->g.cols);
+    if (ldy < matrix->g.rows) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "ldy = %zu is less than rows = %zu", ldy, matrix->g.rows);
+    return VX_OK;
+}
+
 int vx_gemm_i32_dev(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t ldx, int32_t* y, size_t ldy,
                     void* workspace, size_t workspace_len, void* stream) {
     return guard([&]() -> int {
-        VX_TRY(check_kind(matrix, kKindVelurex));
-        if (x == nullptr || y == nullptr || workspace == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "x, y or workspace is NULL");
-        if (m == 0 || m > VX_MAX_GEMM_TOKENS) VX_FAIL(VX_ERR_INVALID_SHAPE, "m must be in 1..=%d (got %zu)", VX_MAX_GEMM_TOKENS, m);
-        if (ldx < matrix->g.cols) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "ldx = %zu is less than cols = %zu", ldx, matrix->g.cols);
-        if (ldy < matrix->g.rows) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "ldy = %zu is less than rows = %zu", ldy, matrix->g.rows);
+        VX_TRY(check_gemm(matrix, x, m, ldx, y, ldy));
+        if (workspace == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "workspace is NULL");
         const size_t need = gemm_workspace_bytes(matrix->g, m, matrix->num_cus);
         if (workspace_len < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "workspace holds %zu bytes, %zu needed", workspace_len, need);
         if (reinterpret_cast<uintptr_t>(workspace) % 256u) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
         VX_TRY(set_device_of(matrix));
         return launch_gemm(matrix->d_w, matrix->g, matrix->num_cus, x, m, ldx, y, ldy, static_cast<uint8_t*>(workspace),
                            static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_gemm_i32_noalloc_dev(const vx_matrix_t* matrix, const int8_t* x, size_t m, size_t ldx, int32_t* y, size_t ldy,
+                            void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_gemm(matrix, x, m, ldx, y, ldy));
+        VX_TRY(set_device_of(matrix));
+        return launch_gemm_noalloc(matrix->d_w, matrix->g, matrix->device, matrix->num_cus, x, m, ldx, y, ldy,
+                                   static_cast<hipStream_t>(stream));
     });
 }
 

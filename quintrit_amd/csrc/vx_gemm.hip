@@ -26,6 +26,7 @@
 #include "vx_internal.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace vx {
 
@@ -406,6 +407,49 @@ int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* 
         VX_HIP(hipGetLastError());
     }
     return VX_OK;
+}
+
+// ---- the no-allocation entry point's workspace -----------------------------------------------------------------------
+
+// Workspace of vx_gemm_i32_noalloc_dev: one array per GPU, allocated with the code object when the library's kernels
+// are first loaded on that GPU and held until the process ends. Host code never passes `scratch` itself (in host code
+// the name is only a stand-in for the symbol); it passes the device address hipGetSymbolAddress returns for the
+// current device, looked up once per device. Every call on a GPU reuses that GPU's array, so calls that overlap on one
+// GPU race; the kernels write every word they later read (staged activations, plane-4 parts, K-slice partials), so
+// no clearing is needed between calls.
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on `device`, which must be the current device.
+static int scratch_address(int device, uint8_t** out) {
+    if (device < 0 || device >= kMaxScratchDevices)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "device %d is beyond the %d devices the no-allocation GEMM serves", device,
+                kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* p = nullptr;
+        VX_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (p == nullptr) VX_FAIL(VX_ERR_DEVICE, "hipGetSymbolAddress returned no address for the GEMM scratch");
+        g_scratch_ptr[device] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scratch_ptr[device];
+    return VX_OK;
+}
+
+int launch_gemm_noalloc(const uint8_t* w, const Geometry& g, int device, int num_cus, const int8_t* x, size_t M,
+                        size_t ldx, int32_t* y, size_t ldy, hipStream_t stream) {
+    const size_t need = gemm_workspace_bytes(g, M, num_cus);
+    if (need > kNoAllocScratchBytes)
+        VX_FAIL(VX_ERR_INVALID_SHAPE,
+                "m = %zu tokens on a %zu x %zu matrix need %zu bytes of workspace, more than the %zu bytes the "
+                "no-allocation GEMM holds; use vx_gemm_i32_dev with a workspace",
+                M, g.rows, g.cols, need, kNoAllocScratchBytes);
+    uint8_t* ws = nullptr;
+    VX_TRY(scratch_address(device, &ws));
+    return launch_gemm(w, g, num_cus, x, M, ldx, y, ldy, ws, stream);
 }
 
 }  // namespace vx

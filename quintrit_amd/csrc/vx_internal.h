@@ -165,6 +165,10 @@ int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream);
+// The same GEMM with its workspace in the library's per-device scratch array (kNoAllocScratchBytes): no allocation.
+constexpr size_t kNoAllocScratchBytes = VX_GEMM_NOALLOC_SCRATCH_BYTES;
+int launch_gemm_noalloc(const uint8_t* w, const Geometry& g, int device, int num_cus, const int8_t* x, size_t M,
+                        size_t ldx, int32_t* y, size_t ldy, hipStream_t stream);
 size_t find_invalid_byte(const uint8_t* planar, size_t n);
 void planar_to_device_layout(const uint8_t* planar, const Geometry& g, uint8_t* dst);
 
