@@ -358,10 +358,25 @@ int vx_decoder_set_head(vx_decoder_t* decoder, const uint16_t* head, size_t n);
  * NULL) receives vocab values; out_next (may be NULL) the greedy token. */
 int vx_decoder_step(vx_decoder_t* decoder, uint32_t token, uint32_t pos, float* logits, size_t logits_capacity,
                     uint32_t* out_next);
-/* Greedy generation from position 0 (engine.rs:590-686 with the greedy sampler, the prompt fed one token at a time):
- * n_new tokens into out_tokens (host). n_prompt >= 1 and n_prompt + n_new - 1 <= max_ctx. */
+/* Greedy generation from position 0 (engine.rs:590-686 with the greedy sampler): the prompt is ingested by prefill
+ * passes (vx_decoder_prefill), then one decode step per further token; n_new tokens into out_tokens (host).
+ * n_prompt >= 1 and n_prompt + n_new - 1 <= max_ctx. The tokens are those of feeding the prompt one token at a time. */
 int vx_decoder_generate(vx_decoder_t* decoder, const uint32_t* prompt, size_t n_prompt, size_t n_new,
                         uint32_t* out_tokens, size_t out_capacity);
+/* The same with the prompt fed one decode step per token, as the reference's loop does (engine.rs:627-630). */
+int vx_decoder_generate_stepwise(vx_decoder_t* decoder, const uint32_t* prompt, size_t n_prompt, size_t n_new,
+                                 uint32_t* out_tokens, size_t out_capacity);
+/* Prompt ingestion (engine.rs:625-631 runs forward_token for each prompt position): the n tokens at positions
+ * pos0 .. pos0 + n - 1 (positions below pos0 must already be in the KV cache) pass each layer together, their
+ * projections as batched GEMMs on the matrix cores (vx_gemm_i32_dev), in chunks of up to 512 tokens. The KV cache, the
+ * logits of the last position (logits, may be NULL) and its greedy token (out_next, may be NULL) are bit-identical to n
+ * calls of vx_decoder_step; the next step continues at pos0 + n. VX_ERR_CONTEXT_OVERFLOW beyond max_ctx. */
+int vx_decoder_prefill(vx_decoder_t* decoder, const uint32_t* tokens, size_t n, uint32_t pos0, float* logits,
+                       size_t logits_capacity, uint32_t* out_next);
+/* The cached f16 key and value of (layer, pos, kv_head): head_dim values each into k and v (host, either may be NULL;
+ * n >= head_dim). KVCache::get_key / get_val (quintrit-runtime/src/kv_cache.rs:142-155). */
+int vx_decoder_kv_get(const vx_decoder_t* decoder, uint32_t layer, uint32_t pos, uint32_t kv_head, uint16_t* k,
+                      uint16_t* v, size_t n);
 /* Device bytes held by the decoder (weights, KV cache, work buffers). */
 int vx_decoder_memory_bytes(const vx_decoder_t* decoder, size_t* out_bytes);
 /* The decoder's configuration (the shape part of quintrit_model_info, quintrit.h:323-340); out_config->struct_size must be

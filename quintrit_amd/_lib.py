@@ -84,6 +84,9 @@ SIGNATURES = {
     "vx_decoder_set_head": (_i32, [_vp, _vp, _sz]),
     "vx_decoder_step": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _sz, _vp]),
     "vx_decoder_generate": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz]),
+    "vx_decoder_generate_stepwise": (_i32, [_vp, _vp, _sz, _sz, _vp, _sz]),
+    "vx_decoder_prefill": (_i32, [_vp, _vp, _sz, ctypes.c_uint32, _vp, _sz, _vp]),
+    "vx_decoder_kv_get": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp, _sz]),
     "vx_decoder_memory_bytes": (_i32, [_vp, _vp]),
     "vx_decoder_config": (_i32, [_vp, _vp]),
     "vx_decoder_adopt_projection": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp]),

@@ -197,6 +197,8 @@ struct StageInput {
     // kInPlain without a norm: the largest |v| as float bits, accumulated by the producing gated pair; each workgroup
     // then reads only the elements of its own K slice
     const uint32_t* amax;
+    // kInEmbed in a prefill: the token of this row (the decode step takes it from the loop state instead)
+    const uint32_t* token_at;
 };
 
 // The loaded inputs of a thread: element e of float4 group k is 4 (tid + k kNT) + e. P4 groups cover P4 * 4 kNT
@@ -228,8 +230,13 @@ template <int P4, int SA, int SB>
 __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA, SB>& r, uint32_t wlo, uint32_t whi) {
     const uint32_t tid = threadIdx.x, n = p.n;
     if (p.kind == kInEmbed) {
-        const uint32_t pos = p.ctl->pos;
-        const uint32_t tok = pos < p.ctl->n_prompt ? p.prompt[pos] : p.ctl->token;
+        uint32_t tok;
+        if (p.token_at != nullptr) {
+            tok = *p.token_at;
+        } else {
+            const uint32_t pos = p.ctl->pos;
+            tok = pos < p.ctl->n_prompt ? p.prompt[pos] : p.ctl->token;
+        }
         const uint2* row = reinterpret_cast<const uint2*>(p.emb + static_cast<size_t>(tok) * n);
 #pragma unroll
         for (int k = 0; k < P4; ++k) {
@@ -799,6 +806,10 @@ struct AttnArgs {
     uint32_t n_heads, gqa, max_ctx;
     uint32_t rope_normal;  // 1: pairs (2i, 2i + 1) (RopeMode::Normal), 0: (i, i + head_dim / 2) (NEOX)
     float scale;
+    // prefill: n_tok tokens at positions ctl->pos + 1 - n_tok .. ctl->pos, their rotated f16 queries in
+    // qbuf[token][n_heads * head_dim] and their k, v already in the cache; out is [token][n_heads * head_dim]
+    const uint16_t* qbuf;
+    uint32_t n_tok;
 };
 
 constexpr uint32_t kAttnMaxCtx = 4096;  // KV positions held in LDS (scores, running maxima)
@@ -825,7 +836,9 @@ __device__ __forceinline__ float r16(float x) { return static_cast<float>(static
 // Wave w accumulates chunk w / 2, coordinates (HD / 2) (w % 2) .. + HD / 2 - 1, HD / 128 per lane (independent
 // chains), with V streamed through LDS in windows of kWin positions, the next window loaded while the current one is
 // consumed.
-template <int HD>
+// PREFILL: blockIdx.y is a token of a prefill; its query comes rotated from qbuf and its own k, v from the cache (written
+// by pf_rope_kernel), so nothing is appended here. The rest is the same arithmetic for every token.
+template <int HD, bool PREFILL>
 __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) {
     constexpr uint32_t kHalf = HD / 2;         // coordinates of a wave
     constexpr int kPerLane = HD / 128;         // coordinates of a lane
@@ -842,7 +855,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t kvh = h / a.gqa;
-    const uint32_t pos = a.ctl->pos;
+    const uint32_t tok = PREFILL ? blockIdx.y : 0u;
+    const uint32_t pos = PREFILL ? a.ctl->pos + 1u - a.n_tok + tok : a.ctl->pos;
     const uint32_t seq = pos + 1;
     const uint16_t* kb = a.kc + static_cast<size_t>(kvh) * a.max_ctx * HD;
     const uint16_t* vb = a.vc + static_cast<size_t>(kvh) * a.max_ctx * HD;
@@ -860,7 +874,13 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         en = min(min(st + chunk, n_kv), seq);
     }
 
-    {
+    if (PREFILL) {
+        if (tid < HD) {
+            qs[tid] = a.qbuf[(static_cast<size_t>(tok) * a.n_heads + h) * HD + tid];
+            kp[tid] = kb[static_cast<size_t>(pos) * HD + tid];
+            vp[tid] = vb[static_cast<size_t>(pos) * HD + tid];
+        }
+    } else {
         const float* cache = a.rope + static_cast<size_t>(pos) * HD;
         if (tid < HD) {  // q (tid < HD / 2) or k: the rotation of pair i
             const bool isq = tid < kHalf;
@@ -886,7 +906,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         }
     }
     __syncthreads();
-    if (h % a.gqa == 0 && tid < HD) {
+    if (!PREFILL && h % a.gqa == 0 && tid < HD) {
         a.kc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + tid] = kp[tid];
         a.vc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + tid] = vp[tid];
     }
@@ -1072,7 +1092,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         window(base, ra);
         if (base + kWin < en) window(base + kWin, rb);
     }
-    float* out = a.out + static_cast<size_t>(h) * HD;
+    float* out = a.out + (static_cast<size_t>(tok) * a.n_heads + h) * HD;
     if (!split) {
         if (c == 0) {
             const float s_inv = ssum == 0.0f ? 0.0f : 1.0f / ssum;
@@ -1236,6 +1256,182 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
     a.ctl->pos = pos + 1;
 }
 
+// ---- prefill: the prompt's tokens in one pass per layer ---------------------------------------------------------------------
+//
+// The reference ingests a prompt one forward_token per position (quintrit-runtime/src/engine.rs:627-630). A prefill
+// runs n tokens through each layer at once: the projections as one batched GEMM per matrix (vx_gemm.hip, exact int32,
+// the same sums as n GEMVs), everything else per token with the decode step's arithmetic (stage_y, the quantizer, the
+// epilogue, RoPE, the attention kernel), so that the KV cache, the logits and the greedy token equal those of n decode
+// steps bit for bit. Positions: the loop state's pos is the last token's (ctl->pos + 1 - n_tok + t for token t).
+
+// One workgroup per token: the token's stage input (embedding row, residual add or a plain vector, with the RMSNorm
+// when gamma is set) and its per-token absmax int8 codes (quantize_activations_int8_with_range, ops.rs:241-267) into
+// codes[t], its scale into as_out[t]. An input with x_out writes the new residual row in place.
+struct PfStageArgs {
+    StageInput in;          // the input of token 0; rows of x_in / x_out are x_stride floats apart, of a.part a_stride
+    uint32_t x_stride, a_stride, n_tok;
+    const uint32_t* prompt;  // kInEmbed: the token at each position
+    int8_t* codes;          // [n_tok][codes_stride]
+    uint32_t codes_stride;
+    float* as_out;          // [n_tok]
+};
+
+template <int P4, int SA>
+__global__ __launch_bounds__(kNT) void pf_stage_kernel(PfStageArgs a) {
+    __shared__ InputLds s;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    StageInput in = a.in;
+    if (in.x_in != nullptr) in.x_in += static_cast<size_t>(t) * a.x_stride;
+    if (in.x_out != nullptr) in.x_out += static_cast<size_t>(t) * a.x_stride;
+    if (in.kind == kInResidual) {
+        in.a.part += static_cast<size_t>(t) * a.a_stride;
+        in.a.as += t;
+    }
+    if (in.kind == kInEmbed) in.token_at = a.prompt + (in.ctl->pos + 1u - a.n_tok + t);
+    InputRegs<P4, SA, 0> r{};
+    stage_load(in, r, 0u, in.n);
+    float y[P4][4];
+    stage_y(in, r, s, true, y);
+    float mx = 0.0f;  // the largest |y|; NaN never counts (as in stage_window)
+#pragma unroll
+    for (int k = 0; k < P4; ++k)
+        if (elem4(tid, k) < in.n) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ay = __builtin_fabsf(y[k][e]);
+                if (ay > mx) mx = ay;
+            }
+        }
+    mx = wave_max_f32(mx);
+    if (lane == 0) s.red_f[wave] = mx;
+    __syncthreads();
+    float m = 0.0f;
+    for (int w = 0; w < kNT / 64; ++w) m = fmax_nn(m, s.red_f[w]);
+    const float sc = m > 0.0f ? 127.0f / m : 0.0f;
+    int8_t* row = a.codes + static_cast<size_t>(t) * a.codes_stride;
+#pragma unroll
+    for (int k = 0; k < P4; ++k) {
+        const uint32_t i = elem4(tid, k);
+        if (i < in.n) {
+            uint32_t w4 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int x = m > 0.0f ? quant_code(y[k][e], sc) : 0;
+                w4 |= (static_cast<uint32_t>(x) & 0xffu) << (8 * e);
+            }
+            *reinterpret_cast<uint32_t*>(row + i) = w4;
+        }
+    }
+    if (tid == 0) a.as_out[t] = sc;
+}
+
+// RoPE of every token's q and k and the KV append (the first part of attention_kernel, for n tokens): q, k, v of token
+// t from the GEMM outputs with the layer epilogue (layer.rs:246-253), rotated at the token's position (ops.rs:199-221),
+// rounded to f16; k and v into the cache, q into qbuf.
+struct PfRopeArgs {
+    const Ctl* ctl;
+    uint32_t n_tok;
+    const int32_t *yq, *yk, *yv;  // [n_tok][ld*]
+    uint32_t ldq, ldk, ldv;
+    const float* as;              // [n_tok] activation scale of the q/k/v input
+    float wsq, wsk, wsv;
+    const float* rope;            // [max_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i + 1
+    uint16_t *kc, *vc;            // this layer: [kv_head][max_ctx][head_dim]
+    uint16_t* qbuf;               // [n_tok][n_heads * head_dim]
+    uint32_t n_heads, n_kv, hd, max_ctx, rope_normal;
+};
+
+__global__ __launch_bounds__(256) void pf_rope_kernel(PfRopeArgs a) {
+    const uint32_t t = blockIdx.x;
+    const uint32_t pos = a.ctl->pos + 1u - a.n_tok + t;
+    const float as = a.as[t];
+    const bool zero = !(as > 0.0f);
+    const float pq = zero ? 0.0f : a.wsq / as, pk = zero ? 0.0f : a.wsk / as, pv = zero ? 0.0f : a.wsv / as;
+    const uint32_t half = a.hd / 2u, nq = a.n_heads * half, nk = a.n_kv * half, nv = a.n_kv * a.hd;
+    const float* cache = a.rope + static_cast<size_t>(pos) * a.hd;
+    for (uint32_t i = threadIdx.x; i < nq + nk + nv; i += blockDim.x) {
+        if (i < nq + nk) {
+            const bool isq = i < nq;
+            const uint32_t j = isq ? i : i - nq, head = j / half, pr = j - head * half;
+            const uint32_t i0 = a.rope_normal ? 2u * pr : pr, i1 = a.rope_normal ? 2u * pr + 1u : pr + half;
+            const int32_t* y = isq ? a.yq + static_cast<size_t>(t) * a.ldq : a.yk + static_cast<size_t>(t) * a.ldk;
+            const float post = isq ? pq : pk;
+            const float x0 = proj_value(y[head * a.hd + i0], post, zero), x1 = proj_value(y[head * a.hd + i1], post, zero);
+            const float cc = cache[2 * pr], ss = cache[2 * pr + 1];
+            const float x1s = x1 * ss, x1c = x1 * cc;
+            const float y0 = __builtin_fmaf(x0, cc, -x1s);
+            const float y1 = __builtin_fmaf(x0, ss, x1c);
+            uint16_t* dst = isq ? a.qbuf + (static_cast<size_t>(t) * a.n_heads + head) * a.hd
+                                : a.kc + (static_cast<size_t>(head) * a.max_ctx + pos) * a.hd;
+            dst[i0] = f32_f16(y0);
+            dst[i1] = f32_f16(y1);
+        } else {
+            const uint32_t j = i - nq - nk, head = j / a.hd, e = j - head * a.hd;
+            a.vc[(static_cast<size_t>(head) * a.max_ctx + pos) * a.hd + e] =
+                f32_f16(proj_value(a.yv[static_cast<size_t>(t) * a.ldv + j], pv, zero));
+        }
+    }
+}
+
+// The gated activation of every token (model.rs:155-170): g and u from the gate and up GEMM outputs with their layer
+// epilogues, then relu2(g) * u (ops.rs:301-308) or swiglu (ops.rs:430-464: ggml's vector expf for the whole blocks
+// of 8, libm's expf for the last ffn % 8 values), as the decode step's gated pair computes them.
+struct PfActArgs {
+    const int32_t *yg, *yu;  // [n_tok][ld]
+    uint32_t ld;
+    const float* as;         // [n_tok]
+    float wsg, wsu;
+    float* out;              // [n_tok][ffn]
+    uint32_t ffn, n8, act;
+};
+
+__global__ __launch_bounds__(256) void pf_act_kernel(PfActArgs a) {
+    const uint32_t t = blockIdx.y, i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= a.ffn) return;
+    const float as = a.as[t];
+    const bool zero = !(as > 0.0f);
+    const float g = zero ? 0.0f : static_cast<float>(a.yg[static_cast<size_t>(t) * a.ld + i]) * (a.wsg / as);
+    const float u = zero ? 0.0f : static_cast<float>(a.yu[static_cast<size_t>(t) * a.ld + i]) * (a.wsu / as);
+    float o;
+    if (a.act == kActSilu) {
+        const float ex = i < a.n8 ? ggml_expf(0.0f - g) : glibc_expf(-g);
+        const float den = 1.0f + ex;
+        const float sl = g / den;
+        o = sl * u;
+    } else {
+        const float pos = g > 0.0f ? g : 0.0f;
+        const float sq = pos * pos;
+        o = sq * u;
+    }
+    a.out[static_cast<size_t>(t) * a.ffn + i] = o;
+}
+
+// Sets the loop state from kernel arguments (no host buffer is read when the kernel runs).
+__global__ void set_ctl_kernel(Ctl* ctl, uint32_t pos, uint32_t token, uint32_t n_prompt, uint32_t n_out) {
+    if (threadIdx.x == 0) {
+        ctl->pos = pos;
+        ctl->token = token;
+        ctl->n_prompt = n_prompt;
+        ctl->n_out = n_out;
+    }
+}
+
+int launch_pf_stage(const PfStageArgs& a, hipStream_t s) {
+    const bool res = a.in.kind == kInResidual;
+    if (a.in.n <= 4u * kNT) {
+        if (res) hipLaunchKernelGGL((pf_stage_kernel<1, 1>), dim3(a.n_tok), dim3(kNT), 0, s, a);
+        else hipLaunchKernelGGL((pf_stage_kernel<1, 0>), dim3(a.n_tok), dim3(kNT), 0, s, a);
+    } else if (a.in.n <= 8u * kNT) {
+        if (res) hipLaunchKernelGGL((pf_stage_kernel<2, 1>), dim3(a.n_tok), dim3(kNT), 0, s, a);
+        else hipLaunchKernelGGL((pf_stage_kernel<2, 0>), dim3(a.n_tok), dim3(kNT), 0, s, a);
+    } else {
+        if (res || a.in.gamma != nullptr) VX_FAIL(VX_ERR_INTERNAL, "a prefill input of %u elements needs a norm", a.in.n);
+        hipLaunchKernelGGL((pf_stage_kernel<kPlainMax / (4 * kNT), 0>), dim3(a.n_tok), dim3(kNT), 0, s, a);
+    }
+    VX_HIP(hipGetLastError());
+    return VX_OK;
+}
+
 // ---- launches ----------------------------------------------------------------------------------------------------------------
 
 // dgemv_kernel instances (DStageArgs::variant): inputs of up to 4096 and 8192 elements of every kind, and plain or
@@ -1269,9 +1465,18 @@ int launch_dgemv(const DStageArgs& a, hipStream_t s) {
 
 int launch_attention(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
     if (head_dim == 256)
-        hipLaunchKernelGGL(attention_kernel<256>, dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
+        hipLaunchKernelGGL((attention_kernel<256, false>), dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
     else
-        hipLaunchKernelGGL(attention_kernel<128>, dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
+        hipLaunchKernelGGL((attention_kernel<128, false>), dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
+    VX_HIP(hipGetLastError());
+    return VX_OK;
+}
+
+int launch_attention_prefill(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
+    if (head_dim == 256)
+        hipLaunchKernelGGL((attention_kernel<256, true>), dim3(a.n_heads, a.n_tok), dim3(kAttnWaves * 64), 0, s, a);
+    else
+        hipLaunchKernelGGL((attention_kernel<128, true>), dim3(a.n_heads, a.n_tok), dim3(kAttnWaves * 64), 0, s, a);
     VX_HIP(hipGetLastError());
     return VX_OK;
 }
@@ -1333,6 +1538,26 @@ struct vx_decoder {
     uint32_t* d_prompt;
     uint32_t* d_tokens;
     std::vector<vx::DStageArgs> stages;  // [layer * 4 + stage]
+    // prefill: buffers for chunks of up to pf_cap tokens, and the recorded chunk graphs by (tokens, with head)
+    uint32_t pf_cap;
+    float* pf_x;                      // [pf_cap][hidden] residual stream
+    int8_t* pf_codes;                 // [pf_cap][pf_codes_ld] int8 inputs of a GEMM
+    uint32_t pf_codes_ld;
+    float* pf_as;                     // [4][pf_cap] activation scales of the q/k/v, o, gate/up and down inputs
+    int32_t* pf_y[vx::kProjKinds];    // [pf_cap][pf_ld[kind]] GEMM outputs
+    uint32_t pf_ld[vx::kProjKinds];
+    uint16_t* pf_q;                   // [pf_cap][n_heads * head_dim] rotated f16 queries
+    float* pf_att;                    // [pf_cap][n_heads * head_dim] attention outputs
+    float* pf_act;                    // [pf_cap][ffn] gated activations
+    uint8_t* pf_staged;               // the GEMM's staged activations
+    uint8_t* pf_part;                 // the GEMM's K-slice partial sums
+    struct PfGraph {
+        uint32_t n;
+        bool head;
+        hipGraph_t graph;
+        hipGraphExec_t exec;
+    };
+    std::vector<PfGraph> pf_graphs;
     vx::Ctl* h_ctl;                   // pinned
     hipStream_t stream;
     hipGraph_t graph;
@@ -1363,10 +1588,35 @@ static void drop_graph(vx_decoder* d) {
     d->exec = nullptr;
     d->graph = nullptr;
     d->ready = false;
+    for (auto& g : d->pf_graphs) {
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        if (g.graph) (void)hipGraphDestroy(g.graph);
+    }
+    d->pf_graphs.clear();
+}
+
+static void free_prefill(vx_decoder* d) {
+    void* bufs[] = {d->pf_x, d->pf_codes, d->pf_as, d->pf_q, d->pf_att, d->pf_act, d->pf_staged, d->pf_part};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    for (int32_t*& y : d->pf_y) {
+        if (y) (void)hipFree(y);
+        y = nullptr;
+    }
+    d->pf_x = nullptr;
+    d->pf_codes = nullptr;
+    d->pf_as = nullptr;
+    d->pf_q = nullptr;
+    d->pf_att = nullptr;
+    d->pf_act = nullptr;
+    d->pf_staged = nullptr;
+    d->pf_part = nullptr;
+    d->pf_cap = 0;
 }
 
 static void destroy_decoder(vx_decoder* d) {
     drop_graph(d);
+    free_prefill(d);
     for (auto* m : d->proj)
         if (m) {
             m->owner = nullptr;
@@ -1726,6 +1976,239 @@ static int record_step(const vx_decoder* d, hipStream_t st) {
     return launch_head(h, c.emb_f16 != 0, grid, st);
 }
 
+// ---- prefill ---------------------------------------------------------------------------------------------------------------
+
+constexpr uint32_t kPrefillChunk = 512;  // tokens per prefill pass; longer prompts run in several
+
+// The prefill buffers, sized for chunks of pf_cap tokens (allocated on the first prefill).
+static int ensure_prefill(vx_decoder* d) {
+    if (d->pf_cap) return VX_OK;
+    const vx_decoder_config_t& c = d->cfg;
+    const uint32_t cap = std::min<uint32_t>(kPrefillChunk, c.max_ctx);
+    const size_t widest = std::max({static_cast<size_t>(c.hidden), d->qd, static_cast<size_t>(c.ffn)});
+    d->pf_codes_ld = static_cast<uint32_t>(round_up(widest, 16));
+    size_t stage_bytes = 0, part_bytes = 0;
+    for (size_t cols : {static_cast<size_t>(c.hidden), d->qd, static_cast<size_t>(c.ffn)})
+        stage_bytes = std::max(stage_bytes, gemm_stage_bytes(cols, cap));
+    for (int k = 0; k < kProjKinds; ++k) {
+        const Geometry& g = d->proj[k]->g;  // every layer's projection k has this shape
+        for (uint32_t m = 1; m <= cap; ++m) part_bytes = std::max(part_bytes, gemm_part_bytes(g, m, d->num_cus));
+    }
+    hipError_t e = hipSuccess;
+    auto grab = [&](auto** p, size_t bytes) {
+        if (e == hipSuccess) e = dalloc(d, p, std::max<size_t>(bytes, 256));
+    };
+    grab(&d->pf_x, static_cast<size_t>(cap) * c.hidden * 4);
+    grab(&d->pf_codes, static_cast<size_t>(cap) * d->pf_codes_ld);
+    grab(&d->pf_as, 4u * cap * 4);
+    for (int k = 0; k < kProjKinds; ++k) {
+        d->pf_ld[k] = static_cast<uint32_t>(round_up(proj_rows(d, k), 4));
+        grab(&d->pf_y[k], static_cast<size_t>(cap) * d->pf_ld[k] * 4);
+    }
+    grab(&d->pf_q, static_cast<size_t>(cap) * d->qd * 2);
+    grab(&d->pf_att, static_cast<size_t>(cap) * d->qd * 4);
+    grab(&d->pf_act, static_cast<size_t>(cap) * c.ffn * 4);
+    grab(&d->pf_staged, stage_bytes);
+    grab(&d->pf_part, part_bytes);
+    if (e != hipSuccess) {
+        free_prefill(d);
+        VX_FAIL(VX_ERR_DEVICE, "prefill buffers: %s", hipGetErrorString(e));
+    }
+    d->pf_cap = cap;
+    return VX_OK;
+}
+
+// The output of projection `kind` of `layer` for token 0 of a prefill (kslices 1; token t is t * pf_ld[kind] further).
+static ProjOut pf_proj_out(const vx_decoder* d, size_t layer, int kind, const float* as) {
+    ProjOut o{};
+    o.part = d->pf_y[kind];
+    o.as = as;
+    o.ws = d->proj[layer * kProjKinds + kind]->weight_scale;
+    o.kslices = 1;
+    o.stride = d->pf_ld[kind];
+    return o;
+}
+
+// Enqueues one prefill pass over n tokens (the last at the loop state's position) on `st`; with `head`, the final norm,
+// head and greedy argmax of the last token follow and advance the loop state as a decode step does.
+static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_t st) {
+    const vx_decoder_config_t& c = d->cfg;
+    const size_t L = c.n_layers, H = c.hidden, F = c.ffn;
+    const bool sub = has_sub_norms(d);
+    const size_t layer_kv = d->kvd * c.max_ctx;
+    const uint32_t cap = d->pf_cap;
+    float* as_qkv = d->pf_as;
+    float* as_o = d->pf_as + cap;
+    float* as_ffn = d->pf_as + 2 * cap;
+    float* as_down = d->pf_as + 3 * cap;
+    auto stage = [&](const StageInput& in, uint32_t x_stride, uint32_t a_stride, float* as_out) -> int {
+        PfStageArgs a{};
+        a.in = in;
+        a.x_stride = x_stride;
+        a.a_stride = a_stride;
+        a.n_tok = n;
+        a.prompt = d->d_prompt;
+        a.codes = d->pf_codes;
+        a.codes_stride = d->pf_codes_ld;
+        a.as_out = as_out;
+        return launch_pf_stage(a, st);
+    };
+    auto gemm = [&](size_t layer, int kind) -> int {
+        const vx_matrix* m = d->proj[layer * kProjKinds + kind];
+        return launch_gemm_staged(m->d_w, m->g, d->num_cus, d->pf_staged, n, d->pf_y[kind], d->pf_ld[kind], d->pf_part, st);
+    };
+    for (size_t l = 0; l < L; ++l) {
+        const float* const* nw = d->norms.data() + l * kNormKinds;
+        // the attention input: the embedding or the residual of the previous layer, the attention norm
+        StageInput in;
+        if (l == 0) {
+            in = stage_input(d, kInEmbed, H, nullptr, d->pf_x, nw[VX_NORM_ATTN]);
+            in.ctl = d->d_ctl;
+            in.emb = d->d_emb;
+        } else {
+            in = stage_input(d, kInResidual, H, d->pf_x, d->pf_x, nw[VX_NORM_ATTN]);
+            in.a = pf_proj_out(d, l - 1, VX_PROJ_DOWN, as_down);
+        }
+        VX_TRY(stage(in, static_cast<uint32_t>(H), d->pf_ld[VX_PROJ_DOWN], as_qkv));
+        VX_TRY(launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, H, d->pf_staged, st));
+        for (int k : {VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}) VX_TRY(gemm(l, k));
+        PfRopeArgs ra{};
+        ra.ctl = d->d_ctl;
+        ra.n_tok = n;
+        ra.yq = d->pf_y[VX_PROJ_Q];
+        ra.yk = d->pf_y[VX_PROJ_K];
+        ra.yv = d->pf_y[VX_PROJ_V];
+        ra.ldq = d->pf_ld[VX_PROJ_Q];
+        ra.ldk = d->pf_ld[VX_PROJ_K];
+        ra.ldv = d->pf_ld[VX_PROJ_V];
+        ra.as = as_qkv;
+        ra.wsq = d->proj[l * kProjKinds + VX_PROJ_Q]->weight_scale;
+        ra.wsk = d->proj[l * kProjKinds + VX_PROJ_K]->weight_scale;
+        ra.wsv = d->proj[l * kProjKinds + VX_PROJ_V]->weight_scale;
+        ra.rope = d->d_rope;
+        ra.kc = d->d_kc + l * layer_kv;
+        ra.vc = d->d_vc + l * layer_kv;
+        ra.qbuf = d->pf_q;
+        ra.n_heads = c.n_heads;
+        ra.n_kv = c.n_kv_heads;
+        ra.hd = c.head_dim;
+        ra.max_ctx = c.max_ctx;
+        ra.rope_normal = c.rope_mode == VX_ROPE_NORMAL ? 1u : 0u;
+        hipLaunchKernelGGL(pf_rope_kernel, dim3(n), dim3(256), 0, st, ra);
+        VX_HIP(hipGetLastError());
+        AttnArgs at{};
+        at.ctl = d->d_ctl;
+        at.kc = d->d_kc + l * layer_kv;
+        at.vc = d->d_vc + l * layer_kv;
+        at.out = d->pf_att;
+        at.n_heads = c.n_heads;
+        at.gqa = c.n_heads / c.n_kv_heads;
+        at.max_ctx = c.max_ctx;
+        at.rope_normal = ra.rope_normal;
+        at.scale = 1.0f / sqrtf(static_cast<float>(c.head_dim));
+        at.qbuf = d->pf_q;
+        at.n_tok = n;
+        VX_TRY(launch_attention_prefill(at, c.head_dim, st));
+        // the o input: attention output (sub-norm or none)
+        in = stage_input(d, kInPlain, d->qd, d->pf_att, nullptr, sub ? nw[VX_NORM_ATTN_SUB] : nullptr);
+        VX_TRY(stage(in, static_cast<uint32_t>(d->qd), 0, as_o));
+        VX_TRY(launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, d->qd, d->pf_staged, st));
+        VX_TRY(gemm(l, VX_PROJ_O));
+        // x + o, FFN norm
+        in = stage_input(d, kInResidual, H, d->pf_x, d->pf_x, nw[VX_NORM_FFN]);
+        in.a = pf_proj_out(d, l, VX_PROJ_O, as_o);
+        VX_TRY(stage(in, static_cast<uint32_t>(H), d->pf_ld[VX_PROJ_O], as_ffn));
+        VX_TRY(launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, H, d->pf_staged, st));
+        VX_TRY(gemm(l, VX_PROJ_GATE));
+        VX_TRY(gemm(l, VX_PROJ_UP));
+        PfActArgs aa{};
+        aa.yg = d->pf_y[VX_PROJ_GATE];
+        aa.yu = d->pf_y[VX_PROJ_UP];
+        aa.ld = d->pf_ld[VX_PROJ_GATE];
+        aa.as = as_ffn;
+        aa.wsg = d->proj[l * kProjKinds + VX_PROJ_GATE]->weight_scale;
+        aa.wsu = d->proj[l * kProjKinds + VX_PROJ_UP]->weight_scale;
+        aa.out = d->pf_act;
+        aa.ffn = static_cast<uint32_t>(F);
+        aa.n8 = static_cast<uint32_t>(F / 8 * 8);
+        aa.act = c.act == VX_ACT_SILU ? kActSilu : kActRelu2;
+        hipLaunchKernelGGL(pf_act_kernel, dim3(static_cast<uint32_t>((F + 255) / 256), n), dim3(256), 0, st, aa);
+        VX_HIP(hipGetLastError());
+        // the down input: the gated activation (sub-norm or none)
+        in = stage_input(d, kInPlain, F, d->pf_act, nullptr, sub ? nw[VX_NORM_FFN_SUB] : nullptr);
+        VX_TRY(stage(in, static_cast<uint32_t>(F), 0, as_down));
+        VX_TRY(launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, F, d->pf_staged, st));
+        VX_TRY(gemm(l, VX_PROJ_DOWN));
+    }
+    if (!head) return VX_OK;
+    HeadArgs h{};
+    h.in = stage_input(d, kInResidual, c.hidden, d->pf_x + static_cast<size_t>(n - 1) * H, nullptr, d->norms[L * kNormKinds]);
+    h.in.a = pf_proj_out(d, L - 1, VX_PROJ_DOWN, as_down + (n - 1));
+    h.in.a.part = d->pf_y[VX_PROJ_DOWN] + static_cast<size_t>(n - 1) * d->pf_ld[VX_PROJ_DOWN];
+    h.w = c.untied ? d->d_head : d->d_emb;
+    h.hidden = c.hidden;
+    h.vocab = c.vocab;
+    h.logits = d->d_logits;
+    h.ctl = d->d_ctl;
+    h.out_tokens = d->d_tokens;
+    h.key = d->d_key;
+    h.ticket = d->d_ticket;
+    const uint32_t rows_per_wg = kNT / 4;
+    const uint32_t grid = std::min<uint32_t>((c.vocab + rows_per_wg - 1) / rows_per_wg, static_cast<uint32_t>(d->num_cus));
+    return launch_head(h, c.emb_f16 != 0, grid, st);
+}
+
+// The graph of a prefill pass over n tokens (recorded on first use; a few are kept).
+static int prefill_graph(vx_decoder* d, uint32_t n, bool head, hipGraphExec_t* out) {
+    for (const auto& g : d->pf_graphs)
+        if (g.n == n && g.head == head) {
+            *out = g.exec;
+            return VX_OK;
+        }
+    if (d->pf_graphs.size() >= 4) {
+        auto& g = d->pf_graphs.front();
+        (void)hipGraphExecDestroy(g.exec);
+        (void)hipGraphDestroy(g.graph);
+        d->pf_graphs.erase(d->pf_graphs.begin());
+    }
+    VX_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+    const int st = record_prefill(d, n, head, d->stream);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(d->stream, &graph);
+    if (st != VX_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return st;
+    }
+    VX_HIP(e);
+    hipGraphExec_t exec = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (ei != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        VX_HIP(ei);
+    }
+    d->pf_graphs.push_back({n, head, graph, exec});
+    *out = exec;
+    return VX_OK;
+}
+
+// Prefills positions pos0 .. pos0 + n - 1 with the tokens already in d_prompt at those positions, in chunks of pf_cap;
+// the last chunk ends with the head (greedy token and logits of the last position). n_prompt and n_out are the loop
+// state's (the head records the token generated after position n_prompt - 1 as out_tokens[0]).
+static int run_prefill(vx_decoder* d, uint32_t pos0, uint32_t n, uint32_t n_prompt, uint32_t n_out) {
+    VX_TRY(ensure_prefill(d));
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t m = std::min(d->pf_cap, n - done);
+        const bool last = done + m == n;
+        hipGraphExec_t exec = nullptr;
+        VX_TRY(prefill_graph(d, m, last, &exec));
+        hipLaunchKernelGGL(set_ctl_kernel, dim3(1), dim3(64), 0, d->stream, d->d_ctl, pos0 + done + m - 1, 0u, n_prompt, n_out);
+        VX_HIP(hipGetLastError());
+        VX_HIP(hipGraphLaunch(exec, d->stream));
+        done += m;
+    }
+    return VX_OK;
+}
+
 static bool norm_needed(const vx_decoder* d, size_t layer, int kind) {
     if (layer == d->cfg.n_layers) return kind == VX_NORM_ATTN;
     return has_sub_norms(d) || (kind != VX_NORM_ATTN_SUB && kind != VX_NORM_FFN_SUB);
@@ -1920,10 +2403,82 @@ int vx_decoder_generate(vx_decoder_t* d, const uint32_t* prompt, size_t n_prompt
         VX_TRY(set_device(d->device));
         VX_TRY(prepare(d));
         VX_HIP(hipMemcpy(d->d_prompt, prompt, n_prompt * 4, hipMemcpyHostToDevice));
+        // the prompt in prefill passes (their last head gives the first new token), then one step per further token
+        VX_TRY(run_prefill(d, 0, static_cast<uint32_t>(n_prompt), static_cast<uint32_t>(n_prompt), static_cast<uint32_t>(n_new)));
+        for (size_t i = n_prompt; i < steps; ++i) VX_HIP(hipGraphLaunch(d->exec, d->stream));
+        VX_HIP(hipStreamSynchronize(d->stream));
+        if (n_new) VX_HIP(hipMemcpy(out_tokens, d->d_tokens, n_new * 4, hipMemcpyDeviceToHost));
+        return VX_OK;
+    });
+}
+
+int vx_decoder_generate_stepwise(vx_decoder_t* d, const uint32_t* prompt, size_t n_prompt, size_t n_new,
+                                 uint32_t* out_tokens, size_t out_capacity) {
+    return guard([&]() -> int {
+        VX_TRY(check_decoder(d));
+        std::lock_guard<std::mutex> lk(d->mu);
+        if (n_prompt == 0) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the prompt is empty");
+        if (prompt == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "prompt is NULL");
+        if (n_new > 0 && out_tokens == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_tokens is NULL");
+        if (out_capacity < n_new) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "out_tokens holds %zu values, %zu requested", out_capacity, n_new);
+        const size_t steps = n_new ? n_prompt + n_new - 1 : n_prompt;
+        if (steps > d->cfg.max_ctx)
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "prompt (%zu) + new tokens (%zu) exceed the context of %u", n_prompt, n_new, d->cfg.max_ctx);
+        for (size_t i = 0; i < n_prompt; ++i)
+            if (prompt[i] >= d->cfg.vocab) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "prompt[%zu] = %u out of range (vocab %u)", i, prompt[i], d->cfg.vocab);
+        VX_TRY(set_device(d->device));
+        VX_TRY(prepare(d));
+        VX_HIP(hipMemcpy(d->d_prompt, prompt, n_prompt * 4, hipMemcpyHostToDevice));
         VX_TRY(put_ctl(d, 0, 0, static_cast<uint32_t>(n_prompt), static_cast<uint32_t>(n_new)));
         for (size_t i = 0; i < steps; ++i) VX_HIP(hipGraphLaunch(d->exec, d->stream));
         VX_HIP(hipStreamSynchronize(d->stream));
         if (n_new) VX_HIP(hipMemcpy(out_tokens, d->d_tokens, n_new * 4, hipMemcpyDeviceToHost));
+        return VX_OK;
+    });
+}
+
+int vx_decoder_prefill(vx_decoder_t* d, const uint32_t* tokens, size_t n, uint32_t pos0, float* logits,
+                       size_t logits_capacity, uint32_t* out_next) {
+    return guard([&]() -> int {
+        VX_TRY(check_decoder(d));
+        std::lock_guard<std::mutex> lk(d->mu);
+        if (n == 0) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "no tokens to prefill");
+        if (tokens == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "tokens is NULL");
+        if (pos0 > d->cfg.max_ctx || n > d->cfg.max_ctx - pos0)
+            VX_FAIL(VX_ERR_CONTEXT_OVERFLOW, "positions %u .. %zu exceed the context of %u", pos0, pos0 + n - 1, d->cfg.max_ctx);
+        if (logits && logits_capacity < d->cfg.vocab)
+            VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "logits hold %zu values but vocab = %u", logits_capacity, d->cfg.vocab);
+        for (size_t i = 0; i < n; ++i)
+            if (tokens[i] >= d->cfg.vocab) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "tokens[%zu] = %u out of range (vocab %u)", i, tokens[i], d->cfg.vocab);
+        VX_TRY(set_device(d->device));
+        VX_TRY(prepare(d));
+        VX_HIP(hipMemcpy(d->d_prompt + pos0, tokens, n * 4, hipMemcpyHostToDevice));
+        // n_prompt beyond every position: the head records no generated token
+        VX_TRY(run_prefill(d, pos0, static_cast<uint32_t>(n), 0xffffffffu, 0u));
+        VX_HIP(hipStreamSynchronize(d->stream));
+        if (logits) VX_HIP(hipMemcpy(logits, d->d_logits, static_cast<size_t>(d->cfg.vocab) * 4, hipMemcpyDeviceToHost));
+        if (out_next) {
+            Ctl c{};
+            VX_HIP(hipMemcpy(&c, d->d_ctl, sizeof c, hipMemcpyDeviceToHost));
+            *out_next = c.token;
+        }
+        return VX_OK;
+    });
+}
+
+int vx_decoder_kv_get(const vx_decoder_t* d, uint32_t layer, uint32_t pos, uint32_t kv_head, uint16_t* k, uint16_t* v,
+                      size_t n) {
+    return guard([&]() -> int {
+        VX_TRY(check_decoder(d));
+        if (layer >= d->cfg.n_layers || pos >= d->cfg.max_ctx || kv_head >= d->cfg.n_kv_heads)
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "layer %u / pos %u / kv_head %u out of range", layer, pos, kv_head);
+        if (n < d->cfg.head_dim) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "k and v hold %zu values, head_dim is %u", n, d->cfg.head_dim);
+        const size_t off = (static_cast<size_t>(layer) * d->kvd * d->cfg.max_ctx) +
+                           (static_cast<size_t>(kv_head) * d->cfg.max_ctx + pos) * d->cfg.head_dim;
+        VX_TRY(set_device(d->device));
+        VX_HIP(hipStreamSynchronize(d->stream));
+        if (k) VX_HIP(hipMemcpy(k, d->d_kc + off, d->cfg.head_dim * 2, hipMemcpyDeviceToHost));
+        if (v) VX_HIP(hipMemcpy(v, d->d_vc + off, d->cfg.head_dim * 2, hipMemcpyDeviceToHost));
         return VX_OK;
     });
 }

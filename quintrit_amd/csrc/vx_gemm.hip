@@ -367,25 +367,39 @@ size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus) {
     return p.xs_bytes + p.s4_bytes + p.part_bytes;
 }
 
-int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
-                size_t ldy, uint8_t* ws, hipStream_t stream) {
-    const GemmPlan p = gemm_plan(g, M, num_cus);
-    uint4* xs = reinterpret_cast<uint4*>(ws);
-    int* s4p = reinterpret_cast<int*>(ws + p.xs_bytes);
-    int32_t* part = p.kslices > 1 ? reinterpret_cast<int32_t*>(ws + p.xs_bytes + p.s4_bytes) : nullptr;
+size_t gemm_stage_bytes(size_t cols, size_t M) {
+    const GemmPlan p = gemm_plan(geometry(1, cols), M, 1);  // the staged activations depend on cols and M only
+    return p.xs_bytes + p.s4_bytes;
+}
+
+size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus) { return gemm_plan(g, M, num_cus).part_bytes; }
+
+// Stages x (M rows of cols int8) into the MFMA operand order at ws (gemm_stage_bytes(cols, M) bytes): the staged
+// activations of one call serve every matrix with cols columns.
+int launch_gemm_stage(const int8_t* x, size_t M, size_t ldx, size_t cols, uint8_t* ws, hipStream_t stream) {
+    const GemmPlan p = gemm_plan(geometry(1, cols), M, 1);
     // B fragments of tokens past M (the rest of the last 32-token group) are left as they are: they only reach C
     // columns that are never stored.
     hipLaunchKernelGGL(gemm_stage_kernel, dim3(static_cast<uint32_t>(M), p.stage_x), dim3(256), 0, stream, x,
-                       static_cast<uint32_t>(ldx), p.n_tg, static_cast<uint32_t>(g.cols), static_cast<uint32_t>(g.tbr),
-                       p.n_ksteps, xs, s4p, static_cast<uint32_t>(M));
+                       static_cast<uint32_t>(ldx), p.n_tg, static_cast<uint32_t>(cols),
+                       static_cast<uint32_t>(tile_row_bytes(cols)), p.n_ksteps, reinterpret_cast<uint4*>(ws),
+                       reinterpret_cast<int*>(ws + p.xs_bytes), static_cast<uint32_t>(M));
     VX_HIP(hipGetLastError());
+    return VX_OK;
+}
+
+// The product of matrix w with activations staged by launch_gemm_stage at `staged`; `part` holds
+// gemm_part_bytes(g, M, num_cus) bytes of K-slice partial sums (unused when the plan has one slice).
+int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const uint8_t* staged, size_t M, int32_t* y,
+                       size_t ldy, uint8_t* part, hipStream_t stream) {
+    const GemmPlan p = gemm_plan(g, M, num_cus);
     GemmArgs a{};
     a.w = w;
-    a.xs = xs;
-    a.s4p = s4p;
+    a.xs = reinterpret_cast<const uint4*>(staged);
+    a.s4p = reinterpret_cast<const int*>(staged + p.xs_bytes);
     a.s4_parts = p.stage_x;
     a.y = y;
-    a.part = part;
+    a.part = p.kslices > 1 ? reinterpret_cast<int32_t*>(part) : nullptr;
     a.rows = static_cast<uint32_t>(g.rows);
     a.n_tiles = static_cast<uint32_t>(g.n_tiles);
     a.n_chunks = static_cast<uint32_t>(g.n_chunks);
@@ -407,6 +421,12 @@ int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* 
         VX_HIP(hipGetLastError());
     }
     return VX_OK;
+}
+
+int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
+                size_t ldy, uint8_t* ws, hipStream_t stream) {
+    VX_TRY(launch_gemm_stage(x, M, ldx, g.cols, ws, stream));
+    return launch_gemm_staged(w, g, num_cus, ws, M, y, ldy, ws + gemm_stage_bytes(g.cols, M), stream);
 }
 
 // ---- the no-allocation entry point's workspace -----------------------------------------------------------------------

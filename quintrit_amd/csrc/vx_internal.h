@@ -165,6 +165,13 @@ int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream);
+// The two halves of launch_gemm: staging of the activations (shared by every matrix with the same cols) and the
+// product; gemm_workspace_bytes = gemm_stage_bytes + gemm_part_bytes.
+size_t gemm_stage_bytes(size_t cols, size_t M);
+size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus);
+int launch_gemm_stage(const int8_t* x, size_t M, size_t ldx, size_t cols, uint8_t* ws, hipStream_t stream);
+int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const uint8_t* staged, size_t M, int32_t* y,
+                       size_t ldy, uint8_t* part, hipStream_t stream);
 // The same GEMM with its workspace in the library's per-device scratch array (kNoAllocScratchBytes): no allocation.
 constexpr size_t kNoAllocScratchBytes = VX_GEMM_NOALLOC_SCRATCH_BYTES;
 int launch_gemm_noalloc(const uint8_t* w, const Geometry& g, int device, int num_cus, const int8_t* x, size_t M,

@@ -142,11 +142,31 @@ class Decoder:
                                     logits.size if want_logits else 0, ctypes.byref(nxt)))
         return logits, int(nxt.value)
 
-    def generate(self, prompt, n_new: int) -> list:
+    def generate(self, prompt, n_new: int, stepwise: bool = False) -> list:
+        """Greedy generation from position 0: the prompt by prefill passes (vx_decoder_generate), or one decode step
+        per prompt token as the reference feeds it (stepwise, vx_decoder_generate_stepwise)."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32).reshape(-1)
         out = np.zeros(max(n_new, 1), dtype=np.uint32)
-        check(lib().vx_decoder_generate(self.handle, _ptr(p), p.size, n_new, _ptr(out), out.size))
+        fn = lib().vx_decoder_generate_stepwise if stepwise else lib().vx_decoder_generate
+        check(fn(self.handle, _ptr(p), p.size, n_new, _ptr(out), out.size))
         return [int(t) for t in out[:n_new]]
+
+    def prefill(self, tokens, pos0: int = 0, want_logits: bool = True):
+        """vx_decoder_prefill: tokens at positions pos0 .. into the KV cache; (logits of the last position, its greedy
+        next token)."""
+        t = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+        logits = np.empty(self.config.vocab, dtype=np.float32) if want_logits else None
+        nxt = ctypes.c_uint32()
+        check(lib().vx_decoder_prefill(self.handle, _ptr(t), t.size, pos0, _ptr(logits) if want_logits else None,
+                                       logits.size if want_logits else 0, ctypes.byref(nxt)))
+        return logits, int(nxt.value)
+
+    def kv(self, layer: int, pos: int, kv_head: int):
+        """The cached f16 key and value bits (uint16 arrays of head_dim) of (layer, pos, kv_head)."""
+        k = np.empty(self.config.head_dim, np.uint16)
+        v = np.empty(self.config.head_dim, np.uint16)
+        check(lib().vx_decoder_kv_get(self.handle, layer, pos, kv_head, _ptr(k), _ptr(v), k.size))
+        return k, v
 
     def memory_bytes(self) -> int:
         b = ctypes.c_size_t()

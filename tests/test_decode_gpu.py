@@ -261,6 +261,16 @@ def test_bitnet2b_greedy_golden(torch_dev, oracle):
         got = dec.generate(gold["prompt"], len(gold["tokens"]))
         first_bad = next((i for i, (a, b) in enumerate(zip(got, gold["tokens"])) if a != b), None)
         assert first_bad is None, f"token {first_bad} differs: {got[first_bad]} vs {gold['tokens'][first_bad]}"
+        # the prompt fed one step per token (the reference's loop) gives the same tokens, and the KV cache the
+        # prefill leaves equals the one the steps leave, at every layer, position and KV head
+        n = len(gold["prompt"])
+        dec.prefill(gold["prompt"])
+        cfg = dec.config
+        kv_pre = {(l, p, h): dec.kv(l, p, h) for l in range(cfg.n_layers) for p in range(n) for h in range(cfg.n_kv_heads)}
+        assert dec.generate(gold["prompt"], len(gold["tokens"]), stepwise=True) == gold["tokens"]
+        for key, (k, v) in kv_pre.items():
+            k2, v2 = dec.kv(*key)
+            assert np.array_equal(k, k2) and np.array_equal(v, v2), f"KV cache at (layer, pos, kv head) {key}"
     finally:
         dec.close()
 
@@ -286,5 +296,10 @@ def test_falcon3_10b_golden_logits_every_position(torch_dev, oracle):
             if pos + 1 >= len(gold["prompt"]):
                 assert nxt == gold["tokens"][pos + 1 - len(gold["prompt"])], f"token after position {pos}"
         assert dec.generate(gold["prompt"], len(gold["tokens"])) == gold["tokens"]
+        # the prompt as one prefill: the last prompt position's logits and the first generated token
+        logits, nxt = dec.prefill(gold["prompt"])
+        n = len(gold["prompt"])
+        assert int(logits.view(np.uint32).astype(np.uint64).sum()) == gold["logits_f32_bits_sums"][n - 1]
+        assert nxt == gold["tokens"][0]
     finally:
         dec.close()
