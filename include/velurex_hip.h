@@ -309,7 +309,7 @@ int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_pl
  * own input: embedding or residual add or gating, RMSNorm, int8 quantization) and attention (RoPE, KV append), then
  * the final norm, head and argmax in one kernel, with the position and the token kept on the device (the reference's
  * CUDA decode graph does the same, quintrit-runtime/src/gpu.rs:459-493).
- * Supported: head_dim 128 or 256, max_ctx <= 4096, hidden a multiple of 32 up to 8192 (4480 with SiLU),
+ * Supported: head_dim 32, 64, 128 or 256, max_ctx <= 8192, hidden a multiple of 32 up to 8192 (4480 with SiLU),
  * n_heads * head_dim <= 8192, ffn a multiple of 4 up to 8192 (24576 with SiLU and no sub-norms). */
 typedef struct vx_decoder vx_decoder_t;
 
@@ -472,7 +472,7 @@ int vx_gguf_upload_q2_matrix(const vx_gguf_t* gguf, const char* name, vx_matrix_
 typedef struct vx_gpu_options {
     uint32_t struct_size;    /* sizeof(vx_gpu_options_t) */
     uint32_t device_index;   /* GPU to use, below hipGetDeviceCount */
-    uint32_t context_length; /* largest context in tokens; 0 = min(4096, the model's maximum); at most 4096 */
+    uint32_t context_length; /* largest context in tokens; 0 = min(4096, the model's maximum); at most 7936 */
     uint32_t flags;          /* 0 */
 } vx_gpu_options_t;
 
@@ -483,7 +483,7 @@ typedef struct vx_gpu_options {
  * the head output.weight (F16) or the embedding. The context is rounded down to a multiple of 256 as gpu.rs:141-146
  * does. Files the reference rejects give VX_ERR_MODEL (missing or misshapen tensors, no tokenizer, absurd dimensions);
  * models it runs elsewhere than this decoder give VX_ERR_UNSUPPORTED (no I2_S tensor, Q2_0, Qwen3 / hybrid / MoE,
- * partial or scaled RoPE, head_dim other than 128 / 256). options may be NULL (device 0, default context). On failure
+ * partial or scaled RoPE, head_dim other than 32 / 64 / 128 / 256). options may be NULL (device 0, default context). On failure
  * *out_decoder is NULL. The handle is used and freed like one from vx_decoder_create. */
 int vx_decoder_open_gguf(const char* path, const vx_gpu_options_t* options, vx_decoder_t** out_decoder);
 

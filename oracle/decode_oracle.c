@@ -436,6 +436,22 @@ const uint16_t* vxo_model_embedding(const vxo_model* m) { return m->emb; }
 const uint16_t* vxo_model_head(const vxo_model* m) { return m->head ? m->head : m->emb; }
 const float* vxo_model_rope_table(const vxo_model* m) { return m->rope; }
 
+/* Test access to the KV cache (KVCache::get_key / get_val and append, kv_cache.rs:124-155): the head_dim f16 key and
+ * value of (layer, pos, kv_head). With them a test can give the oracle a long cache and run single steps at its end. */
+void vxo_model_kv_get(const vxo_model* m, size_t layer, size_t pos, size_t kv_head, uint16_t* k, uint16_t* v) {
+    const vxo_model_config* c = &m->cfg;
+    const size_t off = (layer * c->max_ctx + pos) * c->n_kv_heads * c->head_dim + kv_head * c->head_dim;
+    memcpy(k, m->kc + off, c->head_dim * 2);
+    memcpy(v, m->vc + off, c->head_dim * 2);
+}
+
+void vxo_model_kv_set(vxo_model* m, size_t layer, size_t pos, size_t kv_head, const uint16_t* k, const uint16_t* v) {
+    const vxo_model_config* c = &m->cfg;
+    const size_t off = (layer * c->max_ctx + pos) * c->n_kv_heads * c->head_dim + kv_head * c->head_dim;
+    memcpy(m->kc + off, k, c->head_dim * 2);
+    memcpy(m->vc + off, v, c->head_dim * 2);
+}
+
 void vxo_model_reset(vxo_model* m) {
     const size_t kvn = m->cfg.n_layers * m->cfg.max_ctx * m->cfg.n_kv_heads * m->cfg.head_dim;
     memset(m->kc, 0, kvn * 2);

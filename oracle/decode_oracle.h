@@ -71,6 +71,8 @@ const uint16_t* vxo_model_embedding(const vxo_model* m);
 const uint16_t* vxo_model_head(const vxo_model* m); /* the untied head, or the embedding when tied */
 const float* vxo_model_rope_table(const vxo_model* m);
 void vxo_model_reset(vxo_model* m);
+void vxo_model_kv_get(const vxo_model* m, size_t layer, size_t pos, size_t kv_head, uint16_t* k, uint16_t* v);
+void vxo_model_kv_set(vxo_model* m, size_t layer, size_t pos, size_t kv_head, const uint16_t* k, const uint16_t* v);
 uint32_t vxo_model_forward(vxo_model* m, uint32_t token, size_t pos, float* logits);
 void vxo_model_generate(vxo_model* m, const uint32_t* prompt, size_t n_prompt, size_t n_new, uint32_t* out);
 

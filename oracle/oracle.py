@@ -97,6 +97,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "vxo_model_embedding": (vp, [vp]),
         "vxo_model_rope_table": (vp, [vp]),
         "vxo_model_reset": (None, [vp]),
+        "vxo_model_kv_get": (None, [vp, sz, sz, sz, vp, vp]),
+        "vxo_model_kv_set": (None, [vp, sz, sz, sz, vp, vp]),
         "vxo_model_forward": (ctypes.c_uint32, [vp, ctypes.c_uint32, sz, vp]),
         "vxo_model_generate": (None, [vp, vp, sz, sz, vp]),
         # GGUF ternary decoders (gguf_oracle.c)
@@ -415,6 +417,18 @@ class Model:
 
     def reset(self):
         lib().vxo_model_reset(self._h)
+
+    def kv(self, layer: int, pos: int, kv_head: int):
+        """The cached f16 key and value bits (uint16 arrays of head_dim) of (layer, pos, kv_head)."""
+        k = np.empty(self.cfg.head_dim, np.uint16)
+        v = np.empty(self.cfg.head_dim, np.uint16)
+        lib().vxo_model_kv_get(self._h, layer, pos, kv_head, _p(k), _p(v))
+        return k, v
+
+    def set_kv(self, layer: int, pos: int, kv_head: int, k, v) -> None:
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        lib().vxo_model_kv_set(self._h, layer, pos, kv_head, _p(k), _p(v))
 
     def forward(self, token: int, pos: int):
         logits = np.empty(self.cfg.vocab, np.float32)

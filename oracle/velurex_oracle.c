@@ -336,20 +336,21 @@ uint16_t vxo_f32_to_f16(float f) {
     return (uint16_t)(sign | (base + q - 0x400u));
 }
 
+/* binary16 -> binary32 (exact): a normal half moves its exponent to the f32 bias (e - 15 + 127) and its 10 significand
+ * bits to the top of the 23; a subnormal half is m * 2^-24 (exact in f32); inf and NaN keep their payload. */
 float vxo_f16_to_f32(uint16_t h) {
     const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
     const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t bits;
     float v;
     if (e == 0) {
-        v = ldexpf((float)m, -24);
+        v = (float)m * 0x1p-24f;
+        memcpy(&bits, &v, 4);
     } else if (e == 31) {
-        uint32_t bits = 0x7f800000u | (m << 13);
-        memcpy(&v, &bits, 4);
+        bits = 0x7f800000u | (m << 13);
     } else {
-        v = ldexpf((float)(m | 0x400u), (int)e - 25);
+        bits = ((e + 112u) << 23) | (m << 13);
     }
-    uint32_t bits;
-    memcpy(&bits, &v, 4);
     bits |= sign;
     memcpy(&v, &bits, 4);
     return v;

@@ -801,7 +801,8 @@ struct AttnArgs {
     ProjOut q, k, v;       // the q, k, v projections of this layer
     const float* rope;     // [max_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i + 1
     uint16_t* kc;          // this layer: [kv_head][max_ctx][head_dim] f16
-    uint16_t* vc;
+    uint16_t* vc;          // this layer: [kv_head][vstride / 8][head_dim][8] f16 (V in tiles of 8 positions)
+    uint32_t vstride;      // positions per row of vc: max_ctx rounded up to 8
     float* out;            // n_heads x head_dim
     uint32_t n_heads, gqa, max_ctx;
     uint32_t rope_normal;  // 1: pairs (2i, 2i + 1) (RopeMode::Normal), 0: (i, i + head_dim / 2) (NEOX)
@@ -812,18 +813,24 @@ struct AttnArgs {
     uint32_t n_tok;
 };
 
-constexpr uint32_t kAttnMaxCtx = 4096;  // KV positions held in LDS (scores, running maxima)
-constexpr uint32_t kAttnWaves = 8;      // 4 chunks x 2 halves of the head
-constexpr uint32_t kAttnBatch = 8;      // positions whose LDS operands are read ahead of the accumulator chain
+constexpr uint32_t kAttnMaxCtx = 8192;  // KV positions held in LDS (scores, running maxima)
+constexpr uint32_t kVDepth = 8;         // groups of 8 positions of V in flight per lane in the accumulator chain
+// Positions per row of the transposed V cache: max_ctx rounded up to 8 (one 16-byte load is 8 positions).
+inline uint32_t vstride_of(uint32_t max_ctx) { return (max_ctx + 7u) / 8u * 8u; }
+// The attention kernel's shape for a head dimension: coordinates per lane, waves (4 chunks of attn_waves / 4), threads.
+__host__ __device__ constexpr uint32_t attn_cpl(uint32_t hd) { return hd >= 256u ? hd / 128u : 1u; }
+__host__ __device__ constexpr uint32_t attn_waves(uint32_t hd) { return hd >= 128u ? 8u : 4u; }
+__host__ __device__ constexpr uint32_t attn_threads(uint32_t hd) { return 64u * attn_waves(hd); }
 
 // f16 value of an f32 (round to nearest even, after the f32 rounding of x), kept in an f32
 __device__ __forceinline__ float r16(float x) { return static_cast<float>(static_cast<_Float16>(keep_f32(x))); }
 
-// One workgroup per query head. First the inputs of the position: q of this head and k, v of its KV head, RoPE over
-// all head_dim coordinates (ops.rs:199-221, NEOX or Normal pairing: x0' = fma(x0, c, -(x1 s)), x1' = fma(x0, s, x1 c))
-// and the f16 rounding of the cache (kv_cache.rs:24-182); the first query head of each KV head appends k and v to the
-// cache, and every workgroup uses its own copy of them for the position itself (the other positions come from
-// earlier steps).
+// One workgroup per query head (and token, PREFILL). First the inputs of the position: q of this head and k, v of its KV
+// head, RoPE over all head_dim coordinates (ops.rs:199-221, NEOX or Normal pairing: x0' = fma(x0, c, -(x1 s)),
+// x1' = fma(x0, s, x1 c)) and the f16 rounding of the cache (kv_cache.rs:24-182); the first query head of each KV head
+// appends k and v to the cache, and every workgroup uses its own copy of them for the position itself (the other
+// positions come from earlier steps). PREFILL: the query comes rotated from qbuf and the position's k and v from the
+// cache (pf_rope_kernel wrote them), nothing is appended.
 // Then the reference's attend_head (attention.rs:483-542) over the positions 0..pos. Below a padded KV length of 512 one
 // online softmax covers all positions; from 512 on, 4 chunks of ceil(n_kv / 4) positions run one each and are combined
 // in order. The online softmax of a chunk (attend_range, attention.rs:436-468) is rebuilt without its serial
@@ -833,20 +840,20 @@ __device__ __forceinline__ float r16(float x) { return static_cast<float>(static
 //   factors       every position in parallel: a new maximum gives ms = expf(m_old - score), vs = 1; otherwise ms = 1,
 //                 vs = expf(score - max); stored as -ms or vs (the sign marks the case)
 //   accumulator   per coordinate, in position order: y = f16(y * ms), y = f16(fma(v, vs, y)), s = fma(s, ms, vs)
-// Wave w accumulates chunk w / 2, coordinates (HD / 2) (w % 2) .. + HD / 2 - 1, HD / 128 per lane (independent
-// chains), with V streamed through LDS in windows of kWin positions, the next window loaded while the current one is
-// consumed.
-// PREFILL: blockIdx.y is a token of a prefill; its query comes rotated from qbuf and its own k, v from the cache (written
-// by pf_rope_kernel), so nothing is appended here. The rest is the same arithmetic for every token.
+// The accumulator chains: each chunk has attn_waves(HD) / 4 waves, a lane attn_cpl(HD) coordinates (independent
+// chains). V is cached in tiles of 8 positions, [kv_head][position / 8][coordinate][position % 8]: one 16-byte load is
+// eight consecutive positions of one coordinate, and a wave's load of 64 coordinates reads 1 KiB of contiguous memory;
+// kVDepth such loads per coordinate are in flight ahead of the chain.
 template <int HD, bool PREFILL>
-__global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) {
-    constexpr uint32_t kHalf = HD / 2;         // coordinates of a wave
-    constexpr int kPerLane = HD / 128;         // coordinates of a lane
-    constexpr uint32_t kLP = kHalf / 8;        // lanes loading one position's half row (16 bytes each)
-    constexpr uint32_t kWin = 8u * (64u / kLP);  // positions of V staged per wave at a time (8 loads per lane)
-    __shared__ float sc[kAttnMaxCtx];
+__global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a) {
+    constexpr uint32_t kCpl = attn_cpl(HD);           // coordinates (chains) per lane
+    constexpr uint32_t kWpc = attn_waves(HD) / 4u;    // waves per chunk
+    constexpr uint32_t kLanes = HD / (kWpc * kCpl);   // lanes of a wave with coordinates (64, or 32 at head_dim 32)
+    constexpr uint32_t kThreads = attn_threads(HD);
+    constexpr uint32_t kHalf = HD / 2;        // RoPE pairs
+    constexpr int kBlk = HD / 32;             // 32-value blocks of a row
+    __shared__ __align__(16) float sc[kAttnMaxCtx];
     __shared__ float pm[kAttnMaxCtx];
-    __shared__ __align__(16) uint16_t vbuf[kAttnWaves][kWin * kHalf];
     __shared__ __align__(16) uint16_t qs[HD];
     __shared__ __align__(16) uint16_t kp[HD];  // k and v of the position itself
     __shared__ __align__(16) uint16_t vp[HD];
@@ -859,15 +866,20 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     const uint32_t pos = PREFILL ? a.ctl->pos + 1u - a.n_tok + tok : a.ctl->pos;
     const uint32_t seq = pos + 1;
     const uint16_t* kb = a.kc + static_cast<size_t>(kvh) * a.max_ctx * HD;
-    const uint16_t* vb = a.vc + static_cast<size_t>(kvh) * a.max_ctx * HD;
+    uint16_t* vt = a.vc + static_cast<size_t>(kvh) * HD * a.vstride;  // this KV head's tiles: [vstride / 8][HD][8]
+    auto vt_at = [&](uint32_t p, uint32_t dd) -> size_t {
+        return (static_cast<size_t>(p >> 3) * HD + dd) * 8u + (p & 7u);
+    };
 
     uint32_t n_kv = (seq + 255u) / 256u * 256u;
     if (n_kv > a.max_ctx) n_kv = a.max_ctx;
     const bool split = n_kv >= 512u;
     const uint32_t chunk = split ? (n_kv + 3u) / 4u : seq;
     const uint32_t n_chunks = split ? 4u : 1u;
-    // This wave's chunk and half of the head.
-    const uint32_t c = wave >> 1, half = wave & 1u;
+    // This wave's chunk; the lane's coordinates are d0 + 64 m (m < kCpl) when it has any.
+    const uint32_t c = wave / kWpc;
+    const uint32_t d0 = (wave % kWpc) * 64u * kCpl + lane;
+    const bool has_d = lane < kLanes;
     uint32_t st = 0, en = 0;
     if (c < n_chunks) {
         st = c * chunk;
@@ -878,7 +890,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         if (tid < HD) {
             qs[tid] = a.qbuf[(static_cast<size_t>(tok) * a.n_heads + h) * HD + tid];
             kp[tid] = kb[static_cast<size_t>(pos) * HD + tid];
-            vp[tid] = vb[static_cast<size_t>(pos) * HD + tid];
+            vp[tid] = vt[vt_at(pos, tid)];
         }
     } else {
         const float* cache = a.rope + static_cast<size_t>(pos) * HD;
@@ -908,35 +920,32 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     __syncthreads();
     if (!PREFILL && h % a.gqa == 0 && tid < HD) {
         a.kc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + tid] = kp[tid];
-        a.vc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + tid] = vp[tid];
+        vt[vt_at(pos, tid)] = vp[tid];
     }
-    // This wave's first window of V, requested before the scores so that its latency overlaps them, the scan and
-    // the exponentials; the position itself comes from LDS. Load j of a lane holds 8 coordinates of position
-    // 8 j + lane / kLP of the window.
-    // Rows come from the cache in global memory only (a select between an LDS and a global address would make every
-    // load a flat one); the row of the position itself, not yet visible there, is replaced from vp when a window is
-    // stored to LDS. Every row read is below max_ctx.
-    const uint32_t off = half * kHalf + (lane % kLP) * 8u;
-    const uint16_t* vsrc = vb + off;
-    auto load_v = [&](uint32_t p) -> u32x4 { return *reinterpret_cast<const u32x4*>(vsrc + static_cast<size_t>(p) * HD); };
-    const u32x4 vself = *reinterpret_cast<const u32x4*>(vp + off);
-    constexpr uint32_t kPosPerLoad = 64u / kLP;
-    auto load_window = [&](uint32_t base, u32x4 (&r)[8]) {
+
+    // The chain's V: group g holds positions 8 g .. 8 g + 7 (every tile read is below vstride: groups run to the chunk's
+    // end rounded up to 8). Its first kVDepth groups are requested right after each thread's first k below, so that
+    // they arrive during the scores, the scan and the exponentials without delaying the first score (loads complete in
+    // issue order). The value of the position itself, not yet visible in the cache to every workgroup, is patched from
+    // vp when its group is used.
+    const bool chain = c < n_chunks && st < en;
+    const uint32_t g_first = st / 8u, g_end = chain ? (en + 7u) / 8u : g_first + 1u;
+    const uint32_t dl = has_d ? d0 : 0u;  // a lane without coordinates reads coordinate 0 and never uses it
+    u32x4 ring[kVDepth][kCpl];
+    auto load_group = [&](uint32_t g, u32x4 (&r)[kCpl]) {
+        const uint32_t gg = min(g, g_end - 1u);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) r[j] = load_v(min(base + kPosPerLoad * j + lane / kLP, en - 1u));
+        for (uint32_t m = 0; m < kCpl; ++m)
+            r[m] = *reinterpret_cast<const u32x4*>(vt + (static_cast<size_t>(gg) * HD + dl + 64u * m) * 8u);
     };
-    u32x4 ra[8], rb[8];  // two windows in flight
-    if (st < en) load_window(st, ra);
-    if (st + kWin < en) load_window(st + kWin, rb);
 
     // Scores, four lanes per position (ggml_vec_dot_f16, ops.rs:960-1015): lane j of a group holds accumulator j
-    // (values 32 i + 8 j .. + 7 of every 32-value block i) with q in registers; (a0 + a2) + (a1 + a3) across the
+    // (values 32 i + 8 j .. + 7 of every 32-value block i) with q in registers as f32; (a0 + a2) + (a1 + a3) across the
     // group, then red[k] + red[k + 4] and (t0 + t1) + (t2 + t3) in lane 0. The next position's k is loaded while the
     // current one is summed.
     {
-        constexpr int kBlk = HD / 32;
         const uint32_t j = tid & 3u, g = tid >> 2;
-        constexpr uint32_t kGroups = kAttnWaves * 64u / 4u;
+        constexpr uint32_t kGroups = kThreads / 4u;
         float qf[kBlk][8];
 #pragma unroll
         for (int i = 0; i < kBlk; ++i) {
@@ -979,6 +988,8 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
         uint4 ka[kBlk], kn[kBlk];
         uint32_t p = g;
         if (p < seq) load_k(p, ka);
+#pragma unroll
+        for (uint32_t k = 0; k < kVDepth; ++k) load_group(g_first + k, ring[k]);
         for (; p < seq; p += 2u * kGroups) {  // unrolled by two so that the buffers keep their registers
             if (p + kGroups < seq) load_k(p + kGroups, kn);
             score(p, ka);
@@ -987,6 +998,9 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
             score(p + kGroups, kn);
         }
     }
+    uint16_t vself[kCpl];
+#pragma unroll
+    for (uint32_t m = 0; m < kCpl; ++m) vself[m] = vp[dl + 64u * m];
     __syncthreads();
 
     if (wave < n_chunks) {  // the running maximum of chunk `wave`
@@ -1007,7 +1021,7 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     }
     __syncthreads();
 
-    for (uint32_t p = tid; p < seq; p += kAttnWaves * 64u) {
+    for (uint32_t p = tid; p < seq; p += kThreads) {
         const uint32_t s0 = split ? p / chunk * chunk : 0u;
         const float prev = p == s0 ? -__builtin_inff() : pm[p - 1];
         const float s = sc[p];
@@ -1015,105 +1029,105 @@ __global__ __launch_bounds__(kAttnWaves * 64) void attention_kernel(AttnArgs a) 
     }
     __syncthreads();
 
-    float y[kPerLane], ssum = 0.0f;
+    // The accumulator chains of this lane's coordinates over positions st .. en - 1, eight positions per group; a group
+    // with no new maximum (ms = 1 throughout) takes the shorter step.
+    float y[kCpl], ssum = 0.0f;
 #pragma unroll
-    for (int m = 0; m < kPerLane; ++m) y[m] = 0.0f;
-    uint16_t* buf = vbuf[wave];
-    // One window: its rows (the position itself from vp) into LDS, the window two ahead into the freed registers,
-    // then the accumulator chain over its positions.
-    auto window = [&](uint32_t base, u32x4 (&r)[8]) {
+    for (uint32_t m = 0; m < kCpl; ++m) y[m] = 0.0f;
+    if (chain) {
+        // the factors of the next group are read from LDS while the current group is summed
+        float4 na = *reinterpret_cast<const float4*>(sc + 8u * g_first);
+        float4 nb = *reinterpret_cast<const float4*>(sc + 8u * g_first + 4u);
+        for (uint32_t g0 = g_first; g0 < g_end; g0 += kVDepth) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t pj = base + kPosPerLoad * j + lane / kLP;
-            *reinterpret_cast<u32x4*>(buf + (kPosPerLoad * j + lane / kLP) * kHalf + (lane % kLP) * 8u) =
-                pj == pos ? vself : r[j];
+            for (uint32_t k = 0; k < kVDepth; ++k) {
+                const uint32_t gg = g0 + k;
+                if (gg < g_end) {  // wave-uniform
+                    u32x4 w[kCpl];
+#pragma unroll
+                    for (uint32_t m = 0; m < kCpl; ++m) w[m] = ring[k][m];
+                    load_group(gg + kVDepth, ring[k]);
+                    const uint32_t p0 = 8u * gg;
+                    const float4 fa = na, fb = nb;
+                    const uint32_t pn = 8u * min(gg + 1u, g_end - 1u);
+                    na = *reinterpret_cast<const float4*>(sc + pn);
+                    nb = *reinterpret_cast<const float4*>(sc + pn + 4u);
+                    if (pos >= p0 && pos < p0 + 8u) {  // the position itself, from this workgroup's copy
+                        const uint32_t e = pos - p0, sh = (e & 1u) * 16u, keep = ~(0xffffu << sh);
+#pragma unroll
+                        for (uint32_t m = 0; m < kCpl; ++m) {
+                            const uint32_t ins = static_cast<uint32_t>(vself[m]) << sh;
+                            const uint32_t q = e >> 1;
+                            w[m].x = q == 0 ? ((w[m].x & keep) | ins) : w[m].x;
+                            w[m].y = q == 1 ? ((w[m].y & keep) | ins) : w[m].y;
+                            w[m].z = q == 2 ? ((w[m].z & keep) | ins) : w[m].z;
+                            w[m].w = q == 3 ? ((w[m].w & keep) | ins) : w[m].w;
+                        }
+                    }
+                    const float f[8] = {fa.x, fa.y, fa.z, fa.w, fb.x, fb.y, fb.z, fb.w};
+                    const bool whole = p0 >= st && p0 + 8u <= en;
+                    uint32_t neg = 0;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) neg |= f32_bits(f[e]) >> 31;
+                    neg = __builtin_amdgcn_readfirstlane(neg);
+                    if (whole && neg == 0) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+#pragma unroll
+                            for (uint32_t m = 0; m < kCpl; ++m) {
+                                const uint32_t wv[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
+                                const float v = f16_f32(static_cast<uint16_t>(wv[e >> 1] >> ((e & 1) * 16)));
+                                y[m] = r16(__builtin_fmaf(v, f[e], y[m]));
+                            }
+                            ssum = ssum + f[e];
+                        }
+                    } else {  // a group with a new maximum or the chunk's edge (positions outside it skipped)
+                        const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(8u, en - p0);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            if (static_cast<uint32_t>(e) >= e0 && static_cast<uint32_t>(e) < e1) {
+                                const bool nm = __builtin_signbit(f[e]);
+                                const float ev = __builtin_fabsf(f[e]);
+                                const float ms = nm ? ev : 1.0f, vs = nm ? 1.0f : ev;
+#pragma unroll
+                                for (uint32_t m = 0; m < kCpl; ++m) {
+                                    const uint32_t wv[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
+                                    const float v = f16_f32(static_cast<uint16_t>(wv[e >> 1] >> ((e & 1) * 16)));
+                                    y[m] = r16(y[m] * ms);
+                                    y[m] = r16(__builtin_fmaf(v, vs, y[m]));
+                                }
+                                ssum = __builtin_fmaf(ssum, ms, vs);
+                            }
+                        }
+                    }
+                }
+            }
         }
-        if (base + 2u * kWin < en) load_window(base + 2u * kWin, r);
-        const uint32_t n = min(kWin, en - base);  // wave-uniform
-        const float f = lane < n ? sc[base + lane] : 0.0f;
-        const uint32_t nb = n & ~(kAttnBatch - 1u);
-        // Whole batches of kAttnBatch positions, their LDS operands read before the serial chain uses them; a
-        // window without a new maximum (ms = 1 throughout) takes the shorter chain.
-        if (__ballot(__builtin_signbit(f)) == 0) {
-            auto step = [&](float e, const float (&v)[kPerLane]) {
-#pragma unroll
-                for (int m = 0; m < kPerLane; ++m) y[m] = r16(__builtin_fmaf(v[m], e, y[m]));
-                ssum = ssum + e;
-            };
-            for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
-                float fe[kAttnBatch], fv[kAttnBatch][kPerLane];
-#pragma unroll
-                for (uint32_t u = 0; u < kAttnBatch; ++u) {
-                    fe[u] = sc[base + i0 + u];
-#pragma unroll
-                    for (int m = 0; m < kPerLane; ++m) fv[u][m] = f16_f32(buf[(i0 + u) * kHalf + lane + 64u * m]);
-                }
-#pragma unroll
-                for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
-            }
-            for (uint32_t i = nb; i < n; ++i) {
-                float fv[kPerLane];
-#pragma unroll
-                for (int m = 0; m < kPerLane; ++m) fv[m] = f16_f32(buf[i * kHalf + lane + 64u * m]);
-                step(sc[base + i], fv);
-            }
-        } else {
-            auto step = [&](float fi, const float (&v)[kPerLane]) {
-                const bool nm = __builtin_signbit(fi);
-                const float e = __builtin_fabsf(fi);
-                const float ms = nm ? e : 1.0f, vs = nm ? 1.0f : e;
-#pragma unroll
-                for (int m = 0; m < kPerLane; ++m) {
-                    y[m] = r16(y[m] * ms);
-                    y[m] = r16(__builtin_fmaf(v[m], vs, y[m]));
-                }
-                ssum = __builtin_fmaf(ssum, ms, vs);
-            };
-            for (uint32_t i0 = 0; i0 < nb; i0 += kAttnBatch) {
-                float fe[kAttnBatch], fv[kAttnBatch][kPerLane];
-#pragma unroll
-                for (uint32_t u = 0; u < kAttnBatch; ++u) {
-                    fe[u] = sc[base + i0 + u];
-#pragma unroll
-                    for (int m = 0; m < kPerLane; ++m) fv[u][m] = f16_f32(buf[(i0 + u) * kHalf + lane + 64u * m]);
-                }
-#pragma unroll
-                for (uint32_t u = 0; u < kAttnBatch; ++u) step(fe[u], fv[u]);
-            }
-            for (uint32_t i = nb; i < n; ++i) {
-                float fv[kPerLane];
-#pragma unroll
-                for (int m = 0; m < kPerLane; ++m) fv[m] = f16_f32(buf[i * kHalf + lane + 64u * m]);
-                step(sc[base + i], fv);
-            }
-        }
-    };
-    for (uint32_t base = st; base < en; base += 2u * kWin) {  // unrolled by two so that the windows keep their registers
-        window(base, ra);
-        if (base + kWin < en) window(base + kWin, rb);
     }
     float* out = a.out + (static_cast<size_t>(tok) * a.n_heads + h) * HD;
     if (!split) {
-        if (c == 0) {
+        if (c == 0 && has_d) {
             const float s_inv = ssum == 0.0f ? 0.0f : 1.0f / ssum;
 #pragma unroll
-            for (int m = 0; m < kPerLane; ++m) out[half * kHalf + lane + 64u * m] = y[m] * s_inv;
+            for (uint32_t m = 0; m < kCpl; ++m) out[d0 + 64u * m] = y[m] * s_inv;
         }
         return;
     }
     if (c < 4) {
+        if (has_d) {
 #pragma unroll
-        for (int m = 0; m < kPerLane; ++m) cv[c][half * kHalf + lane + 64u * m] = f32_f16(y[m]);
-        if (half == 0 && lane == 0) {
+            for (uint32_t m = 0; m < kCpl; ++m) cv[c][d0 + 64u * m] = f32_f16(y[m]);
+        }
+        if (wave % kWpc == 0 && lane == 0) {
             cm[c] = st < en ? pm[en - 1] : -__builtin_inff();
             cs[c] = ssum;
         }
     }
     __syncthreads();
-    if (c != 0) return;
+    if (c != 0 || !has_d) return;
 #pragma unroll
-    for (int m = 0; m < kPerLane; ++m) {
-        const uint32_t d = half * kHalf + lane + 64u * m;
+    for (uint32_t m = 0; m < kCpl; ++m) {
+        const uint32_t d = d0 + 64u * m;
         float mf = -__builtin_inff(), sf = 0.0f, acc = 0.0f;
         for (uint32_t k = 0; k < 4; ++k) {
             const uint32_t ks = k * chunk, ke = min(min(ks + chunk, n_kv), seq);
@@ -1336,9 +1350,9 @@ struct PfRopeArgs {
     const float* as;              // [n_tok] activation scale of the q/k/v input
     float wsq, wsk, wsv;
     const float* rope;            // [max_ctx][head_dim]: (cos, sin) of pair i at 2i, 2i + 1
-    uint16_t *kc, *vc;            // this layer: [kv_head][max_ctx][head_dim]
+    uint16_t *kc, *vc;            // this layer: k [kv_head][max_ctx][head_dim], v [kv_head][vstride / 8][head_dim][8]
     uint16_t* qbuf;               // [n_tok][n_heads * head_dim]
-    uint32_t n_heads, n_kv, hd, max_ctx, rope_normal;
+    uint32_t n_heads, n_kv, hd, max_ctx, rope_normal, vstride;
 };
 
 __global__ __launch_bounds__(256) void pf_rope_kernel(PfRopeArgs a) {
@@ -1367,7 +1381,7 @@ __global__ __launch_bounds__(256) void pf_rope_kernel(PfRopeArgs a) {
             dst[i1] = f32_f16(y1);
         } else {
             const uint32_t j = i - nq - nk, head = j / a.hd, e = j - head * a.hd;
-            a.vc[(static_cast<size_t>(head) * a.max_ctx + pos) * a.hd + e] =
+            a.vc[static_cast<size_t>(head) * a.hd * a.vstride + (static_cast<size_t>(pos >> 3) * a.hd + e) * 8u + (pos & 7u)] =
                 f32_f16(proj_value(a.yv[static_cast<size_t>(t) * a.ldv + j], pv, zero));
         }
     }
@@ -1463,22 +1477,22 @@ int launch_dgemv(const DStageArgs& a, hipStream_t s) {
     return VX_OK;
 }
 
-int launch_attention(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
-    if (head_dim == 256)
-        hipLaunchKernelGGL((attention_kernel<256, false>), dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
-    else
-        hipLaunchKernelGGL((attention_kernel<128, false>), dim3(a.n_heads), dim3(kAttnWaves * 64), 0, s, a);
+template <bool PREFILL>
+static int launch_attention_mode(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
+    const dim3 grid(a.n_heads, PREFILL ? a.n_tok : 1u);
+    if (head_dim == 256) hipLaunchKernelGGL((attention_kernel<256, PREFILL>), grid, dim3(attn_threads(256)), 0, s, a);
+    else if (head_dim == 128) hipLaunchKernelGGL((attention_kernel<128, PREFILL>), grid, dim3(attn_threads(128)), 0, s, a);
+    else if (head_dim == 64) hipLaunchKernelGGL((attention_kernel<64, PREFILL>), grid, dim3(attn_threads(64)), 0, s, a);
+    else if (head_dim == 32) hipLaunchKernelGGL((attention_kernel<32, PREFILL>), grid, dim3(attn_threads(32)), 0, s, a);
+    else VX_FAIL(VX_ERR_INTERNAL, "no attention kernel for head_dim %u", head_dim);
     VX_HIP(hipGetLastError());
     return VX_OK;
 }
 
+int launch_attention(const AttnArgs& a, uint32_t head_dim, hipStream_t s) { return launch_attention_mode<false>(a, head_dim, s); }
+
 int launch_attention_prefill(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
-    if (head_dim == 256)
-        hipLaunchKernelGGL((attention_kernel<256, true>), dim3(a.n_heads, a.n_tok), dim3(kAttnWaves * 64), 0, s, a);
-    else
-        hipLaunchKernelGGL((attention_kernel<128, true>), dim3(a.n_heads, a.n_tok), dim3(kAttnWaves * 64), 0, s, a);
-    VX_HIP(hipGetLastError());
-    return VX_OK;
+    return launch_attention_mode<true>(a, head_dim, s);
 }
 
 int launch_head(const HeadArgs& a, bool f16, uint32_t grid, hipStream_t s) {
@@ -1703,8 +1717,8 @@ static int create_decoder(const vx_decoder_config_t* cin, vx_decoder_t** out) {
     if (c->n_layers == 0 || c->n_layers > 1024) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "n_layers must be in 1..=1024");
     if (c->act > VX_ACT_SILU || c->rope_mode > VX_ROPE_NORMAL || c->no_sub_norm > 1 || c->emb_f16 > 1 || c->untied > 1)
         VX_FAIL(VX_ERR_INVALID_ARGUMENT, "act, rope_mode, no_sub_norm, emb_f16 and untied take 0 or 1");
-    if (c->head_dim != 128 && c->head_dim != 256)
-        VX_FAIL(VX_ERR_UNSUPPORTED, "head_dim %u is not supported (128 or 256)", c->head_dim);
+    if (c->head_dim != 32 && c->head_dim != 64 && c->head_dim != 128 && c->head_dim != 256)
+        VX_FAIL(VX_ERR_UNSUPPORTED, "head_dim %u is not supported (32, 64, 128 or 256)", c->head_dim);
     if (c->n_heads == 0 || c->n_kv_heads == 0 || c->n_heads % c->n_kv_heads)
         VX_FAIL(VX_ERR_INVALID_ARGUMENT, "n_heads (%u) must be a positive multiple of n_kv_heads (%u)", c->n_heads, c->n_kv_heads);
     if (c->max_ctx == 0 || c->max_ctx > kAttnMaxCtx) VX_FAIL(VX_ERR_UNSUPPORTED, "max_ctx must be in 1..=%u", kAttnMaxCtx);
@@ -1736,7 +1750,9 @@ static int create_decoder(const vx_decoder_config_t* cin, vx_decoder_t** out) {
     d->norms.assign(static_cast<size_t>(c->n_layers + 1) * kNormKinds, nullptr);
     d->norm_set.assign(d->norms.size(), 0);
     const size_t L = c->n_layers, H = c->hidden;
+    // K [layer][kv_head][max_ctx][head_dim]; V in tiles of 8 positions, [layer][kv_head][vstride / 8][head_dim][8]
     const size_t kv_elems = L * d->kvd * c->max_ctx;
+    const size_t v_elems = L * d->kvd * vstride_of(c->max_ctx);
     hipError_t e = dalloc(d, &d->d_emb, static_cast<size_t>(c->vocab) * H * 2);
     if (e == hipSuccess && c->untied) e = dalloc(d, &d->d_head, static_cast<size_t>(c->vocab) * H * 2);
     if (e == hipSuccess && pair) e = dalloc(d, &d->d_inter, round_up(c->ffn, kTileRows) * 4);
@@ -1744,7 +1760,7 @@ static int create_decoder(const vx_decoder_config_t* cin, vx_decoder_t** out) {
     if (e == hipSuccess && pair) e = hipMemset(d->d_amax, 0, static_cast<size_t>(c->n_layers) * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_rope, static_cast<size_t>(c->max_ctx) * c->head_dim * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_kc, kv_elems * 2);
-    if (e == hipSuccess) e = dalloc(d, &d->d_vc, kv_elems * 2);
+    if (e == hipSuccess) e = dalloc(d, &d->d_vc, v_elems * 2);
     if (e == hipSuccess) e = dalloc(d, &d->d_xa, H * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_xb, H * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_att, d->qd * 4);
@@ -1938,7 +1954,7 @@ static int build_stages(vx_decoder* d) {
 static int record_step(const vx_decoder* d, hipStream_t st) {
     const vx_decoder_config_t& c = d->cfg;
     const size_t L = c.n_layers;
-    const size_t layer_kv = d->kvd * c.max_ctx;
+    const size_t layer_kv = d->kvd * c.max_ctx, layer_v = d->kvd * vstride_of(c.max_ctx);
     for (size_t l = 0; l < L; ++l) {
         VX_TRY(launch_dgemv(d->stages[l * kStages + 0], st));
         AttnArgs at{};
@@ -1948,7 +1964,8 @@ static int record_step(const vx_decoder* d, hipStream_t st) {
         at.v = proj_out(d, l, VX_PROJ_V);
         at.rope = d->d_rope;
         at.kc = d->d_kc + l * layer_kv;
-        at.vc = d->d_vc + l * layer_kv;
+        at.vc = d->d_vc + l * layer_v;
+        at.vstride = vstride_of(c.max_ctx);
         at.out = d->d_att;
         at.n_heads = c.n_heads;
         at.gqa = c.n_heads / c.n_kv_heads;
@@ -2035,7 +2052,7 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
     const vx_decoder_config_t& c = d->cfg;
     const size_t L = c.n_layers, H = c.hidden, F = c.ffn;
     const bool sub = has_sub_norms(d);
-    const size_t layer_kv = d->kvd * c.max_ctx;
+    const size_t layer_kv = d->kvd * c.max_ctx, layer_v = d->kvd * vstride_of(c.max_ctx);
     const uint32_t cap = d->pf_cap;
     float* as_qkv = d->pf_as;
     float* as_o = d->pf_as + cap;
@@ -2087,7 +2104,8 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
         ra.wsv = d->proj[l * kProjKinds + VX_PROJ_V]->weight_scale;
         ra.rope = d->d_rope;
         ra.kc = d->d_kc + l * layer_kv;
-        ra.vc = d->d_vc + l * layer_kv;
+        ra.vc = d->d_vc + l * layer_v;
+        ra.vstride = vstride_of(c.max_ctx);
         ra.qbuf = d->pf_q;
         ra.n_heads = c.n_heads;
         ra.n_kv = c.n_kv_heads;
@@ -2099,7 +2117,8 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
         AttnArgs at{};
         at.ctl = d->d_ctl;
         at.kc = d->d_kc + l * layer_kv;
-        at.vc = d->d_vc + l * layer_kv;
+        at.vc = d->d_vc + l * layer_v;
+        at.vstride = vstride_of(c.max_ctx);
         at.out = d->pf_att;
         at.n_heads = c.n_heads;
         at.gqa = c.n_heads / c.n_kv_heads;
@@ -2473,12 +2492,16 @@ int vx_decoder_kv_get(const vx_decoder_t* d, uint32_t layer, uint32_t pos, uint3
         if (layer >= d->cfg.n_layers || pos >= d->cfg.max_ctx || kv_head >= d->cfg.n_kv_heads)
             VX_FAIL(VX_ERR_INVALID_ARGUMENT, "layer %u / pos %u / kv_head %u out of range", layer, pos, kv_head);
         if (n < d->cfg.head_dim) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "k and v hold %zu values, head_dim is %u", n, d->cfg.head_dim);
+        const size_t hd = d->cfg.head_dim, vs = vstride_of(d->cfg.max_ctx);
         const size_t off = (static_cast<size_t>(layer) * d->kvd * d->cfg.max_ctx) +
-                           (static_cast<size_t>(kv_head) * d->cfg.max_ctx + pos) * d->cfg.head_dim;
+                           (static_cast<size_t>(kv_head) * d->cfg.max_ctx + pos) * hd;
+        const size_t voff = static_cast<size_t>(layer) * d->kvd * vs + static_cast<size_t>(kv_head) * hd * vs +
+                            (static_cast<size_t>(pos / 8) * hd) * 8 + pos % 8;
         VX_TRY(set_device(d->device));
         VX_HIP(hipStreamSynchronize(d->stream));
-        if (k) VX_HIP(hipMemcpy(k, d->d_kc + off, d->cfg.head_dim * 2, hipMemcpyDeviceToHost));
-        if (v) VX_HIP(hipMemcpy(v, d->d_vc + off, d->cfg.head_dim * 2, hipMemcpyDeviceToHost));
+        if (k) VX_HIP(hipMemcpy(k, d->d_kc + off, hd * 2, hipMemcpyDeviceToHost));
+        // V is cached in tiles of 8 positions: the position's values are 8 elements apart
+        if (v) VX_HIP(hipMemcpy2D(v, 2, d->d_vc + voff, 16, 2, hd, hipMemcpyDeviceToHost));
         return VX_OK;
     });
 }

@@ -776,8 +776,9 @@ static int gguf_decoder_config(const vx_gguf* g, uint32_t context_limit, vx_deco
     const TensorRec* on = tensor_get(g, "output_norm.weight");
     if (on == nullptr || on->type != VX_GGML_F32 || on->n_elem != hidden)
         VX_FAIL(VX_ERR_MODEL, "tensor 'output_norm.weight' is missing or not %llu F32 values", static_cast<unsigned long long>(hidden));
-    if (head_dim != 128 && head_dim != 256)
-        VX_FAIL(VX_ERR_UNSUPPORTED, "head dimension %llu is not supported (128 or 256)", static_cast<unsigned long long>(head_dim));
+    if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)  // gpu.rs:163-165
+        VX_FAIL(VX_ERR_UNSUPPORTED, "head dimension %llu is not supported (32, 64, 128 or 256)",
+                static_cast<unsigned long long>(head_dim));
     // validate.rs:241-290: every layer's projections (ternary, of the configured shapes) and F32 norms.
     const uint64_t qd = heads * head_dim, kvd = kv_heads * head_dim;
     const uint64_t shape[7][2] = {{qd, hidden}, {kvd, hidden}, {kvd, hidden}, {hidden, qd},
@@ -811,9 +812,10 @@ static int gguf_decoder_config(const vx_gguf* g, uint32_t context_limit, vx_deco
                         static_cast<unsigned long long>(n));
         }
     }
-    // gpu.rs:141-146: the model's maximum, at most 4096 (or the caller's limit), rounded down to a multiple of 256.
+    // gpu.rs:141-146: the model's maximum, at most the caller's limit (default 4096, gpu.rs:30) and 7936
+    // (quintrit-cuda/src/layer.rs:66-67), rounded down to a multiple of 256.
     uint64_t want = std::min<uint64_t>(ctx, context_limit ? context_limit : 4096);
-    want = std::min<uint64_t>(want, 4096);
+    want = std::min<uint64_t>(want, 7936);
     if (want >= 256) want = want / 256 * 256;
     *c = vx_decoder_config_t{};
     c->struct_size = sizeof(vx_decoder_config_t);

@@ -139,7 +139,7 @@ def test_decoder_config_errors_before_device():
     c = DecoderConfig.bitnet_2b()._c()
     c.struct_size = 4
     assert L.vx_decoder_create(ctypes.byref(c), ctypes.byref(h)) == 2
-    for field, value, status in (("head_dim", 64, 6), ("max_ctx", 8192, 6), ("n_kv_heads", 3, 2), ("hidden", 100, 6),
+    for field, value, status in (("head_dim", 96, 6), ("max_ctx", 8193, 6), ("n_kv_heads", 3, 2), ("hidden", 100, 6),
                                  ("ffn", 9000, 6), ("vocab", 0, 2), ("n_layers", 0, 2)):
         c = DecoderConfig.bitnet_2b()._c()
         setattr(c, field, value)

@@ -64,7 +64,8 @@ def variant_cfg(oracle, name):
     silu_sub SiLU with sub-norms (the pair's output normed), NEOX, head_dim 128, bf16 embedding with an untied head
     relu_raw ReLU^2 without sub-norms (the gating input unnormed), Normal RoPE, f16 tied head
     relu_wide ReLU^2 without sub-norms and an FFN wider than a normed input (8420, not a multiple of 160): gate and up
-             run as the gated pair with the ReLU^2 epilogue, which also produces the down input's absmax"""
+             run as the gated pair with the ReLU^2 epilogue, which also produces the down input's absmax
+    hd64     the BitNet structure at head_dim 64 (the smallest head the reference's GPU decoder accepts, gpu.rs:163-165)"""
     M = oracle.ModelConfig
     return {
         "falcon3": oracle.falcon3(2, 256, 4, 2, 256, 9220, 1000, 640, 1e-5, 100000.0),
@@ -72,6 +73,7 @@ def variant_cfg(oracle, name):
         "silu_sub": M(2, 256, 4, 2, 128, 392, 1000, 640, 1e-5, 10000.0, oracle.ACT_SILU, oracle.ROPE_NEOX, 0, 0, 1),
         "relu_raw": M(2, 256, 4, 1, 128, 384, 1000, 640, 1e-5, 10000.0, oracle.ACT_RELU2, oracle.ROPE_NORMAL, 1, 1, 0),
         "relu_wide": M(2, 256, 4, 1, 128, 8420, 1000, 640, 1e-5, 10000.0, oracle.ACT_RELU2, oracle.ROPE_NORMAL, 1, 1, 0),
+        "hd64": M(2, 256, 8, 2, 64, 384, 1000, 640, 1e-5, 10000.0),
     }[name]
 
 
@@ -140,7 +142,7 @@ def test_tiny_generate_tokens_identical(torch_dev, oracle, max_ctx, n_prompt, n_
         model.close()
 
 
-@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw", "relu_wide"])
+@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw", "relu_wide", "hd64"])
 def test_variant_step_logits_bit_exact(torch_dev, oracle, name):
     """forward_token of each architecture variant at positions 0..299 (teacher forced; the 4-chunk attention split from
     position 256): every logit bit-identical to the oracle's, every greedy token equal."""
@@ -155,6 +157,55 @@ def test_variant_step_logits_bit_exact(torch_dev, oracle, name):
             assert got_next == want_next, f"{name}: pos {pos}"
     finally:
         dec.close()
+        model.close()
+
+
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_long_context_logits_bit_exact(torch_dev, oracle, head_dim):
+    """A context of 7936, the reference GPU decoder's largest (quintrit-cuda/src/layer.rs:66-67). The GPU prefills
+    positions 0..7934 (16 passes of up to 512 tokens); its KV cache then goes into the oracle's cache, and single steps
+    at positions 4095, 4096, 6000 and 7935 (4-chunk attention with chunks of 1024, 1088, 1536 and 1984 positions) give
+    bit-identical logits on both sides, the oracle's own key and value at each of those positions equal the GPU's, and
+    a second GPU decoder stepped through every position holds the same cache as the prefill (sampled positions) and
+    the same logits at the end. (The oracle's token loop is quadratic in the context, so it is given the cache rather
+    than run over all 7936 positions.)"""
+    n_heads = 256 // head_dim
+    cfg = oracle.ModelConfig(2, 256, n_heads, 2, head_dim, 384, 1000, 7936, 1e-5, 10000.0)
+    model = oracle.Model(cfg, 37)
+    pre = load_decoder(oracle, model)
+    ref = load_decoder(oracle, model)
+    try:
+        tokens = np.random.default_rng(head_dim).integers(0, cfg.vocab, 7936)
+        print(f"[long context] head_dim {head_dim}: prefill of 7935", flush=True)
+        pre.prefill(tokens[:7935])
+        for layer in range(cfg.n_layers):
+            for pos in range(7935):
+                for h in range(cfg.n_kv_heads):
+                    model.set_kv(layer, pos, h, *pre.kv(layer, pos, h))
+        for pos in (4095, 4096, 6000, 7935):
+            o_next, o_logits = model.forward(int(tokens[pos]), pos)
+            got, got_next = pre.step(int(tokens[pos]), pos)
+            assert_same_bits(got, o_logits, f"logits at pos {pos}")
+            assert got_next == o_next, f"pos {pos}"
+            for layer in range(cfg.n_layers):
+                for h in range(cfg.n_kv_heads):
+                    ok, ov = model.kv(layer, pos, h)
+                    gk, gv = pre.kv(layer, pos, h)
+                    assert np.array_equal(ok, gk) and np.array_equal(ov, gv), f"KV at layer {layer}, pos {pos}, head {h}"
+        print(f"[long context] head_dim {head_dim}: 7936 steps", flush=True)
+        for pos in range(7936):
+            want, want_next = ref.step(int(tokens[pos]), pos, want_logits=pos == 7935)
+        assert_same_bits(got, want, "steps to 7935 vs prefill")
+        assert got_next == want_next
+        for layer in range(cfg.n_layers):
+            for pos in range(0, 7936, 97):
+                for h in range(cfg.n_kv_heads):
+                    ka, va = pre.kv(layer, pos, h)
+                    kb, vb = ref.kv(layer, pos, h)
+                    assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"KV at layer {layer}, pos {pos}"
+    finally:
+        pre.close()
+        ref.close()
         model.close()
 
 
@@ -187,7 +238,9 @@ def test_decoder_config_switch_errors(torch_dev, oracle):
     with pytest.raises(VxError, match="struct_size"):
         check(lib().vx_decoder_create(ctypes.byref(c), ctypes.byref(h)))
     with pytest.raises(VxError, match="head_dim"):
-        Decoder(DecoderConfig(1, 256, 2, 1, 64, 256, 100, 64))
+        Decoder(DecoderConfig(1, 256, 2, 1, 96, 256, 100, 64))
+    with pytest.raises(VxError, match="max_ctx"):
+        Decoder(DecoderConfig(1, 256, 2, 1, 128, 256, 100, 8193))
     with pytest.raises(VxError, match="ffn"):
         Decoder(DecoderConfig.falcon3(1, 256, 2, 1, 128, 24580, 100, 64))
     with pytest.raises(VxError, match="ffn"):  # a normed down input is limited to 8192

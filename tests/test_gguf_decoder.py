@@ -62,7 +62,7 @@ def test_valid_file_reaches_the_device_check(tmp_path, oracle, tiny):
     ("tokenizer_too_long", ERR_MODEL, "tokenizer"),
     ("zero_heads", ERR_MODEL, "dimension"),
     ("odd_key_length", ERR_MODEL, "key_length"),
-    ("head_dim_64", ERR_UNSUPPORTED, "head dimension"),
+    ("head_dim_96", ERR_UNSUPPORTED, "head dimension"),
     ("partial_rope", ERR_UNSUPPORTED, "partial RoPE"),
     ("rope_yarn", ERR_UNSUPPORTED, "yarn"),
     ("rope_unknown", ERR_MODEL, "scaling type"),
@@ -87,7 +87,7 @@ def test_rejected_files(tmp_path, oracle, tiny, case, code, text):
         "tokenizer_too_long": dict(kvs=[("tokenizer.ggml.tokens", W.ARR, ["x"] * (c.vocab + 1), W.STR)]),
         "zero_heads": dict(kvs=[(f"{a}.attention.head_count", W.U32, 0)]),
         "odd_key_length": dict(kvs=[(f"{a}.attention.key_length", W.U32, 127)]),
-        "head_dim_64": dict(kvs=[(f"{a}.attention.key_length", W.U32, 64)]),
+        "head_dim_96": dict(kvs=[(f"{a}.attention.key_length", W.U32, 96)]),
         "partial_rope": dict(kvs=[(f"{a}.rope.dimension_count", W.U32, 64)]),
         "rope_yarn": dict(kvs=[(f"{a}.rope.scaling.type", W.STR, "yarn"), (f"{a}.rope.scaling.factor", W.F32, 4.0)]),
         "rope_unknown": dict(kvs=[(f"{a}.rope.scaling.type", W.STR, "ntk")]),
