@@ -811,6 +811,12 @@ struct AttnArgs {
     // qbuf[token][n_heads * head_dim] and their k, v already in the cache; out is [token][n_heads * head_dim]
     const uint16_t* qbuf;
     uint32_t n_tok;
+    // decode in two kernels: the scores [n_heads][max_ctx], then per chunk its f16 accumulators cy [n_heads][4][HD],
+    // its (max, sum) pairs cms [n_heads][slices][4][2] and a ticket per (head, slice) (0 between steps)
+    float* scores;
+    uint16_t* cy;
+    float* cms;
+    uint32_t* ticket;
 };
 
 constexpr uint32_t kAttnMaxCtx = 8192;  // KV positions held in LDS (scores, running maxima)
@@ -1145,6 +1151,508 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
             mf = mn;
         }
         out[d] = sf != 0.0f ? acc * (1.0f / sf) : acc;
+    }
+}
+
+// ---- decode attention: scores, then the accumulator chains ---------------------------------------------------------------
+//
+// The decode step spreads attention over many workgroups: attn_score_kernel computes every score of a position range
+// (and the RoPE and KV append of the position itself), attn_chain_kernel runs one chunk's online softmax for 64
+// coordinates of one query head, and the last chunk of a (head, coordinates) pair to finish combines the chunks.
+
+constexpr uint32_t kScoreTile = 64;   // positions per score workgroup: one per 4-lane group of 256 threads
+constexpr uint32_t kScoreHeads = 8;   // query heads (of one KV head) per score workgroup at most
+constexpr uint32_t kChainBlocks = 4;  // blocks of 32 positions of V in flight in a chain (four 8-position tiles each)
+constexpr uint32_t kChunkMax = kAttnMaxCtx / 4u;  // the longest chunk (n_kv / 4 at the largest context)
+constexpr uint32_t kShortCtx = 256;   // positions below which one chunk covers the context (n_kv < 512)
+__host__ __device__ constexpr uint32_t attn_slices(uint32_t hd) { return hd >= 64u ? hd / 64u : 1u; }
+
+// RoPE of pair i of the row at `base` of a projection (ops.rs:199-221, NEOX or Normal pairing): x0' = fma(x0, c, -(x1 s)),
+// x1' = fma(x0, s, x1 c), stored as f16 (kv_cache.rs:24-182).
+template <int HD>
+__device__ __forceinline__ void rope_pair(const ProjOut& o, uint32_t base, uint32_t i, bool normal, const float* cache,
+                                          uint16_t* dst) {
+    const uint32_t i0 = normal ? 2u * i : i, i1 = normal ? 2u * i + 1u : i + HD / 2u;
+    bool zero;
+    const float post = proj_post(o, &zero);
+    const float x0 = proj_at(o, base + i0, post, zero), x1 = proj_at(o, base + i1, post, zero);
+    const float cc = cache[2 * i], ss = cache[2 * i + 1];
+    const float x1s = x1 * ss, x1c = x1 * cc;
+    dst[i0] = f32_f16(__builtin_fmaf(x0, cc, -x1s));
+    dst[i1] = f32_f16(__builtin_fmaf(x0, ss, x1c));
+}
+
+// q . k of one position in ggml_vec_dot_f16's order (ops.rs:960-1015), four lanes per position: lane j holds accumulator
+// j (values 32 i + 8 j .. + 7 of every 32-value block i, q from LDS and k from kr, both f16), then (a0 + a2) + (a1 + a3)
+// across the group and red[k] + red[k + 4], (t0 + t1) + (t2 + t3); the result is lane 0's (the four lanes of a group
+// must run together).
+template <int HD>
+__device__ __forceinline__ float score_dot4(const uint16_t* q, const uint4 (&kr)[HD / 32], uint32_t j) {
+    float acc[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) {
+        const uint4 qv = *reinterpret_cast<const uint4*>(q + 32 * i + 8 * j);
+        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+        const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+        for (int l = 0; l < 8; ++l)
+            acc[l] = __builtin_fmaf(f16_f32(static_cast<uint16_t>(qw[l >> 1] >> ((l & 1) * 16))),
+                                    f16_f32(static_cast<uint16_t>(kw[l >> 1] >> ((l & 1) * 16))), acc[l]);
+    }
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+        acc[l] = acc[l] + __shfl_xor(acc[l], 2);
+        acc[l] = acc[l] + __shfl_xor(acc[l], 1);
+    }
+    const float t0 = acc[0] + acc[4], t1 = acc[1] + acc[5], t2 = acc[2] + acc[6], t3 = acc[3] + acc[7];
+    return (t0 + t1) + (t2 + t3);
+}
+
+// Scores of positions p0 .. p0 + 63 (p0 = blockIdx.y * 64, below pos + 1) for up to kScoreHeads query heads of one KV
+// head (blockIdx.x: KV head, head group), so that each K row is read once for the heads that share it. The workgroup
+// whose range holds the position itself rotates its k (the first head group also appends k and v to the cache); every
+// workgroup rotates its heads' q. Four lanes per position as ggml_vec_dot_f16 (ops.rs:960-1015): lane j holds
+// accumulator j (values 32 i + 8 j .. + 7 of every 32-value block i), then (a0 + a2) + (a1 + a3) across the group,
+// red[k] + red[k + 4] and (t0 + t1) + (t2 + t3) in lane 0, times the scale.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_score_kernel(AttnArgs a) {
+    constexpr int kBlk = HD / 32;
+    __shared__ __align__(16) uint16_t qh[kScoreHeads][HD];
+    __shared__ __align__(16) uint16_t kp[HD];
+    __shared__ __align__(16) uint16_t vp[HD];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t hgroups = (a.gqa + kScoreHeads - 1u) / kScoreHeads;
+    const uint32_t kvh = blockIdx.x / hgroups, hg = blockIdx.x - kvh * hgroups;
+    const uint32_t h0 = kvh * a.gqa + hg * kScoreHeads;
+    const uint32_t nh = min(kScoreHeads, a.gqa - hg * kScoreHeads);
+    const uint32_t pos = a.ctl->pos, seq = pos + 1u;
+    const uint32_t p0 = blockIdx.y * kScoreTile;
+    if (p0 >= seq) return;
+    const bool own = pos - p0 < kScoreTile;
+    const bool normal = a.rope_normal != 0u;
+    const float* cache = a.rope + static_cast<size_t>(pos) * HD;
+    // this thread's K row goes out first (its latency overlaps the rotations' loads); the position itself comes later
+    const uint32_t j = tid & 3u, p = p0 + (tid >> 2);
+    uint4 kr[kBlk];
+    if (p < seq && p != pos) {
+        const uint16_t* row = a.kc + (static_cast<size_t>(kvh) * a.max_ctx + p) * HD + 8 * j;
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i) kr[i] = *reinterpret_cast<const uint4*>(row + 32 * i);
+    }
+    for (uint32_t t = tid; t < nh * (HD / 2u); t += 256u) {
+        const uint32_t hh = t / (HD / 2u), i = t - hh * (HD / 2u);
+        rope_pair<HD>(a.q, (h0 + hh) * HD, i, normal, cache, qh[hh]);
+    }
+    if (own) {
+        for (uint32_t t = tid; t < HD / 2u + HD; t += 256u) {
+            if (t < HD / 2u) {
+                rope_pair<HD>(a.k, kvh * HD, t, normal, cache, kp);
+            } else {
+                bool zero;
+                const float post = proj_post(a.v, &zero);
+                vp[t - HD / 2u] = f32_f16(proj_at(a.v, kvh * HD + (t - HD / 2u), post, zero));
+            }
+        }
+    }
+    __syncthreads();
+    if (own && hg == 0) {
+        uint16_t* vt = a.vc + static_cast<size_t>(kvh) * HD * a.vstride;
+        for (uint32_t t = tid; t < HD; t += 256u) {
+            a.kc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + t] = kp[t];
+            vt[(static_cast<size_t>(pos >> 3) * HD + t) * 8u + (pos & 7u)] = vp[t];
+        }
+    }
+    if (p >= seq) return;  // all four lanes of a position leave together; no barrier follows
+    if (p == pos) {
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i) kr[i] = *reinterpret_cast<const uint4*>(kp + 32 * i + 8 * j);
+    }
+    for (uint32_t hh = 0; hh < nh; ++hh) {
+        const float sv = score_dot4<HD>(qh[hh], kr, j);
+        if (j == 0) a.scores[static_cast<size_t>(h0 + hh) * a.max_ctx + p] = sv * a.scale;
+    }
+}
+
+// The running maximum's combine (attend_range, attention.rs:436-468: the maximum moves only on score > max): `later`
+// replaces `earlier` only when larger. A NaN score never moves the maximum, so it enters a scan as -inf.
+__device__ __forceinline__ float max_later(float earlier, float later) { return later > earlier ? later : earlier; }
+
+// The pieces of one chunk's online softmax (attend_range, attention.rs:436-468) over positions st .. en - 1, in blocks
+// of 32 positions b_first .. b_end - 1 (fac[i] is the factor of position 32 b_first + i, bflag[i] marks block b_first + i
+// when it holds a new maximum).
+//
+// chunk_factors (all NT threads; one barrier inside, one expected after): the running maximum by a scan (runs of
+// R = ceil(len / NT) positions per thread, an inclusive scan of the run maxima over the lanes and a prefix over the
+// waves), then per position ms = expf(m_old - score), vs = 1 at a new maximum and ms = 1, vs = expf(score - max)
+// otherwise, stored as -ms or vs (the sign marks the case). Returns the chunk's maximum (-inf when empty).
+template <int NT>
+__device__ __forceinline__ float chunk_factors(const float* scores, uint32_t st, uint32_t en, uint32_t b_first, float* fac,
+                                               uint32_t* bflag, float* wtot, const uint64_t* etab) {
+    constexpr uint32_t kW = NT / 64;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t len = en - st, R = (len + NT - 1u) / NT;  // R <= 8
+    const uint32_t nb = (en + 31u) / 32u - b_first;
+    for (uint32_t i = tid; i < nb; i += NT) bflag[i] = 0u;
+    float sv[8];
+    float loc = -__builtin_inff();
+#pragma unroll
+    for (uint32_t r = 0; r < 8; ++r) {
+        const uint32_t i = tid * R + r;
+        sv[r] = r < R && i < len ? scores[i] : 0.0f;
+        if (r < R && i < len) loc = max_later(loc, sv[r] != sv[r] ? -__builtin_inff() : sv[r]);
+    }
+    float v = loc;  // inclusive scan over the lanes, earlier lanes first
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) {
+        const float o = __shfl_up(v, sh);
+        if (lane >= static_cast<uint32_t>(sh)) v = max_later(o, v);
+    }
+    if (lane == 63) wtot[wave] = v;
+    __syncthreads();
+    float before = -__builtin_inff(), cmax = -__builtin_inff();
+    for (uint32_t w = 0; w < wave; ++w) before = max_later(before, wtot[w]);
+    for (uint32_t w = 0; w < kW; ++w) cmax = max_later(cmax, wtot[w]);
+    float prev = __shfl_up(v, 1);
+    prev = max_later(before, lane == 0 ? -__builtin_inff() : prev);
+    const uint32_t off = st - 32u * b_first;
+    const auto tab = [&](uint32_t k) { return etab[k]; };
+#pragma unroll
+    for (uint32_t r = 0; r < 8; ++r) {
+        const uint32_t i = tid * R + r;
+        if (r < R && i < len) {
+            const float sc = sv[r];
+            const float f = sc > prev ? -glibc_expf_with(prev - sc, tab) : glibc_expf_with(sc - prev, tab);
+            fac[off + i] = f;
+            if (__builtin_signbit(f)) bflag[(off + i) >> 5] = 1u;
+            prev = max_later(prev, sc != sc ? -__builtin_inff() : sc);
+        }
+    }
+    return cmax;
+}
+
+// The V tiles of 8 positions (16 bytes per coordinate) of block b for coordinate d, up to tile t_last (the last one
+// with a position of the chunk: every read stays inside the cache).
+template <int HD>
+__device__ __forceinline__ void load_vblock(const uint16_t* vt, uint32_t b, uint32_t d, uint32_t t_last, u32x4 (&r)[4]) {
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+        const uint32_t t = min(4u * b + i, t_last);
+        r[i] = *reinterpret_cast<const u32x4*>(vt + (static_cast<size_t>(t) * HD + d) * 8u);
+    }
+}
+
+__device__ __forceinline__ float vhalf(const u32x4 (&w)[4], int e) {
+    const u32x4 ww = w[e >> 3];
+    const uint32_t word = (e & 7) < 2 ? ww.x : (e & 7) < 4 ? ww.y : (e & 7) < 6 ? ww.z : ww.w;
+    return f16_f32(static_cast<uint16_t>(word >> ((e & 1) * 16)));
+}
+
+// The FP16 accumulator of one coordinate (one wave, a coordinate per lane): y = f16(y * ms), y = f16(fma(v, vs, y)) per
+// position, a block per step with the V tiles kChainBlocks blocks ahead in `ring` (already requested for b_first ..);
+// a whole block without a new maximum takes y = f16(fma(v, vs, y)) alone. With a self value, the position `self` (not
+// yet visible in the cache to every workgroup) takes it instead of the cache's.
+template <int HD>
+__device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const uint16_t* vt, uint32_t d, uint32_t st,
+                                         uint32_t en, uint32_t b_first, uint32_t b_end, uint32_t t_last, const float* fac,
+                                         const uint32_t* bflag, uint32_t self, uint16_t vself) {
+    float y = 0.0f;
+    float4 nf[8];
+    uint32_t nflag;
+    auto load_fac = [&](uint32_t b) {
+        const float* fb = fac + 32u * (b - b_first);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nf[i] = *reinterpret_cast<const float4*>(fb + 4 * i);
+        nflag = bflag[b - b_first];
+    };
+    load_fac(b_first);
+    for (uint32_t b0 = b_first; b0 < b_end; b0 += kChainBlocks) {
+#pragma unroll
+        for (uint32_t k = 0; k < kChainBlocks; ++k) {
+            const uint32_t b = b0 + k;
+            if (b < b_end) {  // wave-uniform
+                u32x4 w[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) w[i] = ring[k][i];
+                load_vblock<HD>(vt, b + kChainBlocks, d, t_last, ring[k]);
+                float f[32];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    f[4 * i] = nf[i].x;
+                    f[4 * i + 1] = nf[i].y;
+                    f[4 * i + 2] = nf[i].z;
+                    f[4 * i + 3] = nf[i].w;
+                }
+                const uint32_t flag = __builtin_amdgcn_readfirstlane(nflag);
+                load_fac(min(b + 1u, b_end - 1u));
+                const uint32_t p0 = 32u * b;
+                if (self - p0 < 32u) {  // the position itself lies in this block
+                    const uint32_t e = self - p0, ti = e >> 3, q = (e & 7u) >> 1, sh = (e & 1u) * 16u;
+                    const uint32_t keep = ~(0xffffu << sh), ins = static_cast<uint32_t>(vself) << sh;
+#pragma unroll
+                    for (uint32_t i = 0; i < 4; ++i) {
+                        w[i].x = ti == i && q == 0 ? (w[i].x & keep) | ins : w[i].x;
+                        w[i].y = ti == i && q == 1 ? (w[i].y & keep) | ins : w[i].y;
+                        w[i].z = ti == i && q == 2 ? (w[i].z & keep) | ins : w[i].z;
+                        w[i].w = ti == i && q == 3 ? (w[i].w & keep) | ins : w[i].w;
+                    }
+                }
+                if (p0 >= st && p0 + 32u <= en && flag == 0u) {
+#pragma unroll
+                    for (int e = 0; e < 32; ++e) y = r16(__builtin_fmaf(vhalf(w, e), f[e], y));
+                } else {  // a new maximum or the chunk's edge: positions outside [st, en) keep y
+                    const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(32u, en - p0);
+#pragma unroll
+                    for (int e = 0; e < 32; ++e) {
+                        const bool in = static_cast<uint32_t>(e) >= e0 && static_cast<uint32_t>(e) < e1;
+                        const bool nm = __builtin_signbit(f[e]);
+                        const float ev = __builtin_fabsf(f[e]);
+                        const float ms = nm ? ev : 1.0f, vs = nm ? 1.0f : ev;
+                        float t = r16(y * ms);
+                        t = r16(__builtin_fmaf(vhalf(w, e), vs, t));
+                        y = in ? t : y;
+                    }
+                }
+            }
+        }
+    }
+    return y;
+}
+
+// The chunk's sum s = fma(s, ms, vs) over its positions in order (one wave, the same value in every lane).
+__device__ __forceinline__ float chain_sum(uint32_t st, uint32_t en, uint32_t b_first, uint32_t b_end, const float* fac,
+                                           const uint32_t* bflag) {
+    float ssum = 0.0f;
+    for (uint32_t b = b_first; b < b_end; ++b) {
+        const float* fb = fac + 32u * (b - b_first);
+        float f[32];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 q = *reinterpret_cast<const float4*>(fb + 4 * i);
+            f[4 * i] = q.x;
+            f[4 * i + 1] = q.y;
+            f[4 * i + 2] = q.z;
+            f[4 * i + 3] = q.w;
+        }
+        const uint32_t flag = __builtin_amdgcn_readfirstlane(bflag[b - b_first]);
+        const uint32_t p0 = 32u * b;
+        if (p0 >= st && p0 + 32u <= en && flag == 0u) {
+#pragma unroll
+            for (int e = 0; e < 32; ++e) ssum = ssum + f[e];
+        } else {
+            const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(32u, en - p0);
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const bool in = static_cast<uint32_t>(e) >= e0 && static_cast<uint32_t>(e) < e1;
+                const bool nm = __builtin_signbit(f[e]);
+                const float ev = __builtin_fabsf(f[e]);
+                const float t = __builtin_fmaf(ssum, nm ? ev : 1.0f, nm ? 1.0f : ev);
+                ssum = in ? t : ssum;
+            }
+        }
+    }
+    return ssum;
+}
+
+// The exponential's table in LDS (from literals, so that no load goes out ahead of the V tiles).
+__device__ __forceinline__ void fill_etab(uint64_t* etab) {
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (uint32_t i = 0; i < 32; ++i) etab[i] = expf_tab(i);
+    }
+}
+
+// One chunk (blockIdx.y) of the online softmax of query head h for coordinates 64 sl .. 64 sl + 63 (blockIdx.x =
+// h * slices + sl), from the scores of attn_score_kernel; below a padded KV length of 512 one chunk covers every
+// position, from 512 on four chunks of ceil(n_kv / 4) (attend_head, attention.rs:483-542). All 256 threads turn the
+// scores into factors, then wave 0 runs the accumulators of the slice's coordinates while wave 1 runs the sum. One
+// chunk writes the output; of four, each stores its f16 accumulators and (max, sum), and the last to take the ticket
+// of (h, sl) combines them in chunk order (attention.rs:526-541).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
+    constexpr uint32_t kSlices = attn_slices(HD);
+    constexpr uint32_t kLanes = HD >= 64 ? 64u : static_cast<uint32_t>(HD);
+    __shared__ __align__(16) float fac[kChunkMax + 64u];
+    __shared__ uint32_t bflag[kChunkMax / 32u + 2u];
+    __shared__ float wtot[4];
+    __shared__ float s_sum;
+    __shared__ uint32_t s_last;
+    __shared__ uint64_t etab[32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t h = blockIdx.x / kSlices, sl = blockIdx.x - h * kSlices, c = blockIdx.y;
+    const uint32_t pos = a.ctl->pos, seq = pos + 1u;
+    uint32_t n_kv = (seq + 255u) / 256u * 256u;
+    if (n_kv > a.max_ctx) n_kv = a.max_ctx;
+    const bool split = n_kv >= 512u;
+    const uint32_t chunk = split ? (n_kv + 3u) / 4u : seq;
+    if (c >= (split ? 4u : 1u)) return;
+    const uint32_t st = c * chunk, en = min(min(st + chunk, n_kv), seq);
+    const bool any = st < en;
+    const uint32_t kvh = h / a.gqa;
+    const uint32_t d = sl * 64u + (lane < kLanes ? lane : 0u);  // a lane without a coordinate reads coordinate 0
+    const uint16_t* vt = a.vc + static_cast<size_t>(kvh) * HD * a.vstride;
+    const uint32_t b_first = st / 32u, b_end = any ? (en + 31u) / 32u : b_first + 1u;
+    const uint32_t t_last = any ? (en - 1u) / 8u : st / 8u;
+    fill_etab(etab);
+    u32x4 ring[kChainBlocks][4];
+    if (wave == 0 && any) {
+#pragma unroll
+        for (uint32_t k = 0; k < kChainBlocks; ++k) load_vblock<HD>(vt, b_first + k, d, t_last, ring[k]);
+    }
+    float cmax = -__builtin_inff();
+    if (any) cmax = chunk_factors<256>(a.scores + static_cast<size_t>(h) * a.max_ctx + st, st, en, b_first, fac, bflag, wtot, etab);
+    __syncthreads();
+    float y = 0.0f;
+    if (any && wave == 0) {
+        y = chain_y<HD>(ring, vt, d, st, en, b_first, b_end, t_last, fac, bflag, ~0u, 0);
+    } else if (wave == 1) {
+        const float ssum = any ? chain_sum(st, en, b_first, b_end, fac, bflag) : 0.0f;
+        if (lane == 0) s_sum = ssum;
+    }
+    __syncthreads();
+    const float ssum = s_sum;
+    float* out = a.out + static_cast<size_t>(h) * HD;
+    if (!split) {
+        if (wave == 0 && lane < kLanes) {
+            const float s_inv = ssum == 0.0f ? 0.0f : 1.0f / ssum;
+            out[sl * 64u + lane] = y * s_inv;
+        }
+        return;
+    }
+    // four chunks: this chunk's part, then the ticket of (h, sl); the fourth to arrive combines in chunk order
+    uint16_t* cy = a.cy + static_cast<size_t>(h) * 4u * HD;
+    float* cms = a.cms + (static_cast<size_t>(h) * kSlices + sl) * 8u;
+    if (wave == 0) {
+        if (lane < kLanes) cy[c * HD + sl * 64u + lane] = f32_f16(y);
+        if (lane == 0) {
+            cms[2u * c] = any ? cmax : -__builtin_inff();
+            cms[2u * c + 1u] = ssum;
+        }
+        __threadfence();
+    }
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(a.ticket + blockIdx.x, 1u) == 3u ? 1u : 0u;
+    __syncthreads();
+    if (s_last == 0u || wave != 0) return;
+    __threadfence();
+    if (lane == 0) atomicExch(a.ticket + blockIdx.x, 0u);
+    if (lane >= kLanes) return;
+    const uint32_t dd = sl * 64u + lane;
+    float mf = -__builtin_inff(), sf = 0.0f, acc = 0.0f;
+    for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t ks = k * chunk, ke = min(min(ks + chunk, n_kv), seq);
+        if (ks >= ke) continue;
+        const float sk = __builtin_nontemporal_load(cms + 2u * k + 1u);
+        if (sk == 0.0f) continue;
+        const float mk = __builtin_nontemporal_load(cms + 2u * k);
+        const float mn = __builtin_fmaxf(mf, mk);
+        const float so = glibc_expf(mf - mn);
+        const float sn = glibc_expf(mk - mn);
+        const float vn = f16_f32(__builtin_nontemporal_load(cy + k * HD + dd)) * sn;
+        acc = __builtin_fmaf(acc, so, vn);
+        const float ssn = sk * sn;
+        sf = __builtin_fmaf(sf, so, ssn);
+        mf = mn;
+    }
+    out[dd] = sf != 0.0f ? acc * (1.0f / sf) : acc;
+}
+
+// The decode step's attention while the context is short (pos < kShortCtx: one chunk, no split) in one kernel per
+// (head, 64 coordinates): the RoPE of q, k, v of the position (the first slice of the first head of each KV head
+// appends k and v; every workgroup uses its own copy of the position itself), the scores of every position
+// (512 threads, four lanes per position, as attn_score_kernel), the factors, then the accumulators (wave 0) and the sum
+// (wave 1), and the output.
+template <int HD>
+__global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
+    constexpr uint32_t kSlices = attn_slices(HD);
+    constexpr uint32_t kLanes = HD >= 64 ? 64u : static_cast<uint32_t>(HD);
+    constexpr int kBlk = HD / 32;
+    __shared__ __align__(16) uint16_t qh[HD];
+    __shared__ __align__(16) uint16_t kp[HD];
+    __shared__ __align__(16) uint16_t vp[HD];
+    __shared__ __align__(16) float sc[kShortCtx];
+    __shared__ __align__(16) float fac[kShortCtx + 64u];
+    __shared__ uint32_t bflag[kShortCtx / 32u + 2u];
+    __shared__ float wtot[8];
+    __shared__ float s_sum;
+    __shared__ uint64_t etab[32];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t h = blockIdx.x / kSlices, sl = blockIdx.x - h * kSlices;
+    const uint32_t pos = a.ctl->pos, seq = pos + 1u;  // seq <= kShortCtx (the host's choice of graph)
+    const uint32_t kvh = h / a.gqa;
+    const uint32_t d = sl * 64u + (lane < kLanes ? lane : 0u);
+    const uint16_t* kb = a.kc + static_cast<size_t>(kvh) * a.max_ctx * HD;
+    uint16_t* vt = a.vc + static_cast<size_t>(kvh) * HD * a.vstride;
+    const uint32_t b_end = (seq + 31u) / 32u, t_last = (seq - 1u) / 8u;
+    fill_etab(etab);
+    u32x4 ring[kChainBlocks][4];
+    if (wave == 0) {
+#pragma unroll
+        for (uint32_t k = 0; k < kChainBlocks; ++k) load_vblock<HD>(vt, k, d, t_last, ring[k]);
+    }
+    // K rows of this thread's two positions (the position itself later, from kp)
+    const uint32_t j = tid & 3u, g = tid >> 2;
+    uint4 k0[kBlk], k1[kBlk];
+    if (g < seq && g != pos) {
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i) k0[i] = *reinterpret_cast<const uint4*>(kb + static_cast<size_t>(g) * HD + 8 * j + 32 * i);
+    }
+    if (g + 128u < seq && g + 128u != pos) {
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i)
+            k1[i] = *reinterpret_cast<const uint4*>(kb + static_cast<size_t>(g + 128u) * HD + 8 * j + 32 * i);
+    }
+    const bool normal = a.rope_normal != 0u;
+    const float* cache = a.rope + static_cast<size_t>(pos) * HD;
+    if (tid < HD / 2u) {
+        rope_pair<HD>(a.q, h * HD, tid, normal, cache, qh);
+    } else if (tid < HD) {
+        rope_pair<HD>(a.k, kvh * HD, tid - HD / 2u, normal, cache, kp);
+    } else if (tid < 2u * HD) {
+        bool zero;
+        const float post = proj_post(a.v, &zero);
+        vp[tid - HD] = f32_f16(proj_at(a.v, kvh * HD + (tid - HD), post, zero));
+    }
+    __syncthreads();
+    if (h % a.gqa == 0 && sl == 0 && tid < HD) {
+        a.kc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + tid] = kp[tid];
+        vt[(static_cast<size_t>(pos >> 3) * HD + tid) * 8u + (pos & 7u)] = vp[tid];
+    }
+    const uint16_t vself = vp[d];
+    if (g == pos) {
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i) k0[i] = *reinterpret_cast<const uint4*>(kp + 32 * i + 8 * j);
+    }
+    if (g + 128u == pos) {
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i) k1[i] = *reinterpret_cast<const uint4*>(kp + 32 * i + 8 * j);
+    }
+    if (g < seq) {
+        const float s0 = score_dot4<HD>(qh, k0, j);
+        if (j == 0) sc[g] = s0 * a.scale;
+    }
+    if (g + 128u < seq) {
+        const float s1 = score_dot4<HD>(qh, k1, j);
+        if (j == 0) sc[g + 128u] = s1 * a.scale;
+    }
+    __syncthreads();
+    (void)chunk_factors<512>(sc, 0u, seq, 0u, fac, bflag, wtot, etab);
+    __syncthreads();
+    float y = 0.0f;
+    if (wave == 0) {
+        y = chain_y<HD>(ring, vt, d, 0u, seq, 0u, b_end, t_last, fac, bflag, pos, vself);
+    } else if (wave == 1) {
+        const float ssum = chain_sum(0u, seq, 0u, b_end, fac, bflag);
+        if (lane == 0) s_sum = ssum;
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kLanes) {
+        const float ssum = s_sum;
+        const float s_inv = ssum == 0.0f ? 0.0f : 1.0f / ssum;
+        a.out[static_cast<size_t>(h) * HD + sl * 64u + lane] = y * s_inv;
     }
 }
 
@@ -1489,7 +1997,43 @@ static int launch_attention_mode(const AttnArgs& a, uint32_t head_dim, hipStream
     return VX_OK;
 }
 
-int launch_attention(const AttnArgs& a, uint32_t head_dim, hipStream_t s) { return launch_attention_mode<false>(a, head_dim, s); }
+// The decode step's attention: the score kernel over every 64-position range of max_ctx (ranges past the position
+// return at once), then the chain kernel over (head, 64 coordinates) x 4 chunks (chunks past the split return).
+int launch_attention(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
+    const uint32_t hgroups = (a.gqa + kScoreHeads - 1u) / kScoreHeads;
+    const dim3 sgrid(a.n_heads / a.gqa * hgroups, (a.max_ctx + kScoreTile - 1u) / kScoreTile);
+    const dim3 cgrid(a.n_heads * attn_slices(head_dim), 4u);
+    if (a.max_ctx > kAttnMaxCtx) VX_FAIL(VX_ERR_INTERNAL, "attention context %u above %u", a.max_ctx, kAttnMaxCtx);
+    if (head_dim == 256) {
+        hipLaunchKernelGGL(attn_score_kernel<256>, sgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attn_chain_kernel<256>, cgrid, dim3(256), 0, s, a);
+    } else if (head_dim == 128) {
+        hipLaunchKernelGGL(attn_score_kernel<128>, sgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attn_chain_kernel<128>, cgrid, dim3(256), 0, s, a);
+    } else if (head_dim == 64) {
+        hipLaunchKernelGGL(attn_score_kernel<64>, sgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attn_chain_kernel<64>, cgrid, dim3(256), 0, s, a);
+    } else if (head_dim == 32) {
+        hipLaunchKernelGGL(attn_score_kernel<32>, sgrid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL(attn_chain_kernel<32>, cgrid, dim3(256), 0, s, a);
+    } else {
+        VX_FAIL(VX_ERR_INTERNAL, "no attention kernel for head_dim %u", head_dim);
+    }
+    VX_HIP(hipGetLastError());
+    return VX_OK;
+}
+
+// The short-context form (every position below kShortCtx): one kernel per (head, 64 coordinates).
+int launch_attention_short(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
+    const dim3 grid(a.n_heads * attn_slices(head_dim));
+    if (head_dim == 256) hipLaunchKernelGGL(attn_short_kernel<256>, grid, dim3(512), 0, s, a);
+    else if (head_dim == 128) hipLaunchKernelGGL(attn_short_kernel<128>, grid, dim3(512), 0, s, a);
+    else if (head_dim == 64) hipLaunchKernelGGL(attn_short_kernel<64>, grid, dim3(512), 0, s, a);
+    else if (head_dim == 32) hipLaunchKernelGGL(attn_short_kernel<32>, grid, dim3(512), 0, s, a);
+    else VX_FAIL(VX_ERR_INTERNAL, "no attention kernel for head_dim %u", head_dim);
+    VX_HIP(hipGetLastError());
+    return VX_OK;
+}
 
 int launch_attention_prefill(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
     return launch_attention_mode<true>(a, head_dim, s);
@@ -1546,6 +2090,10 @@ struct vx_decoder {
     uint32_t kslices[vx::kProjKinds];
     float* d_as;                      // activation scale of each projection stage, reused by every layer
     float *d_att, *d_logits;
+    float* d_scores;                  // decode attention: scores [n_heads][max_ctx]
+    uint16_t* d_cy;                   // per chunk f16 accumulators [n_heads][4][head_dim]
+    float* d_cms;                     // per chunk (max, sum) [n_heads][slices][4][2]
+    uint32_t* d_aticket;              // chunks done per (head, slice) (0 between steps)
     unsigned long long* d_key;        // argmax key and ticket of the head kernel
     uint32_t* d_ticket;
     vx::Ctl* d_ctl;
@@ -1574,8 +2122,10 @@ struct vx_decoder {
     std::vector<PfGraph> pf_graphs;
     vx::Ctl* h_ctl;                   // pinned
     hipStream_t stream;
-    hipGraph_t graph;
+    hipGraph_t graph;                 // the decode step; graph_short: the same for positions below kShortCtx
     hipGraphExec_t exec;
+    hipGraph_t graph_short;
+    hipGraphExec_t exec_short;
     bool ready;
     size_t bytes;
     std::mutex mu;
@@ -1599,8 +2149,12 @@ static int set_device(int dev) {
 static void drop_graph(vx_decoder* d) {
     if (d->exec) (void)hipGraphExecDestroy(d->exec);
     if (d->graph) (void)hipGraphDestroy(d->graph);
+    if (d->exec_short) (void)hipGraphExecDestroy(d->exec_short);
+    if (d->graph_short) (void)hipGraphDestroy(d->graph_short);
     d->exec = nullptr;
     d->graph = nullptr;
+    d->exec_short = nullptr;
+    d->graph_short = nullptr;
     d->ready = false;
     for (auto& g : d->pf_graphs) {
         if (g.exec) (void)hipGraphExecDestroy(g.exec);
@@ -1639,7 +2193,8 @@ static void destroy_decoder(vx_decoder* d) {
     for (auto* p : d->norms)
         if (p) (void)hipFree(p);
     void* bufs[] = {d->d_emb, d->d_head, d->d_inter, d->d_rope,   d->d_kc,    d->d_vc,    d->d_xa,
-                    d->d_xb,  d->d_att,  d->d_logits, d->d_key, d->d_ctl, d->d_prompt, d->d_tokens, d->d_amax};
+                    d->d_xb,  d->d_att,  d->d_logits, d->d_key, d->d_ctl, d->d_prompt, d->d_tokens, d->d_amax,
+                    d->d_scores, d->d_cy, d->d_cms, d->d_aticket};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (int32_t* b : d->d_part)
@@ -1765,6 +2320,12 @@ static int create_decoder(const vx_decoder_config_t* cin, vx_decoder_t** out) {
     if (e == hipSuccess) e = dalloc(d, &d->d_xb, H * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_att, d->qd * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_logits, static_cast<size_t>(c->vocab) * 4);
+    const size_t n_sl = static_cast<size_t>(c->n_heads) * attn_slices(c->head_dim);
+    if (e == hipSuccess) e = dalloc(d, &d->d_scores, static_cast<size_t>(c->n_heads) * c->max_ctx * 4);
+    if (e == hipSuccess) e = dalloc(d, &d->d_cy, d->qd * 4 * 2);
+    if (e == hipSuccess) e = dalloc(d, &d->d_cms, n_sl * 8 * 4);
+    if (e == hipSuccess) e = dalloc(d, &d->d_aticket, n_sl * 4);
+    if (e == hipSuccess) e = hipMemset(d->d_aticket, 0, n_sl * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_as, kStages * sizeof(float));
     if (e == hipSuccess) e = dalloc(d, &d->d_key, 16);
     if (e == hipSuccess) e = hipMemset(d->d_key, 0, 16);
@@ -1951,7 +2512,7 @@ static int build_stages(vx_decoder* d) {
 }
 
 // Enqueues one decode step on `st` (also the sequence captured into the step graph).
-static int record_step(const vx_decoder* d, hipStream_t st) {
+static int record_step(const vx_decoder* d, hipStream_t st, bool short_ctx) {
     const vx_decoder_config_t& c = d->cfg;
     const size_t L = c.n_layers;
     const size_t layer_kv = d->kvd * c.max_ctx, layer_v = d->kvd * vstride_of(c.max_ctx);
@@ -1972,7 +2533,11 @@ static int record_step(const vx_decoder* d, hipStream_t st) {
         at.max_ctx = c.max_ctx;
         at.rope_normal = c.rope_mode == VX_ROPE_NORMAL ? 1u : 0u;
         at.scale = 1.0f / sqrtf(static_cast<float>(c.head_dim));
-        VX_TRY(launch_attention(at, c.head_dim, st));
+        at.scores = d->d_scores;
+        at.cy = d->d_cy;
+        at.cms = d->d_cms;
+        at.ticket = d->d_aticket;
+        VX_TRY(short_ctx ? launch_attention_short(at, c.head_dim, st) : launch_attention(at, c.head_dim, st));
         for (int s = 1; s < kStages; ++s) VX_TRY(launch_dgemv(d->stages[l * kStages + s], st));
     }
     HeadArgs h{};
@@ -2247,20 +2812,25 @@ static int prepare(vx_decoder* d) {
     if (d->cfg.untied && !d->head_set) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "the head is not set");
     drop_graph(d);
     VX_TRY(build_stages(d));
-    VX_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
-    const int st = record_step(d, d->stream);
-    hipGraph_t g = nullptr;
-    const hipError_t e = hipStreamEndCapture(d->stream, &g);
-    if (st != VX_OK) {
-        if (g) (void)hipGraphDestroy(g);
-        return st;
+    for (int form = 0; form < 2; ++form) {  // 0: any position, 1: positions below kShortCtx
+        VX_HIP(hipStreamBeginCapture(d->stream, hipStreamCaptureModeThreadLocal));
+        const int st = record_step(d, d->stream, form == 1);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(d->stream, &g);
+        if (st != VX_OK) {
+            if (g) (void)hipGraphDestroy(g);
+            return st;
+        }
+        VX_HIP(e);
+        (form == 0 ? d->graph : d->graph_short) = g;
+        VX_HIP(hipGraphInstantiate(form == 0 ? &d->exec : &d->exec_short, g, nullptr, nullptr, 0));
     }
-    VX_HIP(e);
-    d->graph = g;
-    VX_HIP(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
     d->ready = true;
     return VX_OK;
 }
+
+// The step graph for position pos (the short-context attention below kShortCtx).
+static hipGraphExec_t step_exec(const vx_decoder* d, size_t pos) { return pos < kShortCtx ? d->exec_short : d->exec; }
 
 static int put_ctl(vx_decoder* d, uint32_t pos, uint32_t token, uint32_t n_prompt, uint32_t n_out) {
     d->h_ctl->pos = pos;
@@ -2393,7 +2963,7 @@ int vx_decoder_step(vx_decoder_t* d, uint32_t token, uint32_t pos, float* logits
         VX_TRY(set_device(d->device));
         VX_TRY(prepare(d));
         VX_TRY(put_ctl(d, pos, token, 0, 0));
-        VX_HIP(hipGraphLaunch(d->exec, d->stream));
+        VX_HIP(hipGraphLaunch(step_exec(d, pos), d->stream));
         VX_HIP(hipStreamSynchronize(d->stream));
         if (logits) VX_HIP(hipMemcpy(logits, d->d_logits, static_cast<size_t>(d->cfg.vocab) * 4, hipMemcpyDeviceToHost));
         if (out_next) {
@@ -2424,7 +2994,7 @@ int vx_decoder_generate(vx_decoder_t* d, const uint32_t* prompt, size_t n_prompt
         VX_HIP(hipMemcpy(d->d_prompt, prompt, n_prompt * 4, hipMemcpyHostToDevice));
         // the prompt in prefill passes (their last head gives the first new token), then one step per further token
         VX_TRY(run_prefill(d, 0, static_cast<uint32_t>(n_prompt), static_cast<uint32_t>(n_prompt), static_cast<uint32_t>(n_new)));
-        for (size_t i = n_prompt; i < steps; ++i) VX_HIP(hipGraphLaunch(d->exec, d->stream));
+        for (size_t i = n_prompt; i < steps; ++i) VX_HIP(hipGraphLaunch(step_exec(d, i), d->stream));
         VX_HIP(hipStreamSynchronize(d->stream));
         if (n_new) VX_HIP(hipMemcpy(out_tokens, d->d_tokens, n_new * 4, hipMemcpyDeviceToHost));
         return VX_OK;
@@ -2449,7 +3019,7 @@ int vx_decoder_generate_stepwise(vx_decoder_t* d, const uint32_t* prompt, size_t
         VX_TRY(prepare(d));
         VX_HIP(hipMemcpy(d->d_prompt, prompt, n_prompt * 4, hipMemcpyHostToDevice));
         VX_TRY(put_ctl(d, 0, 0, static_cast<uint32_t>(n_prompt), static_cast<uint32_t>(n_new)));
-        for (size_t i = 0; i < steps; ++i) VX_HIP(hipGraphLaunch(d->exec, d->stream));
+        for (size_t i = 0; i < steps; ++i) VX_HIP(hipGraphLaunch(step_exec(d, i), d->stream));
         VX_HIP(hipStreamSynchronize(d->stream));
         if (n_new) VX_HIP(hipMemcpy(out_tokens, d->d_tokens, n_new * 4, hipMemcpyDeviceToHost));
         return VX_OK;

@@ -46,7 +46,9 @@ VX_HD inline float bits_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
 VX_HD inline double bits_f64(uint64_t u) { return __builtin_bit_cast(double, u); }
 VX_HD inline uint64_t f64_bits(double d) { return __builtin_bit_cast(uint64_t, d); }
 
-VX_HD inline float glibc_expf(float x) {
+// The function with the table read through tab(i) (a device caller may keep the table in LDS).
+template <typename Tab>
+VX_HD inline float glibc_expf_with(float x, Tab tab) {
     const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;
     const double kShift = 0x1.8p+52;
     const double kC0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -65,7 +67,7 @@ VX_HD inline float glibc_expf(float x) {
     const uint64_t ki = f64_bits(kd);
     kd -= kShift;
     const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    uint64_t t = expf_tab(static_cast<uint32_t>(ki % 32u));
+    uint64_t t = tab(static_cast<uint32_t>(ki % 32u));
     t += ki << (52 - 5);
     const double s = bits_f64(t);
     const double z = __builtin_fma(kC0, r, kC1);
@@ -75,5 +77,7 @@ VX_HD inline float glibc_expf(float x) {
     y = y * s;
     return static_cast<float>(y);
 }
+
+VX_HD inline float glibc_expf(float x) { return glibc_expf_with(x, expf_tab); }
 
 }  // namespace vx

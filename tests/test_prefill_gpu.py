@@ -84,7 +84,7 @@ def test_prefill_continues_a_cache(torch_dev, oracle):
         model.close()
 
 
-@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw", "relu_wide", "hd64"])
+@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw", "relu_wide", "hd64", "gqa16"])
 def test_prefill_variants(torch_dev, oracle, name):
     """Every architecture variant: a 300-token prefill (the 4-chunk attention split from position 256) equals the
     steps (KV cache and last logits) and the oracle."""
