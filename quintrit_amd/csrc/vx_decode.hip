@@ -575,9 +575,15 @@ struct DJob {
     uint32_t act, n8;      // gated pair: GateAct; rows below n8 take the vector exponential
     uint32_t* amax_out;    // gated pair: atomic maximum of |act_out| as float bits (a plain unnormed consumer), or null
     uint32_t rows, padded_rows, n_tiles, n_chunks, kslices, slice_chunks, item_begin;
+    uint32_t w_bytes;      // bytes of w (and w2) in the device layout, below kBufferOutOfRange
 };
 
 constexpr int kMaxStageJobs = 3;
+// Buffer loads of the weights: the resource's fourth word for raw (unformatted, unswizzled) access, an offset past any
+// matrix (such a load returns zeros without touching memory) and the non-temporal cache policy.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr uint32_t kBufferOutOfRange = 0x80000000u;
+constexpr int kLoadNt = 2;
 constexpr int kDPer = 7;  // chunks of a work item per wave at most (kStChunks / 16)
 
 struct DStageArgs {
@@ -587,38 +593,39 @@ struct DStageArgs {
     uint32_t tbr;       // tile row bytes of in.n columns
     float* as_out;      // the stage's activation scale (workgroup 0)
     uint32_t variant;   // the kernel instance (host side: the input's length and kinds)
-    uint32_t loop;      // every job has one K slice: a workgroup takes items blockIdx.x, + gridDim.x, ...
+    uint32_t loop;      // every job has one K slice: a workgroup takes items blockIdx.x and blockIdx.x + gridDim.x
     uint32_t grid;      // workgroups of the launch
     uint32_t* amax_clear;  // zeroed by the stage (the StageInput::amax a later stage of the layer accumulates), or null
+    uint32_t dper;         // chunk loads per wave and item of the kernel instance (1, 4 or 7): at least any wave's count
 };
 
 __constant__ DigitTable g_digits = make_digit_table();
 
-// One workgroup per work item, or (loop) fewer workgroups taking every gridDim.x-th item, which computes the stage
-// input once for several items of the same K slice. Order of the loads: the stage input, the digit table, then wave
-// w's chunks q0 + w, q0 + w + 16, ... of the tile (1 KiB each in the device layout), so the input is computed while
-// the weights are in flight; a looping workgroup loads the next item's chunks as the current ones are consumed. The
-// digit-nibble table and the arithmetic are those of the lone GEMV (vx_gemv.hip). Only the entries of the item's own
-// chunks are staged.
-template <int P4, int SA, int SB, bool MULTI>
+// One workgroup per work item, or (loop) a workgroup per two items of the same K slice, which computes the stage input
+// once for both. Order of the loads: the stage input, the digit table, then wave w's chunks q0 + w, q0 + w + 16, ... of
+// the tile (1 KiB each in the device layout) of the first item, so the input is computed while the weights are in
+// flight; the second item's chunks go out one by one as the first item's are consumed. Every wave issues exactly DPER
+// chunk loads per item (buffer loads; a chunk the wave does not have reads past the buffer's end, which returns zeros
+// without a memory access), so each chunk is waited for on its own. The digit-nibble table and the arithmetic are those
+// of the lone GEMV (vx_gemv.hip). Only the entries of the item's own chunks are staged.
+template <int P4, int SA, int SB, bool MULTI, int DPER>
 __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of the digit nibbles of byte B (first half)
     __shared__ uint2 st[kStChunks * 16];
     __shared__ InputLds s;
-    __shared__ int red[MULTI ? 2 : 1][MULTI ? 2 : 1][kNT / 64][64];  // [item parity][gate, up][wave][lane]
+    __shared__ int red[MULTI ? 2 : 1][MULTI ? 2 : 1][kNT / 64][64];  // [item][gate, up][wave][lane]
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const char* tabb = reinterpret_cast<const char*>(tab);
     const uint32_t lane_off = (lane & 31u) * 4u;
 
-    // A work item: its job, tile and K slice, and where wave `wave`'s chunks are.
+    // A work item: its job, tile and K slice, and where wave `wave`'s chunks are (byte offsets in the matrix).
     struct Item {
         DJob jb;
         uint32_t tile, ks, q0, nq, cnt;
-        const g_u4* wp;
-        const g_u4* wp2;
-        size_t cs;  // uint4 between chunks q and q + 1 of the tile
+        uint32_t off;  // the lane's 16 bytes of chunk 0 of the tile
+        uint32_t cs;   // bytes between chunks q and q + 1 of the tile
     };
     auto locate = [&](uint32_t item) {
         Item it;
@@ -635,23 +642,25 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
         it.nq = min(it.jb.slice_chunks, it.jb.n_chunks - it.q0);
         const uint32_t nl = MULTI && it.jb.w2 != nullptr ? 2u * it.nq : it.nq;  // gate chunks, then (pair) up chunks
         it.cnt = wave < nl ? (nl - wave + kTileGroup - 1) / kTileGroup : 0u;
-        const size_t tile_off = (static_cast<size_t>(grp) * kTileGroup * it.jb.n_chunks + tt) * 64u + lane;
-        it.wp = (const g_u4*)(it.jb.w) + tile_off;
-        it.wp2 = MULTI && it.jb.w2 != nullptr ? (const g_u4*)(it.jb.w2) + tile_off : it.wp;
-        it.cs = static_cast<size_t>(T) * 64u;
+        it.off = ((grp * kTileGroup * it.jb.n_chunks + tt) * 64u + lane) * 16u;
+        it.cs = T * 1024u;
         return it;
     };
-    auto chunk_load = [&](const Item& it, int i) {
+    // chunk i of an item for this wave (an absent chunk, or any chunk when !valid, reads past the end)
+    auto issue_one = [&](const Item& it, bool valid, int i) {
         const uint32_t c = wave + kTileGroup * static_cast<uint32_t>(i);
-        const bool up = MULTI && c >= it.nq;
-        return __builtin_nontemporal_load((up ? it.wp2 : it.wp) + (it.q0 + (up ? c - it.nq : c)) * it.cs);
+        const bool up = MULTI && it.jb.w2 != nullptr && c >= it.nq;
+        const uint32_t q = up ? c - it.nq : c;
+        const bool have = valid && static_cast<uint32_t>(i) < it.cnt;
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(up ? it.jb.w2 : it.jb.w), 0, it.jb.w_bytes, kBufferRsrcWord3);
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             r, have ? it.off + (it.q0 + q) * it.cs : kBufferOutOfRange, 0, kLoadNt));
     };
 
-    uint32_t item = blockIdx.x;
-    Item it = locate(item);
-    // The staged slice: every item of a workgroup has the same K slice (one workgroup per item, or a looping stage
-    // whose jobs have one slice each).
-    const uint32_t c0 = it.q0 * 16u, c1 = min((it.q0 + it.nq) * 16u, a.tbr);
+    const Item ia = locate(blockIdx.x);
+    // The staged slice: both items of a workgroup have the same K slice (a looping stage's jobs have one slice each).
+    const uint32_t c0 = ia.q0 * 16u, c1 = min((ia.q0 + ia.nq) * 16u, a.tbr);
     uint32_t lo, hi;
     slice_window(a.in.n, c0, c1, &lo, &hi);
     InputRegs<P4, SA, SB> r;
@@ -660,14 +669,17 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) dig[k] = g_digits.v[(tid + k * kNT) >> 3];
     if (a.amax_clear != nullptr && blockIdx.x == 0 && tid == 0) *a.amax_clear = 0u;
-    // The weight loads go out once the input and the digit table have arrived: a load issued under a runtime condition
-    // (the wave's chunk count) leaves the compiler unsure how many loads follow an earlier one, so any wait for the input
-    // after them would also wait for most of the weights.
+    // The weight loads go out once the input and the digit table have arrived (the waits for the input would otherwise
+    // also wait for the weights, which complete after them).
     input_arrived(r, dig[0] ^ dig[1]);
-    u32x4 b[kDPer];
+    u32x4 ba[DPER];
 #pragma unroll
-    for (int i = 0; i < kDPer; ++i)
-        if (static_cast<uint32_t>(i) < it.cnt) b[i] = chunk_load(it, i);
+    for (int i = 0; i < DPER; ++i) ba[i] = issue_one(ia, true, i);
+    const uint32_t item_b = blockIdx.x + gridDim.x;
+    const bool has_b = MULTI && a.loop && item_b < a.total_items;
+    Item ib{};
+    u32x4 bb[MULTI ? DPER : 1];
+    if constexpr (MULTI) ib = locate(has_b ? item_b : blockIdx.x);
 
     float y[P4][4];
     stage_y(a.in, r, s, blockIdx.x == 0, y);
@@ -683,25 +695,21 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     }
     float act_scale;
     int act_sum;
-    stage_quant(y, s, mx, a.in.n, a.tbr, c0, (it.q0 + it.nq) * 16u, lo, st, &act_scale, &act_sum);
+    stage_quant(y, s, mx, a.in.n, a.tbr, c0, (ia.q0 + ia.nq) * 16u, lo, st, &act_scale, &act_sum);
     if (blockIdx.x == 0 && tid == 0) *a.as_out = act_scale;
 
-    // One item: its chunks from b (refilled with the chunks of the workgroup's next item, `refill`, as they are
-    // consumed), the slice sums reduced in LDS (parity selects the buffer) and stored by wave 0. Returns the next item.
-    auto process = [&](const Item& it, uint32_t parity, uint32_t refill) {
-        const bool more = MULTI && a.loop && refill < a.total_items;
-        Item nt{};
-        if (more) nt = locate(refill);
+    // The sums of an item's chunks (from b) into red[slot] (gate, and up for a pair); with `next`, chunk i of the second
+    // item goes out once chunk i of this one is consumed.
+    auto accumulate = [&](const Item& it, const u32x4 (&b)[DPER], uint32_t slot, bool next) {
         const bool pair = MULTI && it.jb.w2 != nullptr;
         int acc_lo = 0, acc_hi = 0, acc2_lo = 0, acc2_hi = 0;
 #pragma unroll
-        for (int i = 0; i < kDPer; ++i) {
-            u32x4& bi = b[i];
+        for (int i = 0; i < DPER; ++i) {
             if (static_cast<uint32_t>(i) < it.cnt) {
                 const uint32_t c = wave + kTileGroup * i;
                 const bool up = pair && c >= it.nq;
                 const uint32_t q = up ? c - it.nq : c;  // chunk of the slice
-                const uint32_t dw[4] = {bi.x, bi.y, bi.z, bi.w};
+                const uint32_t dw[4] = {b[i].x, b[i].y, b[i].z, b[i].w};
                 const uint2 e = st[q * 16u + (lane & 15u)];
                 __builtin_amdgcn_sched_barrier(0);
                 uint32_t t[16];
@@ -710,8 +718,6 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
                     const uint32_t addr = __builtin_amdgcn_perm(dw[k >> 2], lane_off, 0x0c0c0000u | ((4u + (k & 3)) << 8));
                     t[k] = *reinterpret_cast<const uint32_t*>(tabb + addr);
                 }
-                // the register is free: the next item's chunk goes into it while this one is summed
-                if (more && static_cast<uint32_t>(i) < nt.cnt) bi = chunk_load(nt, i);
                 if (!pair) {
                     dot4_bcast<0>(acc_lo, acc_hi, e.x, e.y, t[0], t[1], t[2], t[3]);
                     dot4_bcast<4>(acc_lo, acc_hi, e.x, e.y, t[4], t[5], t[6], t[7]);
@@ -731,66 +737,67 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
                         acc_hi += h;
                     }
                 }
-            } else if (more && static_cast<uint32_t>(i) < nt.cnt) {
-                bi = chunk_load(nt, i);
+            }
+            if constexpr (MULTI) {
+                if (next) bb[i] = issue_one(ib, has_b, i);
             }
         }
-        red[parity][0][wave][lane] = acc_lo + 16 * acc_hi;
-        if (pair) red[parity][MULTI ? 1 : 0][wave][lane] = acc2_lo + 16 * acc2_hi;
-        // One barrier per item: the next item writes the other parity, and the one after this parity only after the
-        // next item's barrier, which wave 0 reaches once it has read these sums.
-        __syncthreads();
-        if (wave == 0) {
-            // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in
-            // slice 0
-            const DJob& jb = it.jb;
-            int v = 0;
-#pragma unroll
-            for (int w = 0; w < kNT / 64; ++w) v += red[parity][0][w][lane];
-            const uint32_t row = it.tile * kTileRows + lane;
-            // act_sum holds the codes of this slice's elements only: every slice subtracts its own
-            if (it.ks == 0) v += 8 * jb.dsum[row];
-            v -= act_sum;
-            if (!pair) {
-                jb.part[static_cast<size_t>(it.ks) * jb.padded_rows + row] = v;
-            } else {
-                int v2 = 0;
-#pragma unroll
-                for (int w = 0; w < kNT / 64; ++w) v2 += red[parity][MULTI ? 1 : 0][w][lane];
-                v2 += 8 * jb.dsum2[row] - act_sum;
-                // the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170
-                const bool zero = !(act_scale > 0.0f);
-                const float g = zero ? 0.0f : static_cast<float>(v) * (jb.ws / act_scale);
-                const float u = zero ? 0.0f : static_cast<float>(v2) * (jb.ws2 / act_scale);
-                float o;
-                if (jb.act == kActSilu) {
-                    const float ex = row < jb.n8 ? ggml_expf(0.0f - g) : glibc_expf(-g);
-                    const float den = 1.0f + ex;
-                    const float sl = g / den;
-                    o = sl * u;
-                } else {
-                    const float pos = g > 0.0f ? g : 0.0f;
-                    const float sq = pos * pos;
-                    o = sq * u;
-                }
-                if (row < jb.rows) jb.act_out[row] = o;
-                if (jb.amax_out != nullptr) {  // the consumer's absmax (NaN never counts, as in stage_window)
-                    float ao = row < jb.rows ? __builtin_fabsf(o) : 0.0f;
-                    if (!(ao > 0.0f)) ao = 0.0f;
-                    ao = wave_max_f32(ao);
-                    if (lane == 0 && ao > 0.0f) atomicMax(jb.amax_out, __float_as_uint(ao));
-                }
-            }
-        }
-        return nt;
+        red[slot][0][wave][lane] = acc_lo + 16 * acc_hi;
+        if (pair) red[slot][MULTI ? 1 : 0][wave][lane] = acc2_lo + 16 * acc2_hi;
     };
-    // Items item, item + gridDim.x, ... (one unless the stage loops).
-    for (uint32_t parity = 0;; parity ^= 1u) {
-        const uint32_t next = item + gridDim.x;
-        const Item nt = process(it, parity, next);
-        if (!(MULTI && a.loop && next < a.total_items)) break;
-        item = next;
-        it = nt;
+    // Wave 0 after the barrier: the slice sums of an item from red[slot] and its outputs.
+    auto epilogue = [&](const Item& it, uint32_t slot) {
+        const bool pair = MULTI && it.jb.w2 != nullptr;
+        // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in slice 0
+        const DJob& jb = it.jb;
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < kNT / 64; ++w) v += red[slot][0][w][lane];
+        const uint32_t row = it.tile * kTileRows + lane;
+        // act_sum holds the codes of this slice's elements only: every slice subtracts its own
+        if (it.ks == 0) v += 8 * jb.dsum[row];
+        v -= act_sum;
+        if (!pair) {
+            jb.part[static_cast<size_t>(it.ks) * jb.padded_rows + row] = v;
+            return;
+        }
+        int v2 = 0;
+#pragma unroll
+        for (int w = 0; w < kNT / 64; ++w) v2 += red[slot][MULTI ? 1 : 0][w][lane];
+        v2 += 8 * jb.dsum2[row] - act_sum;
+        // the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170
+        const bool zero = !(act_scale > 0.0f);
+        const float g = zero ? 0.0f : static_cast<float>(v) * (jb.ws / act_scale);
+        const float u = zero ? 0.0f : static_cast<float>(v2) * (jb.ws2 / act_scale);
+        float o;
+        if (jb.act == kActSilu) {
+            const float ex = row < jb.n8 ? ggml_expf(0.0f - g) : glibc_expf(-g);
+            const float den = 1.0f + ex;
+            const float sl = g / den;
+            o = sl * u;
+        } else {
+            const float pos = g > 0.0f ? g : 0.0f;
+            const float sq = pos * pos;
+            o = sq * u;
+        }
+        if (row < jb.rows) jb.act_out[row] = o;
+        if (jb.amax_out != nullptr) {  // the consumer's absmax (NaN never counts, as in stage_window)
+            float ao = row < jb.rows ? __builtin_fabsf(o) : 0.0f;
+            if (!(ao > 0.0f)) ao = 0.0f;
+            ao = wave_max_f32(ao);
+            if (lane == 0 && ao > 0.0f) atomicMax(jb.amax_out, __float_as_uint(ao));
+        }
+    };
+    accumulate(ia, ba, 0u, true);
+    if constexpr (MULTI) {
+        if (has_b) accumulate(ib, bb, 1u, false);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        epilogue(ia, 0u);
+        if constexpr (MULTI) {
+            if (has_b) epilogue(ib, 1u);
+        }
     }
 }
 
@@ -1960,25 +1967,29 @@ int launch_pf_stage(const PfStageArgs& a, hipStream_t s) {
 // embedding inputs of up to kPlainMax elements without a norm (the SwiGLU output of a model without sub-norms).
 enum DVariant : uint32_t { kDv4K = 0, kDv8K = 1, kDvPlain = 2 };
 
-// MULTI: the instance that loops over items and runs gated pairs; the others take one plain item per workgroup.
+template <int P4, int SA, int SB, bool MULTI>
+static void launch_dgemv_d(const DStageArgs& a, hipStream_t s) {
+    if (a.dper <= 1) hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, 1>), dim3(a.grid), dim3(kNT), 0, s, a);
+    else if (a.dper <= 4) hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, 4>), dim3(a.grid), dim3(kNT), 0, s, a);
+    else hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, kDPer>), dim3(a.grid), dim3(kNT), 0, s, a);
+}
+
+// MULTI: the instance that takes two items per workgroup and runs gated pairs; the others take one plain item.
 int launch_dgemv(const DStageArgs& a, hipStream_t s) {
     const bool multi = a.loop || a.job[0].w2 != nullptr;
+    if (a.dper == 0 || a.dper > static_cast<uint32_t>(kDPer)) VX_FAIL(VX_ERR_INTERNAL, "stage with %u chunks per wave", a.dper);
     switch (a.variant) {
         case kDv4K:
-            if (multi)
-                hipLaunchKernelGGL((dgemv_kernel<1, kMaxSlicesA, kMaxSlicesB, true>), dim3(a.grid), dim3(kNT), 0, s, a);
-            else
-                hipLaunchKernelGGL((dgemv_kernel<1, kMaxSlicesA, kMaxSlicesB, false>), dim3(a.grid), dim3(kNT), 0, s, a);
+            if (multi) launch_dgemv_d<1, kMaxSlicesA, kMaxSlicesB, true>(a, s);
+            else launch_dgemv_d<1, kMaxSlicesA, kMaxSlicesB, false>(a, s);
             break;
         case kDv8K:
-            if (multi)
-                hipLaunchKernelGGL((dgemv_kernel<2, kMaxSlicesA, kMaxSlicesB, true>), dim3(a.grid), dim3(kNT), 0, s, a);
-            else
-                hipLaunchKernelGGL((dgemv_kernel<2, kMaxSlicesA, kMaxSlicesB, false>), dim3(a.grid), dim3(kNT), 0, s, a);
+            if (multi) launch_dgemv_d<2, kMaxSlicesA, kMaxSlicesB, true>(a, s);
+            else launch_dgemv_d<2, kMaxSlicesA, kMaxSlicesB, false>(a, s);
             break;
         default:  // a wide plain input is a down projection's, split into several K slices: one item per workgroup
             if (multi) VX_FAIL(VX_ERR_INTERNAL, "a looping stage with a %u-element input", a.in.n);
-            hipLaunchKernelGGL((dgemv_kernel<kPlainMax / (4 * kNT), 0, 0, false>), dim3(a.grid), dim3(kNT), 0, s, a);
+            launch_dgemv_d<kPlainMax / (4 * kNT), 0, 0, false>(a, s);
             break;
     }
     VX_HIP(hipGetLastError());
@@ -2439,6 +2450,9 @@ static int build_stages(vx_decoder* d) {
                 j.dsum = mg->d_dsum;
                 j.w2 = mu->d_w;
                 j.dsum2 = mu->d_dsum;
+                j.w_bytes = static_cast<uint32_t>(mg->g.device_bytes);
+                if (mg->g.device_bytes >= kBufferOutOfRange || mu->g.device_bytes != mg->g.device_bytes)
+                    VX_FAIL(VX_ERR_UNSUPPORTED, "gate/up matrices of %zu and %zu bytes", mg->g.device_bytes, mu->g.device_bytes);
                 j.act_out = d->d_inter;
                 j.amax_out = sub ? nullptr : d->d_amax + l;
                 j.ws = mg->weight_scale;
@@ -2460,6 +2474,9 @@ static int build_stages(vx_decoder* d) {
                     j.w = m->d_w;
                     j.dsum = m->d_dsum;
                     j.part = d->d_part[k];
+                    j.w_bytes = static_cast<uint32_t>(m->g.device_bytes);
+                    if (m->g.device_bytes >= kBufferOutOfRange)
+                        VX_FAIL(VX_ERR_UNSUPPORTED, "a projection of %zu bytes (at most 2 GiB)", m->g.device_bytes);
                     j.rows = static_cast<uint32_t>(m->g.rows);
                     j.padded_rows = static_cast<uint32_t>(m->g.padded_rows);
                     j.n_tiles = static_cast<uint32_t>(m->g.n_tiles);
@@ -2471,11 +2488,21 @@ static int build_stages(vx_decoder* d) {
                 }
             }
             a.total_items = items;
-            // A stage whose jobs have one K slice each loops over its items with one workgroup per CU.
+            // A stage whose jobs have one K slice each and more items than CUs gives a workgroup two items.
             bool one_slice = true;
             for (uint32_t jj = 0; jj < a.n_jobs; ++jj) one_slice = one_slice && a.job[jj].kslices == 1;
             a.loop = one_slice && items > static_cast<uint32_t>(d->num_cus) ? 1u : 0u;
-            a.grid = a.loop ? static_cast<uint32_t>(d->num_cus) : items;
+            a.grid = a.loop ? std::max(static_cast<uint32_t>(d->num_cus), (items + 1u) / 2u) : items;
+            // chunks per wave of the largest item (a pair's gate and up chunks count together): the instance loads
+            // 1, 4 or kDPer
+            uint32_t most = 0;
+            for (uint32_t jj = 0; jj < a.n_jobs; ++jj) {
+                const uint32_t nl = a.job[jj].w2 != nullptr ? 2u * a.job[jj].slice_chunks : a.job[jj].slice_chunks;
+                most = std::max(most, (nl + kTileGroup - 1u) / kTileGroup);
+            }
+            if (most > static_cast<uint32_t>(kDPer))
+                VX_FAIL(VX_ERR_INTERNAL, "stage %d with %u chunks per wave (at most %d)", s, most, kDPer);
+            a.dper = most <= 1u ? 1u : (most <= 4u ? 4u : static_cast<uint32_t>(kDPer));
             StageInput& in = a.in;
             if (s == 0 && l == 0) {  // embedding -> attention norm
                 in = stage_input(d, kInEmbed, H, nullptr, d->d_xa, nw[VX_NORM_ATTN]);
