@@ -649,7 +649,42 @@ def build_decoder_gpu(torch, cfg, seed: int):
     return dec, trits
 
 
-def decode_measure(torch, model: str, n_prompt: int = 64, n_new: int = 256, runs: int = 2, layers: int = 0):
+SWEEP_CONTEXTS = (416, 2048, 3900, 7000)  # the reference's published Falcon3-10B context sweep (with its ctx 62)
+SWEEP_STEPS = 8
+
+
+def context_sweep(torch, dec, cfg, runs: int = 2):
+    """Decode time per token at the contexts of the reference's Falcon3-10B sweep: a random prompt of ctx tokens
+    prefilled, then SWEEP_STEPS + 1 greedy tokens (generate); per token = (generate - prefill alone) / SWEEP_STEPS, the
+    steps at positions ctx .. ctx + SWEEP_STEPS - 1. Bytes per step: the trits (0.2 B per weight), the 16-bit head and
+    the K and V rows of every cached position (f16)."""
+    import numpy as np
+    out = []
+    kv_row = cfg.n_kv_heads * cfg.head_dim * 2 * 2 * cfg.n_layers  # K and V, f16, every layer
+    for ctx in SWEEP_CONTEXTS:
+        if ctx + SWEEP_STEPS + 1 > cfg.max_ctx:
+            continue
+        prompt = np.random.default_rng(ctx).integers(0, cfg.vocab, ctx)
+        dec.generate(prompt, SWEEP_STEPS + 1)  # warm-up
+        t_pre = t_gen = float("inf")
+        for _ in range(runs):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            dec.prefill(prompt, want_logits=False)
+            t_pre = min(t_pre, time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            dec.generate(prompt, SWEEP_STEPS + 1)
+            t_gen = min(t_gen, time.perf_counter() - t0)
+        ms = (t_gen - t_pre) / SWEEP_STEPS * 1e3
+        kv = kv_row * (ctx + SWEEP_STEPS / 2)
+        out.append({"ctx": ctx, "ms_per_token": round(ms, 4), "tok_s": round(1e3 / ms, 1),
+                    "kv_bytes_per_token": int(kv), "prefill_ms": round(t_pre * 1e3, 2)})
+        log(f"context {ctx}: {ms:.4f} ms/token, prefill {t_pre * 1e3:.1f} ms")
+    return out
+
+
+def decode_measure(torch, model: str, n_prompt: int = 64, n_new: int = 256, runs: int = 2, layers: int = 0,
+                   sweep: bool = True):
     """Prefill and greedy decode of a random-init model on the GPU (build_decoder_gpu): a 64-token random prompt
     ingested by one prefill (vx_decoder_prefill; the reference feeds it one forward_token per position,
     engine.rs:627-630), then n_new greedy tokens, each one replay of the decode-step graph. Times (wall clock around
@@ -660,7 +695,8 @@ def decode_measure(torch, model: str, n_prompt: int = 64, n_new: int = 256, runs
     import numpy as np
     from quintrit_amd.decoder import DecoderConfig
     falcon = model == "falcon3-10b"
-    cfg = DecoderConfig.falcon3_10b(n_layers=layers or 40) if falcon else DecoderConfig.bitnet_2b()
+    # Falcon3 at the reference GPU decoder's largest context (quintrit-cuda/src/layer.rs:66-67), for the sweep
+    cfg = DecoderConfig.falcon3_10b(max_ctx=7936, n_layers=layers or 40) if falcon else DecoderConfig.bitnet_2b()
     log(f"building a random-init {model}-shaped model on the GPU")
     dec, trits = build_decoder_gpu(torch, cfg, 0xB17)
     prompt = np.random.default_rng(0xB17).integers(0, cfg.vocab, n_prompt)
@@ -682,6 +718,7 @@ def decode_measure(torch, model: str, n_prompt: int = 64, n_new: int = 256, runs
             if again != toks:
                 raise RuntimeError(f"{model}: generation is not repeatable")
         ms_tok = (t_gen - t_pre) / max(1, n_new - 1) * 1e3
+        sweep_r = context_sweep(torch, dec, cfg) if falcon and sweep else None
     finally:
         dec.close()
     head_bytes = cfg.vocab * cfg.hidden * 2
@@ -708,6 +745,14 @@ def decode_measure(torch, model: str, n_prompt: int = 64, n_new: int = 256, runs
          "prefill_roofline": dict(pre_roof, kernel=f"one prefill pass over {n_prompt} tokens (batched MFMA GEMMs, "
                                   f"per-token norms, attention); bytes = trits / 5 + head, ops = 2 n trits"),
          "generate_ms": round(t_gen * 1e3, 3), "first_tokens": toks[:8]}
+    if sweep_r:
+        alg_w = trits / 5.0 + head_bytes
+        for e in sweep_r:
+            b = alg_w + e["kv_bytes_per_token"]
+            e["roofline"] = {"bound": "hbm", "achieved": round(b / (e["ms_per_token"] / 1e3) / 1e9, 1),
+                             "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                             "frac": round(b / (e["ms_per_token"] / 1e3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        r["context_sweep"] = sweep_r
     log(f"{model}: {ms_tok:.4f} ms/token ({1e3 / ms_tok:.1f} tok/s), prefill of {n_prompt} tokens {t_pre * 1e3:.3f} ms")
     return r, cfg, prompt
 
