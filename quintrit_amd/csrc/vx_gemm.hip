@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
 
     // Chunk 2 ks + s of the lane's rows; a chunk past the row (odd n_chunks) reads the last one and is replaced by
     // zero trits when it is decoded.
-    auto load_w = [&](uint32_t ks, u32x4g (&wv)[2]) {
+    auto load_w = [&](uint32_t ks, u32x4g (&wv)[2]) __attribute__((always_inline)) {
         const uint32_t q = min(ks * kStepChunks + half, a.n_chunks - 1u);
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
@@ -200,17 +200,20 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
         const uint32_t tg = min(tt * T + rem / 64u, a.n_tg - 1u);
         return (static_cast<size_t>(ks * 5u + kb) * a.n_tg + tg) * 64u + (rem & 63u);
     };
-    uint4 bv0, bv1, bv2;
-    auto load_b = [&](uint32_t ks) {
-        bv0 = a.xs[b_index(ks, 0)];
-        if (kBPer > 1) bv1 = a.xs[b_index(ks, 1)];
-        if (kBPer > 2) bv2 = a.xs[b_index(ks, 2)];
-    };
-    auto store_b = [&](uint32_t buf) {
-        if (tid < kB) bs[buf][tid] = bv0;
-        if (kBPer > 1 && tid + kGemmWaves * 64u < kB) bs[buf][tid + kGemmWaves * 64u] = bv1;
-        if (kBPer > 2 && tid + 2u * kGemmWaves * 64u < kB) bs[buf][tid + 2u * kGemmWaves * 64u] = bv2;
-    };
+    // B fragments of a step in named registers (three per thread at most: an array or a struct here ends up in
+    // scratch memory once the steps rotate through three sets)
+#define VX_LOAD_B(ks, r0, r1, r2)                            \
+    do {                                                     \
+        r0 = a.xs[b_index((ks), 0)];                         \
+        if (kBPer > 1) r1 = a.xs[b_index((ks), 1)];          \
+        if (kBPer > 2) r2 = a.xs[b_index((ks), 2)];          \
+    } while (0)
+#define VX_STORE_B(buf, r0, r1, r2)                                                           \
+    do {                                                                                      \
+        if (tid < kB) bs[(buf)][tid] = r0;                                                    \
+        if (kBPer > 1 && tid + kGemmWaves * 64u < kB) bs[(buf)][tid + kGemmWaves * 64u] = r1; \
+        if (kBPer > 2 && tid + 2u * kGemmWaves * 64u < kB) bs[(buf)][tid + 2u * kGemmWaves * 64u] = r2; \
+    } while (0)
 
     v16i acc[2][T];
 #pragma unroll
@@ -218,57 +221,70 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int g = 0; g < T; ++g) acc[rb][g] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
-    // One K step ahead: the loads of step ks + 1 (B first, then weights) go out before step ks is multiplied. Every
-    // load is unconditional (the index is clamped at the last step), so the compiler's waits stay exact: the multiply
-    // waits only for step ks's weights, the LDS store at the end of the step only for the B fragments.
-    u32x4g wc[2], wn[2];
-    if (ks0 < ks1) {
-        load_b(ks0);
-        load_w(ks0, wc);
-        store_b(0);
-    }
-    for (uint32_t ks = ks0; ks < ks1; ++ks) {
-        const uint32_t cur = (ks - ks0) & 1u;
-        const uint32_t kn = min(ks + 1, ks1 - 1);
-        load_b(kn);
-        load_w(kn, wn);
-        __syncthreads();  // bs[cur] is complete; every wave is done with bs[cur ^ 1]
-        if (active) {
-            const bool inside = ks * kStepChunks + half < a.n_chunks;
-            v4i A[2][5];
+    // The products of step ks: weights wc, B fragments from bs[buf].
+    auto multiply = [&](uint32_t ks, const u32x4g (&wc)[2], uint32_t buf) __attribute__((always_inline)) {
+        const bool inside = ks * kStepChunks + half < a.n_chunks;
+        v4i A[2][5];
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-                const uint32_t dw[4] = {inside ? wc[rb].x : kZeroWord, inside ? wc[rb].y : kZeroWord,
-                                        inside ? wc[rb].z : kZeroWord, inside ? wc[rb].w : kZeroWord};
+        for (int rb = 0; rb < 2; ++rb) {
+            const uint32_t dw[4] = {inside ? wc[rb].x : kZeroWord, inside ? wc[rb].y : kZeroWord,
+                                    inside ? wc[rb].z : kZeroWord, inside ? wc[rb].w : kZeroWord};
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    int t[4];
+            for (int m = 0; m < 4; ++m) {
+                int t[4];
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + b) << 8));
-                        t[b] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
-                    }
-                    A[rb][m] = v4i{t[0], t[1], t[2], t[3]};
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + b) << 8));
+                    t[b] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
                 }
-                A[rb][4] = v4i{static_cast<int>(d4_bytes(dw[0])), static_cast<int>(d4_bytes(dw[1])),
-                               static_cast<int>(d4_bytes(dw[2])), static_cast<int>(d4_bytes(dw[3]))};
+                A[rb][m] = v4i{t[0], t[1], t[2], t[3]};
             }
-            // K block outer, token group inner: 2 T independent accumulators between two MFMAs on the same one.
+            A[rb][4] = v4i{static_cast<int>(d4_bytes(dw[0])), static_cast<int>(d4_bytes(dw[1])),
+                           static_cast<int>(d4_bytes(dw[2])), static_cast<int>(d4_bytes(dw[3]))};
+        }
+        // K block outer, token group inner: 2 T independent accumulators between two MFMAs on the same one.
 #pragma unroll
-            for (int kb = 0; kb < 5; ++kb) {
+        for (int kb = 0; kb < 5; ++kb) {
 #pragma unroll
-                for (int g = 0; g < T; ++g) {
-                    const uint4 b = bs[cur][(kb * T + g) * 64u + lane];
-                    const v4i B = v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
-                    acc[0][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0][kb], B, acc[0][g], 0, 0, 0);
-                    acc[1][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1][kb], B, acc[1][g], 0, 0, 0);
-                }
+            for (int g = 0; g < T; ++g) {
+                const uint4 b = bs[buf][(kb * T + g) * 64u + lane];
+                const v4i B = v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
+                acc[0][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0][kb], B, acc[0][g], 0, 0, 0);
+                acc[1][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1][kb], B, acc[1][g], 0, 0, 0);
             }
         }
-        store_b(cur ^ 1u);  // after the last step this writes a buffer nobody reads
-        wc[0] = wn[0];
-        wc[1] = wn[1];
+    };
+
+    // Two K steps ahead: step ks issues the loads of step ks + 2 (B fragments first, then weights), multiplies step ks
+    // (weights loaded two steps earlier, B fragments stored in LDS at the end of the previous step) and stores the B
+    // fragments of step ks + 1 (loaded one step earlier). Three register sets rotate through the steps of a 3x
+    // unrolled loop, so no loaded register is ever copied (a copy would wait for its load). Every load is unconditional
+    // (indices clamp at the last step) and the steps past the slice's end only skip the multiply, so the compiler's
+    // waits stay exact.
+    u32x4g w0[2], w1[2], w2[2];
+    uint4 b00, b01, b02, b10, b11, b12, b20, b21, b22;
+    const uint32_t last = ks1 > ks0 ? ks1 - 1u : ks0;
+    VX_LOAD_B(ks0, b00, b01, b02);
+    load_w(ks0, w0);
+    VX_LOAD_B(min(ks0 + 1u, last), b10, b11, b12);
+    load_w(min(ks0 + 1u, last), w1);
+    VX_STORE_B(0, b00, b01, b02);
+#define VX_STEP(ks, WC, N0, N1, N2, M0, M1, M2, WN)                      \
+    do {                                                                 \
+        VX_LOAD_B(min((ks) + 2u, last), M0, M1, M2);                     \
+        load_w(min((ks) + 2u, last), WN);                                \
+        __syncthreads();                                                 \
+        if (active && (ks) < ks1) multiply((ks), WC, ((ks) - ks0) & 1u); \
+        VX_STORE_B((((ks) - ks0) & 1u) ^ 1u, N0, N1, N2);                \
+    } while (0)
+    for (uint32_t ks = ks0; ks < ks1; ks += 3u) {
+        VX_STEP(ks, w0, b10, b11, b12, b20, b21, b22, w2);
+        VX_STEP(ks + 1u, w1, b20, b21, b22, b00, b01, b02, w0);
+        VX_STEP(ks + 2u, w2, b00, b01, b02, b10, b11, b12, w1);
     }
+#undef VX_STEP
+#undef VX_LOAD_B
+#undef VX_STORE_B
     if (!active) return;
     // C of block (rb, g): lane l, register r -> weight row 8 (r / 4) + 4 (l / 32) + r % 4 of the block, token l % 32.
     const uint32_t j = lane & 31u;
