@@ -203,6 +203,57 @@ class Stream:
                 self.lib.check(self.L.vx_matrix_free(h))
 
 
+LONE_SHAPES = (("q/o", 3072, 3072), ("k/v", 1024, 3072), ("gate/up", 23040, 3072), ("down", 3072, 23040))
+
+
+def lone_latency(torch, L, lib, reps: int = 200):
+    """The drop-in path per call at the Falcon3-10B projection shapes: vx_gemv_f32_dev on device buffers (int8
+    activations staged by the call, one stream), as a back-to-back stream of `reps` calls (device time per call, HIP
+    events) and as single calls each followed by a stream synchronisation (wall-clock median: the latency a lone
+    caller sees); and vx_layer_forward, the TernaryGemvLayer::forward stand-in on host buffers (two synchronous PCIe
+    copies around the same call, wall-clock median)."""
+    import numpy as np
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x10E)
+    out = []
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for name, rows, cols in LONE_SHAPES:
+        planar = random_planar(torch, rows, cols, gen)
+        h = ctypes.c_void_p()
+        lib.check(L.vx_matrix_create_dev(ctypes.c_void_p(planar.data_ptr()), planar.numel(), rows, cols,
+                                         ctypes.c_float(0.02), ctypes.byref(h)))
+        del planar
+        q, sc = quantize_i8(torch, torch.randn(cols, device="cuda", generator=gen))
+        y = torch.empty(rows, dtype=torch.float32, device="cuda")
+        call = lambda: lib.check(L.vx_gemv_f32_dev(h, ctypes.c_void_p(q.data_ptr()), cols, ctypes.c_float(sc),  # noqa: E731
+                                                   ctypes.c_void_p(y.data_ptr()), rows, stream))
+        ms, _ = time_fn(torch, call, reps, 20)
+        lat = []
+        for _ in range(50):
+            t0 = time.perf_counter()
+            call()
+            torch.cuda.synchronize()
+            lat.append(time.perf_counter() - t0)
+        qh = q.cpu().numpy()
+        yh = np.empty(rows, np.float32)
+        fwd = []
+        for i in range(52):
+            t0 = time.perf_counter()
+            lib.check(L.vx_layer_forward(h, qh.ctypes.data_as(ctypes.c_void_p), cols, ctypes.c_float(sc),
+                                         yh.ctypes.data_as(ctypes.c_void_p), rows))
+            if i >= 2:
+                fwd.append(time.perf_counter() - t0)
+        if not np.array_equal(yh, y.cpu().numpy()):
+            raise RuntimeError(f"{name}: vx_layer_forward and vx_gemv_f32_dev differ")
+        out.append({"shape": name, "rows": rows, "cols": cols, "gemv_f32_dev_stream_us": round(ms * 1e3, 2),
+                    "gemv_f32_dev_sync_us": round(float(np.median(lat)) * 1e6, 1),
+                    "layer_forward_us": round(float(np.median(fwd)) * 1e6, 1)})
+        log(f"  lone {name} {rows}x{cols}: {ms * 1e3:.2f} us/call streamed, {np.median(lat) * 1e6:.1f} us with a sync, "
+            f"vx_layer_forward {np.median(fwd) * 1e6:.1f} us")
+        lib.check(L.vx_matrix_free(h))
+    return out
+
+
 def capture(torch, fn):
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
@@ -957,6 +1008,7 @@ def main():
                  "note": "one lone-GEMV call per projection (each waits for the previous), as a HIP graph"}
         log(f"  chain of {len(st.jobs())} lone GEMVs in a graph: {mc:.4f} ms/step, {chain['alg_GBps']} GB/s")
         del g
+        chain["lone_calls"] = lone_latency(torch, L, _lib)
 
     for o in st.outs:
         o.fill_(float("nan"))

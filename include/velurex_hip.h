@@ -168,7 +168,8 @@ int vx_gemv_f32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_l
  * column_activation_index(cols, c, p), p = 0..4, of quintrit-core/src/pack.rs:230-237) as two dwords of 4-bit fields:
  * the low nibbles stored as (x & 15) ^ 8, i.e. the signed value (x & 15) - 8, and the high nibbles x >> 4 (signed), so
  * that x = 16 hi + lo (lut.rs:380-388 splits the same way); activations past the end of the row and in padding columns
- * are zero. A 64-byte header holds the sum of all activations. vx_staged_bytes(cols) = 64 + 8 * device_row_bytes.
+ * are zero. A 64-byte header of 16 int32 adds up to the sum of all activations (one part per staging workgroup).
+ * vx_staged_bytes(cols) = 64 + 8 * device_row_bytes.
  * One staged vector serves every matrix with the same cols (Q, K and V share one input, gate and up another). The
  * reference stages its GPU inputs the same way, one permuted entry per byte-column (quintrit-cuda/src/pack.rs:75-85).
  */

@@ -187,7 +187,8 @@ static int check_io(const vx_matrix_t* m, const void* acts, size_t acts_len, con
     return VX_OK;
 }
 
-// A lone GEMV of matrix m on staged activations: one launch (plus the K-slice finish when the matrix is split).
+// A lone GEMV of matrix m on staged activations: one launch (plus the K-slice finish when the matrix is split). Calls
+// on one matrix share its partial sums, so they must not overlap.
 static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint32_t out_kind, float post,
                       hipStream_t s) {
     LaunchArgs a{};

@@ -46,10 +46,13 @@ typedef __attribute__((address_space(4))) const float c_float;
 
 // ---- activation staging -----------------------------------------------------------------------------------------------
 
-// One workgroup. Entry c (device byte-column c): dword 2c = the low nibbles of the five activations of the column,
-// stored as (x & 15) ^ 8 (the signed nibble (x & 15) - 8), dword 2c+1 = their high nibbles x >> 4 (signed);
-// activation p of column c is column_activation_index(cols, c, p) (pack.rs:230-237), zero past the end of the row and
-// in the padding columns. The header holds the sum of all activations.
+// Up to kStageGroups workgroups (grid-stride over the entries). Entry c (device byte-column c): dword 2c = the low
+// nibbles of the five activations of the column, stored as (x & 15) ^ 8 (the signed nibble (x & 15) - 8), dword 2c+1 =
+// their high nibbles x >> 4 (signed); activation p of column c is column_activation_index(cols, c, p)
+// (pack.rs:230-237), zero past the end of the row and in the padding columns. The 16 int32 of the header add up to the
+// sum of all activations: workgroup w writes the sum of its entries to word w, workgroup 0 zeroes the words past the
+// grid.
+constexpr uint32_t kStageGroups = 16;
 __global__ __launch_bounds__(1024) void stage_kernel(const int8_t* __restrict__ acts, uint32_t cols, uint32_t tbr,
                                                      uint32_t dbr, uint8_t* __restrict__ staged) {
     __shared__ int wsum[16];
@@ -57,7 +60,7 @@ __global__ __launch_bounds__(1024) void stage_kernel(const int8_t* __restrict__ 
     const uint32_t full = cols / 160u * 32u;
     uint2* ent = reinterpret_cast<uint2*>(staged + kStageHeader);
     int sum = 0;
-    for (uint32_t c = tid; c < dbr; c += 1024u) {
+    for (uint32_t c = blockIdx.x * 1024u + tid; c < dbr; c += gridDim.x * 1024u) {
         uint32_t lo = 0, hi = 0;
         for (uint32_t p = 0; p < 5; ++p) {
             const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
@@ -74,8 +77,9 @@ __global__ __launch_bounds__(1024) void stage_kernel(const int8_t* __restrict__ 
     if (tid < 16) {
         int s = wsum[tid];
         for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
-        if (tid == 0) reinterpret_cast<int*>(staged)[0] = s;
-        else reinterpret_cast<int*>(staged)[tid] = 0;
+        int* hdr = reinterpret_cast<int*>(staged);
+        if (tid == 0) hdr[blockIdx.x] = s;
+        else if (blockIdx.x == 0 && tid >= gridDim.x) hdr[tid] = 0;
     }
 }
 
@@ -177,7 +181,14 @@ __device__ __forceinline__ void store_out(const Job& jb, uint32_t row, int acc, 
     else __builtin_nontemporal_store(out_value(jb, acc, post, zero), static_cast<float*>(jb.out) + row);
 }
 
-__device__ __forceinline__ int staged_sum(const Job& jb) { return *(const c_int*)(jb.staged); }
+// The sum of all activations: the 16 words of the staged header.
+__device__ __forceinline__ int staged_sum(const Job& jb) {
+    const c_int* h = (const c_int*)(jb.staged);
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += h[i];
+    return s;
+}
 
 // The integer result of row `row` from the two dot-product accumulators summed over all K slices: lo holds
 // sum d (l - 8) with l = x & 15, hi holds sum d (x >> 4), so sum t x = 16 hi + lo + 8 sum d - sum x.
@@ -393,7 +404,8 @@ void plan_job(Job& j, const Geometry& g, uint32_t target_items) {
 }
 
 int launch_stage(const int8_t* acts, size_t cols, uint8_t* staged, hipStream_t stream) {
-    hipLaunchKernelGGL(stage_kernel, dim3(1), dim3(1024), 0, stream, acts, static_cast<uint32_t>(cols),
+    const uint32_t groups = static_cast<uint32_t>(std::min<size_t>(kStageGroups, (device_row_bytes(cols) + 1023) / 1024));
+    hipLaunchKernelGGL(stage_kernel, dim3(std::max(groups, 1u)), dim3(1024), 0, stream, acts, static_cast<uint32_t>(cols),
                        static_cast<uint32_t>(tile_row_bytes(cols)), static_cast<uint32_t>(device_row_bytes(cols)), staged);
     VX_HIP(hipGetLastError());
     return VX_OK;
