@@ -67,6 +67,7 @@ static int set_device_of(const vx_matrix_t* m) {
 static void destroy(vx_matrix* m) {
     if (m->d_w) (void)hipFree(m->d_w);
     if (m->d_part) (void)hipFree(m->d_part);
+    if (m->d_accum) (void)hipFree(m->d_accum);
     if (m->d_dsum) (void)hipFree(m->d_dsum);
     if (m->d_staged) (void)hipFree(m->d_staged);
     if (m->d_io) (void)hipFree(m->d_io);
@@ -96,6 +97,8 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     m->num_cus = di.num_cus;
     m->d_w = nullptr;
     m->d_part = nullptr;
+    m->d_accum = nullptr;
+    m->d_tickets = nullptr;
     m->d_dsum = nullptr;
     m->d_staged = nullptr;
     m->d_io = nullptr;
@@ -108,6 +111,9 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     const size_t io_bytes = round_up(cols, 256) + m->g.padded_rows * 4;
     hipError_t e = hipMalloc(&m->d_w, m->g.device_bytes);
     if (e == hipSuccess && m->kslices > 1) e = hipMalloc(&m->d_part, static_cast<size_t>(m->kslices) * m->g.padded_rows * 4);
+    if (e == hipSuccess && m->kslices > 1) e = hipMalloc(&m->d_accum, m->g.padded_rows * 4 + m->g.n_groups * 4);
+    if (e == hipSuccess && m->kslices > 1) e = hipMemset(m->d_accum, 0, m->g.padded_rows * 4 + m->g.n_groups * 4);
+    if (e == hipSuccess && m->kslices > 1) m->d_tickets = reinterpret_cast<uint32_t*>(m->d_accum + m->g.padded_rows);
     if (e == hipSuccess) e = hipMalloc(&m->d_dsum, m->g.padded_rows * 4);
     if (e == hipSuccess) e = hipMalloc(&m->d_staged, staged_bytes(cols));
     if (e == hipSuccess) e = hipMalloc(&m->d_io, io_bytes);
@@ -187,8 +193,9 @@ static int check_io(const vx_matrix_t* m, const void* acts, size_t acts_len, con
     return VX_OK;
 }
 
-// A lone GEMV of matrix m on staged activations: one launch (plus the K-slice finish when the matrix is split). Calls
-// on one matrix share its partial sums, so they must not overlap.
+// A lone GEMV of matrix m on staged activations: one launch (a split matrix's K slices add their sums atomically and
+// the last of each tile group writes the outputs). Calls on one matrix share its sums and tickets, so they must not
+// overlap.
 static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint32_t out_kind, float post,
                       hipStream_t s) {
     LaunchArgs a{};
@@ -199,6 +206,8 @@ static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint
     j.w = m->d_w;
     j.staged = staged;
     j.part = m->d_part;
+    j.accum = m->d_accum;
+    j.tickets = m->d_tickets;
     j.dsum = m->d_dsum;
     j.out = out;
     j.act_scale = nullptr;
@@ -207,7 +216,7 @@ static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint
     j.out_kind = out_kind;
     j.item_begin = 0;
     a.total_items = job_items(j);
-    return launch_gemv(a, j.rows, nullptr, j.kslices > 1 ? 1u : 0u, m->num_cus, s);
+    return launch_gemv(a, j.rows, nullptr, j.kslices > 1 && j.accum == nullptr ? 1u : 0u, m->num_cus, s);
 }
 
 // out = float(acc) * (ws / as) with the division done once here, as the layers do; zeros when as <= 0 or NaN

@@ -243,6 +243,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
     __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of entry B, then 128 bytes of held results
     __shared__ uint4 acts[2][(kMaxSliceChunks + kGroup) * 8];
     __shared__ Held held[kSlots];
+    __shared__ uint32_t last_slice;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
@@ -252,7 +253,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
     const c_job* cj = (const c_job*)(args.jobs);
 
     uint32_t j = 0, buf = 0;
-    uint32_t done = 0, pending = 0;  // items this workgroup has finished / of those, held in LDS
+    uint32_t done = 0, pending = 0;  // held items this workgroup has finished / of those, still in LDS
+    bool built = false;              // the digit table is in LDS
     for (uint32_t item = blockIdx.x; item < args.total_items; item += gridDim.x, buf ^= 1u) {
         if (MANY)
             while (j + 1 < args.n_jobs && item >= cj[j + 1].item_begin) ++j;
@@ -277,7 +279,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
 #pragma unroll
             for (int i = 0; i < kGroup; ++i) b[i] = __builtin_nontemporal_load(wp + min(static_cast<uint32_t>(i), nq - 1u) * cs);
         }
-        if (done == 0) {
+        if (!built) {
+            built = true;
             for (uint32_t i = tid; i < 256u * 8u; i += kWaves * 64u) {  // 8 uint4 stores per entry
                 const uint32_t e = digit_nibbles(i >> 3);
                 *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
@@ -287,8 +290,10 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
         const uint4* src = reinterpret_cast<const uint4*>(jb.staged + kStageHeader) + static_cast<size_t>(q0) * 8u;
         uint4* ab = acts[buf];
         for (uint32_t i = tid; i < nqp * 8u; i += kWaves * 64u) ab[i] = i < nq * 8u ? src[i] : make_uint4(0, 0, 0, 0);
+        // A lone GEMV's split item adds its sums atomically; the last slice of the tile group writes the outputs.
+        const bool fold = !MANY && jb.kslices > 1 && jb.accum != nullptr;
         const uint32_t slot = done % kSlots;
-        if (tid == 0) {
+        if (tid == 0 && !fold) {
             const size_t first = static_cast<size_t>(grp) * kTileGroup * kTileRows;
             Held h;
             if (jb.kslices == 1) {
@@ -337,6 +342,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
             const int v = acc_lo + 16 * acc_hi;
             const uint32_t r = wave * kTileRows + lane;  // row within the tile group
             const uint32_t row = grp * kTileGroup * kTileRows + r;
+            if (fold) atomicAdd(jb.accum + row, v);
             uint32_t word = static_cast<uint32_t>(v);
             if (jb.kslices == 1 && row < jb.rows) {
                 const int acc = row_result(jb, row, v);
@@ -348,10 +354,31 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
                     word = __float_as_uint(out_value(jb, acc, post, zero));
                 }
             }
-            *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(tab) + held_offset(slot, r)) = word;
+            if (!fold) *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(tab) + held_offset(slot, r)) = word;
         }
-        ++done;
-        ++pending;
+        if (!fold) {
+            ++done;
+            ++pending;
+            continue;
+        }
+        // The sums are complete at the atomics' coherence point before the ticket is taken (every memory operation of
+        // the wave waited for), and the last slice reads them with atomics after its ticket: no cache writeback.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) last_slice = atomicAdd(jb.tickets + grp, 1u) == jb.kslices - 1u ? 1u : 0u;
+        __syncthreads();
+        if (last_slice != 0u) {
+            const uint32_t row = grp * kTileGroup * kTileRows + wave * kTileRows + lane;
+            if (active) {
+                const int total = atomicExch(jb.accum + row, 0);
+                if (row < jb.rows) {
+                    bool zero;
+                    const float post = job_post(jb, &zero);
+                    store_out(jb, row, row_result(jb, row, total), post, zero);
+                }
+            }
+            if (tid == 0) atomicExch(jb.tickets + grp, 0u);
+        }
     }
     __syncthreads();
     flush_held(tabb, held, done, pending, wave, lane);

@@ -134,6 +134,11 @@ struct Job {
     uint32_t kslices, slice_chunks;  // K split: slices of slice_chunks chunks (the last may be shorter)
     uint32_t item_begin;             // first work item of this job in the launch
     uint32_t pad;
+    // A lone GEMV's K-slice sums by atomic addition: accum[padded_rows] and tickets[tile groups], both zero between
+    // calls; the last slice of a tile group to arrive takes (and clears) the sums and writes the outputs, so no finish
+    // kernel runs. Null in a plan.
+    int32_t* accum;
+    uint32_t* tickets;
 };
 
 struct LaunchArgs {
@@ -228,6 +233,8 @@ struct vx_matrix {
     uint32_t kslices, slice_chunks;  // K split of a lone GEMV on this matrix
     uint8_t* d_w;       // weights, device layout (vx_layout)
     int32_t* d_part;    // K-slice partial sums of a lone GEMV
+    int32_t* d_accum;   // a lone GEMV's atomic K-slice sums (padded_rows) and tickets (one per tile group), zero
+    uint32_t* d_tickets;  // between calls
     int32_t* d_dsum;    // per padded row: digit sum of the device row (the signed low-nibble correction)
     uint8_t* d_staged;  // activation staging of the calls that take raw int8 activations
     int8_t* d_io;       // host-API staging: cols bytes of activations + padded_rows * 4 bytes of output
