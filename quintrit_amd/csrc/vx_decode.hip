@@ -818,10 +818,10 @@ struct AttnArgs {
     // qbuf[token][n_heads * head_dim] and their k, v already in the cache; out is [token][n_heads * head_dim]
     const uint16_t* qbuf;
     uint32_t n_tok;
-    // decode in two kernels: the scores [n_heads][max_ctx], then per chunk its f16 accumulators cy [n_heads][4][HD],
-    // its (max, sum) pairs cms [n_heads][slices][4][2] and a ticket per (head, slice) (0 between steps)
+    // decode in two kernels: the scores [n_heads][max_ctx], then per chunk its f16 accumulators cy [n_heads][4][HD]
+    // (one per word), its (max, sum) pairs cms [n_heads][slices][4][2] and a ticket per (head, slice) (0 between steps)
     float* scores;
-    uint16_t* cy;
+    uint32_t* cy;
     float* cms;
     uint32_t* ticket;
 };
@@ -1528,22 +1528,25 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
         }
         return;
     }
-    // four chunks: this chunk's part, then the ticket of (h, sl); the fourth to arrive combines in chunk order
-    uint16_t* cy = a.cy + static_cast<size_t>(h) * 4u * HD;
+    // four chunks: this chunk's part, then the ticket of (h, sl); the fourth to arrive combines in chunk order. The
+    // parts are written and read with agent-scope atomic stores and loads (coherent across the L2 caches without a
+    // cache writeback), every store complete before the ticket is taken.
+    uint32_t* cy = a.cy + static_cast<size_t>(h) * 4u * HD;
     float* cms = a.cms + (static_cast<size_t>(h) * kSlices + sl) * 8u;
     if (wave == 0) {
-        if (lane < kLanes) cy[c * HD + sl * 64u + lane] = f32_f16(y);
+        if (lane < kLanes)
+            __hip_atomic_store(cy + c * HD + sl * 64u + lane, static_cast<uint32_t>(f32_f16(y)), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         if (lane == 0) {
-            cms[2u * c] = any ? cmax : -__builtin_inff();
-            cms[2u * c + 1u] = ssum;
+            __hip_atomic_store(cms + 2u * c, any ? cmax : -__builtin_inff(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(cms + 2u * c + 1u, ssum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        __threadfence();
+        __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
     if (tid == 0) s_last = atomicAdd(a.ticket + blockIdx.x, 1u) == 3u ? 1u : 0u;
     __syncthreads();
     if (s_last == 0u || wave != 0) return;
-    __threadfence();
     if (lane == 0) atomicExch(a.ticket + blockIdx.x, 0u);
     if (lane >= kLanes) return;
     const uint32_t dd = sl * 64u + lane;
@@ -1551,13 +1554,14 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
     for (uint32_t k = 0; k < 4; ++k) {
         const uint32_t ks = k * chunk, ke = min(min(ks + chunk, n_kv), seq);
         if (ks >= ke) continue;
-        const float sk = __builtin_nontemporal_load(cms + 2u * k + 1u);
+        const float sk = __hip_atomic_load(cms + 2u * k + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (sk == 0.0f) continue;
-        const float mk = __builtin_nontemporal_load(cms + 2u * k);
+        const float mk = __hip_atomic_load(cms + 2u * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const float mn = __builtin_fmaxf(mf, mk);
         const float so = glibc_expf(mf - mn);
         const float sn = glibc_expf(mk - mn);
-        const float vn = f16_f32(__builtin_nontemporal_load(cy + k * HD + dd)) * sn;
+        const uint32_t yk = __hip_atomic_load(cy + k * HD + dd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float vn = f16_f32(static_cast<uint16_t>(yk)) * sn;
         acc = __builtin_fmaf(acc, so, vn);
         const float ssn = sk * sn;
         sf = __builtin_fmaf(sf, so, ssn);
@@ -1771,7 +1775,7 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
     for (int w = 1; w < kNT / 64; ++w)
         if (wbest[w] > best) best = wbest[w];
     atomicMax(a.key, best);
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0);  // the maximum is in place (at the atomics' coherence point) before the ticket
     if (atomicAdd(a.ticket, 1u) != gridDim.x - 1u) return;
     const unsigned long long k = atomicExch(a.key, 0ull);
     atomicExch(a.ticket, 0u);
@@ -2102,7 +2106,7 @@ struct vx_decoder {
     float* d_as;                      // activation scale of each projection stage, reused by every layer
     float *d_att, *d_logits;
     float* d_scores;                  // decode attention: scores [n_heads][max_ctx]
-    uint16_t* d_cy;                   // per chunk f16 accumulators [n_heads][4][head_dim]
+    uint32_t* d_cy;                   // per chunk f16 accumulators [n_heads][4][head_dim], one per word
     float* d_cms;                     // per chunk (max, sum) [n_heads][slices][4][2]
     uint32_t* d_aticket;              // chunks done per (head, slice) (0 between steps)
     unsigned long long* d_key;        // argmax key and ticket of the head kernel
@@ -2333,7 +2337,7 @@ static int create_decoder(const vx_decoder_config_t* cin, vx_decoder_t** out) {
     if (e == hipSuccess) e = dalloc(d, &d->d_logits, static_cast<size_t>(c->vocab) * 4);
     const size_t n_sl = static_cast<size_t>(c->n_heads) * attn_slices(c->head_dim);
     if (e == hipSuccess) e = dalloc(d, &d->d_scores, static_cast<size_t>(c->n_heads) * c->max_ctx * 4);
-    if (e == hipSuccess) e = dalloc(d, &d->d_cy, d->qd * 4 * 2);
+    if (e == hipSuccess) e = dalloc(d, &d->d_cy, d->qd * 4 * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_cms, n_sl * 8 * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_aticket, n_sl * 4);
     if (e == hipSuccess) e = hipMemset(d->d_aticket, 0, n_sl * 4);
