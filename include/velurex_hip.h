@@ -151,7 +151,9 @@ int vx_matrix_device_weights(const vx_matrix_t* matrix, const void** out_ptr);
 /*
  * Integer GEMV on device memory: out[i] = sum_j W[i][j] * acts[j] for i < rows, exact for the whole int8 range.
  * acts_len >= cols, out_capacity >= rows. Enqueued on `stream`. Device counterpart of quintrit_gemv_i32
- * (quintrit.h:208-210).
+ * (quintrit.h:208-210). The device calls on one matrix (this, vx_gemv_f32_dev and the staged forms) share its staging
+ * buffer and K-slice sums: calls on one matrix on different streams must be ordered by the caller (vx_layer_forward
+ * takes the matrix's lock itself).
  */
 int vx_gemv_i32_dev(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, int32_t* out, size_t out_capacity,
                     void* stream);
