@@ -1,3 +1,4 @@
+#define _GNU_SOURCE
 /*
  * cpu_avx512.c - the reference's production CPU GEMV, transcribed with AVX-512 intrinsics (CPU BASELINE ONLY).
  *
@@ -21,6 +22,8 @@
 
 #include <immintrin.h>
 #include <omp.h>
+#include <pthread.h>
+#include <sched.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -194,10 +197,90 @@ void vxc_gemv(const uint8_t* tiles64, const int8_t* acts, size_t rows, size_t co
     vxc_gemv_tables(tiles64, table_scratch, rows, cols, out, threads);
 }
 
-/* Host read bandwidth: `threads` threads each sum their share of `bytes` (64-bit words); returns the sum. */
+/* The engine runs the projections that share an input concurrently on one pool after one table build
+ * (forward_linear_triple / forward_linear_pair, quintrit-runtime/src/layer.rs:657-716, the tables built once before
+ * them, attention.rs:138-163); here the blocks of the whole group are split evenly over the threads. */
+void vxc_gemv_group(const uint8_t* const* tiles64, const size_t* rows, int n, const int8_t* acts, size_t cols,
+                    float* const* outs, int threads, int8_t* table_scratch) {
+    vxc_build_tables(acts, cols, table_scratch);
+    const size_t bpr = vxo_tile_row_bytes(cols);
+    size_t total = 0;
+    for (int m = 0; m < n; ++m) total += rows[m] / 64;
+    if (threads < 1) threads = 1;
+    const size_t per = (total + (size_t)threads - 1) / (size_t)threads;
+#pragma omp parallel num_threads(threads)
+    {
+        const size_t g0 = (size_t)omp_get_thread_num() * per, g1 = g0 + per < total ? g0 + per : total;
+        size_t base = 0; /* first global block of matrix m */
+        for (int m = 0; m < n && g0 < g1; ++m) {
+            const size_t nb = rows[m] / 64, lo = g0 > base ? g0 - base : 0, hi = g1 - base < nb ? g1 - base : nb;
+            if (g1 > base && lo < nb && lo < hi)
+                gemv_blocks(tiles64[m] + lo * 64 * bpr, table_scratch, hi - lo, bpr, outs[m] + lo * 64);
+            base += nb;
+        }
+    }
+}
+
+/* Fills out[0..n) with pseudo-random valid packed bytes (splitmix64 per 4 bytes, each 16-bit piece mapped onto the 243
+ * valid values by multiply-shift), in parallel: the CPU baseline's 1.9 GB of random weights in well under a second. */
+void vxc_fill_valid(uint8_t* out, size_t n, uint64_t seed) {
+    uint8_t valid[243];
+    int k = 0;
+    for (int b = 0; b < 256; ++b)
+        if (vxo_byte_is_valid((uint8_t)b)) valid[k++] = (uint8_t)b;
+#pragma omp parallel for schedule(static)
+    for (size_t w = 0; w < (n + 3) / 4; ++w) {
+        uint64_t z = seed + (w + 1) * 0x9E3779B97F4A7C15ull;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        for (size_t j = 0; j < 4 && w * 4 + j < n; ++j) out[w * 4 + j] = valid[(((z >> (16 * j)) & 0xFFFF) * 243) >> 16];
+    }
+}
+
+/* Pins OpenMP thread t of a team of n to logical CPU cpus[t] (the team the GEMV and read-stream calls with n threads
+ * reuse); returns the number of threads that could not be pinned. */
+int vxc_pin_threads(const int* cpus, int n) {
+    int failed = 0;
+#pragma omp parallel num_threads(n) reduction(+ : failed)
+    {
+        cpu_set_t set;
+        CPU_ZERO(&set);
+        CPU_SET(cpus[omp_get_thread_num()], &set);
+        failed += pthread_setaffinity_np(pthread_self(), sizeof set, &set) != 0;
+    }
+    return failed;
+}
+
+/* Sums words [w0, w1) of buf with 64-byte loads into four independent accumulators (the loop is bound by the loads,
+ * not by the adds' latency), prefetching 4 KiB ahead like the GEMV. */
+VXC_TARGET static uint64_t read_range(const uint64_t* buf, size_t w0, size_t w1) {
+    __m512i s0 = _mm512_setzero_si512(), s1 = s0, s2 = s0, s3 = s0;
+    size_t i = w0;
+    for (; i + 32 <= w1; i += 32) {
+        _mm_prefetch((const char*)(buf + i) + 4096, _MM_HINT_T0);
+        _mm_prefetch((const char*)(buf + i) + 4160, _MM_HINT_T0);
+        _mm_prefetch((const char*)(buf + i) + 4224, _MM_HINT_T0);
+        _mm_prefetch((const char*)(buf + i) + 4288, _MM_HINT_T0);
+        s0 = _mm512_add_epi64(s0, _mm512_loadu_si512(buf + i));
+        s1 = _mm512_add_epi64(s1, _mm512_loadu_si512(buf + i + 8));
+        s2 = _mm512_add_epi64(s2, _mm512_loadu_si512(buf + i + 16));
+        s3 = _mm512_add_epi64(s3, _mm512_loadu_si512(buf + i + 24));
+    }
+    uint64_t total = (uint64_t)_mm512_reduce_add_epi64(
+        _mm512_add_epi64(_mm512_add_epi64(s0, s1), _mm512_add_epi64(s2, s3)));
+    for (; i < w1; ++i) total += buf[i];
+    return total;
+}
+
+/* Host read bandwidth: `threads` threads each sum one contiguous share of `words` 64-bit words; returns the sum. */
 uint64_t vxc_read_stream(const uint64_t* buf, size_t words, int threads) {
     uint64_t total = 0;
-#pragma omp parallel for num_threads(threads) schedule(static) reduction(+ : total)
-    for (size_t i = 0; i < words; ++i) total += buf[i];
+#pragma omp parallel num_threads(threads) reduction(+ : total)
+    {
+        const size_t t = (size_t)omp_get_thread_num(), n = (size_t)omp_get_num_threads();
+        const size_t per = (words + n - 1) / n, w0 = t * per < words ? t * per : words;
+        total += read_range(buf, w0, w0 + per < words ? w0 + per : words);
+    }
     return total;
 }

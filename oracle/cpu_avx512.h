@@ -21,6 +21,14 @@ void vxc_gemv_tables(const uint8_t* tiles64, const int8_t* tables, size_t rows, 
 /* Tables then kernel (one call of the reference's GEMV); table_scratch holds vxc_table_bytes(cols). */
 void vxc_gemv(const uint8_t* tiles64, const int8_t* acts, size_t rows, size_t cols, float* out, int threads,
               int8_t* table_scratch);
+/* A projection group of the inference engine: n matrices with the same input (q/k/v, gate/up, or one alone), the
+ * tables built once, then every 64-row block of the group shared out over `threads` threads. */
+void vxc_gemv_group(const uint8_t* const* tiles64, const size_t* rows, int n, const int8_t* acts, size_t cols,
+                    float* const* outs, int threads, int8_t* table_scratch);
+/* out[0..n) = pseudo-random valid packed bytes from `seed` (random weights for the timing). */
+void vxc_fill_valid(uint8_t* out, size_t n, uint64_t seed);
+/* Pins OpenMP thread t of a team of n to logical CPU cpus[t]; returns the threads that could not be pinned. */
+int vxc_pin_threads(const int* cpus, int n);
 uint64_t vxc_read_stream(const uint64_t* buf, size_t words, int threads);
 
 #ifdef __cplusplus

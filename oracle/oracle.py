@@ -115,7 +115,10 @@ def _declare(L: ctypes.CDLL) -> None:
         "vxc_build_tables": (None, [vp, sz, vp]),
         "vxc_gemv_tables": (None, [vp, vp, sz, sz, vp, ctypes.c_int]),
         "vxc_gemv": (None, [vp, vp, sz, sz, vp, ctypes.c_int, vp]),
+        "vxc_gemv_group": (None, [vp, vp, ctypes.c_int, vp, sz, vp, ctypes.c_int, vp]),
+        "vxc_fill_valid": (None, [vp, sz, ctypes.c_uint64]),
         "vxc_read_stream": (u64, [vp, sz, ctypes.c_int]),
+        "vxc_pin_threads": (ctypes.c_int, [vp, ctypes.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -552,6 +555,24 @@ def gemv_avx512(tiles64_: np.ndarray, acts: np.ndarray, rows: int, cols: int, th
     scratch = np.empty(int(lib().vxc_table_bytes(cols)), np.int8)
     lib().vxc_gemv(_p(t), _p(a), rows, cols, _p(out), threads, _p(scratch))
     return out
+
+
+def gemv_group_avx512(tiles: list, rows: list, acts: np.ndarray, cols: int, threads: int = 1) -> list:
+    """One projection group (matrices sharing the input acts) by the AVX-512 kernel: one table build, the group's
+    blocks split over `threads` threads; returns one float32 vector per matrix."""
+    if not cpu_avx512_supported():
+        raise RuntimeError("this host has no AVX-512 F/BW/VBMI")
+    ts = [np.ascontiguousarray(t, dtype=np.uint8) for t in tiles]
+    a = np.ascontiguousarray(acts, dtype=np.int8)
+    outs = [np.empty(r, np.float32) for r in rows]
+    n = len(ts)
+    tp = (ctypes.c_void_p * n)(*[t.ctypes.data for t in ts])
+    op = (ctypes.c_void_p * n)(*[o.ctypes.data for o in outs])
+    rp = (ctypes.c_size_t * n)(*rows)
+    scratch = np.empty(int(lib().vxc_table_bytes(cols)), np.int8)
+    lib().vxc_gemv_group(ctypes.cast(tp, ctypes.c_void_p), ctypes.cast(rp, ctypes.c_void_p), n, _p(a), cols,
+                         ctypes.cast(op, ctypes.c_void_p), threads, _p(scratch))
+    return outs
 
 
 # ---- GGUF ternary decoders (gguf_oracle.c) -------------------------------------------------------------------------

@@ -25,6 +25,23 @@ def test_equals_bruteforce(avx, rows, cols, threads):
     np.testing.assert_array_equal(got.astype(np.int64), o.gemv_bruteforce(t, a))
 
 
+@pytest.mark.parametrize("rows", [(192, 64, 64), (320, 128), (64,), (64, 64, 64, 64, 64)])
+@pytest.mark.parametrize("threads", [1, 2, 3, 7])
+def test_group_equals_bruteforce(avx, rows, threads):
+    """The engine's projection group (one table build, the blocks of all matrices shared out over the threads, as
+    forward_linear_triple / forward_linear_pair run them): every matrix equals its brute-force product, whichever
+    thread's share crosses which matrix boundary."""
+    o = avx
+    cols = 3072
+    rng = np.random.default_rng(sum(rows) + threads)
+    a = o.gen_i8(int(rng.integers(1 << 30)), cols, -128, 127)
+    ts = [o.gen_trits(int(rng.integers(1 << 30)), (r, cols)) for r in rows]
+    got = o.gemv_group_avx512([o.tile64(o.pack_matrix(t), r, cols) for t, r in zip(ts, rows)], list(rows), a, cols,
+                              threads)
+    for g, t in zip(got, ts):
+        np.testing.assert_array_equal(g.astype(np.int64), o.gemv_bruteforce(t, a))
+
+
 @pytest.mark.parametrize("w,x", [(1, 127), (-1, 127), (1, -128), (-1, -128), (0, -128)])
 def test_extreme_magnitudes(avx, w, x):
     """All weights one trit, all activations one extreme value: the int8 and int16 partial sums must not wrap."""
