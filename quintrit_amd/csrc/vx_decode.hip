@@ -576,6 +576,10 @@ struct DJob {
     uint32_t* amax_out;    // gated pair: atomic maximum of |act_out| as float bits (a plain unnormed consumer), or null
     uint32_t rows, padded_rows, n_tiles, n_chunks, kslices, slice_chunks, item_begin;
     uint32_t w_bytes;      // bytes of w (and w2) in the device layout, below kBufferOutOfRange
+    // gated pair split into chunk ranges: per tile the gate and up sums of 64 rows added atomically ([tile][2][64],
+    // zero between launches) and the count of workgroups that have added theirs (zero between launches)
+    int32_t* accum;
+    uint32_t* tickets;
 };
 
 constexpr int kMaxStageJobs = 3;
@@ -585,6 +589,10 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 constexpr uint32_t kBufferOutOfRange = 0x80000000u;
 constexpr int kLoadNt = 2;
 constexpr int kDPer = 7;  // chunks of a work item per wave at most (kStChunks / 16)
+// Tiles a workgroup's chunk range of a gated pair touches at most: a range of at most 16 kDPer chunks starting inside a
+// tile of 2 n_chunks chunks, with 2 n_chunks >= 8 kDPer (the host's condition), ends within the third tile.
+constexpr int kRangeSegs = 3;
+constexpr int kRangeEarly = 3;  // chunks per wave of a range issued before the stage input is computed
 
 struct DStageArgs {
     DJob job[kMaxStageJobs];
@@ -597,6 +605,9 @@ struct DStageArgs {
     uint32_t grid;      // workgroups of the launch
     uint32_t* amax_clear;  // zeroed by the stage (the StageInput::amax a later stage of the layer accumulates), or null
     uint32_t dper;         // chunk loads per wave and item of the kernel instance (1, 4 or 7): at least any wave's count
+    // A gated pair split into equal chunk ranges (0: split into items): the pair's chunks listed tile by tile, the gate
+    // chunks of a tile before its up chunks, range_chunks of them in all; workgroup w takes [w C / G, (w + 1) C / G).
+    uint32_t range_chunks;
 };
 
 __constant__ DigitTable g_digits = make_digit_table();
@@ -608,12 +619,13 @@ __constant__ DigitTable g_digits = make_digit_table();
 // chunk loads per item (buffer loads; a chunk the wave does not have reads past the buffer's end, which returns zeros
 // without a memory access), so each chunk is waited for on its own. The digit-nibble table and the arithmetic are those
 // of the lone GEMV (vx_gemv.hip). Only the entries of the item's own chunks are staged.
-template <int P4, int SA, int SB, bool MULTI, int DPER>
+template <int P4, int SA, int SB, bool MULTI, int DPER, bool RANGE = false>
 __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
+    static_assert(!RANGE || (MULTI && DPER == kDPer), "the chunk-range split runs on the gated-pair instance");
     __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of the digit nibbles of byte B (first half)
     __shared__ uint2 st[kStChunks * 16];
     __shared__ InputLds s;
-    __shared__ int red[MULTI ? 2 : 1][MULTI ? 2 : 1][kNT / 64][64];  // [item][gate, up][wave][lane]
+    __shared__ int red[MULTI ? kRangeSegs : 1][MULTI ? 2 : 1][kNT / 64][64];  // [item or tile][gate, up][wave][lane]
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -627,22 +639,49 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
         uint32_t off;  // the lane's 16 bytes of chunk 0 of the tile
         uint32_t cs;   // bytes between chunks q and q + 1 of the tile
     };
+    // Every kernel argument that the stage input's loads depend on (the job geometry that places the K slice, the
+    // input's kind, length and pointers) is read in one batch and held in registers: read where used, each would be a
+    // scalar load waited for on its own before the next, a chain of memory latencies before the first input load.
+    StageInput in = a.in;
+    uint32_t jib[kMaxStageJobs], jks[kMaxStageJobs], jsc[kMaxStageJobs], jnc[kMaxStageJobs], jnt[kMaxStageJobs];
+    bool jpair[kMaxStageJobs];
+#pragma unroll
+    for (int k = 0; k < kMaxStageJobs; ++k) {
+        jib[k] = a.job[k].item_begin;
+        jks[k] = a.job[k].kslices;
+        jsc[k] = a.job[k].slice_chunks;
+        jnc[k] = a.job[k].n_chunks;
+        jnt[k] = a.job[k].n_tiles;
+        jpair[k] = a.job[k].w2 != nullptr;
+    }
+    const uint32_t n_jobs = a.n_jobs, tbr = a.tbr;
+    asm volatile("" : : "s"(n_jobs), "s"(tbr), "s"(jib[1]), "s"(jib[2]), "s"(jks[0]), "s"(jks[1]), "s"(jks[2]),
+                 "s"(jsc[0]), "s"(jsc[1]), "s"(jsc[2]), "s"(jnc[0]), "s"(jnc[1]), "s"(jnc[2]), "s"(jnt[0]), "s"(jnt[1]),
+                 "s"(jnt[2]), "s"(in.kind), "s"(in.n), "s"(in.x_in), "s"(in.amax), "s"(in.a.part), "s"(in.a.as),
+                 "s"(in.a.kslices), "s"(in.a.stride), "s"(in.b.part), "s"(in.b.as), "s"(in.b.kslices), "s"(in.b.stride),
+                 "s"(in.gamma), "s"(in.ctl), "s"(in.token_at));
     auto locate = [&](uint32_t item) {
         Item it;
         uint32_t j = 0;
-        if (a.n_jobs > 1 && item >= a.job[1].item_begin) j = 1;
-        if (a.n_jobs > 2 && item >= a.job[2].item_begin) j = 2;
+        if (n_jobs > 1 && item >= jib[1]) j = 1;
+        if (n_jobs > 2 && item >= jib[2]) j = 2;
+        const uint32_t ib = j == 0 ? 0u : (j == 1 ? jib[1] : jib[2]);
+        const uint32_t ks = j == 0 ? jks[0] : (j == 1 ? jks[1] : jks[2]);
+        const uint32_t sc = j == 0 ? jsc[0] : (j == 1 ? jsc[1] : jsc[2]);
+        const uint32_t ncj = j == 0 ? jnc[0] : (j == 1 ? jnc[1] : jnc[2]);
+        const uint32_t ntj = j == 0 ? jnt[0] : (j == 1 ? jnt[1] : jnt[2]);
+        const bool pr = j == 0 ? jpair[0] : (j == 1 ? jpair[1] : jpair[2]);
         it.jb = j == 0 ? a.job[0] : (j == 1 ? a.job[1] : a.job[2]);
-        const uint32_t local = item - it.jb.item_begin;
-        it.tile = local / it.jb.kslices;
-        it.ks = local - it.tile * it.jb.kslices;
+        const uint32_t local = item - ib;
+        it.tile = local / ks;
+        it.ks = local - it.tile * ks;
         const uint32_t grp = it.tile / kTileGroup, tt = it.tile - grp * kTileGroup;
-        const uint32_t T = min(static_cast<uint32_t>(kTileGroup), it.jb.n_tiles - grp * kTileGroup);
-        it.q0 = it.ks * it.jb.slice_chunks;
-        it.nq = min(it.jb.slice_chunks, it.jb.n_chunks - it.q0);
-        const uint32_t nl = MULTI && it.jb.w2 != nullptr ? 2u * it.nq : it.nq;  // gate chunks, then (pair) up chunks
+        const uint32_t T = min(static_cast<uint32_t>(kTileGroup), ntj - grp * kTileGroup);
+        it.q0 = it.ks * sc;
+        it.nq = min(sc, ncj - it.q0);
+        const uint32_t nl = MULTI && pr ? 2u * it.nq : it.nq;  // gate chunks, then (pair) up chunks
         it.cnt = wave < nl ? (nl - wave + kTileGroup - 1) / kTileGroup : 0u;
-        it.off = ((grp * kTileGroup * it.jb.n_chunks + tt) * 64u + lane) * 16u;
+        it.off = ((grp * kTileGroup * ncj + tt) * 64u + lane) * 16u;
         it.cs = T * 1024u;
         return it;
     };
@@ -660,11 +699,11 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
 
     const Item ia = locate(blockIdx.x);
     // The staged slice: both items of a workgroup have the same K slice (a looping stage's jobs have one slice each).
-    const uint32_t c0 = ia.q0 * 16u, c1 = min((ia.q0 + ia.nq) * 16u, a.tbr);
+    const uint32_t c0 = ia.q0 * 16u, c1 = min((ia.q0 + ia.nq) * 16u, tbr);
     uint32_t lo, hi;
-    slice_window(a.in.n, c0, c1, &lo, &hi);
+    slice_window(in.n, c0, c1, &lo, &hi);
     InputRegs<P4, SA, SB> r;
-    stage_load(a.in, r, lo, hi);
+    stage_load(in, r, lo, hi);
     uint32_t dig[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) dig[k] = g_digits.v[(tid + k * kNT) >> 3];
@@ -672,9 +711,60 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     // The weight loads go out once the input and the digit table have arrived (the waits for the input would otherwise
     // also wait for the weights, which complete after them).
     input_arrived(r, dig[0] ^ dig[1]);
+    // A gated pair in chunk ranges: this workgroup's chunks [rb, re) of the pair's list; chunk rb + i is chunk j0 + i
+    // counted from the start of tile t_first (so in tile t_first + seg, seg < kRangeSegs).
+    constexpr bool range = RANGE;
+    const uint32_t nc = ia.jb.n_chunks, nc2 = 2u * nc;
+    uint32_t rb = 0, re = 0, t_first = 0, j0 = 0;
+    if constexpr (RANGE) {
+        rb = static_cast<uint32_t>(static_cast<uint64_t>(blockIdx.x) * a.range_chunks / gridDim.x);
+        re = static_cast<uint32_t>(static_cast<uint64_t>(blockIdx.x + 1u) * a.range_chunks / gridDim.x);
+        t_first = rb / nc2;
+        j0 = rb - t_first * nc2;
+    }
+    struct RChunk {
+        uint32_t seg, q;  // tile segment, chunk of the row
+        bool up;
+    };
+    auto rchunk = [&](uint32_t i) {
+        const uint32_t jj = j0 + i;
+        RChunk c;
+        c.seg = (jj >= nc2 ? 1u : 0u) + (jj >= 2u * nc2 ? 1u : 0u);
+        const uint32_t within = jj - c.seg * nc2;
+        c.up = within >= nc;
+        c.q = c.up ? within - nc : within;
+        return c;
+    };
+    // chunk k of this wave in the range: its matrix and byte offset (a chunk past the range reads past the end); the
+    // load itself is issued in one place for both modes, so that the waits for it stay exact
+    auto issue_first = [&](int k) {
+        const uint32_t i = wave + kTileGroup * static_cast<uint32_t>(k);
+        const uint8_t* base;
+        uint32_t off;
+        if constexpr (RANGE) {
+            const RChunk c = rchunk(i);
+            const uint32_t t = min(t_first + c.seg, ia.jb.n_tiles - 1u);
+            const uint32_t grp = t / kTileGroup, tt = t - grp * kTileGroup;
+            const uint32_t T = min(static_cast<uint32_t>(kTileGroup), ia.jb.n_tiles - grp * kTileGroup);
+            base = c.up ? ia.jb.w2 : ia.jb.w;
+            off = rb + i < re ? ((grp * kTileGroup * nc + tt) * 64u + lane) * 16u + c.q * T * 1024u : kBufferOutOfRange;
+        } else {
+            const bool up = MULTI && ia.jb.w2 != nullptr && i >= ia.nq;
+            const uint32_t q = up ? i - ia.nq : i;
+            base = up ? ia.jb.w2 : ia.jb.w;
+            off = static_cast<uint32_t>(k) < ia.cnt ? ia.off + (ia.q0 + q) * ia.cs : kBufferOutOfRange;
+        }
+        const __amdgpu_buffer_rsrc_t r =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, ia.jb.w_bytes, kBufferRsrcWord3);
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kLoadNt));
+    };
+    // A range issues its first kRangeEarly chunks per wave now and the others as the first are consumed: all of them
+    // now would hold the input's waves at their loads (the CU's queue of memory instructions is full) until most of
+    // the stage's weights have arrived.
     u32x4 ba[DPER];
 #pragma unroll
-    for (int i = 0; i < DPER; ++i) ba[i] = issue_one(ia, true, i);
+    for (int i = 0; i < DPER; ++i)
+        if (!range || i < kRangeEarly) ba[i] = issue_first(i);
     const uint32_t item_b = blockIdx.x + gridDim.x;
     const bool has_b = MULTI && a.loop && item_b < a.total_items;
     Item ib{};
@@ -682,9 +772,9 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     if constexpr (MULTI) ib = locate(has_b ? item_b : blockIdx.x);
 
     float y[P4][4];
-    stage_y(a.in, r, s, blockIdx.x == 0, y);
-    float mx = stage_window(y, a.in.n, lo, hi, s);
-    if (a.in.amax != nullptr) mx = __uint_as_float(r.amax);
+    stage_y(in, r, s, blockIdx.x == 0, y);
+    float mx = stage_window(y, in.n, lo, hi, s);
+    if (in.amax != nullptr) mx = __uint_as_float(r.amax);
     // The table is filled after the input's values are computed (its loads were issued after the input's, so waiting
     // for them earlier would also wait for the input) and before the quantization's first barrier.
 #pragma unroll
@@ -695,7 +785,7 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     }
     float act_scale;
     int act_sum;
-    stage_quant(y, s, mx, a.in.n, a.tbr, c0, (ia.q0 + ia.nq) * 16u, lo, st, &act_scale, &act_sum);
+    stage_quant(y, s, mx, in.n, tbr, c0, (ia.q0 + ia.nq) * 16u, lo, st, &act_scale, &act_sum);
     if (blockIdx.x == 0 && tid == 0) *a.as_out = act_scale;
 
     // The sums of an item's chunks (from b) into red[slot] (gate, and up for a pair); with `next`, chunk i of the second
@@ -745,27 +835,50 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
         red[slot][0][wave][lane] = acc_lo + 16 * acc_hi;
         if (pair) red[slot][MULTI ? 1 : 0][wave][lane] = acc2_lo + 16 * acc2_hi;
     };
-    // Wave 0 after the barrier: the slice sums of an item from red[slot] and its outputs.
-    auto epilogue = [&](const Item& it, uint32_t slot) {
-        const bool pair = MULTI && it.jb.w2 != nullptr;
-        // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in slice 0
-        const DJob& jb = it.jb;
-        int v = 0;
+    // The sums of this wave's chunks of the range (from b) into red[tile segment][gate, up].
+    auto accumulate_range = [&](u32x4 (&b)[DPER]) {
+        int s00 = 0, s01 = 0, s10 = 0, s11 = 0, s20 = 0, s21 = 0;
 #pragma unroll
-        for (int w = 0; w < kNT / 64; ++w) v += red[slot][0][w][lane];
-        const uint32_t row = it.tile * kTileRows + lane;
-        // act_sum holds the codes of this slice's elements only: every slice subtracts its own
-        if (it.ks == 0) v += 8 * jb.dsum[row];
-        v -= act_sum;
-        if (!pair) {
-            jb.part[static_cast<size_t>(it.ks) * jb.padded_rows + row] = v;
-            return;
+        for (int k = 0; k < DPER; ++k) {
+            if (k + kRangeEarly < DPER) b[k + kRangeEarly] = issue_first(k + kRangeEarly);
+            const uint32_t i = wave + kTileGroup * static_cast<uint32_t>(k);
+            if (rb + i < re) {
+                const RChunk c = rchunk(i);
+                const uint32_t dw[4] = {b[k].x, b[k].y, b[k].z, b[k].w};
+                const uint2 e = st[c.q * 16u + (lane & 15u)];
+                __builtin_amdgcn_sched_barrier(0);
+                uint32_t t[16];
+#pragma unroll
+                for (int m = 0; m < 16; ++m) {
+                    const uint32_t addr = __builtin_amdgcn_perm(dw[m >> 2], lane_off, 0x0c0c0000u | ((4u + (m & 3)) << 8));
+                    t[m] = *reinterpret_cast<const uint32_t*>(tabb + addr);
+                }
+                int l = 0, h = 0;
+                dot4_bcast<0>(l, h, e.x, e.y, t[0], t[1], t[2], t[3]);
+                dot4_bcast<4>(l, h, e.x, e.y, t[4], t[5], t[6], t[7]);
+                dot4_bcast<8>(l, h, e.x, e.y, t[8], t[9], t[10], t[11]);
+                dot4_bcast<12>(l, h, e.x, e.y, t[12], t[13], t[14], t[15]);
+                const int v = l + 16 * h;
+                const uint32_t slot = c.seg * 2u + (c.up ? 1u : 0u);  // the same in every lane
+                if (slot == 0) s00 += v;
+                else if (slot == 1) s01 += v;
+                else if (slot == 2) s10 += v;
+                else if (slot == 3) s11 += v;
+                else if (slot == 4) s20 += v;
+                else s21 += v;
+            }
         }
-        int v2 = 0;
-#pragma unroll
-        for (int w = 0; w < kNT / 64; ++w) v2 += red[slot][MULTI ? 1 : 0][w][lane];
-        v2 += 8 * jb.dsum2[row] - act_sum;
-        // the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170
+        red[0][0][wave][lane] = s00;
+        red[0][1][wave][lane] = s01;
+        red[1][0][wave][lane] = s10;
+        red[1][1][wave][lane] = s11;
+        red[2][0][wave][lane] = s20;
+        red[2][1][wave][lane] = s21;
+    };
+    // The outputs of row `row` of a gated pair from the complete sums v (gate) and v2 (up) of its row, corrections
+    // included: the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170. A whole
+    // wave calls it (the absmax is a wave reduction).
+    auto gate_out = [&](const DJob& jb, uint32_t row, int v, int v2) {
         const bool zero = !(act_scale > 0.0f);
         const float g = zero ? 0.0f : static_cast<float>(v) * (jb.ws / act_scale);
         const float u = zero ? 0.0f : static_cast<float>(v2) * (jb.ws2 / act_scale);
@@ -788,6 +901,73 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
             if (lane == 0 && ao > 0.0f) atomicMax(jb.amax_out, __float_as_uint(ao));
         }
     };
+    // Wave 0 after the barrier: the slice sums of an item from red[slot] and its outputs.
+    auto epilogue = [&](const Item& it, uint32_t slot) {
+        const bool pair = MULTI && it.jb.w2 != nullptr;
+        // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in slice 0
+        const DJob& jb = it.jb;
+        int v = 0;
+#pragma unroll
+        for (int w = 0; w < kNT / 64; ++w) v += red[slot][0][w][lane];
+        const uint32_t row = it.tile * kTileRows + lane;
+        // act_sum holds the codes of this slice's elements only: every slice subtracts its own
+        if (it.ks == 0) v += 8 * jb.dsum[row];
+        v -= act_sum;
+        if (!pair) {
+            jb.part[static_cast<size_t>(it.ks) * jb.padded_rows + row] = v;
+            return;
+        }
+        int v2 = 0;
+#pragma unroll
+        for (int w = 0; w < kNT / 64; ++w) v2 += red[slot][MULTI ? 1 : 0][w][lane];
+        v2 += 8 * jb.dsum2[row] - act_sum;
+        gate_out(jb, row, v, v2);
+    };
+    if constexpr (RANGE) {
+        {
+            accumulate_range(ba);
+            __syncthreads();
+            // Wave sg takes tile t_first + sg of the range: with the whole tile here its outputs directly; otherwise its
+            // sums go to the tile's accumulators, and the workgroup that adds the last of them (the ticket counts the
+            // workgroups whose ranges meet the tile) takes the totals, clears them and writes the outputs.
+            const uint32_t t_last = (re - 1u) / nc2;
+            if (wave <= t_last - t_first) {
+                const DJob& jb = ia.jb;
+                const uint32_t sg = wave, t = t_first + sg, tb = t * nc2, te = tb + nc2;
+                int v = 0, v2 = 0;
+#pragma unroll
+                for (int w = 0; w < kNT / 64; ++w) {
+                    v += red[sg][0][w][lane];
+                    v2 += red[sg][1][w][lane];
+                }
+                bool last = true;
+                if (rb > tb || re < te) {
+                    int32_t* acc = jb.accum + static_cast<size_t>(t) * 128u;
+                    atomicAdd(acc + lane, v);
+                    atomicAdd(acc + 64u + lane, v2);
+                    __builtin_amdgcn_s_waitcnt(0);  // both adds complete before the ticket
+                    // workgroups whose ranges meet chunks tb and te - 1: w(g) = floor(((g + 1) G - 1) / C)
+                    const uint64_t C = a.range_chunks, G = gridDim.x;
+                    const uint32_t wf = static_cast<uint32_t>(((tb + 1ull) * G - 1ull) / C);
+                    const uint32_t wl = static_cast<uint32_t>((static_cast<uint64_t>(te) * G - 1ull) / C);
+                    uint32_t tk = 0;
+                    if (lane == 0) tk = atomicAdd(jb.tickets + t, 1u);
+                    tk = __builtin_amdgcn_readfirstlane(tk);
+                    last = tk == wl - wf;
+                    if (last) {
+                        v = atomicExch(acc + lane, 0);
+                        v2 = atomicExch(acc + 64u + lane, 0);
+                        if (lane == 0) atomicExch(jb.tickets + t, 0u);
+                    }
+                }
+                if (last) {
+                    const uint32_t row = t * kTileRows + lane;
+                    gate_out(jb, row, v + 8 * jb.dsum[row] - act_sum, v2 + 8 * jb.dsum2[row] - act_sum);
+                }
+            }
+            return;
+        }
+    }
     accumulate(ia, ba, 0u, true);
     if constexpr (MULTI) {
         if (has_b) accumulate(ib, bb, 1u, false);
@@ -1973,6 +2153,12 @@ enum DVariant : uint32_t { kDv4K = 0, kDv8K = 1, kDvPlain = 2 };
 
 template <int P4, int SA, int SB, bool MULTI>
 static void launch_dgemv_d(const DStageArgs& a, hipStream_t s) {
+    if constexpr (MULTI) {
+        if (a.range_chunks != 0) {
+            hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, true, kDPer, true>), dim3(a.grid), dim3(kNT), 0, s, a);
+            return;
+        }
+    }
     if (a.dper <= 1) hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, 1>), dim3(a.grid), dim3(kNT), 0, s, a);
     else if (a.dper <= 4) hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, 4>), dim3(a.grid), dim3(kNT), 0, s, a);
     else hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, kDPer>), dim3(a.grid), dim3(kNT), 0, s, a);
@@ -2098,6 +2284,7 @@ struct vx_decoder {
     uint16_t* d_head;                 // the untied head, or null
     float* d_inter;                   // gated pair output: act(gate, up), [ffn rounded up to 64]
     uint32_t* d_amax;                 // per layer: max |act(gate, up)| bits for an unnormed down input (pair, no sub-norms)
+    int32_t* d_pacc;                  // pair: per tile [gate, up][64] sums of the chunk-range split, then the tickets
     float* d_rope;
     uint16_t *d_kc, *d_vc;            // [layer][kv_head][max_ctx][head_dim]
     float *d_xa, *d_xb;               // the residual stream (written alternately by the stages that add to it)
@@ -2209,7 +2396,7 @@ static void destroy_decoder(vx_decoder* d) {
         if (p) (void)hipFree(p);
     void* bufs[] = {d->d_emb, d->d_head, d->d_inter, d->d_rope,   d->d_kc,    d->d_vc,    d->d_xa,
                     d->d_xb,  d->d_att,  d->d_logits, d->d_key, d->d_ctl, d->d_prompt, d->d_tokens, d->d_amax,
-                    d->d_scores, d->d_cy, d->d_cms, d->d_aticket};
+                    d->d_scores, d->d_cy, d->d_cms, d->d_aticket, d->d_pacc};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (int32_t* b : d->d_part)
@@ -2328,6 +2515,9 @@ static int create_decoder(const vx_decoder_config_t* cin, vx_decoder_t** out) {
     if (e == hipSuccess && pair) e = dalloc(d, &d->d_inter, round_up(c->ffn, kTileRows) * 4);
     if (e == hipSuccess && pair) e = dalloc(d, &d->d_amax, static_cast<size_t>(c->n_layers) * 4);
     if (e == hipSuccess && pair) e = hipMemset(d->d_amax, 0, static_cast<size_t>(c->n_layers) * 4);
+    const size_t pair_tiles = round_up(c->ffn, kTileRows) / kTileRows;
+    if (e == hipSuccess && pair) e = dalloc(d, &d->d_pacc, pair_tiles * (128 + 1) * 4);
+    if (e == hipSuccess && pair) e = hipMemset(d->d_pacc, 0, pair_tiles * (128 + 1) * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_rope, static_cast<size_t>(c->max_ctx) * c->head_dim * 4);
     if (e == hipSuccess) e = dalloc(d, &d->d_kc, kv_elems * 2);
     if (e == hipSuccess) e = dalloc(d, &d->d_vc, v_elems * 2);
@@ -2470,6 +2660,15 @@ static int build_stages(vx_decoder* d) {
                 j.kslices = 1;
                 j.slice_chunks = j.n_chunks;
                 items = j.n_tiles;
+                // Equal chunk ranges over one workgroup per CU when every range is non-empty, fits 16 waves x kDPer
+                // chunks and meets at most kRangeSegs tiles; else one or two tiles per workgroup.
+                const uint64_t C = static_cast<uint64_t>(j.n_tiles) * 2u * j.n_chunks, G = static_cast<uint64_t>(d->num_cus);
+                if (C >= G && (C + G - 1) / G <= static_cast<uint64_t>(kTileGroup * kDPer) &&
+                    2u * j.n_chunks >= static_cast<uint32_t>(8 * kDPer) && j.n_tiles > G) {
+                    a.range_chunks = static_cast<uint32_t>(C);
+                    j.accum = d->d_pacc;
+                    j.tickets = reinterpret_cast<uint32_t*>(d->d_pacc + static_cast<size_t>(j.n_tiles) * 128u);
+                }
             } else {
                 for (int k : kStageKinds[s]) {
                     if (k < 0) continue;
@@ -2495,8 +2694,9 @@ static int build_stages(vx_decoder* d) {
             // A stage whose jobs have one K slice each and more items than CUs gives a workgroup two items.
             bool one_slice = true;
             for (uint32_t jj = 0; jj < a.n_jobs; ++jj) one_slice = one_slice && a.job[jj].kslices == 1;
-            a.loop = one_slice && items > static_cast<uint32_t>(d->num_cus) ? 1u : 0u;
+            a.loop = one_slice && items > static_cast<uint32_t>(d->num_cus) && a.range_chunks == 0 ? 1u : 0u;
             a.grid = a.loop ? std::max(static_cast<uint32_t>(d->num_cus), (items + 1u) / 2u) : items;
+            if (a.range_chunks != 0) a.grid = static_cast<uint32_t>(d->num_cus);
             // chunks per wave of the largest item (a pair's gate and up chunks count together): the instance loads
             // 1, 4 or kDPer
             uint32_t most = 0;
@@ -2507,6 +2707,7 @@ static int build_stages(vx_decoder* d) {
             if (most > static_cast<uint32_t>(kDPer))
                 VX_FAIL(VX_ERR_INTERNAL, "stage %d with %u chunks per wave (at most %d)", s, most, kDPer);
             a.dper = most <= 1u ? 1u : (most <= 4u ? 4u : static_cast<uint32_t>(kDPer));
+            if (a.range_chunks != 0) a.dper = static_cast<uint32_t>(kDPer);
             StageInput& in = a.in;
             if (s == 0 && l == 0) {  // embedding -> attention norm
                 in = stage_input(d, kInEmbed, H, nullptr, d->d_xa, nw[VX_NORM_ATTN]);

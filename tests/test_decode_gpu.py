@@ -66,7 +66,9 @@ def variant_cfg(oracle, name):
     relu_wide ReLU^2 without sub-norms and an FFN wider than a normed input (8420, not a multiple of 160): gate and up
              run as the gated pair with the ReLU^2 epilogue, which also produces the down input's absmax
     hd64     the BitNet structure at head_dim 64 (the smallest head the reference's GPU decoder accepts, gpu.rs:163-165)
-    gqa16    head_dim 32 with 16 query heads on one KV head (a score workgroup takes 8 query heads: two head groups)"""
+    gqa16    head_dim 32 with 16 query heads on one KV head (a score workgroup takes 8 query heads: two head groups)
+    pair_range the Falcon3 structure at hidden 2560 (32 chunks per row) and FFN 1024: the gate/up pair split into equal
+             chunk ranges, one per CU, each tile's sums gathered from 16 workgroups by atomic adds and a ticket"""
     M = oracle.ModelConfig
     return {
         "falcon3": oracle.falcon3(2, 256, 4, 2, 256, 9220, 1000, 640, 1e-5, 100000.0),
@@ -76,6 +78,7 @@ def variant_cfg(oracle, name):
         "relu_wide": M(2, 256, 4, 1, 128, 8420, 1000, 640, 1e-5, 10000.0, oracle.ACT_RELU2, oracle.ROPE_NORMAL, 1, 1, 0),
         "hd64": M(2, 256, 8, 2, 64, 384, 1000, 640, 1e-5, 10000.0),
         "gqa16": M(2, 512, 16, 1, 32, 384, 1000, 640, 1e-5, 10000.0),
+        "pair_range": oracle.falcon3(2, 2560, 4, 2, 256, 1024, 1000, 640, 1e-5, 100000.0),
     }[name]
 
 
@@ -144,7 +147,8 @@ def test_tiny_generate_tokens_identical(torch_dev, oracle, max_ctx, n_prompt, n_
         model.close()
 
 
-@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw", "relu_wide", "hd64", "gqa16"])
+@pytest.mark.parametrize("name", ["falcon3", "hd256", "silu_sub", "relu_raw", "relu_wide", "hd64", "gqa16",
+                                  "pair_range"])
 def test_variant_step_logits_bit_exact(torch_dev, oracle, name):
     """forward_token of each architecture variant at positions 0..299 (teacher forced; the 4-chunk attention split from
     position 256): every logit bit-identical to the oracle's, every greedy token equal."""
