@@ -69,7 +69,7 @@ void q2_to_device_layout(const uint8_t* planar, const uint16_t* scales, size_t r
 // ---- kernel -----------------------------------------------------------------------------------------------------------
 
 constexpr int kQ2Waves = 16;   // 8 tiles x 2 halves of 32 rows
-constexpr int kQ2Pre = 8;      // blocks of weights in flight per wave
+constexpr int kQ2Pre = 4;      // blocks of weights in flight per wave (64 KiB per CU)
 
 __constant__ TritTable g_trits = make_trit_table();
 
@@ -139,79 +139,91 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
                              (static_cast<size_t>(tile) * ng * kTileRows + rb * 32u + (lane & 31u)) * 5u;
         const size_t sstride = static_cast<size_t>(kTileRows) * 5u;  // dwords between scale groups of a tile
 
+        // the loop body is two scale groups of 4 blocks, one per register set, with the same weight slots in both
+        static_assert(kQ2Pre == 4, "four weight slots per scale group");
         u32x4 wq[kQ2Pre];
 #pragma unroll
         for (int i = 0; i < kQ2Pre; ++i) wq[i] = __builtin_nontemporal_load(wp + min(static_cast<uint32_t>(i), nb - 1u) * bstride);
-        uint32_t sc[5], scn[5];
+        // Scale groups alternate between two register sets (group g in set g & 1), each loaded one group ahead, so no
+        // loaded register is ever copied (a copy would wait for its load). Every load is unconditional (indices clamp at
+        // the last block and group) and blocks past the row skip only the arithmetic, so every wait is for its own load.
+        uint32_t sa[5], sb[5];
 #pragma unroll
-        for (int i = 0; i < 5; ++i) sc[i] = sp[i];
-#pragma unroll
-        for (int i = 0; i < 5; ++i) scn[i] = sp[min(1u, ng - 1u) * sstride + i];
+        for (int i = 0; i < 5; ++i) sa[i] = sp[i];
 
         float acc0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, acc1[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t b0 = 0; b0 < nb; b0 += kQ2Pre) {
+        // block b with its weights w and the scales sc of its group
+        auto block = [&](uint32_t b, const u32x4 w, const uint32_t (&sc)[5]) __attribute__((always_inline)) {
+            // W operand: K blocks 0..3 (t0..t3 of bytes 4 m .. 4 m + 3) and 4 (t4 of the 16 bytes)
+            const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
+            v4i Bm[5];
 #pragma unroll
-            for (int ib = 0; ib < kQ2Pre; ++ib) {
+            for (int m = 0; m < 4; ++m) {
+                int t[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + k) << 8));
+                    t[k] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
+                }
+                Bm[m] = v4i{t[0], t[1], t[2], t[3]};
+            }
+            Bm[4] = v4i{static_cast<int>(t4_bytes(dw[0])), static_cast<int>(t4_bytes(dw[1])),
+                        static_cast<int>(t4_bytes(dw[2])), static_cast<int>(t4_bytes(dw[3]))};
+            // A' operands from the activation dwords of this block
+            const uint32_t x = actw[(5u * b + pl) * 8u + jl];
+            const uint32_t x4 = actw[(5u * b + 4u) * 8u + (mr & 7u)];
+            v16i c = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+            v16i c4 = c;
+            const int D[4] = {static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[0])),
+                              static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[1])),
+                              static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[2])),
+                              static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[3]))};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const v4i A = v4i{on[m] ? D[0] : 0, on[m] ? D[1] : 0, on[m] ? D[2] : 0, on[m] ? D[3] : 0};
+                c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm[m], c, 0, 0, 0);
+            }
+            {
+                const int xi = static_cast<int>(x4);
+                const v4i A = v4i{on4[0] ? xi : 0, on4[1] ? xi : 0, on4[2] ? xi : 0, on4[3] ? xi : 0};
+                c4 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm[4], c4, 0, 0, 0);
+            }
+            // the reference's chains: s = 5 b + p in order; register r = 4 p + jj of c holds L[s][4 hh + jj]
+#pragma unroll
+            for (int p = 0; p < 5; ++p) {
+                const uint32_t s = 5u * b + static_cast<uint32_t>(p);
+                if (s >= ns) break;
+                const uint32_t kl = (5u * (b & 3u) + static_cast<uint32_t>(p)) / 2u;  // scale index in the group
+                const uint32_t hw = sc[kl >> 1] >> ((kl & 1u) * 16u);
+                const float d = half_bits_to_float(hw & 0xffffu) * ascl[s];
+                const bool odd = (s / 2u) & 1u;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const int L = p < 4 ? c[4 * p + jj] : c4[jj];
+                    if (odd) acc1[jj] = __builtin_fmaf(d, static_cast<float>(L), acc1[jj]);
+                    else acc0[jj] = __builtin_fmaf(d, static_cast<float>(L), acc0[jj]);
+                }
+            }
+        };
+        for (uint32_t b0 = 0; b0 < nb; b0 += 8u) {
+            const uint32_t g = b0 / 4u;
+#pragma unroll
+            for (int i = 0; i < 5; ++i) sb[i] = sp[min(g + 1u, ng - 1u) * sstride + i];
+#pragma unroll
+            for (int ib = 0; ib < 4; ++ib) {
                 const uint32_t b = b0 + ib;
-                if (b >= nb) break;
                 const u32x4 w = wq[ib];
                 wq[ib] = __builtin_nontemporal_load(wp + min(b + kQ2Pre, nb - 1u) * bstride);
-                if ((b & 3u) == 0 && b > 0) {  // a new group of 4 blocks: its scales, the next group's load
+                if (b < nb) block(b, w, sa);
+            }
 #pragma unroll
-                    for (int i = 0; i < 5; ++i) sc[i] = scn[i];
+            for (int i = 0; i < 5; ++i) sa[i] = sp[min(g + 2u, ng - 1u) * sstride + i];
 #pragma unroll
-                    for (int i = 0; i < 5; ++i) scn[i] = sp[min(b / 4u + 1u, ng - 1u) * sstride + i];
-                }
-                // W operand: K blocks 0..3 (t0..t3 of bytes 4 m .. 4 m + 3) and 4 (t4 of the 16 bytes)
-                const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
-                v4i Bm[5];
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    int t[4];
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + k) << 8));
-                        t[k] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
-                    }
-                    Bm[m] = v4i{t[0], t[1], t[2], t[3]};
-                }
-                Bm[4] = v4i{static_cast<int>(t4_bytes(dw[0])), static_cast<int>(t4_bytes(dw[1])),
-                            static_cast<int>(t4_bytes(dw[2])), static_cast<int>(t4_bytes(dw[3]))};
-                // A' operands from the activation dwords of this block
-                const uint32_t x = actw[(5u * b + pl) * 8u + jl];
-                const uint32_t x4 = actw[(5u * b + 4u) * 8u + (mr & 7u)];
-                v16i c = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-                v16i c4 = c;
-                const int D[4] = {static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[0])),
-                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[1])),
-                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[2])),
-                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[3]))};
-#pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    const v4i A = v4i{on[m] ? D[0] : 0, on[m] ? D[1] : 0, on[m] ? D[2] : 0, on[m] ? D[3] : 0};
-                    c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm[m], c, 0, 0, 0);
-                }
-                {
-                    const int xi = static_cast<int>(x4);
-                    const v4i A = v4i{on4[0] ? xi : 0, on4[1] ? xi : 0, on4[2] ? xi : 0, on4[3] ? xi : 0};
-                    c4 = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm[4], c4, 0, 0, 0);
-                }
-                // the reference's chains: s = 5 b + p in order; register r = 4 p + jj of c holds L[s][4 hh + jj]
-#pragma unroll
-                for (int p = 0; p < 5; ++p) {
-                    const uint32_t s = 5u * b + static_cast<uint32_t>(p);
-                    if (s >= ns) break;
-                    const uint32_t kl = (5u * (b & 3u) + static_cast<uint32_t>(p)) / 2u;  // scale index in the group
-                    const uint32_t hw = sc[kl >> 1] >> ((kl & 1u) * 16u);
-                    const float d = half_bits_to_float(hw & 0xffffu) * ascl[s];
-                    const bool odd = (s / 2u) & 1u;
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const int L = p < 4 ? c[4 * p + jj] : c4[jj];
-                        if (odd) acc1[jj] = __builtin_fmaf(d, static_cast<float>(L), acc1[jj]);
-                        else acc0[jj] = __builtin_fmaf(d, static_cast<float>(L), acc0[jj]);
-                    }
-                }
+            for (int ib = 0; ib < 4; ++ib) {
+                const uint32_t b = b0 + 4u + ib;
+                const u32x4 w = wq[ib];
+                wq[ib] = __builtin_nontemporal_load(wp + min(b + kQ2Pre, nb - 1u) * bstride);
+                if (b < nb) block(b, w, sb);
             }
         }
         // l[j] = acc[0][j] + acc[1][j]; lanes hh = 0 hold j = 0..3, hh = 1 j = 4..7
