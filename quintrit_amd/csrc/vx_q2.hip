@@ -83,18 +83,18 @@ typedef __attribute__((address_space(4))) const Q2Job c_q2job;
 // activations and their scales are staged in LDS once per item; every wave then streams its rows' blocks in order.
 template <bool MANY>
 __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
-    __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of t0..t3 of byte B (first half)
+    __shared__ uint2 tab[256 * 32];  // row B: 32 copies of (t0..t3 of byte B, t4 of B in every byte), 256 bytes
     __shared__ uint32_t actw[kQ2MaxCols / 4 + 64];
     __shared__ float ascl[kQ2MaxCols / 32];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    for (uint32_t i = tid; i < 256u * 8u; i += kQ2Waves * 64u) {
-        const uint32_t e = g_trits.v[i >> 3];
-        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
+    for (uint32_t i = tid; i < 256u * 16u; i += kQ2Waves * 64u) {
+        const uint32_t b = i >> 4, e = g_trits.v[b], e4 = t4_bytes(b * 0x01010101u);
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + b * 256u + (i & 15u) * 16u) = make_uint4(e, e4, e, e4);
     }
     const char* tabb = reinterpret_cast<const char*>(tab);
-    const uint32_t lane_off = (lane & 31u) * 4u;
+    const uint32_t lane_off = (lane & 31u) * 8u;
 
     // This lane's A' rows: C row mr = lane % 32 (plane p = mr / 8, lane sum j = mr % 8) and K half hh = lane / 32.
     // sel[q] places byte q of the activation dword at byte p of K dword q (v_perm selector 0x0c gives 0x00); the
@@ -155,20 +155,25 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
         // block b with its weights w and the scales sc of its group
         auto block = [&](uint32_t b, const u32x4 w, const uint32_t (&sc)[5]) __attribute__((always_inline)) {
             // W operand: K blocks 0..3 (t0..t3 of bytes 4 m .. 4 m + 3) and 4 (t4 of the 16 bytes)
+            // one 8-byte table entry per byte: t0..t3, and t4 in every byte, of which byte k of a dword keeps byte k
             const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
             v4i Bm[5];
+            uint32_t t4w[4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 int t[4];
+                uint32_t e4[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + k) << 8));
-                    t[k] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
+                    const uint2 e = *reinterpret_cast<const uint2*>(tabb + addr);
+                    t[k] = static_cast<int>(e.x);
+                    e4[k] = e.y;
                 }
                 Bm[m] = v4i{t[0], t[1], t[2], t[3]};
+                t4w[m] = __builtin_amdgcn_perm(e4[3], e4[2], 0x07020c0cu) | __builtin_amdgcn_perm(e4[1], e4[0], 0x0c0c0500u);
             }
-            Bm[4] = v4i{static_cast<int>(t4_bytes(dw[0])), static_cast<int>(t4_bytes(dw[1])),
-                        static_cast<int>(t4_bytes(dw[2])), static_cast<int>(t4_bytes(dw[3]))};
+            Bm[4] = v4i{static_cast<int>(t4w[0]), static_cast<int>(t4w[1]), static_cast<int>(t4w[2]), static_cast<int>(t4w[3])};
             // A' operands from the activation dwords of this block
             const uint32_t x = actw[(5u * b + pl) * 8u + jl];
             const uint32_t x4 = actw[(5u * b + 4u) * 8u + (mr & 7u)];
