@@ -136,6 +136,7 @@ class Stream:
         gen.manual_seed(0x5EED)
         self.mats = []      # per layer: list of (name, handle, rows, cols)
         self.staged = []    # per launch: (tensor, nbytes)
+        self.luts = []      # per launch: the input's compact activation tables (tensor, nbytes)
         self.outs = []
         self.weights = 0
         self.alg_bytes = 0
@@ -160,9 +161,13 @@ class Stream:
                 staged = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
                 lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(q.data_ptr()), cols, cols,
                                               ctypes.c_void_p(staged.data_ptr()), nbytes, stream))
+                lbytes = lib.compact_lut_bytes(cols)
+                lut = torch.empty(lbytes, dtype=torch.int8, device="cuda")
+                lib.compact_lut_dev(q.data_ptr(), cols, cols, lut.data_ptr(), lbytes, stream)
                 self.scales[k] = s
                 row.append((name, h, rows, cols))
                 self.staged.append((staged, nbytes))
+                self.luts.append((lut, lbytes))
                 self.outs.append(torch.empty(rows, dtype=torch.float32, device="cuda"))
                 self.weights += rows * cols
                 self.alg_bytes += rows * cols / 5.0
@@ -171,14 +176,15 @@ class Stream:
             self.mats.append(row)
         torch.cuda.synchronize()
 
-    def jobs(self, which=None):
-        """vx_gemv_job_t list in model order (all launch types, or only LAYER_SHAPES[which])."""
+    def jobs(self, which=None, tables=False):
+        """vx_gemv_job_t list in model order (all launch types, or only LAYER_SHAPES[which]); with `tables` each job
+        reads its input's compact activation tables instead of the staged nibbles."""
         out = []
         k = 0
         for row in self.mats:
             for t, (_, h, rows, _) in enumerate(row):
                 if which is None or which == t:
-                    staged, nbytes = self.staged[k]
+                    staged, nbytes = (self.luts if tables else self.staged)[k]
                     out.append(self.lib.GemvJob(out_f32=1, matrix=h.value, staged=staged.data_ptr(), staged_len=nbytes,
                                                 act_scale_dev=self.scales.data_ptr() + 4 * k,
                                                 out=self.outs[k].data_ptr(), out_capacity=rows))
@@ -204,6 +210,37 @@ class Stream:
 
 
 LONE_SHAPES = (("q/o", 3072, 3072), ("k/v", 1024, 3072), ("gate/up", 23040, 3072), ("down", 3072, 23040))
+
+
+def table_decode_ab(torch, st, plan, stream, args) -> dict:
+    """The same 160-projection plan through the compact activation tables (vx_lut_plan_create: U/L split of every
+    byte and two table lookups, the reference CPU kernel's decode) against the digit-table plan: every output equal
+    bit for bit, then both timed back to back."""
+    from quintrit_amd import _lib
+    lplan = _lib.LutPlan(st.jobs(tables=True))
+    plan.run(stream())
+    torch.cuda.synchronize()
+    want = [o.clone() for o in st.outs]
+    for o in st.outs:
+        o.fill_(float("nan"))
+    lplan.run(stream())
+    torch.cuda.synchronize()
+    same = all(torch.equal(a.view(torch.int32), b.view(torch.int32)) for a, b in zip(want, st.outs))
+    if not same:
+        raise SystemExit("the compact-table plan's outputs differ from the digit-table plan's")
+    ml, _ = time_fn(torch, lambda: lplan.run(stream()), max(3, args.steps // 2), 2)
+    md, _ = time_fn(torch, lambda: plan.run(stream()), max(3, args.steps // 2), 2)
+    lbytes = sum(n for _, n in st.luts)
+    out = {"ms_per_step": round(ml, 4), "alg_GBps": round(st.alg_bytes / (ml / 1e3) / 1e9, 1),
+           "frac": round(st.alg_bytes / (ml / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+           "digit_ms_per_step": round(md, 4), "work_items": lplan.work_items(), "table_bytes": lbytes,
+           "outputs": "all 160 equal the digit-table plan's, bit for bit",
+           "note": "A/B of the decode: compact tables (2 LDS lookups + 6.5 VALU per weight byte) vs the digit table "
+                   "(1 lookup + 3 VALU); same plan, same inputs, tables built before the timed region"}
+    log(f"  compact-table plan: {ml:.4f} ms/step ({out['alg_GBps']} GB/s, {out['frac']:.1%} of peak) vs digit-table "
+        f"{md:.4f} ms/step")
+    lplan.close()
+    return out
 
 
 def lone_latency(torch, L, lib, reps: int = 200):
@@ -1063,6 +1100,7 @@ def main():
     # The other measurements run first: they also bring the GPU to its steady clocks before the headline timing.
     breakdown = {}
     chain = None
+    table_decode = None
     if not args.no_breakdown:
         # each launch type alone, over all layers (distinct weights, so no cache reuse)
         for t, (name, rows, cols) in enumerate(LAYER_SHAPES):
@@ -1082,6 +1120,7 @@ def main():
         log(f"  chain of {len(st.jobs())} lone GEMVs in a graph: {mc:.4f} ms/step, {chain['alg_GBps']} GB/s")
         del g
         chain["lone_calls"] = lone_latency(torch, L, _lib)
+        table_decode = table_decode_ab(torch, st, plan, stream, args)
 
     for o in st.outs:
         o.fill_(float("nan"))
@@ -1145,7 +1184,7 @@ def main():
         "vs_baseline_ref": f"{REF_CPU_GWEIGHTS} Gweights/s, the published Falcon3-10B weight-stream rate of the reference AVX-512 kernel, 4 threads, EPYC 9V45 "
                                    f"(docs/benchmarks.md:77)",
         "settle": {"seconds": SETTLE_S, "plan_runs": n_settle},
-        "chain": chain, "breakdown": breakdown, "roofline": roofline, "cpu_baseline": cpu, "decode": decode,
+        "chain": chain, "breakdown": breakdown, "table_decode": table_decode, "roofline": roofline, "cpu_baseline": cpu, "decode": decode,
     }
     print(json.dumps(line), flush=True)
     return 0

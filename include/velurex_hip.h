@@ -185,6 +185,28 @@ int vx_gemv_staged_f32_dev(const vx_matrix_t* matrix, const void* staged, size_t
                            size_t out_capacity, void* stream);
 
 /*
+ * Compact activation tables on device memory: the GPU form of build_activation_lut_wide_avx512_into /
+ * build_compact_wide_impl (quintrit-core/src/simd/avx512.rs:1178-1247), byte for byte. Per device byte-column c and
+ * part (lo, then hi) one 64-byte table of int8 sums: entry s < 9 is t3 a3 + t4 a4 for the 2-trit group U = s, entry
+ * 9 + L is t0 a0 + t1 a1 + t2 a2 for the 3-trit group L < 27, the rest is zero, where a_p is the lo or hi part
+ * (lut.rs:380-388: lo = ((x + 8) & 15) - 8, hi = (x - lo) >> 4) of activation column_activation_index(cols, c, p). The
+ * lo tables of all tile_row_bytes(cols) columns come first, then the hi tables: vx_compact_lut_bytes(cols) =
+ * 2 * 64 * tile_row_bytes(cols). `lut` must be 16-byte aligned. One table set serves every matrix with the same cols.
+ */
+int vx_compact_lut_bytes(size_t cols, size_t* out_bytes);
+int vx_compact_lut_dev(const int8_t* acts, size_t acts_len, size_t cols, int8_t* lut, size_t lut_capacity, void* stream);
+/*
+ * GEMVs through the compact tables: each weight byte is split without a division into U = floor(B / 28) and
+ * L = B - 28 U and looked up at U and 9 + L (decode_compact, avx512.rs:1256-1292; the row loop of compact_multi_block,
+ * avx512.rs:1526-1604). Same results as vx_gemv_staged_i32_dev / vx_gemv_staged_f32_dev on the same activations; the
+ * digit-table kernel of those calls is the faster decode on this GPU and the one the plans and the decoder use.
+ */
+int vx_gemv_lut_i32_dev(const vx_matrix_t* matrix, const int8_t* lut, size_t lut_len, int32_t* out, size_t out_capacity,
+                        void* stream);
+int vx_gemv_lut_f32_dev(const vx_matrix_t* matrix, const int8_t* lut, size_t lut_len, float act_scale, float* out,
+                        size_t out_capacity, void* stream);
+
+/*
  * TernaryGemvLayer::forward (layer.rs:74) on host memory: acts (acts_len >= cols) and out (out_capacity >= rows) are
  * host buffers; the call returns when out holds y = alpha * beta * (W x) with the epilogue of vx_gemv_f32_dev.
  */
@@ -230,6 +252,12 @@ typedef struct vx_plan vx_plan_t;
  * a plan is the single-launch form of both.
  */
 int vx_plan_create(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan);
+/*
+ * The same plan through the compact tables (vx_gemv_lut_i32_dev): each job's `staged` is the table set of its
+ * matrix's cols (vx_compact_lut_dev, staged_len >= vx_compact_lut_bytes(cols), 16-byte aligned). Run, count and free
+ * it with the calls below.
+ */
+int vx_lut_plan_create(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan);
 /* Enqueues the plan on `stream`. Runs of one plan must not overlap (they share the partial-sum workspace). */
 int vx_plan_run(const vx_plan_t* plan, void* stream);
 /* Number of work items (tile group x K slice) of the plan. */

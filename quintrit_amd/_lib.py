@@ -62,10 +62,15 @@ SIGNATURES = {
     "vx_stage_acts_dev": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
     "vx_gemv_staged_i32_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp]),
     "vx_gemv_staged_f32_dev": (_i32, [_vp, _vp, _sz, _f32, _vp, _sz, _vp]),
+    "vx_compact_lut_bytes": (_i32, [_sz, _vp]),
+    "vx_compact_lut_dev": (_i32, [_vp, _sz, _sz, _vp, _sz, _vp]),
+    "vx_gemv_lut_i32_dev": (_i32, [_vp, _vp, _sz, _vp, _sz, _vp]),
+    "vx_gemv_lut_f32_dev": (_i32, [_vp, _vp, _sz, _f32, _vp, _sz, _vp]),
     "vx_layer_forward": (_i32, [_vp, _vp, _sz, _f32, _vp, _sz]),
     "vx_gemv_planar_i32": (_i32, [_vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz]),
     "vx_gemv_planar_f32": (_i32, [_vp, _sz, _sz, _sz, _vp, _sz, _f32, _vp, _sz]),
     "vx_plan_create": (_i32, [_vp, _sz, _vp]),
+    "vx_lut_plan_create": (_i32, [_vp, _sz, _vp]),
     "vx_plan_run": (_i32, [_vp, _vp]),
     "vx_plan_work_items": (_i32, [_vp, _vp]),
     "vx_plan_free": (_i32, [_vp]),
@@ -206,6 +211,32 @@ class Plan:
             self.close()
         except Exception:
             pass
+
+
+class LutPlan(Plan):
+    """A plan of GEMVs through the compact activation tables (vx_lut_plan_create): each job's `staged` is the table
+    set of its matrix's cols (compact_lut_dev); run and freed like Plan."""
+
+    def __init__(self, jobs):  # noqa: super().__init__ builds digit-table plans
+        arr = (GemvJob * len(jobs))()
+        for i, j in enumerate(jobs):
+            arr[i] = j
+            arr[i].struct_size = ctypes.sizeof(GemvJob)
+        h = ctypes.c_void_p()
+        check(lib().vx_lut_plan_create(arr, len(jobs), ctypes.byref(h)))
+        self._h = h
+
+
+def compact_lut_bytes(cols: int) -> int:
+    n = ctypes.c_size_t()
+    check(lib().vx_compact_lut_bytes(cols, ctypes.byref(n)))
+    return n.value
+
+
+def compact_lut_dev(acts_ptr: int, acts_len: int, cols: int, lut_ptr: int, lut_capacity: int, stream_ptr=None) -> None:
+    """Builds the compact activation tables of `cols` int8 activations at acts_ptr into lut_ptr (device pointers)."""
+    check(lib().vx_compact_lut_dev(ctypes.c_void_p(acts_ptr), acts_len, cols, ctypes.c_void_p(lut_ptr), lut_capacity,
+                                   stream_ptr))
 
 
 class Q2Job(ctypes.Structure):

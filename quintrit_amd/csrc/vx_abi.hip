@@ -111,9 +111,11 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     const size_t io_bytes = round_up(cols, 256) + m->g.padded_rows * 4;
     hipError_t e = hipMalloc(&m->d_w, m->g.device_bytes);
     if (e == hipSuccess && m->kslices > 1) e = hipMalloc(&m->d_part, static_cast<size_t>(m->kslices) * m->g.padded_rows * 4);
-    if (e == hipSuccess && m->kslices > 1) e = hipMalloc(&m->d_accum, m->g.padded_rows * 4 + m->g.n_groups * 4);
-    if (e == hipSuccess && m->kslices > 1) e = hipMemset(m->d_accum, 0, m->g.padded_rows * 4 + m->g.n_groups * 4);
-    if (e == hipSuccess && m->kslices > 1) m->d_tickets = reinterpret_cast<uint32_t*>(m->d_accum + m->g.padded_rows);
+    // the atomic slice sums and tickets of the lone calls (the table GEMV splits K more finely than the digit GEMV,
+    // so every matrix has them)
+    if (e == hipSuccess) e = hipMalloc(&m->d_accum, m->g.padded_rows * 4 + m->g.n_groups * 4);
+    if (e == hipSuccess) e = hipMemset(m->d_accum, 0, m->g.padded_rows * 4 + m->g.n_groups * 4);
+    if (e == hipSuccess) m->d_tickets = reinterpret_cast<uint32_t*>(m->d_accum + m->g.padded_rows);
     if (e == hipSuccess) e = hipMalloc(&m->d_dsum, m->g.padded_rows * 4);
     if (e == hipSuccess) e = hipMalloc(&m->d_staged, staged_bytes(cols));
     if (e == hipSuccess) e = hipMalloc(&m->d_io, io_bytes);
@@ -217,6 +219,26 @@ static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint
     j.item_begin = 0;
     a.total_items = job_items(j);
     return launch_gemv(a, j.rows, nullptr, j.kslices > 1 && j.accum == nullptr ? 1u : 0u, m->num_cus, s);
+}
+
+// A lone GEMV of matrix m through the compact activation tables `lut` (its K slices add up in m's atomic sums, as
+// run_single's do).
+static int run_single_lut(const vx_matrix* m, const int8_t* lut, void* out, uint32_t out_kind, float post, hipStream_t s) {
+    LaunchArgs a{};
+    a.jobs = nullptr;
+    a.n_jobs = 1;
+    Job& j = a.one;
+    plan_lut_job(j, m->g, static_cast<uint32_t>(m->num_cus));
+    j.w = m->d_w;
+    j.staged = reinterpret_cast<const uint8_t*>(lut);
+    j.accum = m->d_accum;
+    j.tickets = m->d_tickets;
+    j.out = out;
+    j.post = post;
+    j.weight_scale = m->weight_scale;
+    j.out_kind = out_kind;
+    a.total_items = job_items(j);
+    return launch_gemv_lut(a, j.rows, nullptr, 0, m->num_cus, s);
 }
 
 // out = float(acc) * (ws / as) with the division done once here, as the layers do; zeros when as <= 0 or NaN
@@ -386,6 +408,60 @@ int vx_gemv_staged_f32_dev(const vx_matrix_t* matrix, const void* staged, size_t
     });
 }
 
+int vx_compact_lut_bytes(size_t cols, size_t* out_bytes) {
+    return guard([&]() -> int {
+        if (out_bytes == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_bytes is NULL");
+        VX_TRY(check_shape(1, cols));
+        *out_bytes = compact_lut_bytes(cols);
+        return VX_OK;
+    });
+}
+
+int vx_compact_lut_dev(const int8_t* acts, size_t acts_len, size_t cols, int8_t* lut, size_t lut_capacity, void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_shape(1, cols));
+        if (acts == nullptr || lut == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "activations or lut is NULL");
+        if (acts_len < cols) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "activations hold %zu values but cols = %zu", acts_len, cols);
+        const size_t need = compact_lut_bytes(cols);
+        if (lut_capacity < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "lut holds %zu bytes, %zu needed", lut_capacity, need);
+        if ((reinterpret_cast<uintptr_t>(lut) & 15u) != 0) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "lut must be 16-byte aligned");
+        return launch_compact_lut(acts, cols, lut, static_cast<hipStream_t>(stream));
+    });
+}
+
+static int check_lut(const vx_matrix_t* m, const int8_t* lut, size_t lut_len, const void* out, size_t out_capacity) {
+    if (lut == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "lut is NULL");
+    if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out is NULL");
+    const size_t need = compact_lut_bytes(m->g.cols);
+    if (lut_len < need) VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "lut holds %zu bytes, %zu needed", lut_len, need);
+    if ((reinterpret_cast<uintptr_t>(lut) & 15u) != 0) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "lut must be 16-byte aligned");
+    if (out_capacity < m->g.rows)
+        VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "output holds %zu values but rows = %zu", out_capacity, m->g.rows);
+    return VX_OK;
+}
+
+int vx_gemv_lut_i32_dev(const vx_matrix_t* matrix, const int8_t* lut, size_t lut_len, int32_t* out, size_t out_capacity,
+                        void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_kind(matrix, kKindVelurex));
+        VX_TRY(check_lut(matrix, lut, lut_len, out, out_capacity));
+        VX_TRY(set_device_of(matrix));
+        return run_single_lut(matrix, lut, out, kOutI32, 1.0f, static_cast<hipStream_t>(stream));
+    });
+}
+
+int vx_gemv_lut_f32_dev(const vx_matrix_t* matrix, const int8_t* lut, size_t lut_len, float act_scale, float* out,
+                        size_t out_capacity, void* stream) {
+    return guard([&]() -> int {
+        VX_TRY(check_kind(matrix, kKindVelurex));
+        VX_TRY(check_lut(matrix, lut, lut_len, out, out_capacity));
+        VX_TRY(set_device_of(matrix));
+        const hipStream_t s = static_cast<hipStream_t>(stream);
+        if (!(act_scale > 0.0f)) return launch_fill_f32(out, matrix->g.rows, 0.0f, s);
+        return run_single_lut(matrix, lut, out, kOutF32Post, matrix->weight_scale / act_scale, s);
+    });
+}
+
 int vx_matrix_free(vx_matrix_t* matrix) {
     return guard([&]() -> int {
         if (matrix == nullptr) return VX_OK;
@@ -533,7 +609,7 @@ static void destroy_plan(vx_plan* p) {
     delete p;
 }
 
-static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out) {
+static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, bool lut, vx_plan_t** out) {
     if (out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_plan is NULL");
     *out = nullptr;
     if (jobs == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "jobs is NULL");
@@ -553,17 +629,21 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
         if (m->device != di.device)
             VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].matrix lives on device %d, the current device is %d", i, m->device, di.device);
         if (u.staged == nullptr || u.out == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "jobs[%zu]: staged or out is NULL", i);
-        if (u.staged_len < staged_bytes(m->g.cols))
-            VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "jobs[%zu]: staged holds %zu bytes, %zu needed", i, u.staged_len, staged_bytes(m->g.cols));
+        const size_t need = lut ? compact_lut_bytes(m->g.cols) : staged_bytes(m->g.cols);
+        if (u.staged_len < need)
+            VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "jobs[%zu]: staged holds %zu bytes, %zu needed", i, u.staged_len, need);
+        if (lut && (reinterpret_cast<uintptr_t>(u.staged) & 15u) != 0)
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu]: the compact tables must be 16-byte aligned", i);
         if (u.out_capacity < m->g.rows)
             VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "jobs[%zu]: out holds %zu values but rows = %zu", i, u.out_capacity, m->g.rows);
         if (u.out_f32 != 0 && u.out_f32 != 1) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].out_f32 must be 0 or 1", i);
         if (u.out_f32 == 1 && u.act_scale_dev == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "jobs[%zu].act_scale_dev is NULL", i);
         Job& j = hj[i];
         j = Job{};
-        plan_job(j, m->g, 0);
+        if (lut) plan_lut_job(j, m->g, 0);
+        else plan_job(j, m->g, 0);
         j.w = m->d_w;
-        j.dsum = m->d_dsum;
+        j.dsum = lut ? nullptr : m->d_dsum;
         j.staged = static_cast<const uint8_t*>(u.staged);
         j.out = u.out;
         j.act_scale = u.act_scale_dev;
@@ -591,6 +671,7 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
     p->total_items = items;
     p->max_rows = 0;
     p->n_split = static_cast<uint32_t>(split.size());
+    p->lut = lut ? 1u : 0u;
     for (uint32_t i : split) p->max_rows = std::max(p->max_rows, hj[i].rows);
     hipError_t e = hipMalloc(&p->d_jobs, n_jobs * sizeof(Job));
     if (e == hipSuccess && part_ints) e = hipMalloc(&p->d_part, part_ints * sizeof(int32_t));
@@ -615,7 +696,11 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out
 extern "C" {
 
 int vx_plan_create(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan) {
-    return guard([&]() -> int { return create_plan(jobs, n_jobs, out_plan); });
+    return guard([&]() -> int { return create_plan(jobs, n_jobs, false, out_plan); });
+}
+
+int vx_lut_plan_create(const vx_gemv_job_t* jobs, size_t n_jobs, vx_plan_t** out_plan) {
+    return guard([&]() -> int { return create_plan(jobs, n_jobs, true, out_plan); });
 }
 
 int vx_plan_run(const vx_plan_t* plan, void* stream) {
@@ -635,6 +720,9 @@ int vx_plan_run(const vx_plan_t* plan, void* stream) {
         a.jobs = plan->d_jobs;
         a.n_jobs = plan->n_jobs;
         a.total_items = plan->total_items;
+        if (plan->lut)
+            return launch_gemv_lut(a, plan->max_rows, plan->d_split, plan->n_split, plan->num_cus,
+                                   static_cast<hipStream_t>(stream));
         return launch_gemv(a, plan->max_rows, plan->d_split, plan->n_split, plan->num_cus, static_cast<hipStream_t>(stream));
     });
 }

@@ -133,7 +133,7 @@ struct Job {
     uint32_t rows, padded_rows, n_tiles, n_chunks;
     uint32_t kslices, slice_chunks;  // K split: slices of slice_chunks chunks (the last may be shorter)
     uint32_t item_begin;             // first work item of this job in the launch
-    uint32_t pad;
+    uint32_t tbr;                    // tile row bytes: the byte-columns of a compact-table job's tables
     // A lone GEMV's K-slice sums by atomic addition: accum[padded_rows] and tickets[tile groups], both zero between
     // calls; the last slice of a tile group to arrive takes (and clears) the sums and writes the outputs, so no finish
     // kernel runs. Null in a plan.
@@ -181,6 +181,13 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
 constexpr size_t kNoAllocScratchBytes = VX_GEMM_NOALLOC_SCRATCH_BYTES;
 int launch_gemm_noalloc(const uint8_t* w, const Geometry& g, int device, int num_cus, const int8_t* x, size_t M,
                         size_t ldx, int32_t* y, size_t ldy, hipStream_t stream);
+// The GEMV through the compact activation tables (vx_lut.hip): a job's `staged` is the table of its cols
+// (compact_lut_bytes), dsum is unused; plan_lut_job sets the K split for the tables' LDS slices.
+size_t compact_lut_bytes(size_t cols);
+int launch_compact_lut(const int8_t* acts, size_t cols, int8_t* lut, hipStream_t stream);
+void plan_lut_job(Job& j, const Geometry& g, uint32_t target_items);
+int launch_gemv_lut(const LaunchArgs& a, uint32_t max_rows, const uint32_t* split, uint32_t n_split, int num_cus,
+                    hipStream_t stream);
 size_t find_invalid_byte(const uint8_t* planar, size_t n);
 void planar_to_device_layout(const uint8_t* planar, const Geometry& g, uint8_t* dst);
 
@@ -256,6 +263,7 @@ struct vx_plan {
     uint32_t* d_split;  // indices of the jobs split into K slices
     vx::Q2Job* d_q2jobs;  // Q2_0 plans: their job table (d_jobs unused)
     uint32_t n_jobs, total_items, max_rows, n_split;
+    uint32_t lut;  // the jobs read compact activation tables (vx_lut_plan_create)
 };
 
 constexpr uint32_t kPlanMagic = 0x56585031u;  // "VXP1"

@@ -101,6 +101,26 @@ class VelurexHipLayer:
                                               ctypes.c_float(act_scale), ctypes.c_void_p(out_dev.data_ptr()),
                                               out_dev.numel(), _stream_ptr(stream)))
 
+    def gemv_lut_i32(self, lut_dev, out_dev, stream=None) -> None:
+        """The int32 GEMV through compact activation tables (torch int8 tensor built by compact_lut_dev for this
+        layer's cols) -> int32 [rows]; the same results as gemv_i32 on the same activations."""
+        _lib.check(_lib.lib().vx_gemv_lut_i32_dev(self._h, ctypes.c_void_p(lut_dev.data_ptr()), lut_dev.numel(),
+                                                  ctypes.c_void_p(out_dev.data_ptr()), out_dev.numel(),
+                                                  _stream_ptr(stream)))
+
+    def gemv_lut_f32(self, lut_dev, act_scale: float, out_dev, stream=None) -> None:
+        _lib.check(_lib.lib().vx_gemv_lut_f32_dev(self._h, ctypes.c_void_p(lut_dev.data_ptr()), lut_dev.numel(),
+                                                  ctypes.c_float(act_scale), ctypes.c_void_p(out_dev.data_ptr()),
+                                                  out_dev.numel(), _stream_ptr(stream)))
+
+
+def compact_lut(acts_dev, cols: int, stream=None):
+    """The compact activation tables (vx_compact_lut_dev) of int8 device activations as a new int8 device tensor."""
+    import torch
+    lut = torch.empty(_lib.compact_lut_bytes(cols), dtype=torch.int8, device=acts_dev.device)
+    _lib.compact_lut_dev(acts_dev.data_ptr(), acts_dev.numel(), cols, lut.data_ptr(), lut.numel(), _stream_ptr(stream))
+    return lut
+
 
 def _stream_ptr(stream):
     if stream is None:
