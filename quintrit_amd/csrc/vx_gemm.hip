@@ -20,9 +20,11 @@
 //
 // Work split. A wave computes 64 weight rows (two 32-row blocks, one tile of the device layout) x T groups of 32
 // tokens over a range of K steps; the A fragments of a K step are decoded once and used for all T token groups. A
-// workgroup of 8 waves takes 8 consecutive tiles with the same tokens and K range, so the B fragments of a K step are
-// staged once per workgroup in LDS (double-buffered, the next step's loaded while this one is multiplied). Long K is
-// split into slices whose int32 partial sums a second kernel adds; the host picks T and the number of slices.
+// workgroup of W = 4 or 8 waves takes W consecutive tiles with the same tokens and K range, so the B fragments of a K
+// step are staged once per workgroup in LDS (double-buffered, the next step's loaded while this one is multiplied).
+// Long K is split into slices whose int32 partial sums a second kernel adds; the host picks T, W and the number of
+// slices (4-wave workgroups while the grid fits the CUs in one round: at M <= 128 and for the 3072-row shapes they are
+// 5-25 % faster than 8-wave ones; 23040 rows at M = 512 need the 8-wave form).
 #include "vx_internal.h"
 
 #include <algorithm>
@@ -50,7 +52,6 @@ __device__ __forceinline__ uint32_t d4_bytes(uint32_t w) {
 }
 
 constexpr uint32_t kStepChunks = 2;  // 16-byte chunks per K step
-constexpr int kGemmWaves = 8;        // waves (= 64-row tiles) per workgroup
 constexpr uint32_t kZeroWord = 0x7d7d7d7du;  // four bytes of five zero trits
 
 // ---- activation staging --------------------------------------------------------------------------------------------
@@ -149,86 +150,100 @@ __device__ __forceinline__ int plane4_sum(const GemmArgs& a, uint32_t m) {
     return s;
 }
 
-// Workgroup (rg, tt, kz): tiles 8 rg .. 8 rg + 7, token groups T tt .. T tt + T - 1, K steps of slice kz. LDS: the
-// trit table (32 copies of each entry in the first half of a 256-byte row; lane l reads copy l % 32, conflict-free
-// because LDS serves a wave in two 32-lane halves) and two buffers of one K step's B fragments.
-template <int T>
-__global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
+// Workgroup (rg, tt, kz): W waves, wave w taking the R 32-row blocks (W rg + w) R .. + R - 1 of the matrix (block 2 t + h
+// is half h of 64-row tile t), token groups T tt .. T tt + T - 1, K steps of slice kz. LDS: the trit table (32 copies
+// of each entry in the first half of a 256-byte row; lane l reads copy l % 32, conflict-free because LDS serves a wave
+// in two 32-lane halves) and two buffers of one K step's B fragments, which every wave reads (a B fragment serves the
+// wave's R blocks, an A fragment its T token groups).
+template <int T, int R, int W>
+__global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
     __shared__ uint32_t tab[256 * 64];
     __shared__ uint4 bs[2][5 * T * 64];
-    constexpr uint32_t kB = 5u * T * 64u;                             // B fragments of a K step
-    constexpr uint32_t kBPer = (kB + kGemmWaves * 64u - 1) / (kGemmWaves * 64u);  // per thread
+    constexpr uint32_t kNT = W * 64u;
+    constexpr uint32_t kB = 5u * T * 64u;                // B fragments of a K step
+    constexpr uint32_t kBPer = (kB + kNT - 1) / kNT;     // per thread
+    static_assert(kBPer <= 5, "at most five B fragments per thread and step");
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t tile = blockIdx.x * kGemmWaves + wave;
+    const uint32_t blk0 = (blockIdx.x * W + wave) * R;  // the wave's first 32-row block
+    const uint32_t n_blk = 2u * a.n_tiles;
     const uint32_t tt = blockIdx.y, kz = blockIdx.z;
     const uint32_t ks0 = kz * a.ksteps_per_slice;
     const uint32_t ks1 = min(ks0 + a.ksteps_per_slice, a.n_ksteps);
-    const bool active = tile < a.n_tiles;
 
-    for (uint32_t i = tid; i < 256u * 8u; i += kGemmWaves * 64u) {
+    for (uint32_t i = tid; i < 256u * 8u; i += kNT) {
         const uint32_t e = trits03(i >> 3);
         *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
     }
     const char* tabb = reinterpret_cast<const char*>(tab);
     const uint32_t lane_off = (lane & 31u) * 4u;
 
-    // This lane's row (i = lane % 32 of each 32-row block) in the device layout: tile t of group grp, row 16 bytes. A
-    // wave past the last tile reads the last tile (and stores nothing), so every load has a valid address and none
-    // sits behind a branch (the compiler would then wait for all loads before the next use).
-    const uint32_t ltile = min(tile, a.n_tiles - 1u);
-    const uint32_t grp = ltile / kTileGroup, tt16 = ltile - grp * kTileGroup;
-    const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup);
-    const uint8_t* wbase = a.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + tt16) * 1024u + (lane & 31u) * 16u;
+    // This lane's row (i = lane % 32) of each of the wave's blocks in the device layout: block 2 t + h is rows
+    // 32 h .. 32 h + 31 of tile t (16 bytes a row per chunk, the chunks of a tile T_g KiB apart in its tile group). A
+    // block past the matrix reads the last block (and stores nothing), so every load has a valid address and none sits
+    // behind a branch (the compiler would then wait for all loads before the next use).
+    const uint8_t* wbase[R];
+    uint32_t cstride[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t blk = min(blk0 + r, n_blk - 1u), tile = blk >> 1;
+        const uint32_t grp = tile / kTileGroup, t16 = tile - grp * kTileGroup;
+        const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup);
+        wbase[r] = a.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + t16) * 1024u + (blk & 1u) * 512u +
+                   (lane & 31u) * 16u;
+        cstride[r] = Tg * 1024u;
+    }
     const uint32_t half = lane >> 5;
 
     // Chunk 2 ks + s of the lane's rows; a chunk past the row (odd n_chunks) reads the last one and is replaced by
     // zero trits when it is decoded.
-    auto load_w = [&](uint32_t ks, u32x4g (&wv)[2]) __attribute__((always_inline)) {
+    auto load_w = [&](uint32_t ks, u32x4g (&wv)[R]) __attribute__((always_inline)) {
         const uint32_t q = min(ks * kStepChunks + half, a.n_chunks - 1u);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-            wv[rb] = __builtin_nontemporal_load((g_u4g*)(wbase + static_cast<size_t>(q) * Tg * 1024u + rb * 512u));
+        for (int r = 0; r < R; ++r)
+            wv[r] = __builtin_nontemporal_load((g_u4g*)(wbase[r] + static_cast<size_t>(q) * cstride[r]));
     };
-    // B fragments of step ks (kBPer <= 3 per thread, kept in named registers: an array here would be moved to
-    // scratch LDS and waited for at once); slots past the token groups read a valid fragment that no stored output
-    // depends on (only C columns of tokens >= M).
+    // B fragments of step ks (kBPer per thread, in named registers: an array here would be moved to scratch memory
+    // once the steps rotate through three sets); slots past the token groups read a valid fragment that no stored
+    // output depends on (only C columns of tokens >= M).
     auto b_index = [&](uint32_t ks, uint32_t k) -> size_t {
-        const uint32_t idx = min(tid + k * kGemmWaves * 64u, kB - 1u);
+        const uint32_t idx = min(tid + k * kNT, kB - 1u);
         const uint32_t kb = idx / (T * 64u), rem = idx - kb * T * 64u;
         const uint32_t tg = min(tt * T + rem / 64u, a.n_tg - 1u);
         return (static_cast<size_t>(ks * 5u + kb) * a.n_tg + tg) * 64u + (rem & 63u);
     };
-    // B fragments of a step in named registers (three per thread at most: an array or a struct here ends up in
-    // scratch memory once the steps rotate through three sets)
-#define VX_LOAD_B(ks, r0, r1, r2)                            \
-    do {                                                     \
-        r0 = a.xs[b_index((ks), 0)];                         \
-        if (kBPer > 1) r1 = a.xs[b_index((ks), 1)];          \
-        if (kBPer > 2) r2 = a.xs[b_index((ks), 2)];          \
+#define VX_LOAD_B(ks, r0, r1, r2, r3, r4)                   \
+    do {                                                    \
+        r0 = a.xs[b_index((ks), 0)];                        \
+        if (kBPer > 1) r1 = a.xs[b_index((ks), 1)];         \
+        if (kBPer > 2) r2 = a.xs[b_index((ks), 2)];         \
+        if (kBPer > 3) r3 = a.xs[b_index((ks), 3)];         \
+        if (kBPer > 4) r4 = a.xs[b_index((ks), 4)];         \
     } while (0)
-#define VX_STORE_B(buf, r0, r1, r2)                                                           \
-    do {                                                                                      \
-        if (tid < kB) bs[(buf)][tid] = r0;                                                    \
-        if (kBPer > 1 && tid + kGemmWaves * 64u < kB) bs[(buf)][tid + kGemmWaves * 64u] = r1; \
-        if (kBPer > 2 && tid + 2u * kGemmWaves * 64u < kB) bs[(buf)][tid + 2u * kGemmWaves * 64u] = r2; \
+#define VX_STORE_B(buf, r0, r1, r2, r3, r4)                                             \
+    do {                                                                                \
+        if (tid < kB) bs[(buf)][tid] = r0;                                              \
+        if (kBPer > 1 && tid + kNT < kB) bs[(buf)][tid + kNT] = r1;                     \
+        if (kBPer > 2 && tid + 2u * kNT < kB) bs[(buf)][tid + 2u * kNT] = r2;           \
+        if (kBPer > 3 && tid + 3u * kNT < kB) bs[(buf)][tid + 3u * kNT] = r3;           \
+        if (kBPer > 4 && tid + 4u * kNT < kB) bs[(buf)][tid + 4u * kNT] = r4;           \
     } while (0)
 
-    v16i acc[2][T];
+    v16i acc[R][T];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int g = 0; g < T; ++g) acc[rb][g] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+        for (int g = 0; g < T; ++g) acc[r][g] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 
     // The products of step ks: weights wc, B fragments from bs[buf].
-    auto multiply = [&](uint32_t ks, const u32x4g (&wc)[2], uint32_t buf) __attribute__((always_inline)) {
+    auto multiply = [&](uint32_t ks, const u32x4g (&wc)[R], uint32_t buf) __attribute__((always_inline)) {
         const bool inside = ks * kStepChunks + half < a.n_chunks;
-        v4i A[2][5];
+        v4i A[R][5];
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
-            const uint32_t dw[4] = {inside ? wc[rb].x : kZeroWord, inside ? wc[rb].y : kZeroWord,
-                                    inside ? wc[rb].z : kZeroWord, inside ? wc[rb].w : kZeroWord};
+        for (int r = 0; r < R; ++r) {
+            const uint32_t dw[4] = {inside ? wc[r].x : kZeroWord, inside ? wc[r].y : kZeroWord,
+                                    inside ? wc[r].z : kZeroWord, inside ? wc[r].w : kZeroWord};
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 int t[4];
@@ -237,20 +252,20 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
                     const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + b) << 8));
                     t[b] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
                 }
-                A[rb][m] = v4i{t[0], t[1], t[2], t[3]};
+                A[r][m] = v4i{t[0], t[1], t[2], t[3]};
             }
-            A[rb][4] = v4i{static_cast<int>(d4_bytes(dw[0])), static_cast<int>(d4_bytes(dw[1])),
-                           static_cast<int>(d4_bytes(dw[2])), static_cast<int>(d4_bytes(dw[3]))};
+            A[r][4] = v4i{static_cast<int>(d4_bytes(dw[0])), static_cast<int>(d4_bytes(dw[1])),
+                          static_cast<int>(d4_bytes(dw[2])), static_cast<int>(d4_bytes(dw[3]))};
         }
-        // K block outer, token group inner: 2 T independent accumulators between two MFMAs on the same one.
+        // K block outer, token group, then block: R T independent accumulators between two MFMAs on the same one.
 #pragma unroll
         for (int kb = 0; kb < 5; ++kb) {
 #pragma unroll
             for (int g = 0; g < T; ++g) {
                 const uint4 b = bs[buf][(kb * T + g) * 64u + lane];
                 const v4i B = v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
-                acc[0][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0][kb], B, acc[0][g], 0, 0, 0);
-                acc[1][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1][kb], B, acc[1][g], 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[r][kb], B, acc[r][g], 0, 0, 0);
             }
         }
     };
@@ -261,32 +276,33 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
     // unrolled loop, so no loaded register is ever copied (a copy would wait for its load). Every load is unconditional
     // (indices clamp at the last step) and the steps past the slice's end only skip the multiply, so the compiler's
     // waits stay exact.
-    u32x4g w0[2], w1[2], w2[2];
-    uint4 b00, b01, b02, b10, b11, b12, b20, b21, b22;
+    u32x4g w0[R], w1[R], w2[R];
+    uint4 b00, b01, b02, b03, b04, b10, b11, b12, b13, b14, b20, b21, b22, b23, b24;
     const uint32_t last = ks1 > ks0 ? ks1 - 1u : ks0;
-    VX_LOAD_B(ks0, b00, b01, b02);
+    VX_LOAD_B(ks0, b00, b01, b02, b03, b04);
     load_w(ks0, w0);
-    VX_LOAD_B(min(ks0 + 1u, last), b10, b11, b12);
+    VX_LOAD_B(min(ks0 + 1u, last), b10, b11, b12, b13, b14);
     load_w(min(ks0 + 1u, last), w1);
-    VX_STORE_B(0, b00, b01, b02);
-#define VX_STEP(ks, WC, N0, N1, N2, M0, M1, M2, WN)                      \
+    VX_STORE_B(0, b00, b01, b02, b03, b04);
+    const bool active = blk0 < n_blk;
+#define VX_STEP(ks, WC, N0, N1, N2, N3, N4, M0, M1, M2, M3, M4, WN)      \
     do {                                                                 \
-        VX_LOAD_B(min((ks) + 2u, last), M0, M1, M2);                     \
+        VX_LOAD_B(min((ks) + 2u, last), M0, M1, M2, M3, M4);             \
         load_w(min((ks) + 2u, last), WN);                                \
         __syncthreads();                                                 \
         if (active && (ks) < ks1) multiply((ks), WC, ((ks) - ks0) & 1u); \
-        VX_STORE_B((((ks) - ks0) & 1u) ^ 1u, N0, N1, N2);                \
+        VX_STORE_B((((ks) - ks0) & 1u) ^ 1u, N0, N1, N2, N3, N4);        \
     } while (0)
     for (uint32_t ks = ks0; ks < ks1; ks += 3u) {
-        VX_STEP(ks, w0, b10, b11, b12, b20, b21, b22, w2);
-        VX_STEP(ks + 1u, w1, b20, b21, b22, b00, b01, b02, w0);
-        VX_STEP(ks + 2u, w2, b00, b01, b02, b10, b11, b12, w1);
+        VX_STEP(ks, w0, b10, b11, b12, b13, b14, b20, b21, b22, b23, b24, w2);
+        VX_STEP(ks + 1u, w1, b20, b21, b22, b23, b24, b00, b01, b02, b03, b04, w0);
+        VX_STEP(ks + 2u, w2, b00, b01, b02, b03, b04, b10, b11, b12, b13, b14, w1);
     }
 #undef VX_STEP
 #undef VX_LOAD_B
 #undef VX_STORE_B
     if (!active) return;
-    // C of block (rb, g): lane l, register r -> weight row 8 (r / 4) + 4 (l / 32) + r % 4 of the block, token l % 32.
+    // C of (block, token group g): lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4 of the block, token l % 32.
     const uint32_t j = lane & 31u;
 #pragma unroll
     for (int g = 0; g < T; ++g) {
@@ -294,12 +310,13 @@ __global__ __launch_bounds__(kGemmWaves * 64) void gemm_kernel(GemmArgs a) {
         if (m >= a.M) continue;
         const int corr = a.kslices == 1 ? plane4_sum(a, m) : 0;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+        for (int r = 0; r < R; ++r) {
+            if (blk0 + r >= n_blk) continue;
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const uint32_t n = tile * 64u + rb * 32u + 8u * r4 + 4u * half;
-                const int v0 = acc[rb][g][4 * r4] - corr, v1 = acc[rb][g][4 * r4 + 1] - corr;
-                const int v2 = acc[rb][g][4 * r4 + 2] - corr, v3 = acc[rb][g][4 * r4 + 3] - corr;
+                const uint32_t n = (blk0 + r) * 32u + 8u * r4 + 4u * half;
+                const int v0 = acc[r][g][4 * r4] - corr, v1 = acc[r][g][4 * r4 + 1] - corr;
+                const int v2 = acc[r][g][4 * r4 + 2] - corr, v3 = acc[r][g][4 * r4 + 3] - corr;
                 if (a.kslices > 1) {
                     *reinterpret_cast<int4*>(a.part + (static_cast<size_t>(kz) * a.n_tg * 32u + m) * a.rows_p + n) =
                         make_int4(v0, v1, v2, v3);
@@ -337,7 +354,7 @@ __global__ __launch_bounds__(256) void gemm_finish_kernel(GemmArgs a) {
 // ---- host side ---------------------------------------------------------------------------------------------------------
 
 struct GemmPlan {
-    uint32_t n_ksteps, n_tg, T, n_tt, grid_x, kslices, ksteps_per_slice, stage_x;
+    uint32_t n_ksteps, n_tg, T, R, W, n_tt, grid_x, kslices, ksteps_per_slice, stage_x;
     size_t xs_bytes, s4_bytes, part_bytes;
 };
 
@@ -351,10 +368,17 @@ static GemmPlan gemm_plan(const Geometry& g, size_t M, int num_cus) {
     p.n_tg = static_cast<uint32_t>((M + 31) / 32);
     p.T = p.n_tg >= 4 ? 4u : (p.n_tg >= 2 ? 2u : 1u);
     p.n_tt = (p.n_tg + p.T - 1) / p.T;
-    p.grid_x = static_cast<uint32_t>((g.n_tiles + kGemmWaves - 1) / kGemmWaves);
+    // Two 32-row blocks per wave; 4-wave workgroups while they fit the CUs in one round without a K split (more,
+    // smaller workgroups spread a narrow grid over more CUs), else 8-wave workgroups (the B fragments of a step serve
+    // twice the rows).
+    p.R = 2;
+    const uint64_t blocks = 2 * g.n_tiles;
+    p.W = (blocks + 7) / 8 * p.n_tt <= static_cast<uint64_t>(std::max(num_cus, 1)) ? 4u : 8u;
+    p.grid_x = static_cast<uint32_t>((blocks + p.R * p.W - 1) / (p.R * p.W));
     const uint64_t base = static_cast<uint64_t>(p.grid_x) * p.n_tt;
     const uint64_t slots = static_cast<uint64_t>(std::max(num_cus, 1)) * (p.T == 1 ? 2u : 1u);  // workgroups per CU (LDS)
-    const double t_step = std::max(0.29e-6 * p.T, 1.0e-6);
+    // a K step of a wave is 10 T MFMAs (32 cycles each, W / 4 waves per SIMD), but not less than the HBM latency
+    const double t_step = std::max(0.29e-6 * p.T * p.W / 8.0, 1.0e-6);
     double best = 1e30;
     uint32_t best_ks = 1;
     for (uint32_t ks = 1; ks <= std::min<uint32_t>(p.n_ksteps, 64u); ++ks) {
@@ -428,9 +452,16 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
     a.ksteps_per_slice = p.ksteps_per_slice;
     a.rows_p = static_cast<uint32_t>(g.padded_rows);
     const dim3 grid(p.grid_x, p.n_tt, p.kslices);
-    if (p.T == 4) hipLaunchKernelGGL(gemm_kernel<4>, grid, dim3(kGemmWaves * 64), 0, stream, a);
-    else if (p.T == 2) hipLaunchKernelGGL(gemm_kernel<2>, grid, dim3(kGemmWaves * 64), 0, stream, a);
-    else hipLaunchKernelGGL(gemm_kernel<1>, grid, dim3(kGemmWaves * 64), 0, stream, a);
+    const dim3 block(p.W * 64);
+    if (p.W == 8) {
+        if (p.T == 4) hipLaunchKernelGGL((gemm_kernel<4, 2, 8>), grid, block, 0, stream, a);
+        else if (p.T == 2) hipLaunchKernelGGL((gemm_kernel<2, 2, 8>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_kernel<1, 2, 8>), grid, block, 0, stream, a);
+    } else {
+        if (p.T == 4) hipLaunchKernelGGL((gemm_kernel<4, 2, 4>), grid, block, 0, stream, a);
+        else if (p.T == 2) hipLaunchKernelGGL((gemm_kernel<2, 2, 4>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_kernel<1, 2, 4>), grid, block, 0, stream, a);
+    }
     VX_HIP(hipGetLastError());
     if (p.kslices > 1) {
         hipLaunchKernelGGL(gemm_finish_kernel, dim3((a.rows + 255u) / 256u, static_cast<uint32_t>(M)), dim3(256), 0, stream, a);
