@@ -14,9 +14,9 @@
 // K order. A K step is two 16-byte chunks of a weight row: 32 byte-columns x 5 planes = 160 trits = five 32-deep MFMA
 // blocks. Lane (i, s) (i = row in the 32-row block, s = lane / 32) holds chunk 2 ks + s of its row in one 16-byte load.
 // Block m < 4 takes dword m of that chunk: bytes 4m .. 4m+3, planes 0..3 (t0..t3 as int8, one LDS table lookup per
-// byte). Block 4 takes plane 4 of all 16 bytes: d4 = t4 + 1 from byte-wise compares (B >= 84, B >= 168), and the missing
-// "- 1" is subtracted once per token as the sum of that token's plane-4 activations. The activation staging writes X
-// in exactly this order, so A and B pair every weight with its activation.
+// byte). Block 4 takes plane 4 of all 16 bytes: t4 = floor(B / 84) - 1 per byte from carry-free byte arithmetic
+// (t4_bytes). The activation staging writes X in exactly this order, so A and B pair every weight with its
+// activation.
 //
 // Work split. A wave computes 64 weight rows (two 32-row blocks, one tile of the device layout) x T groups of 32
 // tokens over a range of K steps; the A fragments of a K step are decoded once and used for all T token groups. A
@@ -25,6 +25,7 @@
 // Long K is split into slices whose int32 partial sums a second kernel adds; the host picks T, W and the number of
 // slices (4-wave workgroups while the grid fits the CUs in one round: at M <= 128 and for the 3072-row shapes they are
 // 5-25 % faster than 8-wave ones; 23040 rows at M = 512 need the 8-wave form).
+#include "vx_gemv_core.h"
 #include "vx_internal.h"
 
 #include <algorithm>
@@ -45,12 +46,6 @@ __device__ inline uint32_t trits03(uint32_t b) {
     return ((d0 - 1u) & 0xffu) | (((d1 - 1u) & 0xffu) << 8) | (((d2 - 1u) & 0xffu) << 16) | (((d3 - 1u) & 0xffu) << 24);
 }
 
-// d4 = floor(B / 84) of each byte of w, as bytes (B >= 84 and B >= 168 tested with 7-bit adds that cannot carry).
-__device__ __forceinline__ uint32_t d4_bytes(uint32_t w) {
-    const uint32_t x = (w >> 1) & 0x7f7f7f7fu;
-    return (((x + 0x56565656u) >> 7) & 0x01010101u) + (((x + 0x2c2c2c2cu) >> 7) & 0x01010101u);
-}
-
 constexpr uint32_t kStepChunks = 2;  // 16-byte chunks per K step
 constexpr uint32_t kZeroWord = 0x7d7d7d7du;  // four bytes of five zero trits
 
@@ -63,9 +58,9 @@ constexpr uint32_t kZeroWord = 0x7d7d7d7du;  // four bytes of five zero trits
 // 16 hs + 4 kb + d, its activations of planes 0..3, a(160 ks + 32 e + 16 hs + 4 kb + d), e = 0..3: dword kb of the
 // four 16-byte loads at 160 ks + 32 e + 16 hs, transposed 4 x 4 bytes with v_perm; K block 4 takes plane 4 of the 16
 // byte-columns, the 16 bytes at 160 ks + 128 + 16 hs as they are. The packed tail and unaligned rows take the
-// per-byte gather. A workgroup covers kStagePairs pairs of one token and writes its part of the token's plane-4 sum
-// (the correction for d4 = t4 + 1) to s4p[blockIdx.y * M + m]; the GEMM adds the parts.
-constexpr uint32_t kStagePairs = 256;
+// per-byte gather. Workgroup (pair block, token group): lane j of each 32-thread row is token 32 tg + j and the rows are
+// kStageRows consecutive pairs, so the 32 tokens of a row write one contiguous 512-byte run per K block.
+constexpr uint32_t kStageRows = 8;  // pairs per staging workgroup (256 threads)
 
 // Activation p of device byte-column c of a row (column_activation_index, pack.rs:230-237), 0 outside.
 __device__ __forceinline__ int act_of(const int8_t* __restrict__ xr, uint32_t cols, uint32_t tbr, uint32_t c, uint32_t p) {
@@ -77,58 +72,48 @@ __device__ __forceinline__ int act_of(const int8_t* __restrict__ xr, uint32_t co
 
 __global__ __launch_bounds__(256) void gemm_stage_kernel(const int8_t* __restrict__ x, uint32_t ldx, uint32_t n_tg,
                                                          uint32_t cols, uint32_t tbr, uint32_t n_ksteps,
-                                                         uint4* __restrict__ xs, int* __restrict__ s4p, uint32_t M) {
-    __shared__ int red[4];
-    const uint32_t m = blockIdx.x, tid = threadIdx.x;
-    const uint32_t pair = blockIdx.y * kStagePairs + tid, ks = pair >> 1, hs = pair & 1u;
+                                                         uint4* __restrict__ xs, uint32_t M) {
+    const uint32_t tid = threadIdx.x, j = tid & 31u;
+    const uint32_t pair = blockIdx.x * kStageRows + (tid >> 5), ks = pair >> 1, hs = pair & 1u;
+    const uint32_t tg = blockIdx.y, m = tg * 32u + j;
+    // B fragments of tokens past M (the rest of the last 32-token group) are left as they are: they only reach C
+    // columns that are never stored.
+    if (ks >= n_ksteps || m >= M) return;
     const int8_t* xr = x + static_cast<size_t>(m) * ldx;
-    int s4 = 0;
-    if (ks < n_ksteps) {
-        uint4 o[5];
-        if (ks < cols / 160u && (reinterpret_cast<uintptr_t>(xr) & 15u) == 0) {
-            const int8_t* blk = xr + ks * 160u + 16u * hs;
-            uint4 X[5];
+    uint4 o[5];
+    if (ks < cols / 160u && (reinterpret_cast<uintptr_t>(xr) & 15u) == 0) {
+        const int8_t* blk = xr + ks * 160u + 16u * hs;
+        uint4 X[5];
 #pragma unroll
-            for (int e = 0; e < 5; ++e) X[e] = *reinterpret_cast<const uint4*>(blk + 32 * e);
+        for (int e = 0; e < 5; ++e) X[e] = *reinterpret_cast<const uint4*>(blk + 32 * e);
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
-                auto dw = [&](const uint4& v) { return kb == 0 ? v.x : (kb == 1 ? v.y : (kb == 2 ? v.z : v.w)); };
-                const uint32_t a0 = dw(X[0]), a1 = dw(X[1]), a2 = dw(X[2]), a3 = dw(X[3]);
-                const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u), hi01 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
-                const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u), hi23 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
-                o[kb] = make_uint4(__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
-                                   __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u));
-            }
-            o[4] = X[4];
-            s4 = __builtin_amdgcn_sdot4(static_cast<int>(X[4].x), 0x01010101, 0, false) +
-                 __builtin_amdgcn_sdot4(static_cast<int>(X[4].y), 0x01010101, 0, false) +
-                 __builtin_amdgcn_sdot4(static_cast<int>(X[4].z), 0x01010101, 0, false) +
-                 __builtin_amdgcn_sdot4(static_cast<int>(X[4].w), 0x01010101, 0, false);
-        } else {
-            const uint32_t cb = (ks * kStepChunks + hs) * 16u;  // first byte-column of the chunk
-#pragma unroll
-            for (uint32_t kb = 0; kb < 5; ++kb) {
-                uint32_t w[4];
-                for (uint32_t d = 0; d < 4; ++d) {
-                    uint32_t v = 0;
-                    for (uint32_t e = 0; e < 4; ++e) {
-                        const int a = kb < 4 ? act_of(xr, cols, tbr, cb + 4u * kb + d, e) : act_of(xr, cols, tbr, cb + 4u * d + e, 4);
-                        if (kb == 4) s4 += a;
-                        v |= (static_cast<uint32_t>(a) & 0xffu) << (8 * e);
-                    }
-                    w[d] = v;
-                }
-                o[kb] = make_uint4(w[0], w[1], w[2], w[3]);
-            }
+        for (int kb = 0; kb < 4; ++kb) {
+            auto dw = [&](const uint4& v) { return kb == 0 ? v.x : (kb == 1 ? v.y : (kb == 2 ? v.z : v.w)); };
+            const uint32_t a0 = dw(X[0]), a1 = dw(X[1]), a2 = dw(X[2]), a3 = dw(X[3]);
+            const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u), hi01 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+            const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u), hi23 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+            o[kb] = make_uint4(__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                               __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u));
         }
-        const uint32_t tg = m / 32u, lane0 = m % 32u + 32u * hs;
+        o[4] = X[4];
+    } else {
+        const uint32_t cb = (ks * kStepChunks + hs) * 16u;  // first byte-column of the chunk
 #pragma unroll
-        for (uint32_t kb = 0; kb < 5; ++kb) xs[(static_cast<size_t>(ks * 5u + kb) * n_tg + tg) * 64u + lane0] = o[kb];
+        for (uint32_t kb = 0; kb < 5; ++kb) {
+            uint32_t w[4];
+            for (uint32_t d = 0; d < 4; ++d) {
+                uint32_t v = 0;
+                for (uint32_t e = 0; e < 4; ++e) {
+                    const int a = kb < 4 ? act_of(xr, cols, tbr, cb + 4u * kb + d, e) : act_of(xr, cols, tbr, cb + 4u * d + e, 4);
+                    v |= (static_cast<uint32_t>(a) & 0xffu) << (8 * e);
+                }
+                w[d] = v;
+            }
+            o[kb] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
     }
-    for (int off = 32; off > 0; off >>= 1) s4 += __shfl_xor(s4, off);
-    if ((tid & 63u) == 0) red[tid >> 6] = s4;
-    __syncthreads();
-    if (tid == 0) s4p[static_cast<size_t>(blockIdx.y) * M + m] = red[0] + red[1] + red[2] + red[3];
+#pragma unroll
+    for (uint32_t kb = 0; kb < 5; ++kb) xs[(static_cast<size_t>(ks * 5u + kb) * n_tg + tg) * 64u + j + 32u * hs] = o[kb];
 }
 
 // ---- GEMM -------------------------------------------------------------------------------------------------------------
@@ -136,19 +121,12 @@ __global__ __launch_bounds__(256) void gemm_stage_kernel(const int8_t* __restric
 struct GemmArgs {
     const uint8_t* w;      // device layout
     const uint4* xs;       // staged activations
-    const int* s4p;        // per staging workgroup and token: parts of the plane-4 sums, s4p[kx * M + m]
     int32_t* y;            // M x ldy (kslices == 1)
     int32_t* part;         // kslices x (n_tg * 32) x rows_p partial sums (kslices > 1)
     uint32_t rows, n_tiles, n_chunks, n_ksteps;
     uint32_t M, n_tg, ldy, y_vec4;   // y_vec4: y and ldy allow 16-byte stores
-    uint32_t kslices, ksteps_per_slice, rows_p, s4_parts;  // s4_parts: staging workgroups per token
+    uint32_t kslices, ksteps_per_slice, rows_p;
 };
-
-__device__ __forceinline__ int plane4_sum(const GemmArgs& a, uint32_t m) {
-    int s = 0;
-    for (uint32_t k = 0; k < a.s4_parts; ++k) s += a.s4p[static_cast<size_t>(k) * a.M + m];
-    return s;
-}
 
 // Workgroup (rg, tt, kz): W waves, wave w taking the R 32-row blocks (W rg + w) R .. + R - 1 of the matrix (block 2 t + h
 // is half h of 64-row tile t), token groups T tt .. T tt + T - 1, K steps of slice kz. LDS: the trit table (32 copies
@@ -254,8 +232,8 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
                 }
                 A[r][m] = v4i{t[0], t[1], t[2], t[3]};
             }
-            A[r][4] = v4i{static_cast<int>(d4_bytes(dw[0])), static_cast<int>(d4_bytes(dw[1])),
-                          static_cast<int>(d4_bytes(dw[2])), static_cast<int>(d4_bytes(dw[3]))};
+            A[r][4] = v4i{static_cast<int>(t4_bytes(dw[0])), static_cast<int>(t4_bytes(dw[1])),
+                          static_cast<int>(t4_bytes(dw[2])), static_cast<int>(t4_bytes(dw[3]))};
         }
         // K block outer, token group, then block: R T independent accumulators between two MFMAs on the same one.
 #pragma unroll
@@ -308,15 +286,14 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
     for (int g = 0; g < T; ++g) {
         const uint32_t m = (tt * T + g) * 32u + j;
         if (m >= a.M) continue;
-        const int corr = a.kslices == 1 ? plane4_sum(a, m) : 0;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             if (blk0 + r >= n_blk) continue;
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
                 const uint32_t n = (blk0 + r) * 32u + 8u * r4 + 4u * half;
-                const int v0 = acc[r][g][4 * r4] - corr, v1 = acc[r][g][4 * r4 + 1] - corr;
-                const int v2 = acc[r][g][4 * r4 + 2] - corr, v3 = acc[r][g][4 * r4 + 3] - corr;
+                const int v0 = acc[r][g][4 * r4], v1 = acc[r][g][4 * r4 + 1];
+                const int v2 = acc[r][g][4 * r4 + 2], v3 = acc[r][g][4 * r4 + 3];
                 if (a.kslices > 1) {
                     *reinterpret_cast<int4*>(a.part + (static_cast<size_t>(kz) * a.n_tg * 32u + m) * a.rows_p + n) =
                         make_int4(v0, v1, v2, v3);
@@ -339,7 +316,7 @@ __global__ __launch_bounds__(256) void gemm_finish_kernel(GemmArgs a) {
     if (n >= a.rows) return;
     const size_t stride = static_cast<size_t>(a.n_tg) * 32u * a.rows_p;
     const int32_t* p = a.part + static_cast<size_t>(m) * a.rows_p + n;
-    int s0 = -plane4_sum(a, m), s1 = 0, s2 = 0, s3 = 0;
+    int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
     uint32_t k = 0;
     for (; k + 4 <= a.kslices; k += 4) {
         s0 += p[k * stride];
@@ -354,8 +331,8 @@ __global__ __launch_bounds__(256) void gemm_finish_kernel(GemmArgs a) {
 // ---- host side ---------------------------------------------------------------------------------------------------------
 
 struct GemmPlan {
-    uint32_t n_ksteps, n_tg, T, R, W, n_tt, grid_x, kslices, ksteps_per_slice, stage_x;
-    size_t xs_bytes, s4_bytes, part_bytes;
+    uint32_t n_ksteps, n_tg, T, R, W, n_tt, grid_x, kslices, ksteps_per_slice;
+    size_t xs_bytes, part_bytes;
 };
 
 // T (token groups per wave) from M; then the K split that minimises an estimate of the time: rounds of workgroups
@@ -396,20 +373,18 @@ static GemmPlan gemm_plan(const Geometry& g, size_t M, int num_cus) {
     p.ksteps_per_slice = (p.n_ksteps + best_ks - 1) / best_ks;
     p.kslices = (p.n_ksteps + p.ksteps_per_slice - 1) / p.ksteps_per_slice;
     p.xs_bytes = round_up(static_cast<size_t>(p.n_ksteps) * 5u * p.n_tg * 1024u, 256);
-    p.stage_x = (2u * p.n_ksteps + kStagePairs - 1) / kStagePairs;
-    p.s4_bytes = round_up(static_cast<size_t>(p.stage_x) * M * 4u, 256);
     p.part_bytes = p.kslices > 1 ? static_cast<size_t>(p.kslices) * p.n_tg * 32u * g.padded_rows * 4u : 0;
     return p;
 }
 
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus) {
     const GemmPlan p = gemm_plan(g, M, num_cus);
-    return p.xs_bytes + p.s4_bytes + p.part_bytes;
+    return p.xs_bytes + p.part_bytes;
 }
 
 size_t gemm_stage_bytes(size_t cols, size_t M) {
     const GemmPlan p = gemm_plan(geometry(1, cols), M, 1);  // the staged activations depend on cols and M only
-    return p.xs_bytes + p.s4_bytes;
+    return p.xs_bytes;
 }
 
 size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus) { return gemm_plan(g, M, num_cus).part_bytes; }
@@ -418,12 +393,10 @@ size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus) { return gemm_p
 // activations of one call serve every matrix with cols columns.
 int launch_gemm_stage(const int8_t* x, size_t M, size_t ldx, size_t cols, uint8_t* ws, hipStream_t stream) {
     const GemmPlan p = gemm_plan(geometry(1, cols), M, 1);
-    // B fragments of tokens past M (the rest of the last 32-token group) are left as they are: they only reach C
-    // columns that are never stored.
-    hipLaunchKernelGGL(gemm_stage_kernel, dim3(static_cast<uint32_t>(M), p.stage_x), dim3(256), 0, stream, x,
-                       static_cast<uint32_t>(ldx), p.n_tg, static_cast<uint32_t>(cols),
-                       static_cast<uint32_t>(tile_row_bytes(cols)), p.n_ksteps, reinterpret_cast<uint4*>(ws),
-                       reinterpret_cast<int*>(ws + p.xs_bytes), static_cast<uint32_t>(M));
+    const dim3 grid((2u * p.n_ksteps + kStageRows - 1) / kStageRows, p.n_tg);
+    hipLaunchKernelGGL(gemm_stage_kernel, grid, dim3(256), 0, stream, x, static_cast<uint32_t>(ldx), p.n_tg,
+                       static_cast<uint32_t>(cols), static_cast<uint32_t>(tile_row_bytes(cols)), p.n_ksteps,
+                       reinterpret_cast<uint4*>(ws), static_cast<uint32_t>(M));
     VX_HIP(hipGetLastError());
     return VX_OK;
 }
@@ -436,8 +409,6 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
     GemmArgs a{};
     a.w = w;
     a.xs = reinterpret_cast<const uint4*>(staged);
-    a.s4p = reinterpret_cast<const int*>(staged + p.xs_bytes);
-    a.s4_parts = p.stage_x;
     a.y = y;
     a.part = p.kslices > 1 ? reinterpret_cast<int32_t*>(part) : nullptr;
     a.rows = static_cast<uint32_t>(g.rows);
