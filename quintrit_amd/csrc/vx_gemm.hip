@@ -38,13 +38,9 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4g __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) const u32x4g g_u4g;
 
-// t0..t3 of byte B as int8 in a dword; non-values give zero trits (pack.rs:41-58).
-__device__ inline uint32_t trits03(uint32_t b) {
-    const uint32_t u = b / 28u, l = b - 28u * u;
-    if (b > 250u || l > 26u) return 0u;
-    const uint32_t d0 = l % 3u, d1 = l / 3u % 3u, d2 = l / 9u, d3 = u % 3u;
-    return ((d0 - 1u) & 0xffu) | (((d1 - 1u) & 0xffu) << 8) | (((d2 - 1u) & 0xffu) << 16) | (((d3 - 1u) & 0xffu) << 24);
-}
+// t0..t3 of every byte as int8 in a dword (trits03_word: non-values give zero trits, pack.rs:41-58), built at compile
+// time; a workgroup copies it into its LDS table with loads.
+__constant__ TritTable g_gemm_trits = make_trit_table();
 
 constexpr uint32_t kStepChunks = 2;  // 16-byte chunks per K step
 constexpr uint32_t kZeroWord = 0x7d7d7d7du;  // four bytes of five zero trits
@@ -62,16 +58,8 @@ constexpr uint32_t kZeroWord = 0x7d7d7d7du;  // four bytes of five zero trits
 // kStageRows consecutive pairs, so the 32 tokens of a row write one contiguous 512-byte run per K block.
 constexpr uint32_t kStageRows = 8;  // pairs per staging workgroup (256 threads)
 
-// Activation p of device byte-column c of a row (column_activation_index, pack.rs:230-237), 0 outside.
-__device__ __forceinline__ int act_of(const int8_t* __restrict__ xr, uint32_t cols, uint32_t tbr, uint32_t c, uint32_t p) {
-    if (c >= tbr) return 0;
-    const uint32_t full = cols / 160u * 32u;
-    const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
-    return idx < cols ? xr[idx] : 0;
-}
-
 __global__ __launch_bounds__(256) void gemm_stage_kernel(const int8_t* __restrict__ x, uint32_t ldx, uint32_t n_tg,
-                                                         uint32_t cols, uint32_t tbr, uint32_t n_ksteps,
+                                                         uint32_t cols, uint32_t n_ksteps,
                                                          uint4* __restrict__ xs, uint32_t M) {
     const uint32_t tid = threadIdx.x, j = tid & 31u;
     const uint32_t pair = blockIdx.x * kStageRows + (tid >> 5), ks = pair >> 1, hs = pair & 1u;
@@ -97,16 +85,22 @@ __global__ __launch_bounds__(256) void gemm_stage_kernel(const int8_t* __restric
         }
         o[4] = X[4];
     } else {
-        const uint32_t cb = (ks * kStepChunks + hs) * 16u;  // first byte-column of the chunk
+        // byte-column 16 hs + k of the step (k < 16), activation p: in a whole block 160 ks + 32 p + 16 hs + k, in the
+        // packed tail 160 ks + 5 (16 hs + k) + p (column_activation_index); past the row (and in the tail's padding
+        // columns, whose indices are all >= cols) zero
+        const bool tail = ks >= cols / 160u;
+        auto act = [&](uint32_t k, uint32_t p) -> uint32_t {
+            const uint32_t idx = tail ? ks * 160u + 5u * (16u * hs + k) + p : ks * 160u + 32u * p + 16u * hs + k;
+            return idx < cols ? static_cast<uint32_t>(static_cast<uint8_t>(xr[idx])) : 0u;
+        };
 #pragma unroll
         for (uint32_t kb = 0; kb < 5; ++kb) {
             uint32_t w[4];
+#pragma unroll
             for (uint32_t d = 0; d < 4; ++d) {
                 uint32_t v = 0;
-                for (uint32_t e = 0; e < 4; ++e) {
-                    const int a = kb < 4 ? act_of(xr, cols, tbr, cb + 4u * kb + d, e) : act_of(xr, cols, tbr, cb + 4u * d + e, 4);
-                    v |= (static_cast<uint32_t>(a) & 0xffu) << (8 * e);
-                }
+#pragma unroll
+                for (uint32_t e = 0; e < 4; ++e) v |= (kb < 4 ? act(4u * kb + d, e) : act(4u * d + e, 4u)) << (8 * e);
                 w[d] = v;
             }
             o[kb] = make_uint4(w[0], w[1], w[2], w[3]);
@@ -151,7 +145,7 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
     const uint32_t ks1 = min(ks0 + a.ksteps_per_slice, a.n_ksteps);
 
     for (uint32_t i = tid; i < 256u * 8u; i += kNT) {
-        const uint32_t e = trits03(i >> 3);
+        const uint32_t e = g_gemm_trits.v[i >> 3];
         *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
     }
     const char* tabb = reinterpret_cast<const char*>(tab);
@@ -395,7 +389,7 @@ int launch_gemm_stage(const int8_t* x, size_t M, size_t ldx, size_t cols, uint8_
     const GemmPlan p = gemm_plan(geometry(1, cols), M, 1);
     const dim3 grid((2u * p.n_ksteps + kStageRows - 1) / kStageRows, p.n_tg);
     hipLaunchKernelGGL(gemm_stage_kernel, grid, dim3(256), 0, stream, x, static_cast<uint32_t>(ldx), p.n_tg,
-                       static_cast<uint32_t>(cols), static_cast<uint32_t>(tile_row_bytes(cols)), p.n_ksteps,
+                       static_cast<uint32_t>(cols), p.n_ksteps,
                        reinterpret_cast<uint4*>(ws), static_cast<uint32_t>(M));
     VX_HIP(hipGetLastError());
     return VX_OK;
