@@ -125,8 +125,8 @@ constexpr int kNT = 1024;            // threads of the kernels that compute a st
 constexpr uint32_t kNormMax = 8192;  // longest normed input, and the LDS window of a staged input slice (floats)
 constexpr uint32_t kPlainMax = 24576;  // longest input without a norm (6 float4 groups per thread)
 constexpr uint32_t kStChunks = 112;  // 16-byte chunks of a staged input slice in LDS (16 waves x kDPer)
-constexpr int kMaxSlicesA = 6;       // K slices of a projection read as a residual-add input or by the attention
-constexpr int kMaxSlicesB = 2;       // K slices of the gate and up projections read by a ReLU^2 input
+constexpr int kMaxSlicesA = 6;       // K slices of a q/k/v, o or down projection at most
+constexpr int kMaxSlicesB = 2;       // K slices of a separate gate and up projection at most
 
 struct Ctl {          // device-resident loop state
     uint32_t pos;     // position of the step
@@ -143,10 +143,11 @@ __device__ __forceinline__ T load_if(const T* p, bool c) {
     return v;
 }
 
-// A projection output as its consumers read it: row i is float(sum_k part[k * stride + i]) * (ws / as), zero when as is
-// not > 0 (the layer epilogue, layer.rs:246-253; the K-slice sums are exact int32, so their order does not matter).
+// A projection output as its consumers read it: row i is float(part[i]) * (ws / as), zero when as is not > 0 (the layer
+// epilogue, layer.rs:246-253). A projection split into K slices adds their exact int32 sums atomically into part, so
+// their order does not matter; a prefill's outputs are token rows stride apart (kslices 1 in both).
 struct ProjOut {
-    const int32_t* part;  // [kslices][stride]; slice 0 holds the row corrections
+    const int32_t* part;  // [stride]; the row corrections are added by the producer's slice 0
     const float* as;      // activation scale of the producing stage
     float ws;             // weight scale
     uint32_t kslices, stride;
@@ -165,15 +166,9 @@ __device__ __forceinline__ float proj_post(const ProjOut& o, float as, bool* zer
 __device__ __forceinline__ float proj_value(int32_t acc, float post, bool zero) {
     return zero ? 0.0f : static_cast<float>(acc) * post;
 }
-// Row i of o (attention inputs: a few values per thread); every slice is loaded before the sum uses one.
+// Row i of o (attention inputs: a few values per thread).
 __device__ __forceinline__ float proj_at(const ProjOut& o, uint32_t i, float post, bool zero) {
-    int32_t v[kMaxSlicesA];
-#pragma unroll
-    for (int k = 0; k < kMaxSlicesA; ++k) v[k] = load_if(o.part + static_cast<size_t>(k) * o.stride + i, static_cast<uint32_t>(k) < o.kslices);
-    int32_t acc = 0;
-#pragma unroll
-    for (int k = 0; k < kMaxSlicesA; ++k) acc += v[k];
-    return proj_value(acc, post, zero);
+    return proj_value(o.part[i], post, zero);
 }
 
 enum InputKind : uint32_t {
@@ -221,12 +216,17 @@ struct __align__(16) InputLds {  // ys is accessed 16 bytes at a time
     float mean;
 };
 
-__device__ __forceinline__ uint32_t elem4(uint32_t tid, int k) { return 4u * (tid + static_cast<uint32_t>(k) * kNT); }
+// Elements 4 (tid + k NI) .. + 3 of a stage input belong to thread tid < NI; the threads from NI on hold none (an index
+// past every input).
+template <uint32_t NI = kNT>
+__device__ __forceinline__ uint32_t elem4(uint32_t tid, int k) {
+    return tid < NI ? 4u * (tid + static_cast<uint32_t>(k) * NI) : 0xfffffff0u;
+}
 
 // Issues every load of the thread's inputs (16 bytes each, and the producers' activation scales) without using any, so
 // that the loads a kernel issues after it (weights) do not delay them: vector-memory loads complete in issue order, so
 // a load issued after the weights would wait for all of them.
-template <int P4, int SA, int SB>
+template <int P4, int SA, int SB, uint32_t NI = kNT>
 __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA, SB>& r, uint32_t wlo, uint32_t whi) {
     const uint32_t tid = threadIdx.x, n = p.n;
     if (p.kind == kInEmbed) {
@@ -240,7 +240,7 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
         const uint2* row = reinterpret_cast<const uint2*>(p.emb + static_cast<size_t>(tok) * n);
 #pragma unroll
         for (int k = 0; k < P4; ++k) {
-            const uint32_t i = elem4(tid, k);
+            const uint32_t i = elem4<NI>(tid, k);
             const uint2 e = load_if(row + i / 4u, i < n);
             r.x[k] = make_uint4(e.x, e.y, 0u, 0u);
         }
@@ -250,7 +250,7 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
         if (!all) r.amax = *p.amax;
 #pragma unroll
         for (int k = 0; k < P4; ++k) {
-            const uint32_t i = elem4(tid, k);
+            const uint32_t i = elem4<NI>(tid, k);
             r.x[k] = load_if(reinterpret_cast<const uint4*>(p.x_in + i), i < n && (all || (i >= wlo && i < whi)));
         }
     }
@@ -261,7 +261,7 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
             for (int s = 0; s < SA; ++s)
 #pragma unroll
                 for (int k = 0; k < P4; ++k) {
-                    const uint32_t i = elem4(tid, k);
+                    const uint32_t i = elem4<NI>(tid, k);
                     r.pa[s][k] = load_if(reinterpret_cast<const int4*>(p.a.part + static_cast<size_t>(s) * p.a.stride + i),
                                          i < n && static_cast<uint32_t>(s) < p.a.kslices);
                 }
@@ -274,7 +274,7 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
             for (int s = 0; s < SB; ++s)
 #pragma unroll
                 for (int k = 0; k < P4; ++k) {
-                    const uint32_t i = elem4(tid, k);
+                    const uint32_t i = elem4<NI>(tid, k);
                     r.pb[s][k] = load_if(reinterpret_cast<const int4*>(p.b.part + static_cast<size_t>(s) * p.b.stride + i),
                                          i < n && static_cast<uint32_t>(s) < p.b.kslices);
                 }
@@ -283,7 +283,7 @@ __device__ __forceinline__ void stage_load(const StageInput& p, InputRegs<P4, SA
     if (p.gamma != nullptr) {
 #pragma unroll
         for (int k = 0; k < P4; ++k) {
-            const uint32_t i = elem4(tid, k);
+            const uint32_t i = elem4<NI>(tid, k);
             r.g[k] = load_if(reinterpret_cast<const float4*>(p.gamma + i), i < n);
         }
     }
@@ -329,7 +329,7 @@ __device__ __forceinline__ void slice_sums(const int4 (&pa)[SA > 0 ? SA : 1][P4]
 // y of the thread's elements: v by kind, then (with gamma) its RMSNorm y = (v * inv) * gamma (rms_norm, ops.rs:19-96).
 // Every thread derives the mean from the per-wave sums itself, so the common path has one barrier; without gamma none.
 // With write_x, an input that has an x_out also stores v there.
-template <int P4, int SA, int SB>
+template <int P4, int SA, int SB, uint32_t NI = kNT>
 __device__ __forceinline__ void stage_y(const StageInput& p, const InputRegs<P4, SA, SB>& r, InputLds& s, bool write_x,
                                         float (&y)[P4][4]) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -382,8 +382,8 @@ __device__ __forceinline__ void stage_y(const StageInput& p, const InputRegs<P4,
     if (write_x && (p.kind == kInEmbed || p.kind == kInResidual) && p.x_out != nullptr) {
 #pragma unroll
         for (int k = 0; k < P4; ++k)
-            if (elem4(tid, k) < n)
-                *reinterpret_cast<float4*>(p.x_out + elem4(tid, k)) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
+            if (elem4<NI>(tid, k) < n)
+                *reinterpret_cast<float4*>(p.x_out + elem4<NI>(tid, k)) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
     }
     if (p.gamma == nullptr) {
 #pragma unroll
@@ -395,7 +395,7 @@ __device__ __forceinline__ void stage_y(const StageInput& p, const InputRegs<P4,
     double ss = 0.0;
 #pragma unroll
     for (int k = 0; k < P4; ++k) {
-        const uint32_t i = elem4(tid, k);
+        const uint32_t i = elem4<NI>(tid, k);
         if (i < n) {
             *reinterpret_cast<float4*>(s.ys + i) = make_float4(v[k][0], v[k][1], v[k][2], v[k][3]);
 #pragma unroll
@@ -405,32 +405,39 @@ __device__ __forceinline__ void stage_y(const StageInput& p, const InputRegs<P4,
             }
         }
     }
-    ss = wave_sum_f64(ss);
-    if (lane == 0) s.red_d[wave] = ss;
-    __syncthreads();
-    double t = 0.0;
-    for (int w = 0; w < kNT / 64; ++w) t += s.red_d[w];
-    // The reference's sequential f64 sum and t both lie within (n - 1) 2^-53 S of the exact sum S of the nonnegative
-    // squares, so the reference's quotient by n (rounded) lies within (2 (n - 1) + 3) 2^-53 q of q = t / n and of the
-    // rounded ends of [q - e, q + e] for e = (2 n + 8) 2^-53 q; when both ends round to the same f32, so does it.
-    const double q = t / static_cast<double>(n);
-    const double e = (2.0 * static_cast<double>(n) + 8.0) * 0x1.0p-53 * q;
-    float mean = static_cast<float>(q);
-    const float lo = static_cast<float>(q - e);
-    const float hi = static_cast<float>(q + e);
-    if (lo != hi) {  // (the same in every thread) too close to an f32 rounding boundary: the reference's order
-        if (tid == 0) {
-            double seq = 0.0;
-            for (uint32_t i = 0; i < n; ++i) {
-                const float sqv = s.ys[i] * s.ys[i];
-                seq += static_cast<double>(sqv);
-            }
-            s.mean = static_cast<float>(seq / static_cast<double>(n));
-        }
-        __syncthreads();
-        mean = s.mean;
+    constexpr uint32_t kW = NI / 64;  // waves that hold elements
+    if (wave < kW) {
+        ss = wave_sum_f64(ss);
+        if (lane == 0) s.red_d[wave] = ss;
     }
-    const float scale = 1.0f / __builtin_sqrtf(mean + p.eps);
+    __syncthreads();
+    // Wave 0 alone turns the sums into the scale (the other waves would only repeat it) and hands it over in LDS.
+    if (wave == 0) {
+        double t = 0.0;
+        for (uint32_t w = 0; w < kW; ++w) t += s.red_d[w];
+        // The reference's sequential f64 sum and t (any order of the same additions) both lie within (n - 1) 2^-53 S of
+        // the exact sum S of the nonnegative squares, so the reference's quotient by n (rounded) lies within
+        // (2 (n - 1) + 3) 2^-53 q of q = t / n and of the rounded ends of [q - e, q + e] for e = (2 n + 8) 2^-53 q;
+        // when both ends round to the same f32, so does it.
+        const double q = t / static_cast<double>(n);
+        const double e = (2.0 * static_cast<double>(n) + 8.0) * 0x1.0p-53 * q;
+        float mean = static_cast<float>(q);
+        const float lo = static_cast<float>(q - e);
+        const float hi = static_cast<float>(q + e);
+        if (lane == 0) {
+            if (lo != hi) {  // too close to an f32 rounding boundary: the reference's order
+                double seq = 0.0;
+                for (uint32_t i = 0; i < n; ++i) {
+                    const float sqv = s.ys[i] * s.ys[i];
+                    seq += static_cast<double>(sqv);
+                }
+                mean = static_cast<float>(seq / static_cast<double>(n));
+            }
+            s.mean = 1.0f / __builtin_sqrtf(mean + p.eps);
+        }
+    }
+    __syncthreads();
+    const float scale = s.mean;
 #pragma unroll
     for (int k = 0; k < P4; ++k) {
         const float gm[4] = {r.g[k].x, r.g[k].y, r.g[k].z, r.g[k].w};
@@ -461,13 +468,13 @@ __device__ __forceinline__ void slice_window(uint32_t n, uint32_t c0, uint32_t c
 
 // Writes the thread's y of elements [lo, hi) to s.ys[i - lo] and returns its largest |y| over all elements (NaN never
 // counts). The window must be at most kNormMax long; it is readable after the next barrier.
-template <int P4>
+template <int P4, uint32_t NI = kNT>
 __device__ __forceinline__ float stage_window(const float (&y)[P4][4], uint32_t n, uint32_t lo, uint32_t hi, InputLds& s) {
     const uint32_t tid = threadIdx.x;
     float mx = 0.0f;
 #pragma unroll
     for (int k = 0; k < P4; ++k) {
-        const uint32_t i = elem4(tid, k);
+        const uint32_t i = elem4<NI>(tid, k);
         if (i < n) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -492,15 +499,18 @@ __device__ __forceinline__ int quant_code(float y, float sc) {
 // high nibbles (x >> 4) of its five activations (column_activation_index, pack.rs:230-237; zero past the row), read
 // from the window s.ys[i - lo]. The sum of all n codes comes from the thread's own y. Two barriers; afterwards the
 // entries are complete, *scale is the activation scale and *act_sum the sum of the codes, in every thread.
-template <int P4>
+template <int P4, uint32_t NI = kNT>
 __device__ __forceinline__ void stage_quant(const float (&y)[P4][4], InputLds& s, float mx, uint32_t n, uint32_t tbr,
                                             uint32_t c0, uint32_t c1, uint32_t lo, uint2* st, float* scale, int* act_sum) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    mx = wave_max_f32(mx);
-    if (lane == 0) s.red_f[wave] = mx;
+    constexpr uint32_t kW = NI / 64;  // waves that hold elements
+    if (wave < kW) {
+        mx = wave_max_f32(mx);
+        if (lane == 0) s.red_f[wave] = mx;
+    }
     __syncthreads();
     float m = 0.0f;
-    for (int w = 0; w < kNT / 64; ++w) m = fmax_nn(m, s.red_f[w]);
+    for (uint32_t w = 0; w < kW; ++w) m = fmax_nn(m, s.red_f[w]);
     const float sc = m > 0.0f ? 127.0f / m : 0.0f;
     int sum = 0;  // the codes of the staged columns' elements (each element belongs to one column)
     const uint32_t full = n / 160u * 32u;
@@ -519,11 +529,14 @@ __device__ __forceinline__ void stage_quant(const float (&y)[P4][4], InputLds& s
         }
         st[c - c0] = make_uint2(lo_n, hi_n);
     }
-    sum = wave_sum_i32(sum);
-    if (lane == 0) s.red_i[wave] = sum;
+    const uint32_t cw = c1 > c0 ? min(static_cast<uint32_t>(kNT / 64), (c1 - c0 + 63u) / 64u) : 0u;  // waves with columns
+    if (wave < cw) {
+        sum = wave_sum_i32(sum);
+        if (lane == 0) s.red_i[wave] = sum;
+    }
     __syncthreads();
     int t = 0;
-    for (int w = 0; w < kNT / 64; ++w) t += s.red_i[w];
+    for (uint32_t w = 0; w < cw; ++w) t += s.red_i[w];
     *act_sum = t;
     *scale = sc;
 }
@@ -576,13 +589,15 @@ struct DJob {
     uint32_t* amax_out;    // gated pair: atomic maximum of |act_out| as float bits (a plain unnormed consumer), or null
     uint32_t rows, padded_rows, n_tiles, n_chunks, kslices, slice_chunks, item_begin;
     uint32_t w_bytes;      // bytes of w (and w2) in the device layout, below kBufferOutOfRange
-    // gated pair split into chunk ranges: per tile the gate and up sums of 64 rows added atomically ([tile][2][64],
-    // zero between launches) and the count of workgroups that have added theirs (zero between launches)
-    int32_t* accum;
-    uint32_t* tickets;
+    // gated pair split into chunk ranges: per tile and row one word that the workgroups whose ranges meet the tile add
+    // to atomically ([tile][64], zero between launches): bits 0-23 and 24-47 the gate and up sums, each contribution
+    // raised by kRangeBias, bits 48-63 the count of contributions
+    unsigned long long* accum;
 };
+constexpr int kRangeBias = 1 << 21;  // > the largest |partial sum| of a row (103 chunks x 10880), 3 x 2 kRangeBias < 2^24
 
 constexpr int kMaxStageJobs = 3;
+constexpr int kMaxClear = 6;
 // Buffer loads of the weights: the resource's fourth word for raw (unformatted, unswizzled) access, an offset past any
 // matrix (such a load returns zeros without touching memory) and the non-temporal cache policy.
 constexpr int kBufferRsrcWord3 = 0x00020000;
@@ -608,6 +623,10 @@ struct DStageArgs {
     // A gated pair split into equal chunk ranges (0: split into items): the pair's chunks listed tile by tile, the gate
     // chunks of a tile before its up chunks, range_chunks of them in all; workgroup w takes [w C / G, (w + 1) C / G).
     uint32_t range_chunks;
+    // accumulators this stage zeroes once it is done (outputs of projections whose consumers have run, which a later
+    // stage adds to again), or null
+    int32_t* clear[kMaxClear];
+    uint32_t clear_words[kMaxClear];
 };
 
 __constant__ DigitTable g_digits = make_digit_table();
@@ -619,7 +638,7 @@ __constant__ DigitTable g_digits = make_digit_table();
 // chunk loads per item (buffer loads; a chunk the wave does not have reads past the buffer's end, which returns zeros
 // without a memory access), so each chunk is waited for on its own. The digit-nibble table and the arithmetic are those
 // of the lone GEMV (vx_gemv.hip). Only the entries of the item's own chunks are staged.
-template <int P4, int SA, int SB, bool MULTI, int DPER, bool RANGE = false>
+template <int P4, int SA, int SB, bool MULTI, int DPER, bool RANGE, uint32_t NI>
 __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     static_assert(!RANGE || (MULTI && DPER == kDPer), "the chunk-range split runs on the gated-pair instance");
     __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of the digit nibbles of byte B (first half)
@@ -703,7 +722,7 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     uint32_t lo, hi;
     slice_window(in.n, c0, c1, &lo, &hi);
     InputRegs<P4, SA, SB> r;
-    stage_load(in, r, lo, hi);
+    stage_load<P4, SA, SB, NI>(in, r, lo, hi);
     uint32_t dig[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) dig[k] = g_digits.v[(tid + k * kNT) >> 3];
@@ -770,10 +789,27 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     Item ib{};
     u32x4 bb[MULTI ? DPER : 1];
     if constexpr (MULTI) ib = locate(has_b ? item_b : blockIdx.x);
+    // The row digit sums the epilogue adds (wave 0: the rows of the items; a range: wave sg, the rows of tile
+    // t_first + sg), issued after the weights so that they do not delay them, and first used after the last chunk.
+    // Every wave loads them (unconditional loads at valid rows, so that every wait stays exact); only those waves use
+    // them.
+    int dsa, dsa2, dsb = 0, dsb2 = 0;
+    {
+        uint32_t t = ia.tile;
+        if constexpr (RANGE) t = min(t_first + min(wave, static_cast<uint32_t>(kRangeSegs) - 1u), ia.jb.n_tiles - 1u);
+        const uint32_t row = t * kTileRows + lane;
+        dsa = ia.jb.dsum[row];
+        dsa2 = (ia.jb.dsum2 != nullptr ? ia.jb.dsum2 : ia.jb.dsum)[row];
+        if constexpr (MULTI && !RANGE) {
+            const uint32_t rowb = ib.tile * kTileRows + lane;
+            dsb = ib.jb.dsum[rowb];
+            dsb2 = (ib.jb.dsum2 != nullptr ? ib.jb.dsum2 : ib.jb.dsum)[rowb];
+        }
+    }
 
     float y[P4][4];
-    stage_y(in, r, s, blockIdx.x == 0, y);
-    float mx = stage_window(y, in.n, lo, hi, s);
+    stage_y<P4, SA, SB, NI>(in, r, s, blockIdx.x == 0, y);
+    float mx = stage_window<P4, NI>(y, in.n, lo, hi, s);
     if (in.amax != nullptr) mx = __uint_as_float(r.amax);
     // The table is filled after the input's values are computed (its loads were issued after the input's, so waiting
     // for them earlier would also wait for the input) and before the quantization's first barrier.
@@ -785,7 +821,7 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     }
     float act_scale;
     int act_sum;
-    stage_quant(y, s, mx, in.n, tbr, c0, (ia.q0 + ia.nq) * 16u, lo, st, &act_scale, &act_sum);
+    stage_quant<P4, NI>(y, s, mx, in.n, tbr, c0, (ia.q0 + ia.nq) * 16u, lo, st, &act_scale, &act_sum);
     if (blockIdx.x == 0 && tid == 0) *a.as_out = act_scale;
 
     // The sums of an item's chunks (from b) into red[slot] (gate, and up for a pair); with `next`, chunk i of the second
@@ -878,7 +914,7 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
     // The outputs of row `row` of a gated pair from the complete sums v (gate) and v2 (up) of its row, corrections
     // included: the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170. A whole
     // wave calls it (the absmax is a wave reduction).
-    auto gate_out = [&](const DJob& jb, uint32_t row, int v, int v2) {
+    auto gate_out = [&](const DJob& jb, uint32_t row, int v, int v2, bool own) {
         const bool zero = !(act_scale > 0.0f);
         const float g = zero ? 0.0f : static_cast<float>(v) * (jb.ws / act_scale);
         const float u = zero ? 0.0f : static_cast<float>(v2) * (jb.ws2 / act_scale);
@@ -893,16 +929,16 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
             const float sq = pos * pos;
             o = sq * u;
         }
-        if (row < jb.rows) jb.act_out[row] = o;
+        if (own && row < jb.rows) jb.act_out[row] = o;
         if (jb.amax_out != nullptr) {  // the consumer's absmax (NaN never counts, as in stage_window)
-            float ao = row < jb.rows ? __builtin_fabsf(o) : 0.0f;
+            float ao = own && row < jb.rows ? __builtin_fabsf(o) : 0.0f;
             if (!(ao > 0.0f)) ao = 0.0f;
             ao = wave_max_f32(ao);
             if (lane == 0 && ao > 0.0f) atomicMax(jb.amax_out, __float_as_uint(ao));
         }
     };
     // Wave 0 after the barrier: the slice sums of an item from red[slot] and its outputs.
-    auto epilogue = [&](const Item& it, uint32_t slot) {
+    auto epilogue = [&](const Item& it, uint32_t slot, int dsum, int dsum2) {
         const bool pair = MULTI && it.jb.w2 != nullptr;
         // sum t x = 16 hi + lo + 8 sum d - sum x (the lone GEMV's row_result): the corrections once per row, in slice 0
         const DJob& jb = it.jb;
@@ -911,73 +947,81 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
         for (int w = 0; w < kNT / 64; ++w) v += red[slot][0][w][lane];
         const uint32_t row = it.tile * kTileRows + lane;
         // act_sum holds the codes of this slice's elements only: every slice subtracts its own
-        if (it.ks == 0) v += 8 * jb.dsum[row];
+        if (it.ks == 0) v += 8 * dsum;
         v -= act_sum;
         if (!pair) {
-            jb.part[static_cast<size_t>(it.ks) * jb.padded_rows + row] = v;
+            // the K slices of a row add up in one int32 (exact and order-independent, zero before the stage)
+            if (jb.kslices > 1) atomicAdd(jb.part + row, v);
+            else jb.part[row] = v;
             return;
         }
         int v2 = 0;
 #pragma unroll
         for (int w = 0; w < kNT / 64; ++w) v2 += red[slot][MULTI ? 1 : 0][w][lane];
-        v2 += 8 * jb.dsum2[row] - act_sum;
-        gate_out(jb, row, v, v2);
+        v2 += 8 * dsum2 - act_sum;
+        gate_out(jb, row, v, v2, true);
     };
     if constexpr (RANGE) {
         {
             accumulate_range(ba);
             __syncthreads();
-            // Wave sg takes tile t_first + sg of the range: with the whole tile here its outputs directly; otherwise its
-            // sums go to the tile's accumulators, and the workgroup that adds the last of them (the ticket counts the
-            // workgroups whose ranges meet the tile) takes the totals, clears them and writes the outputs.
+            // Wave sg takes tile t_first + sg of the range: with the whole tile here its outputs directly; otherwise
+            // each row's gate and up sums go into the row's accumulator word together with a count, and the
+            // contribution that completes the count (the workgroups whose ranges meet the tile) takes the totals,
+            // clears the word and writes the outputs.
             const uint32_t t_last = (re - 1u) / nc2;
             if (wave <= t_last - t_first) {
                 const DJob& jb = ia.jb;
                 const uint32_t sg = wave, t = t_first + sg, tb = t * nc2, te = tb + nc2;
+                const int rd = dsa, rd2 = dsa2;  // the digit sums of tile t's rows
                 int v = 0, v2 = 0;
 #pragma unroll
                 for (int w = 0; w < kNT / 64; ++w) {
                     v += red[sg][0][w][lane];
                     v2 += red[sg][1][w][lane];
                 }
-                bool last = true;
+                bool own = true;
                 if (rb > tb || re < te) {
-                    int32_t* acc = jb.accum + static_cast<size_t>(t) * 128u;
-                    atomicAdd(acc + lane, v);
-                    atomicAdd(acc + 64u + lane, v2);
-                    __builtin_amdgcn_s_waitcnt(0);  // both adds complete before the ticket
                     // workgroups whose ranges meet chunks tb and te - 1: w(g) = floor(((g + 1) G - 1) / C)
                     const uint64_t C = a.range_chunks, G = gridDim.x;
                     const uint32_t wf = static_cast<uint32_t>(((tb + 1ull) * G - 1ull) / C);
                     const uint32_t wl = static_cast<uint32_t>((static_cast<uint64_t>(te) * G - 1ull) / C);
-                    uint32_t tk = 0;
-                    if (lane == 0) tk = atomicAdd(jb.tickets + t, 1u);
-                    tk = __builtin_amdgcn_readfirstlane(tk);
-                    last = tk == wl - wf;
-                    if (last) {
-                        v = atomicExch(acc + lane, 0);
-                        v2 = atomicExch(acc + 64u + lane, 0);
-                        if (lane == 0) atomicExch(jb.tickets + t, 0u);
+                    const unsigned long long mine = (1ull << 48) |
+                                                    (static_cast<unsigned long long>(v2 + kRangeBias) << 24) |
+                                                    static_cast<unsigned long long>(v + kRangeBias);
+                    unsigned long long* acc = jb.accum + static_cast<size_t>(t) * 64u + lane;
+                    const unsigned long long sum = atomicAdd(acc, mine) + mine;
+                    // the row's last contribution takes the totals and clears the word for the next launch
+                    const uint32_t c = static_cast<uint32_t>(sum >> 48);
+                    own = c == wl - wf + 1u;
+                    if (own) {
+                        v = static_cast<int>(static_cast<uint32_t>(sum) & 0xffffffu) - static_cast<int>(c) * kRangeBias;
+                        v2 = static_cast<int>(static_cast<uint32_t>(sum >> 24) & 0xffffffu) - static_cast<int>(c) * kRangeBias;
+                        __hip_atomic_store(acc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                 }
-                if (last) {
-                    const uint32_t row = t * kTileRows + lane;
-                    gate_out(jb, row, v + 8 * jb.dsum[row] - act_sum, v2 + 8 * jb.dsum2[row] - act_sum);
-                }
+                gate_out(jb, t * kTileRows + lane, v + 8 * rd - act_sum, v2 + 8 * rd2 - act_sum, own);
             }
-            return;
         }
-    }
-    accumulate(ia, ba, 0u, true);
-    if constexpr (MULTI) {
-        if (has_b) accumulate(ib, bb, 1u, false);
-    }
-    __syncthreads();
-    if (wave == 0) {
-        epilogue(ia, 0u);
+    } else {
+        accumulate(ia, ba, 0u, true);
         if constexpr (MULTI) {
-            if (has_b) epilogue(ib, 1u);
+            if (has_b) accumulate(ib, bb, 1u, false);
         }
+        __syncthreads();
+        if (wave == 0) {
+            epilogue(ia, 0u, dsa, dsa2);
+            if constexpr (MULTI) {
+                if (has_b) epilogue(ib, 1u, dsb, dsb2);
+            }
+        }
+    }
+    // zero the accumulators the stage clears (their consumers have run; a later stage adds to them again)
+#pragma unroll
+    for (int c = 0; c < kMaxClear; ++c) {
+        int32_t* z = a.clear[c];
+        if (z == nullptr) continue;
+        for (uint32_t i = blockIdx.x * kNT + tid; i < a.clear_words[c]; i += gridDim.x * kNT) z[i] = 0;
     }
 }
 
@@ -1884,7 +1928,7 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
     __shared__ uint4 xs[kNormMax / 8];
     __shared__ unsigned long long wbest[kNT / 64];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    InputRegs<2, kMaxSlicesA, 0> r;
+    InputRegs<2, 1, 0> r;
     stage_load(a.in, r, 0u, a.in.n);
     float y[2][4];
     stage_y(a.in, r, s, false, y);
@@ -2155,13 +2199,13 @@ template <int P4, int SA, int SB, bool MULTI>
 static void launch_dgemv_d(const DStageArgs& a, hipStream_t s) {
     if constexpr (MULTI) {
         if (a.range_chunks != 0) {
-            hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, true, kDPer, true>), dim3(a.grid), dim3(kNT), 0, s, a);
+            hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, true, kDPer, true, kNT>), dim3(a.grid), dim3(kNT), 0, s, a);
             return;
         }
     }
-    if (a.dper <= 1) hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, 1>), dim3(a.grid), dim3(kNT), 0, s, a);
-    else if (a.dper <= 4) hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, 4>), dim3(a.grid), dim3(kNT), 0, s, a);
-    else hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, kDPer>), dim3(a.grid), dim3(kNT), 0, s, a);
+    if (a.dper <= 1) hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, 1, false, kNT>), dim3(a.grid), dim3(kNT), 0, s, a);
+    else if (a.dper <= 4) hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, 4, false, kNT>), dim3(a.grid), dim3(kNT), 0, s, a);
+    else hipLaunchKernelGGL((dgemv_kernel<P4, SA, SB, MULTI, kDPer, false, kNT>), dim3(a.grid), dim3(kNT), 0, s, a);
 }
 
 // MULTI: the instance that takes two items per workgroup and runs gated pairs; the others take one plain item.
@@ -2170,12 +2214,12 @@ int launch_dgemv(const DStageArgs& a, hipStream_t s) {
     if (a.dper == 0 || a.dper > static_cast<uint32_t>(kDPer)) VX_FAIL(VX_ERR_INTERNAL, "stage with %u chunks per wave", a.dper);
     switch (a.variant) {
         case kDv4K:
-            if (multi) launch_dgemv_d<1, kMaxSlicesA, kMaxSlicesB, true>(a, s);
-            else launch_dgemv_d<1, kMaxSlicesA, kMaxSlicesB, false>(a, s);
+            if (multi) launch_dgemv_d<1, 1, 1, true>(a, s);
+            else launch_dgemv_d<1, 1, 1, false>(a, s);
             break;
         case kDv8K:
-            if (multi) launch_dgemv_d<2, kMaxSlicesA, kMaxSlicesB, true>(a, s);
-            else launch_dgemv_d<2, kMaxSlicesA, kMaxSlicesB, false>(a, s);
+            if (multi) launch_dgemv_d<2, 1, 1, true>(a, s);
+            else launch_dgemv_d<2, 1, 1, false>(a, s);
             break;
         default:  // a wide plain input is a down projection's, split into several K slices: one item per workgroup
             if (multi) VX_FAIL(VX_ERR_INTERNAL, "a looping stage with a %u-element input", a.in.n);
@@ -2284,7 +2328,7 @@ struct vx_decoder {
     uint16_t* d_head;                 // the untied head, or null
     float* d_inter;                   // gated pair output: act(gate, up), [ffn rounded up to 64]
     uint32_t* d_amax;                 // per layer: max |act(gate, up)| bits for an unnormed down input (pair, no sub-norms)
-    int32_t* d_pacc;                  // pair: per tile [gate, up][64] sums of the chunk-range split, then the tickets
+    int32_t* d_pacc;                  // pair: per tile and row one 64-bit word (gate, up, count) of the chunk-range split
     float* d_rope;
     uint16_t *d_kc, *d_vc;            // [layer][kv_head][max_ctx][head_dim]
     float *d_xa, *d_xb;               // the residual stream (written alternately by the stages that add to it)
@@ -2582,7 +2626,7 @@ static ProjOut proj_out(const vx_decoder* d, size_t layer, int kind) {
     o.part = d->d_part[kind];
     o.as = d->d_as + stage_of(kind);
     o.ws = m->weight_scale;
-    o.kslices = d->kslices[kind];
+    o.kslices = 1;  // the producer's K slices add up in the one array
     o.stride = static_cast<uint32_t>(m->g.padded_rows);
     return o;
 }
@@ -2607,6 +2651,32 @@ static uint32_t input_variant(const StageInput& in) {
     return kDvPlain;  // create_decoder admits only plain, unnormed inputs beyond kNormMax
 }
 
+// The accumulators stage s clears once it is done: a projection split into K slices adds them atomically into one
+// zeroed array, so its array is cleared by a stage that runs after all of its consumers and before its producer runs
+// again. q, k, v (read by the attention) and down (read by the next layer's q/k/v stage, or by the head after the last
+// layer) are cleared by the o stage; o (read by the FFN stage) by the down stage; a ReLU^2 model's separate gate and up
+// (read by the down stage) by the next q/k/v stage (the next step's first one after the last layer).
+static void clear_after(const vx_decoder* d, int s, DStageArgs& a) {
+    uint32_t n = 0;
+    auto add = [&](int kind) {
+        if (d->kslices[kind] <= 1 || d->d_part[kind] == nullptr) return;  // one slice: the producer stores its sums
+        a.clear[n] = d->d_part[kind];
+        a.clear_words[n] = static_cast<uint32_t>(d->proj[kind]->g.padded_rows);
+        ++n;
+    };
+    if (s == 0 && !d->pair) {
+        add(VX_PROJ_GATE);
+        add(VX_PROJ_UP);
+    } else if (s == 1) {
+        add(VX_PROJ_Q);
+        add(VX_PROJ_K);
+        add(VX_PROJ_V);
+        add(VX_PROJ_DOWN);
+    } else if (s == 3) {
+        add(VX_PROJ_O);
+    }
+}
+
 // The stage launches of every layer. A stage's work items are (64-row tile, K slice) pairs of its projections; the K
 // split gives each stage about one item per CU (a 2560-row projection has only 40 tiles). A gated pair (gate and up
 // with SiLU) is one job of one slice whose items cover a tile of both matrices.
@@ -2627,7 +2697,10 @@ static int build_stages(vx_decoder* d) {
             if (!ok) VX_FAIL(VX_ERR_UNSUPPORTED, "projection %d has too many chunks per row (%zu)", k, g.n_chunks);
             if (d->d_part[k]) (void)hipFree(d->d_part[k]);
             d->d_part[k] = nullptr;
-            VX_HIP(hipMalloc(&d->d_part[k], static_cast<size_t>(d->kslices[k]) * g.padded_rows * 4));
+            // one int32 per row: the K slices add their sums atomically (zero before the producing stage: the stages
+            // after its consumers clear it, see clear_after)
+            VX_HIP(hipMalloc(&d->d_part[k], g.padded_rows * 4));
+            VX_HIP(hipMemset(d->d_part[k], 0, g.padded_rows * 4));
         }
     }
     d->stages.assign(L * kStages, DStageArgs{});
@@ -2666,8 +2739,7 @@ static int build_stages(vx_decoder* d) {
                 if (C >= G && (C + G - 1) / G <= static_cast<uint64_t>(kTileGroup * kDPer) &&
                     2u * j.n_chunks >= static_cast<uint32_t>(8 * kDPer) && j.n_tiles > G) {
                     a.range_chunks = static_cast<uint32_t>(C);
-                    j.accum = d->d_pacc;
-                    j.tickets = reinterpret_cast<uint32_t*>(d->d_pacc + static_cast<size_t>(j.n_tiles) * 128u);
+                    j.accum = reinterpret_cast<unsigned long long*>(d->d_pacc);
                 }
             } else {
                 for (int k : kStageKinds[s]) {
@@ -2736,6 +2808,7 @@ static int build_stages(vx_decoder* d) {
             a.tbr = static_cast<uint32_t>(tile_row_bytes(in.n));
             a.as_out = d->d_as + s;
             a.variant = input_variant(in);
+            clear_after(d, s, a);
             if (a.variant == kDvPlain && (in.kind != kInPlain || in.gamma != nullptr))
                 VX_FAIL(VX_ERR_INTERNAL, "stage %d input of %u elements needs a norm", s, in.n);
         }
