@@ -113,8 +113,9 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     if (e == hipSuccess && m->kslices > 1) e = hipMalloc(&m->d_part, static_cast<size_t>(m->kslices) * m->g.padded_rows * 4);
     // the atomic slice sums and tickets of the lone calls (the table GEMV splits K more finely than the digit GEMV,
     // so every matrix has them)
-    if (e == hipSuccess) e = hipMalloc(&m->d_accum, m->g.padded_rows * 4 + m->g.n_groups * 4);
-    if (e == hipSuccess) e = hipMemset(m->d_accum, 0, m->g.padded_rows * 4 + m->g.n_groups * 4);
+    const size_t accum_bytes = (m->g.padded_rows + m->g.n_groups) * 4;
+    if (e == hipSuccess) e = hipMalloc(&m->d_accum, accum_bytes);
+    if (e == hipSuccess) e = hipMemset(m->d_accum, 0, accum_bytes);
     if (e == hipSuccess) m->d_tickets = reinterpret_cast<uint32_t*>(m->d_accum + m->g.padded_rows);
     if (e == hipSuccess) e = hipMalloc(&m->d_dsum, m->g.padded_rows * 4);
     if (e == hipSuccess) e = hipMalloc(&m->d_staged, staged_bytes(cols));

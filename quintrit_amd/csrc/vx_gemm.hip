@@ -371,7 +371,11 @@ static GemmPlan gemm_plan(const Geometry& g, size_t M, int num_cus) {
     return p;
 }
 
+static size_t small_part_bytes(const Geometry& g, size_t M, int num_cus);
+static bool small_path(size_t M);
+
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus) {
+    if (small_path(M)) return std::max<size_t>(small_part_bytes(g, M, num_cus), 256);
     const GemmPlan p = gemm_plan(g, M, num_cus);
     return p.xs_bytes + p.part_bytes;
 }
@@ -435,8 +439,238 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
     return VX_OK;
 }
 
+// ---- one token group (M <= 32): one launch ------------------------------------------------------------------------
+
+// Workgroup (c, kz): kSmallWaves waves, wave w the 64-row tile kSmallWaves c + w, over the kSmallSteps K steps of slice
+// kz. The workgroup first builds the B fragments of its whole slice in LDS straight from X (the staging of
+// gemm_stage_kernel, thread (step, half, token)), so no staging kernel runs; then each wave loads all its weights of
+// the slice at once (2 chunks x kSmallSteps steps per lane, every load unconditional) and multiplies them with no
+// further barrier. With one slice the wave writes Y; otherwise it stores its slice's sums, which
+// gemm_small_finish_kernel adds. (Gathering them in the kernel instead, each tile's last slice reading the others'
+// sums with agent-scope atomic loads after a ticket, was slower: 30-160 us per call at M = 8-32.)
+constexpr uint32_t kSmallSteps = 8;  // K steps per slice at most (40 KiB of B fragments in LDS)
+
+constexpr int kSmallWaves = 4;
+
+struct SmallArgs {
+    const uint8_t* w;
+    const int8_t* x;
+    int32_t* y;
+    int32_t* part;       // [kslices][M][rows_p] slice sums (kslices > 1)
+    uint32_t ldx, ldy, rows, rows_p, cols, n_tiles, n_chunks, n_ksteps, M, kslices;
+    uint32_t steps;      // K steps per slice (at most kSmallSteps)
+};
+
+__global__ __launch_bounds__(kSmallWaves * 64) void gemm_small_kernel(SmallArgs a) {
+    __shared__ uint32_t tab[256 * 64];
+    __shared__ uint4 bs[kSmallSteps * 5 * 64];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t tile = blockIdx.x * kSmallWaves + wave, kz = blockIdx.y;
+    const uint32_t ks0 = kz * a.steps, nst = min(a.steps, a.n_ksteps - ks0);
+    const uint32_t half = lane >> 5;
+
+    // the weights first: they are independent of everything below (a tile past the matrix reads the last one)
+    const uint32_t ltile = min(tile, a.n_tiles - 1u);
+    const uint32_t grp = ltile / kTileGroup, t16 = ltile - grp * kTileGroup;
+    const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup);
+    const uint8_t* wbase = a.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + t16) * 1024u + (lane & 31u) * 16u;
+    u32x4g wv[kSmallSteps][2];
+#pragma unroll
+    for (uint32_t s = 0; s < kSmallSteps; ++s) {
+        const uint32_t q = min((ks0 + min(s, nst - 1u)) * kStepChunks + half, a.n_chunks - 1u);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+            wv[s][rb] = __builtin_nontemporal_load((g_u4g*)(wbase + static_cast<size_t>(q) * Tg * 1024u + rb * 512u));
+    }
+
+    for (uint32_t i = tid; i < 256u * 8u; i += kSmallWaves * 64u) {
+        const uint32_t e = g_gemm_trits.v[i >> 3];
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
+    }
+    // B fragments of the slice: task (step s, half hs, token j); tokens past M get zeros
+    for (uint32_t t = tid; t < nst * 64u; t += kSmallWaves * 64u) {
+        const uint32_t s = t >> 6, hs = (t >> 5) & 1u, j = t & 31u, ks = ks0 + s;
+        uint4 o[5] = {};
+        if (j < a.M) {
+            const int8_t* xr = a.x + static_cast<size_t>(j) * a.ldx;
+            if (ks < a.cols / 160u && (reinterpret_cast<uintptr_t>(xr) & 15u) == 0) {
+                const int8_t* blk = xr + ks * 160u + 16u * hs;
+                uint4 X[5];
+#pragma unroll
+                for (int e = 0; e < 5; ++e) X[e] = *reinterpret_cast<const uint4*>(blk + 32 * e);
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    auto dw = [&](const uint4& v) { return kb == 0 ? v.x : (kb == 1 ? v.y : (kb == 2 ? v.z : v.w)); };
+                    const uint32_t a0 = dw(X[0]), a1 = dw(X[1]), a2 = dw(X[2]), a3 = dw(X[3]);
+                    const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u), hi01 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+                    const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u), hi23 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+                    o[kb] = make_uint4(__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                       __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u));
+                }
+                o[4] = X[4];
+            } else {
+                const bool tail = ks >= a.cols / 160u;
+                auto act = [&](uint32_t k, uint32_t p) -> uint32_t {
+                    const uint32_t idx = tail ? ks * 160u + 5u * (16u * hs + k) + p : ks * 160u + 32u * p + 16u * hs + k;
+                    return idx < a.cols ? static_cast<uint32_t>(static_cast<uint8_t>(xr[idx])) : 0u;
+                };
+#pragma unroll
+                for (uint32_t kb = 0; kb < 5; ++kb) {
+                    uint32_t w[4];
+#pragma unroll
+                    for (uint32_t d = 0; d < 4; ++d) {
+                        uint32_t v = 0;
+#pragma unroll
+                        for (uint32_t e = 0; e < 4; ++e) v |= (kb < 4 ? act(4u * kb + d, e) : act(4u * d + e, 4u)) << (8 * e);
+                        w[d] = v;
+                    }
+                    o[kb] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t kb = 0; kb < 5; ++kb) bs[(s * 5u + kb) * 64u + j + 32u * hs] = o[kb];
+    }
+    __syncthreads();
+    if (tile >= a.n_tiles) return;
+
+    const char* tabb = reinterpret_cast<const char*>(tab);
+    const uint32_t lane_off = (lane & 31u) * 4u;
+    v16i acc[2] = {v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}};
+#pragma unroll
+    for (uint32_t s = 0; s < kSmallSteps; ++s) {
+        if (s >= nst) break;
+        const bool inside = (ks0 + s) * kStepChunks + half < a.n_chunks;
+        v4i A[2][5];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+            const uint32_t dw[4] = {inside ? wv[s][rb].x : kZeroWord, inside ? wv[s][rb].y : kZeroWord,
+                                    inside ? wv[s][rb].z : kZeroWord, inside ? wv[s][rb].w : kZeroWord};
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                int t[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + b) << 8));
+                    t[b] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr));
+                }
+                A[rb][m] = v4i{t[0], t[1], t[2], t[3]};
+            }
+            A[rb][4] = v4i{static_cast<int>(t4_bytes(dw[0])), static_cast<int>(t4_bytes(dw[1])),
+                           static_cast<int>(t4_bytes(dw[2])), static_cast<int>(t4_bytes(dw[3]))};
+        }
+#pragma unroll
+        for (int kb = 0; kb < 5; ++kb) {
+            const uint4 b = bs[(s * 5u + kb) * 64u + lane];
+            const v4i B = v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
+            acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0][kb], B, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1][kb], B, acc[1], 0, 0, 0);
+        }
+    }
+    // C of block rb: lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4 of the block, token l % 32
+    const uint32_t m = lane & 31u;
+    if (a.kslices == 1) {
+        if (m < a.M) {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const uint32_t n = tile * 64u + rb * 32u + 8u * (r / 4) + 4u * half + (r % 4);
+                    if (n < a.rows) a.y[static_cast<size_t>(m) * a.ldy + n] = acc[rb][r];
+                }
+        }
+        return;
+    }
+    if (m < a.M) {  // the slice's sums; gemm_small_finish_kernel adds the slices
+        int32_t* pp = a.part + (static_cast<size_t>(kz) * a.M + m) * a.rows_p + tile * 64u;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+                *reinterpret_cast<int4*>(pp + rb * 32u + 8u * r4 + 4u * half) =
+                    make_int4(acc[rb][4 * r4], acc[rb][4 * r4 + 1], acc[rb][4 * r4 + 2], acc[rb][4 * r4 + 3]);
+    }
+}
+
+// Y[m][n] = sum over the slices of gemm_small_kernel's sums (block = 256 rows of one token).
+__global__ __launch_bounds__(256) void gemm_small_finish_kernel(SmallArgs a) {
+    const uint32_t n = blockIdx.x * 256u + threadIdx.x, m = blockIdx.y;
+    if (n >= a.rows) return;
+    const size_t stride = static_cast<size_t>(a.M) * a.rows_p;
+    const int32_t* p = a.part + static_cast<size_t>(m) * a.rows_p + n;
+    int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+    uint32_t k = 0;
+    for (; k + 4 <= a.kslices; k += 4) {
+        s0 += p[k * stride];
+        s1 += p[(k + 1) * stride];
+        s2 += p[(k + 2) * stride];
+        s3 += p[(k + 3) * stride];
+    }
+    for (; k < a.kslices; ++k) s0 += p[k * stride];
+    a.y[static_cast<size_t>(m) * a.ldy + n] = (s0 + s1) + (s2 + s3);
+}
+
+// K steps per slice: the count from 2 to kSmallSteps that minimises rounds x steps, a round being one workgroup per CU
+// (the trit table and the B fragments take 104 KiB of LDS); on a tie the longer slices (fewer sums to add).
+static uint32_t small_steps(const Geometry& g, int num_cus) {
+    const uint64_t n_ksteps = (g.n_chunks + kStepChunks - 1) / kStepChunks;
+    const uint64_t cols = (g.n_tiles + kSmallWaves - 1) / kSmallWaves;
+    const uint64_t cus = static_cast<uint64_t>(std::max(num_cus, 1));
+    uint64_t best = ~0ull;
+    uint32_t best_st = kSmallSteps;
+    for (uint32_t st = kSmallSteps; st >= 2; --st) {
+        const uint64_t wgs = cols * ((n_ksteps + st - 1) / st);
+        const uint64_t cost = (wgs + cus - 1) / cus * st;
+        if (cost < best) {
+            best = cost;
+            best_st = st;
+        }
+    }
+    return best_st;
+}
+
+static uint32_t small_kslices(const Geometry& g, int num_cus) {
+    const uint32_t n_ksteps = static_cast<uint32_t>((g.n_chunks + kStepChunks - 1) / kStepChunks);
+    const uint32_t st = small_steps(g, num_cus);
+    return (n_ksteps + st - 1) / st;
+}
+
+static bool small_path(size_t M) { return M <= 32; }
+
+static size_t small_part_bytes(const Geometry& g, size_t M, int num_cus) {
+    const uint32_t ks = small_kslices(g, num_cus);
+    return ks > 1 ? round_up(static_cast<size_t>(ks) * M * g.padded_rows * 4u, 256) : 0;
+}
+
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream) {
+    if (small_path(M)) {
+        SmallArgs a{};
+        a.w = w;
+        a.x = x;
+        a.y = y;
+        a.part = reinterpret_cast<int32_t*>(ws);
+        a.ldx = static_cast<uint32_t>(ldx);
+        a.ldy = static_cast<uint32_t>(ldy);
+        a.rows = static_cast<uint32_t>(g.rows);
+        a.rows_p = static_cast<uint32_t>(g.padded_rows);
+        a.cols = static_cast<uint32_t>(g.cols);
+        a.n_tiles = static_cast<uint32_t>(g.n_tiles);
+        a.n_chunks = static_cast<uint32_t>(g.n_chunks);
+        a.n_ksteps = static_cast<uint32_t>((g.n_chunks + kStepChunks - 1) / kStepChunks);
+        a.M = static_cast<uint32_t>(M);
+        a.kslices = small_kslices(g, num_cus);
+        a.steps = small_steps(g, num_cus);
+        const dim3 grid((a.n_tiles + kSmallWaves - 1) / kSmallWaves, a.kslices);
+        hipLaunchKernelGGL(gemm_small_kernel, grid, dim3(kSmallWaves * 64), 0, stream, a);
+        VX_HIP(hipGetLastError());
+        if (a.kslices > 1) {
+            hipLaunchKernelGGL(gemm_small_finish_kernel, dim3((a.rows + 255u) / 256u, a.M), dim3(256), 0, stream, a);
+            VX_HIP(hipGetLastError());
+        }
+        return VX_OK;
+    }
     VX_TRY(launch_gemm_stage(x, M, ldx, g.cols, ws, stream));
     return launch_gemm_staged(w, g, num_cus, ws, M, y, ldy, ws + gemm_stage_bytes(g.cols, M), stream);
 }

@@ -168,6 +168,8 @@ int launch_digit_sums(const uint8_t* w, const Geometry& g, int32_t* dsum, hipStr
 int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
 int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
+// M <= 32 runs without a staging kernel (gemm_small_kernel builds the B fragments in LDS from x; a finish kernel adds
+// the K slices when there are several); larger M as staging + GEMM + finish.
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream);
 // The two halves of launch_gemm: staging of the activations (shared by every matrix with the same cols) and the
