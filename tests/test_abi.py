@@ -126,6 +126,15 @@ def test_argument_errors_without_gpu():
     assert L.vx_q2_matrix_create(buf, 64, buf, 64, 1, 12352, ctypes.byref(h)) == 3
     assert L.vx_q2_matrix_create(buf, 16, buf, 64, 1, 64, ctypes.byref(h)) == 4   # planar too short
     assert L.vx_q2_gemv_f32_dev(None, buf, 64, buf, 2, buf, 1, None) == 14
+    # compact activation tables: 2 x 64 bytes per tile-row byte (avx512.rs:935-938), checks before any device work
+    assert _lib.compact_lut_bytes(3072) == 2 * 64 * 616
+    assert _lib.compact_lut_bytes(161) == 2 * 64 * 34
+    assert L.vx_compact_lut_bytes(3072, None) == 1                               # NULL out
+    assert L.vx_compact_lut_dev(None, 8, 8, buf, 64, None) == 1                   # NULL activations
+    assert L.vx_compact_lut_dev(buf, 4, 8, buf, 64 * 4, None) == 4                # activations too short
+    assert L.vx_compact_lut_dev(buf, 160, 160, buf, 2 * 64 * 32 - 1, None) == 4   # table buffer too short
+    assert L.vx_gemv_lut_i32_dev(None, buf, 64, buf, 1, None) == 14               # NULL handle
+    assert L.vx_lut_plan_create(None, 1, ctypes.byref(h)) == 1                    # NULL jobs
 
 
 def test_decoder_config_errors_before_device():
