@@ -34,6 +34,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <vector>
 
 namespace vx {
@@ -2940,8 +2941,18 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
         a.as_out = as_out;
         return launch_pf_stage(a, st);
     };
+    // GEMMs on the small path read the codes themselves; the others read them staged once per input
+    auto small = [&](int kind) { return gemm_small_path(d->proj[kind]->g, n); };
+    auto gemm_stage = [&](size_t cols, std::initializer_list<int> kinds) -> int {
+        bool need = false;
+        for (int k : kinds) need = need || !small(k);
+        return need ? launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, cols, d->pf_staged, st) : VX_OK;
+    };
     auto gemm = [&](size_t layer, int kind) -> int {
         const vx_matrix* m = d->proj[layer * kProjKinds + kind];
+        if (small(kind))
+            return launch_gemm(m->d_w, m->g, d->num_cus, d->pf_codes, n, d->pf_codes_ld, d->pf_y[kind], d->pf_ld[kind],
+                               d->pf_part, st);
         return launch_gemm_staged(m->d_w, m->g, d->num_cus, d->pf_staged, n, d->pf_y[kind], d->pf_ld[kind], d->pf_part, st);
     };
     for (size_t l = 0; l < L; ++l) {
@@ -2957,7 +2968,7 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
             in.a = pf_proj_out(d, l - 1, VX_PROJ_DOWN, as_down);
         }
         VX_TRY(stage(in, static_cast<uint32_t>(H), d->pf_ld[VX_PROJ_DOWN], as_qkv));
-        VX_TRY(launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, H, d->pf_staged, st));
+        VX_TRY(gemm_stage(H, {VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}));
         for (int k : {VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}) VX_TRY(gemm(l, k));
         PfRopeArgs ra{};
         ra.ctl = d->d_ctl;
@@ -3001,13 +3012,13 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
         // the o input: attention output (sub-norm or none)
         in = stage_input(d, kInPlain, d->qd, d->pf_att, nullptr, sub ? nw[VX_NORM_ATTN_SUB] : nullptr);
         VX_TRY(stage(in, static_cast<uint32_t>(d->qd), 0, as_o));
-        VX_TRY(launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, d->qd, d->pf_staged, st));
+        VX_TRY(gemm_stage(d->qd, {VX_PROJ_O}));
         VX_TRY(gemm(l, VX_PROJ_O));
         // x + o, FFN norm
         in = stage_input(d, kInResidual, H, d->pf_x, d->pf_x, nw[VX_NORM_FFN]);
         in.a = pf_proj_out(d, l, VX_PROJ_O, as_o);
         VX_TRY(stage(in, static_cast<uint32_t>(H), d->pf_ld[VX_PROJ_O], as_ffn));
-        VX_TRY(launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, H, d->pf_staged, st));
+        VX_TRY(gemm_stage(H, {VX_PROJ_GATE, VX_PROJ_UP}));
         VX_TRY(gemm(l, VX_PROJ_GATE));
         VX_TRY(gemm(l, VX_PROJ_UP));
         PfActArgs aa{};
@@ -3026,7 +3037,7 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
         // the down input: the gated activation (sub-norm or none)
         in = stage_input(d, kInPlain, F, d->pf_act, nullptr, sub ? nw[VX_NORM_FFN_SUB] : nullptr);
         VX_TRY(stage(in, static_cast<uint32_t>(F), 0, as_down));
-        VX_TRY(launch_gemm_stage(d->pf_codes, n, d->pf_codes_ld, F, d->pf_staged, st));
+        VX_TRY(gemm_stage(F, {VX_PROJ_DOWN}));
         VX_TRY(gemm(l, VX_PROJ_DOWN));
     }
     if (!head) return VX_OK;

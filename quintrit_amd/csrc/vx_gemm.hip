@@ -372,10 +372,10 @@ static GemmPlan gemm_plan(const Geometry& g, size_t M, int num_cus) {
 }
 
 static size_t small_part_bytes(const Geometry& g, size_t M, int num_cus);
-static bool small_path(size_t M);
+static bool small_path(const Geometry& g, size_t M);
 
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus) {
-    if (small_path(M)) return std::max<size_t>(small_part_bytes(g, M, num_cus), 256);
+    if (small_path(g, M)) return std::max<size_t>(small_part_bytes(g, M, num_cus), 256);
     const GemmPlan p = gemm_plan(g, M, num_cus);
     return p.xs_bytes + p.part_bytes;
 }
@@ -385,7 +385,9 @@ size_t gemm_stage_bytes(size_t cols, size_t M) {
     return p.xs_bytes;
 }
 
-size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus) { return gemm_plan(g, M, num_cus).part_bytes; }
+size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus) {
+    return small_path(g, M) ? small_part_bytes(g, M, num_cus) : gemm_plan(g, M, num_cus).part_bytes;
+}
 
 // Stages x (M rows of cols int8) into the MFMA operand order at ws (gemm_stage_bytes(cols, M) bytes): the staged
 // activations of one call serve every matrix with cols columns.
@@ -441,16 +443,18 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
 
 // ---- one token group (M <= 32): one launch ------------------------------------------------------------------------
 
-// Workgroup (c, kz): kSmallWaves waves, wave w the 64-row tile kSmallWaves c + w, over the kSmallSteps K steps of slice
-// kz. The workgroup first builds the B fragments of its whole slice in LDS straight from X (the staging of
-// gemm_stage_kernel, thread (step, half, token)), so no staging kernel runs; then each wave loads all its weights of
-// the slice at once (2 chunks x kSmallSteps steps per lane, every load unconditional) and multiplies them with no
-// further barrier. With one slice the wave writes Y; otherwise it stores its slice's sums, which
-// gemm_small_finish_kernel adds. (Gathering them in the kernel instead, each tile's last slice reading the others'
-// sums with agent-scope atomic loads after a ticket, was slower: 30-160 us per call at M = 8-32.)
-constexpr uint32_t kSmallSteps = 8;  // K steps per slice at most (40 KiB of B fragments in LDS)
-
-constexpr int kSmallWaves = 4;
+// Workgroup (c, kz): W waves, wave w the 64-row tile W c + w, over the K steps of slice kz (at most kSmallSteps),
+// for T token groups of 32. Each thread first loads the activations of its B-fragment tasks (task = step, token
+// group, half, token) and the trit table's entries, then each wave loads all its weights of the slice at once (2
+// chunks x kSmallSteps steps per lane, every load unconditional: steps past the slice read its last step again), so
+// the wait for the activations and the table does
+// not include the weights' latency (loads return in order); the
+// workgroup then builds the trit table and the slice's B fragments in LDS (the staging of gemm_stage_kernel, so no
+// staging kernel runs) and each wave multiplies with no further barrier. With one slice the wave writes Y; otherwise
+// it stores its slice's sums, which gemm_small_finish_kernel adds. (Gathering them in the kernel instead, each tile's
+// last slice reading the others' sums with agent-scope atomic loads after a ticket, was slower: 30-160 us per call
+// at M = 8-32.)
+constexpr uint32_t kSmallSteps = 8;  // K steps per slice at most (40 KiB of B fragments per token group in LDS)
 
 struct SmallArgs {
     const uint8_t* w;
@@ -461,16 +465,63 @@ struct SmallArgs {
     uint32_t steps;      // K steps per slice (at most kSmallSteps)
 };
 
-__global__ __launch_bounds__(kSmallWaves * 64) void gemm_small_kernel(SmallArgs a) {
+template <int T, int W>
+__global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
     __shared__ uint32_t tab[256 * 64];
-    __shared__ uint4 bs[kSmallSteps * 5 * 64];
+    __shared__ uint4 bs[kSmallSteps * 5 * T * 64];
+    constexpr uint32_t kTasks = kSmallSteps * T / W;  // B-fragment tasks per thread
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t tile = blockIdx.x * kSmallWaves + wave, kz = blockIdx.y;
+    const uint32_t tile = blockIdx.x * W + wave, kz = blockIdx.y;
     const uint32_t ks0 = kz * a.steps, nst = min(a.steps, a.n_ksteps - ks0);
     const uint32_t half = lane >> 5;
 
-    // the weights first: they are independent of everything below (a tile past the matrix reads the last one)
+    // The activations of this thread's tasks, loaded before the weights with every load at a valid address (no
+    // branch that depends on the thread separates them from the weight loads, and nothing waits for them before the
+    // weights are requested). When every row of x is 16-byte aligned: a whole 160-column block as 5 uint4 (kind 1);
+    // when the slice's last step is the partial last block, its task (one per thread, a task holding W / T steps) as
+    // the 80 columns of its half (kind 2). Other tasks are read by bytes after the weight loads (kind 0).
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a.x) | a.ldx) & 15u) == 0 && a.cols >= 160u;  // x holds a block
+    const bool has_tail = a.cols % 160u != 0u && ks0 + nst == a.n_ksteps;
+    uint4 X[kTasks][5];
+    uint32_t kind[kTasks];
+#pragma unroll
+    for (uint32_t r = 0; r < kTasks; ++r) {
+        const uint32_t t = tid + r * W * 64u;
+        const uint32_t s = t / (64u * T), rr = t - s * 64u * T, tok = 32u * (rr >> 6) + (rr & 31u), ks = ks0 + s;
+        const uint32_t hs = (rr >> 5) & 1u;
+        const bool live = s < nst && tok < a.M;
+        kind[r] = !live || !aligned ? 0u : (ks < a.cols / 160u ? 1u : 2u);
+        if (aligned) {
+            const int8_t* blk = (kind[r] == 1u ? a.x + static_cast<size_t>(tok) * a.ldx + ks * 160u : a.x) + 16u * hs;
+#pragma unroll
+            for (int e = 0; e < 5; ++e) X[r][e] = *reinterpret_cast<const uint4*>(blk + 32 * e);
+        }
+    }
+    // kind 2, raw: the words at clamped addresses and the bytes of the word that straddles cols (masked where used).
+    // Loaded by every workgroup (from the weights, which are 256-byte aligned, where no partial block is used) so that
+    // no branch joins them before the weight loads.
+    uint32_t V[20], tb[3];
+    {
+        const bool use = has_tail && aligned;
+        const uint32_t t = tid + (nst - 1u) * T / W * W * 64u;
+        const uint32_t s = t / (64u * T), rr = t - s * 64u * T, tok = 32u * (rr >> 6) + (rr & 31u), hs = (rr >> 5) & 1u;
+        const int8_t* row = use ? a.x + static_cast<size_t>(tok < a.M ? tok : 0u) * a.ldx : reinterpret_cast<const int8_t*>(a.w);
+        const uint32_t base = use ? (a.n_ksteps - 1u) * 160u + 80u * hs : 0u, lastw = use ? (a.cols - 4u) & ~3u : 0u;
+        const uint32_t i0 = use ? a.cols & ~3u : 0u, lastb = use ? a.cols - 1u : 0u;
+#pragma unroll
+        for (uint32_t d = 0; d < 20; ++d) V[d] = *reinterpret_cast<const uint32_t*>(row + min(base + 4u * d, lastw));
+#pragma unroll
+        for (uint32_t e = 0; e < 3; ++e) tb[e] = static_cast<uint8_t>(row[min(i0 + e, lastb)]);
+    }
+
+    // the trit table's entries (256 x 8 uint4 stores of 4 copies each)
+    constexpr uint32_t kTabPer = 256u * 8u / (W * 64u);
+    uint32_t te[kTabPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kTabPer; ++r) te[r] = g_gemm_trits.v[(tid + r * W * 64u) >> 3];
+
+    // the weights (a tile past the matrix reads the last one)
     const uint32_t ltile = min(tile, a.n_tiles - 1u);
     const uint32_t grp = ltile / kTileGroup, t16 = ltile - grp * kTileGroup;
     const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup);
@@ -484,60 +535,84 @@ __global__ __launch_bounds__(kSmallWaves * 64) void gemm_small_kernel(SmallArgs 
             wv[s][rb] = __builtin_nontemporal_load((g_u4g*)(wbase + static_cast<size_t>(q) * Tg * 1024u + rb * 512u));
     }
 
-    for (uint32_t i = tid; i < 256u * 8u; i += kSmallWaves * 64u) {
-        const uint32_t e = g_gemm_trits.v[i >> 3];
-        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) = make_uint4(e, e, e, e);
+#pragma unroll
+    for (uint32_t r = 0; r < kTabPer; ++r) {
+        const uint32_t i = tid + r * W * 64u;
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + (i >> 3) * 256u + (i & 7u) * 16u) =
+            make_uint4(te[r], te[r], te[r], te[r]);
     }
-    // B fragments of the slice: task (step s, half hs, token j); tokens past M get zeros
-    for (uint32_t t = tid; t < nst * 64u; t += kSmallWaves * 64u) {
-        const uint32_t s = t >> 6, hs = (t >> 5) & 1u, j = t & 31u, ks = ks0 + s;
+    // B fragments of the slice; tokens past M get zeros
+#pragma unroll
+    for (uint32_t r = 0; r < kTasks; ++r) {
+        const uint32_t t = tid + r * W * 64u;
+        const uint32_t s = t / (64u * T), rr = t - s * 64u * T, g = rr >> 6, hs = (rr >> 5) & 1u, j = rr & 31u;
+        const uint32_t tok = 32u * g + j, ks = ks0 + s;
+        if (s >= nst) continue;
         uint4 o[5] = {};
-        if (j < a.M) {
-            const int8_t* xr = a.x + static_cast<size_t>(j) * a.ldx;
-            if (ks < a.cols / 160u && (reinterpret_cast<uintptr_t>(xr) & 15u) == 0) {
-                const int8_t* blk = xr + ks * 160u + 16u * hs;
-                uint4 X[5];
+        if (kind[r] == 1u) {
 #pragma unroll
-                for (int e = 0; e < 5; ++e) X[e] = *reinterpret_cast<const uint4*>(blk + 32 * e);
+            for (int kb = 0; kb < 4; ++kb) {
+                auto dw = [&](const uint4& v) { return kb == 0 ? v.x : (kb == 1 ? v.y : (kb == 2 ? v.z : v.w)); };
+                const uint32_t a0 = dw(X[r][0]), a1 = dw(X[r][1]), a2 = dw(X[r][2]), a3 = dw(X[r][3]);
+                const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u), hi01 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
+                const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u), hi23 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
+                o[kb] = make_uint4(__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
+                                   __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u));
+            }
+            o[4] = X[r][4];
+        } else if (kind[r] == 2u) {
+            // column ks * 160 + 80 hs + 5 k + p of the partial block is byte 5 k + p of the 80 loaded
+            const uint32_t base = ks * 160u + 80u * hs, i0 = a.cols & ~3u;
+            auto byte_at = [&](uint32_t i) -> uint32_t {
+                const uint32_t c = base + i;
+                return c < i0 ? (V[i >> 2] >> (8u * (i & 3u))) & 0xffu : (c < a.cols ? tb[c & 3u] : 0u);
+            };
 #pragma unroll
-                for (int kb = 0; kb < 4; ++kb) {
-                    auto dw = [&](const uint4& v) { return kb == 0 ? v.x : (kb == 1 ? v.y : (kb == 2 ? v.z : v.w)); };
-                    const uint32_t a0 = dw(X[0]), a1 = dw(X[1]), a2 = dw(X[2]), a3 = dw(X[3]);
-                    const uint32_t lo01 = __builtin_amdgcn_perm(a1, a0, 0x05010400u), hi01 = __builtin_amdgcn_perm(a1, a0, 0x07030602u);
-                    const uint32_t lo23 = __builtin_amdgcn_perm(a3, a2, 0x05010400u), hi23 = __builtin_amdgcn_perm(a3, a2, 0x07030602u);
-                    o[kb] = make_uint4(__builtin_amdgcn_perm(lo23, lo01, 0x05040100u), __builtin_amdgcn_perm(lo23, lo01, 0x07060302u),
-                                       __builtin_amdgcn_perm(hi23, hi01, 0x05040100u), __builtin_amdgcn_perm(hi23, hi01, 0x07060302u));
+            for (uint32_t kb = 0; kb < 5; ++kb) {
+                uint32_t w[4];
+#pragma unroll
+                for (uint32_t d = 0; d < 4; ++d) {
+                    uint32_t v = 0;
+#pragma unroll
+                    for (uint32_t e = 0; e < 4; ++e)
+                        v |= byte_at(kb < 4 ? 5u * (4u * kb + d) + e : 5u * (4u * d + e) + 4u) << (8 * e);
+                    w[d] = v;
                 }
-                o[4] = X[4];
-            } else {
-                const bool tail = ks >= a.cols / 160u;
-                auto act = [&](uint32_t k, uint32_t p) -> uint32_t {
-                    const uint32_t idx = tail ? ks * 160u + 5u * (16u * hs + k) + p : ks * 160u + 32u * p + 16u * hs + k;
-                    return idx < a.cols ? static_cast<uint32_t>(static_cast<uint8_t>(xr[idx])) : 0u;
-                };
+                o[kb] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        } else if (tok < a.M) {
+            const int8_t* xr = a.x + static_cast<size_t>(tok) * a.ldx;
+            const bool tail = ks >= a.cols / 160u;
+            auto act = [&](uint32_t k, uint32_t p) -> uint32_t {
+                const uint32_t idx = tail ? ks * 160u + 5u * (16u * hs + k) + p : ks * 160u + 32u * p + 16u * hs + k;
+                return idx < a.cols ? static_cast<uint32_t>(static_cast<uint8_t>(xr[idx])) : 0u;
+            };
 #pragma unroll
-                for (uint32_t kb = 0; kb < 5; ++kb) {
-                    uint32_t w[4];
+            for (uint32_t kb = 0; kb < 5; ++kb) {
+                uint32_t w[4];
 #pragma unroll
-                    for (uint32_t d = 0; d < 4; ++d) {
-                        uint32_t v = 0;
+                for (uint32_t d = 0; d < 4; ++d) {
+                    uint32_t v = 0;
 #pragma unroll
-                        for (uint32_t e = 0; e < 4; ++e) v |= (kb < 4 ? act(4u * kb + d, e) : act(4u * d + e, 4u)) << (8 * e);
-                        w[d] = v;
-                    }
-                    o[kb] = make_uint4(w[0], w[1], w[2], w[3]);
+                    for (uint32_t e = 0; e < 4; ++e) v |= (kb < 4 ? act(4u * kb + d, e) : act(4u * d + e, 4u)) << (8 * e);
+                    w[d] = v;
                 }
+                o[kb] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
 #pragma unroll
-        for (uint32_t kb = 0; kb < 5; ++kb) bs[(s * 5u + kb) * 64u + j + 32u * hs] = o[kb];
+        for (uint32_t kb = 0; kb < 5; ++kb) bs[((s * 5u + kb) * T + g) * 64u + j + 32u * hs] = o[kb];
     }
     __syncthreads();
     if (tile >= a.n_tiles) return;
 
     const char* tabb = reinterpret_cast<const char*>(tab);
     const uint32_t lane_off = (lane & 31u) * 4u;
-    v16i acc[2] = {v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}, v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0}};
+    v16i acc[2][T];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int g = 0; g < T; ++g) acc[rb][g] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
     for (uint32_t s = 0; s < kSmallSteps; ++s) {
         if (s >= nst) break;
@@ -562,34 +637,38 @@ __global__ __launch_bounds__(kSmallWaves * 64) void gemm_small_kernel(SmallArgs 
         }
 #pragma unroll
         for (int kb = 0; kb < 5; ++kb) {
-            const uint4 b = bs[(s * 5u + kb) * 64u + lane];
-            const v4i B = v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
-            acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0][kb], B, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1][kb], B, acc[1], 0, 0, 0);
+#pragma unroll
+            for (int g = 0; g < T; ++g) {
+                const uint4 b = bs[((s * 5u + kb) * T + g) * 64u + lane];
+                const v4i B = v4i{static_cast<int>(b.x), static_cast<int>(b.y), static_cast<int>(b.z), static_cast<int>(b.w)};
+                acc[0][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[0][kb], B, acc[0][g], 0, 0, 0);
+                acc[1][g] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A[1][kb], B, acc[1][g], 0, 0, 0);
+            }
         }
     }
-    // C of block rb: lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4 of the block, token l % 32
-    const uint32_t m = lane & 31u;
-    if (a.kslices == 1) {
-        if (m < a.M) {
+    // C of (block rb, token group g): lane l, register r -> row 8 (r / 4) + 4 (l / 32) + r % 4 of the block, token
+    // 32 g + l % 32
+#pragma unroll
+    for (int g = 0; g < T; ++g) {
+        const uint32_t m = 32u * g + (lane & 31u);
+        if (m >= a.M) continue;
+        if (a.kslices == 1) {
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const uint32_t n = tile * 64u + rb * 32u + 8u * (r / 4) + 4u * half + (r % 4);
-                    if (n < a.rows) a.y[static_cast<size_t>(m) * a.ldy + n] = acc[rb][r];
+                    if (n < a.rows) a.y[static_cast<size_t>(m) * a.ldy + n] = acc[rb][g][r];
                 }
+        } else {  // the slice's sums; gemm_small_finish_kernel adds the slices
+            int32_t* pp = a.part + (static_cast<size_t>(kz) * a.M + m) * a.rows_p + tile * 64u;
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4)
+                    *reinterpret_cast<int4*>(pp + rb * 32u + 8u * r4 + 4u * half) =
+                        make_int4(acc[rb][g][4 * r4], acc[rb][g][4 * r4 + 1], acc[rb][g][4 * r4 + 2], acc[rb][g][4 * r4 + 3]);
         }
-        return;
-    }
-    if (m < a.M) {  // the slice's sums; gemm_small_finish_kernel adds the slices
-        int32_t* pp = a.part + (static_cast<size_t>(kz) * a.M + m) * a.rows_p + tile * 64u;
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-                *reinterpret_cast<int4*>(pp + rb * 32u + 8u * r4 + 4u * half) =
-                    make_int4(acc[rb][4 * r4], acc[rb][4 * r4 + 1], acc[rb][4 * r4 + 2], acc[rb][4 * r4 + 3]);
     }
 }
 
@@ -611,41 +690,50 @@ __global__ __launch_bounds__(256) void gemm_small_finish_kernel(SmallArgs a) {
     a.y[static_cast<size_t>(m) * a.ldy + n] = (s0 + s1) + (s2 + s3);
 }
 
-// K steps per slice: the count from 2 to kSmallSteps that minimises rounds x steps, a round being one workgroup per CU
-// (the trit table and the B fragments take 104 KiB of LDS); on a tie the longer slices (fewer sums to add).
-static uint32_t small_steps(const Geometry& g, int num_cus) {
+// The small kernel's shape: waves per workgroup (4 or 8) and K steps per slice (2 to kSmallSteps). A round is one
+// workgroup per CU (the trit table and the B fragments take 104-144 KiB of LDS); a round costs about 3 K steps of
+// loads and staging plus its K steps, each T x W / 4 one-wave steps of matrix-core work per SIMD, and the finish
+// about a quarter step per slice (measured at the configs[2] shapes). The cheapest pair; on a tie the longer slices.
+struct SmallShape {
+    uint32_t waves, steps, kslices;
+};
+
+static SmallShape small_shape(const Geometry& g, int num_cus, size_t M) {
     const uint64_t n_ksteps = (g.n_chunks + kStepChunks - 1) / kStepChunks;
-    const uint64_t cols = (g.n_tiles + kSmallWaves - 1) / kSmallWaves;
     const uint64_t cus = static_cast<uint64_t>(std::max(num_cus, 1));
-    uint64_t best = ~0ull;
-    uint32_t best_st = kSmallSteps;
-    for (uint32_t st = kSmallSteps; st >= 2; --st) {
-        const uint64_t wgs = cols * ((n_ksteps + st - 1) / st);
-        const uint64_t cost = (wgs + cus - 1) / cus * st;
-        if (cost < best) {
-            best = cost;
-            best_st = st;
+    const double T = M <= 32 ? 1.0 : 2.0;
+    double best = 1e300;
+    SmallShape sh{4, kSmallSteps, 1};
+    for (uint32_t st = kSmallSteps; st >= 2; --st)
+        for (uint32_t w : {4u, 8u}) {
+            const uint64_t ks = (n_ksteps + st - 1) / st;
+            const uint64_t rounds = ((g.n_tiles + w - 1) / w * ks + cus - 1) / cus;
+            const double cost = static_cast<double>(rounds) * (3.0 + st * T * w / 4.0) + (ks > 1 ? 0.25 * ks : 0.0);
+            if (cost < best - 1e-9) {
+                best = cost;
+                sh = SmallShape{w, st, static_cast<uint32_t>(ks)};
+            }
         }
-    }
-    return best_st;
+    return sh;
 }
 
-static uint32_t small_kslices(const Geometry& g, int num_cus) {
-    const uint32_t n_ksteps = static_cast<uint32_t>((g.n_chunks + kStepChunks - 1) / kStepChunks);
-    const uint32_t st = small_steps(g, num_cus);
-    return (n_ksteps + st - 1) / st;
-}
+static uint32_t small_kslices(const Geometry& g, int num_cus, size_t M) { return small_shape(g, num_cus, M).kslices; }
 
-static bool small_path(size_t M) { return M <= 32; }
+// M <= 32 always; 33-64 tokens (two token groups) only for matrices of at most 128 tiles (8192 rows), where the
+// slices are few rows and long K: at 23040 x 3072 the staged kernel was faster (28.4 against 31.0 us at M = 64),
+// at 3072 x 23040 slower (24.0 against 20.0 us).
+static bool small_path(const Geometry& g, size_t M) { return M <= 32 || (M <= 64 && g.n_tiles <= 128); }
+
+bool gemm_small_path(const Geometry& g, size_t M) { return small_path(g, M); }
 
 static size_t small_part_bytes(const Geometry& g, size_t M, int num_cus) {
-    const uint32_t ks = small_kslices(g, num_cus);
+    const uint32_t ks = small_kslices(g, num_cus, M);
     return ks > 1 ? round_up(static_cast<size_t>(ks) * M * g.padded_rows * 4u, 256) : 0;
 }
 
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream) {
-    if (small_path(M)) {
+    if (small_path(g, M)) {
         SmallArgs a{};
         a.w = w;
         a.x = x;
@@ -660,10 +748,17 @@ int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* 
         a.n_chunks = static_cast<uint32_t>(g.n_chunks);
         a.n_ksteps = static_cast<uint32_t>((g.n_chunks + kStepChunks - 1) / kStepChunks);
         a.M = static_cast<uint32_t>(M);
-        a.kslices = small_kslices(g, num_cus);
-        a.steps = small_steps(g, num_cus);
-        const dim3 grid((a.n_tiles + kSmallWaves - 1) / kSmallWaves, a.kslices);
-        hipLaunchKernelGGL(gemm_small_kernel, grid, dim3(kSmallWaves * 64), 0, stream, a);
+        const SmallShape sh = small_shape(g, num_cus, M);
+        a.kslices = sh.kslices;
+        a.steps = sh.steps;
+        const dim3 grid((a.n_tiles + sh.waves - 1) / sh.waves, a.kslices), block(sh.waves * 64);
+        if (M <= 32) {
+            if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<1, 8>), grid, block, 0, stream, a);
+            else hipLaunchKernelGGL((gemm_small_kernel<1, 4>), grid, block, 0, stream, a);
+        } else {
+            if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<2, 8>), grid, block, 0, stream, a);
+            else hipLaunchKernelGGL((gemm_small_kernel<2, 4>), grid, block, 0, stream, a);
+        }
         VX_HIP(hipGetLastError());
         if (a.kslices > 1) {
             hipLaunchKernelGGL(gemm_small_finish_kernel, dim3((a.rows + 255u) / 256u, a.M), dim3(256), 0, stream, a);

@@ -168,12 +168,14 @@ int launch_digit_sums(const uint8_t* w, const Geometry& g, int32_t* dsum, hipStr
 int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
 int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
-// M <= 32 runs without a staging kernel (gemm_small_kernel builds the B fragments in LDS from x; a finish kernel adds
-// the K slices when there are several); larger M as staging + GEMM + finish.
+// Up to 64 tokens (gemm_small_path) a call runs without a staging kernel (gemm_small_kernel builds the B fragments
+// in LDS from x; a finish kernel adds the K slices when there are several) and needs gemm_part_bytes of workspace;
+// otherwise it runs as staging + GEMM + finish.
+bool gemm_small_path(const Geometry& g, size_t M);
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream);
 // The two halves of launch_gemm: staging of the activations (shared by every matrix with the same cols) and the
-// product; gemm_workspace_bytes = gemm_stage_bytes + gemm_part_bytes.
+// product; gemm_workspace_bytes = gemm_stage_bytes + gemm_part_bytes outside the small path.
 size_t gemm_stage_bytes(size_t cols, size_t M);
 size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus);
 int launch_gemm_stage(const int8_t* x, size_t M, size_t ldx, size_t cols, uint8_t* ws, hipStream_t stream);

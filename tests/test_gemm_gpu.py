@@ -42,7 +42,8 @@ def gemm(torch, layer, x, ldx=None):
 
 
 @pytest.mark.parametrize("rows,cols,m", [(64, 160, 1), (1, 1, 3), (65, 161, 13), (130, 3072, 8), (1100, 321, 17),
-                                         (200, 4096, 33), (3, 23040, 5), (1024, 3072, 64), (70, 2560, 100)])
+                                         (200, 4096, 33), (3, 23040, 5), (1024, 3072, 64), (70, 2560, 100),
+                                         (300, 6912, 40), (64, 23040, 64), (129, 1, 63), (65, 3200, 65)])
 def test_gemm_equals_bruteforce(torch_dev, oracle, rows, cols, m):
     from quintrit_amd import VelurexHipLayer
     print(f"[gemm bruteforce] {rows}x{cols} m={m}", flush=True)
@@ -79,7 +80,7 @@ def test_gemm_config2_equals_gemv_per_token(torch_dev, oracle, rows, cols):
     t = oracle.gen_trits(0xC2 + rows, (rows, cols))
     layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, 1.0)
     rng = np.random.default_rng(rows)
-    for m in (8, 32, 128, 512):
+    for m in (8, 32, 48, 64, 128, 512):
         print(f"[gemm config2] {rows}x{cols} m={m}", flush=True)
         x = np.stack([oracle.quantize_i8(rng.standard_normal(cols).astype(np.float32))[0] for _ in range(m)])
         got = gemm(torch, layer, x)
