@@ -443,10 +443,10 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
 
 // ---- one token group (M <= 32): one launch ------------------------------------------------------------------------
 
-// Workgroup (c, kz): W waves, wave w the 64-row tile W c + w, over the K steps of slice kz (at most kSmallSteps),
-// for T token groups of 32. Each thread first loads the activations of its B-fragment tasks (task = step, token
+// Workgroup (c, kz): W waves, wave w the 64-row tile W c + w, over the K steps of slice kz (at most
+// small_max_steps(T)), for T token groups of 32 (1, 2 or 4). Each thread first loads the activations of its B-fragment tasks (task = step, token
 // group, half, token) and the trit table's entries, then each wave loads all its weights of the slice at once (2
-// chunks x kSmallSteps steps per lane, every load unconditional: steps past the slice read its last step again), so
+// chunks per K step per lane, every load unconditional: steps past the slice read its last step again), so
 // the wait for the activations and the table does
 // not include the weights' latency (loads return in order); the
 // workgroup then builds the trit table and the slice's B fragments in LDS (the staging of gemm_stage_kernel, so no
@@ -456,20 +456,24 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
 // at M = 8-32.)
 constexpr uint32_t kSmallSteps = 8;  // K steps per slice at most (40 KiB of B fragments per token group in LDS)
 
+// K steps per slice at most for T token groups: the B fragments stay within 80 KiB of LDS (the table takes 64 KiB).
+constexpr uint32_t small_max_steps(int T) { return T <= 2 ? kSmallSteps : kSmallSteps / 2; }
+
 struct SmallArgs {
     const uint8_t* w;
     const int8_t* x;
     int32_t* y;
     int32_t* part;       // [kslices][M][rows_p] slice sums (kslices > 1)
     uint32_t ldx, ldy, rows, rows_p, cols, n_tiles, n_chunks, n_ksteps, M, kslices;
-    uint32_t steps;      // K steps per slice (at most kSmallSteps)
+    uint32_t steps;      // K steps per slice (at most small_max_steps(T))
 };
 
 template <int T, int W>
 __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
     __shared__ uint32_t tab[256 * 64];
-    __shared__ uint4 bs[kSmallSteps * 5 * T * 64];
-    constexpr uint32_t kTasks = kSmallSteps * T / W;  // B-fragment tasks per thread
+    constexpr uint32_t S = small_max_steps(T);
+    __shared__ uint4 bs[S * 5 * T * 64];
+    constexpr uint32_t kTasks = S * T / W;  // B-fragment tasks per thread
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t tile = blockIdx.x * W + wave, kz = blockIdx.y;
@@ -526,9 +530,9 @@ __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
     const uint32_t grp = ltile / kTileGroup, t16 = ltile - grp * kTileGroup;
     const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup);
     const uint8_t* wbase = a.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + t16) * 1024u + (lane & 31u) * 16u;
-    u32x4g wv[kSmallSteps][2];
+    u32x4g wv[S][2];
 #pragma unroll
-    for (uint32_t s = 0; s < kSmallSteps; ++s) {
+    for (uint32_t s = 0; s < S; ++s) {
         const uint32_t q = min((ks0 + min(s, nst - 1u)) * kStepChunks + half, a.n_chunks - 1u);
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb)
@@ -614,7 +618,7 @@ __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
 #pragma unroll
         for (int g = 0; g < T; ++g) acc[rb][g] = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-    for (uint32_t s = 0; s < kSmallSteps; ++s) {
+    for (uint32_t s = 0; s < S; ++s) {
         if (s >= nst) break;
         const bool inside = (ks0 + s) * kStepChunks + half < a.n_chunks;
         v4i A[2][5];
@@ -690,7 +694,7 @@ __global__ __launch_bounds__(256) void gemm_small_finish_kernel(SmallArgs a) {
     a.y[static_cast<size_t>(m) * a.ldy + n] = (s0 + s1) + (s2 + s3);
 }
 
-// The small kernel's shape: waves per workgroup (4 or 8) and K steps per slice (2 to kSmallSteps). A round is one
+// The small kernel's shape: waves per workgroup (4 or 8) and K steps per slice (2 to small_max_steps). A round is one
 // workgroup per CU (the trit table and the B fragments take 104-144 KiB of LDS); a round costs about 3 K steps of
 // loads and staging plus its K steps, each T x W / 4 one-wave steps of matrix-core work per SIMD, and the finish
 // about a quarter step per slice (measured at the configs[2] shapes). The cheapest pair; on a tie the longer slices.
@@ -701,10 +705,12 @@ struct SmallShape {
 static SmallShape small_shape(const Geometry& g, int num_cus, size_t M) {
     const uint64_t n_ksteps = (g.n_chunks + kStepChunks - 1) / kStepChunks;
     const uint64_t cus = static_cast<uint64_t>(std::max(num_cus, 1));
-    const double T = M <= 32 ? 1.0 : 2.0;
+    const int Ti = M <= 32 ? 1 : (M <= 64 ? 2 : 4);
+    const double T = Ti;
+    const uint32_t S = small_max_steps(Ti);
     double best = 1e300;
-    SmallShape sh{4, kSmallSteps, 1};
-    for (uint32_t st = kSmallSteps; st >= 2; --st)
+    SmallShape sh{4, S, 1};
+    for (uint32_t st = S; st >= 2; --st)
         for (uint32_t w : {4u, 8u}) {
             const uint64_t ks = (n_ksteps + st - 1) / st;
             const uint64_t rounds = ((g.n_tiles + w - 1) / w * ks + cus - 1) / cus;
@@ -719,10 +725,13 @@ static SmallShape small_shape(const Geometry& g, int num_cus, size_t M) {
 
 static uint32_t small_kslices(const Geometry& g, int num_cus, size_t M) { return small_shape(g, num_cus, M).kslices; }
 
-// M <= 32 always; 33-64 tokens (two token groups) only for matrices of at most 128 tiles (8192 rows), where the
-// slices are few rows and long K: at 23040 x 3072 the staged kernel was faster (28.4 against 31.0 us at M = 64),
-// at 3072 x 23040 slower (24.0 against 20.0 us).
-static bool small_path(const Geometry& g, size_t M) { return M <= 32 || (M <= 64 && g.n_tiles <= 128); }
+// M <= 32 always; 33-128 tokens (two or four token groups) only for matrices of at most 128 tiles (8192 rows) and
+// 32768 columns (a bounded slice workspace): at 23040 x 3072 the staged kernel was faster (28.4 against 31.0 us at
+// M = 64, 41.5 against 42.6 us at M = 128), at 3072 x 23040 and 3072 x 3072 slower (24.0 against 20.0 us at M = 64;
+// 34.8 against 33.4 and 24.0 against 19.9 us at M = 128).
+static bool small_path(const Geometry& g, size_t M) {
+    return M <= 32 || (M <= 128 && g.n_tiles <= 128 && g.cols <= 32768);
+}
 
 bool gemm_small_path(const Geometry& g, size_t M) { return small_path(g, M); }
 
@@ -755,9 +764,12 @@ int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* 
         if (M <= 32) {
             if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<1, 8>), grid, block, 0, stream, a);
             else hipLaunchKernelGGL((gemm_small_kernel<1, 4>), grid, block, 0, stream, a);
-        } else {
+        } else if (M <= 64) {
             if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<2, 8>), grid, block, 0, stream, a);
             else hipLaunchKernelGGL((gemm_small_kernel<2, 4>), grid, block, 0, stream, a);
+        } else {
+            if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<4, 8>), grid, block, 0, stream, a);
+            else hipLaunchKernelGGL((gemm_small_kernel<4, 4>), grid, block, 0, stream, a);
         }
         VX_HIP(hipGetLastError());
         if (a.kslices > 1) {

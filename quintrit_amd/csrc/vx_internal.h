@@ -168,9 +168,9 @@ int launch_digit_sums(const uint8_t* w, const Geometry& g, int32_t* dsum, hipStr
 int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
 int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
-// Up to 64 tokens (gemm_small_path) a call runs without a staging kernel (gemm_small_kernel builds the B fragments
-// in LDS from x; a finish kernel adds the K slices when there are several) and needs gemm_part_bytes of workspace;
-// otherwise it runs as staging + GEMM + finish.
+// Up to 32 tokens, and up to 128 on matrices of at most 8192 rows and 32768 columns (gemm_small_path), a call runs
+// without a staging kernel (gemm_small_kernel builds the B fragments in LDS from x; a finish kernel adds the K slices
+// when there are several) and needs gemm_part_bytes of workspace; otherwise it runs as staging + GEMM + finish.
 bool gemm_small_path(const Geometry& g, size_t M);
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream);

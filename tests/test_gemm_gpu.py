@@ -43,7 +43,8 @@ def gemm(torch, layer, x, ldx=None):
 
 @pytest.mark.parametrize("rows,cols,m", [(64, 160, 1), (1, 1, 3), (65, 161, 13), (130, 3072, 8), (1100, 321, 17),
                                          (200, 4096, 33), (3, 23040, 5), (1024, 3072, 64), (70, 2560, 100),
-                                         (300, 6912, 40), (64, 23040, 64), (129, 1, 63), (65, 3200, 65)])
+                                         (300, 6912, 40), (64, 23040, 64), (129, 1, 63), (65, 3200, 65),
+                                         (1100, 6913, 97), (8192, 321, 128), (8193, 320, 128)])
 def test_gemm_equals_bruteforce(torch_dev, oracle, rows, cols, m):
     from quintrit_amd import VelurexHipLayer
     print(f"[gemm bruteforce] {rows}x{cols} m={m}", flush=True)
