@@ -2882,6 +2882,13 @@ static int ensure_prefill(vx_decoder* d) {
         const Geometry& g = d->proj[k]->g;  // every layer's projection k has this shape
         for (uint32_t m = 1; m <= cap; ++m) part_bytes = std::max(part_bytes, gemm_part_bytes(g, m, d->num_cus));
     }
+    {  // q, k and v in one launch (record_prefill)
+        GemmSub qkv[3];
+        for (int k = 0; k < 3; ++k) qkv[k] = GemmSub{nullptr, &d->proj[VX_PROJ_Q + k]->g, nullptr, 0};
+        for (uint32_t m = 1; m <= cap; ++m)
+            if (gemm_group_small_path(qkv, 3, m))
+                part_bytes = std::max(part_bytes, gemm_group_part_bytes(qkv, 3, m, d->num_cus));
+    }
     hipError_t e = hipSuccess;
     auto grab = [&](auto** p, size_t bytes) {
         if (e == hipSuccess) e = dalloc(d, p, std::max<size_t>(bytes, 256));
@@ -2968,8 +2975,18 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
             in.a = pf_proj_out(d, l - 1, VX_PROJ_DOWN, as_down);
         }
         VX_TRY(stage(in, static_cast<uint32_t>(H), d->pf_ld[VX_PROJ_DOWN], as_qkv));
-        VX_TRY(gemm_stage(H, {VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}));
-        for (int k : {VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}) VX_TRY(gemm(l, k));
+        // q, k and v in one small-path launch where their concatenation takes that path
+        GemmSub qkv[3];
+        for (int k = 0; k < 3; ++k) {
+            const vx_matrix* m = d->proj[l * kProjKinds + VX_PROJ_Q + k];
+            qkv[k] = GemmSub{m->d_w, &m->g, d->pf_y[VX_PROJ_Q + k], d->pf_ld[VX_PROJ_Q + k]};
+        }
+        if (gemm_group_small_path(qkv, 3, n)) {
+            VX_TRY(launch_gemm_group(qkv, 3, d->num_cus, d->pf_codes, n, d->pf_codes_ld, d->pf_part, st));
+        } else {
+            VX_TRY(gemm_stage(H, {VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}));
+            for (int k : {VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}) VX_TRY(gemm(l, k));
+        }
         PfRopeArgs ra{};
         ra.ctl = d->d_ctl;
         ra.n_tok = n;

@@ -444,7 +444,8 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
 // ---- one token group (M <= 32): one launch ------------------------------------------------------------------------
 
 // Workgroup (c, kz): W waves, wave w the 64-row tile W c + w, over the K steps of slice kz (at most
-// small_max_steps(T)), for T token groups of 32 (1, 2 or 4). Each thread first loads the activations of its B-fragment tasks (task = step, token
+// small_max_steps(T)), for T token groups of 32 (1, 2 or 4). G: the call's tiles may belong to several matrices of the
+// same columns (each wave finds its own; without G the instance reads only the first). Each thread first loads the activations of its B-fragment tasks (task = step, token
 // group, half, token) and the trit table's entries, then each wave loads all its weights of the slice at once (2
 // chunks per K step per lane, every load unconditional: steps past the slice read its last step again), so
 // the wait for the activations and the table does
@@ -459,16 +460,25 @@ constexpr uint32_t kSmallSteps = 8;  // K steps per slice at most (40 KiB of B f
 // K steps per slice at most for T token groups: the B fragments stay within 80 KiB of LDS (the table takes 64 KiB).
 constexpr uint32_t small_max_steps(int T) { return T <= 2 ? kSmallSteps : kSmallSteps / 2; }
 
-struct SmallArgs {
+// One matrix of a small-path call (up to kSmallSubs matrices with the same columns share a launch): its tiles are
+// tiles tile0 .. tile0 + n_tiles - 1 of the call, its rows rows row0 .. row0 + rows_p - 1 of the slice sums.
+constexpr int kSmallSubs = 3;
+struct SmallSub {
     const uint8_t* w;
-    const int8_t* x;
     int32_t* y;
+    uint32_t ldy, rows, rows_p, n_tiles, tile0, row0;
+};
+
+struct SmallArgs {
+    SmallSub sub[kSmallSubs];
+    uint32_t n_sub;
+    const int8_t* x;
     int32_t* part;       // [kslices][M][rows_p] slice sums (kslices > 1)
-    uint32_t ldx, ldy, rows, rows_p, cols, n_tiles, n_chunks, n_ksteps, M, kslices;
+    uint32_t ldx, rows_p, cols, n_tiles, n_chunks, n_ksteps, M, kslices;  // rows_p, n_tiles: of all the matrices
     uint32_t steps;      // K steps per slice (at most small_max_steps(T))
 };
 
-template <int T, int W>
+template <int T, int W, bool G>
 __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
     __shared__ uint32_t tab[256 * 64];
     constexpr uint32_t S = small_max_steps(T);
@@ -477,6 +487,10 @@ __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t tile = blockIdx.x * W + wave, kz = blockIdx.y;
+    // the wave's matrix (wave-uniform) and its tile there (a tile past the call's tiles falls in the last matrix)
+    const uint32_t j = !G ? 0u : (a.n_sub > 1u && tile >= a.sub[1].tile0 ? 1u : 0u) + (a.n_sub > 2u && tile >= a.sub[2].tile0 ? 1u : 0u);
+    const SmallSub sb = j == 0u ? a.sub[0] : (j == 1u ? a.sub[1] : a.sub[2]);
+    const uint32_t lt = tile - sb.tile0;
     const uint32_t ks0 = kz * a.steps, nst = min(a.steps, a.n_ksteps - ks0);
     const uint32_t half = lane >> 5;
 
@@ -510,7 +524,7 @@ __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
         const bool use = has_tail && aligned;
         const uint32_t t = tid + (nst - 1u) * T / W * W * 64u;
         const uint32_t s = t / (64u * T), rr = t - s * 64u * T, tok = 32u * (rr >> 6) + (rr & 31u), hs = (rr >> 5) & 1u;
-        const int8_t* row = use ? a.x + static_cast<size_t>(tok < a.M ? tok : 0u) * a.ldx : reinterpret_cast<const int8_t*>(a.w);
+        const int8_t* row = use ? a.x + static_cast<size_t>(tok < a.M ? tok : 0u) * a.ldx : reinterpret_cast<const int8_t*>(sb.w);
         const uint32_t base = use ? (a.n_ksteps - 1u) * 160u + 80u * hs : 0u, lastw = use ? (a.cols - 4u) & ~3u : 0u;
         const uint32_t i0 = use ? a.cols & ~3u : 0u, lastb = use ? a.cols - 1u : 0u;
 #pragma unroll
@@ -526,10 +540,10 @@ __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
     for (uint32_t r = 0; r < kTabPer; ++r) te[r] = g_gemm_trits.v[(tid + r * W * 64u) >> 3];
 
     // the weights (a tile past the matrix reads the last one)
-    const uint32_t ltile = min(tile, a.n_tiles - 1u);
+    const uint32_t ltile = min(lt, sb.n_tiles - 1u);
     const uint32_t grp = ltile / kTileGroup, t16 = ltile - grp * kTileGroup;
-    const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup);
-    const uint8_t* wbase = a.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + t16) * 1024u + (lane & 31u) * 16u;
+    const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), sb.n_tiles - grp * kTileGroup);
+    const uint8_t* wbase = sb.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + t16) * 1024u + (lane & 31u) * 16u;
     u32x4g wv[S][2];
 #pragma unroll
     for (uint32_t s = 0; s < S; ++s) {
@@ -661,11 +675,11 @@ __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const uint32_t n = tile * 64u + rb * 32u + 8u * (r / 4) + 4u * half + (r % 4);
-                    if (n < a.rows) a.y[static_cast<size_t>(m) * a.ldy + n] = acc[rb][g][r];
+                    const uint32_t n = lt * 64u + rb * 32u + 8u * (r / 4) + 4u * half + (r % 4);
+                    if (n < sb.rows) sb.y[static_cast<size_t>(m) * sb.ldy + n] = acc[rb][g][r];
                 }
         } else {  // the slice's sums; gemm_small_finish_kernel adds the slices
-            int32_t* pp = a.part + (static_cast<size_t>(kz) * a.M + m) * a.rows_p + tile * 64u;
+            int32_t* pp = a.part + (static_cast<size_t>(kz) * a.M + m) * a.rows_p + sb.row0 + lt * 64u;
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -676,10 +690,14 @@ __global__ __launch_bounds__(W * 64) void gemm_small_kernel(SmallArgs a) {
     }
 }
 
-// Y[m][n] = sum over the slices of gemm_small_kernel's sums (block = 256 rows of one token).
+// Y[m][n] = sum over the slices of gemm_small_kernel's sums (block = 256 rows of the call's slice sums, one token).
+template <bool G>
 __global__ __launch_bounds__(256) void gemm_small_finish_kernel(SmallArgs a) {
     const uint32_t n = blockIdx.x * 256u + threadIdx.x, m = blockIdx.y;
-    if (n >= a.rows) return;
+    const uint32_t j = !G ? 0u : (a.n_sub > 1u && n >= a.sub[1].row0 ? 1u : 0u) + (a.n_sub > 2u && n >= a.sub[2].row0 ? 1u : 0u);
+    const SmallSub sb = j == 0u ? a.sub[0] : (j == 1u ? a.sub[1] : a.sub[2]);  // no indexing of the arguments
+    const uint32_t ln = n - sb.row0;
+    if (n >= a.rows_p || ln >= sb.rows) return;
     const size_t stride = static_cast<size_t>(a.M) * a.rows_p;
     const int32_t* p = a.part + static_cast<size_t>(m) * a.rows_p + n;
     int s0 = 0, s1 = 0, s2 = 0, s3 = 0;
@@ -691,8 +709,9 @@ __global__ __launch_bounds__(256) void gemm_small_finish_kernel(SmallArgs a) {
         s3 += p[(k + 3) * stride];
     }
     for (; k < a.kslices; ++k) s0 += p[k * stride];
-    a.y[static_cast<size_t>(m) * a.ldy + n] = (s0 + s1) + (s2 + s3);
+    sb.y[static_cast<size_t>(m) * sb.ldy + ln] = (s0 + s1) + (s2 + s3);
 }
+
 
 // The small kernel's shape: waves per workgroup (4 or 8) and K steps per slice (2 to small_max_steps). A round is one
 // workgroup per CU (the trit table and the B fragments take 104-144 KiB of LDS); a round costs about 3 K steps of
@@ -740,43 +759,79 @@ static size_t small_part_bytes(const Geometry& g, size_t M, int num_cus) {
     return ks > 1 ? round_up(static_cast<size_t>(ks) * M * g.padded_rows * 4u, 256) : 0;
 }
 
+// The small path over n matrices of the same columns (tiles and slice-sum rows concatenated in order).
+template <bool G>
+static int launch_small(const GemmSub* subs, int n, int num_cus, const int8_t* x, size_t M, size_t ldx, uint8_t* ws,
+                        hipStream_t stream) {
+    SmallArgs a{};
+    a.n_sub = static_cast<uint32_t>(n);
+    uint32_t tiles = 0, rows_p = 0;
+    for (int i = 0; i < n; ++i) {
+        const Geometry& gi = *subs[i].g;
+        a.sub[i] = SmallSub{subs[i].w, subs[i].y, static_cast<uint32_t>(subs[i].ldy), static_cast<uint32_t>(gi.rows),
+                            static_cast<uint32_t>(gi.padded_rows), static_cast<uint32_t>(gi.n_tiles), tiles, rows_p};
+        tiles += static_cast<uint32_t>(gi.n_tiles);
+        rows_p += static_cast<uint32_t>(gi.padded_rows);
+    }
+    const Geometry g = geometry(rows_p, subs[0].g->cols);  // the call's tiles, for the planner
+    a.x = x;
+    a.part = reinterpret_cast<int32_t*>(ws);
+    a.ldx = static_cast<uint32_t>(ldx);
+    a.rows_p = rows_p;
+    a.cols = static_cast<uint32_t>(g.cols);
+    a.n_tiles = tiles;
+    a.n_chunks = static_cast<uint32_t>(g.n_chunks);
+    a.n_ksteps = static_cast<uint32_t>((g.n_chunks + kStepChunks - 1) / kStepChunks);
+    a.M = static_cast<uint32_t>(M);
+    const SmallShape sh = small_shape(g, num_cus, M);
+    a.kslices = sh.kslices;
+    a.steps = sh.steps;
+    const dim3 grid((a.n_tiles + sh.waves - 1) / sh.waves, a.kslices), block(sh.waves * 64);
+    if (M <= 32) {
+        if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<1, 8, G>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_small_kernel<1, 4, G>), grid, block, 0, stream, a);
+    } else if (M <= 64) {
+        if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<2, 8, G>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_small_kernel<2, 4, G>), grid, block, 0, stream, a);
+    } else {
+        if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<4, 8, G>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_small_kernel<4, 4, G>), grid, block, 0, stream, a);
+    }
+    VX_HIP(hipGetLastError());
+    if (a.kslices > 1) {
+        hipLaunchKernelGGL(gemm_small_finish_kernel<G>, dim3((a.rows_p + 255u) / 256u, a.M), dim3(256), 0, stream, a);
+        VX_HIP(hipGetLastError());
+    }
+    return VX_OK;
+}
+
+bool gemm_group_small_path(const GemmSub* subs, int n, size_t M) {
+    if (n < 1 || n > kSmallSubs) return false;
+    size_t rows_p = 0;
+    for (int i = 0; i < n; ++i) {
+        if (subs[i].g->cols != subs[0].g->cols) return false;
+        rows_p += subs[i].g->padded_rows;
+    }
+    return small_path(geometry(rows_p, subs[0].g->cols), M);
+}
+
+size_t gemm_group_part_bytes(const GemmSub* subs, int n, size_t M, int num_cus) {
+    size_t rows_p = 0;
+    for (int i = 0; i < n; ++i) rows_p += subs[i].g->padded_rows;
+    return small_part_bytes(geometry(rows_p, subs[0].g->cols), M, num_cus);
+}
+
+int launch_gemm_group(const GemmSub* subs, int n, int num_cus, const int8_t* x, size_t M, size_t ldx, uint8_t* ws,
+                      hipStream_t stream) {
+    if (!gemm_group_small_path(subs, n, M)) VX_FAIL(VX_ERR_INTERNAL, "a grouped GEMM of %d matrices off the small path", n);
+    return launch_small<true>(subs, n, num_cus, x, M, ldx, ws, stream);
+}
+
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream) {
     if (small_path(g, M)) {
-        SmallArgs a{};
-        a.w = w;
-        a.x = x;
-        a.y = y;
-        a.part = reinterpret_cast<int32_t*>(ws);
-        a.ldx = static_cast<uint32_t>(ldx);
-        a.ldy = static_cast<uint32_t>(ldy);
-        a.rows = static_cast<uint32_t>(g.rows);
-        a.rows_p = static_cast<uint32_t>(g.padded_rows);
-        a.cols = static_cast<uint32_t>(g.cols);
-        a.n_tiles = static_cast<uint32_t>(g.n_tiles);
-        a.n_chunks = static_cast<uint32_t>(g.n_chunks);
-        a.n_ksteps = static_cast<uint32_t>((g.n_chunks + kStepChunks - 1) / kStepChunks);
-        a.M = static_cast<uint32_t>(M);
-        const SmallShape sh = small_shape(g, num_cus, M);
-        a.kslices = sh.kslices;
-        a.steps = sh.steps;
-        const dim3 grid((a.n_tiles + sh.waves - 1) / sh.waves, a.kslices), block(sh.waves * 64);
-        if (M <= 32) {
-            if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<1, 8>), grid, block, 0, stream, a);
-            else hipLaunchKernelGGL((gemm_small_kernel<1, 4>), grid, block, 0, stream, a);
-        } else if (M <= 64) {
-            if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<2, 8>), grid, block, 0, stream, a);
-            else hipLaunchKernelGGL((gemm_small_kernel<2, 4>), grid, block, 0, stream, a);
-        } else {
-            if (sh.waves == 8) hipLaunchKernelGGL((gemm_small_kernel<4, 8>), grid, block, 0, stream, a);
-            else hipLaunchKernelGGL((gemm_small_kernel<4, 4>), grid, block, 0, stream, a);
-        }
-        VX_HIP(hipGetLastError());
-        if (a.kslices > 1) {
-            hipLaunchKernelGGL(gemm_small_finish_kernel, dim3((a.rows + 255u) / 256u, a.M), dim3(256), 0, stream, a);
-            VX_HIP(hipGetLastError());
-        }
-        return VX_OK;
+        const GemmSub sub{w, &g, y, ldy};
+        return launch_small<false>(&sub, 1, num_cus, x, M, ldx, ws, stream);
     }
     VX_TRY(launch_gemm_stage(x, M, ldx, g.cols, ws, stream));
     return launch_gemm_staged(w, g, num_cus, ws, M, y, ldy, ws + gemm_stage_bytes(g.cols, M), stream);

@@ -172,6 +172,19 @@ size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
 // without a staging kernel (gemm_small_kernel builds the B fragments in LDS from x; a finish kernel adds the K slices
 // when there are several) and needs gemm_part_bytes of workspace; otherwise it runs as staging + GEMM + finish.
 bool gemm_small_path(const Geometry& g, size_t M);
+// One matrix of a grouped small-path GEMM: its weights, geometry and output.
+struct GemmSub {
+    const uint8_t* w;
+    const Geometry* g;
+    int32_t* y;
+    size_t ldy;
+};
+// Up to 3 matrices with the same columns in one small-path launch (their tiles concatenated), when the concatenation
+// would take the small path at M tokens; gemm_group_part_bytes of workspace.
+bool gemm_group_small_path(const GemmSub* subs, int n, size_t M);
+size_t gemm_group_part_bytes(const GemmSub* subs, int n, size_t M, int num_cus);
+int launch_gemm_group(const GemmSub* subs, int n, int num_cus, const int8_t* x, size_t M, size_t ldx, uint8_t* ws,
+                      hipStream_t stream);
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream);
 // The two halves of launch_gemm: staging of the activations (shared by every matrix with the same cols) and the
