@@ -3036,8 +3036,19 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
         in.a = pf_proj_out(d, l, VX_PROJ_O, as_o);
         VX_TRY(stage(in, static_cast<uint32_t>(H), d->pf_ld[VX_PROJ_O], as_ffn));
         VX_TRY(gemm_stage(H, {VX_PROJ_GATE, VX_PROJ_UP}));
-        VX_TRY(gemm(l, VX_PROJ_GATE));
-        VX_TRY(gemm(l, VX_PROJ_UP));
+        {
+            // a staged gate/up pair as one launch when that needs no K split (twice the workgroups of one matrix)
+            const vx_matrix* mg = d->proj[l * kProjKinds + VX_PROJ_GATE];
+            const vx_matrix* mu = d->proj[l * kProjKinds + VX_PROJ_UP];
+            if (!small(VX_PROJ_GATE) && !small(VX_PROJ_UP) && d->pf_ld[VX_PROJ_GATE] == d->pf_ld[VX_PROJ_UP] &&
+                mg->g.rows == mu->g.rows && mg->g.cols == mu->g.cols && gemm_staged_pair_ok(mg->g, n, d->num_cus)) {
+                VX_TRY(launch_gemm_staged_pair(mg->d_w, mu->d_w, mg->g, d->num_cus, d->pf_staged, n,
+                                               d->pf_y[VX_PROJ_GATE], d->pf_y[VX_PROJ_UP], d->pf_ld[VX_PROJ_GATE], st));
+            } else {
+                VX_TRY(gemm(l, VX_PROJ_GATE));
+                VX_TRY(gemm(l, VX_PROJ_UP));
+            }
+        }
         PfActArgs aa{};
         aa.yg = d->pf_y[VX_PROJ_GATE];
         aa.yu = d->pf_y[VX_PROJ_UP];

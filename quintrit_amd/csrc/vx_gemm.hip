@@ -120,6 +120,11 @@ struct GemmArgs {
     uint32_t rows, n_tiles, n_chunks, n_ksteps;
     uint32_t M, n_tg, ldy, y_vec4;   // y_vec4: y and ldy allow 16-byte stores
     uint32_t kslices, ksteps_per_slice, rows_p;
+    // a pair of matrices of one geometry in one launch (gemm_kernel's G2): the tiles of w (tiles1 of them), then those
+    // of w2 with outputs y2; n_tiles counts both
+    const uint8_t* w2;
+    int32_t* y2;
+    uint32_t tiles1;
 };
 
 // Workgroup (rg, tt, kz): W waves, wave w taking the R 32-row blocks (W rg + w) R .. + R - 1 of the matrix (block 2 t + h
@@ -127,7 +132,7 @@ struct GemmArgs {
 // of each entry in the first half of a 256-byte row; lane l reads copy l % 32, conflict-free because LDS serves a wave
 // in two 32-lane halves) and two buffers of one K step's B fragments, which every wave reads (a B fragment serves the
 // wave's R blocks, an A fragment its T token groups).
-template <int T, int R, int W>
+template <int T, int R, int W, bool G2>
 __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
     __shared__ uint32_t tab[256 * 64];
     __shared__ uint4 bs[2][5 * T * 64];
@@ -138,8 +143,14 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t blk0 = (blockIdx.x * W + wave) * R;  // the wave's first 32-row block
-    const uint32_t n_blk = 2u * a.n_tiles;
+    const uint32_t blk0 = (blockIdx.x * W + wave) * R;  // the wave's first 32-row block of the launch
+    // G2: the wave's matrix (its R blocks lie in one tile, so in one matrix) and its first block there
+    const bool sec = G2 && blk0 >= 2u * a.tiles1;
+    const uint32_t lb0 = sec ? blk0 - 2u * a.tiles1 : blk0;
+    const uint32_t nt = G2 ? a.tiles1 : a.n_tiles;  // tiles of the wave's matrix
+    const uint8_t* wm = sec ? a.w2 : a.w;
+    int32_t* ym = sec ? a.y2 : a.y;
+    const uint32_t n_blk = 2u * nt;
     const uint32_t tt = blockIdx.y, kz = blockIdx.z;
     const uint32_t ks0 = kz * a.ksteps_per_slice;
     const uint32_t ks1 = min(ks0 + a.ksteps_per_slice, a.n_ksteps);
@@ -159,10 +170,10 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
     uint32_t cstride[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t blk = min(blk0 + r, n_blk - 1u), tile = blk >> 1;
+        const uint32_t blk = min(lb0 + r, n_blk - 1u), tile = blk >> 1;
         const uint32_t grp = tile / kTileGroup, t16 = tile - grp * kTileGroup;
-        const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), a.n_tiles - grp * kTileGroup);
-        wbase[r] = a.w + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + t16) * 1024u + (blk & 1u) * 512u +
+        const uint32_t Tg = min(static_cast<uint32_t>(kTileGroup), nt - grp * kTileGroup);
+        wbase[r] = wm + (static_cast<size_t>(grp) * kTileGroup * a.n_chunks + t16) * 1024u + (blk & 1u) * 512u +
                    (lane & 31u) * 16u;
         cstride[r] = Tg * 1024u;
     }
@@ -256,7 +267,7 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
     VX_LOAD_B(min(ks0 + 1u, last), b10, b11, b12, b13, b14);
     load_w(min(ks0 + 1u, last), w1);
     VX_STORE_B(0, b00, b01, b02, b03, b04);
-    const bool active = blk0 < n_blk;
+    const bool active = blk0 < 2u * a.n_tiles;
 #define VX_STEP(ks, WC, N0, N1, N2, N3, N4, M0, M1, M2, M3, M4, WN)      \
     do {                                                                 \
         VX_LOAD_B(min((ks) + 2u, last), M0, M1, M2, M3, M4);             \
@@ -282,19 +293,19 @@ __global__ __launch_bounds__(W * 64) void gemm_kernel(GemmArgs a) {
         if (m >= a.M) continue;
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            if (blk0 + r >= n_blk) continue;
+            if (lb0 + r >= n_blk) continue;
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) {
-                const uint32_t n = (blk0 + r) * 32u + 8u * r4 + 4u * half;
+                const uint32_t n = (lb0 + r) * 32u + 8u * r4 + 4u * half;
                 const int v0 = acc[r][g][4 * r4], v1 = acc[r][g][4 * r4 + 1];
                 const int v2 = acc[r][g][4 * r4 + 2], v3 = acc[r][g][4 * r4 + 3];
                 if (a.kslices > 1) {
                     *reinterpret_cast<int4*>(a.part + (static_cast<size_t>(kz) * a.n_tg * 32u + m) * a.rows_p + n) =
                         make_int4(v0, v1, v2, v3);
                 } else if (a.y_vec4 && n + 3 < a.rows) {
-                    *reinterpret_cast<int4*>(a.y + static_cast<size_t>(m) * a.ldy + n) = make_int4(v0, v1, v2, v3);
+                    *reinterpret_cast<int4*>(ym + static_cast<size_t>(m) * a.ldy + n) = make_int4(v0, v1, v2, v3);
                 } else {
-                    int32_t* yr = a.y + static_cast<size_t>(m) * a.ldy;
+                    int32_t* yr = ym + static_cast<size_t>(m) * a.ldy;
                     if (n < a.rows) yr[n] = v0;
                     if (n + 1 < a.rows) yr[n + 1] = v1;
                     if (n + 2 < a.rows) yr[n + 2] = v2;
@@ -403,9 +414,23 @@ int launch_gemm_stage(const int8_t* x, size_t M, size_t ldx, size_t cols, uint8_
 
 // The product of matrix w with activations staged by launch_gemm_stage at `staged`; `part` holds
 // gemm_part_bytes(g, M, num_cus) bytes of K-slice partial sums (unused when the plan has one slice).
-int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const uint8_t* staged, size_t M, int32_t* y,
-                       size_t ldy, uint8_t* part, hipStream_t stream) {
-    const GemmPlan p = gemm_plan(g, M, num_cus);
+template <bool G2>
+static void launch_staged_kernel(const GemmPlan& p, const GemmArgs& a, hipStream_t stream) {
+    const dim3 grid(p.grid_x, p.n_tt, p.kslices);
+    const dim3 block(p.W * 64);
+    if (p.W == 8) {
+        if (p.T == 4) hipLaunchKernelGGL((gemm_kernel<4, 2, 8, G2>), grid, block, 0, stream, a);
+        else if (p.T == 2) hipLaunchKernelGGL((gemm_kernel<2, 2, 8, G2>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_kernel<1, 2, 8, G2>), grid, block, 0, stream, a);
+    } else {
+        if (p.T == 4) hipLaunchKernelGGL((gemm_kernel<4, 2, 4, G2>), grid, block, 0, stream, a);
+        else if (p.T == 2) hipLaunchKernelGGL((gemm_kernel<2, 2, 4, G2>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((gemm_kernel<1, 2, 4, G2>), grid, block, 0, stream, a);
+    }
+}
+
+static GemmArgs staged_args(const GemmPlan& p, const uint8_t* w, const Geometry& g, const uint8_t* staged, size_t M,
+                            int32_t* y, size_t ldy, uint8_t* part) {
     GemmArgs a{};
     a.w = w;
     a.xs = reinterpret_cast<const uint4*>(staged);
@@ -422,22 +447,41 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
     a.kslices = p.kslices;
     a.ksteps_per_slice = p.ksteps_per_slice;
     a.rows_p = static_cast<uint32_t>(g.padded_rows);
-    const dim3 grid(p.grid_x, p.n_tt, p.kslices);
-    const dim3 block(p.W * 64);
-    if (p.W == 8) {
-        if (p.T == 4) hipLaunchKernelGGL((gemm_kernel<4, 2, 8>), grid, block, 0, stream, a);
-        else if (p.T == 2) hipLaunchKernelGGL((gemm_kernel<2, 2, 8>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((gemm_kernel<1, 2, 8>), grid, block, 0, stream, a);
-    } else {
-        if (p.T == 4) hipLaunchKernelGGL((gemm_kernel<4, 2, 4>), grid, block, 0, stream, a);
-        else if (p.T == 2) hipLaunchKernelGGL((gemm_kernel<2, 2, 4>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((gemm_kernel<1, 2, 4>), grid, block, 0, stream, a);
-    }
+    return a;
+}
+
+int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const uint8_t* staged, size_t M, int32_t* y,
+                       size_t ldy, uint8_t* part, hipStream_t stream) {
+    const GemmPlan p = gemm_plan(g, M, num_cus);
+    const GemmArgs a = staged_args(p, w, g, staged, M, y, ldy, part);
+    launch_staged_kernel<false>(p, a, stream);
     VX_HIP(hipGetLastError());
     if (p.kslices > 1) {
         hipLaunchKernelGGL(gemm_finish_kernel, dim3((a.rows + 255u) / 256u, static_cast<uint32_t>(M)), dim3(256), 0, stream, a);
         VX_HIP(hipGetLastError());
     }
+    return VX_OK;
+}
+
+// The concatenation of two matrices of one geometry as one launch, when its plan needs no K split.
+static GemmPlan pair_plan(const Geometry& g, size_t M, int num_cus) {
+    return gemm_plan(geometry(2 * g.padded_rows, g.cols), M, num_cus);
+}
+
+bool gemm_staged_pair_ok(const Geometry& g, size_t M, int num_cus) { return pair_plan(g, M, num_cus).kslices == 1; }
+
+int launch_gemm_staged_pair(const uint8_t* w, const uint8_t* w2, const Geometry& g, int num_cus, const uint8_t* staged,
+                            size_t M, int32_t* y, int32_t* y2, size_t ldy, hipStream_t stream) {
+    const GemmPlan p = pair_plan(g, M, num_cus);
+    if (p.kslices != 1) VX_FAIL(VX_ERR_INTERNAL, "a paired GEMM with %u K slices", p.kslices);
+    GemmArgs a = staged_args(p, w, g, staged, M, y, ldy, nullptr);
+    a.n_tiles = static_cast<uint32_t>(2 * g.n_tiles);
+    a.w2 = w2;
+    a.y2 = y2;
+    a.tiles1 = static_cast<uint32_t>(g.n_tiles);
+    a.y_vec4 = a.y_vec4 && reinterpret_cast<uintptr_t>(y2) % 16 == 0 ? 1u : 0u;
+    launch_staged_kernel<true>(p, a, stream);
+    VX_HIP(hipGetLastError());
     return VX_OK;
 }
 

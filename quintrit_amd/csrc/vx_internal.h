@@ -192,6 +192,11 @@ int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* 
 size_t gemm_stage_bytes(size_t cols, size_t M);
 size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus);
 int launch_gemm_stage(const int8_t* x, size_t M, size_t ldx, size_t cols, uint8_t* ws, hipStream_t stream);
+// Two matrices of one geometry (a gated pair) as one staged launch over the same staged activations, when that launch
+// needs no K split (gemm_staged_pair_ok).
+bool gemm_staged_pair_ok(const Geometry& g, size_t M, int num_cus);
+int launch_gemm_staged_pair(const uint8_t* w, const uint8_t* w2, const Geometry& g, int num_cus, const uint8_t* staged,
+                            size_t M, int32_t* y, int32_t* y2, size_t ldy, hipStream_t stream);
 int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const uint8_t* staged, size_t M, int32_t* y,
                        size_t ldy, uint8_t* part, hipStream_t stream);
 // The same GEMM with its workspace in the library's per-device scratch array (kNoAllocScratchBytes): no allocation.
