@@ -2882,12 +2882,16 @@ static int ensure_prefill(vx_decoder* d) {
         const Geometry& g = d->proj[k]->g;  // every layer's projection k has this shape
         for (uint32_t m = 1; m <= cap; ++m) part_bytes = std::max(part_bytes, gemm_part_bytes(g, m, d->num_cus));
     }
-    {  // q, k and v in one launch (record_prefill)
-        GemmSub qkv[3];
+    {  // q, k and v, and gate and up, in one launch each (record_prefill)
+        GemmSub qkv[3], gu[2];
         for (int k = 0; k < 3; ++k) qkv[k] = GemmSub{nullptr, &d->proj[VX_PROJ_Q + k]->g, nullptr, 0};
-        for (uint32_t m = 1; m <= cap; ++m)
+        for (int k = 0; k < 2; ++k) gu[k] = GemmSub{nullptr, &d->proj[VX_PROJ_GATE + k]->g, nullptr, 0};
+        for (uint32_t m = 1; m <= cap; ++m) {
             if (gemm_group_small_path(qkv, 3, m))
                 part_bytes = std::max(part_bytes, gemm_group_part_bytes(qkv, 3, m, d->num_cus));
+            if (gemm_group_small_path(gu, 2, m))
+                part_bytes = std::max(part_bytes, gemm_group_part_bytes(gu, 2, m, d->num_cus));
+        }
     }
     hipError_t e = hipSuccess;
     auto grab = [&](auto** p, size_t bytes) {
@@ -3040,7 +3044,11 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
             // a staged gate/up pair as one launch when that needs no K split (twice the workgroups of one matrix)
             const vx_matrix* mg = d->proj[l * kProjKinds + VX_PROJ_GATE];
             const vx_matrix* mu = d->proj[l * kProjKinds + VX_PROJ_UP];
-            if (!small(VX_PROJ_GATE) && !small(VX_PROJ_UP) && d->pf_ld[VX_PROJ_GATE] == d->pf_ld[VX_PROJ_UP] &&
+            GemmSub gu[2] = {GemmSub{mg->d_w, &mg->g, d->pf_y[VX_PROJ_GATE], d->pf_ld[VX_PROJ_GATE]},
+                             GemmSub{mu->d_w, &mu->g, d->pf_y[VX_PROJ_UP], d->pf_ld[VX_PROJ_UP]}};
+            if (gemm_group_small_path(gu, 2, n)) {
+                VX_TRY(launch_gemm_group(gu, 2, d->num_cus, d->pf_codes, n, d->pf_codes_ld, d->pf_part, st));
+            } else if (!small(VX_PROJ_GATE) && !small(VX_PROJ_UP) && d->pf_ld[VX_PROJ_GATE] == d->pf_ld[VX_PROJ_UP] &&
                 mg->g.rows == mu->g.rows && mg->g.cols == mu->g.cols && gemm_staged_pair_ok(mg->g, n, d->num_cus)) {
                 VX_TRY(launch_gemm_staged_pair(mg->d_w, mu->d_w, mg->g, d->num_cus, d->pf_staged, n,
                                                d->pf_y[VX_PROJ_GATE], d->pf_y[VX_PROJ_UP], d->pf_ld[VX_PROJ_GATE], st));

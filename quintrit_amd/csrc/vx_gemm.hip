@@ -851,12 +851,9 @@ static int launch_small(const GemmSub* subs, int n, int num_cus, const int8_t* x
 
 bool gemm_group_small_path(const GemmSub* subs, int n, size_t M) {
     if (n < 1 || n > kSmallSubs) return false;
-    size_t rows_p = 0;
-    for (int i = 0; i < n; ++i) {
-        if (subs[i].g->cols != subs[0].g->cols) return false;
-        rows_p += subs[i].g->padded_rows;
-    }
-    return small_path(geometry(rows_p, subs[0].g->cols), M);
+    for (int i = 0; i < n; ++i)
+        if (subs[i].g->cols != subs[0].g->cols || !small_path(*subs[i].g, M)) return false;
+    return true;
 }
 
 size_t gemm_group_part_bytes(const GemmSub* subs, int n, size_t M, int num_cus) {
