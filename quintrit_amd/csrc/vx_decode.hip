@@ -2979,7 +2979,7 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
             in.a = pf_proj_out(d, l - 1, VX_PROJ_DOWN, as_down);
         }
         VX_TRY(stage(in, static_cast<uint32_t>(H), d->pf_ld[VX_PROJ_DOWN], as_qkv));
-        // q, k and v in one small-path launch where their concatenation takes that path
+        // q, k and v in one small-path launch where each takes that path
         GemmSub qkv[3];
         for (int k = 0; k < 3; ++k) {
             const vx_matrix* m = d->proj[l * kProjKinds + VX_PROJ_Q + k];

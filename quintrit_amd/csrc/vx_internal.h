@@ -179,8 +179,8 @@ struct GemmSub {
     int32_t* y;
     size_t ldy;
 };
-// Up to 3 matrices with the same columns in one small-path launch (their tiles concatenated), when the concatenation
-// would take the small path at M tokens; gemm_group_part_bytes of workspace.
+// Up to 3 matrices with the same columns in one small-path launch (their tiles concatenated), when each of them would
+// take the small path at M tokens; gemm_group_part_bytes of workspace.
 bool gemm_group_small_path(const GemmSub* subs, int n, size_t M);
 size_t gemm_group_part_bytes(const GemmSub* subs, int n, size_t M, int num_cus);
 int launch_gemm_group(const GemmSub* subs, int n, int num_cus, const int8_t* x, size_t M, size_t ldx, uint8_t* ws,
