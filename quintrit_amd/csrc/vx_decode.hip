@@ -2887,9 +2887,9 @@ static int ensure_prefill(vx_decoder* d) {
         for (int k = 0; k < 3; ++k) qkv[k] = GemmSub{nullptr, &d->proj[VX_PROJ_Q + k]->g, nullptr, 0};
         for (int k = 0; k < 2; ++k) gu[k] = GemmSub{nullptr, &d->proj[VX_PROJ_GATE + k]->g, nullptr, 0};
         for (uint32_t m = 1; m <= cap; ++m) {
-            if (gemm_group_small_path(qkv, 3, m))
+            if (gemm_group_small_path(qkv, 3, m, d->num_cus))
                 part_bytes = std::max(part_bytes, gemm_group_part_bytes(qkv, 3, m, d->num_cus));
-            if (gemm_group_small_path(gu, 2, m))
+            if (gemm_group_small_path(gu, 2, m, d->num_cus))
                 part_bytes = std::max(part_bytes, gemm_group_part_bytes(gu, 2, m, d->num_cus));
         }
     }
@@ -2953,7 +2953,7 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
         return launch_pf_stage(a, st);
     };
     // GEMMs on the small path read the codes themselves; the others read them staged once per input
-    auto small = [&](int kind) { return gemm_small_path(d->proj[kind]->g, n); };
+    auto small = [&](int kind) { return gemm_small_path(d->proj[kind]->g, n, d->num_cus); };
     auto gemm_stage = [&](size_t cols, std::initializer_list<int> kinds) -> int {
         bool need = false;
         for (int k : kinds) need = need || !small(k);
@@ -2985,7 +2985,7 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
             const vx_matrix* m = d->proj[l * kProjKinds + VX_PROJ_Q + k];
             qkv[k] = GemmSub{m->d_w, &m->g, d->pf_y[VX_PROJ_Q + k], d->pf_ld[VX_PROJ_Q + k]};
         }
-        if (gemm_group_small_path(qkv, 3, n)) {
+        if (gemm_group_small_path(qkv, 3, n, d->num_cus)) {
             VX_TRY(launch_gemm_group(qkv, 3, d->num_cus, d->pf_codes, n, d->pf_codes_ld, d->pf_part, st));
         } else {
             VX_TRY(gemm_stage(H, {VX_PROJ_Q, VX_PROJ_K, VX_PROJ_V}));
@@ -3046,7 +3046,7 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
             const vx_matrix* mu = d->proj[l * kProjKinds + VX_PROJ_UP];
             GemmSub gu[2] = {GemmSub{mg->d_w, &mg->g, d->pf_y[VX_PROJ_GATE], d->pf_ld[VX_PROJ_GATE]},
                              GemmSub{mu->d_w, &mu->g, d->pf_y[VX_PROJ_UP], d->pf_ld[VX_PROJ_UP]}};
-            if (gemm_group_small_path(gu, 2, n)) {
+            if (gemm_group_small_path(gu, 2, n, d->num_cus)) {
                 VX_TRY(launch_gemm_group(gu, 2, d->num_cus, d->pf_codes, n, d->pf_codes_ld, d->pf_part, st));
             } else if (!small(VX_PROJ_GATE) && !small(VX_PROJ_UP) && d->pf_ld[VX_PROJ_GATE] == d->pf_ld[VX_PROJ_UP] &&
                 mg->g.rows == mu->g.rows && mg->g.cols == mu->g.cols && gemm_staged_pair_ok(mg->g, n, d->num_cus)) {

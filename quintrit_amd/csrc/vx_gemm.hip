@@ -383,10 +383,10 @@ static GemmPlan gemm_plan(const Geometry& g, size_t M, int num_cus) {
 }
 
 static size_t small_part_bytes(const Geometry& g, size_t M, int num_cus);
-static bool small_path(const Geometry& g, size_t M);
+static bool small_path(const Geometry& g, size_t M, int num_cus);
 
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus) {
-    if (small_path(g, M)) return std::max<size_t>(small_part_bytes(g, M, num_cus), 256);
+    if (small_path(g, M, num_cus)) return std::max<size_t>(small_part_bytes(g, M, num_cus), 256);
     const GemmPlan p = gemm_plan(g, M, num_cus);
     return p.xs_bytes + p.part_bytes;
 }
@@ -397,7 +397,7 @@ size_t gemm_stage_bytes(size_t cols, size_t M) {
 }
 
 size_t gemm_part_bytes(const Geometry& g, size_t M, int num_cus) {
-    return small_path(g, M) ? small_part_bytes(g, M, num_cus) : gemm_plan(g, M, num_cus).part_bytes;
+    return small_path(g, M, num_cus) ? small_part_bytes(g, M, num_cus) : gemm_plan(g, M, num_cus).part_bytes;
 }
 
 // Stages x (M rows of cols int8) into the MFMA operand order at ws (gemm_stage_bytes(cols, M) bytes): the staged
@@ -789,14 +789,16 @@ static SmallShape small_shape(const Geometry& g, int num_cus, size_t M) {
 static uint32_t small_kslices(const Geometry& g, int num_cus, size_t M) { return small_shape(g, num_cus, M).kslices; }
 
 // M <= 32 always; 33-128 tokens (two or four token groups) only for matrices of at most 128 tiles (8192 rows) and
-// 32768 columns (a bounded slice workspace): at 23040 x 3072 the staged kernel was faster (28.4 against 31.0 us at
-// M = 64, 41.5 against 42.6 us at M = 128), at 3072 x 23040 and 3072 x 3072 slower (24.0 against 20.0 us at M = 64;
-// 34.8 against 33.4 and 24.0 against 19.9 us at M = 128).
-static bool small_path(const Geometry& g, size_t M) {
-    return M <= 32 || (M <= 128 && g.n_tiles <= 128 && g.cols <= 32768);
+// 32768 columns whose slice sums take at most 64 MiB: at 23040 x 3072 the staged kernel was faster (28.4 against
+// 31.0 us at M = 64, 41.5 against 42.6 us at M = 128), at 3072 x 23040 and 3072 x 3072 slower (24.0 against 20.0 us at
+// M = 64; 34.8 against 33.4 and 24.0 against 19.9 us at M = 128, 54 MiB of slice sums at 3072 x 23040).
+constexpr size_t kSmallPartCap = size_t(64) << 20;
+static bool small_path(const Geometry& g, size_t M, int num_cus) {
+    if (M <= 32) return true;
+    return M <= 128 && g.n_tiles <= 128 && g.cols <= 32768 && small_part_bytes(g, M, num_cus) <= kSmallPartCap;
 }
 
-bool gemm_small_path(const Geometry& g, size_t M) { return small_path(g, M); }
+bool gemm_small_path(const Geometry& g, size_t M, int num_cus) { return small_path(g, M, num_cus); }
 
 static size_t small_part_bytes(const Geometry& g, size_t M, int num_cus) {
     const uint32_t ks = small_kslices(g, num_cus, M);
@@ -849,10 +851,10 @@ static int launch_small(const GemmSub* subs, int n, int num_cus, const int8_t* x
     return VX_OK;
 }
 
-bool gemm_group_small_path(const GemmSub* subs, int n, size_t M) {
+bool gemm_group_small_path(const GemmSub* subs, int n, size_t M, int num_cus) {
     if (n < 1 || n > kSmallSubs) return false;
     for (int i = 0; i < n; ++i)
-        if (subs[i].g->cols != subs[0].g->cols || !small_path(*subs[i].g, M)) return false;
+        if (subs[i].g->cols != subs[0].g->cols || !small_path(*subs[i].g, M, num_cus)) return false;
     return true;
 }
 
@@ -864,13 +866,13 @@ size_t gemm_group_part_bytes(const GemmSub* subs, int n, size_t M, int num_cus) 
 
 int launch_gemm_group(const GemmSub* subs, int n, int num_cus, const int8_t* x, size_t M, size_t ldx, uint8_t* ws,
                       hipStream_t stream) {
-    if (!gemm_group_small_path(subs, n, M)) VX_FAIL(VX_ERR_INTERNAL, "a grouped GEMM of %d matrices off the small path", n);
+    if (!gemm_group_small_path(subs, n, M, num_cus)) VX_FAIL(VX_ERR_INTERNAL, "a grouped GEMM of %d matrices off the small path", n);
     return launch_small<true>(subs, n, num_cus, x, M, ldx, ws, stream);
 }
 
 int launch_gemm(const uint8_t* w, const Geometry& g, int num_cus, const int8_t* x, size_t M, size_t ldx, int32_t* y,
                 size_t ldy, uint8_t* ws, hipStream_t stream) {
-    if (small_path(g, M)) {
+    if (small_path(g, M, num_cus)) {
         const GemmSub sub{w, &g, y, ldy};
         return launch_small<false>(&sub, 1, num_cus, x, M, ldx, ws, stream);
     }

@@ -168,10 +168,11 @@ int launch_digit_sums(const uint8_t* w, const Geometry& g, int32_t* dsum, hipStr
 int launch_find_invalid(const uint8_t* planar_dev, uint64_t n, unsigned long long* first, hipStream_t stream);
 int launch_fill_f32(float* out, size_t n, float v, hipStream_t stream);
 size_t gemm_workspace_bytes(const Geometry& g, size_t M, int num_cus);
-// Up to 32 tokens, and up to 128 on matrices of at most 8192 rows and 32768 columns (gemm_small_path), a call runs
-// without a staging kernel (gemm_small_kernel builds the B fragments in LDS from x; a finish kernel adds the K slices
-// when there are several) and needs gemm_part_bytes of workspace; otherwise it runs as staging + GEMM + finish.
-bool gemm_small_path(const Geometry& g, size_t M);
+// Up to 32 tokens, and up to 128 on matrices of at most 8192 rows and 32768 columns with at most 64 MiB of slice sums
+// (gemm_small_path), a call runs without a staging kernel (gemm_small_kernel builds the B fragments in LDS from x; a
+// finish kernel adds the K slices when there are several) and needs gemm_part_bytes of workspace; otherwise it runs
+// as staging + GEMM + finish.
+bool gemm_small_path(const Geometry& g, size_t M, int num_cus);
 // One matrix of a grouped small-path GEMM: its weights, geometry and output.
 struct GemmSub {
     const uint8_t* w;
@@ -181,7 +182,7 @@ struct GemmSub {
 };
 // Up to 3 matrices with the same columns in one small-path launch (their tiles concatenated), when each of them would
 // take the small path at M tokens; gemm_group_part_bytes of workspace.
-bool gemm_group_small_path(const GemmSub* subs, int n, size_t M);
+bool gemm_group_small_path(const GemmSub* subs, int n, size_t M, int num_cus);
 size_t gemm_group_part_bytes(const GemmSub* subs, int n, size_t M, int num_cus);
 int launch_gemm_group(const GemmSub* subs, int n, int num_cus, const int8_t* x, size_t M, size_t ldx, uint8_t* ws,
                       hipStream_t stream);
