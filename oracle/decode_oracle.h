@@ -10,7 +10,10 @@
  *   vxo_ggml_expf      exact at 0 and in the overflow / underflow branches, within 2 ulps of float64 exp elsewhere,
  *                      and a few values worked by hand through the reference's steps; vxo_swiglu against float64
  *                      silu(g) * u, its scalar tail against the host expf formula
- *   vxo_attend_head    float64 softmax attention, single and 4-chunk paths (FP16 accumulator tolerance)
+ *   vxo_attend_head    bit for bit against hand-computable closed forms in which every softmax weight is exactly 0 or
+ *                      1 (padded length, split threshold, chunk size, FP16 chain, in-order f32 combine), with negative
+ *                      controls (seq_len-based chunks, an f32 accumulator, no padding, 8 chunks, a reversed combine);
+ *                      float64 softmax attention for general scores
  *   vxo_model_forward  a float64 model written from model.rs / attention.rs (logits within 6 % of the largest; the
  *                      structural mistakes tried land at 57-190 %), plus a negative control
  *   quantizer, RMSNorm (velurex_oracle.c)  the reference's known answers (ops.rs:1968-1991); the reference text

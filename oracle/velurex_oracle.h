@@ -72,7 +72,10 @@ float vxo_f16_to_f32(uint16_t h);                                               
 void vxo_rms_norm(const float* x, const float* w, size_t n, float eps, float* out); /* ops.rs:43-57 */
 
 /* ---- Q2_0 x Q8_0 block-scaled GEMV (quintrit-core/src/block_scaled.rs) ---------------------------------------- */
-/* dot_row_scalar (block_scaled.rs:175-202). w_scales: cols/64 per row; a_scales: cols/32. */
+/* dot_row_scalar (block_scaled.rs:175-202). w_scales: cols/64 per row; a_scales: cols/32. Its floating-point order
+ * (two chains by (s/2)&1, fma(ws*as, lane, acc), lanes of both chains added, then hsum8's pairing) is pinned by
+ * hand-computed rows in which f32 absorption makes each step observable, with a negative control per step
+ * (tests/test_oracle.py, test_q2_0_order_*). */
 float vxo_q2_0_dot_row(const uint8_t* row, const float* w_scales, const int8_t* acts, const float* a_scales, size_t cols);
 void vxo_q2_0_gemv(const uint8_t* packed, const float* w_scales, const int8_t* acts, const float* a_scales,
                    size_t rows, size_t cols, float* out);

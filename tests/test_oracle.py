@@ -274,6 +274,105 @@ def test_q2_0_close_to_float64(oracle):
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-5)
 
 
+# Hand-computed rows for the floating-point order of Q2_0 (block_scaled.rs:1-19,140-145,175-202). cols = 256: eight
+# activation blocks s (weight block s / 2, chain (s / 2) & 1), every activation 1, so a lane sum is the sum of four
+# trits. f32 has 24 significant bits: 2^24 + 1 is a tie that rounds to 2^24, while 2^24 + 2 is exact.
+Q2_ROWS, Q2_COLS = 5, 256
+
+
+def q2_order_case():
+    t = np.zeros((Q2_ROWS, Q2_COLS), np.int8)
+    ws = np.ones((Q2_ROWS, Q2_COLS // 64), np.float32)
+    as_ = np.ones(Q2_COLS // 32, np.float32)
+    # row 0, the two chains: s=0 lane 0 = 2^24 (chain 0); s=2 and s=3 lane 0 = 1 each (chain 1, which holds 2).
+    # l0 = 2^24 + 2. One chain: 2^24 + 1 + 1 = 2^24; chains by s & 1: (2^24 + 1) + 1 = 2^24.
+    ws[0, 0] = 2.0 ** 24
+    t[0, [0, 64, 96]] = 1
+    # row 1, hsum8's pairing: l0 = 2^24 (s=0, 4 trits x 2^22), l2 = 1 and l6 = 1 (s=2 lanes 2 and 6).
+    # ((l0+l4) + (l2+l6)) + ... = 2^24 + 2. In lane order, or as ((l0+l1)+(l2+l3)) + ((l4+l5)+(l6+l7)): 2^24.
+    ws[1, 0] = 2.0 ** 22
+    t[1, [0, 1, 2, 3, 64 + 8, 64 + 24]] = 1
+    # row 2, chains added lane by lane before hsum8: chain 0 lane 0 = 2^24, chain 1 lanes 0 and 4 = 1 each.
+    # l0 = 2^24 + 1 = 2^24, l4 = 1, (l0 + l4) = 2^24. hsum8 of each chain, then added: 2^24 + 2.
+    ws[2, 0] = 2.0 ** 22
+    t[2, [0, 1, 2, 3, 64, 64 + 16]] = 1
+    # row 3, the fused multiply-add: s=0 lane 0 = -3 (d = 1); s=1 lane 0 = 3 with d = 1 + 2^-23 (as[1]).
+    # fma(1 + 2^-23, 3, -3) = 3 * 2^-23. A rounded product first: f32(3 + 3 * 2^-23) = 3 + 2^-21, so 2^-21.
+    as_[1] = np.float32(1 + 2.0 ** -23)
+    t[3, [0, 1, 2]] = -1
+    t[3, [32, 33, 34]] = 1
+    # row 4, d = f32(ws * as) before the lane sum: ws = as = 1 + 2^-12 at s=4, lane 0 = 3.
+    # d = f32(1 + 2^-11 + 2^-24) = 1 + 2^-11 (tie to even), 3 d = 3 + 3 * 2^-11 exactly.
+    # ws * (as * 3) = f32(3 + 3 * 2^-11 + 3 * 2^-24) = 3 + 3 * 2^-11 + 2^-22.
+    ws[4, 2] = np.float32(1 + 2.0 ** -12)
+    as_[4] = np.float32(1 + 2.0 ** -12)
+    t[4, [128, 129, 130]] = 1
+    a = np.ones(Q2_COLS, np.int8)
+    want = np.array([2.0 ** 24 + 2, 2.0 ** 24 + 2, 2.0 ** 24, 3 * 2.0 ** -23, 3 + 3 * 2.0 ** -11], np.float32)
+    return t, ws, a, as_, want
+
+
+def q2_definition(t, ws, a, as_, *, chains=2, chain_of_s=None, pairing="ggml", fused=True, scale_first=True,
+                  hsum_per_chain=False):
+    """The documented order with switches for the negative controls. Products and sums are formed in float64 and
+    rounded once to f32, which is exact for these inputs' magnitudes (so fused = one rounding)."""
+    f32 = np.float32
+    rows, cols = t.shape
+    out = np.empty(rows, np.float32)
+    for r in range(rows):
+        acc = np.zeros((2, 8), np.float32)
+        for s in range(cols // 32):
+            c = ((s // 2) & 1 if chain_of_s is None else chain_of_s(s)) if chains == 2 else 0
+            lanes = (t[r, s * 32:(s + 1) * 32].astype(np.int64) * a[s * 32:(s + 1) * 32]).reshape(8, 4).sum(axis=1)
+            for j in range(8):
+                p = float(lanes[j])
+                if scale_first:
+                    d = f32(float(ws[r, s // 2]) * float(as_[s]))
+                    prod = float(d) * p
+                else:
+                    prod = float(ws[r, s // 2]) * float(f32(float(as_[s]) * p))
+                if not fused:
+                    prod = float(f32(prod))
+                acc[c, j] = f32(prod + float(acc[c, j]))
+
+        def hsum(l):
+            if pairing == "ggml":
+                return f32(f32(f32(l[4] + l[0]) + f32(l[6] + l[2])) + f32(f32(l[5] + l[1]) + f32(l[7] + l[3])))
+            if pairing == "sequential":
+                s_ = f32(0)
+                for x in l:
+                    s_ = f32(s_ + x)
+                return s_
+            return f32(f32(f32(l[0] + l[1]) + f32(l[2] + l[3])) + f32(f32(l[4] + l[5]) + f32(l[6] + l[7])))
+        if hsum_per_chain:
+            out[r] = f32(hsum(acc[0]) + hsum(acc[1]))
+        else:
+            out[r] = hsum((acc[0] + acc[1]).astype(np.float32))
+    return out
+
+
+def test_q2_0_order_hand_computed(oracle):
+    """The oracle's Q2_0 rows equal the hand-computed values above bit for bit; so does the documented definition."""
+    t, ws, a, as_, want = q2_order_case()
+    got = oracle.q2_0_gemv(oracle.pack_matrix(t), ws.reshape(-1), a, as_, Q2_ROWS, Q2_COLS)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(q2_definition(t, ws, a, as_).view(np.uint32), want.view(np.uint32))
+
+
+def test_q2_0_order_negative_controls():
+    """Each plausible mistake changes the row built to show it: one accumulator, chains chosen by s & 1, lanes summed in
+    order or in adjacent pairs, an unfused multiply-add, the scale applied after the lane sum, hsum8 of each chain."""
+    t, ws, a, as_, want = q2_order_case()
+    mutants = [
+        (dict(chains=1), 0), (dict(chain_of_s=lambda s: s & 1), 0), (dict(pairing="sequential"), 1),
+        (dict(pairing="adjacent"), 1), (dict(hsum_per_chain=True), 2), (dict(fused=False), 3),
+        (dict(scale_first=False), 4),
+    ]
+    for kw, row in mutants:
+        bad = q2_definition(t, ws, a, as_, **kw)
+        assert bad[row] != want[row], kw
+
+
 # ---- generators -------------------------------------------------------------------------------------------------------
 
 def test_generators(oracle):

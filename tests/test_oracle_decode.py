@@ -371,6 +371,133 @@ def test_attend_head_close_to_float64(oracle, seq_len, max_ctx):
     assert np.max(np.abs(got - want)) < 2e-3 * max(1.0, np.max(np.abs(want)))
 
 
+# Closed forms of attend_head where every softmax weight is exactly 0 or 1. The query is e0 (f16 1.0 in coordinate 0)
+# and each key carries a level of 0 or 60000 in coordinate 0, so a score is 0 or 60000 * scale (~5300); exp(0) = 1 and
+# exp(-5300) = 0 in f32. Within an online-softmax range the positions from the first occurrence of the range's highest
+# level on, at that level, are summed with weight 1 into the FP16 accumulator (each step f16(f32(acc) + f32(v)), which
+# is what f16(fma(v, 1, acc)) and the tail's f16(acc + f32(v * 1)) both are), earlier ones are wiped by a factor 0, later
+# lower ones are added with weight 0. Chunks whose highest level is below the global one drop out of the combine
+# (factor 0); the others are added in chunk order in f32. So the output is fixed by sums a reader can do by hand, and
+# these sums expose the padded length, the split threshold, the chunk size, the accumulator precision and the combine
+# order (attention.rs:436-468,483-542).
+
+SPIKE = 60000.0
+
+
+def attn_closed_form(levels, v, seq_len, max_ctx, *, chunk_from_seq=False, f16_acc=True, pad=True, n_chunks=4,
+                     reverse=False):
+    hd = v.shape[1]
+    n_kv = max(-(-seq_len // 256) * 256, 256) if pad else seq_len
+    n_kv = min(n_kv, max_ctx)
+
+    def run(lo, hi):
+        lv = levels[lo:hi]
+        m = lv.max()
+        first = lo + int(np.argmax(lv == m))
+        acc = np.zeros(hd, np.float32)
+        count = 0
+        for p in range(first, hi):
+            if levels[p] == m:
+                acc = acc + h2f(v[p])
+                if f16_acc:
+                    acc = h2f(f16(acc))
+                count += 1
+        return m, acc, count
+
+    if n_kv < 512:
+        _, acc, s = run(0, seq_len)
+        return acc * (np.float32(1) / np.float32(s))
+    chunk = -(-(seq_len if chunk_from_seq else n_kv) // n_chunks)
+    parts = []
+    for c in range(n_chunks):
+        lo, hi = c * chunk, min(c * chunk + chunk, n_kv, seq_len)
+        if lo < hi:
+            parts.append(run(lo, hi))
+    if reverse:
+        parts = parts[::-1]
+    top = max(p[0] for p in parts)
+    acc = np.zeros(hd, np.float32)
+    s = np.float32(0)
+    for m, a, n in parts:
+        if m == top:
+            acc = acc + a
+            s = np.float32(s + n)
+    return acc * (np.float32(1) / s)
+
+
+def attn_structured_inputs(seq_len, hd, spikes, seed):
+    """q = e0; keys: level 0 or SPIKE in coordinate 0, random elsewhere. Values (none of them -0):
+    column 0 is 2048 at position 0 and 1.0 elsewhere (2048 + 1 rounds back to 2048 in f16, so an FP16 chain absorbs
+    every 1.0 after it while a new chunk counts them exactly); column 1 is 32768 at position 0 and 2^-9 at every 37th
+    position (absorbed in f16 inside a chunk; in the f32 combine 32768 + 2^-9 is a tie that rounds to 32768, so the
+    combine order shows); the other columns are random magnitudes in [0.25, 4) of both signs."""
+    rng = np.random.default_rng(seed)
+    levels = np.zeros(seq_len)
+    if spikes:
+        levels[np.arange(seq_len) % 97 == 13] = SPIKE
+    q = np.zeros(hd, np.float32)
+    q[0] = 1.0
+    k = rng.uniform(-2, 2, (seq_len, hd)).astype(np.float32)
+    k[:, 0] = levels
+    vv = rng.uniform(0.25, 4, (seq_len, hd)) * rng.choice([-1.0, 1.0], (seq_len, hd))
+    vv[:, 0] = 1.0
+    vv[0, 0] = 2048.0
+    vv[:, 1] = 0.0
+    vv[::37, 1] = 2.0 ** -9
+    vv[0, 1] = 32768.0
+    return f16(q), f16(k), f16(vv.astype(np.float32)), levels
+
+
+ATTN_CASES = [(200, 4096), (256, 4096), (257, 4096), (300, 400), (513, 4096), (600, 4096), (600, 640), (1500, 2048)]
+
+
+@pytest.mark.parametrize("spikes", [False, True])
+@pytest.mark.parametrize("seq_len,max_ctx", ATTN_CASES)
+def test_attend_head_closed_form(oracle, seq_len, max_ctx, spikes):
+    """attend_head equals the 0/1-weight closed form bit for bit: KV padded to a multiple of 256 (at least 256, at most
+    the cache length), one online softmax below a padded length of 512, else 4 chunks of ceil(n_kv / 4) positions, FP16
+    accumulators per chunk, an f32 combine in chunk order (attention.rs:483-542). With equal keys (no spikes) the
+    single-softmax output is the plain f16 sequential sum of V divided by n."""
+    hd = 40  # 32 values in ggml_vec_mad_f16's vector body, 8 in its tail
+    q, k, v, levels = attn_structured_inputs(seq_len, hd, spikes, seq_len)
+    scale = np.float32(1.0 / np.sqrt(128.0))
+    got = oracle.attend_head(q, k, v, seq_len, max_ctx, float(scale))
+    want = attn_closed_form(levels, v, seq_len, max_ctx)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if not spikes and seq_len <= 256:
+        seqsum = np.zeros(hd, np.uint16)
+        for p in range(seq_len):
+            seqsum = f16(h2f(seqsum) + h2f(v[p]))
+        plain = h2f(seqsum) * (np.float32(1) / np.float32(seq_len))
+        assert np.array_equal(got.view(np.uint32), plain.view(np.uint32))
+        assert h2f(seqsum)[0] == 2048.0  # every 1.0 absorbed by the f16 chain
+
+
+def test_attend_head_closed_form_negative_controls(oracle):
+    """The closed-form check rejects each plausible mistake: a chunk size from seq_len instead of the padded n_kv, an
+    f32 value accumulator, no KV padding (split decided by seq_len), 8 chunks, and a reversed combine. For each mutant
+    some case gives an output different from the oracle's, so an oracle that made that mistake would fail
+    test_attend_head_closed_form."""
+    hd = 40
+    scale = float(np.float32(1.0 / np.sqrt(128.0)))
+    mutants = dict(chunk_from_seq=dict(chunk_from_seq=True), f32_acc=dict(f16_acc=False), no_pad=dict(pad=False),
+                   eight_chunks=dict(n_chunks=8), reverse=dict(reverse=True))
+    caught = {name: [] for name in mutants}
+    for spikes in (False, True):
+        for seq_len, max_ctx in ATTN_CASES:
+            q, k, v, levels = attn_structured_inputs(seq_len, hd, spikes, seq_len)
+            got = oracle.attend_head(q, k, v, seq_len, max_ctx, scale)
+            for name, kw in mutants.items():
+                bad = attn_closed_form(levels, v, seq_len, max_ctx, **kw)
+                if not np.array_equal(got.view(np.uint32), bad.view(np.uint32)):
+                    caught[name].append((seq_len, max_ctx, spikes))
+    for name, where in caught.items():
+        assert where, f"the closed-form check does not see the mutant {name}"
+    # the chunk-size mistake at the case the review named: seq 600 pads to 768, so chunks are 192 positions, not 150
+    assert (600, 4096, False) in caught["chunk_from_seq"]
+    assert (600, 4096, False) in caught["f32_acc"]
+
+
 # ---- the model forward against a float64 model written from model.rs / attention.rs -------------------------------------
 
 TINY = dict(n_layers=2, hidden=160, n_heads=4, n_kv_heads=2, head_dim=32, ffn=320, vocab=300, max_ctx=64)
