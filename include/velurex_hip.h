@@ -410,6 +410,11 @@ int vx_decoder_kv_get(const vx_decoder_t* decoder, uint32_t layer, uint32_t pos,
                       uint16_t* v, size_t n);
 /* Device bytes held by the decoder (weights, KV cache, work buffers). */
 int vx_decoder_memory_bytes(const vx_decoder_t* decoder, size_t* out_bytes);
+/* Diagnostic, no counterpart in the reference: how many times an RMSNorm on the decoder's GPU has taken the
+ * reference's sequential f64 order (rms_norm, quintrit-runtime/src/ops.rs:43-57) because its tree-summed mean lay
+ * within the error bound of an f32 rounding boundary. One count per workgroup that computed such a norm, summed over
+ * every decoder of the process on that GPU since the library was loaded. */
+int vx_decoder_norm_fallbacks(const vx_decoder_t* decoder, uint64_t* out_count);
 /* The decoder's configuration (the shape part of quintrit_model_info, quintrit.h:323-340); out_config->struct_size must be
  * sizeof(vx_decoder_config_t). */
 int vx_decoder_config(const vx_decoder_t* decoder, vx_decoder_config_t* out_config);

@@ -93,6 +93,7 @@ SIGNATURES = {
     "vx_decoder_prefill": (_i32, [_vp, _vp, _sz, ctypes.c_uint32, _vp, _sz, _vp]),
     "vx_decoder_kv_get": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp, _sz]),
     "vx_decoder_memory_bytes": (_i32, [_vp, _vp]),
+    "vx_decoder_norm_fallbacks": (_i32, [_vp, _vp]),
     "vx_decoder_config": (_i32, [_vp, _vp]),
     "vx_decoder_adopt_projection": (_i32, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp]),
     "vx_decoder_open_gguf": (_i32, [ctypes.c_char_p, _vp, _vp]),

@@ -327,6 +327,10 @@ __device__ __forceinline__ void slice_sums(const int4 (&pa)[SA > 0 ? SA : 1][P4]
     }
 }
 
+// Times an RMSNorm took the reference's sequential order because its tree-summed mean lay too close to an f32 rounding
+// boundary (one count per workgroup that computed such a norm). Diagnostic only: read by vx_decoder_norm_fallbacks.
+__device__ unsigned int g_norm_fallbacks;
+
 // y of the thread's elements: v by kind, then (with gamma) its RMSNorm y = (v * inv) * gamma (rms_norm, ops.rs:19-96).
 // Every thread derives the mean from the per-wave sums itself, so the common path has one barrier; without gamma none.
 // With write_x, an input that has an x_out also stores v there.
@@ -427,6 +431,7 @@ __device__ __forceinline__ void stage_y(const StageInput& p, const InputRegs<P4,
         const float hi = static_cast<float>(q + e);
         if (lane == 0) {
             if (lo != hi) {  // too close to an f32 rounding boundary: the reference's order
+                atomicAdd(&g_norm_fallbacks, 1u);
                 double seq = 0.0;
                 for (uint32_t i = 0; i < n; ++i) {
                     const float sqv = s.ys[i] * s.ys[i];
@@ -595,7 +600,20 @@ struct DJob {
     // raised by kRangeBias, bits 48-63 the count of contributions
     unsigned long long* accum;
 };
-constexpr int kRangeBias = 1 << 21;  // > the largest |partial sum| of a row (103 chunks x 10880), 3 x 2 kRangeBias < 2^24
+// Each contribution to a packed 24-bit field is v + kRangeBias, with |v| at most 80 x 272 per chunk of one matrix that
+// the workgroup's range covers in the tile (80 weights per 16-byte chunk, digits 0..2 times staged values of magnitude
+// at most 136). range_fields_fit() admits a range split only where |v| < kRangeBias and the contributions to one word,
+// each in (0, 2 kRangeBias), add up below 2^24.
+constexpr int kRangeBias = 1 << 21;
+constexpr uint64_t kRangeChunkMax = 80u * 272u;
+inline bool range_fields_fit(uint64_t n_chunks, uint64_t C, uint64_t G) {
+    const uint64_t per_wg = C / G;  // every workgroup's range holds at least this many chunks
+    if (per_wg == 0) return false;
+    const uint64_t covered = std::min(n_chunks, (C + G - 1) / G);  // chunks of one matrix in one contribution
+    const uint64_t contributions = (2u * n_chunks + per_wg - 1) / per_wg + 1u;  // workgroups that meet one tile
+    return covered * kRangeChunkMax < static_cast<uint64_t>(kRangeBias) &&
+           contributions * 2u * static_cast<uint64_t>(kRangeBias) <= (1ull << 24) && contributions < (1u << 16);
+}
 
 constexpr int kMaxStageJobs = 3;
 constexpr int kMaxClear = 6;
@@ -905,12 +923,14 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
                 else s21 += v;
             }
         }
-        red[0][0][wave][lane] = s00;
-        red[0][1][wave][lane] = s01;
-        red[1][0][wave][lane] = s10;
-        red[1][1][wave][lane] = s11;
-        red[2][0][wave][lane] = s20;
-        red[2][1][wave][lane] = s21;
+        if constexpr (MULTI) {  // a range split is a multi-item launch: red has kRangeSegs x 2 slots
+            red[0][0][wave][lane] = s00;
+            red[0][1][wave][lane] = s01;
+            red[1][0][wave][lane] = s10;
+            red[1][1][wave][lane] = s11;
+            red[2][0][wave][lane] = s20;
+            red[2][1][wave][lane] = s21;
+        }
     };
     // The outputs of row `row` of a gated pair from the complete sums v (gate) and v2 (up) of its row, corrections
     // included: the layer epilogue of both projections (layer.rs:246-253), then the gating of model.rs:155-170. A whole
@@ -1769,7 +1789,7 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(a.ticket + blockIdx.x, 1u) == 3u ? 1u : 0u;
+    if (tid == 0) s_last = take_ticket(a.ticket + blockIdx.x, 3u);
     __syncthreads();
     if (s_last == 0u || wave != 0) return;
     if (lane == 0) atomicExch(a.ticket + blockIdx.x, 0u);
@@ -2001,7 +2021,7 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
         if (wbest[w] > best) best = wbest[w];
     atomicMax(a.key, best);
     __builtin_amdgcn_s_waitcnt(0);  // the maximum is in place (at the atomics' coherence point) before the ticket
-    if (atomicAdd(a.ticket, 1u) != gridDim.x - 1u) return;
+    if (take_ticket(a.ticket, gridDim.x - 1u) == 0u) return;
     const unsigned long long k = atomicExch(a.key, 0ull);
     atomicExch(a.ticket, 0u);
     const uint32_t idx = k == 0 ? 0u : 0xffffffffu - static_cast<uint32_t>(k);
@@ -2375,7 +2395,7 @@ struct vx_decoder {
     hipGraphExec_t exec_short;
     bool ready;
     size_t bytes;
-    std::mutex mu;
+    mutable std::mutex mu;  // serialises the calls that launch work or read the KV cache
 };
 
 namespace vx {
@@ -2738,7 +2758,8 @@ static int build_stages(vx_decoder* d) {
                 // chunks and meets at most kRangeSegs tiles; else one or two tiles per workgroup.
                 const uint64_t C = static_cast<uint64_t>(j.n_tiles) * 2u * j.n_chunks, G = static_cast<uint64_t>(d->num_cus);
                 if (C >= G && (C + G - 1) / G <= static_cast<uint64_t>(kTileGroup * kDPer) &&
-                    2u * j.n_chunks >= static_cast<uint32_t>(8 * kDPer) && j.n_tiles > G) {
+                    2u * j.n_chunks >= static_cast<uint32_t>(8 * kDPer) && j.n_tiles > G &&
+                    range_fields_fit(j.n_chunks, C, G)) {
                     a.range_chunks = static_cast<uint32_t>(C);
                     j.accum = reinterpret_cast<unsigned long long*>(d->d_pacc);
                 }
@@ -3419,11 +3440,26 @@ int vx_decoder_kv_get(const vx_decoder_t* d, uint32_t layer, uint32_t pos, uint3
                            (static_cast<size_t>(kv_head) * d->cfg.max_ctx + pos) * hd;
         const size_t voff = static_cast<size_t>(layer) * d->kvd * vs + static_cast<size_t>(kv_head) * hd * vs +
                             (static_cast<size_t>(pos / 8) * hd) * 8 + pos % 8;
+        std::lock_guard<std::mutex> lk(d->mu);  // no step or prefill is half way through the cache meanwhile
         VX_TRY(set_device(d->device));
         VX_HIP(hipStreamSynchronize(d->stream));
         if (k) VX_HIP(hipMemcpy(k, d->d_kc + off, hd * 2, hipMemcpyDeviceToHost));
         // V is cached in tiles of 8 positions: the position's values are 8 elements apart
         if (v) VX_HIP(hipMemcpy2D(v, 2, d->d_vc + voff, 16, 2, hd, hipMemcpyDeviceToHost));
+        return VX_OK;
+    });
+}
+
+int vx_decoder_norm_fallbacks(const vx_decoder_t* d, uint64_t* out_count) {
+    return guard([&]() -> int {
+        VX_TRY(check_decoder(d));
+        if (out_count == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "out_count is NULL");
+        std::lock_guard<std::mutex> lk(d->mu);
+        VX_TRY(set_device(d->device));
+        VX_HIP(hipStreamSynchronize(d->stream));
+        unsigned int c = 0;
+        VX_HIP(hipMemcpyFromSymbol(&c, HIP_SYMBOL(g_norm_fallbacks), sizeof(c), 0, hipMemcpyDeviceToHost));
+        *out_count = c;
         return VX_OK;
     });
 }

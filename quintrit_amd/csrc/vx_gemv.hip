@@ -362,10 +362,11 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
             continue;
         }
         // The sums are complete at the atomics' coherence point before the ticket is taken (every memory operation of
-        // the wave waited for), and the last slice reads them with atomics after its ticket: no cache writeback.
+        // the wave waited for, then an agent-scope release before the ticket), and the last slice reads them with
+        // atomics after its ticket and an agent-scope acquire: no cache writeback.
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tid == 0) last_slice = atomicAdd(jb.tickets + grp, 1u) == jb.kslices - 1u ? 1u : 0u;
+        if (tid == 0) last_slice = take_ticket(jb.tickets + grp, jb.kslices - 1u);
         __syncthreads();
         if (last_slice != 0u) {
             const uint32_t row = grp * kTileGroup * kTileRows + wave * kTileRows + lane;

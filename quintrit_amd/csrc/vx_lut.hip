@@ -209,11 +209,11 @@ __global__ __launch_bounds__(kLutWaves * 64) __attribute__((amdgpu_waves_per_eu(
             else jb.part[static_cast<size_t>(ks) * jb.padded_rows + row] = acc;
         }
         if (!fold) continue;
-        // The sums are complete at the atomics' coherence point before the ticket is taken, and the last slice reads
-        // them back with atomics after its ticket.
+        // The sums are complete at the atomics' coherence point before the ticket is taken (release), and the last
+        // slice reads them back with atomics after its ticket (acquire).
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        if (tid == 0) last_slice = atomicAdd(jb.tickets + grp, 1u) == jb.kslices - 1u ? 1u : 0u;
+        if (tid == 0) last_slice = take_ticket(jb.tickets + grp, jb.kslices - 1u);
         __syncthreads();
         if (last_slice != 0u) {
             const uint32_t row = grp * kTileGroup * kTileRows + wave * kTileRows + lane;

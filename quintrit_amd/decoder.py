@@ -173,6 +173,12 @@ class Decoder:
         check(lib().vx_decoder_memory_bytes(self.handle, ctypes.byref(b)))
         return b.value
 
+    def norm_fallbacks(self) -> int:
+        """Workgroups on this GPU whose RMSNorm took the reference's sequential order (a diagnostic counter)."""
+        c = ctypes.c_uint64()
+        check(lib().vx_decoder_norm_fallbacks(self.handle, ctypes.byref(c)))
+        return c.value
+
     def close(self) -> None:
         if self.handle:
             check(lib().vx_decoder_free(self.handle))

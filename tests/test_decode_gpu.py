@@ -362,3 +362,57 @@ def test_falcon3_10b_golden_logits_every_position(torch_dev, oracle):
         assert nxt == gold["tokens"][0]
     finally:
         dec.close()
+
+
+def test_rms_norm_fallback_on_a_rounding_boundary(torch_dev, oracle):
+    """An embedding row whose RMSNorm mean sits on an f32 rounding boundary: 16 and 2^-8 make the exact sum of squares
+    256 + 2^-16, so the mean is 1 + 2^-24, the midpoint between 1 and 1 + 2^-23, and 254 values of +-2^-23 add squares
+    of 2^-46, below half an ulp (2^-45) of that sum. The reference's sequential f64 sum (ops.rs:43-57) drops each of
+    them and rounds the mean to even, 1.0; a tree sum keeps their total (~2^-38) and rounds up. So the GPU must take its
+    sequential fallback for this norm (the diagnostic counter rises) and its logits, KV cache and greedy tokens must
+    equal the oracle's, in decode steps and in a prefill."""
+    cfg = tiny_cfg(oracle)
+    n = cfg.hidden
+    row = np.full(n, 2.0 ** -23, np.float32) * np.where(np.arange(n) % 2 == 0, 1.0, -1.0).astype(np.float32)
+    row[0], row[1] = 16.0, 2.0 ** -8
+    sq = row.astype(np.float64) ** 2
+    seq = 0.0
+    for v in sq:
+        seq += float(v)
+    assert np.float32(seq / n) == np.float32(1.0)                          # the reference's order
+    assert np.float32(np.sum(sq) / n) == np.float32(1.0 + 2.0 ** -23)       # a pairwise (tree) order
+    token = 7
+    model = oracle.Model(cfg, 29)
+    emb = model.embedding()  # a view: the oracle's model holds the planted row too
+    emb[token] = [oracle.f32_to_bf16(float(v)) for v in row]
+    dec = load_decoder(oracle, model)
+    try:
+        before = dec.norm_fallbacks()
+        prompt = [token, 3, token, 11, token]
+        for pos, tok in enumerate(prompt):
+            logits, nxt = dec.step(tok, pos)
+            want_next, want = model.forward(tok, pos)
+            assert_same_bits(logits, want, f"step at pos {pos}")
+            assert nxt == want_next
+        after_steps = dec.norm_fallbacks()
+        assert after_steps > before, "the sequential fallback did not run"
+        # a prefill of the same prompt on a fresh cache: the per-token norms of the prefill kernels
+        model.reset()
+        dec2 = load_decoder(oracle, model)
+        try:
+            logits, nxt = dec2.prefill(prompt)
+            for pos, tok in enumerate(prompt):
+                want_next, want = model.forward(tok, pos)
+            assert_same_bits(logits, want, "prefill")
+            assert nxt == want_next
+            for pos in range(len(prompt)):
+                for h in range(cfg.n_kv_heads):
+                    k, v = dec2.kv(0, pos, h)
+                    wk, wv = model.kv(0, pos, h)
+                    assert np.array_equal(k, wk) and np.array_equal(v, wv), (pos, h)
+            assert dec2.norm_fallbacks() > after_steps
+        finally:
+            dec2.close()
+    finally:
+        dec.close()
+        model.close()

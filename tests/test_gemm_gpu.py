@@ -2,8 +2,8 @@
 
 The reference has no multi-token kernel; its prefill calls the GEMV once per token (quintrit-runtime/src/engine.rs:
 625-631), so the GEMM must equal M independent GEMVs bit for bit. Small shapes are checked against brute force; the
-BASELINE.json configs[2] shapes (W 23040 x 3072 and 3072 x 23040, M in {8, 32, 128, 512}) against the GEMV of every
-token (itself bit-exact against the oracle) and brute force on sampled rows.
+BASELINE.json configs[2] shapes (W 23040 x 3072 and 3072 x 23040, M in {8, 32, 128, 512}) against a float64 brute
+force of every output.
 """
 import ctypes
 
@@ -74,24 +74,24 @@ def test_gemm_extreme_values(torch_dev, oracle):
 
 
 @pytest.mark.parametrize("rows,cols", [(23040, 3072), (3072, 23040)])
-def test_gemm_config2_equals_gemv_per_token(torch_dev, oracle, rows, cols):
-    """i.i.d. trits (P(-1)=P(+1)=0.35), X quantized per token from N(0,1)."""
+def test_gemm_config2_equals_bruteforce(torch_dev, oracle, rows, cols):
+    """i.i.d. trits (P(-1)=P(+1)=0.35), X quantized per token from N(0,1). Every output of
+    every M is compared with a float64 BLAS product of the unpacked trits, which is exact here: the operands are
+    integers and every partial sum is at most 128 * 23040 < 2^53 in magnitude."""
     from quintrit_amd import VelurexHipLayer
     torch = torch_dev
     t = oracle.gen_trits(0xC2 + rows, (rows, cols))
+    tf = t.astype(np.float64)
     layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, 1.0)
     rng = np.random.default_rng(rows)
     for m in (8, 32, 48, 64, 128, 512):
         print(f"[gemm config2] {rows}x{cols} m={m}", flush=True)
         x = np.stack([oracle.quantize_i8(rng.standard_normal(cols).astype(np.float32))[0] for _ in range(m)])
         got = gemm(torch, layer, x)
-        want = np.empty((m, rows), np.int32)
-        out = torch.empty(rows, dtype=torch.int32, device="cuda")
-        for i in range(m):
-            layer.gemv_i32(torch.from_numpy(x[i]).cuda(), out)
-            want[i] = out.cpu().numpy()
-        assert np.array_equal(got, want), m
-        sample = rng.choice(rows, size=8, replace=False)
-        bf = x.astype(np.int64) @ t[sample].astype(np.int64).T
-        assert np.array_equal(got[:, sample].astype(np.int64), bf), m
+        want = x.astype(np.float64) @ tf.T
+        assert np.array_equal(got.astype(np.float64), want), m
+    # one token through the GEMV as well: the two kernels agree
+    out = torch.empty(rows, dtype=torch.int32, device="cuda")
+    layer.gemv_i32(torch.from_numpy(x[5]).cuda(), out)
+    assert np.array_equal(out.cpu().numpy(), got[5])
     layer.close()

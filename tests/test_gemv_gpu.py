@@ -183,6 +183,41 @@ def test_planar_oneshot_api(torch_dev, oracle):
     assert np.array_equal(f.view(np.uint32), oracle.scale_f32(got, 0.125).view(np.uint32))
 
 
+# The reference's kernel-level C API tests (quintrit-c/tests/ffi_kernel.rs:36-49,195-228): full tiles, remainder rows
+# and columns, partial 160-trit blocks, degenerate sizes, and three realistic projections.
+FFI_SHAPES = [(1, 1), (3, 5), (5, 7), (32, 160), (33, 161), (31, 159), (64, 320), (65, 250), (96, 3072), (100, 1000),
+              (130, 640), (192, 33), (512, 3072), (96, 6000), (70, 777)]
+
+
+@pytest.mark.parametrize("rows,cols", FFI_SHAPES)
+def test_planar_oneshot_reference_ffi_shapes(torch_dev, oracle, rows, cols):
+    """vx_gemv_planar_i32 / _f32 (the argument order of quintrit_gemv_i32 / _f32) against the brute-force int64
+    product, and out = float(acc) * 0.25 bit for bit, as check_gemv asserts (ffi_kernel.rs:195-222)."""
+    from quintrit_amd import gemv_planar_f32, gemv_planar_i32
+    print(f"[gemv ffi] {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows * 131 + cols)
+    t = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+    a = rng.integers(-128, 128, size=cols, dtype=np.int8)
+    planar = oracle.pack_matrix(t)
+    want = t.astype(np.int64) @ a.astype(np.int64)
+    got = gemv_planar_i32(planar, rows, cols, a)
+    assert np.array_equal(got.astype(np.int64), want)
+    f = gemv_planar_f32(planar, rows, cols, a, 0.25)
+    assert np.array_equal(f.view(np.uint32), (want.astype(np.float32) * np.float32(0.25)).view(np.uint32))
+
+
+def test_planar_oneshot_extreme_activations(torch_dev, oracle):
+    """All weights +1 or -1 against constant activations -128, 127, 0, -1, 1 at 64 x 1000: every output is
+    w * fill * cols, the largest sums a row reaches (ffi_kernel.rs:225-248)."""
+    from quintrit_amd import gemv_planar_i32
+    rows, cols = 64, 1000
+    for fill in (-128, 127, 0, -1, 1):
+        for w in (1, -1):
+            planar = oracle.pack_matrix(np.full((rows, cols), w, np.int8))
+            got = gemv_planar_i32(planar, rows, cols, np.full(cols, fill, np.int8))
+            assert np.all(got == w * fill * cols), (fill, w)
+
+
 def test_golden_fixtures(torch_dev):
     """The committed fixtures (tests/golden) reproduce on the GPU."""
     import os

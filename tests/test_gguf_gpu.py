@@ -34,7 +34,15 @@ def test_upload_equals_brute_force(torch_dev, oracle, tmp_path, ty, rows, cols):
     from quintrit_amd.gguf import GgufFile
     from quintrit_amd.layer import VelurexHipLayer
     if ty != 36 and rows * cols % 256:
-        pytest.skip("TQ needs whole blocks")
+        # a TQ tensor holds whole 256-weight blocks: 65 x 384 is refused before any device work
+        from quintrit_amd._lib import VxError
+        d = torch.zeros(rows * cols, dtype=torch.uint8, device="cuda")
+        h = ctypes.c_void_p()
+        with pytest.raises(VxError, match="INVALID_SHAPE"):
+            check(lib().vx_matrix_create_ggml_dev(ty, ctypes.c_void_p(d.data_ptr()), d.numel(), rows, cols,
+                                                  ctypes.c_float(1.0), ctypes.byref(h)))
+        assert not h.value
+        return
     rng = np.random.default_rng(rows * 7 + cols + ty)
     trits = rng.integers(-1, 2, (rows, cols)).astype(np.int8)
     data = payload(oracle, ty, trits)

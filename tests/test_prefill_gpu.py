@@ -108,6 +108,32 @@ def test_prefill_variants(torch_dev, oracle, name):
         model.close()
 
 
+@pytest.mark.parametrize("name", ["pair_range", "gqa16"])
+@pytest.mark.parametrize("n", [7, 64, 128])
+def test_prefill_grouped_k_split(torch_dev, oracle, name, n):
+    """Prompts of up to 128 tokens at hidden 2560 (pair_range) and 512 (gqa16): their grouped q/k/v and gate/up GEMMs
+    take the small path with their K range split into 8 (2) slices, which the grouped finish kernel adds and
+    distributes to each matrix by its first row. KV cache and last logits equal the steps and the oracle."""
+    model = oracle.Model(variant_cfg(oracle, name), 47 + n)
+    pre = load_decoder(oracle, model)
+    ref = load_decoder(oracle, model)
+    try:
+        tokens = np.random.default_rng(n).integers(0, model.cfg.vocab, n)
+        print(f"[prefill k-split] {name} n={n}", flush=True)
+        got, got_next = pre.prefill(tokens)
+        for pos, tok in enumerate(tokens):
+            want, want_next = ref.step(int(tok), pos)
+            o_next, o_logits = model.forward(int(tok), pos)
+        assert_same_bits(got, want, f"{name} n={n}: last logits vs steps")
+        assert_same_bits(got, o_logits, f"{name} n={n}: last logits vs oracle")
+        assert got_next == want_next == o_next
+        kv_equal(pre, ref, model.cfg, range(n))
+    finally:
+        pre.close()
+        ref.close()
+        model.close()
+
+
 @pytest.mark.parametrize("max_ctx,n_prompt,n_new", [(640, 8, 300), (640, 513, 100), (512, 200, 313)])
 def test_generate_prefill_equals_stepwise(torch_dev, oracle, max_ctx, n_prompt, n_new):
     """Greedy generation with the prompt prefilled equals the prompt fed step by step and the oracle's loop."""
