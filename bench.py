@@ -48,6 +48,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="leave the decode/prefill measurements out of the line")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave BASELINE.json configs[0], [2] and [4] out of the default line")
     ap.add_argument("--workload", choices=["stream", "gemm", "q2", "decode", "gguf"], default="stream",
                     help="stream: the driver's line (configs[1]); gemm: the batched GEMM of configs[2]; q2: the "
                          "block-scaled GEMV stream of configs[4]; decode: bs=1 greedy decode of configs[3]")
@@ -137,6 +139,7 @@ class Stream:
         self.mats = []      # per layer: list of (name, handle, rows, cols)
         self.staged = []    # per launch: (tensor, nbytes)
         self.luts = []      # per launch: the input's compact activation tables (tensor, nbytes)
+        self.q = []         # per launch: the int8 input vector the staged bytes were made from
         self.outs = []
         self.weights = 0
         self.alg_bytes = 0
@@ -166,6 +169,7 @@ class Stream:
                 lib.compact_lut_dev(q.data_ptr(), cols, cols, lut.data_ptr(), lbytes, stream)
                 self.scales[k] = s
                 row.append((name, h, rows, cols))
+                self.q.append(q)
                 self.staged.append((staged, nbytes))
                 self.luts.append((lut, lbytes))
                 self.outs.append(torch.empty(rows, dtype=torch.float32, device="cuda"))
@@ -201,6 +205,17 @@ class Stream:
                 self.lib.check(self.L.vx_gemv_staged_f32_dev(h, ctypes.c_void_p(staged.data_ptr()), nbytes,
                                                              ctypes.c_float(1.0), ctypes.c_void_p(self.outs[k].data_ptr()),
                                                              rows, st))
+                k += 1
+
+    def stage_all(self) -> None:
+        """Every projection's int8 input staged again (vx_stage_acts_dev, one launch per projection)."""
+        st = ctypes.c_void_p(self.torch.cuda.current_stream().cuda_stream)
+        k = 0
+        for row in self.mats:
+            for _, _, _, cols in row:
+                staged, nbytes = self.staged[k]
+                self.lib.check(self.L.vx_stage_acts_dev(ctypes.c_void_p(self.q[k].data_ptr()), cols, cols,
+                                                        ctypes.c_void_p(staged.data_ptr()), nbytes, st))
                 k += 1
 
     def free(self):
@@ -289,6 +304,152 @@ def lone_latency(torch, L, lib, reps: int = 200):
             f"vx_layer_forward {np.median(fwd) * 1e6:.1f} us")
         lib.check(L.vx_matrix_free(h))
     return out
+
+
+CFG0_ROTATION_BYTES = 1 << 30  # at least 1 GiB of distinct weight copies: beyond the 256 MB last-level cache
+
+
+def config0_measure(torch, L, lib, cpu: bool) -> dict:
+    """one 2560 x 2560 GEMV, trits i.i.d. with P(-1) = P(+1) = 0.35, x 2560 int8 uniform in
+    [-127, 127], weight scale 0.02 and activation scale 1, so y = float(acc) * 0.02; int32 acc and fp32 y. Both outputs
+    are checked against a numpy brute force of the same planar bytes first. The matrix is 1.31 MB, so a repeated call
+    is cache-resident: its figures are latency (a graph of 100 back-to-back calls, HIP events, and one call followed by
+    a synchronisation, wall clock) and Gweights/s. For HBM GB/s the same GEMV runs over 1 GiB of distinct copies of
+    the matrix (the reference's method: a pass larger than any cache, docs/benchmarks.md:47-49), as one batched plan
+    and as a graph of dependent lone calls."""
+    import numpy as np
+    rows = cols = 2560
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xC0)
+    planar = random_planar(torch, rows, cols, gen)
+    x = torch.randint(-127, 128, (cols,), dtype=torch.int8, device="cuda", generator=gen)
+    h = ctypes.c_void_p()
+    lib.check(L.vx_matrix_create_dev(ctypes.c_void_p(planar.data_ptr()), planar.numel(), rows, cols,
+                                     ctypes.c_float(0.02), ctypes.byref(h)))
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    acc = torch.empty(rows, dtype=torch.int32, device="cuda")
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731  (the capture stream too)
+    stream = cur()
+    call_f32 = lambda: lib.check(L.vx_gemv_f32_dev(h, ctypes.c_void_p(x.data_ptr()), cols, ctypes.c_float(1.0),  # noqa: E731
+                                                    ctypes.c_void_p(y.data_ptr()), rows, cur()))
+    call_i32 = lambda: lib.check(L.vx_gemv_i32_dev(h, ctypes.c_void_p(x.data_ptr()), cols,  # noqa: E731
+                                                    ctypes.c_void_p(acc.data_ptr()), rows, cur()))
+    call_f32()
+    call_i32()
+    torch.cuda.synchronize()
+    planar_np = planar.cpu().numpy()
+    tr = planar_trits_np(planar_np, rows, cols)
+    want = tr.astype(np.int64) @ x.cpu().numpy().astype(np.int64)
+    if not np.array_equal(acc.cpu().numpy().astype(np.int64), want):
+        raise RuntimeError("config 0: int32 accumulators differ from the numpy brute force")
+    wy = want.astype(np.float32) * (np.float32(0.02) / np.float32(1.0))
+    if not np.array_equal(y.cpu().numpy().view(np.uint32), wy.view(np.uint32)):
+        raise RuntimeError("config 0: fp32 outputs differ from float(acc) * 0.02")
+    n_in_graph = 100
+    g = capture(torch, lambda: [call_f32() for _ in range(n_in_graph)])
+    ms, _ = time_fn(torch, g.replay, 20, 3)
+    us_call = ms * 1e3 / n_in_graph
+    del g
+    lat = []
+    for i in range(60):
+        t0 = time.perf_counter()
+        call_f32()
+        torch.cuda.synchronize()
+        if i >= 10:
+            lat.append(time.perf_counter() - t0)
+    w = rows * cols
+    out = {"shape": [rows, cols], "weights": w, "weight_bytes": w // 5,
+           "checked": "int32 acc and fp32 y = float(acc) * 0.02 equal a numpy brute force, bit for bit",
+           "call_us": round(us_call, 3), "call_Gweights_s": round(w / (us_call * 1e-6) / 1e9, 1),
+           "call_note": "vx_gemv_f32_dev (activation staging + GEMV + epilogue), 100 calls in one HIP graph, device "
+                        "time per call; cache-resident",
+           "call_sync_us": round(float(np.median(lat)) * 1e6, 1)}
+    # rotation: distinct copies of the same planar bytes, 1 GiB of weights in all
+    n_copies = -(-CFG0_ROTATION_BYTES // (w // 5))
+    mats = [h]
+    for _ in range(n_copies - 1):
+        hc = ctypes.c_void_p()
+        lib.check(L.vx_matrix_create_dev(ctypes.c_void_p(planar.data_ptr()), planar.numel(), rows, cols,
+                                         ctypes.c_float(0.02), ctypes.byref(hc)))
+        mats.append(hc)
+    del planar
+    nbytes = lib.staged_bytes(cols)
+    staged = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(x.data_ptr()), cols, cols, ctypes.c_void_p(staged.data_ptr()),
+                                  nbytes, stream))
+    one = torch.ones(1, dtype=torch.float32, device="cuda")
+    outs = torch.empty((n_copies, rows), dtype=torch.float32, device="cuda")
+    jobs = [lib.GemvJob(out_f32=1, matrix=m.value, staged=staged.data_ptr(), staged_len=nbytes,
+                        act_scale_dev=one.data_ptr(), out=outs[i].data_ptr(), out_capacity=rows)
+            for i, m in enumerate(mats)]
+    plan = lib.Plan(jobs)
+    mp, _ = time_fn(torch, lambda: plan.run(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), 20, 3)
+    torch.cuda.synchronize()
+    if not torch.equal(outs[-1], y) or not torch.equal(outs[0], y):
+        raise RuntimeError("config 0 rotation: a copy's outputs differ from the single call's")
+
+    def chain():
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i, m in enumerate(mats):
+            lib.check(L.vx_gemv_staged_f32_dev(m, ctypes.c_void_p(staged.data_ptr()), nbytes, ctypes.c_float(1.0),
+                                               ctypes.c_void_p(outs[i].data_ptr()), rows, st))
+    g = capture(torch, chain)
+    mc, _ = time_fn(torch, g.replay, 5, 2)
+    del g
+    tot_w = w * n_copies
+    out["rotation"] = {"copies": n_copies, "weight_bytes": tot_w // 5,
+                       "plan_ms": round(mp, 4), "plan_Gweights_s": round(tot_w / (mp / 1e3) / 1e9, 1),
+                       "plan_GBps": round(tot_w / 5 / (mp / 1e3) / 1e9, 1),
+                       "plan_frac": round(tot_w / 5 / (mp / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+                       "chain_ms": round(mc, 4), "chain_us_per_call": round(mc * 1e3 / n_copies, 3),
+                       "chain_GBps": round(tot_w / 5 / (mc / 1e3) / 1e9, 1),
+                       "note": "plan: all copies in one vx_plan_run (one staged input); chain: one dependent "
+                               "vx_gemv_staged_f32_dev per copy in a HIP graph"}
+    log(f"config 0: {us_call:.3f} us/call cached ({out['call_Gweights_s']} Gweights/s), {out['call_sync_us']} us "
+        f"with a sync; rotation over {n_copies} copies: plan {out['rotation']['plan_GBps']} GB/s, chain "
+        f"{out['rotation']['chain_us_per_call']} us/call")
+    plan.close()
+    for m in mats:
+        lib.check(L.vx_matrix_free(m))
+    if cpu:
+        out["cpu_baseline"] = config0_cpu_baseline(planar_np, rows, cols, x.cpu().numpy(), want)
+    return out
+
+
+def config0_cpu_baseline(planar, rows, cols, acts, want):
+    """configs[0] on the host: the AVX-512 transcription of the reference's production GEMV (oracle/cpu_avx512.c,
+    avx512.rs:1526-1626) on the 2560 x 2560 tiles, checked against the brute force, then timed (table build + GEMV per
+    call, cache-resident as on the reference's machines) at 1, 2, 4, 8, ... threads up to the process's CPUs; the
+    best count is the value."""
+    import numpy as np
+    from oracle import oracle
+    if not oracle.cpu_avx512_supported():
+        return None
+    L = oracle.lib()
+    tiles = oracle.tile64(planar, rows, cols)
+    out = np.empty(rows, np.float32)
+    scratch = np.empty(int(L.vxc_table_bytes(cols)), np.int8)
+    ncpu = len(os.sched_getaffinity(0))
+    res = {}
+    for th in sorted({t for t in (1, 2, 4, 8, 16, 32, 64, ncpu) if t <= ncpu}):
+        call = lambda: L.vxc_gemv(tiles.ctypes.data_as(ctypes.c_void_p), acts.ctypes.data_as(ctypes.c_void_p),  # noqa: E731
+                                  rows, cols, out.ctypes.data_as(ctypes.c_void_p), th,
+                                  scratch.ctypes.data_as(ctypes.c_void_p))
+        call()
+        if not np.array_equal(out.astype(np.int64), want):
+            raise RuntimeError("config 0 CPU baseline differs from the brute force")
+        best = 1e9
+        t_end = time.perf_counter() + 1.0
+        while time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            for _ in range(20):
+                call()
+            best = min(best, (time.perf_counter() - t0) / 20)
+        res[th] = best
+    top = min(res, key=lambda t: res[t])
+    return {"value": round(rows * cols / res[top] / 1e9, 1), "unit": "Gweights/s", "cores": top, "kind": "port",
+            "us_per_call": {str(t): round(v * 1e6, 2) for t, v in res.items()},
+            "sample": "2560x2560 GEMV (table build + kernel), best of 20-call averages over 1 s per thread count"}
 
 
 def capture(torch, fn):
@@ -469,6 +630,27 @@ def cpu_baseline(budget_s: float, layers: int = 40):
                         break
     finally:
         os.sched_setaffinity(0, main_affinity)  # the pinning moved this (the calling) thread too
+    # cache-resident kernel rate of one thread (the reference compares 58-65 weights per cycle for this kernel on
+    # cache-resident weights, docs/benchmarks.md:90-92): a 1024 x 3072 projection (630 KB of tiles) from its tables,
+    # best of repeated calls, against the core clock measured on the same thread
+    pinned_ok &= L.vxc_pin_threads(ctypes.cast(cpus, ctypes.c_void_p), 1) == 0
+    try:
+        ctile = np.empty(KV * oracle.tile_row_bytes(HIDDEN), np.uint8)
+        L.vxc_fill_valid(ctile.ctypes.data_as(ctypes.c_void_p), ctile.size, 17)
+        cact = rng.integers(-127, 128, HIDDEN, dtype=np.int16).astype(np.int8)
+        ctab = np.empty(int(L.vxc_table_bytes(HIDDEN)), np.int8)
+        cout = np.empty(KV, np.float32)
+        L.vxc_build_tables(cact.ctypes.data_as(ctypes.c_void_p), HIDDEN, ctab.ctypes.data_as(ctypes.c_void_p))
+        cbest = float("inf")
+        for _ in range(200):
+            t0 = time.perf_counter()
+            L.vxc_gemv_tables(ctile.ctypes.data_as(ctypes.c_void_p), ctab.ctypes.data_as(ctypes.c_void_p), KV, HIDDEN,
+                              cout.ctypes.data_as(ctypes.c_void_p), 1)
+            cbest = min(cbest, time.perf_counter() - t0)
+        clock_hz = max(L.vxc_clock_hz() for _ in range(3))
+    finally:
+        os.sched_setaffinity(0, main_affinity)
+    cached_wpc = KV * HIDDEN / cbest / clock_hz
     tab = float("inf")  # the serial part of a pass: the groups' table builds alone (one thread, as the engine's)
     for _ in range(3):
         t0 = time.perf_counter()
@@ -493,7 +675,11 @@ def cpu_baseline(budget_s: float, layers: int = 40):
             "table_build_ms_per_pass": round(tab * 1e3, 2),
             "table_build_share": {str(t): round(tab / ((best[t][0] + best[t][1]) / 2), 3) for t in counts},
             "threads_pinned": bool(pinned_ok), "cpu_model": _cpu_model(), "logical_cpus": ncpu,
-            "physical_cores": phys}
+            "physical_cores": phys, "clock_ghz_1t": round(clock_hz / 1e9, 3),
+            "cached_1t": {"shape": [KV, HIDDEN], "us": round(cbest * 1e6, 2),
+                          "gweights_s": round(KV * HIDDEN / cbest / 1e9, 1),
+                          "weights_per_cycle": round(cached_wpc, 1),
+                          "reference": "58-65 weights per cycle, cache-resident, EPYC 9V45 (docs/benchmarks.md:90-92)"}}
 
 
 def cpu_baseline_scalar(budget_s: float, shapes):
@@ -527,9 +713,21 @@ def cpu_baseline_scalar(budget_s: float, shapes):
 
 
 def gemm_bench(torch, L, lib, args) -> int:
+    """BASELINE.json configs[2] alone: one JSON line with every (shape, M) result and the CPU baseline."""
+    results = gemm_measure(torch, L, lib, max(5, args.steps), max(2, args.warmup))
+    cpu = None if args.no_cpu_baseline else gemm_cpu_baseline(args.cpu_seconds)
+    print(json.dumps({"workload": "batched ternary GEMM, BASELINE.json configs[2]", "dtype": "int8 x ternary -> int32",
+                      "data": "synthetic", "note": "time per vx_gemm_i32_dev call (activation staging + GEMM + "
+                      "K-slice finish), HIP events", "results": results, "cpu_baseline": cpu}), flush=True)
+    return 0
+
+
+def gemm_measure(torch, L, lib, steps: int, warmup: int) -> list:
     """Y = X W^T for W 23040 x 3072 and 3072 x 23040 (velurex), X M x K int8 quantized per
-    token from N(0,1), M in {8, 32, 128, 512}; exact int32 on the matrix cores. One JSON line per call of this mode;
+    token from N(0,1), M in {8, 32, 128, 512}; exact int32 on the matrix cores. Every output of one M per shape is
+    checked against a float64 brute force of the same planar bytes first (exact: integer operands, |sums| < 2^53).
     ops = 2 M N K; bytes = weights (N K / 5) + X + Y."""
+    import numpy as np
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0xC2)
     results = []
@@ -539,6 +737,7 @@ def gemm_bench(torch, L, lib, args) -> int:
         h = ctypes.c_void_p()
         lib.check(L.vx_matrix_create_dev(ctypes.c_void_p(planar.data_ptr()), planar.numel(), rows, cols,
                                          ctypes.c_float(0.02), ctypes.byref(h)))
+        trits = planar_trits_np(planar.cpu().numpy(), rows, cols).astype(np.float64)
         del planar
         for m in (8, 32, 128, 512):
             x = torch.randn((m, cols), device="cuda", generator=gen)
@@ -552,7 +751,13 @@ def gemm_bench(torch, L, lib, args) -> int:
             call = lambda: lib.check(L.vx_gemm_i32_dev(h, ctypes.c_void_p(q.data_ptr()), m, cols,  # noqa: E731
                                                        ctypes.c_void_p(y.data_ptr()), rows,
                                                        ctypes.c_void_p(ws.data_ptr()), n.value, stream))
-            ms, _ = time_fn(torch, call, max(5, args.steps), max(2, args.warmup))
+            if m == 32:
+                call()
+                torch.cuda.synchronize()
+                want = q.cpu().numpy().astype(np.float64) @ trits.T
+                if not np.array_equal(y.cpu().numpy().astype(np.float64), want):
+                    raise RuntimeError(f"gemm {rows}x{cols} m={m}: GPU differs from the float64 brute force")
+            ms, _ = time_fn(torch, call, steps, warmup)
             ops = 2.0 * m * rows * cols
             byts = rows * cols / 5.0 + m * cols + 4.0 * m * rows
             r = {"rows": rows, "cols": cols, "m": m, "us": round(ms * 1e3, 2), "TOPS": round(ops / (ms / 1e3) / 1e12, 2),
@@ -566,11 +771,8 @@ def gemm_bench(torch, L, lib, args) -> int:
             log(f"gemm {rows}x{cols} m={m}: {r['us']} us, {r['TOPS']} TOPS, {r['GBps']} GB/s")
             results.append(r)
         lib.check(L.vx_matrix_free(h))
-    cpu = None if args.no_cpu_baseline else gemm_cpu_baseline(args.cpu_seconds)
-    print(json.dumps({"workload": "batched ternary GEMM, BASELINE.json configs[2]", "dtype": "int8 x ternary -> int32",
-                      "data": "synthetic", "note": "time per vx_gemm_i32_dev call (activation staging + GEMM + "
-                      "K-slice finish), HIP events", "results": results, "cpu_baseline": cpu}), flush=True)
-    return 0
+        del trits
+    return results
 
 
 def gemm_cpu_baseline(budget_s: float):
@@ -616,14 +818,25 @@ def gemm_cpu_baseline(budget_s: float):
             "ms_per_pass_at_best": round(best[top] * 1e3, 3)}
 
 
+Q2_SHAPES = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096), (12288, 4096), (4096, 12288)]
+
+
 def q2_bench(torch, L, lib, args) -> int:
+    """BASELINE.json configs[4] alone: one JSON line with the stream's rate and the CPU baseline."""
+    layers = 36 if args.layers == LAYERS else args.layers
+    r = q2_measure(torch, L, lib, layers, args.steps, args.warmup)
+    r["cpu_baseline"] = None if args.no_cpu_baseline else q2_cpu_baseline(args.cpu_seconds, Q2_SHAPES)
+    print(json.dumps(r), flush=True)
+    return 0
+
+
+def q2_measure(torch, L, lib, layers: int, steps: int, warmup: int) -> dict:
     """the projections of one Qwen3-8B-like token (36 layers; q, o 4096 x 4096; k, v
     1024 x 4096; gate, up 12288 x 4096; down 4096 x 12288) as Q2_0 GEMVs: velurex trits plus one fp16 scale per 64
     weights (log-uniform in [0.005, 0.05]) stored beside them, Q8_0 activations (int8 uniform in [-127, 127], one f32
     scale per 32, log-uniform in [0.005, 0.05]). One step = one plan run over all 252 projections."""
     import numpy as np
-    layers = 36 if args.layers == LAYERS else args.layers
-    shapes = [(4096, 4096), (1024, 4096), (1024, 4096), (4096, 4096), (12288, 4096), (12288, 4096), (4096, 12288)]
+    shapes = Q2_SHAPES
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0xC4)
     rng = np.random.default_rng(0xC4)
@@ -651,7 +864,7 @@ def q2_bench(torch, L, lib, args) -> int:
             dev_bytes += n.value
     plan = lib.Q2Plan(jobs)
     stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
-    ms, _ = time_fn(torch, lambda: plan.run(stream()), args.steps, args.warmup)
+    ms, _ = time_fn(torch, lambda: plan.run(stream()), steps, warmup)
     alg = weights / 5.0 + 2.0 * weights / 64.0
     r = {"workload": "Q2_0 projection stream, BASELINE.json configs[4]", "layers": layers, "weights": weights,
          "ms_per_step": round(ms, 4), "Gweights_s": round(weights / (ms / 1e3) / 1e9, 1),
@@ -661,13 +874,11 @@ def q2_bench(torch, L, lib, args) -> int:
     r["roofline"] = {"bound": "hbm", "achieved": r["alg_GBps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(r["alg_GBps"] / HBM_PEAK_GBPS, 4),
                      "kernel": "vx::q2_kernel (one plan run: all 252 projections of a token)"}
-    r["cpu_baseline"] = None if args.no_cpu_baseline else q2_cpu_baseline(args.cpu_seconds, shapes)
     log(f"q2 stream: {ms:.4f} ms/step, {r['Gweights_s']} Gweights/s, {r['alg_GBps']} GB/s algorithmic")
-    print(json.dumps(r), flush=True)
     plan.close()
     for m in mats:
         m.close()
-    return 0
+    return r
 
 
 def q2_cpu_baseline(budget_s: float, shapes):
@@ -1143,9 +1354,22 @@ def main():
     # ... and the outputs of the last timed step, again against numpy (a mismatch fails the run)
     n_checked = check_outputs_np(st, check_layers)
     log(f"after timing: layers {check_layers} still equal the numpy brute force")
+    # the same step with every projection's activation staging inside the timed region (160 more launches), as a graph
+    g = capture(torch, lambda: (st.stage_all(), step()))
+    msg, _ = time_fn(torch, g.replay, args.steps, args.warmup)
+    del g
+    with_staging = {"ms_per_step": round(msg, 5), "Gweights_s": round(st.weights / (msg / 1e3) / 1e9, 1),
+                    "frac": round(st.alg_bytes / (msg / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+                    "note": "160 vx_stage_acts_dev launches (the per-projection int8 staging) + the plan run, one HIP "
+                            "graph per step"}
+    log(f"with the staging in the step: {msg:.4f} ms/step ({with_staging['frac']:.1%} of peak)")
+    n_checked += check_outputs_np(st, check_layers[-1:])
     roofline = {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(gbps / HBM_PEAK_GBPS, 4),
                 "traffic": TRAFFIC_BYTES_PER_STEP if args.layers == LAYERS else None,
+                "traffic_source": "a constant: rocprofv3 FETCH_SIZE + WRITE_SIZE of this launch, scaled by a plain-copy "
+                                  "calibration (profiles/gemv_kernel_falcon3_projection_stream.md), not measured in "
+                                  "this run",
                 "kernel": "vx::gemv_kernel (one plan run: all 160 projections of a token; event-timed region also "
                           "holds the K-slice finish kernel)",
                 "alg_bytes_per_launch": int(st.alg_bytes)}
@@ -1160,6 +1384,19 @@ def main():
     st.free()
     del st, plan
     torch.cuda.empty_cache()
+    config0 = gemm = q2 = None
+    if not args.no_configs:
+        # BASELINE.json configs[0], [2] and [4] in the same line (each also has a --workload mode of its own)
+        config0 = config0_measure(torch, L, _lib, cpu=not args.no_cpu_baseline)
+        torch.cuda.empty_cache()
+        gemm = [{k: r[k] for k in ("rows", "cols", "m", "us", "TOPS", "GBps")} | {"frac": r["roofline"]["frac"],
+                                                                                "bound": r["roofline"]["bound"]}
+                for r in gemm_measure(torch, L, _lib, 20, 5)]
+        torch.cuda.empty_cache()
+        r = q2_measure(torch, L, _lib, 36, 20, 5)
+        q2 = {k: r[k] for k in ("layers", "ms_per_step", "Gweights_s", "alg_GBps", "tok_s_projection_bound")}
+        q2["frac"] = r["roofline"]["frac"]
+        torch.cuda.empty_cache()
     decode = None
     if not args.no_decode:
         # tok/s at bs = 1: both decode models of BASELINE.json (configs[3] BitNet-2B, configs[1]'s Falcon3-10B shapes)
@@ -1184,7 +1421,9 @@ def main():
         "vs_baseline_ref": f"{REF_CPU_GWEIGHTS} Gweights/s, the published Falcon3-10B weight-stream rate of the reference AVX-512 kernel, 4 threads, EPYC 9V45 "
                                    f"(docs/benchmarks.md:77)",
         "settle": {"seconds": SETTLE_S, "plan_runs": n_settle},
-        "chain": chain, "breakdown": breakdown, "table_decode": table_decode, "roofline": roofline, "cpu_baseline": cpu, "decode": decode,
+        "with_staging": with_staging,
+        "chain": chain, "breakdown": breakdown, "table_decode": table_decode, "roofline": roofline, "cpu_baseline": cpu,
+        "config0": config0, "gemm_config2": gemm, "q2_config4": q2, "decode": decode,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -26,6 +26,7 @@
 #include <sched.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "velurex_oracle.h"
 
@@ -67,24 +68,45 @@ static void coefficient_masks(uint64_t pos[5], uint64_t neg[5]) {
     }
 }
 
+/* column_activation_index (pack.rs:230-237), inlined as the reference's builder has it: column c of a full 160-trit
+ * block holds activations (c / 32) 160 + p 32 + c % 32; a column of the packed tail holds five consecutive ones. */
+static inline size_t column_index(size_t cols, size_t full, size_t c, size_t p) {
+    if (c < full) return (c >> 5) * 160 + p * 32 + (c & 31);
+    return cols / 160 * 160 + 5 * (c - full) + p;
+}
+
 VXC_TARGET void vxc_build_tables(const int8_t* acts, size_t cols, int8_t* tables) {
-    const size_t bpr = vxo_tile_row_bytes(cols);
+    const size_t bpr = vxo_tile_row_bytes(cols), full = vxo_tile_full_columns(cols);
     uint64_t pos[5], neg[5];
     coefficient_masks(pos, neg);
+    const __mmask64 p0 = pos[0], p1 = pos[1], p2 = pos[2], p3 = pos[3], p4 = pos[4];
+    const __mmask64 n0 = neg[0], n1 = neg[1], n2 = neg[2], n3 = neg[3], n4 = neg[4];
     int8_t* lo_dst = tables;
     int8_t* hi_dst = tables + bpr * 64;
     for (size_t c = 0; c < bpr; ++c) {
-        __m512i acc_lo = _mm512_setzero_si512(), acc_hi = _mm512_setzero_si512();
+        int8_t l[5], h[5];
         for (size_t p = 0; p < 5; ++p) {
-            const size_t idx = vxo_column_activation_index(cols, c, p);
+            const size_t idx = column_index(cols, full, c, p);
             const int x = idx < cols ? acts[idx] : 0;
-            const int l = ((x + 8) & 15) - 8;
-            const __m512i bl = _mm512_set1_epi8((char)l), bh = _mm512_set1_epi8((char)((x - l) >> 4));
-            acc_lo = _mm512_mask_add_epi8(acc_lo, pos[p], acc_lo, bl);
-            acc_lo = _mm512_mask_sub_epi8(acc_lo, neg[p], acc_lo, bl);
-            acc_hi = _mm512_mask_add_epi8(acc_hi, pos[p], acc_hi, bh);
-            acc_hi = _mm512_mask_sub_epi8(acc_hi, neg[p], acc_hi, bh);
+            const int lv = ((x + 8) & 15) - 8;
+            l[p] = (int8_t)lv;
+            h[p] = (int8_t)((x - lv) >> 4);
         }
+        __m512i acc_lo = _mm512_setzero_si512(), acc_hi = _mm512_setzero_si512();
+#define VXC_PART(P)                                                                              \
+        do {                                                                                     \
+            const __m512i bl = _mm512_set1_epi8(l[P]), bh = _mm512_set1_epi8(h[P]);             \
+            acc_lo = _mm512_mask_add_epi8(acc_lo, p##P, acc_lo, bl);                             \
+            acc_lo = _mm512_mask_sub_epi8(acc_lo, n##P, acc_lo, bl);                             \
+            acc_hi = _mm512_mask_add_epi8(acc_hi, p##P, acc_hi, bh);                             \
+            acc_hi = _mm512_mask_sub_epi8(acc_hi, n##P, acc_hi, bh);                             \
+        } while (0)
+        VXC_PART(0);
+        VXC_PART(1);
+        VXC_PART(2);
+        VXC_PART(3);
+        VXC_PART(4);
+#undef VXC_PART
         _mm512_storeu_si512((void*)(lo_dst + c * 64), acc_lo);
         _mm512_storeu_si512((void*)(hi_dst + c * 64), acc_hi);
     }
@@ -109,25 +131,30 @@ VXC_TARGET static void put_rows(__m512i a0, __m512i a1, __m512i b0, __m512i b1, 
 #define VXC_CHUNK 45
 #define VXC_PF 4096
 
+/* compact_multi_block::<NB, ...> for one compile-time NB (the reference's const generic), so that the per-block
+ * registers are registers: the body is always inlined into multi_block_3 / multi_block_1 with nb a constant. */
 VXC_TARGET static inline __attribute__((always_inline)) void multi_block(const int nb, const uint8_t* w, size_t stride,
                                                                           const int8_t* lo, const int8_t* hi,
                                                                           size_t bpr, float* out) {
-    uint8_t th_b[64], tm_b[64];
-    for (int i = 0; i < 64; ++i) {
-        th_b[i] = (uint8_t)(i / 7);
-        tm_b[i] = (uint8_t)(28 * (i / 7) - 9);
-    }
+    static const uint8_t th_b[64] = {
+        0, 0, 0, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1, 2, 2, 2, 2, 2, 2, 2, 3, 3, 3, 3, 3, 3, 3, 4, 4, 4, 4,
+        4, 4, 4, 5, 5, 5, 5, 5, 5, 5, 6, 6, 6, 6, 6, 6, 6, 7, 7, 7, 7, 7, 7, 7, 8, 8, 8, 8, 8, 8, 8, 9};
+    uint8_t tm_b[64];
+    for (int i = 0; i < 64; ++i) tm_b[i] = (uint8_t)(28 * th_b[i] - 9); /* 28 floor(i / 7) - 9 (avx512.rs:1266-1275) */
     const __m512i th = _mm512_loadu_si512((const void*)th_b), tm = _mm512_loadu_si512((const void*)tm_b);
     const __m512i combine = _mm512_set1_epi16(0x1001);
     const __m512i zero = _mm512_setzero_si512();
     __m512i a0[VXC_NB_MAX], a1[VXC_NB_MAX], b0[VXC_NB_MAX], b1[VXC_NB_MAX];
+#pragma GCC unroll 4
     for (int b = 0; b < nb; ++b) a0[b] = a1[b] = b0[b] = b1[b] = zero;
     for (size_t c = 0; c < bpr;) {
         const size_t len = bpr - c < VXC_CHUNK ? bpr - c : VXC_CHUNK;
         __m512i sa[VXC_NB_MAX], sb[VXC_NB_MAX];
+#pragma GCC unroll 4
         for (int b = 0; b < nb; ++b) sa[b] = sb[b] = zero;
         for (size_t ci = 0; ci < len;) {
             const size_t n = len - ci < 3 ? len - ci : 3;
+#pragma GCC unroll 4
             for (int b = 0; b < nb; ++b) {
                 const char* base = (const char*)(w + b * stride + (c + ci) * 64);
                 _mm_prefetch(base + VXC_PF, _MM_HINT_T0);
@@ -135,10 +162,13 @@ VXC_TARGET static inline __attribute__((always_inline)) void multi_block(const i
                 _mm_prefetch(base + VXC_PF + 128, _MM_HINT_T0);
             }
             __m512i slo[VXC_NB_MAX], shi[VXC_NB_MAX];
-            for (size_t j = 0; j < n; ++j) {
+#pragma GCC unroll 3
+            for (size_t j = 0; j < 3; ++j) {
+                if (j >= n) break;
                 const size_t col = c + ci + j;
                 const __m512i tl = _mm512_loadu_si512((const void*)(lo + col * 64));
                 const __m512i tt = _mm512_loadu_si512((const void*)(hi + col * 64));
+#pragma GCC unroll 4
                 for (int b = 0; b < nb; ++b) {
                     const __m512i wv = _mm512_loadu_si512((const void*)(w + b * stride + col * 64));
                     const __m512i idx = _mm512_srli_epi16(wv, 2);
@@ -146,16 +176,23 @@ VXC_TARGET static inline __attribute__((always_inline)) void multi_block(const i
                     const __m512i r3 = _mm512_sub_epi8(wv, _mm512_permutexvar_epi8(idx, tm));
                     const __m512i l = _mm512_add_epi8(_mm512_permutexvar_epi8(h34, tl), _mm512_permutexvar_epi8(r3, tl));
                     const __m512i h = _mm512_add_epi8(_mm512_permutexvar_epi8(h34, tt), _mm512_permutexvar_epi8(r3, tt));
-                    slo[b] = j == 0 ? l : _mm512_add_epi8(slo[b], l);
-                    shi[b] = j == 0 ? h : _mm512_add_epi8(shi[b], h);
+                    if (j == 0) {
+                        slo[b] = l;
+                        shi[b] = h;
+                    } else {
+                        slo[b] = _mm512_add_epi8(slo[b], l);
+                        shi[b] = _mm512_add_epi8(shi[b], h);
+                    }
                 }
             }
+#pragma GCC unroll 4
             for (int b = 0; b < nb; ++b) {
                 sa[b] = _mm512_add_epi16(sa[b], _mm512_maddubs_epi16(combine, _mm512_unpacklo_epi8(slo[b], shi[b])));
                 sb[b] = _mm512_add_epi16(sb[b], _mm512_maddubs_epi16(combine, _mm512_unpackhi_epi8(slo[b], shi[b])));
             }
             ci += n;
         }
+#pragma GCC unroll 4
         for (int b = 0; b < nb; ++b) {
             a0[b] = _mm512_add_epi32(a0[b], _mm512_cvtepi16_epi32(_mm512_castsi512_si256(sa[b])));
             a1[b] = _mm512_add_epi32(a1[b], _mm512_cvtepi16_epi32(_mm512_extracti64x4_epi64(sa[b], 1)));
@@ -167,13 +204,23 @@ VXC_TARGET static inline __attribute__((always_inline)) void multi_block(const i
     for (int b = 0; b < nb; ++b) put_rows(a0[b], a1[b], b0[b], b1[b], out + b * 64);
 }
 
+VXC_TARGET static void multi_block_3(const uint8_t* w, size_t stride, const int8_t* lo, const int8_t* hi, size_t bpr,
+                                     float* out) {
+    multi_block(3, w, stride, lo, hi, bpr, out);
+}
+
+VXC_TARGET static void multi_block_1(const uint8_t* w, size_t stride, const int8_t* lo, const int8_t* hi, size_t bpr,
+                                     float* out) {
+    multi_block(1, w, stride, lo, hi, bpr, out);
+}
+
 VXC_TARGET static void gemv_blocks(const uint8_t* w, const int8_t* tables, size_t nblocks, size_t bpr, float* out) {
     const size_t stride = 64 * bpr;
     const int8_t* lo = tables;
     const int8_t* hi = tables + bpr * 64;
     size_t b = 0;
-    for (; b + 3 <= nblocks; b += 3) multi_block(3, w + b * stride, stride, lo, hi, bpr, out + b * 64);
-    for (; b < nblocks; ++b) multi_block(1, w + b * stride, stride, lo, hi, bpr, out + b * 64);
+    for (; b + 3 <= nblocks; b += 3) multi_block_3(w + b * stride, stride, lo, hi, bpr, out + b * 64);
+    for (; b < nblocks; ++b) multi_block_1(w + b * stride, stride, lo, hi, bpr, out + b * 64);
 }
 
 void vxc_gemv_tables(const uint8_t* tiles64, const int8_t* tables, size_t rows, size_t cols, float* out, int threads) {
@@ -283,4 +330,21 @@ uint64_t vxc_read_stream(const uint64_t* buf, size_t words, int threads) {
         total += read_range(buf, w0, w0 + per < words ? w0 + per : words);
     }
     return total;
+}
+
+/* The calling thread's core clock: eight dependent register-to-register adds per iteration retire at one per cycle,
+ * so cycles = 8 x iterations, timed against CLOCK_MONOTONIC. (Adds of an immediate would not do: some cores fold
+ * chains of them at register renaming.) */
+double vxc_clock_hz(void) {
+    const uint64_t iters = 50000000;
+    uint64_t x = 0;
+    const uint64_t one = 1;
+    struct timespec t0, t1;
+    clock_gettime(CLOCK_MONOTONIC, &t0);
+    for (uint64_t i = 0; i < iters; ++i)
+        __asm__ volatile("add %1, %0\n\tadd %1, %0\n\tadd %1, %0\n\tadd %1, %0\n\t"
+                         "add %1, %0\n\tadd %1, %0\n\tadd %1, %0\n\tadd %1, %0" : "+r"(x) : "r"(one));
+    clock_gettime(CLOCK_MONOTONIC, &t1);
+    const double dt = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+    return x == 8 * iters ? 8.0 * (double)iters / dt : 0.0;
 }

@@ -30,6 +30,8 @@ void vxc_fill_valid(uint8_t* out, size_t n, uint64_t seed);
 /* Pins OpenMP thread t of a team of n to logical CPU cpus[t]; returns the threads that could not be pinned. */
 int vxc_pin_threads(const int* cpus, int n);
 uint64_t vxc_read_stream(const uint64_t* buf, size_t words, int threads);
+/* The calling thread's core clock in Hz, from a timed chain of dependent adds (one per cycle). */
+double vxc_clock_hz(void);
 
 #ifdef __cplusplus
 }

@@ -115,6 +115,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "vxc_build_tables": (None, [vp, sz, vp]),
         "vxc_gemv_tables": (None, [vp, vp, sz, sz, vp, ctypes.c_int]),
         "vxc_gemv": (None, [vp, vp, sz, sz, vp, ctypes.c_int, vp]),
+        "vxc_clock_hz": (ctypes.c_double, []),
         "vxc_gemv_group": (None, [vp, vp, ctypes.c_int, vp, sz, vp, ctypes.c_int, vp]),
         "vxc_fill_valid": (None, [vp, sz, ctypes.c_uint64]),
         "vxc_read_stream": (u64, [vp, sz, ctypes.c_int]),
