@@ -208,7 +208,10 @@ int vx_gemv_lut_f32_dev(const vx_matrix_t* matrix, const int8_t* lut, size_t lut
 
 /*
  * TernaryGemvLayer::forward (layer.rs:74) on host memory: acts (acts_len >= cols) and out (out_capacity >= rows) are
- * host buffers; the call returns when out holds y = alpha * beta * (W x) with the epilogue of vx_gemv_f32_dev.
+ * host buffers; the call returns when out holds y = alpha * beta * (W x) with the epilogue of vx_gemv_f32_dev. The
+ * matrix keeps a pinned host buffer and a stream for these calls (made at the first call); calls on one matrix are
+ * serialised by its lock, and device calls on the same matrix still in flight on other streams must be waited for
+ * by the caller first.
  */
 int vx_layer_forward(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_len, float act_scale, float* out,
                      size_t out_capacity);
@@ -239,6 +242,10 @@ typedef struct vx_gemv_job {
     const float* act_scale_dev;  /* device; read when out_f32 = 1 */
     void* out;                   /* device; rows values */
     size_t out_capacity;
+    /* device, optional (NULL, or a struct_size that ends before this field): cols int8 activations that each run
+     * stages into `staged` first, every distinct (acts, staged) pair once, all of them in one launch before the
+     * GEMVs (velurex plans only; jobs that share `staged` must then share `acts`) */
+    const int8_t* acts;
 } vx_gemv_job_t;
 
 typedef struct vx_plan vx_plan_t;

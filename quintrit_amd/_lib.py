@@ -179,7 +179,7 @@ class GemvJob(ctypes.Structure):
     """vx_gemv_job_t (include/velurex_hip.h)."""
     _fields_ = [("struct_size", ctypes.c_uint32), ("out_f32", ctypes.c_int32), ("matrix", ctypes.c_void_p),
                 ("staged", ctypes.c_void_p), ("staged_len", ctypes.c_size_t), ("act_scale_dev", ctypes.c_void_p),
-                ("out", ctypes.c_void_p), ("out_capacity", ctypes.c_size_t)]
+                ("out", ctypes.c_void_p), ("out_capacity", ctypes.c_size_t), ("acts", ctypes.c_void_p)]
 
 
 class Plan:
@@ -189,7 +189,8 @@ class Plan:
         arr = (GemvJob * len(jobs))()
         for i, j in enumerate(jobs):
             arr[i] = j
-            arr[i].struct_size = ctypes.sizeof(GemvJob)
+            if not arr[i].struct_size:  # a caller may give the older, shorter size (no acts field)
+                arr[i].struct_size = ctypes.sizeof(GemvJob)
         h = ctypes.c_void_p()
         check(lib().vx_plan_create(arr, len(jobs), ctypes.byref(h)))
         self._h = h

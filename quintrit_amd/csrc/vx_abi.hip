@@ -71,6 +71,8 @@ static void destroy(vx_matrix* m) {
     if (m->d_dsum) (void)hipFree(m->d_dsum);
     if (m->d_staged) (void)hipFree(m->d_staged);
     if (m->d_io) (void)hipFree(m->d_io);
+    if (m->io_stream) (void)hipStreamDestroy(m->io_stream);
+    if (m->h_io) (void)hipHostFree(m->h_io);
     m->magic = 0;
     delete m;
 }
@@ -541,11 +543,29 @@ int vx_layer_forward(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_
         vx_matrix* m = const_cast<vx_matrix*>(matrix);
         std::lock_guard<std::mutex> lock(m->mu);
         VX_TRY(set_device_of(m));
-        int8_t* d_acts = m->d_io;
-        float* d_out = reinterpret_cast<float*>(m->d_io + round_up(m->g.cols, 256));
-        VX_HIP(hipMemcpy(d_acts, acts, m->g.cols, hipMemcpyHostToDevice));
-        VX_TRY(gemv_f32_dev(m, d_acts, act_scale, d_out, nullptr));
-        VX_HIP(hipMemcpy(out, d_out, m->g.rows * sizeof(float), hipMemcpyDeviceToHost));
+        // The activations go into a pinned host buffer that the staging kernel reads over the bus, and the GEMV writes
+        // its outputs into the same buffer: no copy engine, one synchronisation (two synchronous copies through
+        // pageable memory cost 15-25 us per call at the Falcon3-10B shapes).
+        const size_t out_off = round_up(m->g.cols, 256);
+        if (m->h_io == nullptr) {
+            void* h = nullptr;
+            VX_HIP(hipHostMalloc(&h, out_off + m->g.padded_rows * 4, hipHostMallocDefault));
+            void* hd = nullptr;
+            hipError_t e = hipHostGetDevicePointer(&hd, h, 0);
+            hipStream_t st = nullptr;
+            if (e == hipSuccess) e = hipStreamCreate(&st);
+            if (e != hipSuccess) {
+                (void)hipHostFree(h);
+                VX_FAIL(VX_ERR_DEVICE, "pinned staging for vx_layer_forward failed: %s", hipGetErrorString(e));
+            }
+            m->h_io = static_cast<int8_t*>(h);
+            m->h_io_dev = static_cast<int8_t*>(hd);
+            m->io_stream = st;
+        }
+        std::memcpy(m->h_io, acts, m->g.cols);
+        VX_TRY(gemv_f32_dev(m, m->h_io_dev, act_scale, reinterpret_cast<float*>(m->h_io_dev + out_off), m->io_stream));
+        VX_HIP(hipStreamSynchronize(m->io_stream));
+        std::memcpy(out, m->h_io + out_off, m->g.rows * sizeof(float));
         return VX_OK;
     });
 }
@@ -606,6 +626,7 @@ static void destroy_plan(vx_plan* p) {
     if (p->d_part) (void)hipFree(p->d_part);
     if (p->d_split) (void)hipFree(p->d_split);
     if (p->d_q2jobs) (void)hipFree(p->d_q2jobs);
+    if (p->d_stage) (void)hipFree(p->d_stage);
     p->magic = 0;
     delete p;
 }
@@ -621,10 +642,14 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, bool lut, vx_pl
     size_t part_ints = 0;
     uint32_t items = 0;
     std::vector<uint32_t> split;
+    std::vector<StageJob> stages;  // distinct (acts, staged) pairs of jobs that bring raw activations
+    constexpr size_t kJobSizeNoActs = offsetof(vx_gemv_job_t, acts);
     for (size_t i = 0; i < n_jobs; ++i) {
         const vx_gemv_job_t& u = jobs[i];
-        if (u.struct_size != sizeof(vx_gemv_job_t))
-            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].struct_size is %u, expected %zu", i, u.struct_size, sizeof(vx_gemv_job_t));
+        if (u.struct_size != sizeof(vx_gemv_job_t) && u.struct_size != kJobSizeNoActs)
+            VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].struct_size is %u, expected %zu (or %zu without acts)", i,
+                    u.struct_size, sizeof(vx_gemv_job_t), kJobSizeNoActs);
+        const int8_t* raw = u.struct_size == sizeof(vx_gemv_job_t) ? u.acts : nullptr;
         VX_TRY(check_kind(u.matrix, kKindVelurex));
         const vx_matrix* m = u.matrix;
         if (m->device != di.device)
@@ -639,6 +664,25 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, bool lut, vx_pl
             VX_FAIL(VX_ERR_BUFFER_TOO_SMALL, "jobs[%zu]: out holds %zu values but rows = %zu", i, u.out_capacity, m->g.rows);
         if (u.out_f32 != 0 && u.out_f32 != 1) VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu].out_f32 must be 0 or 1", i);
         if (u.out_f32 == 1 && u.act_scale_dev == nullptr) VX_FAIL(VX_ERR_NULL_POINTER, "jobs[%zu].act_scale_dev is NULL", i);
+        {
+            // a staging of this job's input: new, the same as an earlier job's, or a conflict
+            uint8_t* dst = static_cast<uint8_t*>(const_cast<void*>(u.staged));
+            bool seen = false;
+            for (const StageJob& sj : stages) {
+                if (sj.staged != dst) continue;
+                if (sj.acts != raw || sj.cols != m->g.cols)
+                    VX_FAIL(VX_ERR_INVALID_ARGUMENT, "jobs[%zu]: its staged buffer is staged by an earlier job from "
+                            "other activations", i);
+                seen = true;
+            }
+            if (raw != nullptr && lut)
+                VX_FAIL(VX_ERR_UNSUPPORTED, "jobs[%zu]: raw activations are staged by velurex plans only", i);
+            if (raw != nullptr && !seen)
+                stages.push_back(StageJob{raw, dst, static_cast<uint32_t>(m->g.cols), static_cast<uint32_t>(m->g.tbr),
+                                          static_cast<uint32_t>(m->g.dbr), stage_groups(m->g.cols)});
+            if (raw == nullptr && !seen)  // a job that reads a staged input the caller keeps: remembered as such
+                stages.push_back(StageJob{nullptr, dst, static_cast<uint32_t>(m->g.cols), 0, 0, 0});
+        }
         Job& j = hj[i];
         j = Job{};
         if (lut) plan_lut_job(j, m->g, 0);
@@ -673,8 +717,21 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, bool lut, vx_pl
     p->max_rows = 0;
     p->n_split = static_cast<uint32_t>(split.size());
     p->lut = lut ? 1u : 0u;
+    p->d_stage = nullptr;
+    p->n_stage = 0;
+    p->stage_max_groups = 0;
     for (uint32_t i : split) p->max_rows = std::max(p->max_rows, hj[i].rows);
+    std::vector<StageJob> st;
+    for (const StageJob& sj : stages)
+        if (sj.acts != nullptr) {
+            st.push_back(sj);
+            p->stage_max_groups = std::max(p->stage_max_groups, sj.groups);
+        }
+    p->n_stage = static_cast<uint32_t>(st.size());
     hipError_t e = hipMalloc(&p->d_jobs, n_jobs * sizeof(Job));
+    if (e == hipSuccess && !st.empty()) e = hipMalloc(&p->d_stage, st.size() * sizeof(StageJob));
+    if (e == hipSuccess && !st.empty())
+        e = hipMemcpy(p->d_stage, st.data(), st.size() * sizeof(StageJob), hipMemcpyHostToDevice);
     if (e == hipSuccess && part_ints) e = hipMalloc(&p->d_part, part_ints * sizeof(int32_t));
     if (e == hipSuccess && !split.empty()) e = hipMalloc(&p->d_split, split.size() * sizeof(uint32_t));
     if (e == hipSuccess && !split.empty())
@@ -721,6 +778,7 @@ int vx_plan_run(const vx_plan_t* plan, void* stream) {
         a.jobs = plan->d_jobs;
         a.n_jobs = plan->n_jobs;
         a.total_items = plan->total_items;
+        VX_TRY(launch_stage_batch(plan->d_stage, plan->n_stage, plan->stage_max_groups, static_cast<hipStream_t>(stream)));
         if (plan->lut)
             return launch_gemv_lut(a, plan->max_rows, plan->d_split, plan->n_split, plan->num_cus,
                                    static_cast<hipStream_t>(stream));
@@ -941,6 +999,8 @@ int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_pl
         p->d_part = nullptr;
         p->d_split = nullptr;
         p->d_q2jobs = nullptr;
+        p->d_stage = nullptr;
+        p->n_stage = 0;
         p->n_jobs = static_cast<uint32_t>(n_jobs);
         p->total_items = items;
         p->max_rows = 0;

@@ -1082,6 +1082,23 @@ __host__ __device__ constexpr uint32_t attn_threads(uint32_t hd) { return 64u * 
 
 // f16 value of an f32 (round to nearest even, after the f32 rounding of x), kept in an f32
 __device__ __forceinline__ float r16(float x) { return static_cast<float>(static_cast<_Float16>(keep_f32(x))); }
+// r16 of every value of a lane's coordinates; two at a time with one packed conversion (v_cvt_pk_f16_f32, each value
+// rounded to nearest even after its own f32 rounding, as r16 does).
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+template <uint32_t N>
+__device__ __forceinline__ void r16_all(float (&y)[N]) {
+#pragma unroll
+    for (uint32_t m = 0; m + 1 < N; m += 2) {
+        half2_t h;
+        h.x = static_cast<_Float16>(keep_f32(y[m]));
+        h.y = static_cast<_Float16>(keep_f32(y[m + 1]));
+        uint32_t u = __builtin_bit_cast(uint32_t, h);
+        asm volatile("" : "+v"(u));  // the pair stays one packed conversion (not folded back into two)
+        y[m] = f16_f32(static_cast<uint16_t>(u));
+        y[m + 1] = f16_f32(static_cast<uint16_t>(u >> 16));
+    }
+    if constexpr (N % 2 == 1) y[N - 1] = r16(y[N - 1]);
+}
 
 // One workgroup per query head (and token, PREFILL). First the inputs of the position: q of this head and k, v of its KV
 // head, RoPE over all head_dim coordinates (ops.rs:199-221, NEOX or Normal pairing: x0' = fma(x0, c, -(x1 s)),
@@ -1182,10 +1199,9 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
     }
 
     // The chain's V: group g holds positions 8 g .. 8 g + 7 (every tile read is below vstride: groups run to the chunk's
-    // end rounded up to 8). Its first kVDepth groups are requested right after each thread's first k below, so that
-    // they arrive during the scores, the scan and the exponentials without delaying the first score (loads complete in
-    // issue order). The value of the position itself, not yet visible in the cache to every workgroup, is patched from
-    // vp when its group is used.
+    // end rounded up to 8). Its first kVDepth groups are requested once the scores are done, so that they arrive during
+    // the scan and the exponentials without adding to the scores' registers. The value of the position itself, not yet
+    // visible in the cache to every workgroup, is patched from vp when its group is used.
     const bool chain = c < n_chunks && st < en;
     const uint32_t g_first = st / 8u, g_end = chain ? (en + 7u) / 8u : g_first + 1u;
     const uint32_t dl = has_d ? d0 : 0u;  // a lane without coordinates reads coordinate 0 and never uses it
@@ -1204,14 +1220,9 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
     {
         const uint32_t j = tid & 3u, g = tid >> 2;
         constexpr uint32_t kGroups = kThreads / 4u;
-        float qf[kBlk][8];
-#pragma unroll
-        for (int i = 0; i < kBlk; ++i) {
-            const uint4 qv = *reinterpret_cast<const uint4*>(qs + 32 * i + 8 * j);
-            const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
-#pragma unroll
-            for (int l = 0; l < 8; ++l) qf[i][l] = f16_f32(static_cast<uint16_t>(qw[l >> 1] >> ((l & 1) * 16)));
-        }
+        // q is read from LDS at each use (the 4-lane groups of a wave all read the same addresses: broadcasts), two
+        // f16 per register; each product widens both operands exactly, as f16_f32 does. Held in registers as f32 for
+        // the whole loop, it took 4 kBlk of them, which left room for one workgroup per CU instead of two.
         auto load_k = [&](uint32_t p, uint4 (&kr)[kBlk]) {
             if (p == pos) {
 #pragma unroll
@@ -1223,20 +1234,25 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
             }
         };
         auto score = [&](uint32_t p, const uint4 (&kr)[kBlk]) {
+            uint32_t qo = 8u * j;
+            asm volatile("" : "+v"(qo));  // keeps q's reads in the loop (the compiler would hoist them into registers)
             float acc[8];
 #pragma unroll
             for (int l = 0; l < 8; ++l) acc[l] = 0.0f;
 #pragma unroll
             for (int i = 0; i < kBlk; ++i) {
                 const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+                const uint4 qv = *reinterpret_cast<const uint4*>(qs + 32 * i + qo);
+                const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
                 for (int l = 0; l < 8; ++l)
-                    acc[l] = __builtin_fmaf(qf[i][l], f16_f32(static_cast<uint16_t>(kw[l >> 1] >> ((l & 1) * 16))), acc[l]);
+                    acc[l] = __builtin_fmaf(f16_f32(static_cast<uint16_t>(qw[l >> 1] >> ((l & 1) * 16))),
+                                            f16_f32(static_cast<uint16_t>(kw[l >> 1] >> ((l & 1) * 16))), acc[l]);
             }
 #pragma unroll
             for (int l = 0; l < 8; ++l) {
-                acc[l] = acc[l] + __shfl_xor(acc[l], 2);
-                acc[l] = acc[l] + __shfl_xor(acc[l], 1);
+                acc[l] = acc[l] + bits_f32(dpp32<kDppXor2>(f32_bits(acc[l])));  // lane j ^ 2 of the quad (DPP)
+                acc[l] = acc[l] + bits_f32(dpp32<kDppXor1>(f32_bits(acc[l])));  // lane j ^ 1
             }
             if (j == 0) {
                 const float t0 = acc[0] + acc[4], t1 = acc[1] + acc[5], t2 = acc[2] + acc[6], t3 = acc[3] + acc[7];
@@ -1246,8 +1262,6 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
         uint4 ka[kBlk], kn[kBlk];
         uint32_t p = g;
         if (p < seq) load_k(p, ka);
-#pragma unroll
-        for (uint32_t k = 0; k < kVDepth; ++k) load_group(g_first + k, ring[k]);
         for (; p < seq; p += 2u * kGroups) {  // unrolled by two so that the buffers keep their registers
             if (p + kGroups < seq) load_k(p + kGroups, kn);
             score(p, ka);
@@ -1256,6 +1270,8 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
             score(p + kGroups, kn);
         }
     }
+#pragma unroll
+    for (uint32_t k = 0; k < kVDepth; ++k) load_group(g_first + k, ring[k]);
     uint16_t vself[kCpl];
 #pragma unroll
     for (uint32_t m = 0; m < kCpl; ++m) vself[m] = vp[dl + 64u * m];
@@ -1335,8 +1351,9 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
                             for (uint32_t m = 0; m < kCpl; ++m) {
                                 const uint32_t wv[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
                                 const float v = f16_f32(static_cast<uint16_t>(wv[e >> 1] >> ((e & 1) * 16)));
-                                y[m] = r16(__builtin_fmaf(v, f[e], y[m]));
+                                y[m] = __builtin_fmaf(v, f[e], y[m]);
                             }
+                            r16_all(y);
                             ssum = ssum + f[e];
                         }
                     } else {  // a group with a new maximum or the chunk's edge (positions outside it skipped)
@@ -1348,12 +1365,15 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
                                 const float ev = __builtin_fabsf(f[e]);
                                 const float ms = nm ? ev : 1.0f, vs = nm ? 1.0f : ev;
 #pragma unroll
+                                for (uint32_t m = 0; m < kCpl; ++m) y[m] = y[m] * ms;
+                                r16_all(y);
+#pragma unroll
                                 for (uint32_t m = 0; m < kCpl; ++m) {
                                     const uint32_t wv[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
                                     const float v = f16_f32(static_cast<uint16_t>(wv[e >> 1] >> ((e & 1) * 16)));
-                                    y[m] = r16(y[m] * ms);
-                                    y[m] = r16(__builtin_fmaf(v, vs, y[m]));
+                                    y[m] = __builtin_fmaf(v, vs, y[m]);
                                 }
+                                r16_all(y);
                                 ssum = __builtin_fmaf(ssum, ms, vs);
                             }
                         }
@@ -1455,8 +1475,8 @@ __device__ __forceinline__ float score_dot4(const uint16_t* q, const uint4 (&kr)
     }
 #pragma unroll
     for (int l = 0; l < 8; ++l) {
-        acc[l] = acc[l] + __shfl_xor(acc[l], 2);
-        acc[l] = acc[l] + __shfl_xor(acc[l], 1);
+        acc[l] = acc[l] + bits_f32(dpp32<kDppXor2>(f32_bits(acc[l])));  // lane j ^ 2 of the quad (DPP)
+        acc[l] = acc[l] + bits_f32(dpp32<kDppXor1>(f32_bits(acc[l])));  // lane j ^ 1
     }
     const float t0 = acc[0] + acc[4], t1 = acc[1] + acc[5], t2 = acc[2] + acc[6], t3 = acc[3] + acc[7];
     return (t0 + t1) + (t2 + t3);
@@ -1999,8 +2019,8 @@ __global__ __launch_bounds__(kNT) void head_kernel(HeadArgs a) {
         // (a0 + a2) + (a1 + a3): lanes j and j ^ 2, then j and j ^ 1
 #pragma unroll
         for (int l = 0; l < 8; ++l) {
-            acc[l] = acc[l] + __shfl_xor(acc[l], 2);
-            acc[l] = acc[l] + __shfl_xor(acc[l], 1);
+            acc[l] = acc[l] + bits_f32(dpp32<kDppXor2>(f32_bits(acc[l])));  // lane j ^ 2 of the quad (DPP)
+            acc[l] = acc[l] + bits_f32(dpp32<kDppXor1>(f32_bits(acc[l])));  // lane j ^ 1
         }
         if (j == 0 && row_i < a.vocab) {
             const float g0 = acc[0] + acc[4], g1 = acc[1] + acc[5], g2 = acc[2] + acc[6], g3 = acc[3] + acc[7];

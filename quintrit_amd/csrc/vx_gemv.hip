@@ -53,14 +53,14 @@ typedef __attribute__((address_space(4))) const float c_float;
 // sum of all activations: workgroup w writes the sum of its entries to word w, workgroup 0 zeroes the words past the
 // grid.
 constexpr uint32_t kStageGroups = 16;
-__global__ __launch_bounds__(1024) void stage_kernel(const int8_t* __restrict__ acts, uint32_t cols, uint32_t tbr,
-                                                     uint32_t dbr, uint8_t* __restrict__ staged) {
+__device__ __forceinline__ void stage_body(const int8_t* __restrict__ acts, uint32_t cols, uint32_t tbr, uint32_t dbr,
+                                           uint8_t* __restrict__ staged, uint32_t group, uint32_t n_groups) {
     __shared__ int wsum[16];
     const uint32_t tid = threadIdx.x;
     const uint32_t full = cols / 160u * 32u;
     uint2* ent = reinterpret_cast<uint2*>(staged + kStageHeader);
     int sum = 0;
-    for (uint32_t c = blockIdx.x * 1024u + tid; c < dbr; c += gridDim.x * 1024u) {
+    for (uint32_t c = group * 1024u + tid; c < dbr; c += n_groups * 1024u) {
         uint32_t lo = 0, hi = 0;
         for (uint32_t p = 0; p < 5; ++p) {
             const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
@@ -78,9 +78,22 @@ __global__ __launch_bounds__(1024) void stage_kernel(const int8_t* __restrict__ 
         int s = wsum[tid];
         for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 16);
         int* hdr = reinterpret_cast<int*>(staged);
-        if (tid == 0) hdr[blockIdx.x] = s;
-        else if (blockIdx.x == 0 && tid >= gridDim.x) hdr[tid] = 0;
+        if (tid == 0) hdr[group] = s;
+        else if (group == 0 && tid >= n_groups) hdr[tid] = 0;
     }
+}
+
+__global__ __launch_bounds__(1024) void stage_kernel(const int8_t* __restrict__ acts, uint32_t cols, uint32_t tbr,
+                                                     uint32_t dbr, uint8_t* __restrict__ staged) {
+    stage_body(acts, cols, tbr, dbr, staged, blockIdx.x, gridDim.x);
+}
+
+// Many stagings in one launch (a plan's inputs): blockIdx.y is the staging, blockIdx.x its workgroup.
+__global__ __launch_bounds__(1024) void stage_batch_kernel(const StageJob* __restrict__ jobs) {
+    const uint32_t y = blockIdx.y;
+    const uint32_t groups = jobs[y].groups;
+    if (blockIdx.x >= groups) return;
+    stage_body(jobs[y].acts, jobs[y].cols, jobs[y].tbr, jobs[y].dbr, jobs[y].staged, blockIdx.x, groups);
 }
 
 // ---- layout transform -----------------------------------------------------------------------------------------------------
@@ -431,8 +444,19 @@ void plan_job(Job& j, const Geometry& g, uint32_t target_items) {
     j.n_chunks = nc;
 }
 
+uint32_t stage_groups(size_t cols) {
+    return static_cast<uint32_t>(std::max<size_t>(1, std::min<size_t>(kStageGroups, (device_row_bytes(cols) + 1023) / 1024)));
+}
+
+int launch_stage_batch(const StageJob* jobs, uint32_t n, uint32_t max_groups, hipStream_t stream) {
+    if (n == 0) return VX_OK;
+    hipLaunchKernelGGL(stage_batch_kernel, dim3(max_groups, n), dim3(1024), 0, stream, jobs);
+    VX_HIP(hipGetLastError());
+    return VX_OK;
+}
+
 int launch_stage(const int8_t* acts, size_t cols, uint8_t* staged, hipStream_t stream) {
-    const uint32_t groups = static_cast<uint32_t>(std::min<size_t>(kStageGroups, (device_row_bytes(cols) + 1023) / 1024));
+    const uint32_t groups = stage_groups(cols);
     hipLaunchKernelGGL(stage_kernel, dim3(std::max(groups, 1u)), dim3(1024), 0, stream, acts, static_cast<uint32_t>(cols),
                        static_cast<uint32_t>(tile_row_bytes(cols)), static_cast<uint32_t>(device_row_bytes(cols)), staged);
     VX_HIP(hipGetLastError());

@@ -176,6 +176,14 @@ inline uint32_t job_items(const Job& j) {
 }
 
 int launch_stage(const int8_t* acts, size_t cols, uint8_t* staged, hipStream_t stream);
+// One staging of a batch (vx_plan_run of a plan whose jobs bring raw activations).
+struct StageJob {
+    const int8_t* acts;
+    uint8_t* staged;
+    uint32_t cols, tbr, dbr, groups;
+};
+uint32_t stage_groups(size_t cols);
+int launch_stage_batch(const StageJob* jobs, uint32_t n, uint32_t max_groups, hipStream_t stream);
 // Launches the GEMV kernel and, when n_split > 0, the finish kernel over the split jobs (`split`: device array of their
 // indices in a.jobs; unused without a job array).
 int launch_gemv(const LaunchArgs& a, uint32_t max_rows, const uint32_t* split, uint32_t n_split, int num_cus,
@@ -285,7 +293,10 @@ struct vx_matrix {
     uint32_t* d_tickets;  // between calls
     int32_t* d_dsum;    // per padded row: digit sum of the device row (the signed low-nibble correction)
     uint8_t* d_staged;  // activation staging of the calls that take raw int8 activations
-    int8_t* d_io;       // host-API staging: cols bytes of activations + padded_rows * 4 bytes of output
+    int8_t* d_io;       // one-shot host API: cols bytes of activations + padded_rows * 4 bytes of output
+    int8_t* h_io;       // vx_layer_forward: pinned host buffer of the same shape, which the kernels read and write
+    int8_t* h_io_dev;   //   directly (its device address); made at the first call
+    hipStream_t io_stream;  // vx_layer_forward's stream on this matrix (default priority), made at the first call
     const void* owner;  // the decoder that adopted the matrix (it frees it), or null: the caller's
     std::mutex mu;      // serialises the host-pointer API on this handle
 };
@@ -305,6 +316,8 @@ struct vx_plan {
     vx::Q2Job* d_q2jobs;  // Q2_0 plans: their job table (d_jobs unused)
     uint32_t n_jobs, total_items, max_rows, n_split;
     uint32_t lut;  // the jobs read compact activation tables (vx_lut_plan_create)
+    vx::StageJob* d_stage;  // the distinct stagings of jobs that bring raw activations, run first (one launch)
+    uint32_t n_stage, stage_max_groups;
 };
 
 constexpr uint32_t kPlanMagic = 0x56585031u;  // "VXP1"

@@ -237,6 +237,58 @@ def test_golden_fixtures(torch_dev):
         layer.close()
 
 
+def test_plan_stages_raw_activations(torch_dev, oracle):
+    """Jobs that bring raw int8 activations (vx_gemv_job_t.acts): each run stages every distinct (acts, staged) pair
+    in one launch, then runs the GEMVs. Two jobs share one input (as q/k/v do), one job reads an input the caller
+    staged, one gives no acts field at all (the smaller struct_size); all outputs equal brute force, on two runs with
+    new activations; a staged buffer claimed by two different inputs is refused."""
+    from quintrit_amd import VelurexHipLayer, _lib
+    torch = torch_dev
+    L = _lib.lib()
+    rng = np.random.default_rng(77)
+    shapes = [(1024, 3072), (1024, 3072), (3072, 23040), (65, 161), (130, 3072)]
+    share = {0: 0, 1: 0, 2: 1, 3: 2, 4: 3}  # job -> input
+    cols_of = {0: 3072, 1: 23040, 2: 161, 3: 3072}
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    raw = {k: torch.empty(c, dtype=torch.int8, device="cuda") for k, c in cols_of.items()}
+    staged = {k: torch.empty(_lib.staged_bytes(c), dtype=torch.uint8, device="cuda") for k, c in cols_of.items()}
+    layers, mats, outs, jobs = [], [], [], []
+    for i, (rows, cols) in enumerate(shapes):
+        t = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+        layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, 1.0)
+        out = torch.empty(rows, dtype=torch.int32, device="cuda")
+        k = share[i]
+        j = _lib.GemvJob(out_f32=0, matrix=layer.handle.value, staged=staged[k].data_ptr(),
+                         staged_len=staged[k].numel(), out=out.data_ptr(), out_capacity=rows,
+                         acts=None if k == 3 else raw[k].data_ptr())
+        if k == 3:
+            j.struct_size = _lib.GemvJob.acts.offset  # a caller built against the job without the acts field
+        layers.append(layer), mats.append(t), outs.append(out), jobs.append(j)
+    plan = _lib.Plan(jobs)
+    for rep in range(2):
+        acts = {k: rng.integers(-128, 128, size=c, dtype=np.int8) for k, c in cols_of.items()}
+        for k, a in acts.items():
+            raw[k].copy_(torch.from_numpy(a))
+        # input 3 is the caller's own staging (no acts in its job)
+        _lib.check(L.vx_stage_acts_dev(ctypes.c_void_p(raw[3].data_ptr()), 3072, 3072,
+                                       ctypes.c_void_p(staged[3].data_ptr()), staged[3].numel(), stream))
+        plan.run(stream)
+        torch.cuda.synchronize()
+        for i, (t, out) in enumerate(zip(mats, outs)):
+            assert np.array_equal(out.cpu().numpy().astype(np.int64), exact_gemv(t, acts[share[i]])), (rep, i)
+    plan.close()
+    bad = [_lib.GemvJob(out_f32=0, matrix=layers[0].handle.value, staged=staged[0].data_ptr(),
+                        staged_len=staged[0].numel(), out=outs[0].data_ptr(), out_capacity=1024,
+                        acts=raw[0].data_ptr()),
+           _lib.GemvJob(out_f32=0, matrix=layers[1].handle.value, staged=staged[0].data_ptr(),
+                        staged_len=staged[0].numel(), out=outs[1].data_ptr(), out_capacity=1024,
+                        acts=raw[3].data_ptr())]
+    with pytest.raises(_lib.VxError, match="INVALID_ARGUMENT"):
+        _lib.Plan(bad)
+    for layer in layers:
+        layer.close()
+
+
 def test_batched_plan_mixed_jobs(torch_dev, oracle):
     """vx_plan_*: many GEMVs in one persistent launch, int32 and fp32 (scale read from device memory), long rows split
     into K slices; the plan runs again after its inputs change (its pointers are fixed, the contents are not)."""
