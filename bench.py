@@ -1410,7 +1410,7 @@ def main():
                                                                                 "bound": r["roofline"]["bound"]}
                 for r in gemm_measure(torch, L, _lib, 20, 5)]
         torch.cuda.empty_cache()
-        r = q2_measure(torch, L, _lib, 36, 20, 5)
+        r = q2_measure(torch, L, _lib, 36, 50, 10)
         q2 = {k: r[k] for k in ("layers", "ms_per_step", "Gweights_s", "alg_GBps", "tok_s_projection_bound")}
         q2["frac"] = r["roofline"]["frac"]
         torch.cuda.empty_cache()

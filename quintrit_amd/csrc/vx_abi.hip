@@ -90,6 +90,9 @@ static int check_planar(const uint8_t* planar, size_t planar_len, size_t rows, s
 static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix** out) {
     DeviceInfo di;
     VX_TRY(device_info(&di));
+    // the no-allocation GEMM's scratch address, looked up outside any graph capture (a failure is reported by that
+    // entry point's own calls, not here)
+    if (gemm_scratch_prepare(di.device) != VX_OK) clear_error();
     vx_matrix* m = new vx_matrix();
     m->magic = kMatrixMagic;
     m->kind = kKindVelurex;

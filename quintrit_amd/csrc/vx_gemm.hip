@@ -910,6 +910,11 @@ static int scratch_address(int device, uint8_t** out) {
     return VX_OK;
 }
 
+int gemm_scratch_prepare(int device) {
+    uint8_t* p = nullptr;
+    return scratch_address(device, &p);
+}
+
 int launch_gemm_noalloc(const uint8_t* w, const Geometry& g, int device, int num_cus, const int8_t* x, size_t M,
                         size_t ldx, int32_t* y, size_t ldy, hipStream_t stream) {
     const size_t need = gemm_workspace_bytes(g, M, num_cus);

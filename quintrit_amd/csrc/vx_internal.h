@@ -228,6 +228,9 @@ int launch_gemm_staged(const uint8_t* w, const Geometry& g, int num_cus, const u
                        size_t ldy, uint8_t* part, hipStream_t stream);
 // The same GEMM with its workspace in the library's per-device scratch array (kNoAllocScratchBytes): no allocation.
 constexpr size_t kNoAllocScratchBytes = VX_GEMM_NOALLOC_SCRATCH_BYTES;
+// Looks up (once per device; `device` must be current) the device address of the no-allocation GEMM's scratch, so
+// that vx_gemm_i32_noalloc_dev finds it ready and makes no runtime call of its own under graph capture.
+int gemm_scratch_prepare(int device);
 int launch_gemm_noalloc(const uint8_t* w, const Geometry& g, int device, int num_cus, const int8_t* x, size_t M,
                         size_t ldx, int32_t* y, size_t ldy, hipStream_t stream);
 // The GEMV through the compact activation tables (vx_lut.hip): a job's `staged` is the table of its cols

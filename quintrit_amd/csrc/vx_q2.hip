@@ -78,35 +78,42 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
 }
 
 typedef __attribute__((address_space(4))) const Q2Job c_q2job;
+typedef __attribute__((address_space(4))) const float c_q2float;  // uniform reads through the scalar cache
 
 // Work item: 8 consecutive tiles of a tile group (wave w: tile 8 half + w / 2, rows 32 (w % 2) .. + 31 of it). The
 // activations and their scales are staged in LDS once per item; every wave then streams its rows' blocks in order.
 template <bool MANY>
 __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
-    __shared__ uint2 tab[256 * 32];  // row B: 32 copies of (t0..t3 of byte B, t4 of B in every byte), 256 bytes
+    // row B (256 bytes): 32 copies of t0..t3 of byte B, then 32 copies of t4 of B in every byte; lane l of a half-wave
+    // reads copy l of each half (one address, offsets 0 and 128), so the t0..t3 dwords of four bytes land in the
+    // registers of one MFMA operand
+    __shared__ uint32_t tab[256 * 64];
     __shared__ uint32_t actw[kQ2MaxCols / 4 + 64];
-    __shared__ float ascl[kQ2MaxCols / 32];
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     for (uint32_t i = tid; i < 256u * 16u; i += kQ2Waves * 64u) {
-        const uint32_t b = i >> 4, e = g_trits.v[b], e4 = t4_bytes(b * 0x01010101u);
-        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + b * 256u + (i & 15u) * 16u) = make_uint4(e, e4, e, e4);
+        const uint32_t b = i >> 4, e = (i & 8u) ? t4_bytes(b * 0x01010101u) : g_trits.v[b];
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + b * 256u + (i & 15u) * 16u) = make_uint4(e, e, e, e);
     }
     const char* tabb = reinterpret_cast<const char*>(tab);
-    const uint32_t lane_off = (lane & 31u) * 8u;
+    const uint32_t lane_off = (lane & 31u) * 4u;
 
     // This lane's A' rows: C row mr = lane % 32 (plane p = mr / 8, lane sum j = mr % 8) and K half hh = lane / 32.
-    // sel[q] places byte q of the activation dword at byte p of K dword q (v_perm selector 0x0c gives 0x00); the
-    // result is used in the one K block m = j % 4 of the lanes with j / 4 == hh (on[m]) and is zero elsewhere. The
-    // plane-4 dword goes to dword u = j % 4 of the lanes with mr < 8 and mr / 4 == hh (on4[u]).
+    // Dword q of K block m places byte q of the activation dword at byte p (v_perm, selector byte 0x0c gives 0x00) in
+    // the one K block m = j % 4 of the lanes with j / 4 == hh, and is zero elsewhere: selm[m][q] is that selector or
+    // all 0x0c, so one v_perm builds each dword of every K block's operand. The plane-4 dword goes to dword u = j % 4
+    // of the lanes with mr < 8 and mr / 4 == hh (on4[u]).
     const uint32_t mr = lane & 31u, hh = lane >> 5, pl = mr >> 3, jl = mr & 7u;
-    uint32_t sel[4];
+    uint32_t selm[4][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) sel[q] = (0x0c0c0c0cu & ~(0xffu << (8u * pl))) | (static_cast<uint32_t>(q) << (8u * pl));
-    bool on[4], on4[4];
+    for (int m = 0; m < 4; ++m) {
+        const bool on = (jl >> 2) == hh && (jl & 3u) == static_cast<uint32_t>(m);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) on[m] = (jl >> 2) == hh && (jl & 3u) == static_cast<uint32_t>(m);
+        for (int q = 0; q < 4; ++q)
+            selm[m][q] = on ? (0x0c0c0c0cu & ~(0xffu << (8u * pl))) | (static_cast<uint32_t>(q) << (8u * pl)) : 0x0c0c0c0cu;
+    }
+    bool on4[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) on4[u] = mr < 8u && (mr >> 2) == hh && (mr & 3u) == static_cast<uint32_t>(u);
 
@@ -122,10 +129,10 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
         const uint32_t grp = local >> 1, tt = (local & 1u) * 8u + (wave >> 1), rb = wave & 1u;
         const uint32_t T = min(static_cast<uint32_t>(kTileGroup), jb.n_tiles - grp * kTileGroup);
         const uint32_t ns = jb.cols / 32u, nb = jb.nb, n_chunks = 2u * nb, ng = (nb + 3u) / 4u;
-        __syncthreads();  // the previous item is done with actw / ascl
+        __syncthreads();  // the previous item is done with actw
         const uint32_t* a32 = reinterpret_cast<const uint32_t*>(jb.acts);
         for (uint32_t i = tid; i < nb * 40u; i += kQ2Waves * 64u) actw[i] = i < jb.cols / 4u ? a32[i] : 0u;
-        for (uint32_t i = tid; i < ns; i += kQ2Waves * 64u) ascl[i] = jb.act_scales[i];
+        const c_q2float* asp = (const c_q2float*)(jb.act_scales);  // the activation scale of block s: asp[s]
         __syncthreads();
         if (tt >= T) continue;
         const uint32_t tile = grp * kTileGroup + tt;
@@ -155,7 +162,7 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
         // block b with its weights w and the scales sc of its group
         auto block = [&](uint32_t b, const u32x4 w, const uint32_t (&sc)[5]) __attribute__((always_inline)) {
             // W operand: K blocks 0..3 (t0..t3 of bytes 4 m .. 4 m + 3) and 4 (t4 of the 16 bytes)
-            // one 8-byte table entry per byte: t0..t3, and t4 in every byte, of which byte k of a dword keeps byte k
+            // two table reads per byte: t0..t3, and t4 in every byte, of which byte k of a dword keeps byte k
             const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
             v4i Bm[5];
             uint32_t t4w[4];
@@ -163,13 +170,17 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
             for (int m = 0; m < 4; ++m) {
                 int t[4];
                 uint32_t e4[4];
+                uint32_t addr[4];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const uint32_t addr = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + k) << 8));
-                    const uint2 e = *reinterpret_cast<const uint2*>(tabb + addr);
-                    t[k] = static_cast<int>(e.x);
-                    e4[k] = e.y;
+                    addr[k] = __builtin_amdgcn_perm(dw[m], lane_off, 0x0c0c0000u | ((4u + k) << 8));
+                    t[k] = static_cast<int>(*reinterpret_cast<const uint32_t*>(tabb + addr[k]));
                 }
+                // the t4 reads apart from the t0..t3 reads (merged pairwise, each pair would land in two adjacent
+                // registers and the operand would have to be copied together)
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) e4[k] = *reinterpret_cast<const uint32_t*>(tabb + addr[k] + 128u);
                 Bm[m] = v4i{t[0], t[1], t[2], t[3]};
                 t4w[m] = __builtin_amdgcn_perm(e4[3], e4[2], 0x07020c0cu) | __builtin_amdgcn_perm(e4[1], e4[0], 0x0c0c0500u);
             }
@@ -179,13 +190,12 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
             const uint32_t x4 = actw[(5u * b + 4u) * 8u + (mr & 7u)];
             v16i c = v16i{0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
             v16i c4 = c;
-            const int D[4] = {static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[0])),
-                              static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[1])),
-                              static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[2])),
-                              static_cast<int>(__builtin_amdgcn_perm(0u, x, sel[3]))};
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
-                const v4i A = v4i{on[m] ? D[0] : 0, on[m] ? D[1] : 0, on[m] ? D[2] : 0, on[m] ? D[3] : 0};
+                const v4i A = v4i{static_cast<int>(__builtin_amdgcn_perm(0u, x, selm[m][0])),
+                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, selm[m][1])),
+                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, selm[m][2])),
+                                  static_cast<int>(__builtin_amdgcn_perm(0u, x, selm[m][3]))};
                 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, Bm[m], c, 0, 0, 0);
             }
             {
@@ -200,7 +210,7 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
                 if (s >= ns) break;
                 const uint32_t kl = (5u * (b & 3u) + static_cast<uint32_t>(p)) / 2u;  // scale index in the group
                 const uint32_t hw = sc[kl >> 1] >> ((kl & 1u) * 16u);
-                const float d = half_bits_to_float(hw & 0xffffu) * ascl[s];
+                const float d = half_bits_to_float(hw & 0xffffu) * asp[s];
                 const bool odd = (s / 2u) & 1u;
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {

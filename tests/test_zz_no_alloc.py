@@ -45,6 +45,47 @@ def gemm_noalloc(torch, layer, xd, m, y):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("rows,cols,m", [(3072, 3072, 64), (23040, 3072, 256)])
+def test_noalloc_captured_in_a_graph(torch_dev, oracle, rows, cols, m):
+    """The entry point for callers under graph capture, captured (the first test of this file, so in a full run the
+    call that looks the scratch up runs inside the capture) and replayed three times with new activations and eager
+    work in between; every replay equals vx_gemm_i32_dev on the same inputs bit for bit. Two shapes: the small-M path
+    (3072 x 3072, 64 tokens) and the staged path (23040 x 3072, 256 tokens)."""
+    from quintrit_amd import VelurexHipLayer, _lib
+    torch = torch_dev
+    L = _lib.lib()
+    t = oracle.gen_trits(0x7C + rows, (rows, cols))
+    layer = VelurexHipLayer(oracle.pack_matrix(t), rows, cols, 1.0)
+    rng = np.random.default_rng(rows + m)
+    try:
+        xd = torch.zeros((m, cols), dtype=torch.int8, device="cuda")
+        got = torch.full((m, rows), -9, dtype=torch.int32, device="cuda")
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        print(f"[noalloc graph] capture {rows}x{cols} m={m}", flush=True)
+        with torch.cuda.graph(g, stream=side):
+            _lib.check(L.vx_gemm_i32_noalloc_dev(layer.handle, ctypes.c_void_p(xd.data_ptr()), m, cols,
+                                                 ctypes.c_void_p(got.data_ptr()), rows, _stream(torch)))
+        torch.cuda.synchronize()
+        for rep in range(3):
+            x = rng.integers(-128, 128, size=(m, cols), dtype=np.int8)
+            xd.copy_(torch.from_numpy(x))
+            want = torch.full((m, rows), -5, dtype=torch.int32, device="cuda")
+            gemm_with_workspace(torch, layer, xd, m, want)
+            torch.cuda.synchronize()
+            print(f"[noalloc graph] replay {rep}", flush=True)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(got, want), rep
+            got.fill_(-9)  # eager work between replays
+            torch.cuda.synchronize()
+        del g
+    finally:
+        layer.close()
+
+
 @pytest.mark.parametrize("rows,cols,m1,m2", [(3072, 23040, 128, 8), (23040, 3072, 512, 33), (2560, 2560, 64, 3)])
 def test_noalloc_equals_workspace_gemm_twice(torch_dev, oracle, rows, cols, m1, m2):
     """Two calls in a row on one matrix, the second with fewer tokens, each against vx_gemm_i32_dev on the same
