@@ -54,6 +54,8 @@ def parse():
                     help="stream: the driver's line (configs[1]); gemm: the batched GEMM of configs[2]; q2: the "
                          "block-scaled GEMV stream of configs[4]; decode: bs=1 greedy decode of configs[3]")
     ap.add_argument("--decode-new", type=int, default=256, help="decode mode: generated tokens per run")
+    ap.add_argument("--prefill-tokens", type=int, default=0,
+                    help="decode mode: only time the prefill of a prompt of this many tokens")
     ap.add_argument("--model", choices=["bitnet-2b", "falcon3-10b"], default="bitnet-2b",
                     help="decode mode: BASELINE.json configs[3]'s BitNet-2B, or a Falcon3-10B-shaped model (configs[1])")
     ap.add_argument("--copy-probe", action="store_true",
@@ -1144,6 +1146,8 @@ def decode_bench(torch, args) -> int:
     falcon3-10b  configs[1]'s Falcon3-10B shapes as a whole model: 40 layers, hidden 3072, 12/4 heads x 256, FFN 23040
                  SwiGLU, Normal RoPE, no sub-norms, vocab 131072, f16 embedding and untied f16 head"""
     falcon = args.model == "falcon3-10b"
+    if args.prefill_tokens:
+        return prefill_bench(torch, args)
     r, cfg, prompt = decode_measure(torch, args.model, n_new=args.decode_new, runs=max(1, args.steps // 10),
                                     layers=args.layers if falcon and args.layers != LAYERS else 0)
     cpu = None
@@ -1164,6 +1168,37 @@ def decode_bench(torch, args) -> int:
         "decode": r, "roofline": r["roofline"], "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def prefill_bench(torch, args) -> int:
+    """--workload decode --prefill-tokens N: the time to ingest an N-token random prompt (vx_decoder_prefill in passes
+    of at most 512 tokens, KV cache and last logits as N decode steps would leave them), best of two after a warm-up,
+    on the random-init model of --model; one JSON line. A compact command for profiling the prefill kernels."""
+    import numpy as np
+    from quintrit_amd.decoder import DecoderConfig
+    falcon = args.model == "falcon3-10b"
+    n = args.prefill_tokens
+    max_ctx = max(4096, (n + 255) // 256 * 256)
+    if falcon:
+        cfg = DecoderConfig.falcon3_10b(max_ctx=max_ctx, n_layers=args.layers if args.layers != LAYERS else 40)
+    else:
+        cfg = DecoderConfig.bitnet_2b(max_ctx=max_ctx)
+    dec = build_decoder_gpu(torch, cfg, 7)[0]
+    prompt = np.random.default_rng(n).integers(0, cfg.vocab, n)
+    dec.prefill(prompt, want_logits=False)  # warm-up (records the pass graphs)
+    best = float("inf")
+    for _ in range(2):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill(prompt, want_logits=False)
+        torch.cuda.synchronize()
+        best = min(best, time.perf_counter() - t0)
+    log(f"{args.model}: prefill of {n} tokens {best * 1e3:.1f} ms")
+    print(json.dumps({"workload": f"{args.model} prefill of a {n}-token prompt", "layers": cfg.n_layers,
+                      "prefill_ms": round(best * 1e3, 2), "tok_s": round(n / best, 1), "data": "synthetic"}),
+          flush=True)
+    dec.close()
     return 0
 
 
