@@ -35,6 +35,7 @@
 #include <cmath>
 #include <cstring>
 #include <initializer_list>
+#include <type_traits>
 #include <vector>
 
 namespace vx {
@@ -63,6 +64,16 @@ __device__ __forceinline__ uint16_t f32_f16(float f) {
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(keep_f32(f)));
 }
 __device__ __forceinline__ float f16_f32(uint16_t h) { return static_cast<float>(__builtin_bit_cast(_Float16, h)); }
+
+// f(std::integral_constant<uint32_t, k>) for k = 0 .. N - 1: a loop body with its index as a compile-time constant, so that
+// arrays indexed by it stay in fixed registers (a counted loop may be kept rolled, with the registers rotated).
+template <uint32_t N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<uint32_t, N - 1>{});
+    }
+}
 
 // ---- wave reductions (DPP within rows of 16 lanes, then the four row results) ------------------------------------------------
 
@@ -1309,23 +1320,27 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
 #pragma unroll
     for (uint32_t m = 0; m < kCpl; ++m) y[m] = 0.0f;
     if (chain) {
-        // the factors of the next group are read from LDS while the current group is summed
-        float4 na = *reinterpret_cast<const float4*>(sc + 8u * g_first);
-        float4 nb = *reinterpret_cast<const float4*>(sc + 8u * g_first + 4u);
+        // the factors of the next group are read from LDS while the current group is summed, into the other of two
+        // slots (slot k & 1 of group slot k: kVDepth is even, so the pattern repeats on every pass of the loop)
+        static_assert(kVDepth % 2 == 0, "two factor slots alternate over the ring");
+        float4 fq[2][2];
+        fq[0][0] = *reinterpret_cast<const float4*>(sc + 8u * g_first);
+        fq[0][1] = *reinterpret_cast<const float4*>(sc + 8u * g_first + 4u);
         for (uint32_t g0 = g_first; g0 < g_end; g0 += kVDepth) {
-#pragma unroll
-            for (uint32_t k = 0; k < kVDepth; ++k) {
+            static_for<kVDepth>([&](auto kc) {  // the ring's slot as a constant: no rotation of its registers
+                constexpr uint32_t k = decltype(kc)::value;
                 const uint32_t gg = g0 + k;
-                if (gg < g_end) {  // wave-uniform
-                    u32x4 w[kCpl];
-#pragma unroll
-                    for (uint32_t m = 0; m < kCpl; ++m) w[m] = ring[k][m];
-                    load_group(gg + kVDepth, ring[k]);
-                    const uint32_t p0 = 8u * gg;
-                    const float4 fa = na, fb = nb;
+                {
                     const uint32_t pn = 8u * min(gg + 1u, g_end - 1u);
-                    na = *reinterpret_cast<const float4*>(sc + pn);
-                    nb = *reinterpret_cast<const float4*>(sc + pn + 4u);
+                    fq[(k + 1u) & 1u][0] = *reinterpret_cast<const float4*>(sc + pn);
+                    fq[(k + 1u) & 1u][1] = *reinterpret_cast<const float4*>(sc + pn + 4u);
+                }
+                if (gg < g_end) {  // wave-uniform
+                    // the group's V words, used in place; the slot is refilled (kVDepth groups ahead) once they are
+                    // consumed, so that the refill lands in the same registers (no register rotation)
+                    u32x4(&w)[kCpl] = ring[k];
+                    const uint32_t p0 = 8u * gg;
+                    const float4 fa = fq[k & 1u][0], fb = fq[k & 1u][1];
                     if (pos >= p0 && pos < p0 + 8u) {  // the position itself, from this workgroup's copy
                         const uint32_t e = pos - p0, sh = (e & 1u) * 16u, keep = ~(0xffffu << sh);
 #pragma unroll
@@ -1356,7 +1371,77 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
                             r16_all(y);
                             ssum = ssum + f[e];
                         }
-                    } else {  // a group with a new maximum or the chunk's edge (positions outside it skipped)
+                    } else if (whole) {
+                        // a group with a new maximum: only the new maxima (the factor's sign, the same in every lane)
+                        // take the multiply, on a scalar branch; at the others ms = 1 leaves y as it is. The f16
+                        // values are carried packed (two coordinates) or as f16 (one), so that the branches join
+                        // without conversions.
+                        auto pk = [](float lo, float hi) {  // two f16 roundings in one packed conversion
+                            half2_t hh;
+                            hh.x = static_cast<_Float16>(keep_f32(lo));
+                            hh.y = static_cast<_Float16>(keep_f32(hi));
+                            uint32_t u = __builtin_bit_cast(uint32_t, hh);
+                            asm volatile("" : "+v"(u));
+                            return u;
+                        };
+                        auto lo16 = [](uint32_t u) { return f16_f32(static_cast<uint16_t>(u)); };
+                        auto hi16 = [](uint32_t u) { return f16_f32(static_cast<uint16_t>(u >> 16)); };
+                        uint32_t yp = 0;
+                        _Float16 yh = 0;
+                        if constexpr (kCpl == 2) yp = pk(y[0], y[1]);
+                        else yh = static_cast<_Float16>(y[0]);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const float ev = __builtin_fabsf(f[e]);
+                            const bool nm = __builtin_amdgcn_readfirstlane(f32_bits(f[e]) >> 31) != 0u;
+                            // the words of this position's V values; the new-maximum branch takes opaque copies of
+                            // them and of the state, so that the compiler does not convert them ahead of the branch
+                            // (the short step reads the f16 halves as operands of v_fma_mix_f32)
+                            uint32_t wv[kCpl];
+#pragma unroll
+                            for (uint32_t m = 0; m < kCpl; ++m) {
+                                const uint32_t ww[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
+                                wv[m] = ww[e >> 1];
+                            }
+                            const uint32_t sh = (e & 1) * 16;
+                            if (__builtin_expect(nm, 0)) {
+                                uint32_t wq[kCpl];
+#pragma unroll
+                                for (uint32_t m = 0; m < kCpl; ++m) {
+                                    wq[m] = wv[m];
+                                    asm volatile("" : "+v"(wq[m]));
+                                }
+                                if constexpr (kCpl == 2) {
+                                    uint32_t yq = yp;
+                                    asm volatile("" : "+v"(yq));
+                                    yq = pk(lo16(yq) * ev, hi16(yq) * ev);
+                                    yp = pk(__builtin_fmaf(f16_f32(static_cast<uint16_t>(wq[0] >> sh)), 1.0f, lo16(yq)),
+                                            __builtin_fmaf(f16_f32(static_cast<uint16_t>(wq[1] >> sh)), 1.0f, hi16(yq)));
+                                } else {
+                                    _Float16 yq = yh;
+                                    asm volatile("" : "+v"(yq));
+                                    yq = static_cast<_Float16>(keep_f32(static_cast<float>(yq) * ev));
+                                    yh = static_cast<_Float16>(keep_f32(
+                                        __builtin_fmaf(f16_f32(static_cast<uint16_t>(wq[0] >> sh)), 1.0f, static_cast<float>(yq))));
+                                }
+                            } else {
+                                if constexpr (kCpl == 2) {
+                                    yp = pk(__builtin_fmaf(f16_f32(static_cast<uint16_t>(wv[0] >> sh)), f[e], lo16(yp)),
+                                            __builtin_fmaf(f16_f32(static_cast<uint16_t>(wv[1] >> sh)), f[e], hi16(yp)));
+                                } else {
+                                    yh = static_cast<_Float16>(keep_f32(
+                                        __builtin_fmaf(f16_f32(static_cast<uint16_t>(wv[0] >> sh)), f[e], static_cast<float>(yh))));
+                                }
+                            }
+                            ssum = __builtin_fmaf(ssum, nm ? ev : 1.0f, nm ? 1.0f : ev);
+                        }
+                        if constexpr (kCpl == 2) {
+                            y[0] = lo16(yp);
+                            y[1] = hi16(yp);
+                        } else {
+                            y[0] = static_cast<float>(yh);
+                        }
+                    } else {  // the chunk's edge (positions outside it skipped)
                         const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(8u, en - p0);
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
@@ -1379,7 +1464,10 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
                         }
                     }
                 }
-            }
+                // every slot is refilled, used or not (the index stays inside the cache), so that the number of
+                // loads issued after a slot's refill, and with it the wait for the slot, is the same on every path
+                load_group(gg + kVDepth, ring[k]);
+            });
         }
     }
     float* out = a.out + (static_cast<size_t>(tok) * a.n_heads + h) * HD;
@@ -1552,8 +1640,8 @@ __global__ __launch_bounds__(256) void attn_score_kernel(AttnArgs a) {
 __device__ __forceinline__ float max_later(float earlier, float later) { return later > earlier ? later : earlier; }
 
 // The pieces of one chunk's online softmax (attend_range, attention.rs:436-468) over positions st .. en - 1, in blocks
-// of 32 positions b_first .. b_end - 1 (fac[i] is the factor of position 32 b_first + i, bflag[i] marks block b_first + i
-// when it holds a new maximum).
+// of 32 positions b_first .. b_end - 1 (fac[i] is the factor of position 32 b_first + i; bit e of bflag[i] marks position
+// 32 (b_first + i) + e when it holds a new maximum).
 //
 // chunk_factors (all NT threads; one barrier inside, one expected after): the running maximum by a scan (runs of
 // R = ceil(len / NT) positions per thread, an inclusive scan of the run maxima over the lanes and a prefix over the
@@ -1597,7 +1685,7 @@ __device__ __forceinline__ float chunk_factors(const float* scores, uint32_t st,
             const float sc = sv[r];
             const float f = sc > prev ? -glibc_expf_with(prev - sc, tab) : glibc_expf_with(sc - prev, tab);
             fac[off + i] = f;
-            if (__builtin_signbit(f)) bflag[(off + i) >> 5] = 1u;
+            if (__builtin_signbit(f)) atomicOr(bflag + ((off + i) >> 5), 1u << ((off + i) & 31u));
             prev = max_later(prev, sc != sc ? -__builtin_inff() : sc);
         }
     }
@@ -1640,14 +1728,13 @@ __device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const u
     };
     load_fac(b_first);
     for (uint32_t b0 = b_first; b0 < b_end; b0 += kChainBlocks) {
-#pragma unroll
-        for (uint32_t k = 0; k < kChainBlocks; ++k) {
+        static_for<kChainBlocks>([&](auto kc) {  // the ring's slot as a constant: no rotation of its registers
+            constexpr uint32_t k = decltype(kc)::value;
             const uint32_t b = b0 + k;
             if (b < b_end) {  // wave-uniform
-                u32x4 w[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) w[i] = ring[k][i];
-                load_vblock<HD>(vt, b + kChainBlocks, d, t_last, ring[k]);
+                // the block's V tiles, used in place; the slot is refilled (kChainBlocks blocks ahead) once they are
+                // consumed, so that the refill lands in the same registers
+                u32x4(&w)[4] = ring[k];
                 float f[32];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
@@ -1673,7 +1760,23 @@ __device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const u
                 if (p0 >= st && p0 + 32u <= en && flag == 0u) {
 #pragma unroll
                     for (int e = 0; e < 32; ++e) y = r16(__builtin_fmaf(vhalf(w, e), f[e], y));
-                } else {  // a new maximum or the chunk's edge: positions outside [st, en) keep y
+                } else if (p0 >= st && p0 + 32u <= en) {
+                    // A block with a new maximum: a position without one has ms = 1, where y * ms = y and its f16
+                    // rounding leave y unchanged, so only the new maxima (bits of the block's mask, a scalar branch
+                    // each) take the multiply; the others take the short step. y is carried as f16 (it holds an f16
+                    // value), so that the branches join without a conversion.
+                    _Float16 yh = static_cast<_Float16>(y);
+#pragma unroll
+                    for (int e = 0; e < 32; ++e) {
+                        if (__builtin_expect((flag >> e) & 1u, 0u)) {
+                            yh = static_cast<_Float16>(keep_f32(static_cast<float>(yh) * __builtin_fabsf(f[e])));
+                            yh = static_cast<_Float16>(keep_f32(__builtin_fmaf(vhalf(w, e), 1.0f, static_cast<float>(yh))));
+                        } else {
+                            yh = static_cast<_Float16>(keep_f32(__builtin_fmaf(vhalf(w, e), f[e], static_cast<float>(yh))));
+                        }
+                    }
+                    y = static_cast<float>(yh);
+                } else {  // the chunk's edge: positions outside [st, en) keep y
                     const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(32u, en - p0);
 #pragma unroll
                     for (int e = 0; e < 32; ++e) {
@@ -1687,7 +1790,10 @@ __device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const u
                     }
                 }
             }
-        }
+            // every slot is refilled, used or not (the tile index stays inside the cache), so that the number of loads
+            // issued after a slot's refill, and with it the wait for the slot, is the same on every path
+            load_vblock<HD>(vt, b + kChainBlocks, d, t_last, ring[k]);
+        });
     }
     return y;
 }
@@ -1712,6 +1818,13 @@ __device__ __forceinline__ float chain_sum(uint32_t st, uint32_t en, uint32_t b_
         if (p0 >= st && p0 + 32u <= en && flag == 0u) {
 #pragma unroll
             for (int e = 0; e < 32; ++e) ssum = ssum + f[e];
+        } else if (p0 >= st && p0 + 32u <= en) {  // a whole block with a new maximum: one dependent operation each
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const bool nm = __builtin_signbit(f[e]);
+                const float ev = __builtin_fabsf(f[e]);
+                ssum = __builtin_fmaf(ssum, nm ? ev : 1.0f, nm ? 1.0f : ev);
+            }
         } else {
             const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(32u, en - p0);
 #pragma unroll
@@ -1838,13 +1951,17 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
 // The decode step's attention while the context is short (pos < kShortCtx: one chunk, no split) in one kernel per
 // (head, 64 coordinates): the RoPE of q, k, v of the position (the first slice of the first head of each KV head
 // appends k and v; every workgroup uses its own copy of the position itself), the scores of every position
-// (512 threads, four lanes per position, as attn_score_kernel), the factors, then the accumulators (wave 0) and the sum
-// (wave 1), and the output.
+// (512 threads, four lanes per position, as attn_score_kernel), the factors, then the accumulators and the sum (one
+// wave), and the output. The loads go out in the order they are needed: the RoPE inputs, the K rows, then the V tiles of
+// the workgroup's 64 coordinates, which all threads stage into LDS during the scores, so that the chain reads V and the
+// factors from LDS in a compact loop.
 template <int HD>
 __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
     constexpr uint32_t kSlices = attn_slices(HD);
     constexpr uint32_t kLanes = HD >= 64 ? 64u : static_cast<uint32_t>(HD);
     constexpr int kBlk = HD / 32;
+    constexpr uint32_t kTiles = kShortCtx / 8u;           // 8-position V tiles of the context at most
+    constexpr uint32_t kVPer = kTiles * 64u / 512u;       // V entries (tile, coordinate) per thread
     __shared__ __align__(16) uint16_t qh[HD];
     __shared__ __align__(16) uint16_t kp[HD];
     __shared__ __align__(16) uint16_t vp[HD];
@@ -1852,22 +1969,39 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
     __shared__ __align__(16) float fac[kShortCtx + 64u];
     __shared__ uint32_t bflag[kShortCtx / 32u + 2u];
     __shared__ float wtot[8];
-    __shared__ float s_sum;
     __shared__ uint64_t etab[32];
+    __shared__ __align__(16) u32x4 vl[kTiles][64];  // [tile][coordinate]: positions 8 t .. 8 t + 7
+    __shared__ float s_sum;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t h = blockIdx.x / kSlices, sl = blockIdx.x - h * kSlices;
     const uint32_t pos = a.ctl->pos, seq = pos + 1u;  // seq <= kShortCtx (the host's choice of graph)
     const uint32_t kvh = h / a.gqa;
-    const uint32_t d = sl * 64u + (lane < kLanes ? lane : 0u);
     const uint16_t* kb = a.kc + static_cast<size_t>(kvh) * a.max_ctx * HD;
     uint16_t* vt = a.vc + static_cast<size_t>(kvh) * HD * a.vstride;
-    const uint32_t b_end = (seq + 31u) / 32u, t_last = (seq - 1u) / 8u;
+    const uint32_t t_last = (seq - 1u) / 8u;
     fill_etab(etab);
-    u32x4 ring[kChainBlocks][4];
-    if (wave == 0) {
-#pragma unroll
-        for (uint32_t k = 0; k < kChainBlocks; ++k) load_vblock<HD>(vt, k, d, t_last, ring[k]);
+
+    // RoPE inputs: thread i < HD / 2 rotates pair i of q, HD / 2 <= i < HD pair i - HD / 2 of k; HD <= i < 2 HD takes
+    // coordinate i - HD of v. The raw sums, the scale and the rotation are loaded before anything else.
+    const bool normal = a.rope_normal != 0u;
+    const bool is_q = tid < HD / 2u, is_k = !is_q && tid < HD, is_v = tid >= HD && tid < 2u * HD;
+    const ProjOut& po = is_q ? a.q : (is_k ? a.k : a.v);
+    const uint32_t pi = is_q ? tid : tid - HD / 2u;  // the pair (q, k)
+    const uint32_t i0 = normal ? 2u * pi : pi, i1 = normal ? 2u * pi + 1u : pi + HD / 2u;
+    float r_as = 0.0f, r_cc = 0.0f, r_ss = 0.0f;
+    int32_t r_x0 = 0, r_x1 = 0;
+    if (is_q || is_k) {
+        const uint32_t base = (is_q ? h : kvh) * HD;
+        r_as = *po.as;
+        r_x0 = po.part[base + i0];
+        r_x1 = po.part[base + i1];
+        const float* cache = a.rope + static_cast<size_t>(pos) * HD;
+        r_cc = cache[2u * pi];
+        r_ss = cache[2u * pi + 1u];
+    } else if (is_v) {
+        r_as = *a.v.as;
+        r_x0 = a.v.part[kvh * HD + (tid - HD)];
     }
     // K rows of this thread's two positions (the position itself later, from kp)
     const uint32_t j = tid & 3u, g = tid >> 2;
@@ -1881,23 +2015,57 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
         for (int i = 0; i < kBlk; ++i)
             k1[i] = *reinterpret_cast<const uint4*>(kb + static_cast<size_t>(g + 128u) * HD + 8 * j + 32 * i);
     }
-    const bool normal = a.rope_normal != 0u;
-    const float* cache = a.rope + static_cast<size_t>(pos) * HD;
-    if (tid < HD / 2u) {
-        rope_pair<HD>(a.q, h * HD, tid, normal, cache, qh);
-    } else if (tid < HD) {
-        rope_pair<HD>(a.k, kvh * HD, tid - HD / 2u, normal, cache, kp);
-    } else if (tid < 2u * HD) {
+    // V tiles of the slice's coordinates: entry e = tid + 512 r is (tile e / 64, coordinate e % 64)
+    u32x4 vr[kVPer];
+#pragma unroll
+    for (uint32_t r = 0; r < kVPer; ++r) {
+        const uint32_t e = tid + 512u * r, t = e >> 6, c = e & 63u;
+        if (t <= t_last && c < kLanes)
+            vr[r] = *reinterpret_cast<const u32x4*>(vt + (static_cast<size_t>(t) * HD + sl * 64u + c) * 8u);
+    }
+    if (is_q || is_k) {
         bool zero;
-        const float post = proj_post(a.v, &zero);
-        vp[tid - HD] = f32_f16(proj_at(a.v, kvh * HD + (tid - HD), post, zero));
+        const float post = proj_post(po, r_as, &zero);
+        const float x0 = proj_value(r_x0, post, zero), x1 = proj_value(r_x1, post, zero);
+        const float x1s = x1 * r_ss, x1c = x1 * r_cc;
+        uint16_t* dst = is_q ? qh : kp;
+        dst[i0] = f32_f16(__builtin_fmaf(x0, r_cc, -x1s));
+        dst[i1] = f32_f16(__builtin_fmaf(x0, r_ss, x1c));
+    } else if (is_v) {
+        bool zero;
+        const float post = proj_post(a.v, r_as, &zero);
+        vp[tid - HD] = f32_f16(proj_value(r_x0, post, zero));
     }
     __syncthreads();
     if (h % a.gqa == 0 && sl == 0 && tid < HD) {
         a.kc[(static_cast<size_t>(kvh) * a.max_ctx + pos) * HD + tid] = kp[tid];
         vt[(static_cast<size_t>(pos >> 3) * HD + tid) * 8u + (pos & 7u)] = vp[tid];
     }
-    const uint16_t vself = vp[d];
+    // The V tiles into LDS, the position's own value (not yet visible in the cache to every workgroup) from vp, and
+    // positions from seq to the end of the last 32-position block as -0: with a factor of +0 there (vs = 0, ms = 1) a
+    // step adds v * vs = -0, which leaves every accumulator value as it is (-0 + y = y, also for y = +0 or -0), so the
+    // last block needs no edge handling.
+    const uint32_t t_pad = (seq + 31u) / 32u * 4u;  // tiles up to the end of the last block
+#pragma unroll
+    for (uint32_t r = 0; r < kVPer; ++r) {
+        const uint32_t e = tid + 512u * r, t = e >> 6, c = e & 63u;
+        if (t < t_pad && c < kLanes) {
+            u32x4 w = t <= t_last ? vr[r] : u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+            if (t == t_last) {
+                const uint32_t el = pos & 7u;
+                const uint32_t self = vp[sl * 64u + c];
+                uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (uint32_t i = 0; i < 8; ++i) {
+                    const uint32_t sh = (i & 1u) * 16u, keep = ~(0xffffu << sh);
+                    const uint32_t val = i == el ? self : 0x8000u;  // the position itself, then the padding
+                    if (i >= el) ww[i >> 1] = (ww[i >> 1] & keep) | (val << sh);
+                }
+                w = u32x4{ww[0], ww[1], ww[2], ww[3]};
+            }
+            vl[t][c] = w;
+        }
+    }
     if (g == pos) {
 #pragma unroll
         for (int i = 0; i < kBlk; ++i) k0[i] = *reinterpret_cast<const uint4*>(kp + 32 * i + 8 * j);
@@ -1916,19 +2084,80 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
     }
     __syncthreads();
     (void)chunk_factors<512>(sc, 0u, seq, 0u, fac, bflag, wtot, etab);
+    if (tid >= seq && tid < t_pad * 8u) fac[tid] = 0.0f;  // the padding's factors (vs = +0, no new maximum)
     __syncthreads();
-    float y = 0.0f;
+
+    // The accumulator of the lane's coordinate (wave 0: y, f16) and the sum (wave 1: ssum, f32) over the positions in
+    // order, a block of 32 per step (the last one padded), its V words, factors and new-maximum mask read from LDS at
+    // the start of the step. A block without a new maximum takes the short step (one f16 rounding of fma(v, vs, y));
+    // one with new maxima takes the full step everywhere, y = f16(y * ms), y = f16(fma(v, vs, y)), with ms = 1, where
+    // the multiply and its rounding leave y as it is, at the positions without one. Both are straight-line code: a
+    // branch per position costs more than the longer step.
+    const uint32_t nb = (seq + 31u) / 32u;
     if (wave == 0) {
-        y = chain_y<HD>(ring, vt, d, 0u, seq, 0u, b_end, t_last, fac, bflag, pos, vself);
+        const uint32_t cl = lane < kLanes ? lane : 0u;
+        _Float16 yh = 0;
+        for (uint32_t b = 0; b < nb; ++b) {
+            u32x4 w[4];
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) w[i] = vl[4u * b + i][cl];
+            float f[32];
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                const float4 q = *reinterpret_cast<const float4*>(fac + 32u * b + 4u * i);
+                f[4 * i] = q.x;
+                f[4 * i + 1] = q.y;
+                f[4 * i + 2] = q.z;
+                f[4 * i + 3] = q.w;
+            }
+            if (__builtin_amdgcn_readfirstlane(bflag[b]) == 0u) {
+#pragma unroll
+                for (int e = 0; e < 32; ++e)
+                    yh = static_cast<_Float16>(keep_f32(__builtin_fmaf(vhalf(w, e), f[e], static_cast<float>(yh))));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 32; ++e) {
+                    const bool nm = __builtin_signbit(f[e]);
+                    const float ev = __builtin_fabsf(f[e]);
+                    yh = static_cast<_Float16>(keep_f32(static_cast<float>(yh) * (nm ? ev : 1.0f)));
+                    yh = static_cast<_Float16>(keep_f32(__builtin_fmaf(vhalf(w, e), nm ? 1.0f : ev, static_cast<float>(yh))));
+                }
+            }
+        }
+        __syncthreads();  // wave 1's sum
+        if (lane < kLanes) {
+            const float ssum = s_sum;
+            const float s_inv = ssum == 0.0f ? 0.0f : 1.0f / ssum;
+            a.out[static_cast<size_t>(h) * HD + sl * 64u + lane] = static_cast<float>(yh) * s_inv;
+        }
     } else if (wave == 1) {
-        const float ssum = chain_sum(0u, seq, 0u, b_end, fac, bflag);
+        float ssum = 0.0f;
+        for (uint32_t b = 0; b < nb; ++b) {
+            float f[32];
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) {
+                const float4 q = *reinterpret_cast<const float4*>(fac + 32u * b + 4u * i);
+                f[4 * i] = q.x;
+                f[4 * i + 1] = q.y;
+                f[4 * i + 2] = q.z;
+                f[4 * i + 3] = q.w;
+            }
+            if (__builtin_amdgcn_readfirstlane(bflag[b]) == 0u) {
+#pragma unroll
+                for (int e = 0; e < 32; ++e) ssum = ssum + f[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 32; ++e) {
+                    const bool nm = __builtin_signbit(f[e]);
+                    const float ev = __builtin_fabsf(f[e]);
+                    ssum = __builtin_fmaf(ssum, nm ? ev : 1.0f, nm ? 1.0f : ev);
+                }
+            }
+        }
         if (lane == 0) s_sum = ssum;
-    }
-    __syncthreads();
-    if (wave == 0 && lane < kLanes) {
-        const float ssum = s_sum;
-        const float s_inv = ssum == 0.0f ? 0.0f : 1.0f / ssum;
-        a.out[static_cast<size_t>(h) * HD + sl * 64u + lane] = y * s_inv;
+        __syncthreads();
+    } else {
+        __syncthreads();
     }
 }
 
