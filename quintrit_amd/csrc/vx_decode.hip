@@ -1353,8 +1353,26 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
                             w[m].w = q == 3 ? ((w[m].w & keep) | ins) : w[m].w;
                         }
                     }
-                    const float f[8] = {fa.x, fa.y, fa.z, fa.w, fb.x, fb.y, fb.z, fb.w};
-                    const bool whole = p0 >= st && p0 + 8u <= en;
+                    float f[8] = {fa.x, fa.y, fa.z, fa.w, fb.x, fb.y, fb.z, fb.w};
+                    // A group that starts inside the chunk is summed whole: at its positions from en on (the chunk's
+                    // last group) the factor becomes +0 (vs = 0, no new maximum) and V -0, so that a step there adds
+                    // -0 and leaves y and the sum as they are.
+                    const bool whole = p0 >= st;
+                    if (whole && p0 + 8u > en) {
+                        const uint32_t n = en - p0;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) f[e] = static_cast<uint32_t>(e) < n ? f[e] : 0.0f;
+#pragma unroll
+                        for (uint32_t m = 0; m < kCpl; ++m) {
+                            uint32_t ww[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
+#pragma unroll
+                            for (uint32_t q = 0; q < 4; ++q) {
+                                const uint32_t keep = (2u * q < n ? 0xffffu : 0u) | (2u * q + 1u < n ? 0xffff0000u : 0u);
+                                ww[q] = (ww[q] & keep) | (0x80008000u & ~keep);
+                            }
+                            w[m] = u32x4{ww[0], ww[1], ww[2], ww[3]};
+                        }
+                    }
                     uint32_t neg = 0;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) neg |= f32_bits(f[e]) >> 31;
@@ -1372,76 +1390,26 @@ __global__ __launch_bounds__(attn_threads(HD)) void attention_kernel(AttnArgs a)
                             ssum = ssum + f[e];
                         }
                     } else if (whole) {
-                        // a group with a new maximum: only the new maxima (the factor's sign, the same in every lane)
-                        // take the multiply, on a scalar branch; at the others ms = 1 leaves y as it is. The f16
-                        // values are carried packed (two coordinates) or as f16 (one), so that the branches join
-                        // without conversions.
-                        auto pk = [](float lo, float hi) {  // two f16 roundings in one packed conversion
-                            half2_t hh;
-                            hh.x = static_cast<_Float16>(keep_f32(lo));
-                            hh.y = static_cast<_Float16>(keep_f32(hi));
-                            uint32_t u = __builtin_bit_cast(uint32_t, hh);
-                            asm volatile("" : "+v"(u));
-                            return u;
-                        };
-                        auto lo16 = [](uint32_t u) { return f16_f32(static_cast<uint16_t>(u)); };
-                        auto hi16 = [](uint32_t u) { return f16_f32(static_cast<uint16_t>(u >> 16)); };
-                        uint32_t yp = 0;
-                        _Float16 yh = 0;
-                        if constexpr (kCpl == 2) yp = pk(y[0], y[1]);
-                        else yh = static_cast<_Float16>(y[0]);
+                        // a group with a new maximum: the full step at every position (ms = 1 where there is none,
+                        // which leaves y as it is), straight-line
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
+                            const bool nm = __builtin_signbit(f[e]);
                             const float ev = __builtin_fabsf(f[e]);
-                            const bool nm = __builtin_amdgcn_readfirstlane(f32_bits(f[e]) >> 31) != 0u;
-                            // the words of this position's V values; the new-maximum branch takes opaque copies of
-                            // them and of the state, so that the compiler does not convert them ahead of the branch
-                            // (the short step reads the f16 halves as operands of v_fma_mix_f32)
-                            uint32_t wv[kCpl];
+                            const float ms = nm ? ev : 1.0f, vs = nm ? 1.0f : ev;
+#pragma unroll
+                            for (uint32_t m = 0; m < kCpl; ++m) y[m] = y[m] * ms;
+                            r16_all(y);
 #pragma unroll
                             for (uint32_t m = 0; m < kCpl; ++m) {
-                                const uint32_t ww[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
-                                wv[m] = ww[e >> 1];
+                                const uint32_t wv[4] = {w[m].x, w[m].y, w[m].z, w[m].w};
+                                const float v = f16_f32(static_cast<uint16_t>(wv[e >> 1] >> ((e & 1) * 16)));
+                                y[m] = __builtin_fmaf(v, vs, y[m]);
                             }
-                            const uint32_t sh = (e & 1) * 16;
-                            if (__builtin_expect(nm, 0)) {
-                                uint32_t wq[kCpl];
-#pragma unroll
-                                for (uint32_t m = 0; m < kCpl; ++m) {
-                                    wq[m] = wv[m];
-                                    asm volatile("" : "+v"(wq[m]));
-                                }
-                                if constexpr (kCpl == 2) {
-                                    uint32_t yq = yp;
-                                    asm volatile("" : "+v"(yq));
-                                    yq = pk(lo16(yq) * ev, hi16(yq) * ev);
-                                    yp = pk(__builtin_fmaf(f16_f32(static_cast<uint16_t>(wq[0] >> sh)), 1.0f, lo16(yq)),
-                                            __builtin_fmaf(f16_f32(static_cast<uint16_t>(wq[1] >> sh)), 1.0f, hi16(yq)));
-                                } else {
-                                    _Float16 yq = yh;
-                                    asm volatile("" : "+v"(yq));
-                                    yq = static_cast<_Float16>(keep_f32(static_cast<float>(yq) * ev));
-                                    yh = static_cast<_Float16>(keep_f32(
-                                        __builtin_fmaf(f16_f32(static_cast<uint16_t>(wq[0] >> sh)), 1.0f, static_cast<float>(yq))));
-                                }
-                            } else {
-                                if constexpr (kCpl == 2) {
-                                    yp = pk(__builtin_fmaf(f16_f32(static_cast<uint16_t>(wv[0] >> sh)), f[e], lo16(yp)),
-                                            __builtin_fmaf(f16_f32(static_cast<uint16_t>(wv[1] >> sh)), f[e], hi16(yp)));
-                                } else {
-                                    yh = static_cast<_Float16>(keep_f32(
-                                        __builtin_fmaf(f16_f32(static_cast<uint16_t>(wv[0] >> sh)), f[e], static_cast<float>(yh))));
-                                }
-                            }
-                            ssum = __builtin_fmaf(ssum, nm ? ev : 1.0f, nm ? 1.0f : ev);
+                            r16_all(y);
+                            ssum = __builtin_fmaf(ssum, ms, vs);
                         }
-                        if constexpr (kCpl == 2) {
-                            y[0] = lo16(yp);
-                            y[1] = hi16(yp);
-                        } else {
-                            y[0] = static_cast<float>(yh);
-                        }
-                    } else {  // the chunk's edge (positions outside it skipped)
+                    } else {  // the chunk starts inside this group (positions before it skipped)
                         const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(8u, en - p0);
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
@@ -1710,13 +1678,16 @@ __device__ __forceinline__ float vhalf(const u32x4 (&w)[4], int e) {
 }
 
 // The FP16 accumulator of one coordinate (one wave, a coordinate per lane): y = f16(y * ms), y = f16(fma(v, vs, y)) per
-// position, a block per step with the V tiles kChainBlocks blocks ahead in `ring` (already requested for b_first ..);
-// a whole block without a new maximum takes y = f16(fma(v, vs, y)) alone. With a self value, the position `self` (not
-// yet visible in the cache to every workgroup) takes it instead of the cache's.
+// position, a block per step with the V tiles kChainBlocks blocks ahead in `ring` (already requested for b_first ..). A
+// block that starts inside the chunk is summed whole: its positions from en on are padding, V set to -0 here and the
+// factors +0 (the caller writes them), so that a step there adds -0 and leaves y as it is. A block without a new
+// maximum takes y = f16(fma(v, vs, y)) alone; one with new maxima takes the full step at every position (ms = 1 where
+// there is none, which leaves y as it is), straight-line: a branch per position costs more than the longer step. A
+// block that starts before the chunk (a chunk start that is not a multiple of 32) masks its leading positions.
 template <int HD>
 __device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const uint16_t* vt, uint32_t d, uint32_t st,
                                          uint32_t en, uint32_t b_first, uint32_t b_end, uint32_t t_last, const float* fac,
-                                         const uint32_t* bflag, uint32_t self, uint16_t vself) {
+                                         const uint32_t* bflag) {
     float y = 0.0f;
     float4 nf[8];
     uint32_t nflag;
@@ -1746,38 +1717,35 @@ __device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const u
                 const uint32_t flag = __builtin_amdgcn_readfirstlane(nflag);
                 load_fac(min(b + 1u, b_end - 1u));
                 const uint32_t p0 = 32u * b;
-                if (self - p0 < 32u) {  // the position itself lies in this block
-                    const uint32_t e = self - p0, ti = e >> 3, q = (e & 7u) >> 1, sh = (e & 1u) * 16u;
-                    const uint32_t keep = ~(0xffffu << sh), ins = static_cast<uint32_t>(vself) << sh;
+                if (p0 >= st) {
+                    if (p0 + 32u > en) {  // the chunk's last block: V of the positions from en on set to -0
+                        const uint32_t n = en - p0;
 #pragma unroll
-                    for (uint32_t i = 0; i < 4; ++i) {
-                        w[i].x = ti == i && q == 0 ? (w[i].x & keep) | ins : w[i].x;
-                        w[i].y = ti == i && q == 1 ? (w[i].y & keep) | ins : w[i].y;
-                        w[i].z = ti == i && q == 2 ? (w[i].z & keep) | ins : w[i].z;
-                        w[i].w = ti == i && q == 3 ? (w[i].w & keep) | ins : w[i].w;
-                    }
-                }
-                if (p0 >= st && p0 + 32u <= en && flag == 0u) {
+                        for (uint32_t i = 0; i < 4; ++i) {
+                            uint32_t ww[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
 #pragma unroll
-                    for (int e = 0; e < 32; ++e) y = r16(__builtin_fmaf(vhalf(w, e), f[e], y));
-                } else if (p0 >= st && p0 + 32u <= en) {
-                    // A block with a new maximum: a position without one has ms = 1, where y * ms = y and its f16
-                    // rounding leave y unchanged, so only the new maxima (bits of the block's mask, a scalar branch
-                    // each) take the multiply; the others take the short step. y is carried as f16 (it holds an f16
-                    // value), so that the branches join without a conversion.
-                    _Float16 yh = static_cast<_Float16>(y);
-#pragma unroll
-                    for (int e = 0; e < 32; ++e) {
-                        if (__builtin_expect((flag >> e) & 1u, 0u)) {
-                            yh = static_cast<_Float16>(keep_f32(static_cast<float>(yh) * __builtin_fabsf(f[e])));
-                            yh = static_cast<_Float16>(keep_f32(__builtin_fmaf(vhalf(w, e), 1.0f, static_cast<float>(yh))));
-                        } else {
-                            yh = static_cast<_Float16>(keep_f32(__builtin_fmaf(vhalf(w, e), f[e], static_cast<float>(yh))));
+                            for (uint32_t q = 0; q < 4; ++q) {
+                                const uint32_t e = 8u * i + 2u * q;
+                                const uint32_t keep = (e < n ? 0xffffu : 0u) | (e + 1u < n ? 0xffff0000u : 0u);
+                                ww[q] = (ww[q] & keep) | (0x80008000u & ~keep);
+                            }
+                            w[i] = u32x4{ww[0], ww[1], ww[2], ww[3]};
                         }
                     }
-                    y = static_cast<float>(yh);
-                } else {  // the chunk's edge: positions outside [st, en) keep y
-                    const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(32u, en - p0);
+                    if (flag == 0u) {
+#pragma unroll
+                        for (int e = 0; e < 32; ++e) y = r16(__builtin_fmaf(vhalf(w, e), f[e], y));
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 32; ++e) {
+                            const bool nm = __builtin_signbit(f[e]);
+                            const float ev = __builtin_fabsf(f[e]);
+                            const float t = r16(y * (nm ? ev : 1.0f));
+                            y = r16(__builtin_fmaf(vhalf(w, e), nm ? 1.0f : ev, t));
+                        }
+                    }
+                } else {  // the chunk starts inside this block: positions outside [st, en) keep y
+                    const uint32_t e0 = st - p0, e1 = min(32u, en - p0);
 #pragma unroll
                     for (int e = 0; e < 32; ++e) {
                         const bool in = static_cast<uint32_t>(e) >= e0 && static_cast<uint32_t>(e) < e1;
@@ -1798,7 +1766,8 @@ __device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const u
     return y;
 }
 
-// The chunk's sum s = fma(s, ms, vs) over its positions in order (one wave, the same value in every lane).
+// The chunk's sum s = fma(s, ms, vs) over its positions in order (one wave, the same value in every lane); the padding
+// after en has factors +0, which leave s as it is (s >= +0).
 __device__ __forceinline__ float chain_sum(uint32_t st, uint32_t en, uint32_t b_first, uint32_t b_end, const float* fac,
                                            const uint32_t* bflag) {
     float ssum = 0.0f;
@@ -1815,10 +1784,10 @@ __device__ __forceinline__ float chain_sum(uint32_t st, uint32_t en, uint32_t b_
         }
         const uint32_t flag = __builtin_amdgcn_readfirstlane(bflag[b - b_first]);
         const uint32_t p0 = 32u * b;
-        if (p0 >= st && p0 + 32u <= en && flag == 0u) {
+        if (p0 >= st && flag == 0u) {
 #pragma unroll
             for (int e = 0; e < 32; ++e) ssum = ssum + f[e];
-        } else if (p0 >= st && p0 + 32u <= en) {  // a whole block with a new maximum: one dependent operation each
+        } else if (p0 >= st) {
 #pragma unroll
             for (int e = 0; e < 32; ++e) {
                 const bool nm = __builtin_signbit(f[e]);
@@ -1826,7 +1795,7 @@ __device__ __forceinline__ float chain_sum(uint32_t st, uint32_t en, uint32_t b_
                 ssum = __builtin_fmaf(ssum, nm ? ev : 1.0f, nm ? 1.0f : ev);
             }
         } else {
-            const uint32_t e0 = p0 < st ? st - p0 : 0u, e1 = min(32u, en - p0);
+            const uint32_t e0 = st - p0, e1 = min(32u, en - p0);
 #pragma unroll
             for (int e = 0; e < 32; ++e) {
                 const bool in = static_cast<uint32_t>(e) >= e0 && static_cast<uint32_t>(e) < e1;
@@ -1888,10 +1857,11 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
     }
     float cmax = -__builtin_inff();
     if (any) cmax = chunk_factors<256>(a.scores + static_cast<size_t>(h) * a.max_ctx + st, st, en, b_first, fac, bflag, wtot, etab);
+    if (any && tid < 32u && en + tid < 32u * b_end) fac[en + tid - 32u * b_first] = 0.0f;  // the last block's padding
     __syncthreads();
     float y = 0.0f;
     if (any && wave == 0) {
-        y = chain_y<HD>(ring, vt, d, st, en, b_first, b_end, t_last, fac, bflag, ~0u, 0);
+        y = chain_y<HD>(ring, vt, d, st, en, b_first, b_end, t_last, fac, bflag);
     } else if (wave == 1) {
         const float ssum = any ? chain_sum(st, en, b_first, b_end, fac, bflag) : 0.0f;
         if (lane == 0) s_sum = ssum;
