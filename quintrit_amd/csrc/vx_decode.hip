@@ -1660,14 +1660,27 @@ __device__ __forceinline__ float chunk_factors(const float* scores, uint32_t st,
     return cmax;
 }
 
-// The V tiles of 8 positions (16 bytes per coordinate) of block b for coordinate d, up to tile t_last (the last one
-// with a position of the chunk: every read stays inside the cache).
+// The V tiles of 8 positions (16 bytes per coordinate) of a KV head for coordinate d, up to tile t_last (the last one
+// with a position of the chunk: every read stays inside the cache), as a buffer: the lane's offset is fixed, a tile's
+// is a scalar, so a tile costs one load and no address arithmetic.
+struct VTiles {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t voff;  // the lane's coordinate: d * 16 bytes
+};
 template <int HD>
-__device__ __forceinline__ void load_vblock(const uint16_t* vt, uint32_t b, uint32_t d, uint32_t t_last, u32x4 (&r)[4]) {
+__device__ __forceinline__ VTiles vtiles(const uint16_t* vt, uint32_t d, uint32_t t_last) {
+    VTiles v;
+    v.rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vt), 0, (t_last + 1u) * HD * 16u, kBufferRsrcWord3);
+    v.voff = d * 16u;
+    return v;
+}
+// The tiles of block b (4 b .. 4 b + 3, clamped at t_last).
+template <int HD>
+__device__ __forceinline__ void load_vblock(const VTiles& v, uint32_t b, uint32_t t_last, u32x4 (&r)[4]) {
 #pragma unroll
     for (uint32_t i = 0; i < 4; ++i) {
         const uint32_t t = min(4u * b + i, t_last);
-        r[i] = *reinterpret_cast<const u32x4*>(vt + (static_cast<size_t>(t) * HD + d) * 8u);
+        r[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(v.rsrc, v.voff, t * HD * 16u, 0));
     }
 }
 
@@ -1685,23 +1698,27 @@ __device__ __forceinline__ float vhalf(const u32x4 (&w)[4], int e) {
 // there is none, which leaves y as it is), straight-line: a branch per position costs more than the longer step. A
 // block that starts before the chunk (a chunk start that is not a multiple of 32) masks its leading positions.
 template <int HD>
-__device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const uint16_t* vt, uint32_t d, uint32_t st,
-                                         uint32_t en, uint32_t b_first, uint32_t b_end, uint32_t t_last, const float* fac,
+__device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const VTiles& vtl, uint32_t st, uint32_t en,
+                                         uint32_t b_first, uint32_t b_end, uint32_t t_last, const float* fac,
                                          const uint32_t* bflag) {
     float y = 0.0f;
-    float4 nf[8];
-    uint32_t nflag;
-    auto load_fac = [&](uint32_t b) {
+    // The factors and mask of a block, read from LDS one block ahead into the other of two slots (slot k & 1 for ring
+    // slot k: kChainBlocks is even, so the pattern repeats on every pass), every read unconditional: no copies.
+    static_assert(kChainBlocks % 2 == 0, "two factor slots alternate over the ring");
+    float4 fq[2][8];
+    uint32_t fl[2];
+    auto load_fac = [&](uint32_t b, float4 (&q)[8], uint32_t& m) {
         const float* fb = fac + 32u * (b - b_first);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) nf[i] = *reinterpret_cast<const float4*>(fb + 4 * i);
-        nflag = bflag[b - b_first];
+        for (int i = 0; i < 8; ++i) q[i] = *reinterpret_cast<const float4*>(fb + 4 * i);
+        m = bflag[b - b_first];
     };
-    load_fac(b_first);
+    load_fac(b_first, fq[0], fl[0]);
     for (uint32_t b0 = b_first; b0 < b_end; b0 += kChainBlocks) {
         static_for<kChainBlocks>([&](auto kc) {  // the ring's slot as a constant: no rotation of its registers
             constexpr uint32_t k = decltype(kc)::value;
             const uint32_t b = b0 + k;
+            load_fac(min(b + 1u, b_end - 1u), fq[(k + 1u) & 1u], fl[(k + 1u) & 1u]);
             if (b < b_end) {  // wave-uniform
                 // the block's V tiles, used in place; the slot is refilled (kChainBlocks blocks ahead) once they are
                 // consumed, so that the refill lands in the same registers
@@ -1709,13 +1726,12 @@ __device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const u
                 float f[32];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    f[4 * i] = nf[i].x;
-                    f[4 * i + 1] = nf[i].y;
-                    f[4 * i + 2] = nf[i].z;
-                    f[4 * i + 3] = nf[i].w;
+                    f[4 * i] = fq[k & 1u][i].x;
+                    f[4 * i + 1] = fq[k & 1u][i].y;
+                    f[4 * i + 2] = fq[k & 1u][i].z;
+                    f[4 * i + 3] = fq[k & 1u][i].w;
                 }
-                const uint32_t flag = __builtin_amdgcn_readfirstlane(nflag);
-                load_fac(min(b + 1u, b_end - 1u));
+                const uint32_t flag = __builtin_amdgcn_readfirstlane(fl[k & 1u]);
                 const uint32_t p0 = 32u * b;
                 if (p0 >= st) {
                     if (p0 + 32u > en) {  // the chunk's last block: V of the positions from en on set to -0
@@ -1760,7 +1776,7 @@ __device__ __forceinline__ float chain_y(u32x4 (&ring)[kChainBlocks][4], const u
             }
             // every slot is refilled, used or not (the tile index stays inside the cache), so that the number of loads
             // issued after a slot's refill, and with it the wait for the slot, is the same on every path
-            load_vblock<HD>(vt, b + kChainBlocks, d, t_last, ring[k]);
+            load_vblock<HD>(vtl, b + kChainBlocks, t_last, ring[k]);
         });
     }
     return y;
@@ -1850,10 +1866,11 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
     const uint32_t b_first = st / 32u, b_end = any ? (en + 31u) / 32u : b_first + 1u;
     const uint32_t t_last = any ? (en - 1u) / 8u : st / 8u;
     fill_etab(etab);
+    const VTiles vtl = vtiles<HD>(vt, d, t_last);
     u32x4 ring[kChainBlocks][4];
     if (wave == 0 && any) {
 #pragma unroll
-        for (uint32_t k = 0; k < kChainBlocks; ++k) load_vblock<HD>(vt, b_first + k, d, t_last, ring[k]);
+        for (uint32_t k = 0; k < kChainBlocks; ++k) load_vblock<HD>(vtl, b_first + k, t_last, ring[k]);
     }
     float cmax = -__builtin_inff();
     if (any) cmax = chunk_factors<256>(a.scores + static_cast<size_t>(h) * a.max_ctx + st, st, en, b_first, fac, bflag, wtot, etab);
@@ -1861,7 +1878,7 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
     __syncthreads();
     float y = 0.0f;
     if (any && wave == 0) {
-        y = chain_y<HD>(ring, vt, d, st, en, b_first, b_end, t_last, fac, bflag);
+        y = chain_y<HD>(ring, vtl, st, en, b_first, b_end, t_last, fac, bflag);
     } else if (wave == 1) {
         const float ssum = any ? chain_sum(st, en, b_first, b_end, fac, bflag) : 0.0f;
         if (lane == 0) s_sum = ssum;
