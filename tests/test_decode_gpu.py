@@ -215,6 +215,49 @@ def test_long_context_logits_bit_exact(torch_dev, oracle, head_dim):
         model.close()
 
 
+@pytest.mark.parametrize("head_dim", [256, 128])
+def test_chunks_not_aligned_to_blocks(torch_dev, oracle, head_dim):
+    """max_ctx 1000: from 769 positions on the padded KV length is 1000, so the four chunks of attend_head
+    (attention.rs:483-542) hold 250 positions and start at 250, 500 and 750, inside a 32-position block of the decode
+    chains and inside an 8-position group of the prefill chains (every other test's contexts give chunks of a multiple
+    of 32). The GPU prefills positions 0..989, the oracle takes its cache and steps 990..999 beside the GPU with
+    bit-identical logits, and a second GPU decoder stepped through every position holds the same cache (sampled) and
+    the same final logits."""
+    n_heads = 512 // head_dim
+    cfg = oracle.ModelConfig(2, 512, n_heads, 2, head_dim, 384, 1000, 1000, 1e-5, 10000.0)
+    model = oracle.Model(cfg, 41)
+    pre = load_decoder(oracle, model)
+    ref = load_decoder(oracle, model)
+    try:
+        tokens = np.random.default_rng(head_dim + 1).integers(0, cfg.vocab, 1000)
+        print(f"[unaligned chunks] head_dim {head_dim}: prefill of 990", flush=True)
+        pre.prefill(tokens[:990])
+        for layer in range(cfg.n_layers):
+            for pos in range(990):
+                for h in range(cfg.n_kv_heads):
+                    model.set_kv(layer, pos, h, *pre.kv(layer, pos, h))
+        for pos in range(990, 1000):
+            o_next, o_logits = model.forward(int(tokens[pos]), pos)
+            got, got_next = pre.step(int(tokens[pos]), pos)
+            assert_same_bits(got, o_logits, f"logits at pos {pos}")
+            assert got_next == o_next, f"pos {pos}"
+        print(f"[unaligned chunks] head_dim {head_dim}: 1000 steps", flush=True)
+        for pos in range(1000):
+            want, want_next = ref.step(int(tokens[pos]), pos, want_logits=pos == 999)
+        assert_same_bits(got, want, "steps to 999 vs prefill")
+        assert got_next == want_next
+        for layer in range(cfg.n_layers):
+            for pos in list(range(0, 1000, 37)) + [249, 250, 251, 499, 500, 749, 750, 989]:
+                for h in range(cfg.n_kv_heads):
+                    ka, va = pre.kv(layer, pos, h)
+                    kb, vb = ref.kv(layer, pos, h)
+                    assert np.array_equal(ka, kb) and np.array_equal(va, vb), f"KV at layer {layer}, pos {pos}"
+    finally:
+        pre.close()
+        ref.close()
+        model.close()
+
+
 def test_falcon3_generate_tokens_identical(torch_dev, oracle):
     """The Falcon3 variant's greedy loop in one graph per step against the oracle's loop, twice on one decoder."""
     model = oracle.Model(variant_cfg(oracle, "falcon3"), 29)
