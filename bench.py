@@ -266,8 +266,9 @@ def lone_latency(torch, L, lib, reps: int = 200):
     """The drop-in path per call at the Falcon3-10B projection shapes: vx_gemv_f32_dev on device buffers (int8
     activations staged by the call, one stream), as a back-to-back stream of `reps` calls (device time per call, HIP
     events) and as single calls each followed by a stream synchronisation (wall-clock median: the latency a lone
-    caller sees); and vx_layer_forward, the TernaryGemvLayer::forward stand-in on host buffers (two synchronous PCIe
-    copies around the same call, wall-clock median)."""
+    caller sees); and vx_layer_forward, the TernaryGemvLayer::forward stand-in on host buffers (the same call through a
+    pinned buffer that the kernels read and write, the caller waiting on the GEMV's completion flag; wall-clock
+    median)."""
     import numpy as np
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0x10E)
@@ -285,19 +286,20 @@ def lone_latency(torch, L, lib, reps: int = 200):
                                                    ctypes.c_void_p(y.data_ptr()), rows, stream))
         ms, _ = time_fn(torch, call, reps, 20)
         lat = []
-        for _ in range(50):
+        for i in range(220):
             t0 = time.perf_counter()
             call()
             torch.cuda.synchronize()
-            lat.append(time.perf_counter() - t0)
+            if i >= 20:
+                lat.append(time.perf_counter() - t0)
         qh = q.cpu().numpy()
         yh = np.empty(rows, np.float32)
         fwd = []
-        for i in range(52):
+        for i in range(220):
             t0 = time.perf_counter()
             lib.check(L.vx_layer_forward(h, qh.ctypes.data_as(ctypes.c_void_p), cols, ctypes.c_float(sc),
                                          yh.ctypes.data_as(ctypes.c_void_p), rows))
-            if i >= 2:
+            if i >= 20:
                 fwd.append(time.perf_counter() - t0)
         if not np.array_equal(yh, y.cpu().numpy()):
             raise RuntimeError(f"{name}: vx_layer_forward and vx_gemv_f32_dev differ")

@@ -104,6 +104,7 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     m->d_part = nullptr;
     m->d_accum = nullptr;
     m->d_tickets = nullptr;
+    m->d_done = nullptr;
     m->d_dsum = nullptr;
     m->d_staged = nullptr;
     m->d_io = nullptr;
@@ -118,10 +119,11 @@ static int alloc_matrix(size_t rows, size_t cols, float weight_scale, vx_matrix*
     if (e == hipSuccess && m->kslices > 1) e = hipMalloc(&m->d_part, static_cast<size_t>(m->kslices) * m->g.padded_rows * 4);
     // the atomic slice sums and tickets of the lone calls (the table GEMV splits K more finely than the digit GEMV,
     // so every matrix has them)
-    const size_t accum_bytes = (m->g.padded_rows + m->g.n_groups) * 4;
+    const size_t accum_bytes = (m->g.padded_rows + m->g.n_groups + 1) * 4;
     if (e == hipSuccess) e = hipMalloc(&m->d_accum, accum_bytes);
     if (e == hipSuccess) e = hipMemset(m->d_accum, 0, accum_bytes);
     if (e == hipSuccess) m->d_tickets = reinterpret_cast<uint32_t*>(m->d_accum + m->g.padded_rows);
+    if (e == hipSuccess) m->d_done = m->d_tickets + m->g.n_groups;
     if (e == hipSuccess) e = hipMalloc(&m->d_dsum, m->g.padded_rows * 4);
     if (e == hipSuccess) e = hipMalloc(&m->d_staged, staged_bytes(cols));
     if (e == hipSuccess) e = hipMalloc(&m->d_io, io_bytes);
@@ -201,12 +203,18 @@ static int check_io(const vx_matrix_t* m, const void* acts, size_t acts_len, con
     return VX_OK;
 }
 
-// A lone GEMV of matrix m on staged activations: one launch (a split matrix's K slices add their sums atomically and
-// the last of each tile group writes the outputs). Calls on one matrix share its sums and tickets, so they must not
-// overlap.
+// A lone GEMV of matrix m on staged activations, or (raw) on int8 activations that every workgroup stages for its own
+// K slice: one launch (a split matrix's K slices add their sums atomically and the last of each tile group writes the
+// outputs). Calls on one matrix share its sums and tickets, so they must not overlap. With `flag`, the launch's last
+// workgroup stores `seq` there once every output is written.
 static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint32_t out_kind, float post,
-                      hipStream_t s) {
+                      hipStream_t s, uint32_t* flag = nullptr, uint32_t seq = 0, const int8_t* raw = nullptr) {
     LaunchArgs a{};
+    a.done = flag != nullptr ? m->d_done : nullptr;
+    a.flag = flag;
+    a.seq = seq;
+    a.acts = raw;
+    a.cols = static_cast<uint32_t>(m->g.cols);
     a.jobs = nullptr;
     a.n_jobs = 1;
     Job& j = a.one;
@@ -223,6 +231,7 @@ static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint
     j.weight_scale = m->weight_scale;
     j.out_kind = out_kind;
     j.item_begin = 0;
+    j.tbr = static_cast<uint32_t>(m->g.tbr);
     a.total_items = job_items(j);
     return launch_gemv(a, j.rows, nullptr, j.kslices > 1 && j.accum == nullptr ? 1u : 0u, m->num_cus, s);
 }
@@ -254,15 +263,14 @@ static int gemv_f32_staged(const vx_matrix* m, const uint8_t* staged, float act_
     return launch_fill_f32(out, m->g.rows, 0.0f, s);
 }
 
+// The raw-activation calls: one launch, each workgroup staging its own K slice.
 static int gemv_f32_dev(vx_matrix* m, const int8_t* acts, float act_scale, float* out, hipStream_t s) {
     if (!(act_scale > 0.0f)) return launch_fill_f32(out, m->g.rows, 0.0f, s);
-    VX_TRY(launch_stage(acts, m->g.cols, m->d_staged, s));
-    return gemv_f32_staged(m, m->d_staged, act_scale, out, s);
+    return run_single(m, nullptr, out, kOutF32Post, m->weight_scale / act_scale, s, nullptr, 0, acts);
 }
 
 static int gemv_i32_dev(vx_matrix* m, const int8_t* acts, int32_t* out, hipStream_t s) {
-    VX_TRY(launch_stage(acts, m->g.cols, m->d_staged, s));
-    return run_single(m, m->d_staged, out, kOutI32, 1.0f, s);
+    return run_single(m, nullptr, out, kOutI32, 1.0f, s, nullptr, 0, acts);
 }
 
 }  // namespace vx
@@ -545,14 +553,22 @@ int vx_layer_forward(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_
         VX_TRY(check_io(matrix, acts, acts_len, out, out_capacity));
         vx_matrix* m = const_cast<vx_matrix*>(matrix);
         std::lock_guard<std::mutex> lock(m->mu);
+        // A scale that is not > 0 makes every output zero (layer.rs:246-253), as the device path's fill does.
+        if (!(act_scale > 0.0f)) {
+            std::memset(out, 0, m->g.rows * sizeof(float));
+            return VX_OK;
+        }
         VX_TRY(set_device_of(m));
-        // The activations go into a pinned host buffer that the staging kernel reads over the bus, and the GEMV writes
-        // its outputs into the same buffer: no copy engine, one synchronisation (two synchronous copies through
-        // pageable memory cost 15-25 us per call at the Falcon3-10B shapes).
+        // The activations go into a pinned host buffer that the GEMV's workgroups read over the bus (each its own K
+        // slice), and the GEMV writes its outputs into the same buffer: one launch, no copy engine (two synchronous
+        // copies through pageable memory cost 15-25 us per call at the Falcon3-10B shapes). The GEMV's last workgroup
+        // then stores the call's number into the buffer's flag word, on which this thread waits instead of a stream
+        // synchronisation (whose completion path costs about 5 us more per call).
         const size_t out_off = round_up(m->g.cols, 256);
+        const size_t flag_off = out_off + round_up(m->g.padded_rows * 4, 256);
         if (m->h_io == nullptr) {
             void* h = nullptr;
-            VX_HIP(hipHostMalloc(&h, out_off + m->g.padded_rows * 4, hipHostMallocDefault));
+            VX_HIP(hipHostMalloc(&h, flag_off + 256, hipHostMallocDefault));
             void* hd = nullptr;
             hipError_t e = hipHostGetDevicePointer(&hd, h, 0);
             hipStream_t st = nullptr;
@@ -564,10 +580,27 @@ int vx_layer_forward(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_
             m->h_io = static_cast<int8_t*>(h);
             m->h_io_dev = static_cast<int8_t*>(hd);
             m->io_stream = st;
+            m->io_seq = 0;
+            __atomic_store_n(reinterpret_cast<uint32_t*>(m->h_io + flag_off), 0u, __ATOMIC_RELEASE);
         }
+        uint32_t* flag = reinterpret_cast<uint32_t*>(m->h_io + flag_off);
+        const uint32_t seq = m->io_seq + 1u == 0u ? 1u : m->io_seq + 1u;  // never 0, the buffer's initial value
+        m->io_seq = seq;
         std::memcpy(m->h_io, acts, m->g.cols);
-        VX_TRY(gemv_f32_dev(m, m->h_io_dev, act_scale, reinterpret_cast<float*>(m->h_io_dev + out_off), m->io_stream));
-        VX_HIP(hipStreamSynchronize(m->io_stream));
+        VX_TRY(run_single(m, nullptr, m->h_io_dev + out_off, kOutF32Post, m->weight_scale / act_scale, m->io_stream,
+                          reinterpret_cast<uint32_t*>(m->h_io_dev + flag_off), seq, m->h_io_dev));
+        // Wait for the flag; every 65536 reads (tens of microseconds, longer than a call), ask the stream whether it
+        // has ended (an error, or an end without the flag, is reported instead of waiting on).
+        for (uint32_t i = 1;; ++i) {
+            if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == seq) break;
+            if ((i & 0xffffu) == 0u) {
+                const hipError_t q = hipStreamQuery(m->io_stream);
+                if (q == hipErrorNotReady) continue;
+                if (__atomic_load_n(flag, __ATOMIC_ACQUIRE) == seq) break;
+                if (q != hipSuccess) VX_FAIL(VX_ERR_DEVICE, "vx_layer_forward's GEMV failed: %s", hipGetErrorString(q));
+                VX_FAIL(VX_ERR_INTERNAL, "vx_layer_forward's GEMV ended without storing its completion flag");
+            }
+        }
         std::memcpy(out, m->h_io + out_off, m->g.rows * sizeof(float));
         return VX_OK;
     });

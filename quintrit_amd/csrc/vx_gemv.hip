@@ -249,14 +249,34 @@ __device__ __forceinline__ void flush_held(const char* lds, const Held* held, ui
     }
 }
 
+// The staged entry of device byte-column c of a row of `cols` activations (stage_body's entry, the activations read
+// directly; tbr the tile row bytes, full the byte-columns of whole 160-column blocks), and their sum added to *sum.
+__device__ __forceinline__ uint2 raw_entry(const int8_t* __restrict__ acts, uint32_t cols, uint32_t tbr, uint32_t full,
+                                           uint32_t c, int* sum) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (uint32_t p = 0; p < 5; ++p) {
+        const uint32_t idx = c < full ? (c / 32u) * 160u + p * 32u + (c % 32u) : (cols / 160u) * 160u + 5u * (c - full) + p;
+        const int x = c < tbr && idx < cols ? acts[idx] : 0;
+        lo |= ((static_cast<uint32_t>(x) & 15u) ^ 8u) << (4 * p);
+        hi |= (static_cast<uint32_t>(x >> 4) & 15u) << (4 * p);
+        *sum += x;
+    }
+    return make_uint2(lo, hi);
+}
+
 // Two workgroups per CU (64 KiB table and held results + 11 KiB activations each), 8 waves per SIMD: at most 64 VGPRs.
-// MANY: the jobs are a device array (a plan); otherwise the one job travels in the kernel arguments.
-template <bool MANY>
+// MANY: the jobs are a device array (a plan); otherwise the one job travels in the kernel arguments. RAW (a lone GEMV,
+// args.acts): each item stages its K slice from the raw activations and subtracts the slice's activation sum from its
+// sums (so the outputs need no whole-vector sum: sum t x = 16 hi + lo + 8 sum d - sum x, slice by slice).
+template <bool MANY, bool RAW>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 8))) void gemv_kernel(LaunchArgs args) {
+    static_assert(!(MANY && RAW), "raw activations are a lone GEMV's");
     __shared__ uint32_t tab[256 * 64];  // row B: 32 copies of entry B, then 128 bytes of held results
     __shared__ uint4 acts[2][(kMaxSliceChunks + kGroup) * 8];
     __shared__ Held held[kSlots];
     __shared__ uint32_t last_slice;
+    __shared__ int xsum[2][kWaves];  // RAW: the slice's activation sums per wave
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
@@ -300,9 +320,19 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
             }
         }
         // Stage this slice's activations (zero past nq, so the clamped tail loads add nothing).
-        const uint4* src = reinterpret_cast<const uint4*>(jb.staged + kStageHeader) + static_cast<size_t>(q0) * 8u;
         uint4* ab = acts[buf];
-        for (uint32_t i = tid; i < nqp * 8u; i += kWaves * 64u) ab[i] = i < nq * 8u ? src[i] : make_uint4(0, 0, 0, 0);
+        if constexpr (RAW) {
+            uint2* ae = reinterpret_cast<uint2*>(ab);
+            const uint32_t full = args.cols / 160u * 32u;
+            int xs = 0;
+            for (uint32_t i = tid; i < nqp * 16u; i += kWaves * 64u)
+                ae[i] = i < nq * 16u ? raw_entry(args.acts, args.cols, jb.tbr, full, q0 * 16u + i, &xs) : make_uint2(0, 0);
+            for (int off = 32; off > 0; off >>= 1) xs += __shfl_xor(xs, off);
+            if (lane == 0) xsum[buf][wave] = xs;
+        } else {
+            const uint4* src = reinterpret_cast<const uint4*>(jb.staged + kStageHeader) + static_cast<size_t>(q0) * 8u;
+            for (uint32_t i = tid; i < nqp * 8u; i += kWaves * 64u) ab[i] = i < nq * 8u ? src[i] : make_uint4(0, 0, 0, 0);
+        }
         // A lone GEMV's split item adds its sums atomically; the last slice of the tile group writes the outputs.
         const bool fold = !MANY && jb.kslices > 1 && jb.accum != nullptr;
         const uint32_t slot = done % kSlots;
@@ -352,13 +382,17 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
                     dot4_bcast<12>(acc_lo, acc_hi, e.x, e.y, t[12], t[13], t[14], t[15]);
                 }
             }
-            const int v = acc_lo + 16 * acc_hi;
+            int v = acc_lo + 16 * acc_hi;
+            if constexpr (RAW) {
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) v -= xsum[buf][w];
+            }
             const uint32_t r = wave * kTileRows + lane;  // row within the tile group
             const uint32_t row = grp * kTileGroup * kTileRows + r;
             if (fold) atomicAdd(jb.accum + row, v);
             uint32_t word = static_cast<uint32_t>(v);
             if (jb.kslices == 1 && row < jb.rows) {
-                const int acc = row_result(jb, row, v);
+                const int acc = RAW ? v + 8 * jb.dsum[row] : row_result(jb, row, v);
                 if (jb.out_kind == kOutI32) {
                     word = static_cast<uint32_t>(acc);
                 } else {
@@ -388,7 +422,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
                 if (row < jb.rows) {
                     bool zero;
                     const float post = job_post(jb, &zero);
-                    store_out(jb, row, row_result(jb, row, total), post, zero);
+                    store_out(jb, row, RAW ? total + 8 * jb.dsum[row] : row_result(jb, row, total), post, zero);
                 }
             }
             if (tid == 0) atomicExch(jb.tickets + grp, 0u);
@@ -396,6 +430,18 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
     }
     __syncthreads();
     flush_held(tabb, held, done, pending, wave, lane);
+    if constexpr (!MANY) {
+        if (args.flag != nullptr) {
+            // Every output this workgroup wrote has been performed before its ticket (the hand-off of take_ticket); the
+            // last ticket's holder clears the counter and publishes the call's sequence number to the host.
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            if (tid == 0 && take_ticket(args.done, gridDim.x - 1u)) {
+                atomicExch(args.done, 0u);
+                __hip_atomic_store(args.flag, args.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+    }
 }
 
 // Adds the K-slice partial sums of the split jobs and applies their epilogue. Block = 64 rows x 4 waves; wave w adds
@@ -466,9 +512,14 @@ int launch_stage(const int8_t* acts, size_t cols, uint8_t* staged, hipStream_t s
 int launch_gemv(const LaunchArgs& a, uint32_t max_rows, const uint32_t* split, uint32_t n_split, int num_cus,
                 hipStream_t stream) {
     if (a.total_items == 0) return VX_OK;
+    if (a.flag != nullptr && (a.jobs != nullptr || n_split != 0))
+        VX_FAIL(VX_ERR_INTERNAL, "a completion flag on a launch whose outputs are not all written by gemv_kernel");
+    if (a.acts != nullptr && (a.jobs != nullptr || n_split != 0 || (a.one.kslices > 1 && a.one.accum == nullptr)))
+        VX_FAIL(VX_ERR_INTERNAL, "raw activations on a launch that is not a lone GEMV with atomic slice sums");
     const uint32_t grid = std::min<uint32_t>(a.total_items, 2u * static_cast<uint32_t>(num_cus));
-    if (a.jobs) hipLaunchKernelGGL(gemv_kernel<true>, dim3(grid), dim3(kWaves * 64), 0, stream, a);
-    else hipLaunchKernelGGL(gemv_kernel<false>, dim3(grid), dim3(kWaves * 64), 0, stream, a);
+    if (a.jobs) hipLaunchKernelGGL((gemv_kernel<true, false>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
+    else if (a.acts) hipLaunchKernelGGL((gemv_kernel<false, true>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
+    else hipLaunchKernelGGL((gemv_kernel<false, false>), dim3(grid), dim3(kWaves * 64), 0, stream, a);
     VX_HIP(hipGetLastError());
     if (n_split) {
         const dim3 fgrid((max_rows + 63u) / 64u, n_split);

@@ -164,6 +164,16 @@ struct LaunchArgs {
     uint32_t n_jobs;
     uint32_t total_items;  // work items: (tile group, K slice) pairs summed over the jobs
     Job one;
+    // A lone GEMV whose caller waits on host memory (or null): the workgroup that takes the last ticket of `done`
+    // (device memory, zero between launches) after every workgroup's outputs are stored resets it and stores `seq`
+    // into `flag` (pinned host memory) with a system-scope release.
+    uint32_t* done;
+    uint32_t* flag;
+    uint32_t seq;
+    // A lone GEMV on raw int8 activations (or null: the job's staged vector): every workgroup stages its own K slice
+    // from acts[cols] (one.tbr the tile row bytes) and subtracts that slice's activation sum, so no staging kernel runs.
+    const int8_t* acts;
+    uint32_t cols;
 };
 
 constexpr uint32_t kMaxSliceChunks = 40;  // chunks per K slice staged in LDS (5 KiB of activations)
@@ -292,14 +302,16 @@ struct vx_matrix {
     uint32_t kslices, slice_chunks;  // K split of a lone GEMV on this matrix
     uint8_t* d_w;       // weights, device layout (vx_layout)
     int32_t* d_part;    // K-slice partial sums of a lone GEMV
-    int32_t* d_accum;   // a lone GEMV's atomic K-slice sums (padded_rows) and tickets (one per tile group), zero
-    uint32_t* d_tickets;  // between calls
+    int32_t* d_accum;   // a lone GEMV's atomic K-slice sums (padded_rows), tickets (one per tile group) and
+    uint32_t* d_tickets;  // completion counter (d_done), zero between calls
+    uint32_t* d_done;
     int32_t* d_dsum;    // per padded row: digit sum of the device row (the signed low-nibble correction)
     uint8_t* d_staged;  // activation staging of the calls that take raw int8 activations
     int8_t* d_io;       // one-shot host API: cols bytes of activations + padded_rows * 4 bytes of output
     int8_t* h_io;       // vx_layer_forward: pinned host buffer of the same shape, which the kernels read and write
     int8_t* h_io_dev;   //   directly (its device address); made at the first call
     hipStream_t io_stream;  // vx_layer_forward's stream on this matrix (default priority), made at the first call
+    uint32_t io_seq;        // vx_layer_forward's last call number, which its GEMV stores into the buffer's flag word
     const void* owner;  // the decoder that adopted the matrix (it frees it), or null: the caller's
     std::mutex mu;      // serialises the host-pointer API on this handle
 };

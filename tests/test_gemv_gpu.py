@@ -102,6 +102,37 @@ def test_config0_exact_and_epilogue(torch_dev, oracle):
     layer.close()
 
 
+@pytest.mark.parametrize("rows,cols", [(1, 5), (64, 160), (70, 777), (1024, 3072), (3072, 3072), (2100, 23040)])
+def test_layer_forward_calls_in_a_row(torch_dev, oracle, rows, cols):
+    """vx_layer_forward (the caller waits on the GEMV's completion flag in its pinned buffer) over shapes with one K
+    slice and with split slices in one or several tile groups: eight calls in a row with new activations and scales,
+    each equal to the oracle's epilogue bit for bit, interleaved with vx_gemv_f32_dev on device buffers of the same
+    matrix (which shares its slice sums and tickets), and a call with a zero scale between them."""
+    from quintrit_amd import VelurexHipLayer
+    torch = torch_dev
+    print(f"[layer_forward] {rows}x{cols}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols)
+    t = rng.integers(-1, 2, size=(rows, cols), dtype=np.int8)
+    planar = oracle.pack_matrix(t)
+    layer = VelurexHipLayer(planar, rows, cols, 0.05)
+    y = np.empty(rows, np.float32)
+    for call in range(8):
+        a = activations(("random", "max", "min", "alternating")[call % 4], cols, rng)
+        sc = float(rng.uniform(0.1, 3.0))
+        want = exact_gemv(t, a).astype(np.int32)
+        layer.forward(a, sc, y)
+        assert np.array_equal(y.view(np.uint32), oracle.epilogue_f32(want, 0.05, sc).view(np.uint32)), call
+        if call % 3 == 1:
+            yd = torch.empty(rows, dtype=torch.float32, device="cuda")
+            layer.gemv_f32(torch.from_numpy(a).cuda(), sc, yd)
+            torch.cuda.synchronize()
+            assert np.array_equal(yd.cpu().numpy().view(np.uint32), y.view(np.uint32)), call
+        if call == 4:
+            layer.forward(a, 0.0, y)
+            assert np.array_equal(y.view(np.uint32), np.zeros(rows, np.uint32))
+    layer.close()
+
+
 def test_staged_activations_shared_by_matrices(torch_dev, oracle):
     from quintrit_amd import VelurexHipLayer, _lib
     torch = torch_dev
