@@ -637,7 +637,7 @@ constexpr int kDPer = 7;  // chunks of a work item per wave at most (kStChunks /
 // Tiles a workgroup's chunk range of a gated pair touches at most: a range of at most 16 kDPer chunks starting inside a
 // tile of 2 n_chunks chunks, with 2 n_chunks >= 8 kDPer (the host's condition), ends within the third tile.
 constexpr int kRangeSegs = 3;
-constexpr int kRangeEarly = 3;  // chunks per wave of a range issued before the stage input is computed
+constexpr int kRangeEarly = 1;  // chunks per wave of a range issued before the stage input is computed
 
 struct DStageArgs {
     DJob job[kMaxStageJobs];
@@ -807,9 +807,10 @@ __global__ __launch_bounds__(kNT) void dgemv_kernel(DStageArgs a) {
             __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), 0, ia.jb.w_bytes, kBufferRsrcWord3);
         return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kLoadNt));
     };
-    // A range issues its first kRangeEarly chunks per wave now and the others as the first are consumed: all of them
-    // now would hold the input's waves at their loads (the CU's queue of memory instructions is full) until most of
-    // the stage's weights have arrived.
+    // A range issues its first kRangeEarly chunks per wave now and each next one as an earlier one is consumed (then
+    // kRangeEarly chunks ahead): the fewer weight loads there are in flight while the stage input is loaded, the sooner
+    // its loads return (all seven at once held the input's waves at their loads until most of the stage's weights had
+    // arrived; one, two and three measured 2.073, 2.083 and 2.089 ms per Falcon3-10B token).
     u32x4 ba[DPER];
 #pragma unroll
     for (int i = 0; i < DPER; ++i)
