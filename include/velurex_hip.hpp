@@ -5,11 +5,13 @@
 //     velurex_hip::TernaryGemvLayer, with VelurexHipLayer as its GPU implementation (weights resident in HBM); the
 //     kernel kinds of TernaryKernelType (layer.rs:13-68) with the one this library adds, VelurexHip;
 //   - the kernel level of the reference's C++ wrapper (rust/crates/quintrit-c/include/quintrit.hpp:146-191):
-//     version(), check_abi(), layout(), gemv_i32() and gemv_f32() on the planar bytes of quintrit_core::pack.
+//     version(), check_abi(), layout(), gemv_i32() and gemv_f32() on the planar bytes of quintrit_core::pack;
+//   - its GPU model (quintrit::Model::open_gpu, quintrit.hpp:394-430) at the level of token ids: velurex_hip::Decoder,
+//     the greedy token loop of the reference's engine (quintrit-runtime/src/engine.rs:590-686) on one GPU.
 // Conventions of quintrit.hpp (lines 1-57):
 //   - Every failing C call throws velurex_hip::Error, which carries the status code (code(): one of VX_ERR_*, whose
 //     values are QUINTRIT_ERR_*) and the library's message (vx_last_error_message, else vx_status_string).
-//   - The owning class is RAII and move-only; its destructor frees the handle and never throws.
+//   - The owning classes are RAII and move-only; their destructors free the handle and never throw.
 //   - The helpers allocate their outputs (std::vector).
 // forward() requires activations.len() == cols and out.len() == rows, as the trait's implementations assert
 // (layer.rs:124,156,211,259); the Rust trait panics on a mismatch, this header throws Error with VX_ERR_INVALID_ARGUMENT.
@@ -213,11 +215,125 @@ public:
         if (m_ == nullptr) throw Error(VX_ERR_INVALID_HANDLE, "the layer was moved from");
         return m_;
     }
+    /// Gives up the handle (the caller then owns it); the layer is left empty.
+    vx_matrix_t* release() noexcept { return std::exchange(m_, nullptr); }
 
 private:
     vx_matrix_t* m_ = nullptr;
     std::size_t rows_, cols_;
     float weight_scale_;
+};
+
+// -------------------------------------------------------------------------------------------------------------------
+// Decoder (the token loop on the GPU)
+// -------------------------------------------------------------------------------------------------------------------
+
+/// A ternary decoder resident on one GPU (vx_decoder_*): the counterpart of quintrit::Model opened on a GPU
+/// (quintrit.hpp:394-430, Model::open_gpu) at the level of token ids, with the reference's greedy token loop
+/// (quintrit-runtime/src/engine.rs:590-686). Move-only; the destructor frees the decoder and never throws.
+class Decoder {
+public:
+    /// A decoder of the given shape and architecture (ModelConfig, config.rs:155-227) whose weights are set next.
+    explicit Decoder(vx_decoder_config_t config) {
+        config.struct_size = sizeof(config);
+        detail::check(vx_decoder_create(&config, &d_));
+    }
+    /// A GGUF model on GPU `device` (quintrit::Model::open_gpu); `context` bounds the context (0 = default).
+    static Decoder open_gguf(const std::string& path, std::uint32_t device = 0, std::uint32_t context = 0) {
+        vx_gpu_options_t o{};
+        o.struct_size = sizeof(o);
+        o.device_index = device;
+        o.context_length = context;
+        vx_decoder_t* d = nullptr;
+        detail::check(vx_decoder_open_gguf(path.c_str(), &o, &d));
+        return Decoder(d);
+    }
+    ~Decoder() {
+        if (d_ != nullptr) (void)vx_decoder_free(d_);
+    }
+    Decoder(const Decoder&) = delete;
+    Decoder& operator=(const Decoder&) = delete;
+    Decoder(Decoder&& o) noexcept : d_(std::exchange(o.d_, nullptr)) {}
+    Decoder& operator=(Decoder&& o) noexcept {
+        if (this != &o) {
+            if (d_ != nullptr) (void)vx_decoder_free(d_);
+            d_ = std::exchange(o.d_, nullptr);
+        }
+        return *this;
+    }
+
+    /// The configuration (quintrit::Model::info's shape part).
+    vx_decoder_config_t config() const {
+        vx_decoder_config_t c{};
+        c.struct_size = sizeof(c);
+        detail::check(vx_decoder_config(handle(), &c));
+        return c;
+    }
+    /// The weights: a projection from planar bytes, or a matrix handed over (on success the decoder owns it).
+    void set_projection(std::uint32_t layer, std::uint32_t kind, const std::vector<std::uint8_t>& planar, float weight_scale) {
+        detail::check(vx_decoder_set_projection(handle(), layer, kind, planar.data(), planar.size(), weight_scale));
+    }
+    void adopt_projection(std::uint32_t layer, std::uint32_t kind, VelurexHipLayer&& matrix) {
+        detail::check(vx_decoder_adopt_projection(handle(), layer, kind, matrix.handle()));
+        (void)matrix.release();
+    }
+    void set_norm(std::uint32_t layer, std::uint32_t kind, const std::vector<float>& weights) {
+        detail::check(vx_decoder_set_norm(handle(), layer, kind, weights.data(), weights.size()));
+    }
+    void set_embedding_bf16(const std::vector<std::uint16_t>& e) {
+        detail::check(vx_decoder_set_embedding_bf16(handle(), e.data(), e.size()));
+    }
+    void set_embedding_f16(const std::vector<std::uint16_t>& e) {
+        detail::check(vx_decoder_set_embedding_f16(handle(), e.data(), e.size()));
+    }
+    void set_head(const std::vector<std::uint16_t>& h) { detail::check(vx_decoder_set_head(handle(), h.data(), h.size())); }
+
+    /// One token at position `pos` (forward_token); returns the greedy next token, and the logits when asked.
+    std::uint32_t step(std::uint32_t token, std::uint32_t pos, std::vector<float>* logits = nullptr) {
+        std::uint32_t next = 0;
+        if (logits != nullptr) logits->resize(config().vocab);
+        detail::check(vx_decoder_step(handle(), token, pos, logits ? logits->data() : nullptr, logits ? logits->size() : 0,
+                                      &next));
+        return next;
+    }
+    /// The tokens pos0 .. pos0 + n - 1 in batched passes; the last position's greedy token (and logits when asked).
+    std::uint32_t prefill(const std::vector<std::uint32_t>& tokens, std::uint32_t pos0, std::vector<float>* logits = nullptr) {
+        std::uint32_t next = 0;
+        if (logits != nullptr) logits->resize(config().vocab);
+        detail::check(vx_decoder_prefill(handle(), tokens.data(), tokens.size(), pos0, logits ? logits->data() : nullptr,
+                                         logits ? logits->size() : 0, &next));
+        return next;
+    }
+    /// Greedy generation from position 0 (engine.rs:590-686): n_new tokens; `stepwise` feeds the prompt one decode
+    /// step per token, as the reference's loop does, instead of prefill passes (the tokens are the same).
+    std::vector<std::uint32_t> generate(const std::vector<std::uint32_t>& prompt, std::size_t n_new, bool stepwise = false) {
+        std::vector<std::uint32_t> out(n_new);
+        detail::check(stepwise ? vx_decoder_generate_stepwise(handle(), prompt.data(), prompt.size(), n_new, out.data(), out.size())
+                               : vx_decoder_generate(handle(), prompt.data(), prompt.size(), n_new, out.data(), out.size()));
+        return out;
+    }
+    /// The cached f16 key and value of (layer, pos, kv_head) (KVCache::get_key / get_val, kv_cache.rs:142-155).
+    std::pair<std::vector<std::uint16_t>, std::vector<std::uint16_t>> kv(std::uint32_t layer, std::uint32_t pos,
+                                                                        std::uint32_t kv_head) const {
+        const std::size_t hd = config().head_dim;
+        std::vector<std::uint16_t> k(hd), v(hd);
+        detail::check(vx_decoder_kv_get(handle(), layer, pos, kv_head, k.data(), v.data(), hd));
+        return {std::move(k), std::move(v)};
+    }
+    /// Device bytes held (weights, KV cache, work buffers).
+    std::size_t memory_bytes() const {
+        std::size_t n = 0;
+        detail::check(vx_decoder_memory_bytes(handle(), &n));
+        return n;
+    }
+    vx_decoder_t* handle() const {
+        if (d_ == nullptr) throw Error(VX_ERR_INVALID_HANDLE, "the decoder was moved from");
+        return d_;
+    }
+
+private:
+    explicit Decoder(vx_decoder_t* d) : d_(d) {}
+    vx_decoder_t* d_ = nullptr;
 };
 
 }  // namespace velurex_hip

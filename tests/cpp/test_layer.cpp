@@ -1,7 +1,8 @@
 // C++ test of velurex_hip.hpp (the TernaryGemvLayer interface and the kernel-level GEMV over the C ABI), in the manner
 // of the reference's C++ wrapper test (rust/crates/quintrit-c/tests/cpp/test_kernel.cpp): GEMVs against a brute-force
 // product at the shapes of that test and of quintrit-c/tests/ffi_kernel.rs:36-49,195-265, errors as exceptions with
-// their status codes, and the move-only owning class. Exit code 0 means success.
+// their status codes, and the move-only owning classes; the decoder through the wrapper (prefill against steps, greedy
+// generation with and without prefill passes, its errors). Exit code 0 means success.
 //
 //   test_layer          everything (needs a gfx950 device)
 //   test_layer --cpu    only what needs no device: the ABI, the layout, argument errors, the type traits
@@ -194,6 +195,115 @@ void threads_case() {
     CHECK(bad[0] == 0 && bad[1] == 0 && bad[2] == 0 && bad[3] == 0);
 }
 
+// A random decoder of a small BitNet-like (ReLU^2, sub-norms, NEOX RoPE, tied bf16 embedding) or Falcon3-like (SiLU,
+// Normal RoPE, no sub-norms, f16 embedding, untied head) shape: the same weights for every decoder built with one seed.
+velurex_hip::Decoder small_decoder(bool falcon, std::uint64_t seed) {
+    state = seed;
+    vx_decoder_config_t c{};
+    c.n_layers = 2;
+    c.hidden = 256;
+    c.n_heads = 4;
+    c.n_kv_heads = 2;
+    c.head_dim = 64;
+    c.ffn = 512;
+    c.vocab = 1000;
+    c.max_ctx = 640;
+    c.rms_eps = 1e-5f;
+    c.rope_theta = 10000.0f;
+    if (falcon) {
+        c.act = VX_ACT_SILU;
+        c.rope_mode = VX_ROPE_NORMAL;
+        c.no_sub_norm = 1;
+        c.emb_f16 = 1;
+        c.untied = 1;
+    }
+    velurex_hip::Decoder d(c);
+    auto planar = [&](std::size_t rows, std::size_t cols) {
+        std::vector<std::int8_t> t(rows * cols);
+        for (auto& v : t) v = static_cast<std::int8_t>(static_cast<int>(next() % 3) - 1);
+        return pack_planar(t, rows, cols);
+    };
+    const std::size_t q = c.n_heads * c.head_dim, kv = c.n_kv_heads * c.head_dim;
+    const std::size_t shapes[7][2] = {{q, c.hidden}, {kv, c.hidden}, {kv, c.hidden}, {c.hidden, q},
+                                      {c.ffn, c.hidden}, {c.ffn, c.hidden}, {c.hidden, c.ffn}};
+    for (std::uint32_t l = 0; l < c.n_layers; ++l) {
+        for (std::uint32_t k = 0; k < 7; ++k) {
+            const float ws = 0.5f + static_cast<float>(next() % 1000) / 1000.0f;
+            if (k == VX_PROJ_O && l == 1) {  // one projection handed over as a matrix
+                d.adopt_projection(l, k, velurex_hip::VelurexHipLayer(planar(shapes[k][0], shapes[k][1]), shapes[k][0],
+                                                                      shapes[k][1], ws));
+            } else {
+                d.set_projection(l, k, planar(shapes[k][0], shapes[k][1]), ws);
+            }
+        }
+        for (std::uint32_t k : {VX_NORM_ATTN, VX_NORM_ATTN_SUB, VX_NORM_FFN, VX_NORM_FFN_SUB}) {
+            if (falcon && (k == VX_NORM_ATTN_SUB || k == VX_NORM_FFN_SUB)) continue;
+            const std::size_t n = k == VX_NORM_ATTN_SUB ? q : (k == VX_NORM_FFN_SUB ? c.ffn : c.hidden);
+            std::vector<float> w(n);
+            for (auto& v : w) v = 0.8f + static_cast<float>(next() % 400) / 1000.0f;
+            d.set_norm(l, k, w);
+        }
+    }
+    std::vector<float> out_norm(c.hidden);
+    for (auto& v : out_norm) v = 0.8f + static_cast<float>(next() % 400) / 1000.0f;
+    d.set_norm(c.n_layers, VX_NORM_ATTN, out_norm);
+    // 16-bit values of magnitude 2^-5 .. 2^-1 with random signs and mantissas: bf16 (exponent 122..126) or f16 (10..14)
+    auto table = [&](bool f16) {
+        std::vector<std::uint16_t> e(static_cast<std::size_t>(c.vocab) * c.hidden);
+        for (auto& v : e) {
+            const std::uint32_t r = next();
+            v = f16 ? static_cast<std::uint16_t>(((r >> 31) << 15) | ((10u + r % 5u) << 10) | ((r >> 8) & 0x3ffu))
+                    : static_cast<std::uint16_t>(((r >> 31) << 15) | ((122u + r % 5u) << 7) | ((r >> 8) & 0x7fu));
+        }
+        return e;
+    };
+    if (falcon) {
+        d.set_embedding_f16(table(true));
+        d.set_head(table(true));
+    } else {
+        d.set_embedding_bf16(table(false));
+    }
+    return d;
+}
+
+// The decoder through the wrapper: prefill passes and decode steps give the same logits, KV cache and tokens.
+void decoder_case(bool falcon) {
+    std::vector<std::uint32_t> prompt(40);
+    velurex_hip::Decoder a = small_decoder(falcon, 0x5EED0001ULL);
+    velurex_hip::Decoder b = small_decoder(falcon, 0x5EED0001ULL);
+    for (auto& t : prompt) t = next() % 1000;
+    const vx_decoder_config_t c = a.config();
+    CHECK(c.hidden == 256 && c.vocab == 1000 && c.act == (falcon ? VX_ACT_SILU : VX_ACT_RELU2));
+    CHECK(a.memory_bytes() > 0);
+    // the prompt by one prefill on a, by steps on b
+    std::vector<float> la, lb;
+    const std::uint32_t na = a.prefill(prompt, 0, &la);
+    std::uint32_t nb = 0;
+    for (std::uint32_t p = 0; p < prompt.size(); ++p) nb = b.step(prompt[p], p, p + 1 == prompt.size() ? &lb : nullptr);
+    CHECK(na == nb);
+    bool same = la.size() == lb.size();
+    for (std::size_t i = 0; same && i < la.size(); ++i) same = bits(la[i]) == bits(lb[i]);
+    CHECK(same);
+    for (std::uint32_t p : {0u, 17u, 39u})
+        for (std::uint32_t l = 0; l < c.n_layers; ++l) CHECK(a.kv(l, p, 1) == b.kv(l, p, 1));
+    // the next step continues both at position 40
+    std::vector<float> sa, sb;
+    CHECK(a.step(na, 40, &sa) == b.step(nb, 40, &sb));
+    same = true;
+    for (std::size_t i = 0; i < sa.size(); ++i) same = same && bits(sa[i]) == bits(sb[i]);
+    CHECK(same);
+    // greedy generation with prefill passes and fed step by step
+    CHECK(a.generate(prompt, 24) == b.generate(prompt, 24, true));
+    // beyond the context
+    CHECK_THROWS_CODE(a.prefill(std::vector<std::uint32_t>(8, 1u), 636), VX_ERR_CONTEXT_OVERFLOW);
+    // a projection of the wrong size, a sub-norm the architecture does not have
+    CHECK_THROWS_CODE(a.set_projection(0, VX_PROJ_Q, std::vector<std::uint8_t>(100, 125), 1.0f), VX_ERR_BUFFER_TOO_SMALL);
+    if (falcon) CHECK_THROWS_CODE(a.set_norm(0, VX_NORM_ATTN_SUB, std::vector<float>(256, 1.0f)), VX_ERR_INVALID_ARGUMENT);
+    velurex_hip::Decoder moved(std::move(a));
+    CHECK(moved.config().vocab == 1000);
+    CHECK_THROWS_CODE(a.config(), VX_ERR_INVALID_HANDLE);
+}
+
 void cpu_checks() {
     velurex_hip::check_abi();
     CHECK(velurex_hip::version() == VX_VERSION_STRING);
@@ -220,6 +330,9 @@ void cpu_checks() {
     static_assert(!std::is_copy_constructible<velurex_hip::VelurexHipLayer>::value, "VelurexHipLayer must not be copyable");
     static_assert(std::is_base_of<velurex_hip::TernaryGemvLayer, velurex_hip::VelurexHipLayer>::value, "a layer");
     static_assert(std::has_virtual_destructor<velurex_hip::TernaryGemvLayer>::value, "owned through the interface");
+    static_assert(std::is_move_constructible<velurex_hip::Decoder>::value, "Decoder must be movable");
+    static_assert(!std::is_copy_constructible<velurex_hip::Decoder>::value, "Decoder must not be copyable");
+    CHECK_THROWS_CODE(velurex_hip::Decoder::open_gguf("this-file-does-not-exist.gguf"), VX_ERR_IO);
 }
 
 void gpu_checks() {
@@ -235,6 +348,8 @@ void gpu_checks() {
     device_case(3072, 3072);
     device_case(70, 777);
     threads_case();
+    decoder_case(false);
+    decoder_case(true);
 
     // Errors of a valid handle: a byte outside the 243 velurex values, slices of the wrong length, a moved-from layer.
     std::vector<std::uint8_t> bad(32, 125);
