@@ -65,7 +65,8 @@ def test_pack_unpack_round_trip(oracle, cols):
 
 
 def test_tile_row_bytes_matches_published_sizes(oracle):
-    # Values the survey verified against pack.rs:222-225 (bytes per row): planar / tiled.
+    # Bytes per row at the model widths, planar / tiled, as pack.rs:222-225 sizes them (whole 160-column blocks of 32
+    # bytes, then the packed tail of ceil(rest / 5) bytes rounded up to even).
     table = {2560: (512, 512), 3072: (640, 616), 4096: (832, 820), 6912: (1408, 1384), 12288: (2464, 2458),
              23040: (4608, 4608)}
     for cols, (planar, tiled) in table.items():
