@@ -409,8 +409,8 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 
             continue;
         }
         // The sums are complete at the atomics' coherence point before the ticket is taken (every memory operation of
-        // the wave waited for, then an agent-scope release before the ticket), and the last slice reads them with
-        // atomics after its ticket and an agent-scope acquire: no cache writeback.
+        // every wave waited for, then the barrier: take_ticket's hand-off), and the last slice reads them with atomics
+        // after its ticket: no cache writeback.
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0) last_slice = take_ticket(jb.tickets + grp, jb.kslices - 1u);
