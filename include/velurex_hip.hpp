@@ -225,6 +225,92 @@ private:
 };
 
 // -------------------------------------------------------------------------------------------------------------------
+// Many projections in one launch, and many tokens per call
+// -------------------------------------------------------------------------------------------------------------------
+
+/// One GEMV of a plan on device buffers (vx_gemv_job_t): `acts` (cols int8) staged into `staged` by each run, outputs
+/// int32 or, with `act_scale_dev`, float(acc) * (weight_scale / *act_scale_dev) read when the plan runs.
+struct PlanJob {
+    const VelurexHipLayer* layer;
+    const std::int8_t* acts;     // device, cols values
+    void* staged;                // device, staged_bytes(cols) bytes (jobs with the same acts may share it)
+    void* out;                   // device, rows values
+    const float* act_scale_dev;  // device, or null for int32 outputs
+};
+
+/// Bytes of one staged activation vector of `cols` columns (vx_staged_bytes).
+inline std::size_t staged_bytes(std::size_t cols) {
+    std::size_t n = 0;
+    detail::check(vx_staged_bytes(cols, &n));
+    return n;
+}
+
+/// Many GEMVs as one launch per run (vx_plan_*): the single-launch form of the reference's concurrent projections of a
+/// layer and of its per-token CUDA graph (layer.rs:657-716, gpu.rs:389-493). Move-only; a run allocates nothing.
+class Plan {
+public:
+    explicit Plan(const std::vector<PlanJob>& jobs) {
+        std::vector<vx_gemv_job_t> raw(jobs.size());
+        for (std::size_t i = 0; i < jobs.size(); ++i) {
+            const auto shape = jobs[i].layer->shape();
+            vx_gemv_job_t& j = raw[i];
+            j = vx_gemv_job_t{};
+            j.struct_size = sizeof(j);
+            j.out_f32 = jobs[i].act_scale_dev != nullptr ? 1 : 0;
+            j.matrix = jobs[i].layer->handle();
+            j.staged = jobs[i].staged;
+            j.staged_len = staged_bytes(shape.second);
+            j.act_scale_dev = jobs[i].act_scale_dev;
+            j.out = jobs[i].out;
+            j.out_capacity = shape.first;
+            j.acts = jobs[i].acts;
+        }
+        detail::check(vx_plan_create(raw.data(), raw.size(), &p_));
+    }
+    ~Plan() {
+        if (p_ != nullptr) (void)vx_plan_free(p_);
+    }
+    Plan(const Plan&) = delete;
+    Plan& operator=(const Plan&) = delete;
+    Plan(Plan&& o) noexcept : p_(std::exchange(o.p_, nullptr)) {}
+    Plan& operator=(Plan&& o) noexcept {
+        if (this != &o) {
+            if (p_ != nullptr) (void)vx_plan_free(p_);
+            p_ = std::exchange(o.p_, nullptr);
+        }
+        return *this;
+    }
+    /// Enqueues the plan's GEMVs on `stream` (runs of one plan must not overlap).
+    void run(void* stream = nullptr) const { detail::check(vx_plan_run(handle(), stream)); }
+    /// Work items (tile group x K slice) of the launch.
+    std::uint32_t work_items() const {
+        std::uint32_t n = 0;
+        detail::check(vx_plan_work_items(handle(), &n));
+        return n;
+    }
+    vx_plan_t* handle() const {
+        if (p_ == nullptr) throw Error(VX_ERR_INVALID_HANDLE, "the plan was moved from");
+        return p_;
+    }
+
+private:
+    vx_plan_t* p_ = nullptr;
+};
+
+/// Y = X W^T for m tokens on the matrix cores, exact int32 (vx_gemm_i32_dev): x m x ldx int8 and y m x ldy int32 in
+/// device memory, `workspace` of gemm_workspace_bytes(layer, m) bytes (256-byte aligned) owned by the caller.
+inline std::size_t gemm_workspace_bytes(const VelurexHipLayer& layer, std::size_t m) {
+    std::size_t n = 0;
+    detail::check(vx_gemm_workspace_bytes(layer.handle(), m, &n));
+    return n;
+}
+inline void gemm_i32_dev(const VelurexHipLayer& layer, const std::int8_t* x, std::size_t m, std::size_t ldx,
+                         std::int32_t* y, std::size_t ldy, void* workspace, std::size_t workspace_len,
+                         void* stream = nullptr) {
+    detail::check(vx_gemm_i32_dev(layer.handle(), x, m, ldx, y, ldy, workspace, workspace_len, stream));
+}
+
+// -------------------------------------------------------------------------------------------------------------------
 // Decoder (the token loop on the GPU)
 // -------------------------------------------------------------------------------------------------------------------
 

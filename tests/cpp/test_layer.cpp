@@ -1,8 +1,9 @@
 // C++ test of velurex_hip.hpp (the TernaryGemvLayer interface and the kernel-level GEMV over the C ABI), in the manner
 // of the reference's C++ wrapper test (rust/crates/quintrit-c/tests/cpp/test_kernel.cpp): GEMVs against a brute-force
 // product at the shapes of that test and of quintrit-c/tests/ffi_kernel.rs:36-49,195-265, errors as exceptions with
-// their status codes, and the move-only owning classes; the decoder through the wrapper (prefill against steps, greedy
-// generation with and without prefill passes, its errors). Exit code 0 means success.
+// their status codes, and the move-only owning classes; a plan of GEMVs and the batched GEMM on device buffers; the
+// decoder through the wrapper (prefill against steps, greedy generation with and without prefill passes, its errors).
+// Exit code 0 means success.
 //
 //   test_layer          everything (needs a gfx950 device)
 //   test_layer --cpu    only what needs no device: the ABI, the layout, argument errors, the type traits
@@ -166,6 +167,82 @@ void device_case(std::size_t rows, std::size_t cols) {
     CHECK(ok);
     (void)hipFree(da);
     (void)hipFree(dy);
+}
+
+// A plan of three GEMVs (two share an input, one has its own; int32 and fp32 outputs) run twice with new inputs, and a
+// batched GEMM, all on device buffers, against brute force.
+void plan_and_gemm_case() {
+    struct M { std::size_t rows, cols; std::vector<std::int8_t> t; };
+    std::vector<M> mats = {{1024, 3072, {}}, {3072, 3072, {}}, {512, 6000, {}}};
+    std::vector<velurex_hip::VelurexHipLayer> layers;
+    for (auto& m : mats) {
+        m.t.resize(m.rows * m.cols);
+        for (auto& v : m.t) v = static_cast<std::int8_t>(static_cast<int>(next() % 3) - 1);
+        layers.emplace_back(pack_planar(m.t, m.rows, m.cols), m.rows, m.cols, 0.02f);
+    }
+    std::int8_t *a0 = nullptr, *a1 = nullptr;
+    void *s0 = nullptr, *s1 = nullptr, *y0 = nullptr, *y1 = nullptr, *y2 = nullptr;
+    float* as = nullptr;
+    bool ok = hipMalloc(reinterpret_cast<void**>(&a0), 3072) == hipSuccess && hipMalloc(reinterpret_cast<void**>(&a1), 6000) == hipSuccess &&
+              hipMalloc(&s0, velurex_hip::staged_bytes(3072)) == hipSuccess && hipMalloc(&s1, velurex_hip::staged_bytes(6000)) == hipSuccess &&
+              hipMalloc(&y0, 1024 * 4) == hipSuccess && hipMalloc(&y1, 3072 * 4) == hipSuccess && hipMalloc(&y2, 512 * 4) == hipSuccess &&
+              hipMalloc(reinterpret_cast<void**>(&as), 4) == hipSuccess;
+    CHECK(ok);
+    if (!ok) return;
+    const velurex_hip::Plan plan({{&layers[0], a0, s0, y0, nullptr}, {&layers[1], a0, s0, y1, as}, {&layers[2], a1, s1, y2, nullptr}});
+    CHECK(plan.work_items() > 0);
+    for (int run = 0; run < 2; ++run) {
+        std::vector<std::int8_t> x0(3072), x1(6000);
+        for (auto& v : x0) v = static_cast<std::int8_t>(next() & 0xFF);
+        for (auto& v : x1) v = static_cast<std::int8_t>(next() & 0xFF);
+        const float scale = run == 0 ? 0.5f : 1.75f;
+        CHECK(hipMemcpy(a0, x0.data(), 3072, hipMemcpyHostToDevice) == hipSuccess);
+        CHECK(hipMemcpy(a1, x1.data(), 6000, hipMemcpyHostToDevice) == hipSuccess);
+        CHECK(hipMemcpy(as, &scale, 4, hipMemcpyHostToDevice) == hipSuccess);
+        plan.run();
+        CHECK(hipDeviceSynchronize() == hipSuccess);
+        std::vector<std::int32_t> g0(1024), g2(512);
+        std::vector<float> g1(3072);
+        CHECK(hipMemcpy(g0.data(), y0, 1024 * 4, hipMemcpyDeviceToHost) == hipSuccess);
+        CHECK(hipMemcpy(g1.data(), y1, 3072 * 4, hipMemcpyDeviceToHost) == hipSuccess);
+        CHECK(hipMemcpy(g2.data(), y2, 512 * 4, hipMemcpyDeviceToHost) == hipSuccess);
+        const auto w0 = brute_force(mats[0].t, 1024, 3072, x0), w1 = brute_force(mats[1].t, 3072, 3072, x0);
+        const auto w2 = brute_force(mats[2].t, 512, 6000, x1);
+        bool same = true;
+        for (std::size_t r = 0; r < 1024; ++r) same = same && g0[r] == w0[r];
+        for (std::size_t r = 0; r < 3072; ++r) same = same && bits(g1[r]) == bits(epilogue(w1[r], 0.02f, scale));
+        for (std::size_t r = 0; r < 512; ++r) same = same && g2[r] == w2[r];
+        CHECK(same);
+    }
+    // 40 tokens through the GEMM on the 3072 x 3072 matrix
+    const std::size_t m = 40, cols = 3072, rows = 3072;
+    std::vector<std::int8_t> x(m * cols);
+    for (auto& v : x) v = static_cast<std::int8_t>(next() & 0xFF);
+    std::int8_t* dx = nullptr;
+    void *dy = nullptr, *ws = nullptr;
+    const std::size_t wsb = velurex_hip::gemm_workspace_bytes(layers[1], m);
+    ok = hipMalloc(reinterpret_cast<void**>(&dx), m * cols) == hipSuccess && hipMalloc(&dy, m * rows * 4) == hipSuccess &&
+         hipMalloc(&ws, wsb) == hipSuccess;
+    CHECK(ok);
+    if (ok) {
+        CHECK(hipMemcpy(dx, x.data(), m * cols, hipMemcpyHostToDevice) == hipSuccess);
+        velurex_hip::gemm_i32_dev(layers[1], dx, m, cols, static_cast<std::int32_t*>(dy), rows, ws, wsb);
+        CHECK(hipDeviceSynchronize() == hipSuccess);
+        std::vector<std::int32_t> y(m * rows);
+        CHECK(hipMemcpy(y.data(), dy, m * rows * 4, hipMemcpyDeviceToHost) == hipSuccess);
+        bool same = true;
+        for (std::size_t t = 0; t < m; ++t) {
+            const std::vector<std::int8_t> xt(x.begin() + t * cols, x.begin() + (t + 1) * cols);
+            const auto w = brute_force(mats[1].t, rows, cols, xt);
+            for (std::size_t r = 0; r < rows; ++r) same = same && y[t * rows + r] == w[r];
+        }
+        CHECK(same);
+        CHECK_THROWS_CODE(velurex_hip::gemm_i32_dev(layers[1], dx, m, cols, static_cast<std::int32_t*>(dy), rows, ws, wsb - 1),
+                          VX_ERR_BUFFER_TOO_SMALL);
+    }
+    for (void* p : {static_cast<void*>(a0), static_cast<void*>(a1), s0, s1, y0, y1, y2, static_cast<void*>(as),
+                    static_cast<void*>(dx), dy, ws})
+        (void)hipFree(p);
 }
 
 // One layer shared by four threads (the trait is Send + Sync), each with its own activations.
@@ -332,6 +409,8 @@ void cpu_checks() {
     static_assert(std::has_virtual_destructor<velurex_hip::TernaryGemvLayer>::value, "owned through the interface");
     static_assert(std::is_move_constructible<velurex_hip::Decoder>::value, "Decoder must be movable");
     static_assert(!std::is_copy_constructible<velurex_hip::Decoder>::value, "Decoder must not be copyable");
+    static_assert(!std::is_copy_constructible<velurex_hip::Plan>::value, "Plan must not be copyable");
+    CHECK(velurex_hip::staged_bytes(3072) > 0);
     CHECK_THROWS_CODE(velurex_hip::Decoder::open_gguf("this-file-does-not-exist.gguf"), VX_ERR_IO);
 }
 
@@ -348,6 +427,7 @@ void gpu_checks() {
     device_case(3072, 3072);
     device_case(70, 777);
     threads_case();
+    plan_and_gemm_case();
     decoder_case(false);
     decoder_case(true);
 
