@@ -1956,10 +1956,10 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
     __shared__ __align__(16) float sc[kShortCtx];
     __shared__ __align__(16) float fac[kShortCtx + 64u];
     __shared__ uint32_t bflag[kShortCtx / 32u + 2u];
-    __shared__ float wtot[8];
     __shared__ uint64_t etab[32];
     __shared__ __align__(16) u32x4 vl[kTiles][64];  // [tile][coordinate]: positions 8 t .. 8 t + 7
     __shared__ float s_sum;
+    __shared__ uint32_t s_ready;  // 32-position blocks whose factors and mask are in fac and bflag
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t h = blockIdx.x / kSlices, sl = blockIdx.x - h * kSlices;
@@ -1969,6 +1969,7 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
     uint16_t* vt = a.vc + static_cast<size_t>(kvh) * HD * a.vstride;
     const uint32_t t_last = (seq - 1u) / 8u;
     fill_etab(etab);
+    if (tid == 0) s_ready = 0u;
 
     // RoPE inputs: thread i < HD / 2 rotates pair i of q, HD / 2 <= i < HD pair i - HD / 2 of k; HD <= i < 2 HD takes
     // coordinate i - HD of v. The raw sums, the scale and the rotation are loaded before anything else.
@@ -2071,10 +2072,15 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
         if (j == 0) sc[g + 128u] = s1 * a.scale;
     }
     __syncthreads();
-    (void)chunk_factors<512>(sc, 0u, seq, 0u, fac, bflag, wtot, etab);
-    if (tid >= seq && tid < t_pad * 8u) fac[tid] = 0.0f;  // the padding's factors (vs = +0, no new maximum)
-    __syncthreads();
 
+    // The factors (attend_range, attention.rs:436-468, as chunk_factors computes them) come from wave 2, 64 positions
+    // at a time: the running maximum before each position by a scan over the lanes with the previous positions' maximum
+    // carried in (the combine keeps the earliest of equal values, so the scan equals the sequential fold), then ms =
+    // expf(m_old - score) with vs = 1 at a new maximum and ms = 1, vs = expf(score - max) otherwise, stored as -ms or
+    // vs; the positions from seq to the end of the last 32-position block get +0. After each 64 positions wave 2
+    // publishes the count of complete blocks (a workgroup-scope release), and the accumulator and sum waves start on a
+    // block once it is published (an acquire), so the chain does not wait for the factors of the whole context.
+    //
     // The accumulator of the lane's coordinate (wave 0: y, f16) and the sum (wave 1: ssum, f32) over the positions in
     // order, a block of 32 per step (the last one padded), its V words, factors and new-maximum mask read from LDS at
     // the start of the step. A block without a new maximum takes the short step (one f16 rounding of fma(v, vs, y));
@@ -2082,10 +2088,19 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
     // the multiply and its rounding leave y as it is, at the positions without one. Both are straight-line code: a
     // branch per position costs more than the longer step.
     const uint32_t nb = (seq + 31u) / 32u;
+    // Waits until block b is published. The bound (far beyond the producer's few microseconds) only keeps a wave from
+    // spinning for ever should the producer not run; it is never reached when it does.
+    auto wait_block = [&](uint32_t b) {
+        for (uint32_t spin = 0; spin < (1u << 20); ++spin) {
+            if (__hip_atomic_load(&s_ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) > b) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+    };
     if (wave == 0) {
         const uint32_t cl = lane < kLanes ? lane : 0u;
         _Float16 yh = 0;
         for (uint32_t b = 0; b < nb; ++b) {
+            wait_block(b);
             u32x4 w[4];
 #pragma unroll
             for (uint32_t i = 0; i < 4; ++i) w[i] = vl[4u * b + i][cl];
@@ -2121,6 +2136,7 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
     } else if (wave == 1) {
         float ssum = 0.0f;
         for (uint32_t b = 0; b < nb; ++b) {
+            wait_block(b);
             float f[32];
 #pragma unroll
             for (uint32_t i = 0; i < 8; ++i) {
@@ -2143,6 +2159,34 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
             }
         }
         if (lane == 0) s_sum = ssum;
+        __syncthreads();
+    } else if (wave == 2) {
+        const auto tab = [&](uint32_t k) { return etab[k]; };
+        const uint32_t n_pad = 32u * nb;
+        float carry = -__builtin_inff();  // the maximum of the positions before this group of 64
+        for (uint32_t base = 0; base < n_pad; base += 64u) {
+            const uint32_t p = base + lane;
+            const bool in = p < seq;
+            const float sv = in ? sc[p] : 0.0f;
+            float v = in && sv == sv ? sv : -__builtin_inff();  // a NaN score never moves the maximum
+#pragma unroll
+            for (int sh = 1; sh < 64; sh <<= 1) {
+                const float o = __shfl_up(v, sh);
+                if (lane >= static_cast<uint32_t>(sh)) v = max_later(o, v);
+            }
+            float prev = __shfl_up(v, 1);
+            prev = max_later(carry, lane == 0 ? -__builtin_inff() : prev);
+            carry = max_later(carry, __shfl(v, 63));
+            float f = 0.0f;
+            if (in) f = sv > prev ? -glibc_expf_with(prev - sv, tab) : glibc_expf_with(sv - prev, tab);
+            if (p < n_pad) fac[p] = f;
+            const uint64_t neg = __ballot(in && __builtin_signbit(f));
+            if (lane == 0) {
+                bflag[base / 32u] = static_cast<uint32_t>(neg);
+                if (base / 32u + 1u < nb) bflag[base / 32u + 1u] = static_cast<uint32_t>(neg >> 32);
+                __hip_atomic_store(&s_ready, min(nb, base / 32u + 2u), __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
         __syncthreads();
     } else {
         __syncthreads();
