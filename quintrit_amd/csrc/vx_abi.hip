@@ -748,6 +748,7 @@ static int create_plan(const vx_gemv_job_t* jobs, size_t n_jobs, bool lut, vx_pl
     p->d_part = nullptr;
     p->d_split = nullptr;
     p->d_q2jobs = nullptr;
+    p->d_q2sched = nullptr;
     p->n_jobs = static_cast<uint32_t>(n_jobs);
     p->total_items = items;
     p->max_rows = 0;
@@ -808,6 +809,7 @@ int vx_plan_run(const vx_plan_t* plan, void* stream) {
             q.jobs = plan->d_q2jobs;
             q.n_jobs = plan->n_jobs;
             q.total_items = plan->total_items;
+            q.sched = plan->d_q2sched;
             return launch_q2(q, plan->num_cus, static_cast<hipStream_t>(stream));
         }
         LaunchArgs a{};
@@ -1035,14 +1037,23 @@ int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_pl
         p->d_part = nullptr;
         p->d_split = nullptr;
         p->d_q2jobs = nullptr;
+        p->d_q2sched = nullptr;
         p->d_stage = nullptr;
         p->n_stage = 0;
         p->n_jobs = static_cast<uint32_t>(n_jobs);
         p->total_items = items;
         p->max_rows = 0;
         p->n_split = 0;
-        hipError_t e = hipMalloc(&p->d_q2jobs, n_jobs * sizeof(Q2Job));
-        if (e == hipSuccess) e = hipMemcpy(p->d_q2jobs, hj.data(), n_jobs * sizeof(Q2Job), hipMemcpyHostToDevice);
+        // the job table, then the schedule (4-byte words after the 8-byte aligned table)
+        const std::vector<uint32_t> sched = q2_schedule(hj, items, di.num_cus);
+        const size_t job_bytes = n_jobs * sizeof(Q2Job);
+        hipError_t e = hipMalloc(&p->d_q2jobs, job_bytes + sched.size() * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipMemcpy(p->d_q2jobs, hj.data(), job_bytes, hipMemcpyHostToDevice);
+        if (e == hipSuccess) {
+            uint32_t* ds = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(p->d_q2jobs) + job_bytes);
+            e = hipMemcpy(ds, sched.data(), sched.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
+            p->d_q2sched = ds;
+        }
         if (e != hipSuccess) {
             destroy_plan(p);
             VX_FAIL(VX_ERR_DEVICE, "plan allocation failed: %s", hipGetErrorString(e));

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/velurex_hip.h"
 
@@ -269,6 +270,9 @@ struct Q2Args {
     uint32_t n_jobs;
     uint32_t total_items;  // runs of 8 tiles (64 rows each) summed over the jobs
     Q2Job one;
+    // The plan's schedule, or nullptr (workgroup i takes items i, i + grid, ...): workgroup i takes the items
+    // sched[grid + 1 + k] for k in sched[i] .. sched[i + 1] - 1, in increasing order, grid = min(total_items, CUs).
+    const uint32_t* sched;
 };
 
 size_t q2_blocks(size_t cols);
@@ -278,6 +282,8 @@ size_t q2_device_bytes(size_t rows, size_t cols);
 void q2_to_device_layout(const uint8_t* planar, const uint16_t* scales, size_t rows, size_t cols, uint8_t* dst);
 inline uint32_t q2_items(uint32_t rows) { return ((rows + kTileRows - 1) / kTileRows + 7) / 8; }
 int launch_q2(const Q2Args& a, int num_cus, hipStream_t stream);
+// The plan's balanced assignment of its items to min(total_items, num_cus) workgroups (the layout of Q2Args::sched).
+std::vector<uint32_t> q2_schedule(const std::vector<Q2Job>& jobs, uint32_t total_items, int num_cus);
 int launch_q2_lane_sums(const Q2Job& j, int32_t* out, hipStream_t stream);
 
 // ---- device state -------------------------------------------------------------------------------------------------------
@@ -328,7 +334,8 @@ struct vx_plan {
     vx::Job* d_jobs;
     int32_t* d_part;
     uint32_t* d_split;  // indices of the jobs split into K slices
-    vx::Q2Job* d_q2jobs;  // Q2_0 plans: their job table (d_jobs unused)
+    vx::Q2Job* d_q2jobs;  // Q2_0 plans: their job table (d_jobs unused), then the schedule (d_q2sched)
+    const uint32_t* d_q2sched;
     uint32_t n_jobs, total_items, max_rows, n_split;
     uint32_t lut;  // the jobs read compact activation tables (vx_lut_plan_create)
     vx::StageJob* d_stage;  // the distinct stagings of jobs that bring raw activations, run first (one launch)

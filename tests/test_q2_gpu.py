@@ -89,3 +89,41 @@ def test_q2_config4_shapes_and_plan(torch_dev, oracle):
         assert np.all(np.abs(got - want) <= 1e-6 * np.abs(want))
         m.close()
     plan.close()
+
+
+def test_q2_plan_many_ragged_jobs(torch_dev, oracle):
+    """A plan with more items than CUs and items of very different lengths: 300 jobs of ragged shapes (partial tiles
+    and tile groups, 1 to 77 blocks per row) around one 4096 x 12288 projection. The plan hands each workgroup a
+    balanced list of items; every output must be written exactly as the oracle computes it (outputs start as NaN, so an
+    item left out shows)."""
+    from quintrit_amd import _lib
+    torch = torch_dev
+    rng = np.random.default_rng(44)
+    shapes = [(int(rng.integers(1, 700)), int(rng.choice([64, 128, 320, 640, 1600, 3200]))) for _ in range(150)]
+    shapes += [(4096, 12288)]
+    shapes += [(int(rng.integers(1, 1200)), int(rng.choice([64, 704, 4096]))) for _ in range(150)]
+    mats, cases, jobs, outs, keep = [], [], [], [], []
+    for rows, cols in shapes:
+        t, ws16, acts, as32 = make_case(oracle, rng, rows, cols)
+        planar = oracle.pack_matrix(t)
+        m = _lib.Q2Matrix(planar, ws16, rows, cols)
+        a, s = torch.from_numpy(acts).cuda(), torch.from_numpy(as32).cuda()
+        out = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+        jobs.append(_lib.Q2Job(matrix=m.handle.value, acts=a.data_ptr(), acts_len=cols, act_scales=s.data_ptr(),
+                               n_act_scales=cols // 32, out=out.data_ptr(), out_capacity=rows))
+        mats.append(m), cases.append((planar, ws16, acts, as32)), outs.append(out), keep.append((a, s))
+    wants = [oracle.q2_0_gemv(planar, ws16.astype(np.float32), acts, as32, rows, cols)
+             for (rows, cols), (planar, ws16, acts, as32) in zip(shapes, cases)]
+    plan = _lib.Q2Plan(jobs)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for run in range(2):
+        print(f"[q2 ragged plan] run {run}", flush=True)
+        plan.run(stream)
+        torch.cuda.synchronize()
+        for i, ((rows, cols), out, want) in enumerate(zip(shapes, outs, wants)):
+            got = out.cpu().numpy()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (i, rows, cols)
+            out.fill_(float("nan"))
+    plan.close()
+    for m in mats:
+        m.close()
