@@ -1939,17 +1939,18 @@ __global__ __launch_bounds__(256) void attn_chain_kernel(AttnArgs a) {
 // The decode step's attention while the context is short (pos < kShortCtx: one chunk, no split) in one kernel per
 // (head, 64 coordinates): the RoPE of q, k, v of the position (the first slice of the first head of each KV head
 // appends k and v; every workgroup uses its own copy of the position itself), the scores of every position
-// (512 threads, four lanes per position, as attn_score_kernel), the factors, then the accumulators and the sum (one
+// (1024 threads, four lanes per position, as attn_score_kernel), the factors, then the accumulators and the sum (one
 // wave), and the output. The loads go out in the order they are needed: the RoPE inputs, the K rows, then the V tiles of
 // the workgroup's 64 coordinates, which all threads stage into LDS during the scores, so that the chain reads V and the
 // factors from LDS in a compact loop.
 template <int HD>
-__global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
+__global__ __launch_bounds__(1024) void attn_short_kernel(AttnArgs a) {
     constexpr uint32_t kSlices = attn_slices(HD);
     constexpr uint32_t kLanes = HD >= 64 ? 64u : static_cast<uint32_t>(HD);
     constexpr int kBlk = HD / 32;
     constexpr uint32_t kTiles = kShortCtx / 8u;           // 8-position V tiles of the context at most
-    constexpr uint32_t kVPer = kTiles * 64u / 512u;       // V entries (tile, coordinate) per thread
+    constexpr uint32_t kVPer = kTiles * 64u / 1024u;      // V entries (tile, coordinate) per thread
+    static_assert(kShortCtx * 4u == 1024u, "four lanes per position of the context");
     __shared__ __align__(16) uint16_t qh[HD];
     __shared__ __align__(16) uint16_t kp[HD];
     __shared__ __align__(16) uint16_t vp[HD];
@@ -1992,23 +1993,18 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
         r_as = *a.v.as;
         r_x0 = a.v.part[kvh * HD + (tid - HD)];
     }
-    // K rows of this thread's two positions (the position itself later, from kp)
+    // K row of this thread's position (the position itself later, from kp)
     const uint32_t j = tid & 3u, g = tid >> 2;
-    uint4 k0[kBlk], k1[kBlk];
+    uint4 k0[kBlk];
     if (g < seq && g != pos) {
 #pragma unroll
         for (int i = 0; i < kBlk; ++i) k0[i] = *reinterpret_cast<const uint4*>(kb + static_cast<size_t>(g) * HD + 8 * j + 32 * i);
     }
-    if (g + 128u < seq && g + 128u != pos) {
-#pragma unroll
-        for (int i = 0; i < kBlk; ++i)
-            k1[i] = *reinterpret_cast<const uint4*>(kb + static_cast<size_t>(g + 128u) * HD + 8 * j + 32 * i);
-    }
-    // V tiles of the slice's coordinates: entry e = tid + 512 r is (tile e / 64, coordinate e % 64)
+    // V tiles of the slice's coordinates: entry e = tid + 1024 r is (tile e / 64, coordinate e % 64)
     u32x4 vr[kVPer];
 #pragma unroll
     for (uint32_t r = 0; r < kVPer; ++r) {
-        const uint32_t e = tid + 512u * r, t = e >> 6, c = e & 63u;
+        const uint32_t e = tid + 1024u * r, t = e >> 6, c = e & 63u;
         if (t <= t_last && c < kLanes)
             vr[r] = *reinterpret_cast<const u32x4*>(vt + (static_cast<size_t>(t) * HD + sl * 64u + c) * 8u);
     }
@@ -2037,7 +2033,7 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
     const uint32_t t_pad = (seq + 31u) / 32u * 4u;  // tiles up to the end of the last block
 #pragma unroll
     for (uint32_t r = 0; r < kVPer; ++r) {
-        const uint32_t e = tid + 512u * r, t = e >> 6, c = e & 63u;
+        const uint32_t e = tid + 1024u * r, t = e >> 6, c = e & 63u;
         if (t < t_pad && c < kLanes) {
             u32x4 w = t <= t_last ? vr[r] : u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
             if (t == t_last) {
@@ -2059,17 +2055,9 @@ __global__ __launch_bounds__(512) void attn_short_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < kBlk; ++i) k0[i] = *reinterpret_cast<const uint4*>(kp + 32 * i + 8 * j);
     }
-    if (g + 128u == pos) {
-#pragma unroll
-        for (int i = 0; i < kBlk; ++i) k1[i] = *reinterpret_cast<const uint4*>(kp + 32 * i + 8 * j);
-    }
     if (g < seq) {
         const float s0 = score_dot4<HD>(qh, k0, j);
         if (j == 0) sc[g] = s0 * a.scale;
-    }
-    if (g + 128u < seq) {
-        const float s1 = score_dot4<HD>(qh, k1, j);
-        if (j == 0) sc[g + 128u] = s1 * a.scale;
     }
     __syncthreads();
 
@@ -2573,10 +2561,10 @@ int launch_attention(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
 // The short-context form (every position below kShortCtx): one kernel per (head, 64 coordinates).
 int launch_attention_short(const AttnArgs& a, uint32_t head_dim, hipStream_t s) {
     const dim3 grid(a.n_heads * attn_slices(head_dim));
-    if (head_dim == 256) hipLaunchKernelGGL(attn_short_kernel<256>, grid, dim3(512), 0, s, a);
-    else if (head_dim == 128) hipLaunchKernelGGL(attn_short_kernel<128>, grid, dim3(512), 0, s, a);
-    else if (head_dim == 64) hipLaunchKernelGGL(attn_short_kernel<64>, grid, dim3(512), 0, s, a);
-    else if (head_dim == 32) hipLaunchKernelGGL(attn_short_kernel<32>, grid, dim3(512), 0, s, a);
+    if (head_dim == 256) hipLaunchKernelGGL(attn_short_kernel<256>, grid, dim3(1024), 0, s, a);
+    else if (head_dim == 128) hipLaunchKernelGGL(attn_short_kernel<128>, grid, dim3(1024), 0, s, a);
+    else if (head_dim == 64) hipLaunchKernelGGL(attn_short_kernel<64>, grid, dim3(1024), 0, s, a);
+    else if (head_dim == 32) hipLaunchKernelGGL(attn_short_kernel<32>, grid, dim3(1024), 0, s, a);
     else VX_FAIL(VX_ERR_INTERNAL, "no attention kernel for head_dim %u", head_dim);
     VX_HIP(hipGetLastError());
     return VX_OK;
