@@ -810,6 +810,7 @@ int vx_plan_run(const vx_plan_t* plan, void* stream) {
             q.n_jobs = plan->n_jobs;
             q.total_items = plan->total_items;
             q.sched = plan->d_q2sched;
+            q.sched_grid = plan->q2_grid;
             return launch_q2(q, plan->num_cus, static_cast<hipStream_t>(stream));
         }
         LaunchArgs a{};
@@ -1053,6 +1054,7 @@ int vx_q2_plan_create(const vx_q2_job_t* jobs, size_t n_jobs, vx_plan_t** out_pl
             uint32_t* ds = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(p->d_q2jobs) + job_bytes);
             e = hipMemcpy(ds, sched.data(), sched.size() * sizeof(uint32_t), hipMemcpyHostToDevice);
             p->d_q2sched = ds;
+            p->q2_grid = static_cast<uint32_t>(sched.size() - 1u - items);
         }
         if (e != hipSuccess) {
             destroy_plan(p);

@@ -271,8 +271,10 @@ struct Q2Args {
     uint32_t total_items;  // runs of 8 tiles (64 rows each) summed over the jobs
     Q2Job one;
     // The plan's schedule, or nullptr (workgroup i takes items i, i + grid, ...): workgroup i takes the items
-    // sched[grid + 1 + k] for k in sched[i] .. sched[i + 1] - 1, in increasing order, grid = min(total_items, CUs).
+    // sched[grid + 1 + k] for k in sched[i] .. sched[i + 1] - 1, in increasing order; the launch has sched_grid
+    // workgroups, the count the schedule was made for.
     const uint32_t* sched;
+    uint32_t sched_grid;
 };
 
 size_t q2_blocks(size_t cols);
@@ -336,6 +338,7 @@ struct vx_plan {
     uint32_t* d_split;  // indices of the jobs split into K slices
     vx::Q2Job* d_q2jobs;  // Q2_0 plans: their job table (d_jobs unused), then the schedule (d_q2sched)
     const uint32_t* d_q2sched;
+    uint32_t q2_grid;     // the workgroups the schedule was made for
     uint32_t n_jobs, total_items, max_rows, n_split;
     uint32_t lut;  // the jobs read compact activation tables (vx_lut_plan_create)
     vx::StageJob* d_stage;  // the distinct stagings of jobs that bring raw activations, run first (one launch)

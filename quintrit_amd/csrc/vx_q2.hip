@@ -320,7 +320,10 @@ std::vector<uint32_t> q2_schedule(const std::vector<Q2Job>& jobs, uint32_t total
 
 int launch_q2(const Q2Args& a, int num_cus, hipStream_t stream) {
     if (a.total_items == 0) return VX_OK;
-    const uint32_t grid = std::min<uint32_t>(a.total_items, static_cast<uint32_t>(num_cus));
+    if (a.sched != nullptr && (a.jobs == nullptr || a.sched_grid == 0 || a.sched_grid > a.total_items))
+        VX_FAIL(VX_ERR_INTERNAL, "a Q2_0 schedule for %u workgroups over %u items", a.sched_grid, a.total_items);
+    const uint32_t grid =
+        a.sched != nullptr ? a.sched_grid : std::min<uint32_t>(a.total_items, static_cast<uint32_t>(num_cus));
     if (a.jobs) hipLaunchKernelGGL(q2_kernel<true>, dim3(grid), dim3(kQ2Waves * 64), 0, stream, a);
     else hipLaunchKernelGGL(q2_kernel<false>, dim3(grid), dim3(kQ2Waves * 64), 0, stream, a);
     VX_HIP(hipGetLastError());
