@@ -206,9 +206,11 @@ static int check_io(const vx_matrix_t* m, const void* acts, size_t acts_len, con
 // A lone GEMV of matrix m on staged activations, or (raw) on int8 activations that every workgroup stages for its own
 // K slice: one launch (a split matrix's K slices add their sums atomically and the last of each tile group writes the
 // outputs). Calls on one matrix share its sums and tickets, so they must not overlap. With `flag`, the launch's last
-// workgroup stores `seq` there once every output is written.
+// workgroup stores `seq` there once every output is written. K slices hold min_slice_chunks chunks at least (1 where the
+// activations are read from host memory).
 static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint32_t out_kind, float post,
-                      hipStream_t s, uint32_t* flag = nullptr, uint32_t seq = 0, const int8_t* raw = nullptr) {
+                      hipStream_t s, uint32_t* flag = nullptr, uint32_t seq = 0, const int8_t* raw = nullptr,
+                      uint32_t min_slice_chunks = kLoneMinSliceChunks) {
     LaunchArgs a{};
     a.done = flag != nullptr ? m->d_done : nullptr;
     a.flag = flag;
@@ -218,7 +220,7 @@ static int run_single(const vx_matrix* m, const uint8_t* staged, void* out, uint
     a.jobs = nullptr;
     a.n_jobs = 1;
     Job& j = a.one;
-    plan_job(j, m->g, static_cast<uint32_t>(m->num_cus));
+    plan_job(j, m->g, static_cast<uint32_t>(m->num_cus), min_slice_chunks);
     j.w = m->d_w;
     j.staged = staged;
     j.part = m->d_part;
@@ -588,7 +590,7 @@ int vx_layer_forward(const vx_matrix_t* matrix, const int8_t* acts, size_t acts_
         m->io_seq = seq;
         std::memcpy(m->h_io, acts, m->g.cols);
         VX_TRY(run_single(m, nullptr, m->h_io_dev + out_off, kOutF32Post, m->weight_scale / act_scale, m->io_stream,
-                          reinterpret_cast<uint32_t*>(m->h_io_dev + flag_off), seq, m->h_io_dev));
+                          reinterpret_cast<uint32_t*>(m->h_io_dev + flag_off), seq, m->h_io_dev, 1u));
         // Wait for the flag; every 65536 reads (tens of microseconds, longer than a call), ask the stream whether it
         // has ended (an error, or an end without the flag, is reported instead of waiting on).
         for (uint32_t i = 1;; ++i) {

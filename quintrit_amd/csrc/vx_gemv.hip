@@ -476,11 +476,14 @@ __global__ __launch_bounds__(256) void finish_kernel(LaunchArgs args, const uint
 
 // ---- host side ---------------------------------------------------------------------------------------------------------------
 
-void plan_job(Job& j, const Geometry& g, uint32_t target_items) {
+void plan_job(Job& j, const Geometry& g, uint32_t target_items, uint32_t min_slice_chunks) {
     const uint32_t nc = static_cast<uint32_t>(g.n_chunks);
     const uint32_t groups = static_cast<uint32_t>(g.n_groups);
     uint32_t ks = (nc + kMaxSliceChunks - 1) / kMaxSliceChunks;
-    if (target_items) ks = std::max(ks, std::min(nc, (target_items + groups - 1) / groups));
+    if (target_items) {
+        const uint32_t most = std::max(nc / std::max(min_slice_chunks, 1u), 1u);  // slices of min_slice_chunks at most
+        ks = std::max(ks, std::min(most, (target_items + groups - 1) / groups));
+    }
     const uint32_t sc = (nc + ks - 1) / ks;
     j.slice_chunks = sc;
     j.kslices = (nc + sc - 1) / sc;

@@ -179,9 +179,16 @@ struct LaunchArgs {
 
 constexpr uint32_t kMaxSliceChunks = 40;  // chunks per K slice staged in LDS (5 KiB of activations)
 
-// Host planner: fills kslices/slice_chunks of a job. `target_items` spreads a lone GEMV over the GPU; 0 keeps slices as
-// long as kMaxSliceChunks allows (the batched launches, which have work enough).
-void plan_job(Job& j, const Geometry& g, uint32_t target_items);
+// Host planner: fills kslices/slice_chunks of a job. `target_items` spreads a lone GEMV over the GPU, with at least
+// `min_slice_chunks` chunks per slice where the row has them; 0 keeps slices as long as kMaxSliceChunks allows (the
+// batched launches, which have work enough).
+void plan_job(Job& j, const Geometry& g, uint32_t target_items, uint32_t min_slice_chunks = 1);
+// The chunks per K slice a lone GEMV on activations in device memory keeps at least: below that the slices' atomic
+// sums and tickets cost more than their parallelism gains at the shapes of one to three tile groups (2560 x 2560: 7.16
+// -> 6.57 us per call, 3072 x 3072: 7.95 -> 7.03 us, 1024 x 3072: 7.2 -> 6.7-7.0 us; 4 chunks were slower again), and
+// the wide shapes keep their split. Activations read from host memory keep one chunk per slice (vx_layer_forward at
+// 3072 x 3072: 19 us with one, 22-37 us with two or three).
+constexpr uint32_t kLoneMinSliceChunks = 3;
 inline uint32_t job_items(const Job& j) {
     return (j.n_tiles + kTileGroup - 1) / kTileGroup * j.kslices;
 }
