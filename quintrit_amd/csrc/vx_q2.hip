@@ -71,7 +71,8 @@ void q2_to_device_layout(const uint8_t* planar, const uint16_t* scales, size_t r
 
 // ---- kernel -----------------------------------------------------------------------------------------------------------
 
-constexpr int kQ2Waves = 16;   // 8 tiles x 2 halves of 32 rows
+constexpr int kQ2Waves = 16;   // 8 tiles x 2 halves of 32 rows (plans)
+constexpr int kQ2LoneWaves = 4;  // 2 tiles per item: a lone GEMV's waves spread over more CUs
 constexpr int kQ2Pre = 4;      // blocks of weights in flight per wave (64 KiB per CU)
 
 __constant__ TritTable g_trits = make_trit_table();
@@ -84,10 +85,16 @@ typedef __attribute__((address_space(4))) const Q2Job c_q2job;
 typedef __attribute__((address_space(4))) const float c_q2float;  // uniform reads through the scalar cache
 typedef __attribute__((address_space(4))) const uint32_t c_q2u32;
 
-// Work item: 8 consecutive tiles of a tile group (wave w: tile 8 half + w / 2, rows 32 (w % 2) .. + 31 of it). The
-// activations and their scales are staged in LDS once per item; every wave then streams its rows' blocks in order.
-template <bool MANY>
-__global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
+// Work item: W / 2 consecutive tiles of a tile group (wave w: tile (W / 2) i + w / 2 for the item's index i in the
+// group, rows 32 (w % 2) .. + 31 of it). The activations and their scales are staged in LDS once per item; every wave
+// then streams its rows' blocks in order. A lone GEMV takes W = 4 while its items fit the CUs about once: a wave's
+// pass over its rows' blocks sets the call's time, and with two waves per SIMD instead of four it runs faster (at
+// 4096 columns 19.9 against 27.4 us per call, at 12288 48.5 against 72.9; W = 2 took 22.3 and 51.7).
+template <bool MANY, int W>
+__global__ __launch_bounds__(W * 64) void q2_kernel(Q2Args args) {
+    static_assert(W >= 2 && W % 2 == 0 && (2 * kTileGroup) % W == 0, "whole items of a tile group");
+    constexpr uint32_t kPer = W / 2u;                      // tiles per item
+    constexpr uint32_t kItemsPerGroup = kTileGroup / kPer;
     // row B (256 bytes): 32 copies of t0..t3 of byte B, then 32 copies of t4 of B in every byte; lane l of a half-wave
     // reads copy l of each half (one address, offsets 0 and 128), so the t0..t3 dwords of four bytes land in the
     // registers of one MFMA operand
@@ -96,7 +103,7 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    for (uint32_t i = tid; i < 256u * 16u; i += kQ2Waves * 64u) {
+    for (uint32_t i = tid; i < 256u * 16u; i += W * 64u) {
         const uint32_t b = i >> 4, e = (i & 8u) ? t4_bytes(b * 0x01010101u) : g_trits.v[b];
         *reinterpret_cast<uint4*>(reinterpret_cast<char*>(tab) + b * 256u + (i & 15u) * 16u) = make_uint4(e, e, e, e);
     }
@@ -140,12 +147,12 @@ __global__ __launch_bounds__(kQ2Waves * 64) void q2_kernel(Q2Args args) {
         if (MANY) __builtin_memcpy(&jb, (const Q2Job*)(cj + jj_job), sizeof(Q2Job));
         else jb = args.one;
         const uint32_t local = item - jb.item_begin;
-        const uint32_t grp = local >> 1, tt = (local & 1u) * 8u + (wave >> 1), rb = wave & 1u;
+        const uint32_t grp = local / kItemsPerGroup, tt = (local % kItemsPerGroup) * kPer + (wave >> 1), rb = wave & 1u;
         const uint32_t T = min(static_cast<uint32_t>(kTileGroup), jb.n_tiles - grp * kTileGroup);
         const uint32_t ns = jb.cols / 32u, nb = jb.nb, n_chunks = 2u * nb, ng = (nb + 3u) / 4u;
         __syncthreads();  // the previous item is done with actw
         const uint32_t* a32 = reinterpret_cast<const uint32_t*>(jb.acts);
-        for (uint32_t i = tid; i < nb * 40u; i += kQ2Waves * 64u) actw[i] = i < jb.cols / 4u ? a32[i] : 0u;
+        for (uint32_t i = tid; i < nb * 40u; i += W * 64u) actw[i] = i < jb.cols / 4u ? a32[i] : 0u;
         const c_q2float* asp = (const c_q2float*)(jb.act_scales);  // the activation scale of block s: asp[s]
         __syncthreads();
         if (tt >= T) continue;
@@ -322,10 +329,23 @@ int launch_q2(const Q2Args& a, int num_cus, hipStream_t stream) {
     if (a.total_items == 0) return VX_OK;
     if (a.sched != nullptr && (a.jobs == nullptr || a.sched_grid == 0 || a.sched_grid > a.total_items))
         VX_FAIL(VX_ERR_INTERNAL, "a Q2_0 schedule for %u workgroups over %u items", a.sched_grid, a.total_items);
+    if (a.jobs == nullptr) {
+        // a lone GEMV: items of kQ2LoneWaves / 2 tiles while they fit two workgroups per CU, else the plan's form
+        const uint32_t per = kQ2LoneWaves / 2u, items = (a.one.n_tiles + per - 1u) / per;
+        if (items <= 2u * static_cast<uint32_t>(num_cus)) {
+            Q2Args b = a;
+            b.total_items = items;
+            hipLaunchKernelGGL((q2_kernel<false, kQ2LoneWaves>), dim3(items), dim3(kQ2LoneWaves * 64), 0, stream, b);
+        } else {
+            const uint32_t grid = std::min<uint32_t>(a.total_items, static_cast<uint32_t>(num_cus));
+            hipLaunchKernelGGL((q2_kernel<false, kQ2Waves>), dim3(grid), dim3(kQ2Waves * 64), 0, stream, a);
+        }
+        VX_HIP(hipGetLastError());
+        return VX_OK;
+    }
     const uint32_t grid =
         a.sched != nullptr ? a.sched_grid : std::min<uint32_t>(a.total_items, static_cast<uint32_t>(num_cus));
-    if (a.jobs) hipLaunchKernelGGL(q2_kernel<true>, dim3(grid), dim3(kQ2Waves * 64), 0, stream, a);
-    else hipLaunchKernelGGL(q2_kernel<false>, dim3(grid), dim3(kQ2Waves * 64), 0, stream, a);
+    hipLaunchKernelGGL((q2_kernel<true, kQ2Waves>), dim3(grid), dim3(kQ2Waves * 64), 0, stream, a);
     VX_HIP(hipGetLastError());
     return VX_OK;
 }

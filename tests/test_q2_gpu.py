@@ -46,7 +46,8 @@ def run_q2(torch, mat, acts, as32):
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 64), (7, 128), (8, 192), (9, 640), (65, 704), (130, 4096), (1000, 1600),
-                                       (129, 12288), (2049, 320)])
+                                       (129, 12288), (2049, 320),
+                                       (66000, 64)])  # more items than two workgroups per CU: the 16-wave instance
 def test_q2_bit_exact_vs_oracle(torch_dev, oracle, rows, cols):
     from quintrit_amd import _lib
     print(f"[q2] {rows}x{cols}", flush=True)
