@@ -2396,7 +2396,9 @@ __global__ __launch_bounds__(256) void pf_rope_kernel(PfRopeArgs a) {
     const float pq = zero ? 0.0f : a.wsq / as, pk = zero ? 0.0f : a.wsk / as, pv = zero ? 0.0f : a.wsv / as;
     const uint32_t half = a.hd / 2u, nq = a.n_heads * half, nk = a.n_kv * half, nv = a.n_kv * a.hd;
     const float* cache = a.rope + static_cast<size_t>(pos) * a.hd;
-    for (uint32_t i = threadIdx.x; i < nq + nk + nv; i += blockDim.x) {
+    // blockIdx.y spreads the token's elements over several workgroups, so each thread waits for about one load of
+    // the GEMM outputs instead of a dozen in a row
+    for (uint32_t i = blockIdx.y * blockDim.x + threadIdx.x; i < nq + nk + nv; i += gridDim.y * blockDim.x) {
         if (i < nq + nk) {
             const bool isq = i < nq;
             const uint32_t j = isq ? i : i - nq, head = j / half, pr = j - head * half;
@@ -3304,7 +3306,8 @@ static int record_prefill(const vx_decoder* d, uint32_t n, bool head, hipStream_
         ra.hd = c.head_dim;
         ra.max_ctx = c.max_ctx;
         ra.rope_normal = c.rope_mode == VX_ROPE_NORMAL ? 1u : 0u;
-        hipLaunchKernelGGL(pf_rope_kernel, dim3(n), dim3(256), 0, st, ra);
+        const uint32_t n_elem = c.n_heads * c.head_dim / 2u + c.n_kv_heads * c.head_dim / 2u + c.n_kv_heads * c.head_dim;
+        hipLaunchKernelGGL(pf_rope_kernel, dim3(n, (n_elem + 255u) / 256u), dim3(256), 0, st, ra);
         VX_HIP(hipGetLastError());
         AttnArgs at{};
         at.ctl = d->d_ctl;
